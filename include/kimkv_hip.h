@@ -1,0 +1,258 @@
+/*
+ * kimkv_hip.h -- C-ABI of the MI355X (gfx950) paged-KV data path.
+ *
+ * This is the drop-in seam that replaces the reference's internal launch layer
+ * `kimkvcache::cuda_detail::launch*` (src/cuda/kv/kernels.cuh:31-143) and the
+ * device-pool part of `CudaKvStorage` (src/cuda/kv/storage.cpp:99-190).
+ * Every entry point takes plain pointers, sizes and an opaque stream; no HIP,
+ * CUDA or torch types appear in the signatures.  All launches are
+ * asynchronous on the given stream (NULL = the device's default stream), like
+ * the reference's `CudaStream` (include/kim-kv/cuda/cuda_status.h:13).
+ *
+ * Device page layout (private to the storage, identical total size to the
+ * reference's page): for a page of `cap` tokens,
+ *     K(l,t,h,d) = l*2*cap*H*D + h*2*cap*D + t*D + d
+ *     V(l,t,h,d) = l*2*cap*H*D + h*2*cap*D + cap*D + d*cap + t
+ * i.e. per (layer, head) one contiguous block holding K rows [cap][D]
+ * followed by V transposed [D][cap].  The contiguous tensors that cross the
+ * API (append input, gather output) keep the reference order
+ * [layer][K/V][token][head][dim] (include/kim-kv/core/kv_layout.h:73-90).
+ */
+#ifndef KIMKV_HIP_H
+#define KIMKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* kimkv_stream_t;
+
+/* Mirrors CudaError (include/kim-kv/cuda/cuda_status.h:29-38). */
+typedef enum kimkv_status {
+    KIMKV_OK = 0,
+    KIMKV_INVALID_ARGUMENT = 1,
+    KIMKV_RUNTIME_UNAVAILABLE = 2,
+    KIMKV_ALLOCATION_FAILED = 3,
+    KIMKV_SUBMISSION_FAILED = 4,
+    KIMKV_NOT_READY = 5,
+    KIMKV_EXECUTION_FAILED = 6,
+    KIMKV_INTERNAL_ERROR = 7
+} kimkv_status;
+
+/* Page kinds: PageKind (include/kim-kv/core/page_types.h:8-11). */
+#define KIMKV_PAGE_MICRO 0u
+#define KIMKV_PAGE_EXTENT 1u
+
+/* Layer/head/dim triple: cuda_detail::DeviceLayout (kernels.cuh:14-18). */
+typedef struct kimkv_layout {
+    uint32_t layers;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+} kimkv_layout;
+
+/* Page-table entry as the kernels see it.  Same fields, order and size
+ * (20 bytes) as the reference DeviceBlockDescriptor
+ * (include/kim-kv/engine/engine_kv.h:100-127). */
+typedef struct kimkv_block_desc {
+    uint32_t slot;
+    uint32_t generation;
+    uint32_t logical_token_begin;
+    uint16_t valid_tokens;
+    uint16_t page_token_capacity;
+    uint8_t kind;
+    uint8_t reserved[3];
+} kimkv_block_desc;
+
+/* One lane of a ragged decode launch.  Same fields, order and size (56 bytes)
+ * as the reference DevicePagedDecodeBatchItem (engine_kv.h:172-191);
+ * `workspace` is the lane's split-K partial scratch (the reference's
+ * `device_scores`), sized by kimkv_decode_workspace_bytes(). */
+typedef struct kimkv_decode_item {
+    const kimkv_block_desc* descriptors;
+    uint32_t descriptor_count;
+    uint32_t token_count;
+    uint32_t layer;
+    const uint16_t* query;   /* [query_heads][head_dim] fp16 */
+    float* workspace;
+    uint16_t* output;        /* [query_heads][head_dim] fp16 */
+    float attention_scale;
+} kimkv_decode_item;
+
+/* One lane's append.  Writes `token_count` tokens of layers
+ * [layer_begin, layer_begin+layer_count) into page (dst_kind, dst_slot) at
+ * page token `dst_token`.  Source element (l, t, h, d) of K is read at
+ *     src_key + (l-layer_begin)*src_layer_stride + t*src_token_stride + h*D + d
+ * and likewise for V.  When cow_tokens != 0, page tokens [0, cow_tokens) of
+ * those layers are first copied from page (cow_kind, cow_slot): the
+ * partial-tail copy-on-write of src/cuda/engine/transaction.cpp:158-191 and
+ * src/cuda/kv/append.cpp:45-96.  Replaces launchCopyLayerTokens,
+ * launchWriteLayerToken, launchCopyPageTokens and launchAppendTokens
+ * (kernels.cuh:31-55,97-117) with one batched kernel. */
+typedef struct kimkv_append_job {
+    const uint16_t* src_key;
+    const uint16_t* src_value;
+    uint64_t src_layer_stride;
+    uint32_t src_token_stride;
+    uint32_t layer_begin;
+    uint32_t layer_count;
+    uint32_t token_count;
+    uint32_t dst_slot;
+    uint32_t cow_slot;
+    uint16_t dst_token;
+    uint16_t cow_tokens;
+    uint8_t dst_kind;
+    uint8_t cow_kind;
+    uint8_t reserved[2];
+} kimkv_append_job;
+
+/* One 8-micro -> 1-extent promotion (PromotionSlots, kernels.cuh:27-29). */
+typedef struct kimkv_promotion_job {
+    uint32_t micro_slots[8];
+    uint32_t extent_slot;
+} kimkv_promotion_job;
+
+typedef struct kimkv_storage kimkv_storage;
+
+typedef struct kimkv_storage_info {
+    kimkv_layout layout;
+    uint32_t micro_capacity;
+    uint32_t extent_capacity;
+    uint16_t micro_page_tokens;
+    uint16_t extent_page_tokens;
+    uint64_t micro_page_elements;
+    uint64_t extent_page_elements;
+    uint64_t micro_reserved_bytes;
+    uint64_t extent_reserved_bytes;
+    int device;
+    int compute_units;
+} kimkv_storage_info;
+
+/* ---- runtime / memory --------------------------------------------------- */
+
+/* Number of visible HIP devices (0 when the runtime is unavailable). */
+int kimkv_device_count(void);
+
+/* Last native HIP error code seen by this thread (diagnostics only). */
+int kimkv_last_native_error(void);
+
+kimkv_status kimkv_device_malloc(void** ptr, size_t bytes);
+kimkv_status kimkv_device_free(void* ptr);
+kimkv_status kimkv_host_malloc_pinned(void** ptr, size_t bytes);
+kimkv_status kimkv_host_free_pinned(void* ptr);
+kimkv_status kimkv_memcpy_h2d_async(void* dst, const void* src, size_t bytes, kimkv_stream_t stream);
+kimkv_status kimkv_memcpy_d2h_async(void* dst, const void* src, size_t bytes, kimkv_stream_t stream);
+kimkv_status kimkv_memcpy_d2d_async(void* dst, const void* src, size_t bytes, kimkv_stream_t stream);
+kimkv_status kimkv_stream_create(kimkv_stream_t* stream);
+kimkv_status kimkv_stream_destroy(kimkv_stream_t stream);
+kimkv_status kimkv_stream_synchronize(kimkv_stream_t stream);
+kimkv_status kimkv_device_synchronize(void);
+
+/* Completion events (the reference's cudaEventRecord/Synchronize at the token
+ * boundary, src/cuda/engine/transaction.cpp:84-120). */
+kimkv_status kimkv_event_create(void** event, int timing);
+kimkv_status kimkv_event_destroy(void* event);
+kimkv_status kimkv_event_record(void* event, kimkv_stream_t stream);
+kimkv_status kimkv_event_query(void* event);       /* KIMKV_OK or KIMKV_NOT_READY */
+kimkv_status kimkv_event_synchronize(void* event);
+kimkv_status kimkv_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ---- storage ------------------------------------------------------------- */
+
+/* Allocates and zero-fills the micro and extent pools on the current device:
+ * CudaKvStorage::CudaKvStorage (src/cuda/kv/storage.cpp:99-190). */
+kimkv_status kimkv_storage_create(kimkv_storage** out, kimkv_layout layout,
+                                  uint32_t micro_capacity, uint32_t extent_capacity,
+                                  uint16_t micro_page_tokens, uint16_t extent_page_tokens);
+kimkv_status kimkv_storage_destroy(kimkv_storage* storage);
+kimkv_status kimkv_storage_query(const kimkv_storage* storage, kimkv_storage_info* info);
+/* Device address of a page: CudaKvStorage::Impl::pagePointer (storage.cpp:46-68).
+ * Returns NULL for an out-of-range slot. */
+uint16_t* kimkv_storage_page(const kimkv_storage* storage, uint32_t kind, uint32_t slot);
+
+/* ---- data-path kernels ---------------------------------------------------- */
+
+/* Batched append of `job_count` jobs held in DEVICE memory.  `max_layer_count`
+ * is the largest layer_count among the jobs (grid height). */
+kimkv_status kimkv_append_batch(const kimkv_storage* storage,
+                                const kimkv_append_job* device_jobs, uint32_t job_count,
+                                uint32_t max_layer_count, kimkv_stream_t stream);
+
+/* Paged -> contiguous [layer][K/V][token][head][dim] copy of one table
+ * (launchGather, kernels.cuh:67-75; gatherKernel page_kernels.cu:184-242).
+ * Descriptors are in DEVICE memory, sorted and contiguous from token 0. */
+kimkv_status kimkv_gather(const kimkv_storage* storage,
+                          const kimkv_block_desc* device_descriptors, uint32_t descriptor_count,
+                          uint32_t total_tokens, uint16_t* device_output, kimkv_stream_t stream);
+
+/* Batched micro -> extent promotion of DEVICE jobs
+ * (launchPromotion, kernels.cuh:57-65; promotionKernel page_kernels.cu:129-182). */
+kimkv_status kimkv_promote_batch(const kimkv_storage* storage,
+                                 const kimkv_promotion_job* device_jobs, uint32_t job_count,
+                                 kimkv_stream_t stream);
+
+/* Split-K planning for a ragged decode batch.  Given the lanes' token counts
+ * (host array), picks the chunk length (a multiple of 64 tokens, >= 128) and
+ * fills chunk_prefix[0..lane_count] (host array) with the running chunk count.
+ * Returns the total chunk count in *total_chunks. */
+kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* token_counts,
+                               uint32_t lane_count, uint32_t query_heads,
+                               uint32_t* chunk_tokens, uint32_t* chunk_prefix,
+                               uint32_t* total_chunks);
+
+/* Workspace bytes one lane needs for a given token count and chunk length
+ * (0 when the lane fits one chunk).  Never larger than the reference's
+ * score workspace requirement query_heads*token_count*4
+ * (src/cuda/engine/transaction.cpp:56-64). */
+size_t kimkv_decode_workspace_bytes(uint32_t token_count, uint32_t chunk_tokens,
+                                    uint32_t query_heads, uint32_t head_dim);
+
+/* Fused split-K GQA paged decode attention over a ragged batch: replaces
+ * launchPagedDecodeAttention / launchPagedDecodeAttentionBatch
+ * (kernels.cuh:119-143; paged_decode_kernels.cu:132-474,533-617).
+ * q head j reads kv head j / (query_heads / kv_heads); s = (q.k) * scale with
+ * fp32 accumulation; softmax; fp16 round-to-nearest-even output.
+ * `device_items` and `device_chunk_prefix` live in DEVICE memory. */
+kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage,
+                                      const kimkv_decode_item* device_items,
+                                      const uint32_t* device_chunk_prefix,
+                                      uint32_t lane_count, uint32_t total_chunks,
+                                      uint32_t chunk_tokens, uint32_t query_heads,
+                                      kimkv_stream_t stream);
+
+/* Average duration (ms) of the decode kernels launched since the last reset,
+ * measured with events on the launch stream; for the benchmark's roofline. */
+kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launches);
+
+/* ---- synthetic inputs (benchmarks and tests) ----------------------------- */
+
+/* Deterministic pseudo-normal fp16 value used for every synthetic tensor:
+ *   h = mix64(mix64(seed + row * 0x9E3779B97F4A7C15) + col)
+ *   v = (sum of the four 16-bit fields of h) - 131070          (Irwin-Hall n=4)
+ *   x = fp16_rne(v * 2^-15)                                    (std ~1.155)
+ * mix64 is the splitmix64 finalizer.  Host and device compute it bit-exactly. */
+uint16_t kimkv_synth_value(uint64_t seed, uint64_t row, uint32_t col);
+
+/* Row id of KV element (stream, layer, component, token). */
+uint64_t kimkv_synth_kv_row(uint32_t stream, uint32_t layer, uint32_t component, uint32_t token);
+
+/* Fills `count` fp16 values: out[i] = synth(seed, row0 + i / cols, i % cols). */
+kimkv_status kimkv_fill_rows(uint16_t* device_out, uint64_t count, uint64_t seed,
+                             uint64_t row0, uint32_t cols, kimkv_stream_t stream);
+
+/* Writes synthetic K/V for logical tokens [token_begin, token_end) of a table
+ * straight into its pages: value(layer, comp, token, head, dim) =
+ * synth(seed, kv_row(stream_id, layer, comp, token), head*D + dim).  Used to
+ * materialise large contexts without host copies. */
+kimkv_status kimkv_fill_table(const kimkv_storage* storage,
+                              const kimkv_block_desc* device_descriptors, uint32_t descriptor_count,
+                              uint32_t token_begin, uint32_t token_end,
+                              uint64_t seed, uint32_t stream_id, kimkv_stream_t stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* KIMKV_HIP_H */

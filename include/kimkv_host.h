@@ -1,0 +1,234 @@
+/*
+ * kimkv_host.h -- C facade of the C++ host layer (libkimkv.so).
+ *
+ * The C++ API under include/kim-kv/ mirrors the reference's include/kim-kv
+ * (same class names, arguments and error enums).  This header flattens the
+ * parts a non-C++ caller binds (ctypes, cgo, JNI) into plain functions.
+ * Return codes are the numeric values of the C++ enums:
+ *   KvCacheError   (include/kim-kv/core/page_state.h:67-80)   for kimkv_manager_*
+ *   EngineKvError  (include/kim-kv/engine/engine_kv.h:25-37)  for kimkv_engine_* / kimkv_txn_*
+ *   KvCacheError + kimkv_status pair for kimkv_cache_* (CudaKvOperationResult,
+ *   include/kim-kv/cuda/cuda_kv_cache.h:16-31).
+ */
+#ifndef KIMKV_HOST_H
+#define KIMKV_HOST_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "kimkv_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* MappingEntry (include/kim-kv/core/block_table.h:13-41), flattened. */
+typedef struct kimkv_mapping_entry {
+    uint32_t logical_token_begin;
+    uint16_t valid_tokens;
+    uint8_t kind;
+    uint8_t reserved;
+    uint32_t slot;
+    uint32_t generation;
+} kimkv_mapping_entry;
+
+/* PageHandle (include/kim-kv/core/page_handle.h:10-47). */
+typedef struct kimkv_page_handle {
+    uint32_t kind;
+    uint32_t slot;
+    uint32_t generation;
+} kimkv_page_handle;
+
+/* PageMetadataSnapshot (include/kim-kv/runtime/kv_cache_manager.h:21-33). */
+typedef struct kimkv_page_metadata {
+    uint32_t state;          /* PageState: 0 free 1 mutable 2 sealed 3 copy_target 4 retiring */
+    uint32_t valid_tokens;
+    uint32_t ref_count;
+    uint32_t promotion_pins;
+    uint32_t inflight_readers;
+    uint32_t reserved;
+    uint64_t mutable_owner;
+} kimkv_page_metadata;
+
+/* PagePoolSnapshot (include/kim-kv/core/page_pool.h:25-40). */
+typedef struct kimkv_pool_snapshot {
+    uint32_t kind;
+    uint32_t total_slots;
+    uint32_t free_slots;
+    uint32_t allocated_slots;
+    uint64_t successful_allocations;
+    uint64_t successful_releases;
+    uint64_t failed_allocations;
+    uint64_t rejected_releases;
+} kimkv_pool_snapshot;
+
+/* KvCacheManagerSnapshot (kv_cache_manager.h:35-42). */
+typedef struct kimkv_manager_snapshot {
+    uint64_t request_count;
+    uint64_t promotion_count;
+    uint64_t page_lease_count;
+    uint64_t token_reservation_count;
+    kimkv_pool_snapshot micro_pool;
+    kimkv_pool_snapshot extent_pool;
+} kimkv_manager_snapshot;
+
+/* ---- KvCacheManager (include/kim-kv/runtime/kv_cache_manager.h:44-277) ---- */
+typedef struct kimkv_manager kimkv_manager;
+
+kimkv_manager* kimkv_manager_create(uint32_t micro_capacity, uint32_t extent_capacity);
+void kimkv_manager_destroy(kimkv_manager* m);
+int kimkv_manager_create_request(kimkv_manager* m, uint64_t request_id);
+int kimkv_manager_append(kimkv_manager* m, uint64_t request_id, uint32_t token_count);
+/* reserveToken; the reserved (candidate) table is copied out when entries != NULL. */
+int kimkv_manager_reserve_token(kimkv_manager* m, uint64_t request_id, uint32_t expected_committed_tokens,
+                                uint64_t* reservation_id, uint64_t* reserved_version,
+                                kimkv_mapping_entry* entries, uint32_t capacity, uint32_t* count);
+int kimkv_manager_commit_token(kimkv_manager* m, uint64_t reservation_id);
+int kimkv_manager_rollback_token(kimkv_manager* m, uint64_t reservation_id);
+int kimkv_manager_seal_tail(kimkv_manager* m, uint64_t request_id);
+int kimkv_manager_fork_request(kimkv_manager* m, uint64_t source_request_id, uint64_t child_request_id);
+int kimkv_manager_release_request(kimkv_manager* m, uint64_t request_id);
+/* preparePromotion; sources[8] and target receive the handles when non-NULL. */
+int kimkv_manager_prepare_promotion(kimkv_manager* m, uint64_t request_id, uint32_t logical_token_begin,
+                                    uint64_t* promotion_id, kimkv_page_handle* sources,
+                                    kimkv_page_handle* target);
+int kimkv_manager_commit_promotion(kimkv_manager* m, uint64_t promotion_id);
+int kimkv_manager_rollback_promotion(kimkv_manager* m, uint64_t promotion_id);
+int kimkv_manager_acquire_request_lease(kimkv_manager* m, uint64_t request_id, uint64_t* lease_id);
+int kimkv_manager_acquire_promotion_lease(kimkv_manager* m, uint64_t promotion_id, uint64_t* lease_id);
+int kimkv_manager_acquire_reservation_lease(kimkv_manager* m, uint64_t reservation_id, uint64_t* lease_id);
+int kimkv_manager_release_lease(kimkv_manager* m, uint64_t lease_id);
+/* blockTable: returns 0, RequestNotFound (2), or InvalidArgument (1) when
+ * `capacity` is too small (*count then holds the needed size). */
+int kimkv_manager_block_table(const kimkv_manager* m, uint64_t request_id, uint64_t* version,
+                              kimkv_mapping_entry* entries, uint32_t capacity, uint32_t* count);
+/* pageMetadata: 0 when the handle names a live runtime slot, 1 otherwise. */
+int kimkv_manager_page_metadata(const kimkv_manager* m, kimkv_page_handle handle, kimkv_page_metadata* out);
+void kimkv_manager_get_snapshot(const kimkv_manager* m, kimkv_manager_snapshot* out);
+int kimkv_manager_check_invariants(const kimkv_manager* m);
+
+/* Seeded Fisher-Yates permutation of 0..n-1 driven by splitmix64 (shared by
+ * the benchmark, the tests and the oracle's trace driver). */
+void kimkv_seeded_permutation(uint64_t seed, uint32_t n, uint32_t* out);
+
+/* Reorders a fresh manager's free lists through its public API only, so that
+ * the next allocations of `kind` return slots perm(seed)[0], perm[1], ...:
+ * every slot is allocated (one throw-away request per page, extents through
+ * promotion) and the requests are released in reverse permutation order.
+ * Slot generations advance by one.  Returns KvCacheError. */
+int kimkv_manager_permute_free_slots(kimkv_manager* m, uint32_t kind, uint64_t seed);
+
+/* ---- engine backend (include/kim-kv/engine/engine_kv.h:255-427) ----------- */
+typedef struct kimkv_engine kimkv_engine;
+typedef struct kimkv_txn kimkv_txn;
+
+typedef struct kimkv_engine_config {
+    uint32_t layers;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t query_heads;
+    uint64_t attention_workspace_bytes;
+} kimkv_engine_config;
+
+/* PagedDecodeRequest (engine_kv.h:151-158). */
+typedef struct kimkv_decode_request {
+    uint32_t layer;
+    uint32_t reserved;
+    const uint16_t* query;
+    uint16_t* output;
+    void* workspace;
+    uint64_t workspace_bytes;
+    float attention_scale;
+} kimkv_decode_request;
+
+/* EngineKvBackendSnapshot (engine_kv.h:372-391). */
+typedef struct kimkv_engine_snapshot {
+    uint64_t request_count;
+    uint64_t active_transaction_count;
+    uint64_t committed_token_count;
+    uint64_t batched_attention_submissions;
+    uint64_t batched_attention_lanes;
+    uint64_t batched_write_submissions;
+    uint32_t primary_page_tokens;
+    uint32_t secondary_page_tokens;
+    uint32_t primary_page_capacity;
+    uint32_t secondary_page_capacity;
+    uint32_t allocated_primary_pages;
+    uint32_t allocated_secondary_pages;
+    uint64_t successful_primary_allocations;
+    uint64_t successful_secondary_allocations;
+    uint64_t failed_primary_allocations;
+    uint64_t failed_secondary_allocations;
+    uint64_t storage_reserved_bytes;
+} kimkv_engine_snapshot;
+
+/* createHeterogeneousCudaEngineKvBackend (include/kim-kv/cuda/cuda_engine_kv_backend.h:11-16). */
+kimkv_engine* kimkv_engine_create(const kimkv_engine_config* config, uint32_t micro_capacity,
+                                  uint32_t extent_capacity);
+void kimkv_engine_destroy(kimkv_engine* e);
+int kimkv_engine_create_request(kimkv_engine* e, uint64_t request_id);
+int kimkv_engine_fork_request(kimkv_engine* e, uint64_t source_request_id, uint64_t child_request_id);
+int kimkv_engine_release_request(kimkv_engine* e, uint64_t request_id);
+/* reserveToken: *txn receives a transaction owned by the caller (kimkv_txn_destroy). */
+int kimkv_engine_reserve_token(kimkv_engine* e, uint64_t request_id, uint32_t expected_committed_tokens,
+                               kimkv_stream_t stream, kimkv_txn** txn);
+void kimkv_engine_get_snapshot(const kimkv_engine* e, kimkv_engine_snapshot* out);
+int kimkv_engine_check_invariants(const kimkv_engine* e);
+/* injectCudaEngineFailureOnce (cuda_engine_kv_backend.h:25-29): point 0 = submission, 1 = completion. */
+int kimkv_engine_inject_failure_once(kimkv_engine* e, uint32_t point);
+/* Engine-path promotion (no reference counterpart: the reference engine never
+ * promotes).  Promotes every eligible 8-micro run of a committed request on
+ * `stream` and waits for it. */
+int kimkv_engine_promote_request(kimkv_engine* e, uint64_t request_id, kimkv_stream_t stream,
+                                 uint32_t* promoted);
+/* Copies out a request's committed block table (same contract as kimkv_manager_block_table). */
+int kimkv_engine_block_table(const kimkv_engine* e, uint64_t request_id, uint64_t* version,
+                             kimkv_mapping_entry* entries, uint32_t capacity, uint32_t* count);
+/* The engine's device storage (for data-path helpers such as kimkv_gather). */
+const kimkv_storage* kimkv_engine_storage(const kimkv_engine* e);
+
+/* TokenTransaction (engine_kv.h:298-351). */
+int kimkv_txn_write_layer(kimkv_txn* t, uint32_t layer, const uint16_t* key, const uint16_t* value);
+int kimkv_txn_attend_layer(kimkv_txn* t, const kimkv_decode_request* request);
+int kimkv_txn_commit(kimkv_txn* t);
+int kimkv_txn_rollback(kimkv_txn* t);
+/* Fills phase (TokenTransactionPhase), next layer and logical position. */
+void kimkv_txn_state(const kimkv_txn* t, uint32_t* phase, uint32_t* next_layer, uint32_t* position);
+void kimkv_txn_destroy(kimkv_txn* t);   /* rolls back when not committed */
+
+/* attendLayerBatch (engine_kv.h:355): statuses[i] receives each lane's EngineKvError. */
+void kimkv_attend_layer_batch(kimkv_txn** txns, const kimkv_decode_request* requests, uint32_t count,
+                              int* statuses);
+/* writeLayerBatch: batched form of TokenTransaction::writeLayer (one kernel for all lanes). */
+void kimkv_write_layer_batch(kimkv_txn** txns, const uint32_t* layers, const uint16_t* const* keys,
+                             const uint16_t* const* values, uint32_t count, int* statuses);
+
+/* ---- CudaKvCache equivalent (include/kim-kv/cuda/cuda_kv_cache.h:33-100) --- */
+typedef struct kimkv_cache kimkv_cache;
+
+typedef struct kimkv_cache_result {
+    int metadata_error;     /* KvCacheError */
+    int device_status;      /* kimkv_status */
+} kimkv_cache_result;
+
+kimkv_cache* kimkv_cache_create(kimkv_layout layout, uint32_t micro_capacity, uint32_t extent_capacity);
+void kimkv_cache_destroy(kimkv_cache* c);
+int kimkv_cache_status(const kimkv_cache* c);
+kimkv_manager* kimkv_cache_manager(kimkv_cache* c);
+const kimkv_storage* kimkv_cache_storage(const kimkv_cache* c);
+kimkv_cache_result kimkv_cache_append(kimkv_cache* c, uint64_t request_id, uint32_t token_count,
+                                      const uint16_t* device_input, kimkv_stream_t stream);
+kimkv_cache_result kimkv_cache_promote(kimkv_cache* c, uint64_t request_id, uint32_t logical_token_begin,
+                                       kimkv_stream_t stream);
+kimkv_cache_result kimkv_cache_gather(kimkv_cache* c, uint64_t request_id, uint16_t* device_output,
+                                      kimkv_stream_t stream);
+kimkv_cache_result kimkv_cache_reference_attention(kimkv_cache* c, uint64_t request_id,
+                                                   const float* device_query, float* device_output,
+                                                   kimkv_stream_t stream);
+void kimkv_cache_inject_failure_once(kimkv_cache* c, uint32_t point);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KIMKV_HOST_H */

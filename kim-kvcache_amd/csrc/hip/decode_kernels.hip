@@ -1,0 +1,524 @@
+// decode_kernels.hip -- fused split-K GQA paged decode attention for gfx950.
+//
+// Replaces pagedAttentionScores*/pagedAttentionOutput* (scores then output,
+// src/cuda/attention/paged_decode_kernels.cu:132-474) with one pass over the
+// KV pages.  Work unit: a workgroup per (lane, chunk of tokens, group of four
+// kv heads); wave w owns kv head h and that head's query group.
+//
+// Fast path (head_dim 64, group <= 16, page-aligned table): per 64-token tile
+//   S^T[token][q] = K[token][:] . Q[q][:]   -> 4 x 2 MFMA 16x16x32 f16
+//   online softmax (base 2) on the 16 scores each lane holds
+//   O^T[d][q]    += V^T[d][token] . P[q][token] -> 2 x 4 MFMA 16x16x32 f16
+// K rows and V^T rows (V is stored transposed in the page) are read with
+// 16-byte loads straight into MFMA operand registers; the token order inside
+// each 32-token k-block is permuted so that the score layout MFMA produces is
+// exactly the P operand layout the second MFMA consumes (no shuffles).
+// Lanes with more than one chunk write (o, m, l) partials to the lane
+// workspace; combine_kernel merges them.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "device_common.h"
+#include "runtime_internal.h"
+
+namespace kimkv {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr unsigned kBlock = 256;          // 4 waves
+constexpr unsigned kHeadsPerBlock = 4;
+constexpr unsigned kMaxChunk = 8192;      // tokens per chunk (multiple of 64)
+constexpr unsigned kMinChunk = 256;
+constexpr unsigned kMaxGroups = kMaxChunk / 8;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// One 8-token group of the chunk: `base` is the page's (layer, head 0) block.
+struct GroupEntry {
+    const uint16_t* base;
+    uint32_t cap;
+    uint32_t pt0;
+};
+
+__device__ inline float wave_max(float v)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+__device__ inline float wave_sum(float v)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+__device__ inline half8_t load_half8(const uint16_t* p)
+{
+    return *reinterpret_cast<const half8_t*>(p);
+}
+
+// ---------------------------------------------------------------------------
+// Fast path for one wave: kv head h, head_dim 64, group <= 16.
+// ---------------------------------------------------------------------------
+__device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_item& item,
+                                uint32_t h, uint32_t G, uint32_t QH, uint32_t c0, uint32_t c1,
+                                uint32_t chunk_index, bool single_chunk)
+{
+    constexpr uint32_t D = 64;
+    uint32_t const l = threadIdx.x & 63u;
+    uint32_t const a = l >> 4;            // lane group
+    uint32_t const r = l & 15u;           // row/column inside a 16-wide MFMA tile
+    uint32_t const x = (l >> 2) & 3u;     // K-operand row group
+    uint32_t const q = h * G + r;
+    bool const qvalid = r < G;
+    uint64_t const head_unit = static_cast<uint64_t>(h) * 2u * D;   // x cap = head offset
+
+    half8_t qb0 = {};
+    half8_t qb1 = {};
+    if (qvalid) {
+        qb0 = load_half8(item.query + static_cast<uint64_t>(q) * D + a * 8);
+        qb1 = load_half8(item.query + static_cast<uint64_t>(q) * D + 32 + a * 8);
+    }
+    float const scale2 = item.attention_scale * kLog2e;
+    float m_run = -INFINITY;
+    float l_part = 0.0f;
+    float4_t acc[4] = {};
+    half8_t const zero8 = {};
+
+    for (uint32_t t0 = c0; t0 < c1; t0 += 64) {
+        uint32_t const tg = (t0 - c0) >> 3;
+        uint32_t const nvalid = c1 - t0;
+
+        // ---- loads: K rows (QK A operand) and V^T rows (PV A operand) ----
+        half8_t kop[2][2][2];
+        half8_t vop[2][4];
+#pragma unroll
+        for (uint32_t kb = 0; kb < 2; ++kb) {
+            GroupEntry const gk = groups[tg + 4 * kb + x];
+#pragma unroll
+            for (uint32_t e = 0; e < 2; ++e) {
+                uint32_t const tt = 32 * kb + 8 * x + 4 * e + (l & 3u);
+                if (tt < nvalid && gk.base != nullptr) {
+                    const uint16_t* row = gk.base + gk.cap * head_unit
+                        + static_cast<uint64_t>(gk.pt0 + 4 * e + (l & 3u)) * D;
+                    kop[kb][e][0] = load_half8(row + a * 8);
+                    kop[kb][e][1] = load_half8(row + 32 + a * 8);
+                } else {
+                    kop[kb][e][0] = zero8;
+                    kop[kb][e][1] = zero8;
+                }
+            }
+            GroupEntry const gv = groups[tg + 4 * kb + a];
+            uint32_t const vt0 = 32 * kb + 8 * a;
+            if (vt0 < nvalid && gv.base != nullptr) {
+                const uint16_t* vt = gv.base + gv.cap * head_unit + static_cast<uint64_t>(gv.cap) * D + gv.pt0;
+#pragma unroll
+                for (uint32_t db = 0; db < 4; ++db) {
+                    vop[kb][db] = load_half8(vt + static_cast<uint64_t>(db * 16 + r) * gv.cap);
+                }
+                if (vt0 + 8 > nvalid) {
+                    // Tokens past the chunk end may hold stale data: zero them.
+                    uint32_t const keep = nvalid - vt0;
+#pragma unroll
+                    for (uint32_t db = 0; db < 4; ++db) {
+#pragma unroll
+                        for (uint32_t j = 0; j < 8; ++j) {
+                            if (j >= keep) vop[kb][db][j] = static_cast<_Float16>(0.0f);
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (uint32_t db = 0; db < 4; ++db) vop[kb][db] = zero8;
+            }
+        }
+
+        // ---- scores ----
+        float4_t s[2][2];
+#pragma unroll
+        for (uint32_t kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (uint32_t e = 0; e < 2; ++e) {
+                float4_t z = {};
+                z = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][0], qb0, z, 0, 0, 0);
+                s[kb][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][1], qb1, z, 0, 0, 0);
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (uint32_t kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (uint32_t e = 0; e < 2; ++e) {
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i) {
+                    uint32_t const tt = 32 * kb + 8 * a + 4 * e + i;
+                    float const v = tt < nvalid ? s[kb][e][i] * scale2 : -INFINITY;
+                    s[kb][e][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        float const m_new = fmaxf(m_run, mx);
+        float const alpha = exp2f(m_run - m_new);
+        m_run = m_new;
+
+        half8_t pb[2];
+        float psum = 0.0f;
+#pragma unroll
+        for (uint32_t kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (uint32_t e = 0; e < 2; ++e) {
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i) {
+                    float const p = exp2f(s[kb][e][i] - m_new);
+                    psum += p;
+                    pb[kb][4 * e + i] = static_cast<_Float16>(p);
+                }
+            }
+        }
+        l_part = l_part * alpha + psum;
+#pragma unroll
+        for (uint32_t db = 0; db < 4; ++db) acc[db] *= alpha;
+
+        // ---- O^T += V^T . P^T ----
+#pragma unroll
+        for (uint32_t kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (uint32_t db = 0; db < 4; ++db) {
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[kb][db], pb[kb], acc[db], 0, 0, 0);
+            }
+        }
+    }
+
+    float l_tot = l_part + __shfl_xor(l_part, 16);
+    l_tot += __shfl_xor(l_tot, 32);
+    if (!qvalid) return;
+    if (single_chunk) {
+        float const inv = 1.0f / l_tot;
+        uint16_t* out = item.output + static_cast<uint64_t>(q) * D;
+#pragma unroll
+        for (uint32_t db = 0; db < 4; ++db) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) {
+                out[db * 16 + 4 * a + i] = __half_as_ushort(__float2half_rn(acc[db][i] * inv));
+            }
+        }
+    } else {
+        float* ws = item.workspace + (static_cast<uint64_t>(chunk_index) * QH + q) * (D + 2);
+#pragma unroll
+        for (uint32_t db = 0; db < 4; ++db) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) ws[db * 16 + 4 * a + i] = acc[db][i];
+        }
+        if (a == 0) {
+            ws[D] = m_run;
+            ws[D + 1] = l_tot;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Generic path for one wave: any head_dim <= 256, any group size, any table.
+// One query head at a time; lanes own tokens for scores and dims for output.
+// ---------------------------------------------------------------------------
+struct WaveScratch {
+    float p[64];
+    const uint16_t* vrow[64];
+    uint32_t cap[64];
+};
+
+__device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& item, uint32_t h,
+                                    uint32_t G, uint32_t QH, uint32_t c0, uint32_t c1,
+                                    uint32_t chunk_index, bool single_chunk, WaveScratch* scratch)
+{
+    uint32_t const lane = threadIdx.x & 63u;
+    uint32_t const D = P.dim;
+    uint32_t const layer = item.layer;
+    float const scale2 = item.attention_scale * kLog2e;
+    for (uint32_t j = 0; j < G; ++j) {
+        uint32_t const q = h * G + j;
+        const uint16_t* qv = item.query + static_cast<uint64_t>(q) * D;
+        float m_run = -INFINITY;
+        float l_run = 0.0f;
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t t0 = c0; t0 < c1; t0 += 64) {
+            uint32_t const t = t0 + lane;
+            bool const valid = t < c1;
+            uint32_t idx = find_descriptor_wave(item.descriptors, item.descriptor_count, t0);
+            const uint16_t* page = nullptr;
+            uint32_t cap = 0;
+            uint32_t pt = 0;
+            if (valid) {
+                while (idx + 1 < item.descriptor_count
+                       && item.descriptors[idx + 1].logical_token_begin <= t) {
+                    ++idx;
+                }
+                kimkv_block_desc const e = item.descriptors[idx];
+                if (t >= e.logical_token_begin && t < e.logical_token_begin + e.valid_tokens
+                    && e.valid_tokens <= e.page_token_capacity) {
+                    page = page_base(P, e.kind, e.slot, e.page_token_capacity);
+                    cap = e.page_token_capacity;
+                    pt = t - e.logical_token_begin;
+                }
+            }
+            float s = -INFINITY;
+            const uint16_t* vrow = nullptr;
+            if (page != nullptr) {
+                const uint16_t* hb = page + head_block(P, cap, layer, h);
+                const uint16_t* krow = hb + static_cast<uint64_t>(pt) * D;
+                float dot = 0.0f;
+                for (uint32_t d = 0; d < D; ++d) {
+                    dot += __half2float(__ushort_as_half(qv[d])) * __half2float(__ushort_as_half(krow[d]));
+                }
+                s = dot * scale2;
+                vrow = hb + static_cast<uint64_t>(cap) * D + pt;
+            }
+            float const m_new = fmaxf(m_run, wave_max(s));
+            float const alpha = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
+            float const p = (page != nullptr && m_new != -INFINITY) ? exp2f(s - m_new) : 0.0f;
+            l_run = l_run * alpha + wave_sum(p);
+            m_run = m_new;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] *= alpha;
+            scratch->p[lane] = p;
+            scratch->vrow[lane] = vrow;
+            scratch->cap[lane] = cap;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            uint32_t const nt = min(64u, c1 - t0);
+            for (uint32_t tt = 0; tt < nt; ++tt) {
+                float const pp = scratch->p[tt];
+                const uint16_t* vr = scratch->vrow[tt];
+                uint32_t const vc = scratch->cap[tt];
+                if (vr == nullptr || pp == 0.0f) continue;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    uint32_t const d = lane + 64u * k;
+                    if (d < D) o[k] += pp * __half2float(__ushort_as_half(vr[static_cast<uint64_t>(d) * vc]));
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        if (single_chunk) {
+            float const inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t const d = lane + 64u * k;
+                if (d < D) {
+                    item.output[static_cast<uint64_t>(q) * D + d] = __half_as_ushort(__float2half_rn(o[k] * inv));
+                }
+            }
+        } else {
+            float* ws = item.workspace + (static_cast<uint64_t>(chunk_index) * QH + q) * (D + 2);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t const d = lane + 64u * k;
+                if (d < D) ws[d] = o[k];
+            }
+            if (lane == 0) {
+                ws[D] = m_run;
+                ws[D + 1] = l_run;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void decode_kernel(PoolView P, const kimkv_decode_item* items,
+                                                        const uint32_t* prefix, uint32_t lane_count,
+                                                        uint32_t chunk_tokens, uint32_t QH)
+{
+    __shared__ GroupEntry groups[kMaxGroups];
+    __shared__ WaveScratch scratch[kHeadsPerBlock];
+    __shared__ uint32_t s_lane;
+    __shared__ uint32_t s_idx0;
+    __shared__ uint32_t s_generic;
+
+    uint32_t const tid = threadIdx.x;
+    uint32_t const chunk_id = blockIdx.x;
+    if (tid == 0) {
+        s_lane = 0xFFFFFFFFu;
+        s_generic = 0;
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < lane_count; i += kBlock) {
+        if (prefix[i] <= chunk_id && chunk_id < prefix[i + 1]) s_lane = i;
+    }
+    __syncthreads();
+    uint32_t const lane = s_lane;
+    if (lane == 0xFFFFFFFFu) return;
+
+    kimkv_decode_item const item = items[lane];
+    uint32_t const H = P.heads;
+    uint32_t const D = P.dim;
+    uint32_t const chunk_index = chunk_id - prefix[lane];
+    uint32_t const nchunks = prefix[lane + 1] - prefix[lane];
+    uint32_t const T = item.token_count;
+    uint32_t const c0 = chunk_index * chunk_tokens;
+    if (T == 0 || c0 >= T || item.descriptors == nullptr || item.descriptor_count == 0
+        || item.query == nullptr || item.output == nullptr || item.layer >= P.layers
+        || QH == 0 || QH % H != 0 || D > 256 || chunk_tokens > kMaxChunk
+        || (nchunks > 1 && item.workspace == nullptr)) {
+        return;
+    }
+    uint32_t const c1 = min(c0 + chunk_tokens, T);
+    uint32_t const G = QH / H;
+    bool const single = nchunks == 1;
+
+    if (tid < 64) {
+        uint32_t const idx0 = find_descriptor_wave(item.descriptors, item.descriptor_count, c0);
+        if (tid == 0) s_idx0 = idx0;
+    }
+    uint32_t const ngroups = (c1 - c0 + 7) / 8;
+    for (uint32_t g = tid; g < ngroups; g += kBlock) {
+        groups[g] = GroupEntry{nullptr, 0, 0};
+    }
+    __syncthreads();
+    uint32_t const idx0 = s_idx0;
+    bool fast_shape = D == 64 && G <= 16;
+    for (uint32_t j = tid; j <= ngroups && idx0 + j < item.descriptor_count; j += kBlock) {
+        kimkv_block_desc const e = item.descriptors[idx0 + j];
+        uint32_t const b = e.logical_token_begin;
+        uint32_t const end = b + e.valid_tokens;
+        uint32_t const lo = max(b, c0);
+        uint32_t const hi = min(end, c1);
+        if (lo >= hi) continue;
+        uint32_t const cap = e.page_token_capacity;
+        const uint16_t* page = page_base(P, e.kind, e.slot, cap);
+        bool const aligned = (b & 7u) == 0 && (cap & 7u) == 0 && e.valid_tokens <= cap
+            && ((end & 7u) == 0 || end >= T) && page != nullptr;
+        if (!aligned) {
+            s_generic = 1;
+            continue;
+        }
+        const uint16_t* base = page + head_block(P, cap, item.layer, 0);
+        for (uint32_t g = (lo - c0) >> 3; g < (hi - c0 + 7) >> 3; ++g) {
+            groups[g] = GroupEntry{base, cap, c0 + 8 * g - b};
+        }
+    }
+    __syncthreads();
+
+    uint32_t const wave = tid >> 6;
+    uint32_t const h = blockIdx.y * kHeadsPerBlock + wave;
+    if (h >= H) return;
+    if (fast_shape && s_generic == 0) {
+        decode_wave_d64(groups, item, h, G, QH, c0, c1, chunk_index, single);
+    } else {
+        decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &scratch[wave]);
+    }
+}
+
+// Merges the per-chunk partials of every multi-chunk lane: block = (lane, q head).
+__global__ __launch_bounds__(64) void combine_kernel(const kimkv_decode_item* items, const uint32_t* prefix,
+                                                     uint32_t QH, uint32_t D)
+{
+    uint32_t const lane = blockIdx.x;
+    uint32_t const q = blockIdx.y;
+    uint32_t const n = prefix[lane + 1] - prefix[lane];
+    if (n <= 1) return;
+    kimkv_decode_item const item = items[lane];
+    if (item.workspace == nullptr || item.output == nullptr) return;
+    uint32_t const stride = QH * (D + 2);
+    const float* ws = item.workspace + static_cast<uint64_t>(q) * (D + 2);
+    float M = -INFINITY;
+    for (uint32_t k = 0; k < n; ++k) M = fmaxf(M, ws[static_cast<uint64_t>(k) * stride + D]);
+    float den = 0.0f;
+    for (uint32_t k = 0; k < n; ++k) {
+        const float* part = ws + static_cast<uint64_t>(k) * stride;
+        den += exp2f(part[D] - M) * part[D + 1];
+    }
+    float const inv = 1.0f / den;
+    for (uint32_t d = threadIdx.x; d < D; d += 64) {
+        float num = 0.0f;
+        for (uint32_t k = 0; k < n; ++k) {
+            const float* part = ws + static_cast<uint64_t>(k) * stride;
+            num += exp2f(part[D] - M) * part[d];
+        }
+        item.output[static_cast<uint64_t>(q) * D + d] = __half_as_ushort(__float2half_rn(num * inv));
+    }
+}
+
+}  // namespace
+}  // namespace kimkv
+
+using namespace kimkv;
+
+extern "C" {
+
+kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* token_counts,
+                               uint32_t lane_count, uint32_t query_heads, uint32_t* chunk_tokens,
+                               uint32_t* chunk_prefix, uint32_t* total_chunks)
+{
+    if (storage == nullptr || chunk_tokens == nullptr || chunk_prefix == nullptr || total_chunks == nullptr
+        || (lane_count != 0 && token_counts == nullptr) || query_heads == 0) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < lane_count; ++i) total += token_counts[i];
+    uint64_t const cus = storage->compute_units > 0 ? static_cast<uint64_t>(storage->compute_units) : 256u;
+    uint64_t const heads_per_block = kHeadsPerBlock;
+    uint64_t const head_blocks = (storage->layout.kv_heads + heads_per_block - 1) / heads_per_block;
+    // Aim for ~32 workgroups per compute unit.
+    uint64_t target = total * head_blocks / (cus * 32);
+    target = (target + 63) / 64 * 64;
+    if (target < kMinChunk) target = kMinChunk;
+    if (target > kMaxChunk) target = kMaxChunk;
+    uint64_t acc = 0;
+    chunk_prefix[0] = 0;
+    for (uint32_t i = 0; i < lane_count; ++i) {
+        acc += (token_counts[i] + target - 1) / target;
+        if (acc > 0x7FFFFFFFu) return KIMKV_INVALID_ARGUMENT;
+        chunk_prefix[i + 1] = static_cast<uint32_t>(acc);
+    }
+    *chunk_tokens = static_cast<uint32_t>(target);
+    *total_chunks = static_cast<uint32_t>(acc);
+    return KIMKV_OK;
+}
+
+size_t kimkv_decode_workspace_bytes(uint32_t token_count, uint32_t chunk_tokens, uint32_t query_heads,
+                                    uint32_t head_dim)
+{
+    if (chunk_tokens == 0) return 0;
+    uint64_t const chunks = (static_cast<uint64_t>(token_count) + chunk_tokens - 1) / chunk_tokens;
+    if (chunks <= 1) return 0;
+    return static_cast<size_t>(chunks * query_heads * (head_dim + 2ull) * sizeof(float));
+}
+
+kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage, const kimkv_decode_item* device_items,
+                                      const uint32_t* device_chunk_prefix, uint32_t lane_count,
+                                      uint32_t total_chunks, uint32_t chunk_tokens, uint32_t query_heads,
+                                      kimkv_stream_t stream)
+{
+    if (storage == nullptr || device_items == nullptr || device_chunk_prefix == nullptr || lane_count == 0
+        || query_heads == 0 || query_heads % storage->layout.kv_heads != 0 || chunk_tokens == 0
+        || chunk_tokens % 64 != 0 || chunk_tokens > kMaxChunk || storage->layout.head_dim > 256) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    if (total_chunks == 0) return KIMKV_OK;
+    hipStream_t const s = native(stream);
+    dim3 const grid(total_chunks, (storage->layout.kv_heads + kHeadsPerBlock - 1) / kHeadsPerBlock);
+    void* start = nullptr;
+    decode_timing_begin(s, &start);
+    decode_kernel<<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix, lane_count,
+                                          chunk_tokens, query_heads);
+    decode_timing_end(s, start);
+    kimkv_status const status = launch_status();
+    if (status != KIMKV_OK) return status;
+    if (total_chunks > lane_count) {
+        dim3 const cgrid(lane_count, query_heads);
+        combine_kernel<<<cgrid, 64, 0, s>>>(device_items, device_chunk_prefix, query_heads,
+                                            storage->layout.head_dim);
+        return launch_status();
+    }
+    return KIMKV_OK;
+}
+
+}  // extern "C"

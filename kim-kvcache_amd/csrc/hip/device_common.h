@@ -1,0 +1,142 @@
+// device_common.h -- shared device-side definitions for the gfx950 KV kernels.
+//
+// Page layout (see include/kimkv_hip.h): per (layer, head) a contiguous block
+// of 2*cap*D halves: K rows [cap][D] followed by V transposed [D][cap].
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+
+#include "kimkv_hip.h"
+
+struct kimkv_storage {
+    kimkv_layout layout{};
+    uint32_t micro_capacity{0};
+    uint32_t extent_capacity{0};
+    uint16_t micro_tokens{0};
+    uint16_t extent_tokens{0};
+    uint64_t micro_page_elements{0};
+    uint64_t extent_page_elements{0};
+    uint16_t* micro{nullptr};
+    uint16_t* extent{nullptr};
+    int device{0};
+    int compute_units{0};
+};
+
+namespace kimkv {
+
+constexpr unsigned kWave = 64;
+
+// Pool view passed to kernels by value.
+struct PoolView {
+    uint16_t* micro;
+    uint16_t* extent;
+    uint64_t micro_page_elements;
+    uint64_t extent_page_elements;
+    uint32_t micro_capacity;
+    uint32_t extent_capacity;
+    uint32_t micro_tokens;
+    uint32_t extent_tokens;
+    uint32_t layers;
+    uint32_t heads;
+    uint32_t dim;
+};
+
+inline PoolView pool_view(const kimkv_storage& s)
+{
+    return PoolView{s.micro, s.extent, s.micro_page_elements, s.extent_page_elements,
+                    s.micro_capacity, s.extent_capacity, s.micro_tokens, s.extent_tokens,
+                    s.layout.layers, s.layout.kv_heads, s.layout.head_dim};
+}
+
+// Page base for a (kind, slot), or nullptr when the handle does not name a page
+// of this storage or its declared capacity disagrees with the pool's.
+__device__ inline uint16_t* page_base(const PoolView& p, uint32_t kind, uint32_t slot,
+                                      uint32_t capacity)
+{
+    if (kind == KIMKV_PAGE_MICRO) {
+        if (slot >= p.micro_capacity || capacity != p.micro_tokens || p.micro == nullptr) {
+            return nullptr;
+        }
+        return p.micro + static_cast<uint64_t>(slot) * p.micro_page_elements;
+    }
+    if (kind == KIMKV_PAGE_EXTENT) {
+        if (slot >= p.extent_capacity || capacity != p.extent_tokens || p.extent == nullptr) {
+            return nullptr;
+        }
+        return p.extent + static_cast<uint64_t>(slot) * p.extent_page_elements;
+    }
+    return nullptr;
+}
+
+__device__ inline uint32_t pool_tokens(const PoolView& p, uint32_t kind)
+{
+    return kind == KIMKV_PAGE_MICRO ? p.micro_tokens : p.extent_tokens;
+}
+
+// Element offset of the (layer, head) block inside a page of `cap` tokens.
+__device__ inline uint64_t head_block(const PoolView& p, uint32_t cap, uint32_t layer, uint32_t head)
+{
+    return (static_cast<uint64_t>(layer) * p.heads + head) * 2ull * cap * p.dim;
+}
+
+// ---- synthetic generator (bit-identical to kimkv_synth_value) -------------
+__host__ __device__ inline uint64_t mix64(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__host__ __device__ inline int32_t synth_int(uint64_t seed, uint64_t row, uint32_t col)
+{
+    uint64_t const h = mix64(mix64(seed + row * 0x9E3779B97F4A7C15ull) + col);
+    return static_cast<int32_t>(h & 0xFFFFu) + static_cast<int32_t>((h >> 16) & 0xFFFFu)
+        + static_cast<int32_t>((h >> 32) & 0xFFFFu) + static_cast<int32_t>(h >> 48) - 131070;
+}
+
+__device__ inline uint16_t synth_f16(uint64_t seed, uint64_t row, uint32_t col)
+{
+    float const x = static_cast<float>(synth_int(seed, row, col)) * (1.0f / 32768.0f);
+    return __half_as_ushort(__float2half_rn(x));
+}
+
+__host__ __device__ inline uint64_t kv_row(uint32_t stream, uint32_t layer, uint32_t component,
+                                           uint32_t token)
+{
+    return (static_cast<uint64_t>(stream & 0xFFFFu) << 48)
+        | (static_cast<uint64_t>(layer & 0x7FFFu) << 33)
+        | (static_cast<uint64_t>(component & 1u) << 32) | static_cast<uint64_t>(token);
+}
+
+// ---- wave-parallel page-table search ----------------------------------------
+// Index of the last descriptor whose logical_token_begin <= token (descriptors
+// are sorted by begin).  64-ary search: each round every lane probes one
+// candidate, so a 4096-entry table resolves in two dependent rounds.
+// Must be called by all 64 lanes of a wave; the result is wave-uniform.
+__device__ inline uint32_t find_descriptor_wave(const kimkv_block_desc* d, uint32_t count,
+                                                uint32_t token)
+{
+    uint32_t const lane = threadIdx.x & (kWave - 1);
+    uint32_t lo = 0;
+    uint32_t hi = count;
+    while (hi - lo > 1) {
+        uint32_t const step = (hi - lo + kWave - 1) / kWave;
+        uint32_t const i = lo + lane * step;
+        bool const pred = i < hi && d[i].logical_token_begin <= token;
+        uint64_t const mask = __ballot(pred);
+        if (mask == 0) {
+            return lo;
+        }
+        uint32_t const last = 63u - static_cast<uint32_t>(__clzll(mask));
+        lo = lo + last * step;
+        hi = min(lo + step, hi);
+    }
+    return lo;
+}
+
+inline uint32_t ceil_div(uint64_t a, uint64_t b) { return static_cast<uint32_t>((a + b - 1) / b); }
+
+}  // namespace kimkv

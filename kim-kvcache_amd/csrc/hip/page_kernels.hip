@@ -1,0 +1,435 @@
+// page_kernels.hip -- append (with fused partial-tail COW), gather, promotion
+// and synthetic fill kernels for gfx950.
+//
+// Reference kernels these replace (semantics only):
+//   copyPageTokensKernel / appendTokensKernel  src/cuda/kv/page_kernels.cu:46-127
+//   copyLayerTokensKernel / writeLayerTokenKernel
+//                                      src/cuda/attention/paged_decode_kernels.cu:29-99
+//   promotionKernel                    src/cuda/kv/page_kernels.cu:129-182
+//   gatherKernel                       src/cuda/kv/page_kernels.cu:184-242
+#include <hip/hip_runtime.h>
+
+#include "device_common.h"
+#include "runtime_internal.h"
+
+namespace kimkv {
+namespace {
+
+constexpr unsigned kBlock = 256;
+constexpr unsigned kTile = 64;   // tokens per gather/fill tile
+
+struct TokEntry {
+    uint16_t* page;
+    uint32_t cap;
+    uint32_t pt;
+};
+
+// Resolves tokens [t0, t0+n) (n <= 64) of a table into LDS entries.  Tokens
+// not covered by a valid descriptor get page == nullptr.  All threads of the
+// block must call it.
+__device__ void build_tile_table(const PoolView& P, const kimkv_block_desc* desc, uint32_t count,
+                                 uint32_t t0, uint32_t n, TokEntry* tab, uint32_t* s_idx)
+{
+    uint32_t const tid = threadIdx.x;
+    if (tid < kTile) {
+        tab[tid].page = nullptr;
+        uint32_t const idx = find_descriptor_wave(desc, count, t0);
+        if (tid == 0) {
+            *s_idx = idx;
+        }
+    }
+    __syncthreads();
+    uint32_t const idx = *s_idx;
+    // At most n descriptors overlap the tile, starting at idx.
+    if (tid < n && idx + tid < count) {
+        kimkv_block_desc const e = desc[idx + tid];
+        uint32_t const b = e.logical_token_begin;
+        uint32_t const end = b + e.valid_tokens;
+        uint32_t const lo = max(b, t0);
+        uint32_t const hi = min(end, t0 + n);
+        if (lo < hi && e.valid_tokens <= e.page_token_capacity) {
+            uint16_t* page = page_base(P, e.kind, e.slot, e.page_token_capacity);
+            if (page != nullptr) {
+                for (uint32_t t = lo; t < hi; ++t) {
+                    tab[t - t0] = TokEntry{page, e.page_token_capacity, t - b};
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Batched append: one block per (job, layer).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBlock) void append_kernel(PoolView P, const kimkv_append_job* jobs,
+                                                        uint32_t job_count)
+{
+    if (blockIdx.x >= job_count) return;
+    kimkv_append_job const job = jobs[blockIdx.x];
+    uint32_t const li = blockIdx.y;
+    if (li >= job.layer_count) return;
+    uint32_t const layer = job.layer_begin + li;
+    if (layer >= P.layers) return;
+    uint32_t const H = P.heads;
+    uint32_t const D = P.dim;
+    uint32_t const dcap = pool_tokens(P, job.dst_kind);
+    uint16_t* dst = page_base(P, job.dst_kind, job.dst_slot, dcap);
+    if (dst == nullptr || static_cast<uint32_t>(job.dst_token) + job.token_count > dcap) return;
+    uint32_t const tid = threadIdx.x;
+
+    if (job.cow_tokens != 0) {
+        uint32_t const scap = pool_tokens(P, job.cow_kind);
+        uint16_t const* src = page_base(P, job.cow_kind, job.cow_slot, scap);
+        uint32_t const n = job.cow_tokens;
+        if (src != nullptr && n <= scap && n <= dcap && n <= job.dst_token) {
+            uint32_t const per_head = n * D;
+            for (uint32_t i = tid; i < H * per_head; i += kBlock) {
+                uint32_t const h = i / per_head;
+                uint32_t const rem = i - h * per_head;
+                uint32_t const t = rem / D;
+                uint32_t const d = rem - t * D;
+                uint64_t const sh = head_block(P, scap, layer, h);
+                uint64_t const dh = head_block(P, dcap, layer, h);
+                dst[dh + static_cast<uint64_t>(t) * D + d] = src[sh + static_cast<uint64_t>(t) * D + d];
+                dst[dh + static_cast<uint64_t>(dcap) * D + static_cast<uint64_t>(d) * dcap + t] =
+                    src[sh + static_cast<uint64_t>(scap) * D + static_cast<uint64_t>(d) * scap + t];
+            }
+        }
+        __syncthreads();
+    }
+
+    uint32_t const HD = H * D;
+    uint32_t const total = job.token_count * HD;
+    uint64_t const layer_off = static_cast<uint64_t>(li) * job.src_layer_stride;
+    for (uint32_t i = tid; i < total; i += kBlock) {
+        uint32_t const t = i / HD;
+        uint32_t const rem = i - t * HD;
+        uint32_t const h = rem / D;
+        uint32_t const d = rem - h * D;
+        uint64_t const so = layer_off + static_cast<uint64_t>(t) * job.src_token_stride + rem;
+        uint64_t const dh = head_block(P, dcap, layer, h);
+        uint32_t const pt = job.dst_token + t;
+        dst[dh + static_cast<uint64_t>(pt) * D + d] = job.src_key[so];
+        dst[dh + static_cast<uint64_t>(dcap) * D + static_cast<uint64_t>(d) * dcap + pt] = job.src_value[so];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Gather: block = (64-token tile, layer, component); output [L][2][T][H][D].
+// K rows are copied with 16-byte vectors; V is transposed through LDS.
+// ---------------------------------------------------------------------------
+constexpr unsigned kRowChunk = 256;   // V rows staged per pass
+
+__global__ __launch_bounds__(kBlock) void gather_kernel(PoolView P, const kimkv_block_desc* desc,
+                                                        uint32_t count, uint32_t T, uint16_t* out)
+{
+    __shared__ TokEntry tab[kTile];
+    __shared__ uint32_t s_idx;
+    __shared__ __align__(16) uint16_t stage[kTile * kRowChunk];
+
+    uint32_t const t0 = blockIdx.x * kTile;
+    uint32_t const n = min(kTile, T - t0);
+    uint32_t const layer = blockIdx.y;
+    uint32_t const comp = blockIdx.z;
+    build_tile_table(P, desc, count, t0, n, tab, &s_idx);
+
+    uint32_t const D = P.dim;
+    uint32_t const HD = P.heads * D;
+    uint16_t* out_base = out + (static_cast<uint64_t>(layer * 2 + comp) * T + t0) * HD;
+    uint32_t const tid = threadIdx.x;
+
+    if (comp == 0) {
+        if ((D & 7u) == 0) {
+            uint32_t const dchunks = D / 8;
+            uint32_t const per_token = HD / 8;
+            for (uint32_t i = tid; i < n * per_token; i += kBlock) {
+                uint32_t const t = i / per_token;
+                uint32_t const c = i - t * per_token;
+                TokEntry const e = tab[t];
+                if (e.page == nullptr) continue;
+                uint32_t const h = c / dchunks;
+                uint32_t const dc = c - h * dchunks;
+                uint4 const* src = reinterpret_cast<uint4 const*>(
+                    e.page + head_block(P, e.cap, layer, h) + static_cast<uint64_t>(e.pt) * D + dc * 8);
+                reinterpret_cast<uint4*>(out_base)[i] = *src;
+            }
+        } else {
+            for (uint32_t i = tid; i < n * HD; i += kBlock) {
+                uint32_t const t = i / HD;
+                uint32_t const r = i - t * HD;
+                TokEntry const e = tab[t];
+                if (e.page == nullptr) continue;
+                uint32_t const h = r / D;
+                uint32_t const d = r - h * D;
+                out_base[i] = e.page[head_block(P, e.cap, layer, h) + static_cast<uint64_t>(e.pt) * D + d];
+            }
+        }
+        return;
+    }
+
+    for (uint32_t r0 = 0; r0 < HD; r0 += kRowChunk) {
+        uint32_t const rows = min(kRowChunk, HD - r0);
+        if (tid < rows) {
+            uint32_t const r = r0 + tid;
+            uint32_t const h = r / D;
+            uint32_t const d = r - h * D;
+            uint32_t t = 0;
+            while (t < n) {
+                TokEntry const e = tab[t];
+                if (e.page == nullptr) {
+                    stage[t * kRowChunk + tid] = 0;
+                    ++t;
+                    continue;
+                }
+                uint16_t const* row = e.page + head_block(P, e.cap, layer, h)
+                    + static_cast<uint64_t>(e.cap) * D + static_cast<uint64_t>(d) * e.cap;
+                bool const vec = (t & 7u) == 0 && t + 8 <= n && (e.pt & 7u) == 0 && (e.cap & 7u) == 0
+                    && e.pt + 8 <= e.cap && tab[t + 7].page == e.page && tab[t + 7].pt == e.pt + 7;
+                if (vec) {
+                    uint4 const v = *reinterpret_cast<uint4 const*>(row + e.pt);
+                    uint32_t const w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (uint32_t j = 0; j < 4; ++j) {
+                        stage[(t + 2 * j) * kRowChunk + tid] = static_cast<uint16_t>(w[j] & 0xFFFFu);
+                        stage[(t + 2 * j + 1) * kRowChunk + tid] = static_cast<uint16_t>(w[j] >> 16);
+                    }
+                    t += 8;
+                } else {
+                    stage[t * kRowChunk + tid] = row[e.pt];
+                    ++t;
+                }
+            }
+        }
+        __syncthreads();
+        if ((rows & 7u) == 0) {
+            uint32_t const per_token = rows / 8;
+            for (uint32_t i = tid; i < n * per_token; i += kBlock) {
+                uint32_t const t = i / per_token;
+                uint32_t const c = (i - t * per_token) * 8;
+                if (tab[t].page == nullptr) continue;
+                *reinterpret_cast<uint4*>(out_base + static_cast<uint64_t>(t) * HD + r0 + c) =
+                    *reinterpret_cast<uint4 const*>(&stage[t * kRowChunk + c]);
+            }
+        } else {
+            for (uint32_t i = tid; i < n * rows; i += kBlock) {
+                uint32_t const t = i / rows;
+                uint32_t const c = i - t * rows;
+                if (tab[t].page == nullptr) continue;
+                out_base[static_cast<uint64_t>(t) * HD + r0 + c] = stage[t * kRowChunk + c];
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Batched promotion: block = (job, layer).  Extent token t <- micro page t/8.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBlock) void promote_kernel(PoolView P, const kimkv_promotion_job* jobs,
+                                                         uint32_t job_count)
+{
+    if (blockIdx.x >= job_count) return;
+    kimkv_promotion_job const job = jobs[blockIdx.x];
+    uint32_t const layer = blockIdx.y;
+    uint32_t const mt = P.micro_tokens;
+    uint32_t const et = P.extent_tokens;
+    if (mt * 8 != et || layer >= P.layers) return;
+    uint16_t* dst = page_base(P, KIMKV_PAGE_EXTENT, job.extent_slot, et);
+    if (dst == nullptr) return;
+    uint16_t const* src[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        src[k] = page_base(P, KIMKV_PAGE_MICRO, job.micro_slots[k], mt);
+        if (src[k] == nullptr) return;
+    }
+    uint32_t const H = P.heads;
+    uint32_t const D = P.dim;
+    uint32_t const tid = threadIdx.x;
+    if ((D & 7u) == 0 && mt == 8) {
+        uint32_t const dchunks = D / 8;
+        // K: (h, t, dc) 16-byte chunks.
+        uint32_t const kchunks = H * et * dchunks;
+        for (uint32_t i = tid; i < kchunks; i += kBlock) {
+            uint32_t const h = i / (et * dchunks);
+            uint32_t const rem = i - h * et * dchunks;
+            uint32_t const t = rem / dchunks;
+            uint32_t const dc = rem - t * dchunks;
+            uint4 const v = *reinterpret_cast<uint4 const*>(
+                src[t >> 3] + head_block(P, mt, layer, h) + (t & 7u) * D + dc * 8);
+            *reinterpret_cast<uint4*>(dst + head_block(P, et, layer, h) + t * D + dc * 8) = v;
+        }
+        // V^T: (h, d, k) -- micro row d (8 tokens, 16 bytes) -> extent row d at 8k.
+        uint32_t const vchunks = H * D * 8;
+        for (uint32_t i = tid; i < vchunks; i += kBlock) {
+            uint32_t const h = i / (D * 8);
+            uint32_t const rem = i - h * D * 8;
+            uint32_t const d = rem / 8;
+            uint32_t const k = rem & 7u;
+            uint4 const v = *reinterpret_cast<uint4 const*>(
+                src[k] + head_block(P, mt, layer, h) + mt * D + d * mt);
+            *reinterpret_cast<uint4*>(dst + head_block(P, et, layer, h) + et * D + d * et + 8 * k) = v;
+        }
+        return;
+    }
+    uint32_t const total = H * et * D;
+    for (uint32_t i = tid; i < total; i += kBlock) {
+        uint32_t const h = i / (et * D);
+        uint32_t const rem = i - h * et * D;
+        uint32_t const t = rem / D;
+        uint32_t const d = rem - t * D;
+        uint16_t const* s = src[t / mt];
+        uint32_t const st = t % mt;
+        uint64_t const sh = head_block(P, mt, layer, h);
+        uint64_t const dh = head_block(P, et, layer, h);
+        dst[dh + t * D + d] = s[sh + st * D + d];
+        dst[dh + static_cast<uint64_t>(et) * D + d * et + t] = s[sh + static_cast<uint64_t>(mt) * D + d * mt + st];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic fill of a table's pages: block = (64-token tile, layer, component).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBlock) void fill_table_kernel(PoolView P, const kimkv_block_desc* desc,
+                                                            uint32_t count, uint32_t token_begin,
+                                                            uint32_t token_end, uint64_t seed,
+                                                            uint32_t stream_id)
+{
+    __shared__ TokEntry tab[kTile];
+    __shared__ uint32_t s_idx;
+    uint32_t const t0 = token_begin + blockIdx.x * kTile;
+    uint32_t const n = min(kTile, token_end - t0);
+    uint32_t const layer = blockIdx.y;
+    uint32_t const comp = blockIdx.z;
+    build_tile_table(P, desc, count, t0, n, tab, &s_idx);
+    uint32_t const D = P.dim;
+    uint32_t const HD = P.heads * D;
+    uint32_t const tid = threadIdx.x;
+
+    if (comp == 0) {
+        for (uint32_t i = tid; i < n * HD; i += kBlock) {
+            uint32_t const t = i / HD;
+            uint32_t const r = i - t * HD;
+            TokEntry const e = tab[t];
+            if (e.page == nullptr) continue;
+            uint32_t const h = r / D;
+            uint32_t const d = r - h * D;
+            e.page[head_block(P, e.cap, layer, h) + static_cast<uint64_t>(e.pt) * D + d] =
+                synth_f16(seed, kv_row(stream_id, layer, 0, t0 + t), r);
+        }
+        return;
+    }
+    // V^T: thread per (row, token group of 8) with 16-byte stores when aligned.
+    uint32_t const groups = (n + 7) / 8;
+    for (uint32_t i = tid; i < HD * groups; i += kBlock) {
+        uint32_t const r = i / groups;
+        uint32_t const g = i - r * groups;
+        uint32_t const h = r / D;
+        uint32_t const d = r - h * D;
+        uint32_t const tb = g * 8;
+        uint32_t const te = min(tb + 8, n);
+        TokEntry const e = tab[tb];
+        bool const vec = te == tb + 8 && e.page != nullptr && (e.pt & 7u) == 0 && (e.cap & 7u) == 0
+            && tab[tb + 7].page == e.page && tab[tb + 7].pt == e.pt + 7;
+        if (vec) {
+            uint32_t w[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                uint32_t const lo = synth_f16(seed, kv_row(stream_id, layer, 1, t0 + tb + 2 * j), r);
+                uint32_t const hi = synth_f16(seed, kv_row(stream_id, layer, 1, t0 + tb + 2 * j + 1), r);
+                w[j] = lo | (hi << 16);
+            }
+            *reinterpret_cast<uint4*>(e.page + head_block(P, e.cap, layer, h)
+                                      + static_cast<uint64_t>(e.cap) * D + static_cast<uint64_t>(d) * e.cap + e.pt) =
+                make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+            for (uint32_t t = tb; t < te; ++t) {
+                TokEntry const f = tab[t];
+                if (f.page == nullptr) continue;
+                f.page[head_block(P, f.cap, layer, h) + static_cast<uint64_t>(f.cap) * D
+                       + static_cast<uint64_t>(d) * f.cap + f.pt] =
+                    synth_f16(seed, kv_row(stream_id, layer, 1, t0 + t), r);
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void fill_rows_kernel(uint16_t* out, uint64_t count, uint64_t seed,
+                                                           uint64_t row0, uint32_t cols)
+{
+    uint64_t const stride = static_cast<uint64_t>(gridDim.x) * kBlock;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; i < count; i += stride) {
+        out[i] = synth_f16(seed, row0 + i / cols, static_cast<uint32_t>(i % cols));
+    }
+}
+
+}  // namespace
+}  // namespace kimkv
+
+using namespace kimkv;
+
+extern "C" {
+
+kimkv_status kimkv_append_batch(const kimkv_storage* storage, const kimkv_append_job* device_jobs,
+                                uint32_t job_count, uint32_t max_layer_count, kimkv_stream_t stream)
+{
+    if (storage == nullptr || (job_count != 0 && device_jobs == nullptr)) return KIMKV_INVALID_ARGUMENT;
+    if (job_count == 0 || max_layer_count == 0) return KIMKV_OK;
+    if (max_layer_count > storage->layout.layers || job_count > 0x7FFFFFFFu) return KIMKV_INVALID_ARGUMENT;
+    dim3 const grid(job_count, max_layer_count);
+    append_kernel<<<grid, kBlock, 0, native(stream)>>>(pool_view(*storage), device_jobs, job_count);
+    return launch_status();
+}
+
+kimkv_status kimkv_gather(const kimkv_storage* storage, const kimkv_block_desc* device_descriptors,
+                          uint32_t descriptor_count, uint32_t total_tokens, uint16_t* device_output,
+                          kimkv_stream_t stream)
+{
+    if (storage == nullptr || device_descriptors == nullptr || device_output == nullptr
+        || descriptor_count == 0 || total_tokens == 0) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    dim3 const grid(ceil_div(total_tokens, kTile), storage->layout.layers, 2);
+    gather_kernel<<<grid, kBlock, 0, native(stream)>>>(pool_view(*storage), device_descriptors,
+                                                       descriptor_count, total_tokens, device_output);
+    return launch_status();
+}
+
+kimkv_status kimkv_promote_batch(const kimkv_storage* storage, const kimkv_promotion_job* device_jobs,
+                                 uint32_t job_count, kimkv_stream_t stream)
+{
+    if (storage == nullptr || (job_count != 0 && device_jobs == nullptr)) return KIMKV_INVALID_ARGUMENT;
+    if (job_count == 0) return KIMKV_OK;
+    if (static_cast<uint32_t>(storage->micro_tokens) * 8 != storage->extent_tokens) return KIMKV_INVALID_ARGUMENT;
+    dim3 const grid(job_count, storage->layout.layers);
+    promote_kernel<<<grid, kBlock, 0, native(stream)>>>(pool_view(*storage), device_jobs, job_count);
+    return launch_status();
+}
+
+kimkv_status kimkv_fill_table(const kimkv_storage* storage, const kimkv_block_desc* device_descriptors,
+                              uint32_t descriptor_count, uint32_t token_begin, uint32_t token_end,
+                              uint64_t seed, uint32_t stream_id, kimkv_stream_t stream)
+{
+    if (storage == nullptr || device_descriptors == nullptr || descriptor_count == 0 || token_end < token_begin) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    if (token_end == token_begin) return KIMKV_OK;
+    dim3 const grid(ceil_div(token_end - token_begin, kTile), storage->layout.layers, 2);
+    fill_table_kernel<<<grid, kBlock, 0, native(stream)>>>(pool_view(*storage), device_descriptors,
+                                                           descriptor_count, token_begin, token_end, seed,
+                                                           stream_id);
+    return launch_status();
+}
+
+kimkv_status kimkv_fill_rows(uint16_t* device_out, uint64_t count, uint64_t seed, uint64_t row0,
+                             uint32_t cols, kimkv_stream_t stream)
+{
+    if (device_out == nullptr || cols == 0) return KIMKV_INVALID_ARGUMENT;
+    if (count == 0) return KIMKV_OK;
+    uint64_t const blocks64 = (count + kBlock - 1) / kBlock;
+    unsigned const blocks = static_cast<unsigned>(blocks64 < 65536 ? blocks64 : 65536);
+    fill_rows_kernel<<<blocks, kBlock, 0, native(stream)>>>(device_out, count, seed, row0, cols);
+    return launch_status();
+}
+
+}  // extern "C"

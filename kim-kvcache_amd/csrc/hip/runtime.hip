@@ -1,0 +1,356 @@
+// runtime.hip -- C-ABI runtime wrappers and device pool storage.
+//
+// Storage follows CudaKvStorage (src/cuda/kv/storage.cpp:99-190): one device
+// allocation per pool, zero-filled, page pointer = base + slot * page_elements.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <limits>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "device_common.h"
+#include "runtime_internal.h"
+
+namespace kimkv {
+
+namespace {
+thread_local int g_last_native_error = 0;
+
+struct DecodeTiming {
+    std::mutex mutex;
+    bool enabled{false};
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+    double total_ms{0.0};
+    uint64_t launches{0};
+};
+
+DecodeTiming& timing()
+{
+    static DecodeTiming instance;
+    return instance;
+}
+
+void drain_locked(DecodeTiming& t)
+{
+    for (auto& pair : t.pending) {
+        if (hipEventSynchronize(pair.second) == hipSuccess) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, pair.first, pair.second) == hipSuccess) {
+                t.total_ms += ms;
+                t.launches += 1;
+            }
+        }
+        static_cast<void>(hipEventDestroy(pair.first));
+        static_cast<void>(hipEventDestroy(pair.second));
+    }
+    t.pending.clear();
+}
+}  // namespace
+
+kimkv_status record_error(hipError_t error, kimkv_status failure)
+{
+    if (error == hipSuccess) {
+        return KIMKV_OK;
+    }
+    g_last_native_error = static_cast<int>(error);
+    return failure;
+}
+
+void decode_timing_begin(hipStream_t stream, void** start)
+{
+    *start = nullptr;
+    DecodeTiming& t = timing();
+    std::lock_guard<std::mutex> lock(t.mutex);
+    if (!t.enabled) {
+        return;
+    }
+    hipEvent_t event = nullptr;
+    if (hipEventCreate(&event) == hipSuccess && hipEventRecord(event, stream) == hipSuccess) {
+        *start = event;
+    } else if (event != nullptr) {
+        static_cast<void>(hipEventDestroy(event));
+    }
+}
+
+void decode_timing_end(hipStream_t stream, void* start)
+{
+    if (start == nullptr) {
+        return;
+    }
+    DecodeTiming& t = timing();
+    std::lock_guard<std::mutex> lock(t.mutex);
+    hipEvent_t stop = nullptr;
+    if (hipEventCreate(&stop) == hipSuccess && hipEventRecord(stop, stream) == hipSuccess) {
+        t.pending.emplace_back(static_cast<hipEvent_t>(start), stop);
+    } else {
+        static_cast<void>(hipEventDestroy(static_cast<hipEvent_t>(start)));
+        if (stop != nullptr) {
+            static_cast<void>(hipEventDestroy(stop));
+        }
+    }
+}
+
+}  // namespace kimkv
+
+using kimkv::record_error;
+
+extern "C" {
+
+int kimkv_device_count(void)
+{
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess) {
+        return 0;
+    }
+    return count;
+}
+
+int kimkv_last_native_error(void) { return kimkv::g_last_native_error; }
+
+kimkv_status kimkv_device_malloc(void** ptr, size_t bytes)
+{
+    if (ptr == nullptr) return KIMKV_INVALID_ARGUMENT;
+    *ptr = nullptr;
+    if (bytes == 0) return KIMKV_OK;
+    return record_error(hipMalloc(ptr, bytes), KIMKV_ALLOCATION_FAILED);
+}
+
+kimkv_status kimkv_device_free(void* ptr)
+{
+    if (ptr == nullptr) return KIMKV_OK;
+    return record_error(hipFree(ptr), KIMKV_INTERNAL_ERROR);
+}
+
+kimkv_status kimkv_host_malloc_pinned(void** ptr, size_t bytes)
+{
+    if (ptr == nullptr) return KIMKV_INVALID_ARGUMENT;
+    *ptr = nullptr;
+    if (bytes == 0) return KIMKV_OK;
+    return record_error(hipHostMalloc(ptr, bytes, hipHostMallocDefault), KIMKV_ALLOCATION_FAILED);
+}
+
+kimkv_status kimkv_host_free_pinned(void* ptr)
+{
+    if (ptr == nullptr) return KIMKV_OK;
+    return record_error(hipHostFree(ptr), KIMKV_INTERNAL_ERROR);
+}
+
+kimkv_status kimkv_memcpy_h2d_async(void* dst, const void* src, size_t bytes, kimkv_stream_t stream)
+{
+    if (bytes == 0) return KIMKV_OK;
+    if (dst == nullptr || src == nullptr) return KIMKV_INVALID_ARGUMENT;
+    return record_error(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, kimkv::native(stream)),
+                        KIMKV_SUBMISSION_FAILED);
+}
+
+kimkv_status kimkv_memcpy_d2h_async(void* dst, const void* src, size_t bytes, kimkv_stream_t stream)
+{
+    if (bytes == 0) return KIMKV_OK;
+    if (dst == nullptr || src == nullptr) return KIMKV_INVALID_ARGUMENT;
+    return record_error(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, kimkv::native(stream)),
+                        KIMKV_SUBMISSION_FAILED);
+}
+
+kimkv_status kimkv_memcpy_d2d_async(void* dst, const void* src, size_t bytes, kimkv_stream_t stream)
+{
+    if (bytes == 0) return KIMKV_OK;
+    if (dst == nullptr || src == nullptr) return KIMKV_INVALID_ARGUMENT;
+    return record_error(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, kimkv::native(stream)),
+                        KIMKV_SUBMISSION_FAILED);
+}
+
+kimkv_status kimkv_stream_create(kimkv_stream_t* stream)
+{
+    if (stream == nullptr) return KIMKV_INVALID_ARGUMENT;
+    hipStream_t s = nullptr;
+    kimkv_status const status = record_error(hipStreamCreateWithFlags(&s, hipStreamNonBlocking),
+                                             KIMKV_RUNTIME_UNAVAILABLE);
+    *stream = s;
+    return status;
+}
+
+kimkv_status kimkv_stream_destroy(kimkv_stream_t stream)
+{
+    if (stream == nullptr) return KIMKV_OK;
+    return record_error(hipStreamDestroy(kimkv::native(stream)), KIMKV_INTERNAL_ERROR);
+}
+
+kimkv_status kimkv_stream_synchronize(kimkv_stream_t stream)
+{
+    return record_error(hipStreamSynchronize(kimkv::native(stream)), KIMKV_EXECUTION_FAILED);
+}
+
+kimkv_status kimkv_device_synchronize(void)
+{
+    return record_error(hipDeviceSynchronize(), KIMKV_EXECUTION_FAILED);
+}
+
+kimkv_status kimkv_event_create(void** event, int timing)
+{
+    if (event == nullptr) return KIMKV_INVALID_ARGUMENT;
+    hipEvent_t e = nullptr;
+    kimkv_status const status = record_error(
+        hipEventCreateWithFlags(&e, timing ? hipEventDefault : hipEventDisableTiming),
+        KIMKV_RUNTIME_UNAVAILABLE);
+    *event = e;
+    return status;
+}
+
+kimkv_status kimkv_event_destroy(void* event)
+{
+    if (event == nullptr) return KIMKV_OK;
+    return record_error(hipEventDestroy(static_cast<hipEvent_t>(event)), KIMKV_INTERNAL_ERROR);
+}
+
+kimkv_status kimkv_event_record(void* event, kimkv_stream_t stream)
+{
+    if (event == nullptr) return KIMKV_INVALID_ARGUMENT;
+    return record_error(hipEventRecord(static_cast<hipEvent_t>(event), kimkv::native(stream)),
+                        KIMKV_SUBMISSION_FAILED);
+}
+
+kimkv_status kimkv_event_query(void* event)
+{
+    if (event == nullptr) return KIMKV_INVALID_ARGUMENT;
+    hipError_t const e = hipEventQuery(static_cast<hipEvent_t>(event));
+    if (e == hipErrorNotReady) return KIMKV_NOT_READY;
+    return record_error(e, KIMKV_EXECUTION_FAILED);
+}
+
+kimkv_status kimkv_event_synchronize(void* event)
+{
+    if (event == nullptr) return KIMKV_INVALID_ARGUMENT;
+    return record_error(hipEventSynchronize(static_cast<hipEvent_t>(event)), KIMKV_EXECUTION_FAILED);
+}
+
+kimkv_status kimkv_event_elapsed_ms(float* ms, void* start, void* stop)
+{
+    if (ms == nullptr || start == nullptr || stop == nullptr) return KIMKV_INVALID_ARGUMENT;
+    return record_error(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
+                        KIMKV_EXECUTION_FAILED);
+}
+
+kimkv_status kimkv_storage_create(kimkv_storage** out, kimkv_layout layout, uint32_t micro_capacity,
+                                  uint32_t extent_capacity, uint16_t micro_page_tokens,
+                                  uint16_t extent_page_tokens)
+{
+    if (out == nullptr) return KIMKV_INVALID_ARGUMENT;
+    *out = nullptr;
+    if (layout.layers == 0 || layout.kv_heads == 0 || layout.head_dim == 0
+        || micro_page_tokens == 0 || extent_page_tokens == 0 || layout.layers > 0x7FFFu) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    uint64_t const per_token = 2ull * layout.layers * layout.kv_heads * layout.head_dim;
+    uint64_t const micro_elems = per_token * micro_page_tokens;
+    uint64_t const extent_elems = per_token * extent_page_tokens;
+    uint64_t const limit = std::numeric_limits<uint64_t>::max() / 4;
+    if ((micro_capacity != 0 && micro_elems > limit / micro_capacity)
+        || (extent_capacity != 0 && extent_elems > limit / extent_capacity)) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+        return KIMKV_RUNTIME_UNAVAILABLE;
+    }
+    auto* s = new (std::nothrow) kimkv_storage{};
+    if (s == nullptr) return KIMKV_ALLOCATION_FAILED;
+    s->layout = layout;
+    s->micro_capacity = micro_capacity;
+    s->extent_capacity = extent_capacity;
+    s->micro_tokens = micro_page_tokens;
+    s->extent_tokens = extent_page_tokens;
+    s->micro_page_elements = micro_elems;
+    s->extent_page_elements = extent_elems;
+    hipError_t e = hipGetDevice(&s->device);
+    if (e == hipSuccess) {
+        e = hipDeviceGetAttribute(&s->compute_units, hipDeviceAttributeMultiprocessorCount, s->device);
+    }
+    uint64_t const micro_bytes = micro_elems * micro_capacity * 2ull;
+    uint64_t const extent_bytes = extent_elems * extent_capacity * 2ull;
+    if (e == hipSuccess && micro_bytes != 0) {
+        e = hipMalloc(reinterpret_cast<void**>(&s->micro), micro_bytes);
+        if (e == hipSuccess) e = hipMemset(s->micro, 0, micro_bytes);
+    }
+    if (e == hipSuccess && extent_bytes != 0) {
+        e = hipMalloc(reinterpret_cast<void**>(&s->extent), extent_bytes);
+        if (e == hipSuccess) e = hipMemset(s->extent, 0, extent_bytes);
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        record_error(e, KIMKV_ALLOCATION_FAILED);
+        if (s->micro) static_cast<void>(hipFree(s->micro));
+        if (s->extent) static_cast<void>(hipFree(s->extent));
+        delete s;
+        return KIMKV_ALLOCATION_FAILED;
+    }
+    *out = s;
+    return KIMKV_OK;
+}
+
+kimkv_status kimkv_storage_destroy(kimkv_storage* storage)
+{
+    if (storage == nullptr) return KIMKV_OK;
+    // In-flight work may still read the pools (storage.cpp:22-32 waits too).
+    static_cast<void>(hipDeviceSynchronize());
+    if (storage->micro) static_cast<void>(hipFree(storage->micro));
+    if (storage->extent) static_cast<void>(hipFree(storage->extent));
+    delete storage;
+    return KIMKV_OK;
+}
+
+kimkv_status kimkv_storage_query(const kimkv_storage* s, kimkv_storage_info* info)
+{
+    if (s == nullptr || info == nullptr) return KIMKV_INVALID_ARGUMENT;
+    info->layout = s->layout;
+    info->micro_capacity = s->micro_capacity;
+    info->extent_capacity = s->extent_capacity;
+    info->micro_page_tokens = s->micro_tokens;
+    info->extent_page_tokens = s->extent_tokens;
+    info->micro_page_elements = s->micro_page_elements;
+    info->extent_page_elements = s->extent_page_elements;
+    info->micro_reserved_bytes = s->micro_page_elements * s->micro_capacity * 2ull;
+    info->extent_reserved_bytes = s->extent_page_elements * s->extent_capacity * 2ull;
+    info->device = s->device;
+    info->compute_units = s->compute_units;
+    return KIMKV_OK;
+}
+
+uint16_t* kimkv_storage_page(const kimkv_storage* s, uint32_t kind, uint32_t slot)
+{
+    if (s == nullptr) return nullptr;
+    if (kind == KIMKV_PAGE_MICRO && slot < s->micro_capacity && s->micro != nullptr) {
+        return s->micro + static_cast<uint64_t>(slot) * s->micro_page_elements;
+    }
+    if (kind == KIMKV_PAGE_EXTENT && slot < s->extent_capacity && s->extent != nullptr) {
+        return s->extent + static_cast<uint64_t>(slot) * s->extent_page_elements;
+    }
+    return nullptr;
+}
+
+uint16_t kimkv_synth_value(uint64_t seed, uint64_t row, uint32_t col)
+{
+    float const x = static_cast<float>(kimkv::synth_int(seed, row, col)) * (1.0f / 32768.0f);
+    return __half_as_ushort(__float2half(x));
+}
+
+uint64_t kimkv_synth_kv_row(uint32_t stream, uint32_t layer, uint32_t component, uint32_t token)
+{
+    return kimkv::kv_row(stream, layer, component, token);
+}
+
+kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launches)
+{
+    kimkv::DecodeTiming& t = kimkv::timing();
+    std::lock_guard<std::mutex> lock(t.mutex);
+    kimkv::drain_locked(t);
+    if (total_ms != nullptr) *total_ms = t.total_ms;
+    if (launches != nullptr) *launches = t.launches;
+    t.total_ms = 0.0;
+    t.launches = 0;
+    t.enabled = enable != 0;
+    return KIMKV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,357 @@
+"""ctypes binding of the device C-ABI (include/kimkv_hip.h).
+
+This is the Python-side binding a maintainer would add for the data path.
+It loads the in-tree libkimkv_hip.so and fails loudly when it is missing:
+there is no CPU fallback.  Device memory, streams and events come from the
+library itself (numpy holds host data), so no second HIP runtime is loaded.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "_lib", "libkimkv_hip.so")
+
+OK = 0
+STATUS_NAMES = {
+    0: "ok", 1: "invalid_argument", 2: "runtime_unavailable", 3: "allocation_failed",
+    4: "submission_failed", 5: "not_ready", 6: "execution_failed", 7: "internal_error",
+}
+PAGE_MICRO = 0
+PAGE_EXTENT = 1
+
+# numpy views of the C structs (field order, offsets and sizes of kimkv_hip.h).
+BLOCK_DESC = np.dtype({
+    "names": ["slot", "generation", "logical_token_begin", "valid_tokens", "page_token_capacity", "kind"],
+    "formats": ["<u4", "<u4", "<u4", "<u2", "<u2", "u1"],
+    "offsets": [0, 4, 8, 12, 14, 16],
+    "itemsize": 20,
+})
+DECODE_ITEM = np.dtype({
+    "names": ["descriptors", "descriptor_count", "token_count", "layer", "query", "workspace", "output",
+              "attention_scale"],
+    "formats": ["<u8", "<u4", "<u4", "<u4", "<u8", "<u8", "<u8", "<f4"],
+    "offsets": [0, 8, 12, 16, 24, 32, 40, 48],
+    "itemsize": 56,
+})
+APPEND_JOB = np.dtype({
+    "names": ["src_key", "src_value", "src_layer_stride", "src_token_stride", "layer_begin", "layer_count",
+              "token_count", "dst_slot", "cow_slot", "dst_token", "cow_tokens", "dst_kind", "cow_kind"],
+    "formats": ["<u8", "<u8", "<u8", "<u4", "<u4", "<u4", "<u4", "<u4", "<u4", "<u2", "<u2", "u1", "u1"],
+    "offsets": [0, 8, 16, 24, 28, 32, 36, 40, 44, 48, 50, 52, 53],
+    "itemsize": 56,
+})
+PROMOTION_JOB = np.dtype({
+    "names": ["micro_slots", "extent_slot"],
+    "formats": [("<u4", (8,)), "<u4"],
+    "offsets": [0, 32],
+    "itemsize": 36,
+})
+
+
+class KimkvError(RuntimeError):
+    def __init__(self, where: str, status: int, native: int = 0):
+        super().__init__(f"{where}: {STATUS_NAMES.get(status, status)} (native {native})")
+        self.status = status
+
+
+class Layout(ctypes.Structure):
+    _fields_ = [("layers", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32)]
+
+
+class StorageInfo(ctypes.Structure):
+    _fields_ = [
+        ("layout", Layout), ("micro_capacity", ctypes.c_uint32), ("extent_capacity", ctypes.c_uint32),
+        ("micro_page_tokens", ctypes.c_uint16), ("extent_page_tokens", ctypes.c_uint16),
+        ("micro_page_elements", ctypes.c_uint64), ("extent_page_elements", ctypes.c_uint64),
+        ("micro_reserved_bytes", ctypes.c_uint64), ("extent_reserved_bytes", ctypes.c_uint64),
+        ("device", ctypes.c_int), ("compute_units", ctypes.c_int),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+_SIGNATURES = {
+    "kimkv_device_count": (ctypes.c_int, []),
+    "kimkv_last_native_error": (ctypes.c_int, []),
+    "kimkv_device_malloc": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]),
+    "kimkv_device_free": (ctypes.c_int, [ctypes.c_void_p]),
+    "kimkv_host_malloc_pinned": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]),
+    "kimkv_host_free_pinned": (ctypes.c_int, [ctypes.c_void_p]),
+    "kimkv_memcpy_h2d_async": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "kimkv_memcpy_d2h_async": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "kimkv_memcpy_d2d_async": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "kimkv_stream_create": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p)]),
+    "kimkv_stream_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "kimkv_stream_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
+    "kimkv_device_synchronize": (ctypes.c_int, []),
+    "kimkv_event_create": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int]),
+    "kimkv_event_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "kimkv_event_record": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "kimkv_event_query": (ctypes.c_int, [ctypes.c_void_p]),
+    "kimkv_event_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
+    "kimkv_event_elapsed_ms": (ctypes.c_int, [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]),
+    "kimkv_storage_create": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), Layout, ctypes.c_uint32,
+                                            ctypes.c_uint32, ctypes.c_uint16, ctypes.c_uint16]),
+    "kimkv_storage_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "kimkv_storage_query": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(StorageInfo)]),
+    "kimkv_storage_page": (ctypes.c_void_p, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32]),
+    "kimkv_append_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                          ctypes.c_void_p]),
+    "kimkv_gather": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                    ctypes.c_void_p, ctypes.c_void_p]),
+    "kimkv_promote_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_decode_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                         ctypes.POINTER(ctypes.c_uint32), ctypes.c_void_p,
+                                         ctypes.POINTER(ctypes.c_uint32)]),
+    "kimkv_decode_workspace_bytes": (ctypes.c_size_t, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                                       ctypes.c_uint32]),
+    "kimkv_paged_decode_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                                ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_decode_timing": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                           ctypes.POINTER(ctypes.c_uint64)]),
+    "kimkv_synth_value": (ctypes.c_uint16, [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32]),
+    "kimkv_synth_kv_row": (ctypes.c_uint64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
+    "kimkv_fill_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
+                                       ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_fill_table": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                        ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_void_p]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+
+def lib() -> ctypes.CDLL:
+    """Load libkimkv_hip.so (raises when it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def check(status: int, where: str) -> None:
+    if status != OK:
+        raise KimkvError(where, status, lib().kimkv_last_native_error())
+
+
+def device_count() -> int:
+    return lib().kimkv_device_count()
+
+
+class DeviceBuffer:
+    """Owning device allocation."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        ptr = ctypes.c_void_p()
+        check(lib().kimkv_device_malloc(ctypes.byref(ptr), self.nbytes), "device_malloc")
+        self.ptr = ptr.value or 0
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().kimkv_device_free(ctypes.c_void_p(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        handle = ctypes.c_void_p()
+        check(lib().kimkv_stream_create(ctypes.byref(handle)), "stream_create")
+        self.handle = handle.value
+
+    def synchronize(self) -> None:
+        check(lib().kimkv_stream_synchronize(ctypes.c_void_p(self.handle)), "stream_synchronize")
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().kimkv_stream_destroy(ctypes.c_void_p(self.handle))
+            self.handle = None
+
+
+class Event:
+    def __init__(self, timing: bool = True):
+        handle = ctypes.c_void_p()
+        check(lib().kimkv_event_create(ctypes.byref(handle), 1 if timing else 0), "event_create")
+        self.handle = handle.value
+
+    def record(self, stream: Optional[Stream]) -> None:
+        check(lib().kimkv_event_record(ctypes.c_void_p(self.handle), _sh(stream)), "event_record")
+
+    def synchronize(self) -> None:
+        check(lib().kimkv_event_synchronize(ctypes.c_void_p(self.handle)), "event_synchronize")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        check(lib().kimkv_event_elapsed_ms(ctypes.byref(ms), ctypes.c_void_p(self.handle),
+                                           ctypes.c_void_p(end.handle)), "event_elapsed")
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().kimkv_event_destroy(ctypes.c_void_p(self.handle))
+        except Exception:
+            pass
+
+
+def _sh(stream: Optional[Stream]):
+    return ctypes.c_void_p(stream.handle if stream is not None else None)
+
+
+def upload(array: np.ndarray, stream: Optional[Stream] = None) -> DeviceBuffer:
+    array = np.ascontiguousarray(array)
+    buf = DeviceBuffer(max(array.nbytes, 1))
+    if array.nbytes:
+        check(lib().kimkv_memcpy_h2d_async(ctypes.c_void_p(buf.ptr), array.ctypes.data_as(ctypes.c_void_p),
+                                           array.nbytes, _sh(stream)), "h2d")
+        sync(stream)
+    return buf
+
+
+def copy_to_device(dst_ptr: int, array: np.ndarray, stream: Optional[Stream] = None) -> None:
+    array = np.ascontiguousarray(array)
+    check(lib().kimkv_memcpy_h2d_async(ctypes.c_void_p(dst_ptr), array.ctypes.data_as(ctypes.c_void_p),
+                                       array.nbytes, _sh(stream)), "h2d")
+    sync(stream)
+
+
+def download(src_ptr: int, shape, dtype, stream: Optional[Stream] = None) -> np.ndarray:
+    out = np.empty(shape, dtype=dtype)
+    if out.nbytes:
+        check(lib().kimkv_memcpy_d2h_async(out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(src_ptr),
+                                           out.nbytes, _sh(stream)), "d2h")
+        sync(stream)
+    return out
+
+
+def sync(stream: Optional[Stream] = None) -> None:
+    if stream is None:
+        check(lib().kimkv_device_synchronize(), "device_synchronize")
+    else:
+        stream.synchronize()
+
+
+def synth_value(seed: int, row: int, col: int) -> int:
+    return int(lib().kimkv_synth_value(seed, row, col))
+
+
+def synth_kv_row(stream_id: int, layer: int, component: int, token: int) -> int:
+    return int(lib().kimkv_synth_kv_row(stream_id, layer, component, token))
+
+
+def fill_rows(ptr: int, count: int, seed: int, row0: int, cols: int, stream: Optional[Stream] = None) -> None:
+    check(lib().kimkv_fill_rows(ctypes.c_void_p(ptr), count, seed, row0, cols, _sh(stream)), "fill_rows")
+
+
+class Storage:
+    """Device page pools (kimkv_storage)."""
+
+    def __init__(self, layers: int, kv_heads: int, head_dim: int, micro_capacity: int, extent_capacity: int,
+                 micro_tokens: int = 8, extent_tokens: int = 64):
+        handle = ctypes.c_void_p()
+        check(lib().kimkv_storage_create(ctypes.byref(handle), Layout(layers, kv_heads, head_dim),
+                                         micro_capacity, extent_capacity, micro_tokens, extent_tokens),
+              "storage_create")
+        self.handle = handle.value
+        self.layers, self.kv_heads, self.head_dim = layers, kv_heads, head_dim
+        self.micro_tokens, self.extent_tokens = micro_tokens, extent_tokens
+
+    @property
+    def h(self):
+        return ctypes.c_void_p(self.handle)
+
+    def info(self) -> StorageInfo:
+        info = StorageInfo()
+        check(lib().kimkv_storage_query(self.h, ctypes.byref(info)), "storage_query")
+        return info
+
+    def page(self, kind: int, slot: int) -> int:
+        return lib().kimkv_storage_page(self.h, kind, slot) or 0
+
+    def append_batch(self, jobs: np.ndarray, stream: Optional[Stream] = None) -> None:
+        jobs = np.ascontiguousarray(jobs, dtype=APPEND_JOB)
+        if len(jobs) == 0:
+            return
+        dev = upload(jobs, stream)
+        check(lib().kimkv_append_batch(self.h, ctypes.c_void_p(dev.ptr), len(jobs),
+                                       int(jobs["layer_count"].max()), _sh(stream)), "append_batch")
+        sync(stream)
+
+    def gather(self, descs: np.ndarray, total_tokens: int, stream: Optional[Stream] = None) -> np.ndarray:
+        descs = np.ascontiguousarray(descs, dtype=BLOCK_DESC)
+        d = upload(descs, stream)
+        n = self.layers * 2 * total_tokens * self.kv_heads * self.head_dim
+        out = DeviceBuffer(n * 2)
+        check(lib().kimkv_gather(self.h, ctypes.c_void_p(d.ptr), len(descs), total_tokens,
+                                 ctypes.c_void_p(out.ptr), _sh(stream)), "gather")
+        return download(out.ptr, (n,), np.uint16, stream)
+
+    def promote_batch(self, jobs: np.ndarray, stream: Optional[Stream] = None) -> None:
+        jobs = np.ascontiguousarray(jobs, dtype=PROMOTION_JOB)
+        if len(jobs) == 0:
+            return
+        dev = upload(jobs, stream)
+        check(lib().kimkv_promote_batch(self.h, ctypes.c_void_p(dev.ptr), len(jobs), _sh(stream)), "promote")
+        sync(stream)
+
+    def fill_table(self, descs_ptr: int, count: int, token_begin: int, token_end: int, seed: int,
+                   stream_id: int, stream: Optional[Stream] = None) -> None:
+        check(lib().kimkv_fill_table(self.h, ctypes.c_void_p(descs_ptr), count, token_begin, token_end, seed,
+                                     stream_id, _sh(stream)), "fill_table")
+
+    def decode_plan(self, token_counts, query_heads: int):
+        counts = np.ascontiguousarray(np.asarray(token_counts, dtype=np.uint32))
+        prefix = np.zeros(len(counts) + 1, dtype=np.uint32)
+        chunk = ctypes.c_uint32()
+        total = ctypes.c_uint32()
+        check(lib().kimkv_decode_plan(self.h, counts.ctypes.data_as(ctypes.c_void_p), len(counts), query_heads,
+                                      ctypes.byref(chunk), prefix.ctypes.data_as(ctypes.c_void_p),
+                                      ctypes.byref(total)), "decode_plan")
+        return int(chunk.value), prefix, int(total.value)
+
+    def decode_launch(self, items_ptr: int, prefix_ptr: int, lanes: int, total_chunks: int, chunk_tokens: int,
+                      query_heads: int, stream: Optional[Stream] = None) -> None:
+        check(lib().kimkv_paged_decode_batch(self.h, ctypes.c_void_p(items_ptr), ctypes.c_void_p(prefix_ptr),
+                                             lanes, total_chunks, chunk_tokens, query_heads, _sh(stream)),
+              "paged_decode_batch")
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().kimkv_storage_destroy(self.h)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+def workspace_bytes(token_count: int, chunk_tokens: int, query_heads: int, head_dim: int) -> int:
+    return int(lib().kimkv_decode_workspace_bytes(token_count, chunk_tokens, query_heads, head_dim))
+
+
+def decode_timing(enable: bool):
+    total = ctypes.c_double()
+    launches = ctypes.c_uint64()
+    check(lib().kimkv_decode_timing(1 if enable else 0, ctypes.byref(total), ctypes.byref(launches)),
+          "decode_timing")
+    return float(total.value), int(launches.value)

@@ -1,0 +1,225 @@
+"""GPU parity of every data-path kernel against the CPU oracle.
+
+Integer/byte work (append, COW, promotion, gather, synthetic fill) must be
+bit-exact.  Decode attention must satisfy |gpu - ref| <= 2e-3 + 1e-3*|ref|
+against the oracle's fp32-accumulated result on the same seeded inputs.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests import helpers
+
+pytestmark = pytest.mark.gpu
+
+TINYLLAMA = dict(layers=22, kv_heads=4, head_dim=64)
+
+
+def _input(L, H, D, T, seed):
+    """Contiguous [L][2][T][H][D] synthetic input (fp16 codes)."""
+    return oracle.synth_rows(L * 2 * T * H * D, seed, 0, H * D).reshape(L, 2, T, H, D)
+
+
+def _append_jobs(dev, table, inp_ptr, T, L, H, D):
+    jobs = np.zeros(len(table), dtype=dev.APPEND_JOB)
+    hd = H * D
+    for i, e in enumerate(table):
+        b = int(e["logical_token_begin"])
+        jobs[i]["src_key"] = inp_ptr + 2 * b * hd
+        jobs[i]["src_value"] = inp_ptr + 2 * (T + b) * hd
+        jobs[i]["src_layer_stride"] = 2 * T * hd
+        jobs[i]["src_token_stride"] = hd
+        jobs[i]["layer_begin"] = 0
+        jobs[i]["layer_count"] = L
+        jobs[i]["token_count"] = int(e["valid_tokens"])
+        jobs[i]["dst_slot"] = int(e["slot"])
+        jobs[i]["dst_kind"] = int(e["kind"])
+        jobs[i]["dst_token"] = 0
+    return jobs
+
+
+def _populate(dev, storage, pools, table, inp):
+    L, _, T, H, D = inp.shape
+    buf = dev.upload(inp)
+    storage.append_batch(_append_jobs(dev, table, buf.ptr, T, L, H, D))
+    for e in table:
+        pools.append_tokens(inp, T, int(e["logical_token_begin"]), int(e["kind"]), int(e["slot"]), 0,
+                            int(e["valid_tokens"]))
+    return buf
+
+
+@pytest.mark.parametrize("shape,T", [((2, 2, 8), 70), ((22, 4, 64), 300), ((3, 1, 12), 9)])
+def test_append_gather_bit_exact(dev, shape, T):
+    L, H, D = shape
+    print(f"append/gather L={L} H={H} D={D} T={T}", flush=True)
+    storage = dev.Storage(L, H, D, 64, 8)
+    pools = oracle.HostPools(L, H, D, 64, 8)
+    table = helpers.hetero_table(T, helpers.SlotAllocator(64, 8, seed=T))
+    inp = _input(L, H, D, T, seed=11)
+    _populate(dev, storage, pools, table, inp)
+    got = storage.gather(table, T)
+    assert np.array_equal(got, inp.reshape(-1))
+    assert np.array_equal(got, pools.gather(table, T))
+
+
+def test_fill_rows_matches_oracle(dev):
+    n = 100003
+    buf = dev.DeviceBuffer(n * 2)
+    dev.fill_rows(buf.ptr, n, 77, 5, 256)
+    got = dev.download(buf.ptr, (n,), np.uint16)
+    assert np.array_equal(got, oracle.synth_rows(n, 77, 5, 256))
+
+
+def test_fill_table_matches_generator(dev):
+    L, H, D = 4, 4, 64
+    T = 333
+    storage = dev.Storage(L, H, D, 64, 8)
+    table = helpers.hetero_table(T, helpers.SlotAllocator(64, 8, seed=3))
+    d = dev.upload(table)
+    storage.fill_table(d.ptr, len(table), 0, T, 99, 5)
+    dev.sync()
+    got = storage.gather(table, T).reshape(L, 2, T, H * D)
+    want = np.empty_like(got)
+    for l in range(L):
+        for c in range(2):
+            for t in range(T):
+                want[l, c, t] = oracle.synth_rows(H * D, 99, oracle.kv_row(5, l, c, t), H * D)
+    assert np.array_equal(got, want)
+
+
+def test_single_token_append_with_cow(dev):
+    """Engine-style per-layer write into a COW-replaced partial tail
+    (src/cuda/engine/transaction.cpp:158-204)."""
+    L, H, D = 22, 4, 64
+    storage = dev.Storage(L, H, D, 32, 4)
+    pools = oracle.HostPools(L, H, D, 32, 4)
+    T = 13                                              # pages [0,8) [8,13)
+    table = np.array([(3, 1, 0, 8, 8, 0), (9, 1, 8, 5, 8, 0)], dtype=helpers.DESC)
+    inp = _input(L, H, D, T, seed=5)
+    _populate(dev, storage, pools, table, inp)
+    new_kv = oracle.synth_rows(L * 2 * H * D, 123, 0, H * D).reshape(L, 2, H * D)
+    buf = dev.upload(new_kv)
+    jobs = np.zeros(L, dtype=dev.APPEND_JOB)
+    for l in range(L):                                   # one job per layer, COW 5 tokens 9 -> 17
+        jobs[l] = (buf.ptr + 2 * (l * 2) * H * D, buf.ptr + 2 * (l * 2 + 1) * H * D, 0, 0, l, 1, 1,
+                   17, 9, 5, 5, 0, 0)
+    storage.append_batch(jobs)
+    for l in range(L):
+        pools.copy_layer_tokens(0, 9, 0, 17, 5, l)
+        pools.write_layer_token(0, 17, 5, l, new_kv[l, 0], new_kv[l, 1])
+    after = np.array([(3, 1, 0, 8, 8, 0), (17, 1, 8, 6, 8, 0)], dtype=helpers.DESC)
+    got = storage.gather(after, 14)
+    assert np.array_equal(got, pools.gather(after, 14))
+    # The shared source tail is untouched.
+    assert np.array_equal(storage.gather(table, T), inp.reshape(-1))
+
+
+def test_promotion_bit_exact(dev):
+    L, H, D = 22, 4, 64
+    storage = dev.Storage(L, H, D, 32, 4)
+    pools = oracle.HostPools(L, H, D, 32, 4)
+    T = 70
+    slots = [5, 2, 9, 30, 11, 0, 17, 23, 8]
+    table = np.array([(slots[i], 1, 8 * i, min(8, T - 8 * i), 8, 0) for i in range(9)], dtype=helpers.DESC)
+    inp = _input(L, H, D, T, seed=21)
+    _populate(dev, storage, pools, table, inp)
+    jobs = np.zeros(1, dtype=dev.PROMOTION_JOB)
+    jobs[0]["micro_slots"] = slots[:8]
+    jobs[0]["extent_slot"] = 3
+    storage.promote_batch(jobs)
+    pools.promote(slots[:8], 3)
+    promoted = np.array([(3, 1, 0, 64, 64, 1), (slots[8], 1, 64, 6, 8, 0)], dtype=helpers.DESC)
+    got = storage.gather(promoted, T)
+    assert np.array_equal(got, inp.reshape(-1))
+    assert np.array_equal(got, pools.gather(promoted, T))
+
+
+# ---- decode ---------------------------------------------------------------------
+
+def _run_decode(dev, storage, lanes, query_heads, stream=None):
+    """lanes: list of (desc array, token_count, layer, query codes, scale)."""
+    counts = [t for (_, t, _, _, _) in lanes]
+    chunk, prefix, total = storage.decode_plan(counts, query_heads)
+    keep = []
+    items = np.zeros(len(lanes), dtype=dev.DECODE_ITEM)
+    outs = []
+    for i, (table, T, layer, q, scale) in enumerate(lanes):
+        dbuf = dev.upload(table)
+        qbuf = dev.upload(q)
+        obuf = dev.DeviceBuffer(query_heads * storage.head_dim * 2)
+        wsz = dev.workspace_bytes(T, chunk, query_heads, storage.head_dim)
+        wbuf = dev.DeviceBuffer(max(wsz, 4))
+        items[i] = (dbuf.ptr, len(table), T, layer, qbuf.ptr, wbuf.ptr if wsz else 0, obuf.ptr, scale)
+        keep += [dbuf, qbuf, wbuf]
+        outs.append(obuf)
+    ibuf = dev.upload(items)
+    pbuf = dev.upload(prefix)
+    storage.decode_launch(ibuf.ptr, pbuf.ptr, len(lanes), total, chunk, query_heads, stream)
+    dev.sync(stream)
+    return [dev.download(o.ptr, (query_heads * storage.head_dim,), np.uint16) for o in outs], chunk, total
+
+
+def _decode_case(dev, shape, token_counts, G, micro_tokens=8, extent_tokens=64, layer=None, seed=1,
+                 uniform_pages=None):
+    L, H, D = shape
+    QH = H * G
+    micro_cap = sum(t // micro_tokens + 2 for t in token_counts) + 8
+    ext_cap = sum(t // extent_tokens + 1 for t in token_counts) + 2
+    storage = dev.Storage(L, H, D, micro_cap, ext_cap, micro_tokens, extent_tokens)
+    pools = oracle.HostPools(L, H, D, micro_cap, ext_cap, micro_tokens, extent_tokens)
+    alloc = helpers.SlotAllocator(micro_cap, ext_cap, seed=seed, micro_tokens=micro_tokens,
+                                  extent_tokens=extent_tokens)
+    lanes = []
+    keep = []
+    for i, T in enumerate(token_counts):
+        if uniform_pages:
+            table = helpers.uniform_table(T, micro_tokens, alloc)
+        else:
+            table = helpers.hetero_table(T, alloc)
+        inp = _input(L, H, D, T, seed=seed * 100 + i)
+        keep.append(_populate(dev, storage, pools, table, inp))
+        q = oracle.synth_rows(QH * D, seed * 1000 + i, 0, D)
+        lay = (i * 7) % L if layer is None else layer
+        lanes.append((table, T, lay, q, 1.0 / math.sqrt(D)))
+    outs, chunk, total = _run_decode(dev, storage, lanes, QH)
+    worst = 0.0
+    for (table, T, lay, q, scale), got in zip(lanes, outs):
+        want = pools.paged_decode(table, T, lay, QH, q, scale, f32=True)
+        worst = max(worst, helpers.assert_attention_close(got, want))
+    print(f"decode shape={shape} G={G} T={token_counts} chunk={chunk} chunks={total} max_err={worst:.2e}",
+          flush=True)
+    return chunk, total
+
+
+def test_decode_config1_tinyllama(dev):
+    """One TinyLlama layer, 4 lanes at {17,100,513,1000} + 1 appended token."""
+    _decode_case(dev, (1, 4, 64), [18, 101, 514, 1001], G=8, layer=0)
+
+
+def test_decode_single_token_lane_is_value(dev):
+    _decode_case(dev, (2, 4, 64), [1, 2, 7, 8, 9, 63, 64, 65], G=8)
+
+
+def test_decode_split_k_long_lanes(dev):
+    chunk, total = _decode_case(dev, (22, 4, 64), [4000, 9000, 300, 12345], G=8, seed=4)
+    assert total > 4          # several lanes split across chunks -> combine path
+
+
+def test_decode_group_sizes_fast_path(dev):
+    _decode_case(dev, (2, 2, 64), [130, 700], G=16, seed=6)
+    _decode_case(dev, (2, 8, 64), [70, 333], G=1, seed=7)
+
+
+def test_decode_generic_head_dim(dev):
+    # The reference contract layouts {L=2,H=2,D=8} (tests/cuda/cuda_kv_test.cpp:668) and D=2 GQA.
+    _decode_case(dev, (2, 2, 8), [5, 70, 600], G=2, seed=8)
+    _decode_case(dev, (2, 1, 2), [3, 12], G=2, seed=9)
+    _decode_case(dev, (1, 2, 128), [90, 1500], G=4, seed=10)
+
+
+def test_decode_unaligned_pages_generic(dev):
+    # 6-token pages: tables not 8-aligned take the generic path.
+    _decode_case(dev, (2, 4, 64), [17, 200, 3000], G=8, micro_tokens=6, extent_tokens=48, seed=12,
+                 uniform_pages=True)
