@@ -1,0 +1,351 @@
+"""Paged GQA decode attention + KV append on one MI355X.
+
+Workload (the HBM-scale decode configuration): 256 lanes, each with a
+32768-token TinyLlama-shaped context (22 layers, 4 KV heads x 64 dims fp16,
+32 query heads) held in 64-token extent pages whose slot ids are a seeded
+permutation of the pool (~189 GB of KV), plus trailing 8-token micro pages
+for the appended tokens.  One step = for every layer: append one new K/V token
+per lane (one batched kernel) then fused split-K GQA decode attention for all
+lanes (one kernel + merge), i.e. 22 x (append + decode) launches, with the
+per-step page-table update and upload included.
+
+Prints one JSON line (see the contract in the repository's docs).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+from _loader import load_package  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def permutation(seed: int, n: int) -> np.ndarray:
+    """splitmix64 Fisher-Yates (kimkv_seeded_permutation), vectorised over the draws."""
+    mask = np.uint64(0xFFFFFFFFFFFFFFFF)
+    steps = np.arange(1, n, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = (np.uint64(seed) + steps * np.uint64(0x9E3779B97F4A7C15)) & mask
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    out = np.arange(n, dtype=np.uint32)
+    bounds = np.arange(n, 1, -1, dtype=np.uint64)
+    js = (z % bounds).astype(np.int64)
+    for k, i in enumerate(range(n, 1, -1)):
+        j = js[k]
+        out[i - 1], out[j] = out[j], out[i - 1]
+    return out
+
+
+class Workload:
+    def __init__(self, dev, lanes, context, layers, kv_heads, head_dim, query_heads, total_steps, seed):
+        self.dev = dev
+        self.lanes, self.context, self.L = lanes, context, layers
+        self.H, self.D, self.QH = kv_heads, head_dim, query_heads
+        self.total_steps = total_steps
+        self.seed = seed
+        self.ext_per_lane = context // 64
+        assert context % 64 == 0
+        self.micro_per_lane = (total_steps + 7) // 8
+        self.max_entries = self.ext_per_lane + self.micro_per_lane
+        n_ext = lanes * self.ext_per_lane
+        n_micro = lanes * self.micro_per_lane + 8
+        t0 = time.time()
+        self.storage = dev.Storage(layers, kv_heads, head_dim, n_micro, n_ext)
+        info = self.storage.info()
+        log(f"pools: extent {info.extent_reserved_bytes / 1e9:.1f} GB, micro {info.micro_reserved_bytes / 1e9:.2f} GB "
+            f"({time.time() - t0:.1f}s)")
+        ext_perm = permutation(seed, n_ext)
+        micro_perm = permutation(seed + 1, n_micro)
+        # Descriptor arena: lanes x max_entries, tables begin at each lane's row.
+        self.desc = np.zeros((lanes, self.max_entries), dtype=dev.BLOCK_DESC)
+        for i in range(lanes):
+            d = self.desc[i]
+            d["slot"][: self.ext_per_lane] = ext_perm[i * self.ext_per_lane:(i + 1) * self.ext_per_lane]
+            d["generation"][: self.ext_per_lane] = 1
+            d["logical_token_begin"][: self.ext_per_lane] = np.arange(self.ext_per_lane) * 64
+            d["valid_tokens"][: self.ext_per_lane] = 64
+            d["page_token_capacity"][: self.ext_per_lane] = 64
+            d["kind"][: self.ext_per_lane] = 1
+            m = self.ext_per_lane
+            d["slot"][m:] = micro_perm[i * self.micro_per_lane:(i + 1) * self.micro_per_lane]
+            d["generation"][m:] = 1
+            d["logical_token_begin"][m:] = context + np.arange(self.micro_per_lane) * 8
+            d["page_token_capacity"][m:] = 8
+            d["kind"][m:] = 0
+        self.desc_dev = dev.upload(self.desc)
+        self.desc_stride = self.max_entries * dev.BLOCK_DESC.itemsize
+        # Fill every context page with the synthetic generator (stream id = lane).
+        t0 = time.time()
+        for i in range(lanes):
+            self.storage.fill_table(self.desc_dev.ptr + i * self.desc_stride, self.ext_per_lane, 0, context,
+                                    seed, i)
+            if (i + 1) % 64 == 0:
+                dev.sync()
+                log(f"  filled {i + 1}/{lanes} lanes ({time.time() - t0:.1f}s)")
+        dev.sync()
+        log(f"filled {lanes} x {context} tokens in {time.time() - t0:.1f}s")
+        # New K/V per (lane, layer, comp, step) and queries per (lane, layer, step).
+        HD = kv_heads * head_dim
+        self.newkv = dev.DeviceBuffer(lanes * layers * 2 * total_steps * HD * 2)
+        self.query = dev.DeviceBuffer(lanes * layers * total_steps * query_heads * head_dim * 2)
+        self.qseed = seed ^ 0x5155455259
+        for i in range(lanes):
+            for l in range(layers):
+                for c in range(2):
+                    off = (((i * layers + l) * 2 + c) * total_steps) * HD
+                    dev.fill_rows(self.newkv.ptr + 2 * off, total_steps * HD, seed,
+                                  dev.synth_kv_row(i, l, c, context), HD)
+                qoff = ((i * layers + l) * total_steps) * query_heads * head_dim
+                dev.fill_rows(self.query.ptr + 2 * qoff, total_steps * query_heads * head_dim, self.qseed,
+                              dev.synth_kv_row(i, l, 0, context), query_heads * head_dim)
+        dev.sync()
+        self.out = dev.DeviceBuffer(layers * lanes * query_heads * head_dim * 2)
+        self.items_dev = dev.DeviceBuffer(layers * lanes * dev.DECODE_ITEM.itemsize)
+        self.jobs_dev = dev.DeviceBuffer(layers * lanes * dev.APPEND_JOB.itemsize)
+        self.prefix_dev = dev.DeviceBuffer((lanes + 1) * 4)
+        self.ws = None
+        self.ws_stride = 0
+        self.step_index = 0
+
+    def lane_tokens(self, step):
+        return self.context + step + 1
+
+    def prepare_step(self, step):
+        """Host metadata for one step: tail entries, decode items, append jobs."""
+        dev = self.dev
+        m = self.ext_per_lane + step // 8
+        self.desc["valid_tokens"][:, m] = step % 8 + 1
+        count = m + 1
+        T = self.lane_tokens(step)
+        chunk, prefix, total = self.storage.decode_plan([T] * self.lanes, self.QH)
+        ws_lane = dev.workspace_bytes(T, chunk, self.QH, self.D)
+        if self.ws is None or ws_lane > self.ws_stride:
+            self.ws_stride = max(ws_lane, 256)
+            self.ws = dev.DeviceBuffer(self.ws_stride * self.lanes)
+        HD = self.H * self.D
+        QD = self.QH * self.D
+        L, N, S = self.L, self.lanes, self.total_steps
+        lane = np.arange(N, dtype=np.uint64)
+        items = np.zeros((L, N), dtype=dev.DECODE_ITEM)
+        jobs = np.zeros((L, N), dtype=dev.APPEND_JOB)
+        for l in range(L):
+            it = items[l]
+            it["descriptors"] = self.desc_dev.ptr + lane * np.uint64(self.desc_stride)
+            it["descriptor_count"] = count
+            it["token_count"] = T
+            it["layer"] = l
+            it["query"] = self.query.ptr + 2 * (((lane * L + l) * S + step) * QD)
+            it["workspace"] = (self.ws.ptr + lane * np.uint64(self.ws_stride)) if ws_lane else 0
+            it["output"] = self.out.ptr + 2 * ((l * N + lane) * QD)
+            it["attention_scale"] = 1.0 / math.sqrt(self.D)
+            jb = jobs[l]
+            kbase = ((lane * L + l) * 2) * S
+            jb["src_key"] = self.newkv.ptr + 2 * ((kbase + step) * HD)
+            jb["src_value"] = self.newkv.ptr + 2 * ((kbase + S + step) * HD)
+            jb["layer_begin"] = l
+            jb["layer_count"] = 1
+            jb["token_count"] = 1
+            jb["dst_slot"] = self.desc["slot"][:, m]
+            jb["dst_kind"] = 0
+            jb["dst_token"] = step % 8
+        self.items_host = items
+        self.jobs_host = jobs
+        self.prefix = prefix
+        self.plan = (chunk, total)
+
+    def upload_step(self, stream):
+        dev = self.dev
+        dev.copy_to_device(self.desc_dev.ptr, self.desc, stream)
+        dev.copy_to_device(self.items_dev.ptr, self.items_host, stream)
+        dev.copy_to_device(self.jobs_dev.ptr, self.jobs_host, stream)
+        dev.copy_to_device(self.prefix_dev.ptr, self.prefix, stream)
+
+    def launch_step(self, stream):
+        dev = self.dev
+        lib = dev.lib()
+        chunk, total = self.plan
+        sh = ctypes.c_void_p(stream.handle)
+        for l in range(self.L):
+            dev.check(lib.kimkv_append_batch(self.storage.h,
+                                             ctypes.c_void_p(self.jobs_dev.ptr + l * self.lanes * dev.APPEND_JOB.itemsize),
+                                             self.lanes, 1, sh), "append")
+            dev.check(lib.kimkv_paged_decode_batch(
+                self.storage.h, ctypes.c_void_p(self.items_dev.ptr + l * self.lanes * dev.DECODE_ITEM.itemsize),
+                ctypes.c_void_p(self.prefix_dev.ptr), self.lanes, total, chunk, self.QH, sh), "decode")
+
+    def step(self, step, stream):
+        self.prepare_step(step)
+        self.upload_step(stream)
+        self.launch_step(stream)
+
+
+def cpu_baseline(kimkv, w: Workload, lanes_sample: int, step: int):
+    """Oracle decode of `lanes_sample` lanes x 1 layer at full context (single thread)."""
+    import oracle
+    layer = 0
+    T = w.lane_tokens(step)
+    H, D, QH = w.H, w.D, w.QH
+    outs = []
+    total_s = 0.0
+    for lane in range(lanes_sample):
+        n_ext = w.ext_per_lane
+        n_micro = (step // 8) + 1
+        pools = oracle.HostPools(1, H, D, n_micro, n_ext)
+        table = np.zeros(n_ext + n_micro, dtype=oracle.DESC)
+        # Rebuild this lane's layer-0 KV from the generator into host pages (reference layout, L=1).
+        kv = np.empty((1, 2, T, H, D), dtype=np.uint16)
+        for c in range(2):
+            rows = oracle.synth_rows(w.context * H * D, w.seed, oracle.kv_row(lane, layer, c, 0), H * D)
+            kv[0, c, :w.context] = rows.reshape(w.context, H, D)
+            new = oracle.synth_rows((step + 1) * H * D, w.seed, oracle.kv_row(lane, layer, c, w.context), H * D)
+            kv[0, c, w.context:] = new.reshape(step + 1, H, D)
+        for e in range(n_ext):
+            table[e] = (e, 1, 64 * e, 64, 64, 1)
+            pools.append_tokens(kv, T, 64 * e, 1, e, 0, 64)
+        for k in range(n_micro):
+            b = w.context + 8 * k
+            n = min(8, T - b)
+            table[n_ext + k] = (k, 1, b, n, 8, 0)
+            pools.append_tokens(kv, T, b, 0, k, 0, n)
+        q = oracle.synth_rows(QH * D, w.qseed, oracle.kv_row(lane, layer, 0, w.context) + step, QH * D)
+        t0 = time.perf_counter()
+        ref = pools.paged_decode(table, T, layer, QH, q, 1.0 / math.sqrt(D), f32=True)
+        total_s += time.perf_counter() - t0
+        outs.append(ref)
+    kv_bytes = lanes_sample * T * 2 * H * D * 2
+    return outs, total_s, kv_bytes
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=16)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--lanes", type=int, default=256)
+    ap.add_argument("--context", type=int, default=32768)
+    ap.add_argument("--layers", type=int, default=22)
+    ap.add_argument("--cpu-lanes", type=int, default=32, help="lanes in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--seed", type=int, default=20260829)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}), flush=True)
+        return 2
+
+    kimkv = load_package()
+    dev = kimkv.device
+    if dev.device_count() == 0:
+        print(json.dumps({"error": "no HIP device visible"}), flush=True)
+        return 1
+    H, D, QH = 4, 64, 32
+    total_steps = args.warmup + args.steps
+    w = Workload(dev, args.lanes, args.context, args.layers, H, D, QH, total_steps, args.seed)
+    stream = dev.Stream()
+
+    for s in range(args.warmup):
+        w.step(s, stream)
+    stream.synchronize()
+    log(f"warmup done; plan chunk={w.plan[0]} chunks={w.plan[1]}")
+
+    start, stop = dev.Event(), dev.Event()
+    dev.decode_timing(True)
+    dev.sync()
+    t_wall = time.perf_counter()
+    start.record(stream)
+    for s in range(args.warmup, total_steps):
+        w.step(s, stream)
+    stop.record(stream)
+    stop.synchronize()
+    wall_ms = (time.perf_counter() - t_wall) * 1000.0
+    decode_ms_total, decode_launches = dev.decode_timing(False)
+    gpu_ms = start.elapsed_ms(stop)
+    ms_per_step = max(gpu_ms, wall_ms) / args.steps
+
+    # Algorithmic bytes of the timed steps.
+    tok_bytes = 2 * H * D * 2
+    qo_bytes = 2 * QH * D * 2
+    decode_bytes = 0
+    append_bytes = 0
+    for s in range(args.warmup, total_steps):
+        T = w.lane_tokens(s)
+        decode_bytes += args.layers * args.lanes * (T * tok_bytes + qo_bytes)
+        append_bytes += args.layers * args.lanes * 2 * tok_bytes     # read new K/V + write page
+    step_bytes = (decode_bytes + append_bytes) / args.steps
+    value_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    per_launch_decode_bytes = decode_bytes / (args.steps * args.layers)
+    decode_avg_ms = decode_ms_total / max(decode_launches, 1)
+    achieved = per_launch_decode_bytes / (decode_avg_ms * 1e-3) / 1e9
+
+    # Correctness sample + CPU baseline: lanes 0..k-1, layer 0, last step.
+    last = total_steps - 1
+    cpu = None
+    check = None
+    if args.cpu_lanes > 0:
+        outs, cpu_s, cpu_bytes = cpu_baseline(kimkv, w, args.cpu_lanes, last)
+        got = dev.download(w.out.ptr, (args.lanes, QH * D), np.uint16)   # layer 0 block
+        errs = []
+        for lane, ref in enumerate(outs):
+            a = got[lane].view(np.float16).astype(np.float32)
+            err = np.abs(a - ref)
+            ok = bool(np.all(err <= 2e-3 + 1e-3 * np.abs(ref)))
+            errs.append((float(err.max()), ok))
+        check = {"lanes": args.cpu_lanes, "layer": 0, "max_abs_err": max(e for e, _ in errs),
+                 "within_tolerance": all(ok for _, ok in errs), "tolerance": "2e-3 + 1e-3*|ref|"}
+        cpu = {"value": round(cpu_bytes / cpu_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"oracle kvo_paged_decode, {args.cpu_lanes} lanes x 1 layer x {w.lane_tokens(last)} tokens "
+                         f"(QH=32, H=4, D=64), {cpu_s:.1f}s on {platform.processor() or platform.machine()}",
+               "seconds": round(cpu_s, 2)}
+
+    result = {
+        "metric": "paged decode attn+append HBM GB/s (% peak) & us/layer, TinyLlama GQA, 1 GPU",
+        "value": round(value_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "us_per_layer": round(ms_per_step * 1000.0 / args.layers, 1),
+        "pct_of_peak_hbm": round(100.0 * value_gbs / PEAK_HBM_GBS, 1),
+        "tokens_per_s": round(args.lanes / (ms_per_step * 1e-3), 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 storage, fp32 accumulate",
+        "data": "synthetic (seeded Irwin-Hall fp16 K/V/Q generated on device)",
+        "config": {"workload": f"HBM-scale decode: {args.lanes} lanes x {args.context}-token contexts "
+                               f"(+{total_steps} appended), {args.layers} layers TinyLlama GQA 32q/4kv/64d fp16, "
+                               f"extent pages in permuted slots",
+                   "lanes": args.lanes, "context": args.context, "layers": args.layers,
+                   "decode_chunk_tokens": w.plan[0], "decode_chunks": w.plan[1]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "decode_kernel", "avg_launch_ms": round(decode_avg_ms, 4),
+                     "bytes_per_launch": int(per_launch_decode_bytes)},
+        "cpu_baseline": cpu,
+        "check": check,
+        "timing": {"gpu_event_ms": round(gpu_ms, 3), "wall_ms": round(wall_ms, 3)},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
