@@ -233,8 +233,125 @@ def cpu_baseline(kimkv, w: Workload, lanes_sample: int, step: int):
     return outs, total_s, kv_bytes
 
 
+def run_gather(dev, args) -> int:
+    """Long-sequence gather: one sequence of --gather-tokens tokens x 22 layers in
+    64-token extents (permuted slots) -> contiguous [22][2][T][4][64].  Also the
+    known-size copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters."""
+    L, H, D = args.layers, 4, 64
+    T = args.gather_tokens
+    n_ext = T // 64
+    n_micro = (T % 64 + 7) // 8 + 1
+    storage = dev.Storage(L, H, D, n_micro, n_ext)
+    ext_perm = permutation(args.seed, n_ext)
+    entries = [(int(ext_perm[e]), 1, 64 * e, 64, 64, 1) for e in range(n_ext)]
+    b = 64 * n_ext
+    k = 0
+    while b < T:
+        n = min(8, T - b)
+        entries.append((k, 1, b, n, 8, 0))
+        b += n
+        k += 1
+    table = np.array(entries, dtype=dev.BLOCK_DESC)
+    d = dev.upload(table)
+    storage.fill_table(d.ptr, len(table), 0, T, args.seed, 0)
+    n = L * 2 * T * H * D
+    out = dev.DeviceBuffer(n * 2)
+    stream = dev.Stream()
+    lib = dev.lib()
+    sh = ctypes.c_void_p(stream.handle)
+
+    def launch():
+        dev.check(lib.kimkv_gather(storage.h, ctypes.c_void_p(d.ptr), len(table), T, ctypes.c_void_p(out.ptr), sh),
+                  "gather")
+
+    for _ in range(args.warmup):
+        launch()
+    stream.synchronize()
+    start, stop = dev.Event(), dev.Event()
+    start.record(stream)
+    for _ in range(args.steps):
+        launch()
+    stop.record(stream)
+    stop.synchronize()
+    ms = start.elapsed_ms(stop) / args.steps
+    moved = 2 * n * 2                       # read + write
+    got = dev.download(out.ptr, (L, 2, T, H * D), np.uint16)
+    # Bit-exact check of sampled (layer, component, token) rows against the generator.
+    import oracle
+    rng = np.random.default_rng(args.seed)
+    bad = 0
+    for _ in range(256):
+        l, c, t = int(rng.integers(L)), int(rng.integers(2)), int(rng.integers(T))
+        want = oracle.synth_rows(H * D, args.seed, oracle.kv_row(0, l, c, t), H * D)
+        bad += int(not np.array_equal(got[l, c, t], want))
+    print(json.dumps({
+        "metric": "long-sequence gather (paged -> contiguous) GB/s", "value": round(moved / (ms * 1e-3) / 1e9, 1),
+        "unit": "GB/s", "us_per_launch": round(ms * 1000, 2), "bytes_per_launch": moved,
+        "read_bytes": n * 2, "write_bytes": n * 2, "pct_of_peak_hbm": round(100 * moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+        "config": {"workload": f"gather of one {T}-token sequence x {L} layers (4 kv heads x 64, fp16), "
+                               f"{n_ext} extents in permuted slots + {k} micro pages"},
+        "steps": args.steps, "check": {"sampled_rows": 256, "mismatches": bad}}), flush=True)
+    return 0 if bad == 0 else 1
+
+
+def run_copy(dev, args) -> int:
+    """Plain device-to-device copy of a known size: the achievable copy
+    bandwidth of the box and the calibration run for the FETCH_SIZE /
+    WRITE_SIZE counters."""
+    nbytes = args.copy_mib << 20
+    src, dst = dev.DeviceBuffer(nbytes), dev.DeviceBuffer(nbytes)
+    dev.fill_rows(src.ptr, nbytes // 2, args.seed, 0, 4096)
+    stream = dev.Stream()
+    lib = dev.lib()
+    sh = ctypes.c_void_p(stream.handle)
+    for _ in range(args.warmup):
+        dev.check(lib.kimkv_memcpy_d2d_async(ctypes.c_void_p(dst.ptr), ctypes.c_void_p(src.ptr), nbytes, sh), "copy")
+    stream.synchronize()
+    start, stop = dev.Event(), dev.Event()
+    start.record(stream)
+    for _ in range(args.steps):
+        dev.check(lib.kimkv_memcpy_d2d_async(ctypes.c_void_p(dst.ptr), ctypes.c_void_p(src.ptr), nbytes, sh), "copy")
+    stop.record(stream)
+    stop.synchronize()
+    ms = start.elapsed_ms(stop) / args.steps
+    moved = 2 * nbytes
+    print(json.dumps({"metric": "device-to-device copy GB/s (read + write)",
+                      "value": round(moved / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+                      "us_per_copy": round(ms * 1000, 2), "read_bytes": nbytes, "write_bytes": nbytes,
+                      "pct_of_peak_hbm": round(100 * moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+                      "steps": args.steps}), flush=True)
+    return 0
+
+
+def profiled_traffic(lanes: int, context: int, layers: int):
+    """HBM bytes per decode launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE per dispatch, each times its copy-calibrated
+    factor), for the default workload that summary was measured on."""
+    path = os.path.join(ROOT, "profiles", "decode_kernel_hbm_scale.md")
+    if (lanes, context, layers) != (256, 32768, 22) or not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        if ":" in line:
+            k, _, v = line.strip().partition(":")
+            try:
+                vals[k.strip()] = float(v)
+            except ValueError:
+                pass
+    try:
+        return int(vals["fetch_size_kib_per_dispatch"] * 1024 * vals["fetch_factor"]
+                   + vals["write_size_kib_per_dispatch"] * 1024 * vals["write_factor"])
+    except KeyError:
+        return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
+    ap.add_argument("--config", choices=["decode", "gather", "copy"], default="decode",
+                    help="decode: HBM-scale decode+append (the headline line); gather: long-sequence gather; "
+                         "copy: plain device copy (bandwidth and counter calibration)")
+    ap.add_argument("--copy-mib", type=int, default=4096)
+    ap.add_argument("--gather-tokens", type=int, default=16384)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=16)
     ap.add_argument("--warmup", type=int, default=2)
@@ -255,6 +372,10 @@ def main() -> int:
     if dev.device_count() == 0:
         print(json.dumps({"error": "no HIP device visible"}), flush=True)
         return 1
+    if args.config == "gather":
+        return run_gather(dev, args)
+    if args.config == "copy":
+        return run_copy(dev, args)
     H, D, QH = 4, 64, 32
     total_steps = args.warmup + args.steps
     w = Workload(dev, args.lanes, args.context, args.layers, H, D, QH, total_steps, args.seed)
@@ -336,7 +457,8 @@ def main() -> int:
                    "lanes": args.lanes, "context": args.context, "layers": args.layers,
                    "decode_chunk_tokens": w.plan[0], "decode_chunks": w.plan[1]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic(args.lanes, args.context, args.layers),
                      "kernel": "decode_kernel", "avg_launch_ms": round(decode_avg_ms, 4),
                      "bytes_per_launch": int(per_launch_decode_bytes)},
         "cpu_baseline": cpu,
