@@ -222,6 +222,16 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage,
                                       uint32_t chunk_tokens, uint32_t query_heads,
                                       kimkv_stream_t stream);
 
+/* Reference attention over one table (the comparator of the reference's
+ * launchAttentionScores / launchAttentionOutput, kernels.cuh:77-95, and of the
+ * CPU referenceAttention, src/reference/kv_reference.cpp:136-234): MHA with
+ * query head h on kv head h, fp32 query/output [layers][kv_heads][head_dim],
+ * scale 1/sqrt(head_dim), fp32 accumulation, all layers. */
+kimkv_status kimkv_reference_attention(const kimkv_storage* storage,
+                                       const kimkv_block_desc* device_descriptors, uint32_t descriptor_count,
+                                       uint32_t total_tokens, const float* device_query, float* device_output,
+                                       kimkv_stream_t stream);
+
 /* Average duration (ms) of the decode kernels launched since the last reset,
  * measured with events on the launch stream; for the benchmark's roofline. */
 kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launches);

@@ -446,6 +446,80 @@ __global__ __launch_bounds__(64) void combine_kernel(const kimkv_decode_item* it
     }
 }
 
+// Reference MHA attention, fp32 query/output: block = (kv head, layer), one wave.
+__global__ __launch_bounds__(64) void reference_attention_kernel(PoolView P, const kimkv_block_desc* desc,
+                                                                 uint32_t count, uint32_t T, const float* query,
+                                                                 float* output)
+{
+    __shared__ WaveScratch scratch;
+    uint32_t const h = blockIdx.x;
+    uint32_t const layer = blockIdx.y;
+    uint32_t const lane = threadIdx.x;
+    uint32_t const D = P.dim;
+    const float* qv = query + (static_cast<uint64_t>(layer) * P.heads + h) * D;
+    float const scale = 1.0f / sqrtf(static_cast<float>(D));
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t t0 = 0; t0 < T; t0 += 64) {
+        uint32_t const t = t0 + lane;
+        uint32_t idx = find_descriptor_wave(desc, count, t0);
+        const uint16_t* page = nullptr;
+        uint32_t cap = 0;
+        uint32_t pt = 0;
+        if (t < T) {
+            while (idx + 1 < count && desc[idx + 1].logical_token_begin <= t) ++idx;
+            kimkv_block_desc const e = desc[idx];
+            if (t >= e.logical_token_begin && t < e.logical_token_begin + e.valid_tokens
+                && e.valid_tokens <= e.page_token_capacity) {
+                page = page_base(P, e.kind, e.slot, e.page_token_capacity);
+                cap = e.page_token_capacity;
+                pt = t - e.logical_token_begin;
+            }
+        }
+        float s = -INFINITY;
+        const uint16_t* vrow = nullptr;
+        if (page != nullptr) {
+            const uint16_t* hb = page + head_block(P, cap, layer, h);
+            const uint16_t* krow = hb + static_cast<uint64_t>(pt) * D;
+            float dot = 0.0f;
+            for (uint32_t d = 0; d < D; ++d) dot += qv[d] * __half2float(__ushort_as_half(krow[d]));
+            s = dot * scale;
+            vrow = hb + static_cast<uint64_t>(cap) * D + pt;
+        }
+        float const m_new = fmaxf(m_run, wave_max(s));
+        float const alpha = m_new == -INFINITY ? 1.0f : expf(m_run - m_new);
+        float const p = (page != nullptr && m_new != -INFINITY) ? expf(s - m_new) : 0.0f;
+        l_run = l_run * alpha + wave_sum(p);
+        m_run = m_new;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] *= alpha;
+        scratch.p[lane] = p;
+        scratch.vrow[lane] = vrow;
+        scratch.cap[lane] = cap;
+        __syncthreads();
+        uint32_t const nt = min(64u, T - t0);
+        for (uint32_t tt = 0; tt < nt; ++tt) {
+            float const pp = scratch.p[tt];
+            const uint16_t* vr = scratch.vrow[tt];
+            uint32_t const vc = scratch.cap[tt];
+            if (vr == nullptr || pp == 0.0f) continue;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t const d = lane + 64u * k;
+                if (d < D) o[k] += pp * __half2float(__ushort_as_half(vr[static_cast<uint64_t>(d) * vc]));
+            }
+        }
+        __syncthreads();
+    }
+    float const inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        uint32_t const d = lane + 64u * k;
+        if (d < D) output[(static_cast<uint64_t>(layer) * P.heads + h) * D + d] = o[k] * inv;
+    }
+}
+
 }  // namespace
 }  // namespace kimkv
 
@@ -519,6 +593,21 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage, const kimkv_
         return launch_status();
     }
     return KIMKV_OK;
+}
+
+kimkv_status kimkv_reference_attention(const kimkv_storage* storage, const kimkv_block_desc* device_descriptors,
+                                       uint32_t descriptor_count, uint32_t total_tokens, const float* device_query,
+                                       float* device_output, kimkv_stream_t stream)
+{
+    if (storage == nullptr || device_descriptors == nullptr || descriptor_count == 0 || total_tokens == 0
+        || device_query == nullptr || device_output == nullptr || storage->layout.head_dim > 256) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    dim3 const grid(storage->layout.kv_heads, storage->layout.layers);
+    reference_attention_kernel<<<grid, 64, 0, native(stream)>>>(pool_view(*storage), device_descriptors,
+                                                                descriptor_count, total_tokens, device_query,
+                                                                device_output);
+    return launch_status();
 }
 
 }  // extern "C"

@@ -1,0 +1,709 @@
+// Heterogeneous engine backend on MI355X.
+//
+// Behaviour follows the reference's CUDA backend (src/cuda/engine/backend.cpp:
+// 19-610 and transaction.cpp:24-423): reserve = metadata reservation + page
+// lease + descriptor upload; writeLayer / attendLayer only enqueue; commit
+// waits on one completion event, releases the lease and publishes the table;
+// any failure rolls back after in-flight work has drained; error codes map as
+// in backend.cpp:19-65.  Differences: batched attention has no lane cap and
+// one decode launch covers every lane; writeLayerBatch appends all lanes in
+// one launch; descriptors come from a buffer cache and small per-launch
+// uploads go through a pinned staging ring instead of cudaMalloc per token.
+#include "kim-kv/hip/hip_engine_kv_backend.h"
+
+#include "kim-kv/runtime/kv_cache_manager.h"
+#include "storage.h"
+
+#include <atomic>
+#include <cstring>
+#include <optional>
+#include <memory>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+namespace kimkvcache {
+namespace {
+
+EngineKvStatus mapMetadata(KvCacheError e) noexcept
+{
+    switch (e) {
+    case KvCacheError::None: return {};
+    case KvCacheError::InvalidArgument: return {EngineKvError::InvalidArgument};
+    case KvCacheError::RequestNotFound: return {EngineKvError::RequestNotFound};
+    case KvCacheError::RequestAlreadyExists: return {EngineKvError::RequestAlreadyExists};
+    case KvCacheError::RequestConflict:
+    case KvCacheError::PromotionConflict: return {EngineKvError::RequestConflict};
+    case KvCacheError::ResourceExhausted: return {EngineKvError::ResourceExhausted};
+    case KvCacheError::InvalidState: return {EngineKvError::InvalidState};
+    default: return {EngineKvError::InternalError};
+    }
+}
+
+EngineKvStatus mapDevice(HipStatus s) noexcept
+{
+    switch (s.error) {
+    case HipError::None: return {};
+    case HipError::InvalidArgument: return {EngineKvError::InvalidArgument};
+    case HipError::AllocationFailed: return {EngineKvError::ResourceExhausted};
+    case HipError::SubmissionFailed: return {EngineKvError::SubmissionFailed};
+    case HipError::ExecutionFailed: return {EngineKvError::ExecutionFailed};
+    default: return {EngineKvError::InternalError};
+    }
+}
+
+HipStatus invalidArgument() noexcept { return HipStatus{HipError::InvalidArgument, 0}; }
+HipStatus injectedSubmission() noexcept { return HipStatus{HipError::SubmissionFailed, 0}; }
+
+struct BackendState final {
+    EngineKvConfig config;
+    KvCacheManager manager;
+    HipKvStorage storage;
+    std::unordered_map<RequestId, std::uint32_t> committed_lengths;
+    std::uint64_t active_transactions{0};
+    std::atomic<std::uint64_t> batched_attention_submissions{0};
+    std::atomic<std::uint64_t> batched_attention_lanes{0};
+    std::atomic<std::uint64_t> batched_write_submissions{0};
+    std::atomic<std::uint64_t> next_transaction_id{1};
+    mutable std::mutex mutex;
+    std::mutex launch_mutex;   // serialises staging + launches of batch calls
+
+    BackendState(EngineKvConfig c, std::uint32_t micro, std::uint32_t extent)
+        : config(c), manager(micro, extent), storage(c.kv_layout, micro, extent)
+    {
+    }
+};
+
+class HipTokenTransaction final : public TokenTransactionBackend {
+public:
+    HipTokenTransaction(std::shared_ptr<BackendState> owner, TokenReservationResult const& r, PageLeaseId lease,
+                        HipStream stream)
+        : owner_(std::move(owner)),
+          reservation_(r.reservation_id),
+          request_(r.request_id),
+          lease_(lease),
+          stream_(stream),
+          token_count_(r.reserved.tokenCount())
+    {
+        MappingEntry const& tail = r.reserved.entries().back();
+        tail_ = tail.handle;
+        tail_token_ = static_cast<std::uint16_t>(token_count_ - 1 - tail.logical_token_begin);
+        if (!r.before.entries().empty()) {
+            MappingEntry const& old = r.before.entries().back();
+            if (old.logical_token_begin == tail.logical_token_begin && old.handle != tail.handle) {
+                cow_src_ = old.handle;           // partial tail replaced: copy per layer
+                cow_tokens_ = old.valid_tokens;
+            }
+        }
+    }
+
+    ~HipTokenTransaction() override
+    {
+        static_cast<void>(finish());
+        releaseDescriptors();
+        if (event_ != nullptr) static_cast<void>(kimkv_event_destroy(event_));
+    }
+
+    // Descriptor upload at reserve time (beginEngineTransaction).
+    HipStatus begin(BlockTable const& reserved)
+    {
+        HipKvStorage& st = owner_->storage;
+        std::vector<kimkv_block_desc> d;
+        st.descriptors(reserved, d);
+        desc_count_ = static_cast<std::uint32_t>(d.size());
+        std::size_t const bytes = d.size() * sizeof(kimkv_block_desc);
+        descriptors_ = st.buffers().acquire(bytes, desc_granted_);
+        if (descriptors_ == nullptr) return HipStatus{HipError::AllocationFailed, kimkv_last_native_error()};
+        if (kimkv_event_create(&event_, 0) != KIMKV_OK) {
+            return HipStatus{HipError::AllocationFailed, kimkv_last_native_error()};
+        }
+        // Staging and its fence stay under the launch lock so that no other
+        // thread's region lands between them (a fence covers the regions
+        // before it on its stream).
+        std::lock_guard<std::mutex> lock(owner_->launch_mutex);
+        bool const staged = st.ring().uploadTo(descriptors_, d.data(), bytes, stream_);
+        st.ring().fence(stream_);
+        if (!staged) return HipStatus{HipError::SubmissionFailed, kimkv_last_native_error()};
+        submission_ = {};
+        return {};
+    }
+
+    EngineKvStatus writeLayer(LayerKvWrite const& write, EngineStream) override
+    {
+        kimkv_append_job job{};
+        HipStatus s = prepareWrite(write, job);
+        if (!s.ok()) return mapDevice(s);
+        std::lock_guard<std::mutex> lock(owner_->launch_mutex);
+        return mapDevice(launchWrites(&job, 1, stream_, {this}));
+    }
+
+    EngineKvStatus attendLayer(PagedDecodeRequest const& request, EngineStream) override
+    {
+        kimkv_decode_item item{};
+        std::vector<std::uint32_t> prefix(2, 0);
+        std::uint32_t chunk = 0;
+        std::uint32_t total = 0;
+        HipStatus s = planOne(request, item, prefix, chunk, total);
+        if (!s.ok()) return mapDevice(s);
+        std::lock_guard<std::mutex> lock(owner_->launch_mutex);
+        HipKvStorage& st = owner_->storage;
+        void* items = st.ring().upload(&item, sizeof(item), stream_);
+        void* pre = items != nullptr ? st.ring().upload(prefix.data(), prefix.size() * 4, stream_) : nullptr;
+        if (items == nullptr || pre == nullptr) return mapDevice(failSubmission(kimkv_last_native_error()));
+        kimkv_status const k = kimkv_paged_decode_batch(st.handle(), static_cast<kimkv_decode_item const*>(items),
+                                                        static_cast<std::uint32_t const*>(pre), 1, total, chunk,
+                                                        owner_->config.query_head_count, stream_);
+        st.ring().fence(stream_);
+        if (k != KIMKV_OK) return mapDevice(failSubmission(kimkv_last_native_error()));
+        return {};
+    }
+
+    void attendLayerBatch(PagedDecodeBatch& batch) override
+    {
+        std::vector<HipTokenTransaction*> lanes;
+        std::vector<std::size_t> index;
+        if (!collect(batch, lanes, index)) {
+            TokenTransactionBackend::attendLayerBatch(batch);
+            return;
+        }
+        BackendState& o = *owner_;
+        HipKvStorage& st = o.storage;
+        std::uint32_t const QH = o.config.query_head_count;
+        std::uint32_t const D = o.config.kv_layout.head_dimension;
+        // Prepare every lane (per-lane validation, fault hook) before planning.
+        std::vector<std::uint32_t> tokens;
+        std::vector<std::size_t> ready;
+        for (std::size_t k = 0; k < lanes.size(); ++k) {
+            PagedDecodeBatchItem& item = batch.items[index[k]];
+            HipStatus const s = lanes[k]->checkAttention(item.request);
+            if (!s.ok()) {
+                item.status = mapDevice(s);
+                continue;
+            }
+            ready.push_back(k);
+            tokens.push_back(lanes[k]->token_count_);
+        }
+        if (ready.empty()) return;
+        std::vector<std::uint32_t> prefix(ready.size() + 1, 0);
+        std::uint32_t chunk = 0;
+        std::uint32_t total = 0;
+        if (kimkv_decode_plan(st.handle(), tokens.data(), static_cast<std::uint32_t>(ready.size()), QH, &chunk,
+                              prefix.data(), &total) != KIMKV_OK) {
+            for (std::size_t k : ready) batch.items[index[k]].status = {EngineKvError::InvalidArgument};
+            return;
+        }
+        std::size_t n = 0;
+        std::vector<std::size_t> launched;
+        std::vector<std::uint32_t> launch_prefix(1, 0);
+        std::vector<std::uint32_t> launch_tokens;
+        for (std::size_t k : ready) {
+            PagedDecodeBatchItem& item = batch.items[index[k]];
+            HipTokenTransaction* t = lanes[k];
+            std::size_t const need = kimkv_decode_workspace_bytes(t->token_count_, chunk, QH, D);
+            if (item.request.workspace_bytes < need) {
+                item.status = {EngineKvError::InvalidArgument};
+                continue;
+            }
+            batch.host_items[n] = t->deviceItem(item.request, need != 0);
+            launched.push_back(index[k]);
+            launch_tokens.push_back(t->token_count_);
+            ++n;
+        }
+        if (n == 0) return;
+        // Prefix over the surviving lanes with the chunk length their workspaces
+        // were checked against (re-planning could shrink it and overflow them).
+        std::vector<std::uint32_t> pre(n + 1, 0);
+        for (std::size_t i = 0; i < n; ++i) pre[i + 1] = pre[i] + (launch_tokens[i] + chunk - 1) / chunk;
+        total = pre[n];
+        std::lock_guard<std::mutex> lock(o.launch_mutex);
+        HipStream const stream = stream_;
+        bool ok = st.ring().uploadTo(batch.device_items, batch.host_items, n * sizeof(DevicePagedDecodeBatchItem),
+                                     stream);
+        void* dpre = ok ? st.ring().upload(pre.data(), pre.size() * 4, stream) : nullptr;
+        kimkv_status k = KIMKV_SUBMISSION_FAILED;
+        if (dpre != nullptr) {
+            k = kimkv_paged_decode_batch(st.handle(), reinterpret_cast<kimkv_decode_item const*>(batch.device_items),
+                                         static_cast<std::uint32_t const*>(dpre), static_cast<std::uint32_t>(n), total,
+                                         chunk, QH, stream);
+        }
+        st.ring().fence(stream);
+        std::uint64_t good = 0;
+        for (std::size_t i : launched) {
+            PagedDecodeBatchItem& item = batch.items[i];
+            auto* t = static_cast<HipTokenTransaction*>(batchBackend(item));
+            item.status = k == KIMKV_OK ? EngineKvStatus{} : mapDevice(t->failSubmission(kimkv_last_native_error()));
+            good += item.status.ok() ? 1 : 0;
+        }
+        if (good != 0) {
+            o.batched_attention_submissions.fetch_add(1, std::memory_order_relaxed);
+            o.batched_attention_lanes.fetch_add(good, std::memory_order_relaxed);
+        }
+    }
+
+    void writeLayerBatch(LayerKvWriteBatch& batch) override
+    {
+        std::vector<HipTokenTransaction*> lanes;
+        std::vector<std::size_t> index;
+        for (std::size_t i = 0; i < batch.item_count; ++i) {
+            LayerKvWriteBatchItem const& item = batch.items[i];
+            if (!item.status.ok()) continue;
+            auto* t = dynamic_cast<HipTokenTransaction*>(batchBackend(item));
+            if (t == nullptr || t->owner_.get() != owner_.get() || t->stream_ != stream_) {
+                TokenTransactionBackend::writeLayerBatch(batch);
+                return;
+            }
+            lanes.push_back(t);
+            index.push_back(i);
+        }
+        std::vector<kimkv_append_job> jobs;
+        std::vector<HipTokenTransaction*> launched;
+        std::vector<std::size_t> launched_index;
+        for (std::size_t k = 0; k < lanes.size(); ++k) {
+            LayerKvWriteBatchItem& item = batch.items[index[k]];
+            kimkv_append_job job{};
+            HipStatus const s = lanes[k]->prepareWrite(item.write, job);
+            if (!s.ok()) {
+                item.status = mapDevice(s);
+                continue;
+            }
+            jobs.push_back(job);
+            launched.push_back(lanes[k]);
+            launched_index.push_back(index[k]);
+        }
+        if (jobs.empty()) return;
+        HipStatus s;
+        {
+            std::lock_guard<std::mutex> lock(owner_->launch_mutex);
+            s = launchWrites(jobs.data(), jobs.size(), stream_, launched);
+        }
+        for (std::size_t k = 0; k < launched.size(); ++k) {
+            batch.items[launched_index[k]].status = mapDevice(s.ok() ? HipStatus{} : launched[k]->submission_);
+        }
+        if (s.ok()) owner_->batched_write_submissions.fetch_add(1, std::memory_order_relaxed);
+    }
+
+    EngineKvStatus commit(EngineStream) override
+    {
+        HipStatus const done = finish();
+        if (!done.ok()) return mapDevice(done);
+        std::lock_guard<std::mutex> lock(owner_->mutex);
+        EngineKvStatus const lease = releaseLeaseLocked();
+        if (!lease.ok()) return lease;
+        KvCacheError const c = owner_->manager.commitTokenReservation(reservation_);
+        if (c != KvCacheError::None) return mapMetadata(c);
+        auto it = owner_->committed_lengths.find(request_);
+        if (it == owner_->committed_lengths.end()) return {EngineKvError::InternalError};
+        ++it->second;
+        --owner_->active_transactions;
+        resolved_ = true;
+        return {};
+    }
+
+    void rollback(EngineStream) noexcept override
+    {
+        if (resolved_) return;
+        static_cast<void>(finish());
+        std::lock_guard<std::mutex> lock(owner_->mutex);
+        static_cast<void>(releaseLeaseLocked());
+        static_cast<void>(owner_->manager.rollbackTokenReservation(reservation_));
+        if (owner_->active_transactions != 0) --owner_->active_transactions;
+        resolved_ = true;
+    }
+
+private:
+    bool collect(PagedDecodeBatch& batch, std::vector<HipTokenTransaction*>& lanes, std::vector<std::size_t>& index)
+    {
+        for (std::size_t i = 0; i < batch.item_count; ++i) {
+            PagedDecodeBatchItem const& item = batch.items[i];
+            if (!item.status.ok()) continue;
+            auto* t = dynamic_cast<HipTokenTransaction*>(batchBackend(item));
+            if (t == nullptr || t->owner_.get() != owner_.get() || t->stream_ != stream_) return false;
+            lanes.push_back(t);
+            index.push_back(i);
+        }
+        return true;
+    }
+
+    HipStatus failSubmission(int native) noexcept
+    {
+        submission_ = HipStatus{HipError::SubmissionFailed, native};
+        return submission_;
+    }
+
+    HipStatus prepareWrite(LayerKvWrite const& write, kimkv_append_job& job)
+    {
+        if (finished_ || !submission_.ok() || write.layer >= owner_->config.kv_layout.layer_count
+            || write.device_key == nullptr || write.device_value == nullptr) {
+            return !submission_.ok() ? submission_ : invalidArgument();
+        }
+        if (owner_->storage.consumeFailure(HipFailurePoint::Submission)) {
+            submission_ = injectedSubmission();
+            return submission_;
+        }
+        job.src_key = write.device_key;
+        job.src_value = write.device_value;
+        job.src_layer_stride = 0;
+        job.src_token_stride = 0;
+        job.layer_begin = write.layer;
+        job.layer_count = 1;
+        job.token_count = 1;
+        job.dst_slot = tail_.slot;
+        job.dst_kind = static_cast<std::uint8_t>(tail_.kind);
+        job.dst_token = tail_token_;
+        if (cow_tokens_ != 0) {
+            job.cow_slot = cow_src_.slot;
+            job.cow_kind = static_cast<std::uint8_t>(cow_src_.kind);
+            job.cow_tokens = cow_tokens_;
+        }
+        return {};
+    }
+
+    HipStatus launchWrites(kimkv_append_job const* jobs, std::size_t n, HipStream stream,
+                           std::vector<HipTokenTransaction*> const& owners)
+    {
+        HipKvStorage& st = owner_->storage;
+        void* d = st.ring().upload(jobs, n * sizeof(kimkv_append_job), stream);
+        kimkv_status k = KIMKV_SUBMISSION_FAILED;
+        if (d != nullptr) {
+            k = kimkv_append_batch(st.handle(), static_cast<kimkv_append_job const*>(d),
+                                   static_cast<std::uint32_t>(n), 1, stream);
+        }
+        st.ring().fence(stream);
+        if (k == KIMKV_OK) return {};
+        int const native = kimkv_last_native_error();
+        for (HipTokenTransaction* t : owners) static_cast<void>(t->failSubmission(native));
+        return HipStatus{HipError::SubmissionFailed, native};
+    }
+
+    HipStatus checkAttention(PagedDecodeRequest const& r)
+    {
+        if (finished_ || !submission_.ok() || r.layer >= owner_->config.kv_layout.layer_count
+            || r.device_query == nullptr || r.device_output == nullptr || r.device_workspace == nullptr
+            || !(r.attention_scale > 0.0F)) {
+            return !submission_.ok() ? submission_ : invalidArgument();
+        }
+        if (token_count_ == 0) return invalidArgument();
+        if (owner_->storage.consumeFailure(HipFailurePoint::Submission)) {
+            submission_ = injectedSubmission();
+            return submission_;
+        }
+        return {};
+    }
+
+    DevicePagedDecodeBatchItem deviceItem(PagedDecodeRequest const& r, bool uses_workspace) const
+    {
+        return DevicePagedDecodeBatchItem{static_cast<DeviceBlockDescriptor const*>(descriptors_), desc_count_,
+                                          token_count_, r.layer, r.device_query,
+                                          uses_workspace ? static_cast<float*>(r.device_workspace) : nullptr,
+                                          r.device_output, r.attention_scale};
+    }
+
+    HipStatus planOne(PagedDecodeRequest const& r, kimkv_decode_item& item, std::vector<std::uint32_t>& prefix,
+                      std::uint32_t& chunk, std::uint32_t& total)
+    {
+        HipStatus const s = checkAttention(r);
+        if (!s.ok()) return s;
+        std::uint32_t const QH = owner_->config.query_head_count;
+        if (kimkv_decode_plan(owner_->storage.handle(), &token_count_, 1, QH, &chunk, prefix.data(), &total)
+            != KIMKV_OK) {
+            return invalidArgument();
+        }
+        std::size_t const need =
+            kimkv_decode_workspace_bytes(token_count_, chunk, QH, owner_->config.kv_layout.head_dimension);
+        if (r.workspace_bytes < need) return invalidArgument();
+        DevicePagedDecodeBatchItem const d = deviceItem(r, need != 0);
+        static_assert(sizeof(d) == sizeof(item));
+        std::memcpy(&item, &d, sizeof(item));
+        return {};
+    }
+
+    HipStatus finish() noexcept
+    {
+        if (finished_) return final_;
+        if (!submission_.ok()) {
+            static_cast<void>(kimkv_stream_synchronize(stream_));
+            final_ = submission_;
+        } else if (event_ == nullptr) {
+            final_ = HipStatus{HipError::InternalError, 0};
+        } else if (kimkv_event_record(event_, stream_) != KIMKV_OK || kimkv_event_synchronize(event_) != KIMKV_OK) {
+            final_ = HipStatus{HipError::ExecutionFailed, kimkv_last_native_error()};
+        } else if (owner_->storage.consumeFailure(HipFailurePoint::Completion)) {
+            final_ = HipStatus{HipError::ExecutionFailed, -1};
+        } else {
+            final_ = {};
+        }
+        finished_ = true;
+        releaseDescriptors();
+        return final_;
+    }
+
+    void releaseDescriptors() noexcept
+    {
+        if (descriptors_ != nullptr) {
+            owner_->storage.buffers().release(descriptors_, desc_granted_);
+            descriptors_ = nullptr;
+        }
+    }
+
+    EngineKvStatus releaseLeaseLocked() noexcept
+    {
+        if (lease_ == kInvalidPageLeaseId) return {};
+        KvCacheError const e = owner_->manager.releasePageLease(lease_);
+        if (e == KvCacheError::None) lease_ = kInvalidPageLeaseId;
+        return mapMetadata(e);
+    }
+
+    std::shared_ptr<BackendState> owner_;
+    KvTokenReservationId reservation_;
+    RequestId request_;
+    PageLeaseId lease_;
+    HipStream stream_;
+    std::uint32_t token_count_;
+    PageHandle tail_{};
+    std::uint16_t tail_token_{0};
+    PageHandle cow_src_{};
+    std::uint16_t cow_tokens_{0};
+    void* descriptors_{nullptr};
+    std::size_t desc_granted_{0};
+    std::uint32_t desc_count_{0};
+    void* event_{nullptr};
+    HipStatus submission_{HipError::InvalidArgument, 0};
+    HipStatus final_{};
+    bool finished_{false};
+    bool resolved_{false};
+};
+
+class HipEngineKvBackend final : public EngineKvBackend {
+public:
+    explicit HipEngineKvBackend(std::shared_ptr<BackendState> s) : state_(std::move(s)) {}
+
+    EngineKvBackendKind kind() const noexcept override { return EngineKvBackendKind::Heterogeneous; }
+    EngineKvConfig config() const noexcept override { return state_->config; }
+
+    EngineKvStatus createRequest(RequestId request_id) override
+    {
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        if (!state_->config.valid() || !state_->storage.status().ok()) return {EngineKvError::InvalidState};
+        KvCacheError const e = state_->manager.createRequest(request_id);
+        if (e == KvCacheError::None) state_->committed_lengths.emplace(request_id, 0);
+        return mapMetadata(e);
+    }
+
+    EngineKvStatus forkRequest(RequestId source, RequestId child) override
+    {
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        auto it = state_->committed_lengths.find(source);
+        if (it == state_->committed_lengths.end()) return {EngineKvError::RequestNotFound};
+        KvCacheError const e = state_->manager.forkRequest(source, child);
+        if (e == KvCacheError::None) state_->committed_lengths.emplace(child, it->second);
+        return mapMetadata(e);
+    }
+
+    EngineKvStatus releaseRequest(RequestId request_id) override
+    {
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        KvCacheError const e = state_->manager.releaseRequest(request_id);
+        if (e == KvCacheError::None) state_->committed_lengths.erase(request_id);
+        return mapMetadata(e);
+    }
+
+    TokenReserveResult reserveToken(ReserveTokenRequest const& request) override
+    {
+        TokenReserveResult result;
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        auto const length = state_->committed_lengths.find(request.request_id);
+        if (request.request_id == kInvalidRequestId) {
+            result.status = {EngineKvError::InvalidArgument};
+            return result;
+        }
+        if (length == state_->committed_lengths.end()) {
+            result.status = {EngineKvError::RequestNotFound};
+            return result;
+        }
+        TokenReservationResult r = state_->manager.reserveToken(request.request_id, request.expected_committed_tokens);
+        if (!r.ok()) {
+            result.status = mapMetadata(r.error);
+            return result;
+        }
+        PageLeaseAcquireResult lease = state_->manager.acquireTokenReservationLease(r.reservation_id);
+        if (!lease.ok()) {
+            static_cast<void>(state_->manager.rollbackTokenReservation(r.reservation_id));
+            result.status = mapMetadata(lease.error);
+            return result;
+        }
+        auto undo = [&](EngineKvStatus s) {
+            static_cast<void>(state_->manager.releasePageLease(lease.lease_id));
+            static_cast<void>(state_->manager.rollbackTokenReservation(r.reservation_id));
+            result.status = s;
+            return std::move(result);
+        };
+        HipKvStorage& st = state_->storage;
+        if (!st.status().ok()) return undo(mapDevice(st.status()));
+        if (!st.validTable(r.before) || !st.validTable(r.reserved) || r.reserved.entries().empty()) {
+            return undo({EngineKvError::InvalidArgument});
+        }
+        if (st.consumeFailure(HipFailurePoint::Submission)) return undo({EngineKvError::SubmissionFailed});
+        std::unique_ptr<HipTokenTransaction> tx;
+        try {
+            tx = std::make_unique<HipTokenTransaction>(state_, r, lease.lease_id, request.stream);
+        } catch (...) {
+            return undo({EngineKvError::ResourceExhausted});
+        }
+        HipStatus const begun = tx->begin(r.reserved);
+        if (!begun.ok()) {
+            tx.reset();   // drains its stream before the metadata is undone
+            return undo(mapDevice(begun));
+        }
+        std::uint64_t const id = state_->next_transaction_id.fetch_add(1, std::memory_order_relaxed);
+        result.transaction = TokenTransaction(std::move(tx), id, r.request_id, r.logical_token_position,
+                                              state_->config.kv_layout.layer_count, request.stream);
+        if (!result.transaction.valid()) {
+            result.status = {EngineKvError::InternalError};
+            return result;
+        }
+        ++state_->active_transactions;
+        result.status = {};
+        return result;
+    }
+
+    EngineKvBackendSnapshot snapshot() const override
+    {
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        EngineKvBackendSnapshot s;
+        s.request_count = state_->committed_lengths.size();
+        s.active_transaction_count = state_->active_transactions;
+        for (auto const& kv : state_->committed_lengths) s.committed_token_count += kv.second;
+        s.batched_attention_submissions = state_->batched_attention_submissions.load(std::memory_order_relaxed);
+        s.batched_attention_lanes = state_->batched_attention_lanes.load(std::memory_order_relaxed);
+        s.batched_write_submissions = state_->batched_write_submissions.load(std::memory_order_relaxed);
+        s.storage_reserved_bytes = state_->storage.snapshot().totalReservedBytes();
+        KvCacheManagerSnapshot const m = state_->manager.snapshot();
+        s.primary_page_tokens = kMicroPageTokenCapacity;
+        s.secondary_page_tokens = kExtentPageTokenCapacity;
+        s.primary_page_capacity = m.micro_pool.total_slots;
+        s.secondary_page_capacity = m.extent_pool.total_slots;
+        s.allocated_primary_pages = m.micro_pool.allocated_slots;
+        s.allocated_secondary_pages = m.extent_pool.allocated_slots;
+        s.successful_primary_allocations = m.micro_pool.successful_allocations;
+        s.successful_secondary_allocations = m.extent_pool.successful_allocations;
+        s.failed_primary_allocations = m.micro_pool.failed_allocations;
+        s.failed_secondary_allocations = m.extent_pool.failed_allocations;
+        return s;
+    }
+
+    bool checkInvariants() const override
+    {
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        return state_->config.valid() && state_->storage.status().ok() && state_->manager.checkInvariants()
+            && state_->active_transactions == state_->manager.snapshot().token_reservation_count;
+    }
+
+    EngineKvStatus promote(RequestId request_id, HipStream stream, std::uint32_t* promoted)
+    {
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        if (promoted) *promoted = 0;
+        KvCacheManager& m = state_->manager;
+        std::optional<BlockTable> t = m.blockTable(request_id);
+        if (!t.has_value()) return {EngineKvError::RequestNotFound};
+        std::vector<PromotionPrepareResult> prepared;
+        auto const& e = t->entries();
+        for (std::size_t i = 0; i + kPromotionSourcePageCount <= e.size();) {
+            bool run = true;
+            for (std::size_t k = 0; k < kPromotionSourcePageCount && run; ++k) {
+                run = e[i + k].kind == PageKind::Micro && e[i + k].valid_tokens == kMicroPageTokenCapacity;
+            }
+            if (!run) {
+                ++i;
+                continue;
+            }
+            PromotionPrepareResult p = m.preparePromotion(request_id, e[i].logical_token_begin);
+            if (p.ok()) {
+                prepared.push_back(p);
+                i += kPromotionSourcePageCount;
+            } else if (p.error == KvCacheError::RequestConflict || p.error == KvCacheError::ResourceExhausted) {
+                break;
+            } else {
+                ++i;
+            }
+        }
+        if (prepared.empty()) return {};
+        std::vector<PageLeaseId> leases;
+        for (PromotionPrepareResult const& p : prepared) {
+            PageLeaseAcquireResult l = m.acquirePromotionIoLease(p.promotion_id);
+            if (l.ok()) leases.push_back(l.lease_id);
+        }
+        HipStatus const copied = state_->storage.promoteBatch(prepared, stream);
+        for (PageLeaseId l : leases) static_cast<void>(m.releasePageLease(l));
+        if (!copied.ok()) {
+            for (PromotionPrepareResult const& p : prepared) static_cast<void>(m.rollbackPromotion(p.promotion_id));
+            return mapDevice(copied);
+        }
+        std::uint32_t n = 0;
+        EngineKvStatus status{};
+        for (PromotionPrepareResult const& p : prepared) {
+            KvCacheError const c = m.commitPromotion(p.promotion_id);
+            if (c == KvCacheError::None) {
+                ++n;
+            } else if (status.ok()) {
+                status = mapMetadata(c);
+            }
+        }
+        if (promoted) *promoted = n;
+        return status;
+    }
+
+    std::shared_ptr<BackendState> const& state() const noexcept { return state_; }
+
+private:
+    std::shared_ptr<BackendState> state_;
+};
+
+}  // namespace
+
+std::unique_ptr<EngineKvBackend> createHeterogeneousHipEngineKvBackend(EngineKvConfig config,
+                                                                       std::uint32_t micro_page_capacity,
+                                                                       std::uint32_t extent_page_capacity)
+{
+    if (!config.valid() || micro_page_capacity == 0 || extent_page_capacity == 0) return nullptr;
+    try {
+        auto state = std::make_shared<BackendState>(config, micro_page_capacity, extent_page_capacity);
+        if (!state->storage.status().ok()) return nullptr;
+        return std::make_unique<HipEngineKvBackend>(std::move(state));
+    } catch (...) {
+        return nullptr;
+    }
+}
+
+bool injectHipEngineFailureOnce(EngineKvBackend& backend, HipFailurePoint point) noexcept
+{
+    auto* b = dynamic_cast<HipEngineKvBackend*>(&backend);
+    if (b == nullptr) return false;
+    b->state()->storage.injectFailureOnce(point);
+    return true;
+}
+
+EngineKvStatus promoteRequest(EngineKvBackend& backend, RequestId request_id, HipStream stream,
+                              std::uint32_t* promoted_pages)
+{
+    auto* b = dynamic_cast<HipEngineKvBackend*>(&backend);
+    if (b == nullptr) return {EngineKvError::InvalidArgument};
+    return b->promote(request_id, stream, promoted_pages);
+}
+
+bool engineBlockTable(EngineKvBackend const& backend, RequestId request_id, BlockTable& out)
+{
+    auto const* b = dynamic_cast<HipEngineKvBackend const*>(&backend);
+    if (b == nullptr) return false;
+    std::optional<BlockTable> t = b->state()->manager.blockTable(request_id);
+    if (!t.has_value()) return false;
+    out = std::move(*t);
+    return true;
+}
+
+void const* engineStorage(EngineKvBackend const& backend) noexcept
+{
+    auto const* b = dynamic_cast<HipEngineKvBackend const*>(&backend);
+    return b != nullptr ? b->state()->storage.handle() : nullptr;
+}
+
+}  // namespace kimkvcache

@@ -1,0 +1,445 @@
+// HipKvStorage and its staging helpers.  Data-path behaviour follows the
+// reference's CudaKvStorage (src/cuda/kv/append.cpp:10-140, gather.cpp:9-107,
+// promotion.cpp:8-64, src/cuda/attention/reference_attention.cpp:10-170): the
+// only old mapping whose page may change in an append is the partial micro
+// tail (copy-on-write), every appended segment lands in its page at
+// (segment begin - entry begin), promotions copy 8 micro pages to one extent.
+#include "storage.h"
+
+#include <algorithm>
+#include <cstring>
+#include <new>
+
+namespace kimkvcache {
+
+HipStatus mapStatus(kimkv_status s, HipError failure) noexcept
+{
+    if (s == KIMKV_OK) return {};
+    switch (s) {
+    case KIMKV_INVALID_ARGUMENT: return {HipError::InvalidArgument, kimkv_last_native_error()};
+    case KIMKV_RUNTIME_UNAVAILABLE: return {HipError::RuntimeUnavailable, kimkv_last_native_error()};
+    case KIMKV_ALLOCATION_FAILED: return {HipError::AllocationFailed, kimkv_last_native_error()};
+    case KIMKV_NOT_READY: return {HipError::NotReady, 0};
+    default: return {failure, kimkv_last_native_error()};
+    }
+}
+
+// ---- DeviceMemory -------------------------------------------------------------
+
+DeviceMemory::DeviceMemory(std::size_t bytes) : bytes_(bytes)
+{
+    if (bytes != 0 && kimkv_device_malloc(&ptr_, bytes) != KIMKV_OK) {
+        ptr_ = nullptr;
+    }
+}
+
+DeviceMemory::~DeviceMemory()
+{
+    if (ptr_ != nullptr) static_cast<void>(kimkv_device_free(ptr_));
+}
+
+DeviceMemory& DeviceMemory::operator=(DeviceMemory&& o) noexcept
+{
+    if (this != &o) {
+        if (ptr_ != nullptr) static_cast<void>(kimkv_device_free(ptr_));
+        ptr_ = o.ptr_;
+        bytes_ = o.bytes_;
+        o.ptr_ = nullptr;
+        o.bytes_ = 0;
+    }
+    return *this;
+}
+
+// ---- StagingRing -----------------------------------------------------------------
+
+StagingRing::StagingRing(std::size_t bytes) : size_(bytes), device_()
+{
+    void* host = nullptr;
+    if (kimkv_host_malloc_pinned(&host, bytes) == KIMKV_OK) host_ = static_cast<unsigned char*>(host);
+}
+
+StagingRing::~StagingRing()
+{
+    for (Region& r : live_) {
+        if (r.event != nullptr) {
+            static_cast<void>(kimkv_event_synchronize(r.event));
+            static_cast<void>(kimkv_event_destroy(r.event));
+        }
+    }
+    for (void* e : spare_events_) static_cast<void>(kimkv_event_destroy(e));
+    if (host_ != nullptr) static_cast<void>(kimkv_host_free_pinned(host_));
+}
+
+std::size_t StagingRing::reserve(std::size_t bytes)
+{
+    if (device_.get() == nullptr && host_ != nullptr) device_ = DeviceMemory(size_);
+    bytes = (bytes + 255) & ~std::size_t{255};
+    std::size_t begin = head_;
+    if (begin + bytes > size_) begin = 0;
+    std::size_t const end = begin + bytes;
+    // Regions are handed out in ring order and each fence event completes
+    // after every older region's consumer, so waiting on the first event at or
+    // after an overlapping region frees it and everything before it.
+    while (!live_.empty() && live_.front().begin < end && begin < live_.front().end) {
+        auto covering = std::find_if(live_.begin(), live_.end(), [](Region const& r) { return r.event != nullptr; });
+        if (covering == live_.end()) {
+            static_cast<void>(kimkv_device_synchronize());
+            for (Region const& r : live_) {
+                if (r.event != nullptr) spare_events_.push_back(r.event);
+            }
+            live_.clear();
+            break;
+        }
+        static_cast<void>(kimkv_event_synchronize(covering->event));
+        spare_events_.push_back(covering->event);
+        live_.erase(live_.begin(), std::next(covering));
+    }
+    live_.push_back(Region{begin, end, nullptr});
+    head_ = end;
+    return begin;
+}
+
+void* StagingRing::upload(void const* data, std::size_t bytes, HipStream stream)
+{
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (host_ == nullptr || bytes > size_ / 2) return nullptr;
+    std::size_t const off = reserve(bytes);
+    if (device_.get() == nullptr) return nullptr;
+    std::memcpy(host_ + off, data, bytes);
+    unsigned char* dev = static_cast<unsigned char*>(device_.get()) + off;
+    if (kimkv_memcpy_h2d_async(dev, host_ + off, bytes, stream) != KIMKV_OK) return nullptr;
+    return dev;
+}
+
+bool StagingRing::uploadTo(void* device_dst, void const* data, std::size_t bytes, HipStream stream)
+{
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (host_ == nullptr || bytes > size_ / 2) return false;
+    std::size_t const off = reserve(bytes);
+    std::memcpy(host_ + off, data, bytes);
+    return kimkv_memcpy_h2d_async(device_dst, host_ + off, bytes, stream) == KIMKV_OK;
+}
+
+void StagingRing::fence(HipStream stream)
+{
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (live_.empty() || live_.back().event != nullptr) return;
+    void* event = nullptr;
+    if (!spare_events_.empty()) {
+        event = spare_events_.back();
+        spare_events_.pop_back();
+    } else if (kimkv_event_create(&event, 0) != KIMKV_OK) {
+        event = nullptr;
+    }
+    if (event != nullptr && kimkv_event_record(event, stream) != KIMKV_OK) {
+        spare_events_.push_back(event);
+        event = nullptr;
+    }
+    if (event == nullptr) {
+        // Cannot fence: drain so every staged region is free again.
+        static_cast<void>(kimkv_stream_synchronize(stream));
+        for (Region const& r : live_) {
+            if (r.event != nullptr) spare_events_.push_back(r.event);
+        }
+        live_.clear();
+        return;
+    }
+    live_.back().event = event;   // covers every older region too
+}
+
+// ---- DeviceBufferCache ----------------------------------------------------------------
+
+DeviceBufferCache::~DeviceBufferCache()
+{
+    for (auto& [size, list] : free_) {
+        for (void* p : list) static_cast<void>(kimkv_device_free(p));
+    }
+}
+
+void* DeviceBufferCache::acquire(std::size_t bytes, std::size_t& granted)
+{
+    std::size_t cls = 4096;
+    while (cls < bytes) cls <<= 1;
+    {
+        std::lock_guard<std::mutex> lock(mutex_);
+        auto it = free_.find(cls);
+        if (it != free_.end() && !it->second.empty()) {
+            void* p = it->second.back();
+            it->second.pop_back();
+            granted = cls;
+            return p;
+        }
+    }
+    void* p = nullptr;
+    if (kimkv_device_malloc(&p, cls) != KIMKV_OK) return nullptr;
+    granted = cls;
+    return p;
+}
+
+void DeviceBufferCache::release(void* ptr, std::size_t granted) noexcept
+{
+    if (ptr == nullptr) return;
+    std::lock_guard<std::mutex> lock(mutex_);
+    try {
+        free_[granted].push_back(ptr);
+    } catch (...) {
+        static_cast<void>(kimkv_device_free(ptr));
+    }
+}
+
+// ---- HipKvStorage --------------------------------------------------------------------
+
+HipKvStorage::HipKvStorage(KvLayout layout, std::uint32_t micro_capacity, std::uint32_t extent_capacity,
+                           std::uint16_t micro_page_tokens, std::uint16_t extent_page_tokens) noexcept
+    : layout_(layout),
+      micro_capacity_(micro_capacity),
+      extent_capacity_(extent_capacity),
+      micro_tokens_(micro_page_tokens),
+      extent_tokens_(extent_page_tokens),
+      ring_(8u << 20)
+{
+    if (!layout.valid() || micro_page_tokens == 0 || extent_page_tokens == 0) {
+        status_ = HipStatus{HipError::InvalidArgument, 0};
+        return;
+    }
+    if (kimkv_device_count() == 0) {
+        status_ = HipStatus{HipError::RuntimeUnavailable, 0};
+        return;
+    }
+    kimkv_layout const l{layout.layer_count, layout.kv_head_count, layout.head_dimension};
+    status_ = mapStatus(kimkv_storage_create(&storage_, l, micro_capacity, extent_capacity, micro_page_tokens,
+                                             extent_page_tokens),
+                        HipError::AllocationFailed);
+}
+
+HipKvStorage::~HipKvStorage()
+{
+    if (storage_ != nullptr) static_cast<void>(kimkv_storage_destroy(storage_));
+}
+
+HipStorageSnapshot HipKvStorage::snapshot() const noexcept
+{
+    HipStorageSnapshot s;
+    s.micro_capacity = micro_capacity_;
+    s.extent_capacity = extent_capacity_;
+    s.micro_page_tokens = micro_tokens_;
+    s.extent_page_tokens = extent_tokens_;
+    std::size_t per_token = 0;
+    if (layout_.bytesForTokens(1, per_token)) {
+        s.micro_reserved_bytes = per_token * micro_tokens_ * micro_capacity_;
+        s.extent_reserved_bytes = per_token * extent_tokens_ * extent_capacity_;
+    }
+    return s;
+}
+
+bool HipKvStorage::pageExists(PageHandle h) const noexcept
+{
+    if (!h.isStructurallyValid() || storage_ == nullptr) return false;
+    return h.kind == PageKind::Micro ? h.slot < micro_capacity_ : h.slot < extent_capacity_;
+}
+
+bool HipKvStorage::validTable(BlockTable const& table) const
+{
+    bool const standard = micro_tokens_ == kMicroPageTokenCapacity && extent_tokens_ == kExtentPageTokenCapacity;
+    bool const structure = standard ? table.checkInvariants()
+                                    : extent_capacity_ == 0 && table.checkInvariants(micro_tokens_);
+    if (!structure) return false;
+    return std::all_of(table.entries().begin(), table.entries().end(),
+                       [this](MappingEntry const& e) { return pageExists(e.handle); });
+}
+
+void HipKvStorage::descriptors(BlockTable const& table, std::vector<kimkv_block_desc>& out) const
+{
+    out.clear();
+    out.reserve(table.entries().size());
+    for (MappingEntry const& e : table.entries()) {
+        kimkv_block_desc d{};
+        d.slot = e.handle.slot;
+        d.generation = e.handle.generation;
+        d.logical_token_begin = e.logical_token_begin;
+        d.valid_tokens = e.valid_tokens;
+        d.page_token_capacity = pageTokenCapacity(e.kind);
+        d.kind = static_cast<std::uint8_t>(e.kind);
+        out.push_back(d);
+    }
+}
+
+bool HipKvStorage::consumeFailure(HipFailurePoint point) noexcept
+{
+    std::lock_guard<std::mutex> lock(fault_mutex_);
+    bool& flag = point == HipFailurePoint::Submission ? fail_submission_once_ : fail_completion_once_;
+    bool const fire = flag;
+    flag = false;
+    return fire;
+}
+
+void HipKvStorage::injectFailureOnce(HipFailurePoint point) noexcept
+{
+    std::lock_guard<std::mutex> lock(fault_mutex_);
+    (point == HipFailurePoint::Submission ? fail_submission_once_ : fail_completion_once_) = true;
+}
+
+HipStatus HipKvStorage::finish(HipStream stream, HipStatus submitted) noexcept
+{
+    kimkv_status const s = kimkv_stream_synchronize(stream);
+    if (!submitted.ok()) return submitted;
+    if (s != KIMKV_OK) return HipStatus{HipError::ExecutionFailed, kimkv_last_native_error()};
+    if (consumeFailure(HipFailurePoint::Completion)) return HipStatus{HipError::ExecutionFailed, -1};
+    return {};
+}
+
+namespace {
+
+struct TempDevice {
+    DeviceMemory mem;
+    bool upload(void const* data, std::size_t bytes, HipStream stream)
+    {
+        mem = DeviceMemory(bytes);
+        return mem.get() != nullptr && kimkv_memcpy_h2d_async(mem.get(), data, bytes, stream) == KIMKV_OK;
+    }
+};
+
+}  // namespace
+
+HipStatus HipKvStorage::append(BlockTable const& before, BlockTable const& after, std::uint32_t begin,
+                               std::uint32_t count, KvScalar const* input, HipStream stream)
+{
+    if (!status_.ok()) return status_;
+    if (consumeFailure(HipFailurePoint::Submission)) return HipStatus{HipError::SubmissionFailed, 0};
+    std::uint64_t const end = static_cast<std::uint64_t>(begin) + count;
+    if (input == nullptr || count == 0 || end > 0xFFFFFFFFull || !validTable(before) || !validTable(after)
+        || before.tokenCount() != begin || after.tokenCount() != end) {
+        return HipStatus{HipError::InvalidArgument, 0};
+    }
+    std::size_t const hd = static_cast<std::size_t>(layout_.kv_head_count) * layout_.head_dimension;
+    std::vector<kimkv_append_job> jobs;
+    // Copy-on-write source of the replaced partial tail, if any.
+    PageHandle cow_src = PageHandle::invalid();
+    std::uint16_t cow_tokens = 0;
+    PageHandle cow_dst = PageHandle::invalid();
+    for (MappingEntry const& old : before.entries()) {
+        auto rep = std::find_if(after.entries().begin(), after.entries().end(), [&old](MappingEntry const& e) {
+            return e.logical_token_begin == old.logical_token_begin;
+        });
+        if (rep == after.entries().end()) return HipStatus{HipError::InvalidArgument, 0};
+        if (rep->handle == old.handle) continue;
+        bool const tail = old.logicalTokenEnd() == begin;
+        if (!tail || old.kind != PageKind::Micro || rep->kind != PageKind::Micro || old.valid_tokens >= micro_tokens_
+            || rep->valid_tokens < old.valid_tokens) {
+            return HipStatus{HipError::InvalidArgument, 0};
+        }
+        cow_src = old.handle;
+        cow_tokens = old.valid_tokens;
+        cow_dst = rep->handle;
+    }
+    for (MappingEntry const& e : after.entries()) {
+        std::uint32_t const sb = std::max(begin, e.logical_token_begin);
+        std::uint32_t const se = std::min(static_cast<std::uint32_t>(end), e.logicalTokenEnd());
+        if (sb >= se) continue;
+        kimkv_append_job j{};
+        std::size_t const off = static_cast<std::size_t>(sb - begin) * hd;
+        j.src_key = input + off;
+        j.src_value = input + static_cast<std::size_t>(count) * hd + off;
+        j.src_layer_stride = 2ull * count * hd;
+        j.src_token_stride = static_cast<std::uint32_t>(hd);
+        j.layer_begin = 0;
+        j.layer_count = layout_.layer_count;
+        j.token_count = se - sb;
+        j.dst_slot = e.handle.slot;
+        j.dst_kind = static_cast<std::uint8_t>(e.kind);
+        j.dst_token = static_cast<std::uint16_t>(sb - e.logical_token_begin);
+        if (cow_dst.isStructurallyValid() && e.handle == cow_dst) {
+            j.cow_slot = cow_src.slot;
+            j.cow_kind = static_cast<std::uint8_t>(cow_src.kind);
+            j.cow_tokens = cow_tokens;
+        }
+        jobs.push_back(j);
+    }
+    if (jobs.empty()) return HipStatus{HipError::InvalidArgument, 0};
+    TempDevice dev;
+    if (!dev.upload(jobs.data(), jobs.size() * sizeof(kimkv_append_job), stream)) {
+        return finish(stream, HipStatus{HipError::SubmissionFailed, kimkv_last_native_error()});
+    }
+    HipStatus const s = mapStatus(kimkv_append_batch(storage_, static_cast<kimkv_append_job const*>(dev.mem.get()),
+                                                     static_cast<std::uint32_t>(jobs.size()), layout_.layer_count,
+                                                     stream),
+                                  HipError::SubmissionFailed);
+    return finish(stream, s);
+}
+
+HipStatus HipKvStorage::gather(BlockTable const& table, KvScalar* out, HipStream stream)
+{
+    if (!status_.ok()) return status_;
+    if (consumeFailure(HipFailurePoint::Submission)) return HipStatus{HipError::SubmissionFailed, 0};
+    if (out == nullptr || table.tokenCount() == 0 || !validTable(table)) return HipStatus{HipError::InvalidArgument, 0};
+    std::vector<kimkv_block_desc> d;
+    descriptors(table, d);
+    TempDevice dev;
+    if (!dev.upload(d.data(), d.size() * sizeof(kimkv_block_desc), stream)) {
+        return finish(stream, HipStatus{HipError::SubmissionFailed, kimkv_last_native_error()});
+    }
+    HipStatus const s = mapStatus(kimkv_gather(storage_, static_cast<kimkv_block_desc const*>(dev.mem.get()),
+                                               static_cast<std::uint32_t>(d.size()), table.tokenCount(), out, stream),
+                                  HipError::SubmissionFailed);
+    return finish(stream, s);
+}
+
+HipStatus HipKvStorage::promoteBatch(std::vector<PromotionPrepareResult> const& promotions, HipStream stream)
+{
+    if (!status_.ok()) return status_;
+    if (consumeFailure(HipFailurePoint::Submission)) return HipStatus{HipError::SubmissionFailed, 0};
+    if (micro_tokens_ != kMicroPageTokenCapacity || extent_tokens_ != kExtentPageTokenCapacity) {
+        return HipStatus{HipError::InvalidArgument, 0};
+    }
+    std::vector<kimkv_promotion_job> jobs;
+    for (PromotionPrepareResult const& p : promotions) {
+        if (!p.ok() || p.target_handle.kind != PageKind::Extent || !pageExists(p.target_handle)) {
+            return HipStatus{HipError::InvalidArgument, 0};
+        }
+        kimkv_promotion_job j{};
+        for (std::size_t i = 0; i < kPromotionSourcePageCount; ++i) {
+            PageHandle const s = p.source_handles[i];
+            if (s.kind != PageKind::Micro || !pageExists(s)) return HipStatus{HipError::InvalidArgument, 0};
+            j.micro_slots[i] = s.slot;
+        }
+        j.extent_slot = p.target_handle.slot;
+        jobs.push_back(j);
+    }
+    if (jobs.empty()) return {};
+    TempDevice dev;
+    if (!dev.upload(jobs.data(), jobs.size() * sizeof(kimkv_promotion_job), stream)) {
+        return finish(stream, HipStatus{HipError::SubmissionFailed, kimkv_last_native_error()});
+    }
+    HipStatus const s = mapStatus(kimkv_promote_batch(storage_, static_cast<kimkv_promotion_job const*>(dev.mem.get()),
+                                                      static_cast<std::uint32_t>(jobs.size()), stream),
+                                  HipError::SubmissionFailed);
+    return finish(stream, s);
+}
+
+HipStatus HipKvStorage::promote(PromotionPrepareResult const& promotion, HipStream stream)
+{
+    return promoteBatch(std::vector<PromotionPrepareResult>{promotion}, stream);
+}
+
+HipStatus HipKvStorage::referenceAttention(BlockTable const& table, float const* query, float* output,
+                                           HipStream stream)
+{
+    if (!status_.ok()) return status_;
+    if (consumeFailure(HipFailurePoint::Submission)) return HipStatus{HipError::SubmissionFailed, 0};
+    if (query == nullptr || output == nullptr || table.tokenCount() == 0 || !validTable(table)) {
+        return HipStatus{HipError::InvalidArgument, 0};
+    }
+    std::vector<kimkv_block_desc> d;
+    descriptors(table, d);
+    TempDevice dev;
+    if (!dev.upload(d.data(), d.size() * sizeof(kimkv_block_desc), stream)) {
+        return finish(stream, HipStatus{HipError::SubmissionFailed, kimkv_last_native_error()});
+    }
+    HipStatus const s = mapStatus(
+        kimkv_reference_attention(storage_, static_cast<kimkv_block_desc const*>(dev.mem.get()),
+                                  static_cast<std::uint32_t>(d.size()), table.tokenCount(), query, output, stream),
+        HipError::SubmissionFailed);
+    return finish(stream, s);
+}
+
+}  // namespace kimkvcache

@@ -1,0 +1,148 @@
+// HipKvStorage: the host side of the device pools (counterpart of the
+// reference's src/cuda/kv/storage.h:18-166).  It owns a kimkv_storage from the
+// C-ABI, validates tables against it, converts block tables to device
+// descriptors and stages small per-launch uploads without blocking the host.
+#pragma once
+
+#include "kimkv_hip.h"
+
+#include "kim-kv/core/block_table.h"
+#include "kim-kv/core/kv_layout.h"
+#include "kim-kv/hip/hip_status.h"
+#include "kim-kv/runtime/promotion.h"
+
+#include <cstddef>
+#include <cstdint>
+#include <deque>
+#include <map>
+#include <mutex>
+#include <vector>
+
+namespace kimkvcache {
+
+HipStatus mapStatus(kimkv_status s, HipError failure) noexcept;
+
+// Owning device allocation.
+class DeviceMemory final {
+public:
+    DeviceMemory() = default;
+    explicit DeviceMemory(std::size_t bytes);
+    ~DeviceMemory();
+    DeviceMemory(DeviceMemory&& o) noexcept : ptr_(o.ptr_), bytes_(o.bytes_) { o.ptr_ = nullptr; o.bytes_ = 0; }
+    DeviceMemory& operator=(DeviceMemory&& o) noexcept;
+    DeviceMemory(DeviceMemory const&) = delete;
+    DeviceMemory& operator=(DeviceMemory const&) = delete;
+
+    [[nodiscard]] void* get() const noexcept { return ptr_; }
+    [[nodiscard]] std::size_t size() const noexcept { return bytes_; }
+    [[nodiscard]] bool ok() const noexcept { return ptr_ != nullptr || bytes_ == 0; }
+
+private:
+    void* ptr_{nullptr};
+    std::size_t bytes_{0};
+};
+
+// Pinned host ring + device ring of the same size.  upload() copies host bytes
+// into the ring and enqueues the H2D copy; fence() records an event after the
+// work that consumes the uploaded bytes so the region is only reused after it.
+class StagingRing final {
+public:
+    explicit StagingRing(std::size_t bytes);
+    ~StagingRing();
+    StagingRing(StagingRing const&) = delete;
+    StagingRing& operator=(StagingRing const&) = delete;
+
+    [[nodiscard]] bool ok() const noexcept { return host_ != nullptr && device_.get() != nullptr; }
+    // Returns the device address of the staged copy, or nullptr on failure.
+    [[nodiscard]] void* upload(void const* data, std::size_t bytes, HipStream stream);
+    // Host staging only (the caller names the device destination).
+    [[nodiscard]] bool uploadTo(void* device_dst, void const* data, std::size_t bytes, HipStream stream);
+    void fence(HipStream stream);
+
+private:
+    struct Region {
+        std::size_t begin;
+        std::size_t end;
+        void* event;   // nullptr until fenced
+    };
+    [[nodiscard]] std::size_t reserve(std::size_t bytes);
+
+    std::size_t size_;
+    std::size_t head_{0};
+    unsigned char* host_{nullptr};
+    DeviceMemory device_;
+    std::deque<Region> live_;
+    std::vector<void*> spare_events_;
+    std::mutex mutex_;
+};
+
+// Size-class cache of device buffers (per-transaction descriptor arrays).
+class DeviceBufferCache final {
+public:
+    ~DeviceBufferCache();
+    [[nodiscard]] void* acquire(std::size_t bytes, std::size_t& granted);
+    void release(void* ptr, std::size_t granted) noexcept;
+
+private:
+    std::map<std::size_t, std::vector<void*>> free_;
+    std::mutex mutex_;
+};
+
+class HipKvStorage final {
+public:
+    HipKvStorage(KvLayout layout, std::uint32_t micro_capacity, std::uint32_t extent_capacity,
+                 std::uint16_t micro_page_tokens = kMicroPageTokenCapacity,
+                 std::uint16_t extent_page_tokens = kExtentPageTokenCapacity) noexcept;
+    ~HipKvStorage();
+    HipKvStorage(HipKvStorage const&) = delete;
+    HipKvStorage& operator=(HipKvStorage const&) = delete;
+
+    [[nodiscard]] HipStatus status() const noexcept { return status_; }
+    [[nodiscard]] kimkv_storage* handle() const noexcept { return storage_; }
+    [[nodiscard]] KvLayout layout() const noexcept { return layout_; }
+    [[nodiscard]] HipStorageSnapshot snapshot() const noexcept;
+    [[nodiscard]] std::uint16_t pageTokenCapacity(PageKind kind) const noexcept
+    {
+        return kind == PageKind::Micro ? micro_tokens_ : extent_tokens_;
+    }
+    [[nodiscard]] bool pageExists(PageHandle handle) const noexcept;
+    // Structure (standard or uniform capacities) plus every page in range
+    // (CudaKvStorage::Impl::validTable, src/cuda/kv/storage.cpp:79-97).
+    [[nodiscard]] bool validTable(BlockTable const& table) const;
+    void descriptors(BlockTable const& table, std::vector<kimkv_block_desc>& out) const;
+
+    [[nodiscard]] bool consumeFailure(HipFailurePoint point) noexcept;
+    void injectFailureOnce(HipFailurePoint point) noexcept;
+
+    StagingRing& ring() noexcept { return ring_; }
+    DeviceBufferCache& buffers() noexcept { return buffers_; }
+
+    // Synchronous data-path operations used by HipKvCache: enqueue on
+    // `stream`, then wait for completion.
+    [[nodiscard]] HipStatus append(BlockTable const& before, BlockTable const& after,
+                                   std::uint32_t append_token_begin, std::uint32_t token_count,
+                                   KvScalar const* device_input, HipStream stream);
+    [[nodiscard]] HipStatus gather(BlockTable const& table, KvScalar* device_output, HipStream stream);
+    [[nodiscard]] HipStatus promote(PromotionPrepareResult const& promotion, HipStream stream);
+    [[nodiscard]] HipStatus promoteBatch(std::vector<PromotionPrepareResult> const& promotions, HipStream stream);
+    [[nodiscard]] HipStatus referenceAttention(BlockTable const& table, float const* device_query,
+                                               float* device_output, HipStream stream);
+
+private:
+    [[nodiscard]] HipStatus finish(HipStream stream, HipStatus submitted) noexcept;
+
+    KvLayout layout_{};
+    std::uint32_t micro_capacity_{0};
+    std::uint32_t extent_capacity_{0};
+    std::uint16_t micro_tokens_{0};
+    std::uint16_t extent_tokens_{0};
+    kimkv_storage* storage_{nullptr};
+    HipStatus status_{};
+    StagingRing ring_;
+    DeviceBufferCache buffers_;
+    std::mutex fault_mutex_;
+    bool fail_submission_once_{false};
+    bool fail_completion_once_{false};
+};
+
+}  // namespace kimkvcache

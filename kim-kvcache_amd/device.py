@@ -113,6 +113,8 @@ _SIGNATURES = {
     "kimkv_paged_decode_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                 ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                 ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_reference_attention": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "kimkv_decode_timing": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                            ctypes.POINTER(ctypes.c_uint64)]),
     "kimkv_synth_value": (ctypes.c_uint16, [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32]),

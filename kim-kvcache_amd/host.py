@@ -1,0 +1,338 @@
+"""ctypes binding of the host facade (include/kimkv_host.h, libkimkv.so).
+
+Engine (EngineKvBackend + TokenTransaction), Cache (the CudaKvCache
+counterpart) and Manager (KvCacheManager) for Python callers: tests and the
+benchmark drive the C++ host layer through these.  Fails loudly when the
+library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import List, Optional, Sequence
+
+from . import device
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "_lib", "libkimkv.so")
+
+U16, U32, U64, P, I = ctypes.c_uint16, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int
+
+# EngineKvError values (include/kim-kv/engine/engine_kv.h).
+ENGINE_ERRORS = ["none", "invalid_argument", "invalid_state", "request_not_found", "request_already_exists",
+                 "request_conflict", "resource_exhausted", "layer_out_of_order", "submission_failed",
+                 "execution_failed", "internal_error"]
+# KvCacheError values (include/kim-kv/core/page_state.h).
+KV_ERRORS = ["none", "invalid_argument", "request_not_found", "request_already_exists", "request_conflict",
+             "resource_exhausted", "invalid_state", "token_reservation_not_found", "promotion_not_eligible",
+             "promotion_not_found", "promotion_conflict", "internal_invariant_violation"]
+PHASES = ["empty", "awaiting_layer_write", "awaiting_layer_attention", "ready_to_commit", "failed", "committed",
+          "rolled_back"]
+
+
+class MappingEntry(ctypes.Structure):
+    _fields_ = [("logical_token_begin", U32), ("valid_tokens", U16), ("kind", ctypes.c_uint8),
+                ("reserved", ctypes.c_uint8), ("slot", U32), ("generation", U32)]
+
+
+class EngineConfig(ctypes.Structure):
+    _fields_ = [("layers", U32), ("kv_heads", U32), ("head_dim", U32), ("query_heads", U32),
+                ("attention_workspace_bytes", U64)]
+
+
+class DecodeRequest(ctypes.Structure):
+    _fields_ = [("layer", U32), ("reserved", U32), ("query", P), ("output", P), ("workspace", P),
+                ("workspace_bytes", U64), ("attention_scale", ctypes.c_float)]
+
+
+class EngineSnapshot(ctypes.Structure):
+    _fields_ = [("request_count", U64), ("active_transaction_count", U64), ("committed_token_count", U64),
+                ("batched_attention_submissions", U64), ("batched_attention_lanes", U64),
+                ("batched_write_submissions", U64), ("primary_page_tokens", U32), ("secondary_page_tokens", U32),
+                ("primary_page_capacity", U32), ("secondary_page_capacity", U32),
+                ("allocated_primary_pages", U32), ("allocated_secondary_pages", U32),
+                ("successful_primary_allocations", U64), ("successful_secondary_allocations", U64),
+                ("failed_primary_allocations", U64), ("failed_secondary_allocations", U64),
+                ("storage_reserved_bytes", U64)]
+
+
+class PoolSnapshot(ctypes.Structure):
+    _fields_ = [("kind", U32), ("total_slots", U32), ("free_slots", U32), ("allocated_slots", U32),
+                ("successful_allocations", U64), ("successful_releases", U64), ("failed_allocations", U64),
+                ("rejected_releases", U64)]
+
+
+class ManagerSnapshot(ctypes.Structure):
+    _fields_ = [("request_count", U64), ("promotion_count", U64), ("page_lease_count", U64),
+                ("token_reservation_count", U64), ("micro_pool", PoolSnapshot), ("extent_pool", PoolSnapshot)]
+
+
+class CacheResult(ctypes.Structure):
+    _fields_ = [("metadata_error", I), ("device_status", I)]
+
+    def ok(self) -> bool:
+        return self.metadata_error == 0 and self.device_status == 0
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+_SIG = {
+    "kimkv_engine_create": (P, [ctypes.POINTER(EngineConfig), U32, U32]),
+    "kimkv_engine_destroy": (None, [P]),
+    "kimkv_engine_create_request": (I, [P, U64]),
+    "kimkv_engine_fork_request": (I, [P, U64, U64]),
+    "kimkv_engine_release_request": (I, [P, U64]),
+    "kimkv_engine_reserve_token": (I, [P, U64, U32, P, ctypes.POINTER(P)]),
+    "kimkv_engine_get_snapshot": (None, [P, ctypes.POINTER(EngineSnapshot)]),
+    "kimkv_engine_check_invariants": (I, [P]),
+    "kimkv_engine_inject_failure_once": (I, [P, U32]),
+    "kimkv_engine_promote_request": (I, [P, U64, P, ctypes.POINTER(U32)]),
+    "kimkv_engine_block_table": (I, [P, U64, ctypes.POINTER(U64), P, U32, ctypes.POINTER(U32)]),
+    "kimkv_engine_storage": (P, [P]),
+    "kimkv_txn_write_layer": (I, [P, U32, P, P]),
+    "kimkv_txn_attend_layer": (I, [P, ctypes.POINTER(DecodeRequest)]),
+    "kimkv_txn_commit": (I, [P]),
+    "kimkv_txn_rollback": (I, [P]),
+    "kimkv_txn_state": (None, [P, ctypes.POINTER(U32), ctypes.POINTER(U32), ctypes.POINTER(U32)]),
+    "kimkv_txn_destroy": (None, [P]),
+    "kimkv_attend_layer_batch": (None, [ctypes.POINTER(P), ctypes.POINTER(DecodeRequest), U32, ctypes.POINTER(I)]),
+    "kimkv_write_layer_batch": (None, [ctypes.POINTER(P), ctypes.POINTER(U32), ctypes.POINTER(P), ctypes.POINTER(P),
+                                       U32, ctypes.POINTER(I)]),
+    "kimkv_cache_create": (P, [device.Layout, U32, U32]),
+    "kimkv_cache_destroy": (None, [P]),
+    "kimkv_cache_status": (I, [P]),
+    "kimkv_cache_manager": (P, [P]),
+    "kimkv_cache_storage": (P, [P]),
+    "kimkv_cache_append": (CacheResult, [P, U64, U32, P, P]),
+    "kimkv_cache_promote": (CacheResult, [P, U64, U32, P]),
+    "kimkv_cache_gather": (CacheResult, [P, U64, P, P]),
+    "kimkv_cache_reference_attention": (CacheResult, [P, U64, P, P, P]),
+    "kimkv_cache_inject_failure_once": (None, [P, U32]),
+    "kimkv_manager_create": (P, [U32, U32]),
+    "kimkv_manager_destroy": (None, [P]),
+    "kimkv_manager_create_request": (I, [P, U64]),
+    "kimkv_manager_append": (I, [P, U64, U32]),
+    "kimkv_manager_prepare_promotion": (I, [P, U64, U32, ctypes.POINTER(U64), P, P]),
+    "kimkv_manager_commit_promotion": (I, [P, U64]),
+    "kimkv_manager_fork_request": (I, [P, U64, U64]),
+    "kimkv_manager_block_table": (I, [P, U64, ctypes.POINTER(U64), P, U32, ctypes.POINTER(U32)]),
+    "kimkv_manager_permute_free_slots": (I, [P, U32, U64]),
+    "kimkv_manager_check_invariants": (I, [P]),
+    "kimkv_manager_get_snapshot": (None, [P, ctypes.POINTER(ManagerSnapshot)]),
+    "kimkv_manager_release_request": (I, [P, U64]),
+    "kimkv_seeded_permutation": (None, [U64, U32, P]),
+}
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        device.lib()   # libkimkv.so links libkimkv_hip.so
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIG.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def _table(getter, handle, rid):
+    version, count = U64(), U32()
+    rc = getter(handle, rid, ctypes.byref(version), None, 0, ctypes.byref(count))
+    if rc != 0:
+        return None
+    buf = (MappingEntry * max(count.value, 1))()
+    rc = getter(handle, rid, ctypes.byref(version), buf, count.value, ctypes.byref(count))
+    assert rc == 0
+    return version.value, [(e.logical_token_begin, e.valid_tokens, e.kind, e.slot, e.generation)
+                           for e in buf[:count.value]]
+
+
+def storage_info(handle: int) -> device.StorageInfo:
+    info = device.StorageInfo()
+    device.check(device.lib().kimkv_storage_query(ctypes.c_void_p(handle), ctypes.byref(info)), "storage_query")
+    return info
+
+
+def descriptors_from_entries(entries, micro_tokens: int = 8, extent_tokens: int = 64):
+    import numpy as np
+    out = np.zeros(len(entries), dtype=device.BLOCK_DESC)
+    for i, (b, v, k, s, g) in enumerate(entries):
+        out[i] = (s, g, b, v, micro_tokens if k == 0 else extent_tokens, k)
+    return out
+
+
+class Transaction:
+    def __init__(self, handle: int):
+        self.h = handle
+
+    def write_layer(self, layer: int, key: int, value: int) -> int:
+        return lib().kimkv_txn_write_layer(self.h, layer, key, value)
+
+    def attend_layer(self, layer, query, output, workspace, workspace_bytes, scale) -> int:
+        r = DecodeRequest(layer, 0, query, output, workspace, workspace_bytes, scale)
+        return lib().kimkv_txn_attend_layer(self.h, ctypes.byref(r))
+
+    def commit(self) -> int:
+        return lib().kimkv_txn_commit(self.h)
+
+    def rollback(self) -> int:
+        return lib().kimkv_txn_rollback(self.h)
+
+    def state(self):
+        ph, nl, pos = U32(), U32(), U32()
+        lib().kimkv_txn_state(self.h, ctypes.byref(ph), ctypes.byref(nl), ctypes.byref(pos))
+        return PHASES[ph.value], nl.value, pos.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().kimkv_txn_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def attend_layer_batch(txns: Sequence[Transaction], requests: Sequence[tuple]) -> List[int]:
+    n = len(txns)
+    hs = (P * n)(*[t.h for t in txns])
+    rs = (DecodeRequest * n)(*[DecodeRequest(r[0], 0, *r[1:]) for r in requests])
+    st = (I * n)()
+    lib().kimkv_attend_layer_batch(hs, rs, n, st)
+    return list(st)
+
+
+def write_layer_batch(txns: Sequence[Transaction], layers, keys, values) -> List[int]:
+    n = len(txns)
+    hs = (P * n)(*[t.h for t in txns])
+    st = (I * n)()
+    lib().kimkv_write_layer_batch(hs, (U32 * n)(*layers), (P * n)(*keys), (P * n)(*values), n, st)
+    return list(st)
+
+
+class Engine:
+    """createHeterogeneousHipEngineKvBackend through the C facade."""
+
+    def __init__(self, layers, kv_heads, head_dim, query_heads, workspace_bytes, micro_capacity, extent_capacity):
+        cfg = EngineConfig(layers, kv_heads, head_dim, query_heads, workspace_bytes)
+        self.h = lib().kimkv_engine_create(ctypes.byref(cfg), micro_capacity, extent_capacity)
+        if not self.h:
+            raise RuntimeError("engine backend creation failed")
+        self.layers, self.kv_heads, self.head_dim, self.query_heads = layers, kv_heads, head_dim, query_heads
+
+    def create_request(self, rid) -> int:
+        return lib().kimkv_engine_create_request(self.h, rid)
+
+    def fork_request(self, src, child) -> int:
+        return lib().kimkv_engine_fork_request(self.h, src, child)
+
+    def release_request(self, rid) -> int:
+        return lib().kimkv_engine_release_request(self.h, rid)
+
+    def reserve_token(self, rid, expected, stream: Optional[device.Stream] = None):
+        out = P()
+        rc = lib().kimkv_engine_reserve_token(self.h, rid, expected, stream.handle if stream else None,
+                                              ctypes.byref(out))
+        return rc, (Transaction(out.value) if rc == 0 else None)
+
+    def snapshot(self) -> EngineSnapshot:
+        s = EngineSnapshot()
+        lib().kimkv_engine_get_snapshot(self.h, ctypes.byref(s))
+        return s
+
+    def check_invariants(self) -> bool:
+        return lib().kimkv_engine_check_invariants(self.h) == 1
+
+    def inject_failure_once(self, point: str) -> bool:
+        return lib().kimkv_engine_inject_failure_once(self.h, 0 if point == "submission" else 1) == 1
+
+    def promote_request(self, rid, stream: Optional[device.Stream] = None):
+        n = U32()
+        rc = lib().kimkv_engine_promote_request(self.h, rid, stream.handle if stream else None, ctypes.byref(n))
+        return rc, n.value
+
+    def block_table(self, rid):
+        return _table(lib().kimkv_engine_block_table, self.h, rid)
+
+    def storage_handle(self) -> int:
+        return lib().kimkv_engine_storage(self.h)
+
+    def close(self):
+        if self.h:
+            lib().kimkv_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Cache:
+    """The CudaKvCache counterpart (HipKvCache)."""
+
+    def __init__(self, layers, kv_heads, head_dim, micro_capacity, extent_capacity):
+        self.h = lib().kimkv_cache_create(device.Layout(layers, kv_heads, head_dim), micro_capacity, extent_capacity)
+        if not self.h:
+            raise RuntimeError("cache creation failed")
+        self.mgr = lib().kimkv_cache_manager(self.h)
+        self.layers, self.kv_heads, self.head_dim = layers, kv_heads, head_dim
+
+    def status(self) -> int:
+        return lib().kimkv_cache_status(self.h)
+
+    def create_request(self, rid) -> int:
+        return lib().kimkv_manager_create_request(self.mgr, rid)
+
+    def fork_request(self, src, child) -> int:
+        return lib().kimkv_manager_fork_request(self.mgr, src, child)
+
+    def append(self, rid, n, input_ptr, stream: Optional[device.Stream] = None) -> CacheResult:
+        return lib().kimkv_cache_append(self.h, rid, n, input_ptr, stream.handle if stream else None)
+
+    def promote(self, rid, begin, stream: Optional[device.Stream] = None) -> CacheResult:
+        return lib().kimkv_cache_promote(self.h, rid, begin, stream.handle if stream else None)
+
+    def gather(self, rid, out_ptr, stream: Optional[device.Stream] = None) -> CacheResult:
+        return lib().kimkv_cache_gather(self.h, rid, out_ptr, stream.handle if stream else None)
+
+    def reference_attention(self, rid, q_ptr, o_ptr, stream: Optional[device.Stream] = None) -> CacheResult:
+        return lib().kimkv_cache_reference_attention(self.h, rid, q_ptr, o_ptr, stream.handle if stream else None)
+
+    def inject_failure_once(self, point: str) -> None:
+        lib().kimkv_cache_inject_failure_once(self.h, 0 if point == "submission" else 1)
+
+    def storage_info(self) -> device.StorageInfo:
+        return storage_info(lib().kimkv_cache_storage(self.h))
+
+    def snapshot(self):
+        s = ManagerSnapshot()
+        lib().kimkv_manager_get_snapshot(self.mgr, ctypes.byref(s))
+        return s
+
+    def release_request(self, rid) -> int:
+        return lib().kimkv_manager_release_request(self.mgr, rid)
+
+    def block_table(self, rid):
+        return _table(lib().kimkv_manager_block_table, self.mgr, rid)
+
+    def check_invariants(self) -> bool:
+        return lib().kimkv_manager_check_invariants(self.mgr) == 1
+
+    def close(self):
+        if self.h:
+            lib().kimkv_cache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -53,3 +53,12 @@ def test_workspace_never_exceeds_reference_requirement(kimkv):
             assert ws <= 32 * T * 4          # src/cuda/engine/transaction.cpp:56-64
             if T <= chunk:
                 assert ws == 0
+
+
+def test_host_library_exports_every_declared_symbol(kimkv):
+    path = os.path.join(os.path.dirname(kimkv.device.LIB_PATH), "libkimkv.so")
+    lib = ctypes.CDLL(path)
+    names = _declared("kimkv_host.h")
+    assert len(names) >= 45
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing

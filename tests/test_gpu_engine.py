@@ -1,0 +1,413 @@
+"""GPU tests of the C++ host layer over the HIP kernels: the engine backend
+(token transactions, batched attention/write, fork + partial-tail COW, fault
+injection, engine promotion) and the HipKvCache facade.  Scenarios mirror the
+reference's tests/cuda/cuda_engine_kv_backend_test.cpp and
+tests/cuda/cuda_kv_test.cpp; every data check is against closed forms or the
+oracle."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import make_kv_closed_form, to_f32
+
+pytestmark = pytest.mark.gpu
+
+SUBMISSION_FAILED = 8   # EngineKvError::SubmissionFailed
+EXECUTION_FAILED = 9    # EngineKvError::ExecutionFailed
+DEV_SUBMISSION_FAILED = 4
+DEV_EXECUTION_FAILED = 6
+
+
+def f16(*values):
+    return np.array(values, dtype=np.float16).view(np.uint16)
+
+
+@pytest.fixture(scope="module")
+def host(kimkv, dev):
+    import importlib
+    return importlib.import_module(kimkv.__name__ + ".host")
+
+
+class Buffers:
+    """Per-lane device buffers (key/value per layer, query, output, workspace)."""
+
+    def __init__(self, dev, layers=2, kv=2, qh=2, dim=2, workspace=4096):
+        self.dev = dev
+        self.keys = [dev.DeviceBuffer(kv * dim * 2) for _ in range(layers)]
+        self.values = [dev.DeviceBuffer(kv * dim * 2) for _ in range(layers)]
+        self.query = dev.DeviceBuffer(qh * dim * 2)
+        self.output = dev.DeviceBuffer(qh * dim * 2)
+        self.workspace = dev.DeviceBuffer(workspace)
+        self.workspace_bytes = workspace
+
+
+def reference_output(history, new_token):
+    """Closed-form GQA output for the engine scenario (cuda_engine_kv_backend_test.cpp:96-130)."""
+    tokens = list(history) + [new_token]
+    scale = 1.0 / math.sqrt(2.0)
+    queries = [(0.5, 0.25), (-0.2, 0.4)]
+    out = [0.0] * 4
+    for qh in range(2):
+        scores = [(queries[qh][0] * (0.1 * (t + 1) + 0.02) + queries[qh][1] * (-0.05 * t + 0.01)) * scale
+                  for t in tokens]
+        m = max(scores)
+        den = sum(math.exp(s - m) for s in scores)
+        for t, s in zip(tokens, scores):
+            p = math.exp(s - m) / den
+            out[2 * qh] += p * (t + 1 + 0.2)
+            out[2 * qh + 1] += p * ((t + 1) * 0.5 - 0.1)
+    return out
+
+
+def run_token(host, dev, engine, rid, history, token, buf, stream, fault=None):
+    """One decode token through reserve/write/attend/commit (cuda_engine_kv_backend_test.cpp:132-244)."""
+    rc, txn = engine.reserve_token(rid, len(history), stream)
+    assert rc == 0, host.ENGINE_ERRORS[rc]
+    assert engine.snapshot().active_transaction_count == 1
+    dev.copy_to_device(buf.query.ptr, f16(0.5, 0.25, -0.2, 0.4), stream)
+    if fault == "submission":
+        assert engine.inject_failure_once("submission")
+    for layer in range(2):
+        off = 0.02 if layer == 1 else 0.0
+        dev.copy_to_device(buf.keys[layer].ptr, f16(0.1 * (token + 1) + off, -0.05 * token + off * 0.5), stream)
+        dev.copy_to_device(buf.values[layer].ptr, f16(token + 1 + off * 10.0, (token + 1) * 0.5 - off * 5.0), stream)
+        rc = txn.write_layer(layer, buf.keys[layer].ptr, buf.values[layer].ptr)
+        if fault == "submission" and layer == 0:
+            assert rc == SUBMISSION_FAILED
+            assert txn.rollback() == 0
+            assert engine.check_invariants()
+            return False
+        assert rc == 0, host.ENGINE_ERRORS[rc]
+        rc = txn.attend_layer(layer, buf.query.ptr, buf.output.ptr, buf.workspace.ptr, buf.workspace_bytes,
+                              1.0 / math.sqrt(2.0))
+        assert rc == 0, host.ENGINE_ERRORS[rc]
+    if fault == "completion":
+        assert engine.inject_failure_once("completion")
+        assert txn.commit() == EXECUTION_FAILED
+        assert engine.check_invariants()
+        return False
+    assert txn.commit() == 0
+    out = to_f32(dev.download(buf.output.ptr, (4,), np.uint16))
+    expected = np.array(reference_output(history, token), dtype=np.float32)
+    assert np.all(np.abs(out - expected) < 0.035), (out, expected)
+    history.append(token)
+    assert engine.check_invariants()
+    assert engine.snapshot().active_transaction_count == 0
+    return True
+
+
+def test_engine_backend_tokens_fork_and_faults(host, dev):
+    """testBackend(Heterogeneous), cuda_engine_kv_backend_test.cpp:246-345."""
+    engine = host.Engine(2, 1, 2, 2, 4096, 32, 4)
+    snap = engine.snapshot()
+    assert snap.primary_page_tokens == 8 and snap.secondary_page_tokens == 64
+    assert snap.primary_page_capacity == 32 and snap.secondary_page_capacity == 4
+    assert snap.storage_reserved_bytes != 0
+    assert engine.create_request(1) == 0
+    stream = dev.Stream()
+    buf = Buffers(dev)
+    parent = []
+    for token in range(10):
+        assert run_token(host, dev, engine, 1, parent, token, buf, stream)
+    snap = engine.snapshot()
+    assert snap.committed_token_count == 10
+    assert snap.allocated_primary_pages != 0 and snap.successful_primary_allocations != 0
+
+    assert engine.fork_request(1, 2) == 0
+    child = list(parent)
+    assert run_token(host, dev, engine, 2, child, 21, buf, stream)   # partial-tail COW
+    assert engine.snapshot().committed_token_count == 21
+
+    before = engine.snapshot().committed_token_count
+    assert not run_token(host, dev, engine, 1, parent, 30, buf, stream, fault="submission")
+    assert engine.snapshot().committed_token_count == before
+    assert not run_token(host, dev, engine, 1, parent, 31, buf, stream, fault="completion")
+    assert engine.snapshot().committed_token_count == before
+
+    # The parent still decodes correctly after both faults.
+    assert run_token(host, dev, engine, 1, parent, 12, buf, stream)
+    assert engine.release_request(2) == 0
+    assert engine.release_request(1) == 0
+    snap = engine.snapshot()
+    assert snap.request_count == 0 and snap.committed_token_count == 0
+    assert snap.allocated_primary_pages == 0 and snap.allocated_secondary_pages == 0
+    assert engine.check_invariants()
+    stream.destroy()
+
+
+def test_extent_plus_micro_attention_known_answer(host, dev):
+    """testExtentPagedAttention, cuda_engine_kv_backend_test.cpp:347-500: 64
+    tokens K=(1,1), V=(t/64, -t/128) promoted into one extent, then a token
+    K=(1,1) V=(1,-1) attended with q=(1,1): uniform weights give
+    (0.5, -0.2577)."""
+    engine = host.Engine(1, 1, 2, 1, 65 * 4, 9, 1)
+    assert engine.create_request(50) == 0
+    stream = dev.Stream()
+    buf = Buffers(dev, layers=1, kv=1, qh=1, dim=2, workspace=65 * 4)
+    dev.copy_to_device(buf.query.ptr, f16(1.0, 1.0), stream)
+    for t in range(64):
+        rc, txn = engine.reserve_token(50, t, stream)
+        assert rc == 0
+        dev.copy_to_device(buf.keys[0].ptr, f16(1.0, 1.0), stream)
+        dev.copy_to_device(buf.values[0].ptr, f16(t / 64.0, -t / 128.0), stream)
+        assert txn.write_layer(0, buf.keys[0].ptr, buf.values[0].ptr) == 0
+        assert txn.attend_layer(0, buf.query.ptr, buf.output.ptr, buf.workspace.ptr, buf.workspace_bytes,
+                                1.0 / math.sqrt(2.0)) == 0
+        assert txn.commit() == 0
+    rc, promoted = engine.promote_request(50, stream)
+    assert rc == 0 and promoted == 1
+    version, entries = engine.block_table(50)
+    assert len(entries) == 1 and entries[0][2] == 1   # one extent entry
+
+    rc, txn = engine.reserve_token(50, 64, stream)
+    assert rc == 0
+    dev.copy_to_device(buf.keys[0].ptr, f16(1.0, 1.0), stream)
+    dev.copy_to_device(buf.values[0].ptr, f16(1.0, -1.0), stream)
+    assert txn.write_layer(0, buf.keys[0].ptr, buf.values[0].ptr) == 0
+    assert txn.attend_layer(0, buf.query.ptr, buf.output.ptr, buf.workspace.ptr, buf.workspace_bytes,
+                            1.0 / math.sqrt(2.0)) == 0
+    assert txn.commit() == 0
+    out = to_f32(dev.download(buf.output.ptr, (2,), np.uint16))
+    assert abs(out[0] - 0.5) < 0.01 and abs(out[1] + 0.2577) < 0.01, out
+    _, entries = engine.block_table(50)
+    assert [e[2] for e in entries] == [1, 0]          # extent then micro
+    assert engine.check_invariants()
+    assert engine.release_request(50) == 0
+    stream.destroy()
+
+
+def test_batched_attention_failure_isolation(host, dev):
+    """testBatchedAttentionFailureIsolation(Heterogeneous), cuda_engine_kv_backend_test.cpp:502-610."""
+    engine = host.Engine(1, 1, 2, 2, 4096, 16, 2)
+    assert engine.create_request(70) == 0 and engine.create_request(71) == 0
+    stream = dev.Stream()
+    first, second = Buffers(dev, layers=1, kv=1), Buffers(dev, layers=1, kv=1)
+    rc1, t1 = engine.reserve_token(70, 0, stream)
+    rc2, t2 = engine.reserve_token(71, 0, stream)
+    assert rc1 == 0 and rc2 == 0
+    for b, k, v in ((first, (0.1, 0.2), (1.0, 2.0)), (second, (0.3, 0.4), (3.0, 4.0))):
+        dev.copy_to_device(b.query.ptr, f16(0.5, 0.25, -0.2, 0.4), stream)
+        dev.copy_to_device(b.keys[0].ptr, f16(*k), stream)
+        dev.copy_to_device(b.values[0].ptr, f16(*v), stream)
+    assert t1.write_layer(0, first.keys[0].ptr, first.values[0].ptr) == 0
+    assert t2.write_layer(0, second.keys[0].ptr, second.values[0].ptr) == 0
+    assert engine.inject_failure_once("submission")
+    scale = 1.0 / math.sqrt(2.0)
+    st = host.attend_layer_batch(
+        [t1, t2], [(0, b.query.ptr, b.output.ptr, b.workspace.ptr, 4096, scale) for b in (first, second)])
+    assert st[0] == SUBMISSION_FAILED
+    assert st[1] == 0
+    assert t1.rollback() == 0
+    assert t2.commit() == 0
+    out = to_f32(dev.download(second.output.ptr, (4,), np.uint16))
+    np.testing.assert_allclose(out, [3.0, 4.0, 3.0, 4.0], atol=0.01)
+    snap = engine.snapshot()
+    assert snap.committed_token_count == 1 and snap.active_transaction_count == 0
+    assert snap.batched_attention_submissions == 1 and snap.batched_attention_lanes == 1
+    assert engine.release_request(71) == 0 and engine.release_request(70) == 0
+    assert engine.check_invariants()
+    stream.destroy()
+
+
+def _oracle_lane(history_kv, layer, q_codes, qh, kv, dim, scale):
+    """fp32 GQA over a lane's full history for one layer; history_kv[t] = (K[kv][dim], V[kv][dim]) per layer."""
+    K = np.stack([to_f32(h[layer][0]).reshape(kv, dim) for h in history_kv])   # [T][kv][dim]
+    V = np.stack([to_f32(h[layer][1]).reshape(kv, dim) for h in history_kv])
+    q = to_f32(q_codes).reshape(qh, dim)
+    g = qh // kv
+    out = np.zeros((qh, dim), dtype=np.float64)
+    for h in range(qh):
+        s = K[:, h // g, :].astype(np.float64) @ q[h].astype(np.float64) * scale
+        p = np.exp(s - s.max())
+        out[h] = (p[:, None] * V[:, h // g, :]).sum(0) / p.sum()
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("dim,qh,kv", [(64, 8, 2), (128, 4, 4)])
+def test_batched_write_and_attention_many_lanes(host, dev, dim, qh, kv):
+    """Ragged lanes decoding through writeLayerBatch + attendLayerBatch with
+    engine promotion mid-way; every lane's output is checked against an fp32
+    GQA over its own history (tolerance 2e-3 abs + 1e-3 rel)."""
+    L, lanes, steps = 2, 6, 80
+    rng = np.random.default_rng(dim + qh)
+    start = [int(x) for x in rng.integers(1, 40, lanes)]
+    engine = host.Engine(L, kv, dim, qh, 1 << 20, 512, 16)
+    stream = dev.Stream()
+    scale = 1.0 / math.sqrt(dim)
+    hist = {r: [] for r in range(lanes)}
+    bufs = [Buffers(dev, layers=L, kv=kv, qh=qh, dim=dim, workspace=1 << 20) for _ in range(lanes)]
+    for r in range(lanes):
+        assert engine.create_request(100 + r) == 0
+
+    def token_kv():
+        return [(f16(*rng.uniform(-1, 1, kv * dim)), f16(*rng.uniform(-1, 1, kv * dim))) for _ in range(L)]
+
+    # Prefill each lane token by token through single transactions.
+    for r in range(lanes):
+        for t in range(start[r]):
+            rc, txn = engine.reserve_token(100 + r, t, stream)
+            assert rc == 0
+            kvs = token_kv()
+            q = f16(*rng.uniform(-1, 1, qh * dim))
+            dev.copy_to_device(bufs[r].query.ptr, q, stream)
+            for layer in range(L):
+                dev.copy_to_device(bufs[r].keys[layer].ptr, kvs[layer][0], stream)
+                dev.copy_to_device(bufs[r].values[layer].ptr, kvs[layer][1], stream)
+                assert txn.write_layer(layer, bufs[r].keys[layer].ptr, bufs[r].values[layer].ptr) == 0
+                assert txn.attend_layer(layer, bufs[r].query.ptr, bufs[r].output.ptr, bufs[r].workspace.ptr,
+                                        bufs[r].workspace_bytes, scale) == 0
+            assert txn.commit() == 0
+            hist[r].append(kvs)
+    worst = 0.0
+    for step in range(steps):
+        if step == steps // 2:
+            for r in range(lanes):
+                rc, _ = engine.promote_request(100 + r, stream)
+                assert rc == 0
+        txns = []
+        for r in range(lanes):
+            rc, txn = engine.reserve_token(100 + r, len(hist[r]), stream)
+            assert rc == 0
+            txns.append(txn)
+        kvs = [token_kv() for _ in range(lanes)]
+        qs = [f16(*rng.uniform(-1, 1, qh * dim)) for _ in range(lanes)]
+        for r in range(lanes):
+            dev.copy_to_device(bufs[r].query.ptr, qs[r], stream)
+            for layer in range(L):
+                dev.copy_to_device(bufs[r].keys[layer].ptr, kvs[r][layer][0], stream)
+                dev.copy_to_device(bufs[r].values[layer].ptr, kvs[r][layer][1], stream)
+        for layer in range(L):
+            st = host.write_layer_batch(txns, [layer] * lanes, [b.keys[layer].ptr for b in bufs],
+                                        [b.values[layer].ptr for b in bufs])
+            assert st == [0] * lanes
+            st = host.attend_layer_batch(
+                txns, [(layer, b.query.ptr, b.output.ptr, b.workspace.ptr, b.workspace_bytes, scale) for b in bufs])
+            assert st == [0] * lanes
+            dev.sync(stream)
+            for r in range(lanes):
+                got = to_f32(dev.download(bufs[r].output.ptr, (qh * dim,), np.uint16))
+                want = _oracle_lane(hist[r] + [kvs[r]], layer, qs[r], qh, kv, dim, scale)
+                err = np.abs(got - want)
+                assert np.all(err <= 2e-3 + 1e-3 * np.abs(want)), (step, r, layer, err.max())
+                worst = max(worst, float(err.max()))
+        for r, txn in enumerate(txns):
+            assert txn.commit() == 0
+            hist[r].append(kvs[r])
+    snap = engine.snapshot()
+    assert snap.committed_token_count == sum(len(h) for h in hist.values())
+    assert snap.batched_write_submissions >= steps * L
+    assert snap.allocated_secondary_pages > 0   # promotion published extents
+    assert engine.check_invariants()
+    for r in range(lanes):
+        assert engine.release_request(100 + r) == 0
+    stream.destroy()
+
+
+# --- HipKvCache (tests/cuda/cuda_kv_test.cpp) ------------------------------------------------------------
+
+LAYOUT = (2, 2, 8)
+
+
+def _append(dev, cache, rid, begin, count, stream):
+    data = make_kv_closed_form(*LAYOUT, begin, count)
+    buf = dev.upload(data.reshape(-1), stream)
+    res = cache.append(rid, count, buf.ptr, stream)
+    assert res.ok(), (res.metadata_error, res.device_status)
+    return buf
+
+
+def _gather(dev, cache, rid, count, stream):
+    L, H, D = LAYOUT
+    out = dev.DeviceBuffer(L * 2 * count * H * D * 2)
+    res = cache.gather(rid, out.ptr, stream)
+    assert res.ok(), (res.metadata_error, res.device_status)
+    return dev.download(out.ptr, (L * 2 * count * H * D,), np.uint16)
+
+
+def test_cache_append_gather_promotion_attention(host, dev):
+    """testAppendGatherPromotionAndAttention, cuda_kv_test.cpp:287-351."""
+    L, H, D = LAYOUT
+    cache = host.Cache(L, H, D, 16, 2)
+    assert cache.status() == 0
+    info = cache.storage_info()
+    token_bytes = L * 2 * H * D * 2
+    assert info.micro_reserved_bytes == 16 * 8 * token_bytes
+    assert info.extent_reserved_bytes == 2 * 64 * token_bytes
+    stream = dev.Stream()
+    assert cache.create_request(1) == 0
+    keep = [_append(dev, cache, 1, b, n, stream) for b, n in ((0, 5), (5, 11), (16, 48))]
+    expected = make_kv_closed_form(L, H, D, 0, 64).reshape(-1)
+    assert np.array_equal(_gather(dev, cache, 1, 64, stream), expected)
+    res = cache.promote(1, 0, stream)
+    assert res.ok()
+    _, entries = cache.block_table(1)
+    assert len(entries) == 1 and entries[0][2] == 1
+    assert np.array_equal(_gather(dev, cache, 1, 64, stream), expected)
+
+    query = ((np.arange(L * H * D) % 11) + 1).astype(np.float32) * 0.03125
+    ref = oracle.reference_attention(L, H, D, expected, 64, query)
+    q = dev.upload(query, stream)
+    o = dev.DeviceBuffer(query.nbytes)
+    assert cache.reference_attention(1, q.ptr, o.ptr, stream).ok()
+    got = dev.download(o.ptr, query.shape, np.float32)
+    assert np.max(np.abs(got - ref)) <= 5e-4
+    assert cache.check_invariants()
+    assert cache.release_request(1) == 0
+    assert cache.check_invariants()
+    del keep
+    stream.destroy()
+
+
+def test_cache_partial_tail_cow(host, dev):
+    """testPartialTailCow, cuda_kv_test.cpp:353-391."""
+    cache = host.Cache(*LAYOUT, 4, 1)
+    stream = dev.Stream()
+    assert cache.create_request(10) == 0
+    a = _append(dev, cache, 10, 0, 5, stream)
+    assert cache.fork_request(10, 11) == 0
+    b = _append(dev, cache, 11, 5, 3, stream)
+    assert np.array_equal(_gather(dev, cache, 10, 5, stream), make_kv_closed_form(*LAYOUT, 0, 5).reshape(-1))
+    assert np.array_equal(_gather(dev, cache, 11, 8, stream), make_kv_closed_form(*LAYOUT, 0, 8).reshape(-1))
+    assert cache.check_invariants()
+    assert cache.release_request(11) == 0 and cache.release_request(10) == 0
+    del a, b
+    stream.destroy()
+
+
+def test_cache_fault_rollback(host, dev):
+    """testFaultRollback, cuda_kv_test.cpp:393-454."""
+    cache = host.Cache(*LAYOUT, 16, 1)
+    stream = dev.Stream()
+    assert cache.create_request(20) == 0
+    a = _append(dev, cache, 20, 0, 64, stream)
+    cache.inject_failure_once("submission")
+    res = cache.promote(20, 0, stream)
+    assert res.device_status == DEV_SUBMISSION_FAILED
+    _, entries = cache.block_table(20)
+    assert len(entries) == 8
+    snap = cache.snapshot()
+    assert snap.promotion_count == 0 and snap.extent_pool.allocated_slots == 0
+
+    cache.inject_failure_once("completion")
+    res = cache.promote(20, 0, stream)
+    assert res.device_status == DEV_EXECUTION_FAILED
+    _, entries = cache.block_table(20)
+    assert len(entries) == 8
+    assert cache.snapshot().extent_pool.allocated_slots == 0
+    assert cache.check_invariants()
+
+    assert cache.create_request(21) == 0
+    one = dev.upload(make_kv_closed_form(*LAYOUT, 0, 1).reshape(-1), stream)
+    cache.inject_failure_once("submission")
+    res = cache.append(21, 1, one.ptr, stream)
+    assert res.device_status == DEV_SUBMISSION_FAILED
+    assert cache.block_table(21) is None
+    assert cache.check_invariants()
+    # The surviving request's data is intact and still promotable.
+    assert cache.promote(20, 0, stream).ok()
+    assert np.array_equal(_gather(dev, cache, 20, 64, stream), make_kv_closed_form(*LAYOUT, 0, 64).reshape(-1))
+    assert cache.release_request(20) == 0
+    del a
+    stream.destroy()
