@@ -4,10 +4,13 @@ Workload (the HBM-scale decode configuration): 256 lanes, each with a
 32768-token TinyLlama-shaped context (22 layers, 4 KV heads x 64 dims fp16,
 32 query heads) held in 64-token extent pages whose slot ids are a seeded
 permutation of the pool (~189 GB of KV), plus trailing 8-token micro pages
-for the appended tokens.  One step = for every layer: append one new K/V token
-per lane (one batched kernel) then fused split-K GQA decode attention for all
-lanes (one kernel + merge), i.e. 22 x (append + decode) launches, with the
-per-step page-table update and upload included.
+for the appended tokens.  One step = reserve one token per lane, then for
+every layer: append the new K/V of every lane (one batched kernel) and fused
+split-K GQA decode attention for all lanes (one kernel + merge), then commit.
+With --path engine (default) the step goes through the engine API
+(reserveToken / writeLayerBatch / attendLayerBatch / commit, contexts built by
+bulk prefill + promotion); with --path kernel the bench builds the page tables
+itself and calls the C-ABI kernels directly.
 
 Prints one JSON line (see the contract in the repository's docs).
 """
@@ -54,7 +57,8 @@ def permutation(seed: int, n: int) -> np.ndarray:
 
 
 class Workload:
-    def __init__(self, dev, lanes, context, layers, kv_heads, head_dim, query_heads, total_steps, seed):
+    def __init__(self, dev, lanes, context, layers, kv_heads, head_dim, query_heads, total_steps, seed,
+                 permute=True):
         self.dev = dev
         self.lanes, self.context, self.L = lanes, context, layers
         self.H, self.D, self.QH = kv_heads, head_dim, query_heads
@@ -71,8 +75,12 @@ class Workload:
         info = self.storage.info()
         log(f"pools: extent {info.extent_reserved_bytes / 1e9:.1f} GB, micro {info.micro_reserved_bytes / 1e9:.2f} GB "
             f"({time.time() - t0:.1f}s)")
-        ext_perm = permutation(seed, n_ext)
-        micro_perm = permutation(seed + 1, n_micro)
+        if permute:
+            ext_perm = permutation(seed, n_ext)
+            micro_perm = permutation(seed + 1, n_micro)
+        else:
+            ext_perm = np.arange(n_ext, dtype=np.uint32)
+            micro_perm = np.arange(n_micro, dtype=np.uint32)
         # Descriptor arena: lanes x max_entries, tables begin at each lane's row.
         self.desc = np.zeros((lanes, self.max_entries), dtype=dev.BLOCK_DESC)
         for i in range(lanes):
@@ -194,6 +202,146 @@ class Workload:
         self.prepare_step(step)
         self.upload_step(stream)
         self.launch_step(stream)
+
+
+class EngineWorkload:
+    """The same workload driven through the engine API (createHeterogeneous
+    backend, per step: reserveToken for every lane, then per layer one
+    writeLayerBatch and one attendLayerBatch over all lanes, then commit).
+    Contexts are built with the bulk prefill append + promotion, so every
+    page id comes from the manager's (permuted) pools."""
+
+    def __init__(self, kimkv, dev, lanes, context, layers, kv_heads, head_dim, query_heads, total_steps, seed,
+                 groups=2):
+        import importlib
+        host = importlib.import_module(kimkv.__name__ + ".host")
+        self.dev, self.host = dev, host
+        self.lanes, self.context, self.L = lanes, context, layers
+        self.H, self.D, self.QH = kv_heads, head_dim, query_heads
+        self.total_steps = total_steps
+        self.seed = seed
+        assert context % 64 == 0
+        self.ext_per_lane = context // 64
+        HD = kv_heads * head_dim
+        n_ext = lanes * self.ext_per_lane
+        n_micro = 512 // 8 + 8 + lanes * ((total_steps + 7) // 8 + 1)
+        T_max = context + total_steps
+        self.ws_lane = max(dev.workspace_bytes(T_max, 256, query_heads, head_dim), 256)
+        t0 = time.time()
+        self.engine = host.Engine(layers, kv_heads, head_dim, query_heads, self.ws_lane, n_micro, n_ext)
+        snap = self.engine.snapshot()
+        log(f"engine pools: {snap.storage_reserved_bytes / 1e9:.1f} GB ({time.time() - t0:.1f}s)")
+        t0 = time.time()
+        for kind, sd in ((1, seed), (0, seed + 1)):
+            rc = self.engine.permute_free_slots(kind, sd)
+            if rc != 0:
+                raise RuntimeError(f"permute_free_slots({kind}) failed: {host.ENGINE_ERRORS[rc]}")
+        log(f"permuted free lists ({time.time() - t0:.1f}s)")
+        # Prefill in 512-token chunks: synthetic [L][2][512][H][D] (stream id = lane),
+        # bulk append, then promotion of the chunk's eight 64-token runs.
+        chunk = 512
+        stage = dev.DeviceBuffer(layers * 2 * chunk * HD * 2)
+        stream = dev.Stream()
+        t0 = time.time()
+        for i in range(lanes):
+            rc = self.engine.create_request(i + 1)
+            assert rc == 0, host.ENGINE_ERRORS[rc]
+            for t in range(0, context, chunk):
+                dev.fill_kv(stage.ptr, layers, chunk, HD, seed, i, t, stream)
+                rc, promoted = self.engine.append_prefill(i + 1, chunk, stage.ptr, stream, promote=True)
+                if rc != 0 or promoted != chunk // 64:
+                    raise RuntimeError(f"prefill lane {i} at {t}: {host.ENGINE_ERRORS[rc]}, promoted {promoted}")
+            if (i + 1) % 64 == 0:
+                log(f"  prefilled {i + 1}/{lanes} lanes ({time.time() - t0:.1f}s)")
+        stream.synchronize()
+        del stage
+        log(f"prefilled {lanes} x {context} tokens in {time.time() - t0:.1f}s")
+        # New K/V per (lane, layer, comp, step) and queries per (lane, layer, step), as in the kernel path.
+        S = total_steps
+        self.newkv = dev.DeviceBuffer(lanes * layers * 2 * S * HD * 2)
+        self.query = dev.DeviceBuffer(lanes * layers * S * query_heads * head_dim * 2)
+        self.qseed = seed ^ 0x5155455259
+        for i in range(lanes):
+            for l in range(layers):
+                for c in range(2):
+                    off = (((i * layers + l) * 2 + c) * S) * HD
+                    dev.fill_rows(self.newkv.ptr + 2 * off, S * HD, seed, dev.synth_kv_row(i, l, c, context), HD)
+                qoff = ((i * layers + l) * S) * query_heads * head_dim
+                dev.fill_rows(self.query.ptr + 2 * qoff, S * query_heads * head_dim, self.qseed,
+                              dev.synth_kv_row(i, l, 0, context), query_heads * head_dim)
+        dev.sync()
+        QD = query_heads * head_dim
+        self.out = dev.DeviceBuffer(layers * lanes * QD * 2)
+        self.ws = dev.DeviceBuffer(self.ws_lane * lanes)
+        lane = np.arange(lanes, dtype=np.uint64)
+        lay = np.arange(layers, dtype=np.uint64)[:, None]
+        kbase = self.newkv.ptr + np.uint64(2 * HD) * ((lane[None, :] * np.uint64(layers) + lay) * np.uint64(2 * S))
+        qbase = self.query.ptr + np.uint64(2 * QD) * ((lane[None, :] * np.uint64(layers) + lay) * np.uint64(S))
+        obase = self.out.ptr + np.uint64(2 * QD) * (lay * np.uint64(lanes) + lane[None, :])
+        # Lane groups: each group is one batch of token transactions; with two
+        # groups the host reserves/launches one while the GPU runs the other.
+        self.groups = []
+        bounds = np.linspace(0, lanes, groups + 1).astype(int)
+        for g in range(groups):
+            sl = slice(bounds[g], bounds[g + 1])
+            b = host.LaneBatch(self.engine, lane[sl] + np.uint64(1), self.ws.ptr + lane[sl] * np.uint64(self.ws_lane),
+                               self.ws_lane, 1.0 / math.sqrt(head_dim), stream)
+            b.outputs[:] = obase[:, sl]
+            self.groups.append((b, kbase[:, sl], kbase[:, sl] + np.uint64(2 * HD * S), qbase[:, sl]))
+        self.stream = stream
+        self.reserve_s = 0.0
+        self.commit_s = 0.0
+        self.plan = (0, 0)
+        self.pending = None
+
+    def lane_tokens(self, step):
+        return self.context + step + 1
+
+    @staticmethod
+    def _check(b, what):
+        if b.failed():
+            raise RuntimeError(f"{what}: {sorted(set(b.status.tolist()))}")
+
+    def _launch(self, group, step):
+        b, kb, vb, qb = group
+        HD, QD = self.H * self.D, self.QH * self.D
+        b.keys[:] = kb + np.uint64(2 * HD * step)
+        b.values[:] = vb + np.uint64(2 * HD * step)
+        b.queries[:] = qb + np.uint64(2 * QD * step)
+        t0 = time.perf_counter()
+        b.reserve(self.context + step)
+        self.reserve_s += time.perf_counter() - t0
+        self._check(b, "reserve")
+        for l in range(self.L):
+            b.write(l)
+            self._check(b, f"writeLayerBatch layer {l}")
+            b.attend(l)
+            self._check(b, f"attendLayerBatch layer {l}")
+
+    def _commit(self, group):
+        b = group[0]
+        t0 = time.perf_counter()
+        b.commit()
+        self.commit_s += time.perf_counter() - t0
+        self._check(b, "commit")
+
+    def step(self, step, stream=None):
+        """One token for every lane.  A group is committed only after the next
+        group's layers are queued, so the GPU has work while the host commits
+        one group and reserves the next."""
+        for g in self.groups:
+            if self.pending is g:          # a single group commits before its next token
+                self._commit(g)
+                self.pending = None
+            self._launch(g, step)
+            if self.pending is not None:
+                self._commit(self.pending)
+            self.pending = g
+
+    def drain(self):
+        if self.pending is not None:
+            self._commit(self.pending)
+            self.pending = None
 
 
 def cpu_baseline(kimkv, w: Workload, lanes_sample: int, step: int):
@@ -350,6 +498,13 @@ def main() -> int:
     ap.add_argument("--config", choices=["decode", "gather", "copy"], default="decode",
                     help="decode: HBM-scale decode+append (the headline line); gather: long-sequence gather; "
                          "copy: plain device copy (bandwidth and counter calibration)")
+    ap.add_argument("--path", choices=["engine", "kernel"], default="engine",
+                    help="engine: EngineKvBackend token transactions (reserve / writeLayerBatch / attendLayerBatch / "
+                         "commit); kernel: the C-ABI kernels driven directly with bench-built page tables")
+    ap.add_argument("--groups", type=int, default=2,
+                    help="engine path: lane groups pipelined against each other (1 = one batch per step)")
+    ap.add_argument("--slots", choices=["permuted", "sequential"], default="permuted",
+                    help="kernel path: page slots in seeded-permutation order (default) or in pool order")
     ap.add_argument("--copy-mib", type=int, default=4096)
     ap.add_argument("--gather-tokens", type=int, default=16384)
     ap.add_argument("--gpus", type=int, default=1)
@@ -378,13 +533,26 @@ def main() -> int:
         return run_copy(dev, args)
     H, D, QH = 4, 64, 32
     total_steps = args.warmup + args.steps
-    w = Workload(dev, args.lanes, args.context, args.layers, H, D, QH, total_steps, args.seed)
-    stream = dev.Stream()
+    if args.path == "engine":
+        w = EngineWorkload(kimkv, dev, args.lanes, args.context, args.layers, H, D, QH, total_steps, args.seed,
+                           args.groups)
+        stream = w.stream
+    else:
+        w = Workload(dev, args.lanes, args.context, args.layers, H, D, QH, total_steps, args.seed,
+                     permute=args.slots == "permuted")
+        stream = dev.Stream()
 
     for s in range(args.warmup):
         w.step(s, stream)
+    if args.path == "engine":
+        w.drain()
     stream.synchronize()
-    log(f"warmup done; plan chunk={w.plan[0]} chunks={w.plan[1]}")
+    log("warmup done")
+    if args.path == "engine":
+        w.reserve_s = w.commit_s = 0.0
+        group_lanes = w.groups[0][0].n
+        chunk, _, total = dev.decode_plan(w.engine.storage_handle(), [w.lane_tokens(args.warmup)] * group_lanes, QH)
+        w.plan = (chunk, total)
 
     start, stop = dev.Event(), dev.Event()
     dev.decode_timing(True)
@@ -393,6 +561,8 @@ def main() -> int:
     start.record(stream)
     for s in range(args.warmup, total_steps):
         w.step(s, stream)
+    if args.path == "engine":
+        w.drain()
     stop.record(stream)
     stop.synchronize()
     wall_ms = (time.perf_counter() - t_wall) * 1000.0
@@ -411,7 +581,8 @@ def main() -> int:
         append_bytes += args.layers * args.lanes * 2 * tok_bytes     # read new K/V + write page
     step_bytes = (decode_bytes + append_bytes) / args.steps
     value_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
-    per_launch_decode_bytes = decode_bytes / (args.steps * args.layers)
+    # One decode launch per layer per lane group: bytes and time per launch.
+    per_launch_decode_bytes = decode_bytes / max(decode_launches, 1)
     decode_avg_ms = decode_ms_total / max(decode_launches, 1)
     achieved = per_launch_decode_bytes / (decode_avg_ms * 1e-3) / 1e9
 
@@ -453,9 +624,13 @@ def main() -> int:
         "data": "synthetic (seeded Irwin-Hall fp16 K/V/Q generated on device)",
         "config": {"workload": f"HBM-scale decode: {args.lanes} lanes x {args.context}-token contexts "
                                f"(+{total_steps} appended), {args.layers} layers TinyLlama GQA 32q/4kv/64d fp16, "
-                               f"extent pages in permuted slots",
+                               f"extent pages in permuted slots, "
+                               + ("through the engine token transactions" if args.path == "engine"
+                                  else "kernels driven directly"),
+                   "path": args.path,
                    "lanes": args.lanes, "context": args.context, "layers": args.layers,
-                   "decode_chunk_tokens": w.plan[0], "decode_chunks": w.plan[1]},
+                   "decode_chunk_tokens": w.plan[0], "decode_chunks_per_launch": w.plan[1],
+                   "lane_groups": args.groups if args.path == "engine" else 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": profiled_traffic(args.lanes, args.context, args.layers),
@@ -464,6 +639,9 @@ def main() -> int:
         "cpu_baseline": cpu,
         "check": check,
         "timing": {"gpu_event_ms": round(gpu_ms, 3), "wall_ms": round(wall_ms, 3)},
+        "host": ({"path": "engine", "reserve_ms_per_step": round(w.reserve_s * 1000 / args.steps, 3),
+                  "commit_ms_per_step": round(w.commit_s * 1000 / args.steps, 3)}
+                 if args.path == "engine" else {"path": "kernel"}),
     }
     print(json.dumps(result), flush=True)
     return 0

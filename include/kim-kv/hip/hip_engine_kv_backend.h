@@ -29,6 +29,29 @@ namespace kimkvcache {
 [[nodiscard]] EngineKvStatus promoteRequest(EngineKvBackend& backend, RequestId request_id, HipStream stream,
                                             std::uint32_t* promoted_pages);
 
+// Bulk append of prompt KV, layout [layer][K/V][token_count][head][dim] in
+// device memory, to a request with no token in flight (no reference
+// counterpart: the reference engine appends one token per transaction).
+// Waits for the copy; seals a full tail; with promote_runs, promotes every
+// complete run of 8 micro pages as promoteRequest does.  A device failure
+// cancels the request.
+[[nodiscard]] EngineKvStatus appendPrefill(EngineKvBackend& backend, RequestId request_id,
+                                           std::uint32_t token_count, KvScalar const* device_kv, HipStream stream,
+                                           bool promote_runs, std::uint32_t* promoted_pages);
+
+// reserveToken for `count` requests on one stream (no reference counterpart:
+// the reference reserves lane by lane, with a device allocation and upload
+// each).  Results match calling reserveToken in order, except that all
+// descriptor tables share one device arena filled by a single upload.  A
+// request naming a different stream than requests[0] gets InvalidArgument.
+// Returns false when `backend` is not a HIP backend.
+[[nodiscard]] bool reserveTokenBatch(EngineKvBackend& backend, ReserveTokenRequest const* requests,
+                                     std::size_t count, TokenReserveResult* results);
+
+// Seeded permutation of a pool's free list while no request exists (see
+// kim-kv/runtime/pool_permutation.h).
+[[nodiscard]] EngineKvStatus permuteEngineFreeSlots(EngineKvBackend& backend, PageKind kind, std::uint64_t seed);
+
 // Committed block table of a request (diagnostics and tests).
 [[nodiscard]] bool engineBlockTable(EngineKvBackend const& backend, RequestId request_id, BlockTable& out);
 

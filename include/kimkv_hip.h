@@ -252,6 +252,12 @@ uint64_t kimkv_synth_kv_row(uint32_t stream, uint32_t layer, uint32_t component,
 kimkv_status kimkv_fill_rows(uint16_t* device_out, uint64_t count, uint64_t seed,
                              uint64_t row0, uint32_t cols, kimkv_stream_t stream);
 
+/* Fills a contiguous K/V block [layers][2][tokens][cols] (the layout of a
+ * bulk append input): element (l, c, t, col) = synth(seed,
+ * synth_kv_row(stream_id, l, c, token0 + t), col). */
+kimkv_status kimkv_fill_kv(uint16_t* device_out, uint32_t layers, uint32_t tokens, uint32_t cols, uint64_t seed,
+                           uint32_t stream_id, uint32_t token0, kimkv_stream_t stream);
+
 /* Writes synthetic K/V for logical tokens [token_begin, token_end) of a table
  * straight into its pages: value(layer, comp, token, head, dim) =
  * synth(seed, kv_row(stream_id, layer, comp, token), head*D + dim).  Used to

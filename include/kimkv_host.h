@@ -186,6 +186,20 @@ int kimkv_engine_block_table(const kimkv_engine* e, uint64_t request_id, uint64_
                              kimkv_mapping_entry* entries, uint32_t capacity, uint32_t* count);
 /* The engine's device storage (for data-path helpers such as kimkv_gather). */
 const kimkv_storage* kimkv_engine_storage(const kimkv_engine* e);
+/* Bulk prompt append (no reference counterpart: the reference engine appends
+ * one token per transaction).  device_kv is [layer][K/V][token_count][head][dim]
+ * fp16; waits for the copy, seals a full tail and, when promote != 0,
+ * promotes every complete 64-token run (count in *promoted).  A device
+ * failure cancels the request. */
+int kimkv_engine_append_prefill(kimkv_engine* e, uint64_t request_id, uint32_t token_count,
+                                const uint16_t* device_kv, kimkv_stream_t stream, int promote, uint32_t* promoted);
+/* Seeded permutation of a pool's free list (kind 0 micro, 1 extent) while the
+ * engine has no request: page ids then come out scattered over the pool. */
+int kimkv_engine_permute_free_slots(kimkv_engine* e, uint32_t kind, uint64_t seed);
+/* reserveToken for `count` requests on one stream: txns[i] / statuses[i] as
+ * kimkv_engine_reserve_token would return them one by one. */
+void kimkv_engine_reserve_batch(kimkv_engine* e, const uint64_t* request_ids, const uint32_t* expected_committed,
+                                uint32_t count, kimkv_stream_t stream, kimkv_txn** txns, int* statuses);
 
 /* TokenTransaction (engine_kv.h:298-351). */
 int kimkv_txn_write_layer(kimkv_txn* t, uint32_t layer, const uint16_t* key, const uint16_t* value);
@@ -195,10 +209,17 @@ int kimkv_txn_rollback(kimkv_txn* t);
 /* Fills phase (TokenTransactionPhase), next layer and logical position. */
 void kimkv_txn_state(const kimkv_txn* t, uint32_t* phase, uint32_t* next_layer, uint32_t* position);
 void kimkv_txn_destroy(kimkv_txn* t);   /* rolls back when not committed */
+/* commit of `count` transactions; each is destroyed afterwards and txns[i]
+ * set to NULL (a failed commit has rolled back). */
+void kimkv_txn_commit_batch(kimkv_txn** txns, uint32_t count, int* statuses);
 
-/* attendLayerBatch (engine_kv.h:355): statuses[i] receives each lane's EngineKvError. */
+/* attendLayerBatch (engine_kv.h:355): statuses[i] receives each lane's
+ * EngineKvError.  device_items / device_capacity are PagedDecodeBatch's
+ * caller-owned device scratch (capacity >= count is required, as in the
+ * reference); the HIP backend stages the items together with the chunk
+ * prefix through its own ring, so the scratch is never written. */
 void kimkv_attend_layer_batch(kimkv_txn** txns, const kimkv_decode_request* requests, uint32_t count,
-                              int* statuses);
+                              void* device_items, uint32_t device_capacity, int* statuses);
 /* writeLayerBatch: batched form of TokenTransaction::writeLayer (one kernel for all lanes). */
 void kimkv_write_layer_batch(kimkv_txn** txns, const uint32_t* layers, const uint16_t* const* keys,
                              const uint16_t* const* values, uint32_t count, int* statuses);

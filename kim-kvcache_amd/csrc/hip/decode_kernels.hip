@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "device_common.h"
 #include "runtime_internal.h"
@@ -61,6 +62,21 @@ __device__ inline half8_t load_half8(const uint16_t* p)
     return *reinterpret_cast<const half8_t*>(p);
 }
 
+// K/V page rows are read once per launch: non-temporal loads stream them
+// without displacing reusable lines (measured on MI355X: a plain 16-byte
+// streaming read reaches ~6.2 TB/s, the non-temporal form ~6.9 TB/s).
+//
+// The page pointers come out of the LDS group table as generic pointers; the
+// address-space cast makes these global (not flat) loads, which count only
+// against vmcnt, so waiting for a later LDS read does not also wait for the
+// K/V bytes in flight.
+typedef const __attribute__((address_space(1))) half8_t global_half8_t;
+
+__device__ inline half8_t load_half8_stream(const uint16_t* p)
+{
+    return __builtin_nontemporal_load((global_half8_t*)(p));
+}
+
 // ---------------------------------------------------------------------------
 // Fast path for one wave: kv head h, head_dim 64, group <= 16.
 // ---------------------------------------------------------------------------
@@ -89,51 +105,71 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
     float4_t acc[4] = {};
     half8_t const zero8 = {};
 
-    for (uint32_t t0 = c0; t0 < c1; t0 += 64) {
+    // One 64-token step is a load phase (K rows and V^T rows of the step into
+    // registers) and a compute phase; the next step's loads are issued before
+    // the current step's compute (two register buffers), so each wave keeps
+    // up to two steps of K/V in flight and the compute hides under them.  The
+    // tail variants mask tokens past the chunk end; full steps skip every
+    // per-token compare.
+    struct Ops {
+        half8_t k[2][2][2];
+        half8_t v[2][4];
+    };
+    auto load = [&](Ops& o, uint32_t t0, auto tail) {
+        constexpr bool kTail = decltype(tail)::value;
         uint32_t const tg = (t0 - c0) >> 3;
         uint32_t const nvalid = c1 - t0;
-
-        // ---- loads: K rows (QK A operand) and V^T rows (PV A operand) ----
-        half8_t kop[2][2][2];
-        half8_t vop[2][4];
 #pragma unroll
         for (uint32_t kb = 0; kb < 2; ++kb) {
             GroupEntry const gk = groups[tg + 4 * kb + x];
 #pragma unroll
             for (uint32_t e = 0; e < 2; ++e) {
                 uint32_t const tt = 32 * kb + 8 * x + 4 * e + (l & 3u);
-                if (tt < nvalid && gk.base != nullptr) {
+                if ((!kTail || tt < nvalid) && gk.base != nullptr) {
+                    // K column blocks of 32 dims: dims [8a, 8a+8) and [32+8a, 40+8a).
                     const uint16_t* row = gk.base + gk.cap * head_unit
-                        + static_cast<uint64_t>(gk.pt0 + 4 * e + (l & 3u)) * D;
-                    kop[kb][e][0] = load_half8(row + a * 8);
-                    kop[kb][e][1] = load_half8(row + 32 + a * 8);
+                        + static_cast<uint64_t>(gk.pt0 + 4 * e + (l & 3u)) * 32 + a * 8;
+                    o.k[kb][e][0] = load_half8_stream(row);
+                    o.k[kb][e][1] = load_half8_stream(row + static_cast<uint64_t>(gk.cap) * 32);
                 } else {
-                    kop[kb][e][0] = zero8;
-                    kop[kb][e][1] = zero8;
+                    o.k[kb][e][0] = zero8;
+                    o.k[kb][e][1] = zero8;
                 }
             }
             GroupEntry const gv = groups[tg + 4 * kb + a];
             uint32_t const vt0 = 32 * kb + 8 * a;
-            if (vt0 < nvalid && gv.base != nullptr) {
-                const uint16_t* vt = gv.base + gv.cap * head_unit + static_cast<uint64_t>(gv.cap) * D + gv.pt0;
+            if ((!kTail || vt0 < nvalid) && gv.base != nullptr) {
+                // V^T column block of vw tokens holding this 8-token group; row d = 16 db + r.
+                uint32_t const vw = v_width(gv.cap);
+                const uint16_t* vt = gv.base + gv.cap * head_unit + v_offset(gv.cap, D, gv.pt0, r);
 #pragma unroll
                 for (uint32_t db = 0; db < 4; ++db) {
-                    vop[kb][db] = load_half8(vt + static_cast<uint64_t>(db * 16 + r) * gv.cap);
+                    o.v[kb][db] = load_half8_stream(vt + static_cast<uint64_t>(db * 16) * vw);
                 }
-                if (vt0 + 8 > nvalid) {
-                    // Tokens past the chunk end may hold stale data: zero them.
+            } else {
+#pragma unroll
+                for (uint32_t db = 0; db < 4; ++db) o.v[kb][db] = zero8;
+            }
+        }
+    };
+    auto compute = [&](Ops& o, uint32_t t0, auto tail) {
+        constexpr bool kTail = decltype(tail)::value;
+        uint32_t const nvalid = c1 - t0;
+        if (kTail) {
+            // Tokens past the chunk end may hold stale data: zero their V.
+#pragma unroll
+            for (uint32_t kb = 0; kb < 2; ++kb) {
+                uint32_t const vt0 = 32 * kb + 8 * a;
+                if (vt0 < nvalid && vt0 + 8 > nvalid) {
                     uint32_t const keep = nvalid - vt0;
 #pragma unroll
                     for (uint32_t db = 0; db < 4; ++db) {
 #pragma unroll
                         for (uint32_t j = 0; j < 8; ++j) {
-                            if (j >= keep) vop[kb][db][j] = static_cast<_Float16>(0.0f);
+                            if (j >= keep) o.v[kb][db][j] = static_cast<_Float16>(0.0f);
                         }
                     }
                 }
-            } else {
-#pragma unroll
-                for (uint32_t db = 0; db < 4; ++db) vop[kb][db] = zero8;
             }
         }
 
@@ -144,8 +180,8 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
 #pragma unroll
             for (uint32_t e = 0; e < 2; ++e) {
                 float4_t z = {};
-                z = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][0], qb0, z, 0, 0, 0);
-                s[kb][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][1], qb1, z, 0, 0, 0);
+                z = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.k[kb][e][0], qb0, z, 0, 0, 0);
+                s[kb][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.k[kb][e][1], qb1, z, 0, 0, 0);
             }
         }
         float mx = -INFINITY;
@@ -156,7 +192,7 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i) {
                     uint32_t const tt = 32 * kb + 8 * a + 4 * e + i;
-                    float const v = tt < nvalid ? s[kb][e][i] * scale2 : -INFINITY;
+                    float const v = !kTail || tt < nvalid ? s[kb][e][i] * scale2 : -INFINITY;
                     s[kb][e][i] = v;
                     mx = fmaxf(mx, v);
                 }
@@ -165,7 +201,7 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         float const m_new = fmaxf(m_run, mx);
-        float const alpha = exp2f(m_run - m_new);
+        float const alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         m_run = m_new;
 
         half8_t pb[2];
@@ -176,7 +212,7 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
             for (uint32_t e = 0; e < 2; ++e) {
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i) {
-                    float const p = exp2f(s[kb][e][i] - m_new);
+                    float const p = __builtin_amdgcn_exp2f(s[kb][e][i] - m_new);
                     psum += p;
                     pb[kb][4 * e + i] = static_cast<_Float16>(p);
                 }
@@ -191,9 +227,38 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
         for (uint32_t kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (uint32_t db = 0; db < 4; ++db) {
-                acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[kb][db], pb[kb], acc[db], 0, 0, 0);
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.v[kb][db], pb[kb], acc[db], 0, 0, 0);
             }
         }
+    };
+    auto load_step = [&](Ops& o, uint32_t t0) {
+        if (c1 - t0 >= 64) {
+            load(o, t0, std::false_type{});
+        } else {
+            load(o, t0, std::true_type{});
+        }
+    };
+    auto compute_step = [&](Ops& o, uint32_t t0) {
+        if (c1 - t0 >= 64) {
+            compute(o, t0, std::false_type{});
+        } else {
+            compute(o, t0, std::true_type{});
+        }
+    };
+    Ops buf_a;
+    Ops buf_b;
+    uint32_t t0 = c0;
+    load_step(buf_a, t0);
+    while (true) {
+        uint32_t const t1 = t0 + 64;
+        if (t1 < c1) load_step(buf_b, t1);
+        compute_step(buf_a, t0);
+        if (t1 >= c1) break;
+        uint32_t const t2 = t1 + 64;
+        if (t2 < c1) load_step(buf_a, t2);
+        compute_step(buf_b, t1);
+        if (t2 >= c1) break;
+        t0 = t2;
     }
 
     float l_tot = l_part + __shfl_xor(l_part, 16);
@@ -229,8 +294,9 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
 // ---------------------------------------------------------------------------
 struct WaveScratch {
     float p[64];
-    const uint16_t* vrow[64];
+    const uint16_t* head[64];   // (layer, head) block of the token's page
     uint32_t cap[64];
+    uint32_t pt[64];
 };
 
 __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& item, uint32_t h,
@@ -268,16 +334,15 @@ __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& 
                 }
             }
             float s = -INFINITY;
-            const uint16_t* vrow = nullptr;
+            const uint16_t* hb = nullptr;
             if (page != nullptr) {
-                const uint16_t* hb = page + head_block(P, cap, layer, h);
-                const uint16_t* krow = hb + static_cast<uint64_t>(pt) * D;
+                hb = page + head_block(P, cap, layer, h);
                 float dot = 0.0f;
                 for (uint32_t d = 0; d < D; ++d) {
-                    dot += __half2float(__ushort_as_half(qv[d])) * __half2float(__ushort_as_half(krow[d]));
+                    dot += __half2float(__ushort_as_half(qv[d]))
+                        * __half2float(__ushort_as_half(hb[k_offset(cap, D, pt, d)]));
                 }
                 s = dot * scale2;
-                vrow = hb + static_cast<uint64_t>(cap) * D + pt;
             }
             float const m_new = fmaxf(m_run, wave_max(s));
             float const alpha = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
@@ -287,21 +352,23 @@ __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& 
 #pragma unroll
             for (int k = 0; k < 4; ++k) o[k] *= alpha;
             scratch->p[lane] = p;
-            scratch->vrow[lane] = vrow;
+            scratch->head[lane] = hb;
             scratch->cap[lane] = cap;
+            scratch->pt[lane] = pt;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             uint32_t const nt = min(64u, c1 - t0);
             for (uint32_t tt = 0; tt < nt; ++tt) {
                 float const pp = scratch->p[tt];
-                const uint16_t* vr = scratch->vrow[tt];
+                const uint16_t* vb = scratch->head[tt];
                 uint32_t const vc = scratch->cap[tt];
-                if (vr == nullptr || pp == 0.0f) continue;
+                uint32_t const vp = scratch->pt[tt];
+                if (vb == nullptr || pp == 0.0f) continue;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     uint32_t const d = lane + 64u * k;
-                    if (d < D) o[k] += pp * __half2float(__ushort_as_half(vr[static_cast<uint64_t>(d) * vc]));
+                    if (d < D) o[k] += pp * __half2float(__ushort_as_half(vb[v_offset(vc, D, vp, d)]));
                 }
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -332,31 +399,75 @@ __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& 
     }
 }
 
-__global__ __launch_bounds__(kBlock) void decode_kernel(PoolView P, const kimkv_decode_item* items,
+// Records the 8-token groups of [c0, c1) that entry `e` covers.  An entry
+// whose pages do not keep 8-token groups aligned (or names no page of the
+// storage) switches the chunk to the generic path.
+__device__ inline void add_groups(const PoolView& P, kimkv_block_desc const& e, uint32_t layer, uint32_t c0,
+                                  uint32_t c1, uint32_t T, GroupEntry* groups, uint32_t* s_generic)
+{
+    uint32_t const b = e.logical_token_begin;
+    uint32_t const end = b + e.valid_tokens;
+    uint32_t const lo = max(b, c0);
+    uint32_t const hi = min(end, c1);
+    if (lo >= hi) return;
+    uint32_t const cap = e.page_token_capacity;
+    const uint16_t* page = page_base(P, e.kind, e.slot, cap);
+    bool const aligned = (b & 7u) == 0 && (cap & 7u) == 0 && e.valid_tokens <= cap
+        && ((end & 7u) == 0 || end >= T) && page != nullptr;
+    if (!aligned) {
+        *s_generic = 1;
+        return;
+    }
+    const uint16_t* base = page + head_block(P, cap, layer, 0);
+    for (uint32_t g = (lo - c0) >> 3; g < (hi - c0 + 7) >> 3; ++g) {
+        groups[g] = GroupEntry{base, cap, c0 + 8 * g - b};
+    }
+}
+
+// Four waves per SIMD (127 VGPRs, no spills): the loop is latency bound, so
+// occupancy is what keeps enough K/V bytes in flight.
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(PoolView P, const kimkv_decode_item* items,
                                                         const uint32_t* prefix, uint32_t lane_count,
                                                         uint32_t chunk_tokens, uint32_t QH)
 {
     __shared__ GroupEntry groups[kMaxGroups];
     __shared__ WaveScratch scratch[kHeadsPerBlock];
     __shared__ uint32_t s_lane;
+    __shared__ uint32_t s_hit;
     __shared__ uint32_t s_idx0;
+    __shared__ uint32_t s_dok;
     __shared__ uint32_t s_generic;
 
     uint32_t const tid = threadIdx.x;
     uint32_t const chunk_id = blockIdx.x;
+    if (lane_count == 0) return;
+    // The prologue is a chain of dependent global reads, and under full HBM
+    // load each costs microseconds while this workgroup streams nothing, so
+    // both lookups are guessed and verified in the same round trip.
+    // Lane: guess from the average chunk count per lane (exact when lanes
+    // have equal chunk counts), with that lane's item loaded alongside.
+    uint32_t const guess = static_cast<uint32_t>(
+        min(static_cast<uint64_t>(chunk_id) * lane_count / gridDim.x, static_cast<uint64_t>(lane_count - 1)));
+    kimkv_decode_item item = items[guess];
+    uint32_t const pg0 = prefix[guess];
+    uint32_t const pg1 = prefix[guess + 1];
     if (tid == 0) {
+        s_hit = pg0 <= chunk_id && chunk_id < pg1 ? 1u : 0u;
         s_lane = 0xFFFFFFFFu;
         s_generic = 0;
     }
     __syncthreads();
-    for (uint32_t i = tid; i < lane_count; i += kBlock) {
-        if (prefix[i] <= chunk_id && chunk_id < prefix[i + 1]) s_lane = i;
+    uint32_t lane = guess;
+    if (s_hit == 0) {
+        for (uint32_t i = tid; i < lane_count; i += kBlock) {
+            if (prefix[i] <= chunk_id && chunk_id < prefix[i + 1]) s_lane = i;
+        }
+        __syncthreads();
+        lane = s_lane;
+        if (lane == 0xFFFFFFFFu) return;
+        item = items[lane];
     }
-    __syncthreads();
-    uint32_t const lane = s_lane;
-    if (lane == 0xFFFFFFFFu) return;
 
-    kimkv_decode_item const item = items[lane];
     uint32_t const H = P.heads;
     uint32_t const D = P.dim;
     uint32_t const chunk_index = chunk_id - prefix[lane];
@@ -372,39 +483,39 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(PoolView P, const kimkv_
     uint32_t const c1 = min(c0 + chunk_tokens, T);
     uint32_t const G = QH / H;
     bool const single = nchunks == 1;
-
-    if (tid < 64) {
-        uint32_t const idx0 = find_descriptor_wave(item.descriptors, item.descriptor_count, c0);
-        if (tid == 0) s_idx0 = idx0;
-    }
+    bool const fast_shape = D == 64 && G <= 16;
     uint32_t const ngroups = (c1 - c0 + 7) / 8;
     for (uint32_t g = tid; g < ngroups; g += kBlock) {
         groups[g] = GroupEntry{nullptr, 0, 0};
     }
     __syncthreads();
-    uint32_t const idx0 = s_idx0;
-    bool fast_shape = D == 64 && G <= 16;
-    for (uint32_t j = tid; j <= ngroups && idx0 + j < item.descriptor_count; j += kBlock) {
-        kimkv_block_desc const e = item.descriptors[idx0 + j];
-        uint32_t const b = e.logical_token_begin;
-        uint32_t const end = b + e.valid_tokens;
-        uint32_t const lo = max(b, c0);
-        uint32_t const hi = min(end, c1);
-        if (lo >= hi) continue;
-        uint32_t const cap = e.page_token_capacity;
-        const uint16_t* page = page_base(P, e.kind, e.slot, cap);
-        bool const aligned = (b & 7u) == 0 && (cap & 7u) == 0 && e.valid_tokens <= cap
-            && ((end & 7u) == 0 || end >= T) && page != nullptr;
-        if (!aligned) {
-            s_generic = 1;
-            continue;
-        }
-        const uint16_t* base = page + head_block(P, cap, item.layer, 0);
-        for (uint32_t g = (lo - c0) >> 3; g < (hi - c0 + 7) >> 3; ++g) {
-            groups[g] = GroupEntry{base, cap, c0 + 8 * g - b};
-        }
+
+    // First descriptor of the chunk: an entry holds at most 64 tokens, so the
+    // one holding c0 has index >= c0 / 64, and equals it when the table is all
+    // extents up to c0.  Build the group table from that guess; the thread
+    // reading the guessed entry checks that it holds c0.
+    uint32_t const dguess = min(c0 / 64u, item.descriptor_count - 1);
+    for (uint32_t j = tid; j <= ngroups && dguess + j < item.descriptor_count; j += kBlock) {
+        kimkv_block_desc const e = item.descriptors[dguess + j];
+        if (j == 0) s_dok = e.logical_token_begin <= c0 && c0 - e.logical_token_begin < e.valid_tokens ? 1u : 0u;
+        add_groups(P, e, item.layer, c0, c1, T, groups, &s_generic);
     }
     __syncthreads();
+    if (s_dok == 0) {
+        for (uint32_t g = tid; g < ngroups; g += kBlock) {
+            groups[g] = GroupEntry{nullptr, 0, 0};
+        }
+        if (tid < 64) {
+            uint32_t const idx0 = find_descriptor_wave(item.descriptors, item.descriptor_count, c0);
+            if (tid == 0) s_idx0 = idx0;
+        }
+        __syncthreads();
+        uint32_t const idx0 = s_idx0;
+        for (uint32_t j = tid; j <= ngroups && idx0 + j < item.descriptor_count; j += kBlock) {
+            add_groups(P, item.descriptors[idx0 + j], item.layer, c0, c1, T, groups, &s_generic);
+        }
+        __syncthreads();
+    }
 
     uint32_t const wave = tid >> 6;
     uint32_t const h = blockIdx.y * kHeadsPerBlock + wave;
@@ -416,33 +527,48 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(PoolView P, const kimkv_
     }
 }
 
-// Merges the per-chunk partials of every multi-chunk lane: block = (lane, q head).
-__global__ __launch_bounds__(64) void combine_kernel(const kimkv_decode_item* items, const uint32_t* prefix,
-                                                     uint32_t QH, uint32_t D)
+// Merges the per-chunk partials of every multi-chunk lane.  Block = (lane,
+// 4 query heads), one wave per head: the max and denominator are wave
+// reductions over the chunks (lane k takes chunks k, k+64, ...); the output
+// pass streams one 64-float partial row per chunk with all lanes loading
+// consecutive floats, unrolled so several rows are in flight.
+constexpr unsigned kCombineHeads = 4;
+
+__global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(const kimkv_decode_item* items,
+                                                                    const uint32_t* prefix, uint32_t QH, uint32_t D)
 {
     uint32_t const lane = blockIdx.x;
-    uint32_t const q = blockIdx.y;
+    uint32_t const q = blockIdx.y * kCombineHeads + (threadIdx.x >> 6);
+    uint32_t const l = threadIdx.x & 63u;
+    if (q >= QH) return;
     uint32_t const n = prefix[lane + 1] - prefix[lane];
     if (n <= 1) return;
     kimkv_decode_item const item = items[lane];
     if (item.workspace == nullptr || item.output == nullptr) return;
-    uint32_t const stride = QH * (D + 2);
+    uint64_t const stride = static_cast<uint64_t>(QH) * (D + 2);
     const float* ws = item.workspace + static_cast<uint64_t>(q) * (D + 2);
-    float M = -INFINITY;
-    for (uint32_t k = 0; k < n; ++k) M = fmaxf(M, ws[static_cast<uint64_t>(k) * stride + D]);
+    float m = -INFINITY;
+    for (uint32_t k = l; k < n; k += 64) m = fmaxf(m, ws[k * stride + D]);
+    float const M = wave_max(m);
     float den = 0.0f;
+    for (uint32_t k = l; k < n; k += 64) den += exp2f(ws[k * stride + D] - M) * ws[k * stride + D + 1];
+    den = wave_sum(den);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
     for (uint32_t k = 0; k < n; ++k) {
-        const float* part = ws + static_cast<uint64_t>(k) * stride;
-        den += exp2f(part[D] - M) * part[D + 1];
+        const float* part = ws + k * stride;
+        float const w = exp2f(part[D] - M);
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            uint32_t const d = l + 64u * j;
+            if (d < D) acc[j] += w * part[d];
+        }
     }
     float const inv = 1.0f / den;
-    for (uint32_t d = threadIdx.x; d < D; d += 64) {
-        float num = 0.0f;
-        for (uint32_t k = 0; k < n; ++k) {
-            const float* part = ws + static_cast<uint64_t>(k) * stride;
-            num += exp2f(part[D] - M) * part[d];
-        }
-        item.output[static_cast<uint64_t>(q) * D + d] = __half_as_ushort(__float2half_rn(num * inv));
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        uint32_t const d = l + 64u * j;
+        if (d < D) item.output[static_cast<uint64_t>(q) * D + d] = __half_as_ushort(__float2half_rn(acc[j] * inv));
     }
 }
 
@@ -478,14 +604,12 @@ __global__ __launch_bounds__(64) void reference_attention_kernel(PoolView P, con
             }
         }
         float s = -INFINITY;
-        const uint16_t* vrow = nullptr;
+        const uint16_t* hb = nullptr;
         if (page != nullptr) {
-            const uint16_t* hb = page + head_block(P, cap, layer, h);
-            const uint16_t* krow = hb + static_cast<uint64_t>(pt) * D;
+            hb = page + head_block(P, cap, layer, h);
             float dot = 0.0f;
-            for (uint32_t d = 0; d < D; ++d) dot += qv[d] * __half2float(__ushort_as_half(krow[d]));
+            for (uint32_t d = 0; d < D; ++d) dot += qv[d] * __half2float(__ushort_as_half(hb[k_offset(cap, D, pt, d)]));
             s = dot * scale;
-            vrow = hb + static_cast<uint64_t>(cap) * D + pt;
         }
         float const m_new = fmaxf(m_run, wave_max(s));
         float const alpha = m_new == -INFINITY ? 1.0f : expf(m_run - m_new);
@@ -495,19 +619,21 @@ __global__ __launch_bounds__(64) void reference_attention_kernel(PoolView P, con
 #pragma unroll
         for (int k = 0; k < 4; ++k) o[k] *= alpha;
         scratch.p[lane] = p;
-        scratch.vrow[lane] = vrow;
+        scratch.head[lane] = hb;
         scratch.cap[lane] = cap;
+        scratch.pt[lane] = pt;
         __syncthreads();
         uint32_t const nt = min(64u, T - t0);
         for (uint32_t tt = 0; tt < nt; ++tt) {
             float const pp = scratch.p[tt];
-            const uint16_t* vr = scratch.vrow[tt];
+            const uint16_t* vb = scratch.head[tt];
             uint32_t const vc = scratch.cap[tt];
-            if (vr == nullptr || pp == 0.0f) continue;
+            uint32_t const vp = scratch.pt[tt];
+            if (vb == nullptr || pp == 0.0f) continue;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 uint32_t const d = lane + 64u * k;
-                if (d < D) o[k] += pp * __half2float(__ushort_as_half(vr[static_cast<uint64_t>(d) * vc]));
+                if (d < D) o[k] += pp * __half2float(__ushort_as_half(vb[v_offset(vc, D, vp, d)]));
             }
         }
         __syncthreads();
@@ -587,9 +713,9 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage, const kimkv_
     kimkv_status const status = launch_status();
     if (status != KIMKV_OK) return status;
     if (total_chunks > lane_count) {
-        dim3 const cgrid(lane_count, query_heads);
-        combine_kernel<<<cgrid, 64, 0, s>>>(device_items, device_chunk_prefix, query_heads,
-                                            storage->layout.head_dim);
+        dim3 const cgrid(lane_count, (query_heads + kCombineHeads - 1) / kCombineHeads);
+        combine_kernel<<<cgrid, 64 * kCombineHeads, 0, s>>>(device_items, device_chunk_prefix, query_heads,
+                                                            storage->layout.head_dim);
         return launch_status();
     }
     return KIMKV_OK;

@@ -1,7 +1,8 @@
 // device_common.h -- shared device-side definitions for the gfx950 KV kernels.
 //
 // Page layout (see include/kimkv_hip.h): per (layer, head) a contiguous block
-// of 2*cap*D halves: K rows [cap][D] followed by V transposed [D][cap].
+// of 2*cap*D halves, K first, then V transposed, both cut into 32-wide blocks
+// (k_offset / v_offset below).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -80,6 +81,31 @@ __device__ inline uint32_t pool_tokens(const PoolView& p, uint32_t kind)
 __device__ inline uint64_t head_block(const PoolView& p, uint32_t cap, uint32_t layer, uint32_t head)
 {
     return (static_cast<uint64_t>(layer) * p.heads + head) * 2ull * cap * p.dim;
+}
+
+// Inside a (layer, head) block of a page with `cap` tokens and head dim D:
+//   K(t, d) = (d / kw) * cap * kw + t * kw + d % kw,             kw = k_width(D)
+//   V(t, d) = cap * D + (t / vw) * D * vw + d * vw + t % vw,      vw = v_width(cap)
+// K is split into 32-dim column blocks and V^T into 32-token column blocks,
+// so the 16-byte loads of one decode instruction (16 tokens x 8 dims of K,
+// or 16 dims x 8 tokens of V) land on whole 64-byte row pieces that tile
+// complete 128-byte lines.  8 consecutive dims of K (d % 8 == 0) and 8
+// consecutive tokens of V (t % 8 == 0) stay contiguous whenever D and cap
+// are multiples of 8.
+__host__ __device__ inline uint32_t k_width(uint32_t D) { return D % 32u == 0u ? 32u : D; }
+__host__ __device__ inline uint32_t v_width(uint32_t cap) { return cap % 32u == 0u ? 32u : cap; }
+
+__host__ __device__ inline uint64_t k_offset(uint32_t cap, uint32_t D, uint32_t t, uint32_t d)
+{
+    uint32_t const kw = k_width(D);
+    return static_cast<uint64_t>(d / kw) * cap * kw + static_cast<uint64_t>(t) * kw + d % kw;
+}
+
+__host__ __device__ inline uint64_t v_offset(uint32_t cap, uint32_t D, uint32_t t, uint32_t d)
+{
+    uint32_t const vw = v_width(cap);
+    return static_cast<uint64_t>(cap) * D + static_cast<uint64_t>(t / vw) * D * vw + static_cast<uint64_t>(d) * vw
+        + t % vw;
 }
 
 // ---- synthetic generator (bit-identical to kimkv_synth_value) -------------

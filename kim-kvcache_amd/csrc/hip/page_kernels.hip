@@ -91,9 +91,8 @@ __global__ __launch_bounds__(kBlock) void append_kernel(PoolView P, const kimkv_
                 uint32_t const d = rem - t * D;
                 uint64_t const sh = head_block(P, scap, layer, h);
                 uint64_t const dh = head_block(P, dcap, layer, h);
-                dst[dh + static_cast<uint64_t>(t) * D + d] = src[sh + static_cast<uint64_t>(t) * D + d];
-                dst[dh + static_cast<uint64_t>(dcap) * D + static_cast<uint64_t>(d) * dcap + t] =
-                    src[sh + static_cast<uint64_t>(scap) * D + static_cast<uint64_t>(d) * scap + t];
+                dst[dh + k_offset(dcap, D, t, d)] = src[sh + k_offset(scap, D, t, d)];
+                dst[dh + v_offset(dcap, D, t, d)] = src[sh + v_offset(scap, D, t, d)];
             }
         }
         __syncthreads();
@@ -110,8 +109,8 @@ __global__ __launch_bounds__(kBlock) void append_kernel(PoolView P, const kimkv_
         uint64_t const so = layer_off + static_cast<uint64_t>(t) * job.src_token_stride + rem;
         uint64_t const dh = head_block(P, dcap, layer, h);
         uint32_t const pt = job.dst_token + t;
-        dst[dh + static_cast<uint64_t>(pt) * D + d] = job.src_key[so];
-        dst[dh + static_cast<uint64_t>(dcap) * D + static_cast<uint64_t>(d) * dcap + pt] = job.src_value[so];
+        dst[dh + k_offset(dcap, D, pt, d)] = job.src_key[so];
+        dst[dh + v_offset(dcap, D, pt, d)] = job.src_value[so];
     }
 }
 
@@ -151,7 +150,7 @@ __global__ __launch_bounds__(kBlock) void gather_kernel(PoolView P, const kimkv_
                 uint32_t const h = c / dchunks;
                 uint32_t const dc = c - h * dchunks;
                 uint4 const* src = reinterpret_cast<uint4 const*>(
-                    e.page + head_block(P, e.cap, layer, h) + static_cast<uint64_t>(e.pt) * D + dc * 8);
+                    e.page + head_block(P, e.cap, layer, h) + k_offset(e.cap, D, e.pt, dc * 8));
                 reinterpret_cast<uint4*>(out_base)[i] = *src;
             }
         } else {
@@ -162,7 +161,7 @@ __global__ __launch_bounds__(kBlock) void gather_kernel(PoolView P, const kimkv_
                 if (e.page == nullptr) continue;
                 uint32_t const h = r / D;
                 uint32_t const d = r - h * D;
-                out_base[i] = e.page[head_block(P, e.cap, layer, h) + static_cast<uint64_t>(e.pt) * D + d];
+                out_base[i] = e.page[head_block(P, e.cap, layer, h) + k_offset(e.cap, D, e.pt, d)];
             }
         }
         return;
@@ -182,12 +181,11 @@ __global__ __launch_bounds__(kBlock) void gather_kernel(PoolView P, const kimkv_
                     ++t;
                     continue;
                 }
-                uint16_t const* row = e.page + head_block(P, e.cap, layer, h)
-                    + static_cast<uint64_t>(e.cap) * D + static_cast<uint64_t>(d) * e.cap;
+                uint16_t const* hb = e.page + head_block(P, e.cap, layer, h);
                 bool const vec = (t & 7u) == 0 && t + 8 <= n && (e.pt & 7u) == 0 && (e.cap & 7u) == 0
                     && e.pt + 8 <= e.cap && tab[t + 7].page == e.page && tab[t + 7].pt == e.pt + 7;
                 if (vec) {
-                    uint4 const v = *reinterpret_cast<uint4 const*>(row + e.pt);
+                    uint4 const v = *reinterpret_cast<uint4 const*>(hb + v_offset(e.cap, D, e.pt, d));
                     uint32_t const w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                     for (uint32_t j = 0; j < 4; ++j) {
@@ -196,7 +194,7 @@ __global__ __launch_bounds__(kBlock) void gather_kernel(PoolView P, const kimkv_
                     }
                     t += 8;
                 } else {
-                    stage[t * kRowChunk + tid] = row[e.pt];
+                    stage[t * kRowChunk + tid] = hb[v_offset(e.cap, D, e.pt, d)];
                     ++t;
                 }
             }
@@ -256,8 +254,8 @@ __global__ __launch_bounds__(kBlock) void promote_kernel(PoolView P, const kimkv
             uint32_t const t = rem / dchunks;
             uint32_t const dc = rem - t * dchunks;
             uint4 const v = *reinterpret_cast<uint4 const*>(
-                src[t >> 3] + head_block(P, mt, layer, h) + (t & 7u) * D + dc * 8);
-            *reinterpret_cast<uint4*>(dst + head_block(P, et, layer, h) + t * D + dc * 8) = v;
+                src[t >> 3] + head_block(P, mt, layer, h) + k_offset(mt, D, t & 7u, dc * 8));
+            *reinterpret_cast<uint4*>(dst + head_block(P, et, layer, h) + k_offset(et, D, t, dc * 8)) = v;
         }
         // V^T: (h, d, k) -- micro row d (8 tokens, 16 bytes) -> extent row d at 8k.
         uint32_t const vchunks = H * D * 8;
@@ -267,8 +265,8 @@ __global__ __launch_bounds__(kBlock) void promote_kernel(PoolView P, const kimkv
             uint32_t const d = rem / 8;
             uint32_t const k = rem & 7u;
             uint4 const v = *reinterpret_cast<uint4 const*>(
-                src[k] + head_block(P, mt, layer, h) + mt * D + d * mt);
-            *reinterpret_cast<uint4*>(dst + head_block(P, et, layer, h) + et * D + d * et + 8 * k) = v;
+                src[k] + head_block(P, mt, layer, h) + v_offset(mt, D, 0, d));
+            *reinterpret_cast<uint4*>(dst + head_block(P, et, layer, h) + v_offset(et, D, 8 * k, d)) = v;
         }
         return;
     }
@@ -282,8 +280,8 @@ __global__ __launch_bounds__(kBlock) void promote_kernel(PoolView P, const kimkv
         uint32_t const st = t % mt;
         uint64_t const sh = head_block(P, mt, layer, h);
         uint64_t const dh = head_block(P, et, layer, h);
-        dst[dh + t * D + d] = s[sh + st * D + d];
-        dst[dh + static_cast<uint64_t>(et) * D + d * et + t] = s[sh + static_cast<uint64_t>(mt) * D + d * mt + st];
+        dst[dh + k_offset(et, D, t, d)] = s[sh + k_offset(mt, D, st, d)];
+        dst[dh + v_offset(et, D, t, d)] = s[sh + v_offset(mt, D, st, d)];
     }
 }
 
@@ -314,7 +312,7 @@ __global__ __launch_bounds__(kBlock) void fill_table_kernel(PoolView P, const ki
             if (e.page == nullptr) continue;
             uint32_t const h = r / D;
             uint32_t const d = r - h * D;
-            e.page[head_block(P, e.cap, layer, h) + static_cast<uint64_t>(e.pt) * D + d] =
+            e.page[head_block(P, e.cap, layer, h) + k_offset(e.cap, D, e.pt, d)] =
                 synth_f16(seed, kv_row(stream_id, layer, 0, t0 + t), r);
         }
         return;
@@ -339,15 +337,13 @@ __global__ __launch_bounds__(kBlock) void fill_table_kernel(PoolView P, const ki
                 uint32_t const hi = synth_f16(seed, kv_row(stream_id, layer, 1, t0 + tb + 2 * j + 1), r);
                 w[j] = lo | (hi << 16);
             }
-            *reinterpret_cast<uint4*>(e.page + head_block(P, e.cap, layer, h)
-                                      + static_cast<uint64_t>(e.cap) * D + static_cast<uint64_t>(d) * e.cap + e.pt) =
+            *reinterpret_cast<uint4*>(e.page + head_block(P, e.cap, layer, h) + v_offset(e.cap, D, e.pt, d)) =
                 make_uint4(w[0], w[1], w[2], w[3]);
         } else {
             for (uint32_t t = tb; t < te; ++t) {
                 TokEntry const f = tab[t];
                 if (f.page == nullptr) continue;
-                f.page[head_block(P, f.cap, layer, h) + static_cast<uint64_t>(f.cap) * D
-                       + static_cast<uint64_t>(d) * f.cap + f.pt] =
+                f.page[head_block(P, f.cap, layer, h) + v_offset(f.cap, D, f.pt, d)] =
                     synth_f16(seed, kv_row(stream_id, layer, 1, t0 + t), r);
             }
         }
@@ -360,6 +356,26 @@ __global__ __launch_bounds__(kBlock) void fill_rows_kernel(uint16_t* out, uint64
     uint64_t const stride = static_cast<uint64_t>(gridDim.x) * kBlock;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; i < count; i += stride) {
         out[i] = synth_f16(seed, row0 + i / cols, static_cast<uint32_t>(i % cols));
+    }
+}
+
+// Contiguous K/V block [layers][2][tokens][cols]: the row of (l, c, t) is
+// kv_row(stream_id, l, c, token0 + t).
+__global__ __launch_bounds__(kBlock) void fill_kv_kernel(uint16_t* out, uint32_t layers, uint32_t tokens,
+                                                         uint32_t cols, uint64_t seed, uint32_t stream_id,
+                                                         uint32_t token0)
+{
+    uint64_t const per_block = static_cast<uint64_t>(tokens) * cols;
+    uint64_t const count = per_block * 2u * layers;
+    uint64_t const stride = static_cast<uint64_t>(gridDim.x) * kBlock;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; i < count; i += stride) {
+        uint64_t const lc = i / per_block;
+        uint64_t const r = i - lc * per_block;
+        uint32_t const t = static_cast<uint32_t>(r / cols);
+        uint32_t const col = static_cast<uint32_t>(r - static_cast<uint64_t>(t) * cols);
+        out[i] = synth_f16(seed, kv_row(stream_id, static_cast<uint32_t>(lc >> 1), static_cast<uint32_t>(lc & 1u),
+                                        token0 + t),
+                           col);
     }
 }
 
@@ -429,6 +445,20 @@ kimkv_status kimkv_fill_rows(uint16_t* device_out, uint64_t count, uint64_t seed
     uint64_t const blocks64 = (count + kBlock - 1) / kBlock;
     unsigned const blocks = static_cast<unsigned>(blocks64 < 65536 ? blocks64 : 65536);
     fill_rows_kernel<<<blocks, kBlock, 0, native(stream)>>>(device_out, count, seed, row0, cols);
+    return launch_status();
+}
+
+kimkv_status kimkv_fill_kv(uint16_t* device_out, uint32_t layers, uint32_t tokens, uint32_t cols, uint64_t seed,
+                           uint32_t stream_id, uint32_t token0, kimkv_stream_t stream)
+{
+    if (device_out == nullptr || cols == 0 || static_cast<uint64_t>(token0) + tokens > (1ull << 32)) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    uint64_t const count = static_cast<uint64_t>(layers) * 2u * tokens * cols;
+    if (count == 0) return KIMKV_OK;
+    uint64_t const blocks64 = (count + kBlock - 1) / kBlock;
+    unsigned const blocks = static_cast<unsigned>(blocks64 < 65536 ? blocks64 : 65536);
+    fill_kv_kernel<<<blocks, kBlock, 0, native(stream)>>>(device_out, layers, tokens, cols, seed, stream_id, token0);
     return launch_status();
 }
 

@@ -156,6 +156,40 @@ const kimkv_storage* kimkv_engine_storage(const kimkv_engine* e)
     return static_cast<const kimkv_storage*>(engineStorage(*e->backend));
 }
 
+int kimkv_engine_append_prefill(kimkv_engine* e, uint64_t id, uint32_t n, const uint16_t* device_kv,
+                                kimkv_stream_t stream, int promote, uint32_t* promoted)
+{
+    return code(appendPrefill(*e->backend, id, n, device_kv, stream, promote != 0, promoted));
+}
+
+int kimkv_engine_permute_free_slots(kimkv_engine* e, uint32_t kind, uint64_t seed)
+{
+    if (kind > 1) return static_cast<int>(EngineKvError::InvalidArgument);
+    return code(permuteEngineFreeSlots(*e->backend, kind == 0 ? PageKind::Micro : PageKind::Extent, seed));
+}
+
+void kimkv_engine_reserve_batch(kimkv_engine* e, const uint64_t* ids, const uint32_t* expected, uint32_t count,
+                                kimkv_stream_t stream, kimkv_txn** txns, int* statuses)
+{
+    std::vector<ReserveTokenRequest> requests(count);
+    std::vector<TokenReserveResult> results(count);
+    for (uint32_t i = 0; i < count; ++i) requests[i] = ReserveTokenRequest{ids[i], expected[i], stream};
+    if (!reserveTokenBatch(*e->backend, requests.data(), count, results.data())) {
+        for (uint32_t i = 0; i < count; ++i) statuses[i] = kimkv_engine_reserve_token(e, ids[i], expected[i], stream, &txns[i]);
+        return;
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+        txns[i] = nullptr;
+        TokenReserveResult& r = results[i];
+        if (!r.ok()) {
+            statuses[i] = r.status.ok() ? static_cast<int>(EngineKvError::InternalError) : code(r.status);
+            continue;
+        }
+        txns[i] = new (std::nothrow) kimkv_txn{std::move(r.transaction)};
+        statuses[i] = txns[i] != nullptr ? 0 : static_cast<int>(EngineKvError::ResourceExhausted);
+    }
+}
+
 int kimkv_txn_write_layer(kimkv_txn* t, uint32_t layer, const uint16_t* key, const uint16_t* value)
 {
     return code(t->t.writeLayer(LayerKvWrite{layer, key, value}));
@@ -180,26 +214,35 @@ void kimkv_txn_state(const kimkv_txn* t, uint32_t* phase, uint32_t* next_layer, 
 
 void kimkv_txn_destroy(kimkv_txn* t) { delete t; }
 
-void kimkv_attend_layer_batch(kimkv_txn** txns, const kimkv_decode_request* requests, uint32_t count, int* statuses)
+void kimkv_txn_commit_batch(kimkv_txn** txns, uint32_t count, int* statuses)
+{
+    for (uint32_t i = 0; i < count; ++i) {
+        if (txns[i] == nullptr) {
+            statuses[i] = static_cast<int>(EngineKvError::InvalidArgument);
+            continue;
+        }
+        statuses[i] = code(txns[i]->t.commit());
+        delete txns[i];
+        txns[i] = nullptr;
+    }
+}
+
+void kimkv_attend_layer_batch(kimkv_txn** txns, const kimkv_decode_request* requests, uint32_t count,
+                              void* device_items, uint32_t device_capacity, int* statuses)
 {
     if (count == 0) return;
-    std::vector<PagedDecodeBatchItem> items(count);
-    std::vector<DevicePagedDecodeBatchItem> host(count);
-    void* device = nullptr;
-    bool const have_device = kimkv_device_malloc(&device, count * sizeof(DevicePagedDecodeBatchItem)) == KIMKV_OK;
+    thread_local std::vector<PagedDecodeBatchItem> items;
+    thread_local std::vector<DevicePagedDecodeBatchItem> host;
+    items.assign(count, PagedDecodeBatchItem{});
+    host.resize(count);
     for (uint32_t i = 0; i < count; ++i) {
         items[i].transaction = txns[i] != nullptr ? &txns[i]->t : nullptr;
         items[i].request = request(requests[i]);
     }
-    PagedDecodeBatch batch{items.data(), count, host.data(),
-                           have_device ? static_cast<DevicePagedDecodeBatchItem*>(device) : nullptr, count};
+    PagedDecodeBatch batch{items.data(), count, host.data(), static_cast<DevicePagedDecodeBatchItem*>(device_items),
+                           device_items != nullptr ? device_capacity : 0};
     attendLayerBatch(batch);
     for (uint32_t i = 0; i < count; ++i) statuses[i] = code(items[i].status);
-    if (device != nullptr) {
-        // The launch reads the item array asynchronously: free after it drained.
-        static_cast<void>(kimkv_device_synchronize());
-        static_cast<void>(kimkv_device_free(device));
-    }
 }
 
 void kimkv_write_layer_batch(kimkv_txn** txns, const uint32_t* layers, const uint16_t* const* keys,

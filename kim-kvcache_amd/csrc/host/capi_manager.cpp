@@ -3,6 +3,7 @@
 
 #include "capi_internal.h"
 #include "kim-kv/runtime/kv_cache_manager.h"
+#include "kim-kv/runtime/pool_permutation.h"
 
 #include <new>
 #include <optional>
@@ -41,15 +42,6 @@ void poolOut(PagePoolSnapshot const& p, kimkv_pool_snapshot* o)
     *o = kimkv_pool_snapshot{static_cast<std::uint32_t>(p.kind), p.total_slots, p.free_slots, p.allocated_slots,
                              p.successful_allocations, p.successful_releases, p.failed_allocations,
                              p.rejected_releases};
-}
-
-std::uint64_t splitmixNext(std::uint64_t& state)
-{
-    state += 0x9E3779B97F4A7C15ull;
-    std::uint64_t z = state;
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
 }
 
 }  // namespace
@@ -162,54 +154,12 @@ void kimkv_manager_get_snapshot(const kimkv_manager* m, kimkv_manager_snapshot* 
 
 int kimkv_manager_check_invariants(const kimkv_manager* m) { return m->m->checkInvariants() ? 1 : 0; }
 
-void kimkv_seeded_permutation(uint64_t seed, uint32_t n, uint32_t* out)
-{
-    for (uint32_t i = 0; i < n; ++i) out[i] = i;
-    std::uint64_t state = seed;
-    for (uint32_t i = n; i > 1; --i) {
-        uint32_t const j = static_cast<uint32_t>(splitmixNext(state) % i);
-        std::swap(out[i - 1], out[j]);
-    }
-}
+void kimkv_seeded_permutation(uint64_t seed, uint32_t n, uint32_t* out) { seededPermutation(seed, n, out); }
 
 int kimkv_manager_permute_free_slots(kimkv_manager* m, uint32_t kind, uint64_t seed)
 {
-    KvCacheManager& mgr = *m->m;
-    KvCacheManagerSnapshot const snap = mgr.snapshot();
     if (kind > 1) return code(KvCacheError::InvalidState);
-    PagePoolSnapshot const pool = kind == 0 ? snap.micro_pool : snap.extent_pool;
-    uint32_t const n = pool.total_slots;
-    if (pool.free_slots != n) return code(KvCacheError::InvalidState);
-    std::vector<uint32_t> perm(n);
-    kimkv_seeded_permutation(seed, n, perm.data());
-    // Throw-away request ids live in the top 16 bits so they cannot collide
-    // with caller ids below 2^48.
-    constexpr std::uint64_t kBase = 0xFFFF000000000000ull;
-    std::vector<std::uint64_t> owner(n, 0);
-    for (uint32_t i = 0; i < n; ++i) {
-        std::uint64_t const id = kBase + i;
-        KvCacheError e = mgr.createRequest(id);
-        if (e != KvCacheError::None) return code(e);
-        if (kind == 0) {
-            e = mgr.append(id, kMicroPageTokenCapacity);
-        } else {
-            e = mgr.append(id, kExtentPageTokenCapacity);
-            if (e == KvCacheError::None) {
-                PromotionPrepareResult const p = mgr.preparePromotion(id, 0);
-                e = p.error;
-                if (e == KvCacheError::None) e = mgr.commitPromotion(p.promotion_id);
-            }
-        }
-        if (e != KvCacheError::None) return code(e);
-        std::optional<BlockTable> t = mgr.blockTable(id);
-        if (!t.has_value() || t->entries().size() != 1) return code(KvCacheError::InternalInvariantViolation);
-        owner[t->entries()[0].handle.slot] = id;
-    }
-    for (uint32_t k = n; k > 0; --k) {
-        KvCacheError const e = mgr.releaseRequest(owner[perm[k - 1]]);
-        if (e != KvCacheError::None) return code(e);
-    }
-    return 0;
+    return code(permuteFreeSlotsOf(*m->m, kind == 0 ? PageKind::Micro : PageKind::Extent, seed));
 }
 
 }  // extern "C"

@@ -6,14 +6,15 @@
 #include <cstddef>
 #include <cstdint>
 #include <limits>
-#include <tuple>
 #include <vector>
 
 namespace kimkvcache {
 namespace {
 
-// True when no physical page appears twice.  Pairwise for short tables, a
-// sort of the handles for long ones (same answer, O(n log n)).
+// True when no physical page appears twice.  Pairwise for short tables; for
+// long ones an open-addressing set on (kind, slot) with per-call stamps (no
+// clearing), comparing the generation on a (kind, slot) hit: same answer as
+// comparing every pair, linear time.
 bool handlesDistinct(std::vector<MappingEntry> const& entries)
 {
     std::size_t const n = entries.size();
@@ -25,13 +26,31 @@ bool handlesDistinct(std::vector<MappingEntry> const& entries)
         }
         return true;
     }
-    std::vector<std::tuple<std::uint8_t, std::uint32_t, std::uint32_t>> keys;
-    keys.reserve(n);
-    for (MappingEntry const& e : entries) {
-        keys.emplace_back(static_cast<std::uint8_t>(e.handle.kind), e.handle.slot, e.handle.generation);
+    struct Slot {
+        std::uint64_t key;
+        std::uint32_t generation;
+        std::uint32_t stamp;
+    };
+    thread_local std::vector<Slot> set;
+    thread_local std::uint32_t stamp = 0;
+    std::size_t cap = 64;
+    while (cap < 2 * n) cap <<= 1;
+    if (set.size() < cap) set.assign(cap, Slot{0, 0, 0});
+    if (++stamp == 0) {
+        for (Slot& s : set) s.stamp = 0;
+        stamp = 1;
     }
-    std::sort(keys.begin(), keys.end());
-    return std::adjacent_find(keys.begin(), keys.end()) == keys.end();
+    std::size_t const mask = cap - 1;
+    for (MappingEntry const& e : entries) {
+        std::uint64_t const key = (static_cast<std::uint64_t>(e.handle.kind) << 32) | e.handle.slot;
+        std::size_t h = static_cast<std::size_t>((key * 0x9E3779B97F4A7C15ull) >> 32) & mask;
+        while (set[h].stamp == stamp) {
+            if (set[h].key == key && set[h].generation == e.handle.generation) return false;
+            h = (h + 1) & mask;
+        }
+        set[h] = Slot{key, e.handle.generation, stamp};
+    }
+    return true;
 }
 
 bool tableValid(std::vector<MappingEntry> const& entries, std::uint16_t uniform_capacity)

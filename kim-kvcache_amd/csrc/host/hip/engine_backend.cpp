@@ -12,9 +12,11 @@
 #include "kim-kv/hip/hip_engine_kv_backend.h"
 
 #include "kim-kv/runtime/kv_cache_manager.h"
+#include "kim-kv/runtime/pool_permutation.h"
 #include "storage.h"
 
 #include <atomic>
+#include <cstddef>
 #include <cstring>
 #include <optional>
 #include <memory>
@@ -67,11 +69,91 @@ struct BackendState final {
     std::atomic<std::uint64_t> next_transaction_id{1};
     mutable std::mutex mutex;
     std::mutex launch_mutex;   // serialises staging + launches of batch calls
+    std::mutex event_mutex;
+    std::vector<void*> free_events;   // completion events of finished transactions
 
     BackendState(EngineKvConfig c, std::uint32_t micro, std::uint32_t extent)
         : config(c), manager(micro, extent), storage(c.kv_layout, micro, extent)
     {
     }
+
+    ~BackendState()
+    {
+        for (void* e : free_events) static_cast<void>(kimkv_event_destroy(e));
+    }
+
+    // Completion events are recycled: creating one per token costs more than
+    // the rest of a reserve.
+    void* acquireEvent() noexcept
+    {
+        {
+            std::lock_guard<std::mutex> lock(event_mutex);
+            if (!free_events.empty()) {
+                void* e = free_events.back();
+                free_events.pop_back();
+                return e;
+            }
+        }
+        void* e = nullptr;
+        return kimkv_event_create(&e, 0) == KIMKV_OK ? e : nullptr;
+    }
+
+    // Only events that have been waited for (or never recorded) come back.
+    void releaseEvent(void* e) noexcept
+    {
+        if (e == nullptr) return;
+        std::lock_guard<std::mutex> lock(event_mutex);
+        try {
+            free_events.push_back(e);
+        } catch (...) {
+            static_cast<void>(kimkv_event_destroy(e));
+        }
+    }
+};
+
+// Completion of one launch, shared by every transaction in it: an event
+// recorded right after the launch.  Commit waits on the mark of the
+// transaction's last launch rather than on an event recorded at commit time,
+// so committing one lane group is not held up by work queued after it on the
+// same stream (the next group's layers).
+struct CompletionMark final {
+    std::shared_ptr<BackendState> owner;
+    void* event{nullptr};
+
+    CompletionMark(std::shared_ptr<BackendState> o, void* e) : owner(std::move(o)), event(e) {}
+    ~CompletionMark() { owner->releaseEvent(event); }
+    CompletionMark(CompletionMark const&) = delete;
+    CompletionMark& operator=(CompletionMark const&) = delete;
+};
+
+std::shared_ptr<CompletionMark> markLaunch(std::shared_ptr<BackendState> const& owner, HipStream stream) noexcept
+{
+    void* e = owner->acquireEvent();
+    if (e == nullptr) return nullptr;
+    if (kimkv_event_record(e, stream) != KIMKV_OK) {
+        owner->releaseEvent(e);
+        return nullptr;
+    }
+    try {
+        return std::make_shared<CompletionMark>(owner, e);
+    } catch (...) {
+        owner->releaseEvent(e);
+        return nullptr;
+    }
+}
+
+// Device block descriptors of one reserve call: every transaction of a
+// batched reserve points into one arena filled by a single upload; the
+// buffer returns to the cache when the last of them has finished.
+struct DescriptorArena final {
+    std::shared_ptr<BackendState> owner;
+    void* ptr{nullptr};
+    std::size_t granted{0};
+
+    DescriptorArena(std::shared_ptr<BackendState> o, void* p, std::size_t g) : owner(std::move(o)), ptr(p), granted(g) {}
+    ~DescriptorArena() { owner->storage.buffers().release(ptr, granted); }
+    DescriptorArena(DescriptorArena const&) = delete;
+    DescriptorArena& operator=(DescriptorArena const&) = delete;
 };
 
 class HipTokenTransaction final : public TokenTransactionBackend {
@@ -101,31 +183,18 @@ public:
     {
         static_cast<void>(finish());
         releaseDescriptors();
-        if (event_ != nullptr) static_cast<void>(kimkv_event_destroy(event_));
     }
 
-    // Descriptor upload at reserve time (beginEngineTransaction).
-    HipStatus begin(BlockTable const& reserved)
+    // Binds the transaction to its slice of a reserve call's descriptor arena
+    // (the descriptor upload of beginEngineTransaction, issued by the caller
+    // on this transaction's stream before any of its launches).
+    void attach(std::shared_ptr<DescriptorArena> arena, std::size_t first, std::uint32_t count) noexcept
     {
-        HipKvStorage& st = owner_->storage;
-        std::vector<kimkv_block_desc> d;
-        st.descriptors(reserved, d);
-        desc_count_ = static_cast<std::uint32_t>(d.size());
-        std::size_t const bytes = d.size() * sizeof(kimkv_block_desc);
-        descriptors_ = st.buffers().acquire(bytes, desc_granted_);
-        if (descriptors_ == nullptr) return HipStatus{HipError::AllocationFailed, kimkv_last_native_error()};
-        if (kimkv_event_create(&event_, 0) != KIMKV_OK) {
-            return HipStatus{HipError::AllocationFailed, kimkv_last_native_error()};
-        }
-        // Staging and its fence stay under the launch lock so that no other
-        // thread's region lands between them (a fence covers the regions
-        // before it on its stream).
-        std::lock_guard<std::mutex> lock(owner_->launch_mutex);
-        bool const staged = st.ring().uploadTo(descriptors_, d.data(), bytes, stream_);
-        st.ring().fence(stream_);
-        if (!staged) return HipStatus{HipError::SubmissionFailed, kimkv_last_native_error()};
+        descriptors_ = static_cast<kimkv_block_desc const*>(arena->ptr) + first;
+        desc_count_ = count;
+        arena_ = std::move(arena);
+        dirty_ = true;   // the descriptor copy is in flight
         submission_ = {};
-        return {};
     }
 
     EngineKvStatus writeLayer(LayerKvWrite const& write, EngineStream) override
@@ -147,14 +216,19 @@ public:
         if (!s.ok()) return mapDevice(s);
         std::lock_guard<std::mutex> lock(owner_->launch_mutex);
         HipKvStorage& st = owner_->storage;
-        void* items = st.ring().upload(&item, sizeof(item), stream_);
-        void* pre = items != nullptr ? st.ring().upload(prefix.data(), prefix.size() * 4, stream_) : nullptr;
-        if (items == nullptr || pre == nullptr) return mapDevice(failSubmission(kimkv_last_native_error()));
-        kimkv_status const k = kimkv_paged_decode_batch(st.handle(), static_cast<kimkv_decode_item const*>(items),
-                                                        static_cast<std::uint32_t const*>(pre), 1, total, chunk,
-                                                        owner_->config.query_head_count, stream_);
+        struct {
+            kimkv_decode_item item;
+            std::uint32_t prefix[2];
+        } packed{item, {prefix[0], prefix[1]}};
+        auto* staged = static_cast<unsigned char*>(st.ring().upload(&packed, sizeof(packed), stream_));
+        if (staged == nullptr) return mapDevice(failSubmission(kimkv_last_native_error()));
+        kimkv_status const k = kimkv_paged_decode_batch(
+            st.handle(), reinterpret_cast<kimkv_decode_item const*>(staged),
+            reinterpret_cast<std::uint32_t const*>(staged + offsetof(decltype(packed), prefix)), 1, total, chunk,
+            owner_->config.query_head_count, stream_);
         st.ring().fence(stream_);
         if (k != KIMKV_OK) return mapDevice(failSubmission(kimkv_last_native_error()));
+        setMark(markLaunch(owner_, stream_));
         return {};
     }
 
@@ -215,23 +289,31 @@ public:
         std::vector<std::uint32_t> pre(n + 1, 0);
         for (std::size_t i = 0; i < n; ++i) pre[i + 1] = pre[i] + (launch_tokens[i] + chunk - 1) / chunk;
         total = pre[n];
+        // Items and chunk prefix travel in one staged copy (each copy on the
+        // stream costs a dispatch and a gap between kernels); the caller's
+        // device_items scratch is validated by the API but not needed here.
+        std::size_t const items_bytes = (n * sizeof(DevicePagedDecodeBatchItem) + 15) & ~std::size_t{15};
+        thread_local std::vector<unsigned char> staging;
+        staging.resize(items_bytes + pre.size() * 4);
+        std::memcpy(staging.data(), batch.host_items, n * sizeof(DevicePagedDecodeBatchItem));
+        std::memcpy(staging.data() + items_bytes, pre.data(), pre.size() * 4);
         std::lock_guard<std::mutex> lock(o.launch_mutex);
         HipStream const stream = stream_;
-        bool ok = st.ring().uploadTo(batch.device_items, batch.host_items, n * sizeof(DevicePagedDecodeBatchItem),
-                                     stream);
-        void* dpre = ok ? st.ring().upload(pre.data(), pre.size() * 4, stream) : nullptr;
+        auto* staged = static_cast<unsigned char*>(st.ring().upload(staging.data(), staging.size(), stream));
         kimkv_status k = KIMKV_SUBMISSION_FAILED;
-        if (dpre != nullptr) {
-            k = kimkv_paged_decode_batch(st.handle(), reinterpret_cast<kimkv_decode_item const*>(batch.device_items),
-                                         static_cast<std::uint32_t const*>(dpre), static_cast<std::uint32_t>(n), total,
-                                         chunk, QH, stream);
+        if (staged != nullptr) {
+            k = kimkv_paged_decode_batch(st.handle(), reinterpret_cast<kimkv_decode_item const*>(staged),
+                                         reinterpret_cast<std::uint32_t const*>(staged + items_bytes),
+                                         static_cast<std::uint32_t>(n), total, chunk, QH, stream);
         }
         st.ring().fence(stream);
+        std::shared_ptr<CompletionMark> const mark = k == KIMKV_OK ? markLaunch(owner_, stream) : nullptr;
         std::uint64_t good = 0;
         for (std::size_t i : launched) {
             PagedDecodeBatchItem& item = batch.items[i];
             auto* t = static_cast<HipTokenTransaction*>(batchBackend(item));
             item.status = k == KIMKV_OK ? EngineKvStatus{} : mapDevice(t->failSubmission(kimkv_last_native_error()));
+            if (k == KIMKV_OK) t->setMark(mark);
             good += item.status.ok() ? 1 : 0;
         }
         if (good != 0) {
@@ -369,6 +451,7 @@ private:
                                    static_cast<std::uint32_t>(n), 1, stream);
         }
         st.ring().fence(stream);
+        for (HipTokenTransaction* t : owners) t->dirty_ = true;
         if (k == KIMKV_OK) return {};
         int const native = kimkv_last_native_error();
         for (HipTokenTransaction* t : owners) static_cast<void>(t->failSubmission(native));
@@ -392,7 +475,7 @@ private:
 
     DevicePagedDecodeBatchItem deviceItem(PagedDecodeRequest const& r, bool uses_workspace) const
     {
-        return DevicePagedDecodeBatchItem{static_cast<DeviceBlockDescriptor const*>(descriptors_), desc_count_,
+        return DevicePagedDecodeBatchItem{reinterpret_cast<DeviceBlockDescriptor const*>(descriptors_), desc_count_,
                                           token_count_, r.layer, r.device_query,
                                           uses_workspace ? static_cast<float*>(r.device_workspace) : nullptr,
                                           r.device_output, r.attention_scale};
@@ -423,26 +506,36 @@ private:
         if (!submission_.ok()) {
             static_cast<void>(kimkv_stream_synchronize(stream_));
             final_ = submission_;
-        } else if (event_ == nullptr) {
-            final_ = HipStatus{HipError::InternalError, 0};
-        } else if (kimkv_event_record(event_, stream_) != KIMKV_OK || kimkv_event_synchronize(event_) != KIMKV_OK) {
-            final_ = HipStatus{HipError::ExecutionFailed, kimkv_last_native_error()};
-        } else if (owner_->storage.consumeFailure(HipFailurePoint::Completion)) {
-            final_ = HipStatus{HipError::ExecutionFailed, -1};
         } else {
-            final_ = {};
+            // The last attention launch carries a mark; anything enqueued after
+            // it (a rollback mid-layer) is drained with the whole stream.
+            kimkv_status const waited = mark_ != nullptr && !dirty_ ? kimkv_event_synchronize(mark_->event)
+                                                                     : kimkv_stream_synchronize(stream_);
+            if (waited != KIMKV_OK) {
+                final_ = HipStatus{HipError::ExecutionFailed, kimkv_last_native_error()};
+            } else if (owner_->storage.consumeFailure(HipFailurePoint::Completion)) {
+                final_ = HipStatus{HipError::ExecutionFailed, -1};
+            } else {
+                final_ = {};
+            }
         }
         finished_ = true;
+        mark_.reset();
         releaseDescriptors();
         return final_;
     }
 
+    void setMark(std::shared_ptr<CompletionMark> mark) noexcept
+    {
+        if (mark == nullptr) return;   // keep dirty: finish() drains the stream instead
+        mark_ = std::move(mark);
+        dirty_ = false;
+    }
+
     void releaseDescriptors() noexcept
     {
-        if (descriptors_ != nullptr) {
-            owner_->storage.buffers().release(descriptors_, desc_granted_);
-            descriptors_ = nullptr;
-        }
+        arena_.reset();
+        descriptors_ = nullptr;
     }
 
     EngineKvStatus releaseLeaseLocked() noexcept
@@ -463,10 +556,11 @@ private:
     std::uint16_t tail_token_{0};
     PageHandle cow_src_{};
     std::uint16_t cow_tokens_{0};
-    void* descriptors_{nullptr};
-    std::size_t desc_granted_{0};
+    std::shared_ptr<DescriptorArena> arena_;
+    kimkv_block_desc const* descriptors_{nullptr};
     std::uint32_t desc_count_{0};
-    void* event_{nullptr};
+    std::shared_ptr<CompletionMark> mark_;
+    bool dirty_{false};   // work enqueued after mark_ (or no mark yet)
     HipStatus submission_{HipError::InvalidArgument, 0};
     HipStatus final_{};
     bool finished_{false};
@@ -510,60 +604,134 @@ public:
     TokenReserveResult reserveToken(ReserveTokenRequest const& request) override
     {
         TokenReserveResult result;
-        std::lock_guard<std::mutex> lock(state_->mutex);
-        auto const length = state_->committed_lengths.find(request.request_id);
-        if (request.request_id == kInvalidRequestId) {
-            result.status = {EngineKvError::InvalidArgument};
-            return result;
-        }
-        if (length == state_->committed_lengths.end()) {
-            result.status = {EngineKvError::RequestNotFound};
-            return result;
-        }
-        TokenReservationResult r = state_->manager.reserveToken(request.request_id, request.expected_committed_tokens);
-        if (!r.ok()) {
-            result.status = mapMetadata(r.error);
-            return result;
-        }
-        PageLeaseAcquireResult lease = state_->manager.acquireTokenReservationLease(r.reservation_id);
-        if (!lease.ok()) {
-            static_cast<void>(state_->manager.rollbackTokenReservation(r.reservation_id));
-            result.status = mapMetadata(lease.error);
-            return result;
-        }
-        auto undo = [&](EngineKvStatus s) {
-            static_cast<void>(state_->manager.releasePageLease(lease.lease_id));
-            static_cast<void>(state_->manager.rollbackTokenReservation(r.reservation_id));
-            result.status = s;
-            return std::move(result);
-        };
-        HipKvStorage& st = state_->storage;
-        if (!st.status().ok()) return undo(mapDevice(st.status()));
-        if (!st.validTable(r.before) || !st.validTable(r.reserved) || r.reserved.entries().empty()) {
-            return undo({EngineKvError::InvalidArgument});
-        }
-        if (st.consumeFailure(HipFailurePoint::Submission)) return undo({EngineKvError::SubmissionFailed});
-        std::unique_ptr<HipTokenTransaction> tx;
-        try {
-            tx = std::make_unique<HipTokenTransaction>(state_, r, lease.lease_id, request.stream);
-        } catch (...) {
-            return undo({EngineKvError::ResourceExhausted});
-        }
-        HipStatus const begun = tx->begin(r.reserved);
-        if (!begun.ok()) {
-            tx.reset();   // drains its stream before the metadata is undone
-            return undo(mapDevice(begun));
-        }
-        std::uint64_t const id = state_->next_transaction_id.fetch_add(1, std::memory_order_relaxed);
-        result.transaction = TokenTransaction(std::move(tx), id, r.request_id, r.logical_token_position,
-                                              state_->config.kv_layout.layer_count, request.stream);
-        if (!result.transaction.valid()) {
-            result.status = {EngineKvError::InternalError};
-            return result;
-        }
-        ++state_->active_transactions;
-        result.status = {};
+        reserveBatch(&request, 1, &result);
         return result;
+    }
+
+    // reserveToken for several requests sharing one stream: per-request
+    // metadata (reservation, lease, table checks) exactly as one by one, then
+    // every descriptor table in one arena with a single upload.  A request
+    // that fails keeps its own status and does not affect the others.
+    void reserveBatch(ReserveTokenRequest const* requests, std::size_t count, TokenReserveResult* results)
+    {
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        KvCacheManager& m = state_->manager;
+        HipKvStorage& st = state_->storage;
+        struct Pending {
+            std::size_t index;
+            TokenReservationResult r;
+            PageLeaseId lease;
+            std::unique_ptr<HipTokenTransaction> tx;
+            std::size_t first;
+            std::uint32_t descriptors;
+        };
+        std::vector<Pending> pending;
+        pending.reserve(count);
+        thread_local std::vector<kimkv_block_desc> all;
+        all.clear();
+        HipStream const stream = count != 0 ? requests[0].stream : nullptr;
+        for (std::size_t i = 0; i < count; ++i) {
+            ReserveTokenRequest const& request = requests[i];
+            TokenReserveResult& result = results[i];
+            result = TokenReserveResult{};
+            if (request.request_id == kInvalidRequestId || request.stream != stream) {
+                result.status = {EngineKvError::InvalidArgument};
+                continue;
+            }
+            if (state_->committed_lengths.find(request.request_id) == state_->committed_lengths.end()) {
+                result.status = {EngineKvError::RequestNotFound};
+                continue;
+            }
+            TokenReservationResult r = m.reserveToken(request.request_id, request.expected_committed_tokens);
+            if (!r.ok()) {
+                result.status = mapMetadata(r.error);
+                continue;
+            }
+            PageLeaseAcquireResult lease = m.acquireTokenReservationLease(r.reservation_id);
+            if (!lease.ok()) {
+                static_cast<void>(m.rollbackTokenReservation(r.reservation_id));
+                result.status = mapMetadata(lease.error);
+                continue;
+            }
+            EngineKvStatus refuse{};
+            if (!st.status().ok()) {
+                refuse = mapDevice(st.status());
+            } else if (!st.validTable(r.before) || !st.validTable(r.reserved) || r.reserved.entries().empty()) {
+                refuse = {EngineKvError::InvalidArgument};
+            } else if (st.consumeFailure(HipFailurePoint::Submission)) {
+                refuse = {EngineKvError::SubmissionFailed};
+            }
+            std::unique_ptr<HipTokenTransaction> tx;
+            if (refuse.ok()) {
+                try {
+                    tx = std::make_unique<HipTokenTransaction>(state_, r, lease.lease_id, stream);
+                } catch (...) {
+                    refuse = {EngineKvError::ResourceExhausted};
+                }
+            }
+            if (!refuse.ok()) {
+                static_cast<void>(m.releasePageLease(lease.lease_id));
+                static_cast<void>(m.rollbackTokenReservation(r.reservation_id));
+                result.status = refuse;
+                continue;
+            }
+            std::size_t const first = all.size();
+            for (MappingEntry const& e : r.reserved.entries()) {
+                kimkv_block_desc d{};
+                d.slot = e.handle.slot;
+                d.generation = e.handle.generation;
+                d.logical_token_begin = e.logical_token_begin;
+                d.valid_tokens = e.valid_tokens;
+                d.page_token_capacity = st.pageTokenCapacity(e.kind);
+                d.kind = static_cast<std::uint8_t>(e.kind);
+                all.push_back(d);
+            }
+            auto const n = static_cast<std::uint32_t>(all.size() - first);
+            pending.push_back(Pending{i, std::move(r), lease.lease_id, std::move(tx), first, n});
+        }
+        if (pending.empty()) return;
+        // One arena and one upload for every table of the call.
+        std::size_t const bytes = all.size() * sizeof(kimkv_block_desc);
+        std::size_t granted = 0;
+        void* mem = st.buffers().acquire(bytes, granted);
+        std::shared_ptr<DescriptorArena> arena;
+        EngineKvStatus failure{};
+        if (mem == nullptr) {
+            failure = {EngineKvError::ResourceExhausted};
+        } else {
+            try {
+                arena = std::make_shared<DescriptorArena>(state_, mem, granted);
+            } catch (...) {
+                st.buffers().release(mem, granted);
+                failure = {EngineKvError::ResourceExhausted};
+            }
+        }
+        if (failure.ok()) {
+            std::lock_guard<std::mutex> launch(state_->launch_mutex);
+            bool const staged = st.ring().uploadTo(arena->ptr, all.data(), bytes, stream);
+            st.ring().fence(stream);
+            if (!staged) failure = {EngineKvError::SubmissionFailed};
+        }
+        for (Pending& p : pending) {
+            TokenReserveResult& result = results[p.index];
+            if (failure.ok()) p.tx->attach(arena, p.first, p.descriptors);
+            if (!failure.ok()) {
+                p.tx.reset();   // drains its stream before the metadata is undone
+                static_cast<void>(m.releasePageLease(p.lease));
+                static_cast<void>(m.rollbackTokenReservation(p.r.reservation_id));
+                result.status = failure;
+                continue;
+            }
+            std::uint64_t const id = state_->next_transaction_id.fetch_add(1, std::memory_order_relaxed);
+            result.transaction = TokenTransaction(std::move(p.tx), id, p.r.request_id, p.r.logical_token_position,
+                                                  state_->config.kv_layout.layer_count, stream);
+            if (!result.transaction.valid()) {
+                result.status = {EngineKvError::InternalError};
+                continue;
+            }
+            ++state_->active_transactions;
+            result.status = {};
+        }
     }
 
     EngineKvBackendSnapshot snapshot() const override
@@ -598,58 +766,137 @@ public:
             && state_->active_transactions == state_->manager.snapshot().token_reservation_count;
     }
 
+    // Promotes every run of 8 full sealed micro pages of a committed request.
+    // The manager serialises promotions of one request (a commit is checked
+    // against the table version seen at prepare), so the metadata goes run by
+    // run: prepare, IO lease, release, commit.  The copies are then issued as
+    // one batched launch and waited for, all under the backend lock: this
+    // backend is the only user of its manager, so no source page freed by a
+    // commit can be handed out again before the copy has read it, and no
+    // reader can reserve the request before its extents hold the data.  A
+    // failed copy cancels the request (its table already names the extents).
     EngineKvStatus promote(RequestId request_id, HipStream stream, std::uint32_t* promoted)
     {
-        std::lock_guard<std::mutex> lock(state_->mutex);
         if (promoted) *promoted = 0;
+        std::lock_guard<std::mutex> lock(state_->mutex);
         KvCacheManager& m = state_->manager;
         std::optional<BlockTable> t = m.blockTable(request_id);
         if (!t.has_value()) return {EngineKvError::RequestNotFound};
-        std::vector<PromotionPrepareResult> prepared;
+        std::vector<std::uint32_t> runs;
         auto const& e = t->entries();
         for (std::size_t i = 0; i + kPromotionSourcePageCount <= e.size();) {
             bool run = true;
             for (std::size_t k = 0; k < kPromotionSourcePageCount && run; ++k) {
                 run = e[i + k].kind == PageKind::Micro && e[i + k].valid_tokens == kMicroPageTokenCapacity;
             }
-            if (!run) {
-                ++i;
-                continue;
-            }
-            PromotionPrepareResult p = m.preparePromotion(request_id, e[i].logical_token_begin);
-            if (p.ok()) {
-                prepared.push_back(p);
+            if (run) {
+                runs.push_back(e[i].logical_token_begin);
                 i += kPromotionSourcePageCount;
-            } else if (p.error == KvCacheError::RequestConflict || p.error == KvCacheError::ResourceExhausted) {
-                break;
             } else {
                 ++i;
             }
         }
-        if (prepared.empty()) return {};
-        std::vector<PageLeaseId> leases;
-        for (PromotionPrepareResult const& p : prepared) {
+        std::vector<PromotionPrepareResult> committed;
+        EngineKvStatus status{};
+        for (std::uint32_t begin : runs) {
+            PromotionPrepareResult p = m.preparePromotion(request_id, begin);
+            if (!p.ok()) {
+                if (p.error == KvCacheError::RequestConflict || p.error == KvCacheError::ResourceExhausted) break;
+                continue;   // not eligible (e.g. a shared or still-mutable page): leave the run as micro
+            }
             PageLeaseAcquireResult l = m.acquirePromotionIoLease(p.promotion_id);
-            if (l.ok()) leases.push_back(l.lease_id);
+            if (!l.ok()) {
+                static_cast<void>(m.rollbackPromotion(p.promotion_id));
+                status = mapMetadata(l.error);
+                break;
+            }
+            static_cast<void>(m.releasePageLease(l.lease_id));
+            KvCacheError const c = m.commitPromotion(p.promotion_id);
+            if (c != KvCacheError::None) {
+                status = mapMetadata(c);
+                break;
+            }
+            committed.push_back(p);
         }
-        HipStatus const copied = state_->storage.promoteBatch(prepared, stream);
-        for (PageLeaseId l : leases) static_cast<void>(m.releasePageLease(l));
+        if (committed.empty()) return status;
+        HipStatus const copied = state_->storage.promoteBatch(committed, stream);
         if (!copied.ok()) {
-            for (PromotionPrepareResult const& p : prepared) static_cast<void>(m.rollbackPromotion(p.promotion_id));
+            static_cast<void>(m.releaseRequest(request_id));
+            state_->committed_lengths.erase(request_id);
             return mapDevice(copied);
         }
-        std::uint32_t n = 0;
-        EngineKvStatus status{};
-        for (PromotionPrepareResult const& p : prepared) {
-            KvCacheError const c = m.commitPromotion(p.promotion_id);
-            if (c == KvCacheError::None) {
-                ++n;
-            } else if (status.ok()) {
-                status = mapMetadata(c);
+        if (promoted) *promoted = static_cast<std::uint32_t>(committed.size());
+        return status;
+    }
+
+    // Bulk append of prompt KV ([layer][K/V][token_count][head][dim]) to a
+    // request with no token in flight: one metadata append, one batched
+    // append launch (waited for), then the full tail is sealed and, when
+    // asked, every complete 64-token run is promoted.  A device failure
+    // cancels the request, as HipKvCache::append does.
+    EngineKvStatus appendPrefill(RequestId request_id, std::uint32_t token_count, KvScalar const* device_kv,
+                                 HipStream stream, bool promote_runs, std::uint32_t* promoted)
+    {
+        if (promoted) *promoted = 0;
+        if (request_id == kInvalidRequestId || token_count == 0 || device_kv == nullptr) {
+            return {EngineKvError::InvalidArgument};
+        }
+        PageLeaseAcquireResult before;
+        PageLeaseAcquireResult after;
+        std::uint32_t begin = 0;
+        {
+            std::lock_guard<std::mutex> lock(state_->mutex);
+            if (!state_->storage.status().ok()) return mapDevice(state_->storage.status());
+            auto len = state_->committed_lengths.find(request_id);
+            if (len == state_->committed_lengths.end()) return {EngineKvError::RequestNotFound};
+            KvCacheManager& m = state_->manager;
+            before = m.acquireRequestReadLease(request_id);
+            if (!before.ok()) return mapMetadata(before.error);
+            begin = before.table.tokenCount();
+            KvCacheError const appended = m.append(request_id, token_count);
+            if (appended != KvCacheError::None) {
+                static_cast<void>(m.releasePageLease(before.lease_id));
+                return mapMetadata(appended);
+            }
+            after = m.acquireRequestReadLease(request_id);
+            if (!after.ok()) {
+                static_cast<void>(m.releasePageLease(before.lease_id));
+                static_cast<void>(m.releaseRequest(request_id));
+                state_->committed_lengths.erase(request_id);
+                return mapMetadata(after.error);
             }
         }
-        if (promoted) *promoted = n;
-        return status;
+        HipStatus const device =
+            state_->storage.append(before.table, after.table, begin, token_count, device_kv, stream);
+        {
+            std::lock_guard<std::mutex> lock(state_->mutex);
+            KvCacheManager& m = state_->manager;
+            static_cast<void>(m.releasePageLease(after.lease_id));
+            static_cast<void>(m.releasePageLease(before.lease_id));
+            if (!device.ok()) {
+                static_cast<void>(m.releaseRequest(request_id));
+                state_->committed_lengths.erase(request_id);
+                return mapDevice(device);
+            }
+            auto len = state_->committed_lengths.find(request_id);
+            if (len == state_->committed_lengths.end()) return {EngineKvError::RequestNotFound};
+            len->second += token_count;
+            MappingEntry const& tail = after.table.entries().back();
+            if (tail.valid_tokens == kMicroPageTokenCapacity && tail.kind == PageKind::Micro) {
+                KvCacheError const sealed = m.sealTail(request_id);
+                if (sealed != KvCacheError::None) return mapMetadata(sealed);
+            }
+        }
+        return promote_runs ? promote(request_id, stream, promoted) : EngineKvStatus{};
+    }
+
+    // Shuffles a pool's free list with a seeded permutation (benchmarks: page
+    // ids scattered over the pool).  Only while no request exists.
+    EngineKvStatus permuteFreeSlots(PageKind kind, std::uint64_t seed)
+    {
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        if (!state_->committed_lengths.empty()) return {EngineKvError::InvalidState};
+        return mapMetadata(permuteFreeSlotsOf(state_->manager, kind, seed));
     }
 
     std::shared_ptr<BackendState> const& state() const noexcept { return state_; }
@@ -698,6 +945,31 @@ bool engineBlockTable(EngineKvBackend const& backend, RequestId request_id, Bloc
     if (!t.has_value()) return false;
     out = std::move(*t);
     return true;
+}
+
+EngineKvStatus appendPrefill(EngineKvBackend& backend, RequestId request_id, std::uint32_t token_count,
+                             KvScalar const* device_kv, HipStream stream, bool promote_runs,
+                             std::uint32_t* promoted_pages)
+{
+    auto* b = dynamic_cast<HipEngineKvBackend*>(&backend);
+    if (b == nullptr) return {EngineKvError::InvalidArgument};
+    return b->appendPrefill(request_id, token_count, device_kv, stream, promote_runs, promoted_pages);
+}
+
+bool reserveTokenBatch(EngineKvBackend& backend, ReserveTokenRequest const* requests, std::size_t count,
+                       TokenReserveResult* results)
+{
+    auto* b = dynamic_cast<HipEngineKvBackend*>(&backend);
+    if (b == nullptr) return false;
+    b->reserveBatch(requests, count, results);
+    return true;
+}
+
+EngineKvStatus permuteEngineFreeSlots(EngineKvBackend& backend, PageKind kind, std::uint64_t seed)
+{
+    auto* b = dynamic_cast<HipEngineKvBackend*>(&backend);
+    if (b == nullptr) return {EngineKvError::InvalidArgument};
+    return b->permuteFreeSlots(kind, seed);
 }
 
 void const* engineStorage(EngineKvBackend const& backend) noexcept

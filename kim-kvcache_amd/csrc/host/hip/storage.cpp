@@ -241,11 +241,34 @@ bool HipKvStorage::pageExists(PageHandle h) const noexcept
 bool HipKvStorage::validTable(BlockTable const& table) const
 {
     bool const standard = micro_tokens_ == kMicroPageTokenCapacity && extent_tokens_ == kExtentPageTokenCapacity;
-    bool const structure = standard ? table.checkInvariants()
-                                    : extent_capacity_ == 0 && table.checkInvariants(micro_tokens_);
-    if (!structure) return false;
-    return std::all_of(table.entries().begin(), table.entries().end(),
-                       [this](MappingEntry const& e) { return pageExists(e.handle); });
+    if (!standard) {
+        return extent_capacity_ == 0 && table.checkInvariants(micro_tokens_)
+            && std::all_of(table.entries().begin(), table.entries().end(),
+                           [this](MappingEntry const& e) { return pageExists(e.handle); });
+    }
+    std::uint64_t next = 0;
+    for (MappingEntry const& e : table.entries()) {
+        if (!pageExists(e.handle) || e.kind != e.handle.kind) return false;
+        std::uint16_t const cap = pageTokenCapacity(e.kind);
+        if (e.valid_tokens == 0 || e.valid_tokens > cap || e.logical_token_begin != next) return false;
+        next += e.valid_tokens;
+        if (next > 0xFFFFFFFFull) return false;
+    }
+    // No page twice: stamp each slot with this call's number.
+    std::lock_guard<std::mutex> lock(stamp_mutex_);
+    if (micro_stamp_.size() != micro_capacity_) micro_stamp_.assign(micro_capacity_, 0);
+    if (extent_stamp_.size() != extent_capacity_) extent_stamp_.assign(extent_capacity_, 0);
+    if (++stamp_ == 0) {
+        std::fill(micro_stamp_.begin(), micro_stamp_.end(), 0);
+        std::fill(extent_stamp_.begin(), extent_stamp_.end(), 0);
+        stamp_ = 1;
+    }
+    for (MappingEntry const& e : table.entries()) {
+        std::uint32_t& seen = (e.kind == PageKind::Micro ? micro_stamp_ : extent_stamp_)[e.handle.slot];
+        if (seen == stamp_) return false;
+        seen = stamp_;
+    }
+    return true;
 }
 
 void HipKvStorage::descriptors(BlockTable const& table, std::vector<kimkv_block_desc>& out) const

@@ -107,7 +107,10 @@ public:
     }
     [[nodiscard]] bool pageExists(PageHandle handle) const noexcept;
     // Structure (standard or uniform capacities) plus every page in range
-    // (CudaKvStorage::Impl::validTable, src/cuda/kv/storage.cpp:79-97).
+    // (CudaKvStorage::Impl::validTable, src/cuda/kv/storage.cpp:79-97).  For
+    // the standard 8/64 layout the distinct-page check is a stamp per pool
+    // slot, linear in the entry count (a reserve at 32k tokens checks ~514
+    // entries twice per lane per token).
     [[nodiscard]] bool validTable(BlockTable const& table) const;
     void descriptors(BlockTable const& table, std::vector<kimkv_block_desc>& out) const;
 
@@ -140,6 +143,11 @@ private:
     HipStatus status_{};
     StagingRing ring_;
     DeviceBufferCache buffers_;
+    // Per-slot visit stamps for the O(entries) duplicate-page check.
+    mutable std::mutex stamp_mutex_;
+    mutable std::vector<std::uint32_t> micro_stamp_;
+    mutable std::vector<std::uint32_t> extent_stamp_;
+    mutable std::uint32_t stamp_{0};
     std::mutex fault_mutex_;
     bool fail_submission_once_{false};
     bool fail_completion_once_{false};

@@ -121,6 +121,8 @@ _SIGNATURES = {
     "kimkv_synth_kv_row": (ctypes.c_uint64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
     "kimkv_fill_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
                                        ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_fill_kv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                     ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]),
     "kimkv_fill_table": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                         ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_void_p]),
 }
@@ -263,6 +265,13 @@ def fill_rows(ptr: int, count: int, seed: int, row0: int, cols: int, stream: Opt
     check(lib().kimkv_fill_rows(ctypes.c_void_p(ptr), count, seed, row0, cols, _sh(stream)), "fill_rows")
 
 
+def fill_kv(ptr: int, layers: int, tokens: int, cols: int, seed: int, stream_id: int, token0: int,
+            stream: Optional[Stream] = None) -> None:
+    """Synthetic [layers][2][tokens][cols] K/V block (rows synth_kv_row(stream_id, l, c, token0 + t))."""
+    check(lib().kimkv_fill_kv(ctypes.c_void_p(ptr), layers, tokens, cols, seed, stream_id, token0, _sh(stream)),
+          "fill_kv")
+
+
 class Storage:
     """Device page pools (kimkv_storage)."""
 
@@ -320,14 +329,7 @@ class Storage:
                                      stream_id, _sh(stream)), "fill_table")
 
     def decode_plan(self, token_counts, query_heads: int):
-        counts = np.ascontiguousarray(np.asarray(token_counts, dtype=np.uint32))
-        prefix = np.zeros(len(counts) + 1, dtype=np.uint32)
-        chunk = ctypes.c_uint32()
-        total = ctypes.c_uint32()
-        check(lib().kimkv_decode_plan(self.h, counts.ctypes.data_as(ctypes.c_void_p), len(counts), query_heads,
-                                      ctypes.byref(chunk), prefix.ctypes.data_as(ctypes.c_void_p),
-                                      ctypes.byref(total)), "decode_plan")
-        return int(chunk.value), prefix, int(total.value)
+        return decode_plan(self.handle, token_counts, query_heads)
 
     def decode_launch(self, items_ptr: int, prefix_ptr: int, lanes: int, total_chunks: int, chunk_tokens: int,
                       query_heads: int, stream: Optional[Stream] = None) -> None:
@@ -345,6 +347,18 @@ class Storage:
             self.destroy()
         except Exception:
             pass
+
+
+def decode_plan(storage_handle: int, token_counts, query_heads: int):
+    """kimkv_decode_plan: (chunk_tokens, chunk prefix over lanes, total chunks)."""
+    counts = np.ascontiguousarray(np.asarray(token_counts, dtype=np.uint32))
+    prefix = np.zeros(len(counts) + 1, dtype=np.uint32)
+    chunk = ctypes.c_uint32()
+    total = ctypes.c_uint32()
+    check(lib().kimkv_decode_plan(ctypes.c_void_p(storage_handle), counts.ctypes.data_as(ctypes.c_void_p),
+                                  len(counts), query_heads, ctypes.byref(chunk),
+                                  prefix.ctypes.data_as(ctypes.c_void_p), ctypes.byref(total)), "decode_plan")
+    return int(chunk.value), prefix, int(total.value)
 
 
 def workspace_bytes(token_count: int, chunk_tokens: int, query_heads: int, head_dim: int) -> int:

@@ -89,13 +89,18 @@ _SIG = {
     "kimkv_engine_promote_request": (I, [P, U64, P, ctypes.POINTER(U32)]),
     "kimkv_engine_block_table": (I, [P, U64, ctypes.POINTER(U64), P, U32, ctypes.POINTER(U32)]),
     "kimkv_engine_storage": (P, [P]),
+    "kimkv_engine_append_prefill": (I, [P, U64, U32, P, P, I, ctypes.POINTER(U32)]),
+    "kimkv_engine_permute_free_slots": (I, [P, U32, U64]),
+    "kimkv_engine_reserve_batch": (None, [P, P, P, U32, P, P, P]),
+    "kimkv_txn_commit_batch": (None, [P, U32, P]),
     "kimkv_txn_write_layer": (I, [P, U32, P, P]),
     "kimkv_txn_attend_layer": (I, [P, ctypes.POINTER(DecodeRequest)]),
     "kimkv_txn_commit": (I, [P]),
     "kimkv_txn_rollback": (I, [P]),
     "kimkv_txn_state": (None, [P, ctypes.POINTER(U32), ctypes.POINTER(U32), ctypes.POINTER(U32)]),
     "kimkv_txn_destroy": (None, [P]),
-    "kimkv_attend_layer_batch": (None, [ctypes.POINTER(P), ctypes.POINTER(DecodeRequest), U32, ctypes.POINTER(I)]),
+    "kimkv_attend_layer_batch": (None, [ctypes.POINTER(P), ctypes.POINTER(DecodeRequest), U32, P, U32,
+                                        ctypes.POINTER(I)]),
     "kimkv_write_layer_batch": (None, [ctypes.POINTER(P), ctypes.POINTER(U32), ctypes.POINTER(P), ctypes.POINTER(P),
                                        U32, ctypes.POINTER(I)]),
     "kimkv_cache_create": (P, [device.Layout, U32, U32]),
@@ -199,12 +204,21 @@ class Transaction:
             pass
 
 
-def attend_layer_batch(txns: Sequence[Transaction], requests: Sequence[tuple]) -> List[int]:
+DECODE_ITEM_BYTES = 56   # kimkv_decode_item / DevicePagedDecodeBatchItem
+
+
+def attend_layer_batch(txns: Sequence[Transaction], requests: Sequence[tuple],
+                       device_items: Optional[device.DeviceBuffer] = None) -> List[int]:
+    """requests[i] = (layer, query, output, workspace, workspace_bytes, scale).
+    device_items: caller-owned scratch of >= len(txns) items (allocated here when omitted)."""
     n = len(txns)
     hs = (P * n)(*[t.h for t in txns])
     rs = (DecodeRequest * n)(*[DecodeRequest(r[0], 0, *r[1:]) for r in requests])
     st = (I * n)()
-    lib().kimkv_attend_layer_batch(hs, rs, n, st)
+    scratch = device_items if device_items is not None else device.DeviceBuffer(n * DECODE_ITEM_BYTES)
+    lib().kimkv_attend_layer_batch(hs, rs, n, scratch.ptr, scratch.nbytes // DECODE_ITEM_BYTES, st)
+    if device_items is None:
+        device.sync()
     return list(st)
 
 
@@ -245,6 +259,16 @@ class Engine:
         s = EngineSnapshot()
         lib().kimkv_engine_get_snapshot(self.h, ctypes.byref(s))
         return s
+
+    def append_prefill(self, rid, token_count, device_kv, stream: Optional[device.Stream] = None, promote=True):
+        n = U32()
+        rc = lib().kimkv_engine_append_prefill(self.h, rid, token_count, device_kv,
+                                               stream.handle if stream else None, 1 if promote else 0,
+                                               ctypes.byref(n))
+        return rc, n.value
+
+    def permute_free_slots(self, kind: int, seed: int) -> int:
+        return lib().kimkv_engine_permute_free_slots(self.h, kind, seed)
 
     def check_invariants(self) -> bool:
         return lib().kimkv_engine_check_invariants(self.h) == 1
@@ -336,3 +360,85 @@ class Cache:
             self.close()
         except Exception:
             pass
+
+
+DECODE_REQUEST_DTYPE = None
+
+
+def _request_dtype():
+    import numpy as np
+    global DECODE_REQUEST_DTYPE
+    if DECODE_REQUEST_DTYPE is None:
+        DECODE_REQUEST_DTYPE = np.dtype({
+            "names": ["layer", "reserved", "query", "output", "workspace", "workspace_bytes", "attention_scale"],
+            "formats": ["<u4", "<u4", "<u8", "<u8", "<u8", "<u8", "<f4"],
+            "offsets": [0, 4, 8, 16, 24, 32, 40], "itemsize": ctypes.sizeof(DecodeRequest)})
+    return DECODE_REQUEST_DTYPE
+
+
+class LaneBatch:
+    """Prebuilt argument arrays for driving the lanes through
+    reserve -> per layer (writeLayerBatch, attendLayerBatch) -> commit with a
+    constant number of FFI crossings per step.  keys/values/queries/outputs
+    are [layers][lanes] device addresses (numpy views, updatable in place);
+    the caller owns the buffers."""
+
+    def __init__(self, engine: Engine, request_ids, workspaces, workspace_bytes: int, scale: float,
+                 stream: Optional[device.Stream] = None):
+        import numpy as np
+        n = len(request_ids)
+        L = engine.layers
+        self.engine, self.n, self.L = engine, n, L
+        self.stream = stream.handle if stream else None
+        self.ids = np.ascontiguousarray(request_ids, dtype=np.uint64)
+        self.expected = np.zeros(n, dtype=np.uint32)
+        self.txns = np.zeros(n, dtype=np.uint64)
+        self.status = np.zeros(n, dtype=np.int32)
+        self.keys = np.zeros((L, n), dtype=np.uint64)
+        self.values = np.zeros((L, n), dtype=np.uint64)
+        self.layer_ids = np.repeat(np.arange(L, dtype=np.uint32)[:, None], n, axis=1)
+        self._req = (DecodeRequest * (L * n))()
+        self.requests = np.frombuffer(self._req, dtype=_request_dtype()).reshape(L, n)
+        self.requests["layer"] = np.arange(L, dtype=np.uint32)[:, None]
+        self.requests["workspace"] = np.asarray(workspaces, dtype=np.uint64)[None, :]
+        self.requests["workspace_bytes"] = workspace_bytes
+        self.requests["attention_scale"] = scale
+        self._req_base = ctypes.addressof(self._req)
+        self._req_stride = n * ctypes.sizeof(DecodeRequest)
+        self.device_items = device.DeviceBuffer(n * DECODE_ITEM_BYTES)
+
+    @property
+    def queries(self):
+        return self.requests["query"]
+
+    @property
+    def outputs(self):
+        return self.requests["output"]
+
+    @staticmethod
+    def _p(a):
+        return a.ctypes.data_as(ctypes.c_void_p)
+
+    def reserve(self, expected) -> None:
+        self.expected[:] = expected
+        lib().kimkv_engine_reserve_batch(self.engine.h, self._p(self.ids), self._p(self.expected), self.n,
+                                         self.stream, self._p(self.txns), self._p(self.status))
+
+    def write(self, layer: int) -> None:
+        lib().kimkv_write_layer_batch(ctypes.cast(self._p(self.txns), ctypes.POINTER(P)),
+                                      ctypes.cast(self._p(self.layer_ids[layer]), ctypes.POINTER(U32)),
+                                      ctypes.cast(self._p(self.keys[layer]), ctypes.POINTER(P)),
+                                      ctypes.cast(self._p(self.values[layer]), ctypes.POINTER(P)),
+                                      self.n, ctypes.cast(self._p(self.status), ctypes.POINTER(I)))
+
+    def attend(self, layer: int) -> None:
+        reqs = ctypes.cast(ctypes.c_void_p(self._req_base + layer * self._req_stride), ctypes.POINTER(DecodeRequest))
+        lib().kimkv_attend_layer_batch(ctypes.cast(self._p(self.txns), ctypes.POINTER(P)), reqs, self.n,
+                                       self.device_items.ptr, self.n,
+                                       ctypes.cast(self._p(self.status), ctypes.POINTER(I)))
+
+    def commit(self) -> None:
+        lib().kimkv_txn_commit_batch(self._p(self.txns), self.n, self._p(self.status))
+
+    def failed(self) -> bool:
+        return bool(self.status.any())

@@ -4,6 +4,7 @@ injection, engine promotion) and the HipKvCache facade.  Scenarios mirror the
 reference's tests/cuda/cuda_engine_kv_backend_test.cpp and
 tests/cuda/cuda_kv_test.cpp; every data check is against closed forms or the
 oracle."""
+import ctypes
 import math
 
 import numpy as np
@@ -410,4 +411,56 @@ def test_cache_fault_rollback(host, dev):
     assert np.array_equal(_gather(dev, cache, 20, 64, stream), make_kv_closed_form(*LAYOUT, 0, 64).reshape(-1))
     assert cache.release_request(20) == 0
     del a
+    stream.destroy()
+
+
+def test_engine_prefill_promotion_then_decode(host, dev):
+    """Bulk prefill through the engine (append + seal + promotion), then gather
+    is bit-exact against the input and one decode token matches the oracle."""
+    L, H, D, QH = 3, 2, 64, 8
+    T = 200                                   # 3 extents + one full micro page
+    engine = host.Engine(L, H, D, QH, 1 << 16, 64, 8)
+    assert engine.permute_free_slots(1, 11) == 0 and engine.permute_free_slots(0, 12) == 0
+    assert engine.create_request(5) == 0
+    rng = np.random.default_rng(3)
+    kv = f16(*rng.uniform(-1, 1, L * 2 * T * H * D)).reshape(L, 2, T, H, D)
+    stream = dev.Stream()
+    src = dev.upload(kv.reshape(-1), stream)
+    rc, promoted = engine.append_prefill(5, T, src.ptr, stream, promote=True)
+    assert rc == 0 and promoted == 3
+    _, entries = engine.block_table(5)
+    assert [e[2] for e in entries] == [1, 1, 1, 0] and entries[-1][1] == 8
+    assert engine.snapshot().committed_token_count == T
+    assert engine.check_invariants()
+
+    descs = host.descriptors_from_entries(entries)
+    d = dev.upload(descs, stream)
+    out = dev.DeviceBuffer(kv.nbytes)
+    dev.check(dev.lib().kimkv_gather(ctypes.c_void_p(engine.storage_handle()), ctypes.c_void_p(d.ptr), len(descs), T,
+                                     ctypes.c_void_p(out.ptr), ctypes.c_void_p(stream.handle)), "gather")
+    got = dev.download(out.ptr, kv.shape, np.uint16, stream)
+    assert np.array_equal(got, kv)
+
+    buf = Buffers(dev, layers=L, kv=H, qh=QH, dim=D, workspace=1 << 16)
+    rc, txn = engine.reserve_token(5, T, stream)
+    assert rc == 0
+    new = [(f16(*rng.uniform(-1, 1, H * D)), f16(*rng.uniform(-1, 1, H * D))) for _ in range(L)]
+    q = f16(*rng.uniform(-1, 1, QH * D))
+    dev.copy_to_device(buf.query.ptr, q, stream)
+    scale = 1.0 / math.sqrt(D)
+    for layer in range(L):
+        dev.copy_to_device(buf.keys[layer].ptr, new[layer][0], stream)
+        dev.copy_to_device(buf.values[layer].ptr, new[layer][1], stream)
+        assert txn.write_layer(layer, buf.keys[layer].ptr, buf.values[layer].ptr) == 0
+        assert txn.attend_layer(layer, buf.query.ptr, buf.output.ptr, buf.workspace.ptr, buf.workspace_bytes,
+                                scale) == 0
+    assert txn.commit() == 0
+    hist = [[(kv[l, 0, t].reshape(-1), kv[l, 1, t].reshape(-1)) for l in range(L)] for t in range(T)]
+    want = _oracle_lane(hist + [new], L - 1, q, QH, H, D, scale)
+    got = to_f32(dev.download(buf.output.ptr, (QH * D,), np.uint16))
+    assert np.all(np.abs(got - want) <= 2e-3 + 1e-3 * np.abs(want))
+    _, entries = engine.block_table(5)
+    assert [e[2] for e in entries] == [1, 1, 1, 0, 0] and entries[-1][1] == 1   # new tail after the sealed page
+    assert engine.release_request(5) == 0
+    assert engine.check_invariants()
     stream.destroy()

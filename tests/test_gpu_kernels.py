@@ -223,3 +223,16 @@ def test_decode_unaligned_pages_generic(dev):
     # 6-token pages: tables not 8-aligned take the generic path.
     _decode_case(dev, (2, 4, 64), [17, 200, 3000], G=8, micro_tokens=6, extent_tokens=48, seed=12,
                  uniform_pages=True)
+
+
+def test_fill_kv_block_matches_oracle(dev):
+    """kimkv_fill_kv: [L][2][T][cols] block with rows synth_kv_row(stream, l, c, token0 + t)."""
+    L, T, cols, seed, sid, t0 = 3, 37, 96, 99, 5, 1000
+    buf = dev.DeviceBuffer(L * 2 * T * cols * 2)
+    dev.fill_kv(buf.ptr, L, T, cols, seed, sid, t0)
+    dev.sync()
+    got = dev.download(buf.ptr, (L, 2, T, cols), np.uint16)
+    for l in range(L):
+        for c in range(2):
+            want = oracle.synth_rows(T * cols, seed, oracle.kv_row(sid, l, c, t0), cols).reshape(T, cols)
+            assert np.array_equal(got[l, c], want)
