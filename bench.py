@@ -471,12 +471,12 @@ def run_copy(dev, args) -> int:
     return 0
 
 
-def profiled_traffic(lanes: int, context: int, layers: int):
+def profiled_traffic(lanes_per_launch: int, context: int, layers: int):
     """HBM bytes per decode launch from the committed rocprofv3 PMC summary
     (FETCH_SIZE and WRITE_SIZE per dispatch, each times its copy-calibrated
-    factor), for the default workload that summary was measured on."""
+    factor), when the summary was measured on this launch shape."""
     path = os.path.join(ROOT, "profiles", "decode_kernel_hbm_scale.md")
-    if (lanes, context, layers) != (256, 32768, 22) or not os.path.exists(path):
+    if not os.path.exists(path):
         return None
     vals = {}
     for line in open(path):
@@ -487,6 +487,9 @@ def profiled_traffic(lanes: int, context: int, layers: int):
             except ValueError:
                 pass
     try:
+        if (int(vals["lanes_per_launch"]), int(vals["context"]), int(vals["layers"])) != (
+                lanes_per_launch, context, layers):
+            return None
         return int(vals["fetch_size_kib_per_dispatch"] * 1024 * vals["fetch_factor"]
                    + vals["write_size_kib_per_dispatch"] * 1024 * vals["write_factor"])
     except KeyError:
@@ -581,6 +584,7 @@ def main() -> int:
         append_bytes += args.layers * args.lanes * 2 * tok_bytes     # read new K/V + write page
     step_bytes = (decode_bytes + append_bytes) / args.steps
     value_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    lanes_per_launch = w.groups[0][0].n if args.path == "engine" else args.lanes
     # One decode launch per layer per lane group: bytes and time per launch.
     per_launch_decode_bytes = decode_bytes / max(decode_launches, 1)
     decode_avg_ms = decode_ms_total / max(decode_launches, 1)
@@ -633,8 +637,9 @@ def main() -> int:
                    "lane_groups": args.groups if args.path == "engine" else 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": profiled_traffic(args.lanes, args.context, args.layers),
+                     "traffic": profiled_traffic(lanes_per_launch, args.context, args.layers),
                      "kernel": "decode_kernel", "avg_launch_ms": round(decode_avg_ms, 4),
+                     "lanes_per_launch": lanes_per_launch,
                      "bytes_per_launch": int(per_launch_decode_bytes)},
         "cpu_baseline": cpu,
         "check": check,
