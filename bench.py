@@ -226,7 +226,7 @@ class EngineWorkload:
         n_ext = lanes * self.ext_per_lane
         n_micro = 512 // 8 + 8 + lanes * ((total_steps + 7) // 8 + 1)
         T_max = context + total_steps
-        self.ws_lane = max(dev.workspace_bytes(T_max, 256, query_heads, head_dim), 256)
+        self.ws_lane = max(dev.workspace_bytes(T_max, 64, query_heads, head_dim), 256)
         t0 = time.time()
         self.engine = host.Engine(layers, kv_heads, head_dim, query_heads, self.ws_lane, n_micro, n_ext)
         snap = self.engine.snapshot()
@@ -442,6 +442,273 @@ def run_gather(dev, args) -> int:
     return 0 if bad == 0 else 1
 
 
+def run_append(kimkv, dev, args) -> int:
+    """Ragged append: 64 lanes with contexts uniform in [1, 4096] tokens (seeded),
+    22 layers x 4 kv heads x 64 fp16, micro/extent pages in permuted pool order
+    (contexts built by bulk append + promotion of every full 64-token run).
+    One step appends one token of K/V per lane per layer into the page tails,
+    tail-page allocation (and its metadata) included: HipKvCache::appendBatch,
+    i.e. per lane metadata append + leases, then one append kernel for all
+    lanes and layers, waited for."""
+    import importlib
+    import oracle
+    host = importlib.import_module(kimkv.__name__ + ".host")
+    L, H, D = args.layers, 4, 64
+    HD = H * D
+    lanes = args.append_lanes
+    rng = np.random.default_rng(args.seed)
+    lengths = rng.integers(1, 4097, lanes)
+    total_steps = args.warmup + args.steps
+    n_ext = int(sum(lengths // 64)) + 16
+    n_micro = 512 + lanes * (8 + total_steps // 8 + 2)
+    cache = host.Cache(L, H, D, n_micro, n_ext)
+    for kind, sd in ((1, args.seed), (0, args.seed + 1)):
+        rc = cache.permute_free_slots(kind, sd)
+        assert rc == 0, rc
+    stream = dev.Stream()
+    stage = dev.DeviceBuffer(L * 2 * 4096 * HD * 2)
+    t0 = time.time()
+    for i in range(lanes):
+        assert cache.create_request(i + 1) == 0
+        n = int(lengths[i])
+        dev.fill_kv(stage.ptr, L, n, HD, args.seed, i, 0, stream)
+        r = cache.append(i + 1, n, stage.ptr, stream)
+        assert r.ok(), (r.metadata_error, r.device_status)
+        for b in range(0, n - n % 64, 64):
+            r = cache.promote(i + 1, b, stream)
+            assert r.ok(), (i, b, r.metadata_error, r.device_status)
+    log(f"built {lanes} contexts ({int(lengths.sum())} tokens) in {time.time() - t0:.1f}s")
+    # New token per (lane, step): [L][2][1][HD] blocks, rows kv_row(lane, l, c, length + step).
+    per = L * 2 * HD
+    newkv = dev.DeviceBuffer(lanes * total_steps * per * 2)
+    for i in range(lanes):
+        for s_ in range(total_steps):
+            dev.fill_kv(newkv.ptr + 2 * (i * total_steps + s_) * per, L, 1, HD, args.seed, i,
+                        int(lengths[i]) + s_, stream)
+    stream.synchronize()
+    ids = np.arange(1, lanes + 1, dtype=np.uint64)
+    results = (host.CacheResult * lanes)()
+    lane = np.arange(lanes, dtype=np.uint64)
+
+    def step(s_):
+        inputs = newkv.ptr + np.uint64(2 * per) * (lane * np.uint64(total_steps) + np.uint64(s_))
+        cache.append_batch(ids, 1, inputs, results, stream)
+        bad = [k for k in range(lanes) if not results[k].ok()]
+        if bad:
+            raise RuntimeError(f"append failed for lanes {bad[:4]}: {results[bad[0]].metadata_error}, "
+                               f"{results[bad[0]].device_status}")
+
+    for s_ in range(args.warmup):
+        step(s_)
+    start, stop = dev.Event(), dev.Event()
+    walls = []
+    start.record(stream)
+    for s_ in range(args.warmup, total_steps):
+        t = time.perf_counter()
+        step(s_)
+        walls.append(time.perf_counter() - t)
+    stop.record(stream)
+    stop.synchronize()
+    gpu_ms = start.elapsed_ms(stop)
+    wall_us = 1e6 * sum(walls) / len(walls)
+    step_bytes = lanes * L * 2 * (2 * HD * 2)          # read new K/V + write into the page
+    # Bit-exact check: gather sampled lanes and compare with the generator.
+    bad = 0
+    checked = 0
+    for i in rng.choice(lanes, size=min(args.append_check, lanes), replace=False):
+        T = int(lengths[i]) + total_steps
+        out = dev.DeviceBuffer(L * 2 * T * HD * 2)
+        r = cache.gather(int(i) + 1, out.ptr, stream)
+        assert r.ok()
+        got = dev.download(out.ptr, (L, 2, T, HD), np.uint16, stream)
+        for l in range(L):
+            for c in range(2):
+                want = oracle.synth_rows(T * HD, args.seed, oracle.kv_row(int(i), l, c, 0), HD).reshape(T, HD)
+                bad += int(not np.array_equal(got[l, c], want))
+        checked += 1
+    print(json.dumps({
+        "metric": "ragged KV append (1 token x 22 layers per lane, tail allocation included) us/step",
+        "value": round(wall_us, 2), "unit": "us/step", "higher_is_better": False,
+        "gb_per_s": round(step_bytes / (wall_us * 1e-6) / 1e9, 2), "bytes_per_step": step_bytes,
+        "gpu_span_us_per_step": round(1000 * gpu_ms / args.steps, 2),
+        "config": {"workload": f"{lanes} lanes, contexts uniform in [1, 4096] tokens, {L} layers x 4 kv heads x 64 "
+                               f"fp16, micro/extent pages in permuted pool order",
+                   "tokens": int(lengths.sum())},
+        "steps": args.steps, "warmup": args.warmup,
+        "check": {"lanes": checked, "mismatched_rows_blocks": bad, "bit_exact": bad == 0}}), flush=True)
+    return 0 if bad == 0 else 1
+
+
+def oracle_decode_layer(kv_layer, T, q, QH, D):
+    """fp32-accumulated GQA decode of one layer (kv_layer: uint16 [2][T][H][D]) by the oracle, with the
+    tokens held in 8-token pages (the page structure does not change the result)."""
+    import oracle
+    H = kv_layer.shape[2]
+    n_pages = (T + 7) // 8
+    pools = oracle.HostPools(1, H, D, n_pages, 1)
+    kv = kv_layer.reshape(1, 2, T, H, D)
+    table = np.zeros(n_pages, dtype=oracle.DESC)
+    for k in range(n_pages):
+        b = 8 * k
+        n = min(8, T - b)
+        table[k] = (k, 1, b, n, 8, 0)
+        pools.append_tokens(kv, T, b, 0, k, 0, n)
+    return pools.paged_decode(table, T, 0, QH, q, 1.0 / math.sqrt(D), f32=True)
+
+
+def run_shared(kimkv, dev, args) -> int:
+    """Batched paged decode with sharing: 32 lanes in 8 groups of 4, context
+    lengths log-uniform in [128, 8192] (seeded).  Each group's root holds a
+    2048 + r token prefix (r in 1..7, so the prefix ends in a partial micro
+    page), the 4 lanes fork it, and each lane's first own token copies that
+    partial page (copy-on-write) before the lanes diverge; lengths below the
+    prefix are raised to prefix + 8.  Contexts are built through the engine
+    (bulk prefill + promotion); one step = reserve 32 tokens, 22 x
+    (writeLayerBatch + attendLayerBatch), commit."""
+    import importlib
+    host = importlib.import_module(kimkv.__name__ + ".host")
+    L, H, D, QH = args.layers, 4, 64, 32
+    HD, QD = H * D, QH * D
+    groups, per_group = 8, 4
+    lanes = groups * per_group
+    rng = np.random.default_rng(args.seed)
+    r = rng.integers(1, 8, groups)
+    prefix = 2048 + r
+    lengths = np.exp(rng.uniform(np.log(128), np.log(8192), lanes)).astype(np.int64)
+    for g in range(groups):
+        sl = slice(g * per_group, (g + 1) * per_group)
+        lengths[sl] = np.maximum(lengths[sl], prefix[g] + 8)
+    total_steps = args.warmup + args.steps
+    n_ext = int(sum(lengths // 64)) + groups * 2 + 16
+    n_micro = 1024 + lanes * (8 + total_steps // 8 + 2)
+    ws_lane = max(dev.workspace_bytes(int(lengths.max()) + total_steps, 64, QH, D), 256)
+    engine = host.Engine(L, H, D, QH, ws_lane, n_micro, n_ext)
+    for kind, sd in ((1, args.seed), (0, args.seed + 1)):
+        assert engine.permute_free_slots(kind, sd) == 0
+    stream = dev.Stream()
+    stage = dev.DeviceBuffer(L * 2 * int(lengths.max()) * HD * 2)
+    root_sid = 200
+    t0 = time.time()
+    for g in range(groups):
+        root = 10_000 + g
+        assert engine.create_request(root) == 0
+        P = int(prefix[g])
+        dev.fill_kv(stage.ptr, L, P, HD, args.seed, root_sid + g, 0, stream)
+        rc, _ = engine.append_prefill(root, P, stage.ptr, stream, promote=True)
+        assert rc == 0, host.ENGINE_ERRORS[rc]
+        for j in range(per_group):
+            lane = g * per_group + j
+            assert engine.fork_request(root, lane + 1) == 0
+            n = int(lengths[lane]) - P
+            dev.fill_kv(stage.ptr, L, n, HD, args.seed, lane, P, stream)
+            rc, _ = engine.append_prefill(lane + 1, n, stage.ptr, stream, promote=True)
+            assert rc == 0, host.ENGINE_ERRORS[rc]
+        assert engine.release_request(root) == 0
+    assert engine.check_invariants()
+    log(f"built {lanes} shared contexts ({int(lengths.sum())} tokens) in {time.time() - t0:.1f}s")
+    # Unique physical pages vs logical tokens (per layer).
+    logical = int(lengths.sum())
+    unique = {}
+    for lane in range(lanes):
+        _, entries = engine.block_table(lane + 1)
+        for (b, v, k, slot, gen) in entries:
+            unique[(k, slot)] = v
+    physical = sum(unique.values())
+    # Per-step inputs: new K/V rows kv_row(lane, l, c, length + step), queries.
+    S = total_steps
+    newkv = dev.DeviceBuffer(lanes * L * 2 * S * HD * 2)
+    query = dev.DeviceBuffer(lanes * L * S * QD * 2)
+    qseed = args.seed ^ 0x5155455259
+    for i in range(lanes):
+        for l in range(L):
+            for c in range(2):
+                off = (((i * L + l) * 2 + c) * S) * HD
+                dev.fill_rows(newkv.ptr + 2 * off, S * HD, args.seed, dev.synth_kv_row(i, l, c, int(lengths[i])), HD)
+            qoff = ((i * L + l) * S) * QD
+            dev.fill_rows(query.ptr + 2 * qoff, S * QD, qseed, dev.synth_kv_row(i, l, 0, int(lengths[i])), QD)
+    out = dev.DeviceBuffer(L * lanes * QD * 2)
+    ws = dev.DeviceBuffer(ws_lane * lanes)
+    lane_ix = np.arange(lanes, dtype=np.uint64)
+    batch = host.LaneBatch(engine, lane_ix + np.uint64(1), ws.ptr + lane_ix * np.uint64(ws_lane), ws_lane,
+                           1.0 / math.sqrt(D), stream)
+    lay = np.arange(L, dtype=np.uint64)[:, None]
+    kbase = newkv.ptr + np.uint64(2 * HD) * ((lane_ix[None, :] * np.uint64(L) + lay) * np.uint64(2 * S))
+    vbase = kbase + np.uint64(2 * HD * S)
+    qbase = query.ptr + np.uint64(2 * QD) * ((lane_ix[None, :] * np.uint64(L) + lay) * np.uint64(S))
+    batch.outputs[:] = out.ptr + np.uint64(2 * QD) * (lay * np.uint64(lanes) + lane_ix[None, :])
+    stream.synchronize()
+
+    def step(s_):
+        batch.keys[:] = kbase + np.uint64(2 * HD * s_)
+        batch.values[:] = vbase + np.uint64(2 * HD * s_)
+        batch.queries[:] = qbase + np.uint64(2 * QD * s_)
+        batch.expected[:] = lengths + s_
+        batch.reserve(lengths + s_)
+        assert not batch.failed(), batch.status
+        for l in range(L):
+            batch.write(l)
+            assert not batch.failed(), batch.status
+            batch.attend(l)
+            assert not batch.failed(), batch.status
+        batch.commit()
+        assert not batch.failed(), batch.status
+
+    for s_ in range(args.warmup):
+        step(s_)
+    stream.synchronize()
+    start, stop = dev.Event(), dev.Event()
+    dev.decode_timing(True)
+    t_wall = time.perf_counter()
+    start.record(stream)
+    for s_ in range(args.warmup, total_steps):
+        step(s_)
+    stop.record(stream)
+    stop.synchronize()
+    wall_ms = (time.perf_counter() - t_wall) * 1000.0
+    dec_ms, dec_n = dev.decode_timing(False)
+    ms_per_step = max(start.elapsed_ms(stop), wall_ms) / args.steps
+    us_per_layer = ms_per_step * 1000.0 / L
+    appended = args.warmup + (args.steps + 1) / 2.0          # mean tokens appended by the timed steps
+    logical_bytes = (lengths.sum() + lanes * appended) * 2 * HD * 2
+    physical_bytes = (physical + lanes * appended) * 2 * HD * 2
+    # Check: last step, layer 0, sampled lanes against the oracle.
+    last = total_steps - 1
+    got = dev.download(out.ptr, (lanes, QD), np.uint16)
+    worst, ok = 0.0, True
+    import oracle
+    for i in rng.choice(lanes, size=min(args.shared_check, lanes), replace=False):
+        i = int(i)
+        g = i // per_group
+        P = int(prefix[g])
+        T = int(lengths[i]) + last + 1
+        kv = np.empty((2, T, H, D), dtype=np.uint16)
+        for c in range(2):
+            kv[c, :P] = oracle.synth_rows(P * HD, args.seed, oracle.kv_row(root_sid + g, 0, c, 0), HD).reshape(P, H, D)
+            n = T - P
+            kv[c, P:] = oracle.synth_rows(n * HD, args.seed, oracle.kv_row(i, 0, c, P), HD).reshape(n, H, D)
+        q = oracle.synth_rows(QD, qseed, oracle.kv_row(i, 0, 0, int(lengths[i])) + last, QD)
+        ref = oracle_decode_layer(kv, T, q, QH, D)
+        a = got[i].view(np.float16).astype(np.float32)
+        err = np.abs(a - ref)
+        worst = max(worst, float(err.max()))
+        ok = ok and bool(np.all(err <= 2e-3 + 1e-3 * np.abs(ref)))
+    print(json.dumps({
+        "metric": "shared-prefix paged decode attn+append us/layer (logical GB/s)",
+        "value": round(us_per_layer, 2), "unit": "us/layer", "higher_is_better": False,
+        "logical_gb_per_s": round(logical_bytes / (us_per_layer * 1e-6) / 1e9, 1),
+        "physical_gb_per_s": round(physical_bytes / (us_per_layer * 1e-6) / 1e9, 1),
+        "decode_kernel_avg_us": round(1000 * dec_ms / max(dec_n, 1), 2),
+        "ms_per_step": round(ms_per_step, 3),
+        "config": {"workload": f"{lanes} lanes ({groups} groups of {per_group} forking a 2048+r-token prefix, "
+                               f"partial-tail COW), contexts log-uniform in [128, 8192], {L} layers TinyLlama GQA "
+                               f"32q/4kv/64d fp16, through the engine",
+                   "logical_tokens": logical, "unique_physical_tokens": physical},
+        "steps": args.steps, "warmup": args.warmup,
+        "check": {"lanes": min(args.shared_check, lanes), "layer": 0, "max_abs_err": worst, "within_tolerance": ok,
+                  "tolerance": "2e-3 + 1e-3*|ref|"}}), flush=True)
+    return 0 if ok else 1
+
+
 def run_copy(dev, args) -> int:
     """Plain device-to-device copy of a known size: the achievable copy
     bandwidth of the box and the calibration run for the FETCH_SIZE /
@@ -498,9 +765,13 @@ def profiled_traffic(lanes_per_launch: int, context: int, layers: int):
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", choices=["decode", "gather", "copy"], default="decode",
+    ap.add_argument("--config", choices=["decode", "gather", "append", "shared", "copy"], default="decode",
                     help="decode: HBM-scale decode+append (the headline line); gather: long-sequence gather; "
-                         "copy: plain device copy (bandwidth and counter calibration)")
+                         "append: ragged one-token append with tail allocation; shared: fork/COW shared-prefix "
+                         "decode; copy: plain device copy (bandwidth and counter calibration)")
+    ap.add_argument("--shared-check", type=int, default=4, help="lanes of the shared config checked")
+    ap.add_argument("--append-lanes", type=int, default=64)
+    ap.add_argument("--append-check", type=int, default=4, help="lanes gathered and compared bit-exactly")
     ap.add_argument("--path", choices=["engine", "kernel"], default="engine",
                     help="engine: EngineKvBackend token transactions (reserve / writeLayerBatch / attendLayerBatch / "
                          "commit); kernel: the C-ABI kernels driven directly with bench-built page tables")
@@ -534,6 +805,10 @@ def main() -> int:
         return run_gather(dev, args)
     if args.config == "copy":
         return run_copy(dev, args)
+    if args.config == "append":
+        return run_append(kimkv, dev, args)
+    if args.config == "shared":
+        return run_shared(kimkv, dev, args)
     H, D, QH = 4, 64, 32
     total_steps = args.warmup + args.steps
     if args.path == "engine":

@@ -42,6 +42,13 @@ public:
     // after the metadata append cancels the request.
     [[nodiscard]] HipKvOperationResult append(RequestId request_id, std::uint32_t token_count,
                                               KvScalar const* device_input, HipStream stream = nullptr);
+    // append for `count` requests with one kernel launch (no reference
+    // counterpart: the reference appends request by request).  results[i] is
+    // what append(request_ids[i], token_count, device_inputs[i]) would
+    // return; a device failure cancels every request whose metadata was
+    // appended in this call.
+    void appendBatch(RequestId const* request_ids, std::size_t count, std::uint32_t token_count,
+                     KvScalar const* const* device_inputs, HipStream stream, HipKvOperationResult* results);
     [[nodiscard]] HipKvOperationResult promote(RequestId request_id, std::uint32_t logical_token_begin,
                                                HipStream stream = nullptr);
     // device_output: [layer][K/V][tokens][head][dim].

@@ -142,6 +142,10 @@ kimkv_status kimkv_device_malloc(void** ptr, size_t bytes);
 kimkv_status kimkv_device_free(void* ptr);
 kimkv_status kimkv_host_malloc_pinned(void** ptr, size_t bytes);
 kimkv_status kimkv_host_free_pinned(void* ptr);
+/* Pinned, coherent host memory that kernels read directly (zero-copy):
+ * *host_ptr is the host address, *device_ptr the address kernels use.  Free
+ * with kimkv_host_free_pinned. */
+kimkv_status kimkv_host_malloc_mapped(void** host_ptr, void** device_ptr, size_t bytes);
 kimkv_status kimkv_memcpy_h2d_async(void* dst, const void* src, size_t bytes, kimkv_stream_t stream);
 kimkv_status kimkv_memcpy_d2h_async(void* dst, const void* src, size_t bytes, kimkv_stream_t stream);
 kimkv_status kimkv_memcpy_d2d_async(void* dst, const void* src, size_t bytes, kimkv_stream_t stream);

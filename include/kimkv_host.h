@@ -237,6 +237,12 @@ void kimkv_cache_destroy(kimkv_cache* c);
 int kimkv_cache_status(const kimkv_cache* c);
 kimkv_manager* kimkv_cache_manager(kimkv_cache* c);
 const kimkv_storage* kimkv_cache_storage(const kimkv_cache* c);
+/* append for `count` requests in one launch (HipKvCache::appendBatch; no
+ * reference counterpart).  device_inputs[i] is request i's
+ * [layer][K/V][token_count][head][dim] block; results[i] as kimkv_cache_append. */
+void kimkv_cache_append_batch(kimkv_cache* c, const uint64_t* request_ids, uint32_t count, uint32_t token_count,
+                              const uint16_t* const* device_inputs, kimkv_stream_t stream,
+                              kimkv_cache_result* results);
 kimkv_cache_result kimkv_cache_append(kimkv_cache* c, uint64_t request_id, uint32_t token_count,
                                       const uint16_t* device_input, kimkv_stream_t stream);
 kimkv_cache_result kimkv_cache_promote(kimkv_cache* c, uint64_t request_id, uint32_t logical_token_begin,

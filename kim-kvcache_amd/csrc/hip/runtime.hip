@@ -131,6 +131,26 @@ kimkv_status kimkv_host_malloc_pinned(void** ptr, size_t bytes)
     return record_error(hipHostMalloc(ptr, bytes, hipHostMallocDefault), KIMKV_ALLOCATION_FAILED);
 }
 
+kimkv_status kimkv_host_malloc_mapped(void** host_ptr, void** device_ptr, size_t bytes)
+{
+    if (host_ptr == nullptr || device_ptr == nullptr) return KIMKV_INVALID_ARGUMENT;
+    *host_ptr = nullptr;
+    *device_ptr = nullptr;
+    if (bytes == 0) return KIMKV_OK;
+    kimkv_status const s =
+        record_error(hipHostMalloc(host_ptr, bytes, hipHostMallocMapped | hipHostMallocCoherent), KIMKV_ALLOCATION_FAILED);
+    if (s != KIMKV_OK) return s;
+    void* dev = nullptr;
+    kimkv_status const d = record_error(hipHostGetDevicePointer(&dev, *host_ptr, 0), KIMKV_ALLOCATION_FAILED);
+    if (d != KIMKV_OK) {
+        static_cast<void>(hipHostFree(*host_ptr));
+        *host_ptr = nullptr;
+        return d;
+    }
+    *device_ptr = dev;
+    return KIMKV_OK;
+}
+
 kimkv_status kimkv_host_free_pinned(void* ptr)
 {
     if (ptr == nullptr) return KIMKV_OK;

@@ -249,7 +249,8 @@ void kimkv_write_layer_batch(kimkv_txn** txns, const uint32_t* layers, const uin
                              const uint16_t* const* values, uint32_t count, int* statuses)
 {
     if (count == 0) return;
-    std::vector<LayerKvWriteBatchItem> items(count);
+    thread_local std::vector<LayerKvWriteBatchItem> items;
+    items.assign(count, LayerKvWriteBatchItem{});
     for (uint32_t i = 0; i < count; ++i) {
         items[i].transaction = txns[i] != nullptr ? &txns[i]->t : nullptr;
         items[i].write = LayerKvWrite{layers[i], keys[i], values[i]};
@@ -286,6 +287,14 @@ kimkv_cache_result kimkv_cache_append(kimkv_cache* c, uint64_t id, uint32_t n, c
                                       kimkv_stream_t stream)
 {
     return result(c->cache.append(id, n, input, stream));
+}
+
+void kimkv_cache_append_batch(kimkv_cache* c, const uint64_t* ids, uint32_t count, uint32_t n,
+                              const uint16_t* const* inputs, kimkv_stream_t stream, kimkv_cache_result* out)
+{
+    std::vector<HipKvOperationResult> results(count);
+    c->cache.appendBatch(ids, count, n, inputs, stream, results.data());
+    for (uint32_t i = 0; i < count; ++i) out[i] = result(results[i]);
 }
 
 kimkv_cache_result kimkv_cache_promote(kimkv_cache* c, uint64_t id, uint32_t begin, kimkv_stream_t stream)

@@ -68,7 +68,6 @@ struct BackendState final {
     std::atomic<std::uint64_t> batched_write_submissions{0};
     std::atomic<std::uint64_t> next_transaction_id{1};
     mutable std::mutex mutex;
-    std::mutex launch_mutex;   // serialises staging + launches of batch calls
     std::mutex event_mutex;
     std::vector<void*> free_events;   // completion events of finished transactions
 
@@ -202,7 +201,7 @@ public:
         kimkv_append_job job{};
         HipStatus s = prepareWrite(write, job);
         if (!s.ok()) return mapDevice(s);
-        std::lock_guard<std::mutex> lock(owner_->launch_mutex);
+        std::lock_guard<std::mutex> lock(owner_->storage.launchMutex());
         return mapDevice(launchWrites(&job, 1, stream_, {this}));
     }
 
@@ -214,13 +213,13 @@ public:
         std::uint32_t total = 0;
         HipStatus s = planOne(request, item, prefix, chunk, total);
         if (!s.ok()) return mapDevice(s);
-        std::lock_guard<std::mutex> lock(owner_->launch_mutex);
+        std::lock_guard<std::mutex> lock(owner_->storage.launchMutex());
         HipKvStorage& st = owner_->storage;
         struct {
             kimkv_decode_item item;
             std::uint32_t prefix[2];
         } packed{item, {prefix[0], prefix[1]}};
-        auto* staged = static_cast<unsigned char*>(st.ring().upload(&packed, sizeof(packed), stream_));
+        auto* staged = static_cast<unsigned char*>(st.ring().stage(&packed, sizeof(packed), stream_));
         if (staged == nullptr) return mapDevice(failSubmission(kimkv_last_native_error()));
         kimkv_status const k = kimkv_paged_decode_batch(
             st.handle(), reinterpret_cast<kimkv_decode_item const*>(staged),
@@ -228,7 +227,8 @@ public:
             owner_->config.query_head_count, stream_);
         st.ring().fence(stream_);
         if (k != KIMKV_OK) return mapDevice(failSubmission(kimkv_last_native_error()));
-        setMark(markLaunch(owner_, stream_));
+        dirty_ = true;
+        if (request.layer + 1 == owner_->config.kv_layout.layer_count) setMark(markLaunch(owner_, stream_));
         return {};
     }
 
@@ -289,17 +289,18 @@ public:
         std::vector<std::uint32_t> pre(n + 1, 0);
         for (std::size_t i = 0; i < n; ++i) pre[i + 1] = pre[i] + (launch_tokens[i] + chunk - 1) / chunk;
         total = pre[n];
-        // Items and chunk prefix travel in one staged copy (each copy on the
-        // stream costs a dispatch and a gap between kernels); the caller's
+        // Items and chunk prefix are staged together in pinned host memory
+        // that the kernels read directly (a copy command on the stream would
+        // cost a dispatch and a gap between kernels); the caller's
         // device_items scratch is validated by the API but not needed here.
         std::size_t const items_bytes = (n * sizeof(DevicePagedDecodeBatchItem) + 15) & ~std::size_t{15};
         thread_local std::vector<unsigned char> staging;
         staging.resize(items_bytes + pre.size() * 4);
         std::memcpy(staging.data(), batch.host_items, n * sizeof(DevicePagedDecodeBatchItem));
         std::memcpy(staging.data() + items_bytes, pre.data(), pre.size() * 4);
-        std::lock_guard<std::mutex> lock(o.launch_mutex);
+        std::lock_guard<std::mutex> lock(o.storage.launchMutex());
         HipStream const stream = stream_;
-        auto* staged = static_cast<unsigned char*>(st.ring().upload(staging.data(), staging.size(), stream));
+        auto* staged = static_cast<unsigned char*>(st.ring().stage(staging.data(), staging.size(), stream));
         kimkv_status k = KIMKV_SUBMISSION_FAILED;
         if (staged != nullptr) {
             k = kimkv_paged_decode_batch(st.handle(), reinterpret_cast<kimkv_decode_item const*>(staged),
@@ -307,13 +308,22 @@ public:
                                          static_cast<std::uint32_t>(n), total, chunk, QH, stream);
         }
         st.ring().fence(stream);
-        std::shared_ptr<CompletionMark> const mark = k == KIMKV_OK ? markLaunch(owner_, stream) : nullptr;
+        // Only the last layer's launch needs a completion mark (commit waits
+        // on it); earlier launches leave the transactions dirty.
+        bool last_layer = false;
+        for (std::size_t i : launched) {
+            last_layer = last_layer || batch.items[i].request.layer + 1 == o.config.kv_layout.layer_count;
+        }
+        std::shared_ptr<CompletionMark> const mark = k == KIMKV_OK && last_layer ? markLaunch(owner_, stream) : nullptr;
         std::uint64_t good = 0;
         for (std::size_t i : launched) {
             PagedDecodeBatchItem& item = batch.items[i];
             auto* t = static_cast<HipTokenTransaction*>(batchBackend(item));
             item.status = k == KIMKV_OK ? EngineKvStatus{} : mapDevice(t->failSubmission(kimkv_last_native_error()));
-            if (k == KIMKV_OK) t->setMark(mark);
+            if (k == KIMKV_OK) {
+                t->dirty_ = true;
+                if (item.request.layer + 1 == o.config.kv_layout.layer_count) t->setMark(mark);
+            }
             good += item.status.ok() ? 1 : 0;
         }
         if (good != 0) {
@@ -355,7 +365,7 @@ public:
         if (jobs.empty()) return;
         HipStatus s;
         {
-            std::lock_guard<std::mutex> lock(owner_->launch_mutex);
+            std::lock_guard<std::mutex> lock(owner_->storage.launchMutex());
             s = launchWrites(jobs.data(), jobs.size(), stream_, launched);
         }
         for (std::size_t k = 0; k < launched.size(); ++k) {
@@ -444,13 +454,15 @@ private:
                            std::vector<HipTokenTransaction*> const& owners)
     {
         HipKvStorage& st = owner_->storage;
-        void* d = st.ring().upload(jobs, n * sizeof(kimkv_append_job), stream);
+        void* d = st.ring().stage(jobs, n * sizeof(kimkv_append_job), stream);
         kimkv_status k = KIMKV_SUBMISSION_FAILED;
         if (d != nullptr) {
             k = kimkv_append_batch(st.handle(), static_cast<kimkv_append_job const*>(d),
                                    static_cast<std::uint32_t>(n), 1, stream);
         }
-        st.ring().fence(stream);
+        // No fence here: the layer's attention launch fences this stream's
+        // staged regions (an unfenced region is reclaimed by draining its
+        // stream).
         for (HipTokenTransaction* t : owners) t->dirty_ = true;
         if (k == KIMKV_OK) return {};
         int const native = kimkv_last_native_error();
@@ -707,9 +719,9 @@ public:
             }
         }
         if (failure.ok()) {
-            std::lock_guard<std::mutex> launch(state_->launch_mutex);
+            std::lock_guard<std::mutex> launch(state_->storage.launchMutex());
+            // Fenced by the first attention launch on this stream.
             bool const staged = st.ring().uploadTo(arena->ptr, all.data(), bytes, stream);
-            st.ring().fence(stream);
             if (!staged) failure = {EngineKvError::SubmissionFailed};
         }
         for (Pending& p : pending) {

@@ -6,6 +6,8 @@
 
 #include "storage.h"
 
+#include <vector>
+
 namespace kimkvcache {
 namespace {
 
@@ -69,6 +71,77 @@ HipKvOperationResult HipKvCache::append(RequestId request_id, std::uint32_t toke
     }
     if (!manager_.blockTable(request_id).has_value()) return metadataFailure(KvCacheError::RequestNotFound);
     return {};
+}
+
+void HipKvCache::appendBatch(RequestId const* request_ids, std::size_t count, std::uint32_t token_count,
+                             KvScalar const* const* device_inputs, HipStream stream, HipKvOperationResult* results)
+{
+    struct Pending {
+        std::size_t index;
+        PageLeaseAcquireResult before;
+        PageLeaseAcquireResult after;
+        std::uint32_t begin;
+    };
+    std::vector<Pending> pending;
+    pending.reserve(count);
+    HipStatus const st = status();
+    for (std::size_t i = 0; i < count; ++i) {
+        RequestId const id = request_ids[i];
+        if (id == kInvalidRequestId || token_count == 0 || device_inputs[i] == nullptr) {
+            results[i] = metadataFailure(KvCacheError::InvalidArgument);
+            continue;
+        }
+        if (!st.ok()) {
+            results[i] = HipKvOperationResult{KvCacheError::None, st};
+            continue;
+        }
+        PageLeaseAcquireResult before = manager_.acquireRequestReadLease(id);
+        if (!before.ok()) {
+            results[i] = metadataFailure(before.error);
+            continue;
+        }
+        std::uint32_t const begin = before.table.tokenCount();
+        KvCacheError const appended = manager_.append(id, token_count);
+        if (appended != KvCacheError::None) {
+            KvCacheError const l = manager_.releasePageLease(before.lease_id);
+            results[i] = metadataFailure(l == KvCacheError::None ? appended : l);
+            continue;
+        }
+        PageLeaseAcquireResult after = manager_.acquireRequestReadLease(id);
+        if (!after.ok()) {
+            KvCacheError const l = manager_.releasePageLease(before.lease_id);
+            if (after.error != KvCacheError::RequestNotFound) static_cast<void>(manager_.releaseRequest(id));
+            results[i] = metadataFailure(l == KvCacheError::None ? after.error : l);
+            continue;
+        }
+        pending.push_back(Pending{i, std::move(before), std::move(after), begin});
+    }
+    if (pending.empty()) return;
+    std::vector<HipKvStorage::AppendPlan> plans;
+    plans.reserve(pending.size());
+    for (Pending const& p : pending) {
+        plans.push_back(HipKvStorage::AppendPlan{&p.before.table, &p.after.table, p.begin, token_count,
+                                                 device_inputs[p.index]});
+    }
+    HipStatus const device = storage_->appendMany(plans, stream);
+    for (Pending& p : pending) {
+        KvCacheError const ra = manager_.releasePageLease(p.after.lease_id);
+        KvCacheError const rb = manager_.releasePageLease(p.before.lease_id);
+        RequestId const id = request_ids[p.index];
+        if (!device.ok()) {
+            KvCacheError const c = manager_.releaseRequest(id);
+            results[p.index] = HipKvOperationResult{
+                c != KvCacheError::None && c != KvCacheError::RequestNotFound ? c : KvCacheError::None, device};
+            continue;
+        }
+        if (ra != KvCacheError::None) {
+            results[p.index] = metadataFailure(ra);
+        } else if (rb != KvCacheError::None) {
+            results[p.index] = metadataFailure(rb);
+        } else {
+            results[p.index] = {};
+        }
+    }
 }
 
 HipKvOperationResult HipKvCache::promote(RequestId request_id, std::uint32_t logical_token_begin, HipStream stream)

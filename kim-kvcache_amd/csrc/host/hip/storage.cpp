@@ -55,56 +55,82 @@ DeviceMemory& DeviceMemory::operator=(DeviceMemory&& o) noexcept
 StagingRing::StagingRing(std::size_t bytes) : size_(bytes), device_()
 {
     void* host = nullptr;
-    if (kimkv_host_malloc_pinned(&host, bytes) == KIMKV_OK) host_ = static_cast<unsigned char*>(host);
+    void* view = nullptr;
+    if (kimkv_host_malloc_mapped(&host, &view, bytes) == KIMKV_OK) {
+        host_ = static_cast<unsigned char*>(host);
+        view_ = static_cast<unsigned char*>(view);
+    }
 }
 
 StagingRing::~StagingRing()
 {
-    for (Region& r : live_) {
+    for (Region const& r : live_) {
+        if (r.done) continue;
         if (r.event != nullptr) {
             static_cast<void>(kimkv_event_synchronize(r.event));
-            static_cast<void>(kimkv_event_destroy(r.event));
+        } else {
+            static_cast<void>(kimkv_stream_synchronize(r.stream));
         }
     }
+    for (auto const& e : event_refs_) static_cast<void>(kimkv_event_destroy(e.first));
     for (void* e : spare_events_) static_cast<void>(kimkv_event_destroy(e));
     if (host_ != nullptr) static_cast<void>(kimkv_host_free_pinned(host_));
 }
 
-std::size_t StagingRing::reserve(std::size_t bytes)
+void StagingRing::dropRef(void* event)
 {
-    if (device_.get() == nullptr && host_ != nullptr) device_ = DeviceMemory(size_);
+    if (event == nullptr) return;
+    auto it = std::find_if(event_refs_.begin(), event_refs_.end(),
+                           [event](std::pair<void*, int> const& e) { return e.first == event; });
+    if (it == event_refs_.end()) return;
+    if (--it->second == 0) {
+        spare_events_.push_back(event);
+        event_refs_.erase(it);
+    }
+}
+
+std::size_t StagingRing::reserve(std::size_t bytes, HipStream stream)
+{
     bytes = (bytes + 255) & ~std::size_t{255};
     std::size_t begin = head_;
     if (begin + bytes > size_) begin = 0;
     std::size_t const end = begin + bytes;
-    // Regions are handed out in ring order and each fence event completes
-    // after every older region's consumer, so waiting on the first event at or
-    // after an overlapping region frees it and everything before it.
+    // Regions are handed out in ring order; the oldest one overlapping the
+    // new range is freed by waiting on its own fence event, or, if it was
+    // never fenced, on its stream.
     while (!live_.empty() && live_.front().begin < end && begin < live_.front().end) {
-        auto covering = std::find_if(live_.begin(), live_.end(), [](Region const& r) { return r.event != nullptr; });
-        if (covering == live_.end()) {
-            static_cast<void>(kimkv_device_synchronize());
-            for (Region const& r : live_) {
-                if (r.event != nullptr) spare_events_.push_back(r.event);
+        Region const r = live_.front();
+        if (!r.done) {
+            if (r.event != nullptr) {
+                static_cast<void>(kimkv_event_synchronize(r.event));
+            } else {
+                static_cast<void>(kimkv_stream_synchronize(r.stream));
             }
-            live_.clear();
-            break;
         }
-        static_cast<void>(kimkv_event_synchronize(covering->event));
-        spare_events_.push_back(covering->event);
-        live_.erase(live_.begin(), std::next(covering));
+        dropRef(r.event);
+        live_.pop_front();
     }
-    live_.push_back(Region{begin, end, nullptr});
+    live_.push_back(Region{begin, end, stream, nullptr, false});
     head_ = end;
     return begin;
+}
+
+void* StagingRing::stage(void const* data, std::size_t bytes, HipStream stream)
+{
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (host_ == nullptr || view_ == nullptr || bytes > size_ / 2) return nullptr;
+    std::size_t const off = reserve(bytes, stream);
+    std::memcpy(host_ + off, data, bytes);
+    return view_ + off;
 }
 
 void* StagingRing::upload(void const* data, std::size_t bytes, HipStream stream)
 {
     std::lock_guard<std::mutex> lock(mutex_);
     if (host_ == nullptr || bytes > size_ / 2) return nullptr;
-    std::size_t const off = reserve(bytes);
+    if (device_.get() == nullptr) device_ = DeviceMemory(size_);
     if (device_.get() == nullptr) return nullptr;
+    std::size_t const off = reserve(bytes, stream);
     std::memcpy(host_ + off, data, bytes);
     unsigned char* dev = static_cast<unsigned char*>(device_.get()) + off;
     if (kimkv_memcpy_h2d_async(dev, host_ + off, bytes, stream) != KIMKV_OK) return nullptr;
@@ -115,7 +141,7 @@ bool StagingRing::uploadTo(void* device_dst, void const* data, std::size_t bytes
 {
     std::lock_guard<std::mutex> lock(mutex_);
     if (host_ == nullptr || bytes > size_ / 2) return false;
-    std::size_t const off = reserve(bytes);
+    std::size_t const off = reserve(bytes, stream);
     std::memcpy(host_ + off, data, bytes);
     return kimkv_memcpy_h2d_async(device_dst, host_ + off, bytes, stream) == KIMKV_OK;
 }
@@ -123,7 +149,9 @@ bool StagingRing::uploadTo(void* device_dst, void const* data, std::size_t bytes
 void StagingRing::fence(HipStream stream)
 {
     std::lock_guard<std::mutex> lock(mutex_);
-    if (live_.empty() || live_.back().event != nullptr) return;
+    int pending = 0;
+    for (Region const& r : live_) pending += (!r.done && r.event == nullptr && r.stream == stream) ? 1 : 0;
+    if (pending == 0) return;
     void* event = nullptr;
     if (!spare_events_.empty()) {
         event = spare_events_.back();
@@ -136,15 +164,19 @@ void StagingRing::fence(HipStream stream)
         event = nullptr;
     }
     if (event == nullptr) {
-        // Cannot fence: drain so every staged region is free again.
+        // Cannot fence: drain the stream so its staged regions are free again.
         static_cast<void>(kimkv_stream_synchronize(stream));
-        for (Region const& r : live_) {
-            if (r.event != nullptr) spare_events_.push_back(r.event);
+        for (Region& r : live_) {
+            if (!r.done && r.event == nullptr && r.stream == stream) r.done = true;
         }
-        live_.clear();
         return;
     }
-    live_.back().event = event;   // covers every older region too
+    // One event, recorded after everything staged on this stream so far,
+    // covers all of that stream's unfenced regions.
+    for (Region& r : live_) {
+        if (!r.done && r.event == nullptr && r.stream == stream) r.event = event;
+    }
+    event_refs_.emplace_back(event, pending);
 }
 
 // ---- DeviceBufferCache ----------------------------------------------------------------
@@ -324,18 +356,15 @@ struct TempDevice {
 
 }  // namespace
 
-HipStatus HipKvStorage::append(BlockTable const& before, BlockTable const& after, std::uint32_t begin,
-                               std::uint32_t count, KvScalar const* input, HipStream stream)
+bool HipKvStorage::appendJobs(BlockTable const& before, BlockTable const& after, std::uint32_t begin,
+                              std::uint32_t count, KvScalar const* input, std::vector<kimkv_append_job>& jobs) const
 {
-    if (!status_.ok()) return status_;
-    if (consumeFailure(HipFailurePoint::Submission)) return HipStatus{HipError::SubmissionFailed, 0};
     std::uint64_t const end = static_cast<std::uint64_t>(begin) + count;
     if (input == nullptr || count == 0 || end > 0xFFFFFFFFull || !validTable(before) || !validTable(after)
         || before.tokenCount() != begin || after.tokenCount() != end) {
-        return HipStatus{HipError::InvalidArgument, 0};
+        return false;
     }
     std::size_t const hd = static_cast<std::size_t>(layout_.kv_head_count) * layout_.head_dimension;
-    std::vector<kimkv_append_job> jobs;
     // Copy-on-write source of the replaced partial tail, if any.
     PageHandle cow_src = PageHandle::invalid();
     std::uint16_t cow_tokens = 0;
@@ -344,17 +373,18 @@ HipStatus HipKvStorage::append(BlockTable const& before, BlockTable const& after
         auto rep = std::find_if(after.entries().begin(), after.entries().end(), [&old](MappingEntry const& e) {
             return e.logical_token_begin == old.logical_token_begin;
         });
-        if (rep == after.entries().end()) return HipStatus{HipError::InvalidArgument, 0};
+        if (rep == after.entries().end()) return false;
         if (rep->handle == old.handle) continue;
         bool const tail = old.logicalTokenEnd() == begin;
         if (!tail || old.kind != PageKind::Micro || rep->kind != PageKind::Micro || old.valid_tokens >= micro_tokens_
             || rep->valid_tokens < old.valid_tokens) {
-            return HipStatus{HipError::InvalidArgument, 0};
+            return false;
         }
         cow_src = old.handle;
         cow_tokens = old.valid_tokens;
         cow_dst = rep->handle;
     }
+    std::size_t const first = jobs.size();
     for (MappingEntry const& e : after.entries()) {
         std::uint32_t const sb = std::max(begin, e.logical_token_begin);
         std::uint32_t const se = std::min(static_cast<std::uint32_t>(end), e.logicalTokenEnd());
@@ -378,16 +408,61 @@ HipStatus HipKvStorage::append(BlockTable const& before, BlockTable const& after
         }
         jobs.push_back(j);
     }
-    if (jobs.empty()) return HipStatus{HipError::InvalidArgument, 0};
-    TempDevice dev;
-    if (!dev.upload(jobs.data(), jobs.size() * sizeof(kimkv_append_job), stream)) {
+    return jobs.size() > first;
+}
+
+HipStatus HipKvStorage::launchAppendJobs(std::vector<kimkv_append_job> const& jobs, HipStream stream)
+{
+    std::size_t const bytes = jobs.size() * sizeof(kimkv_append_job);
+    HipStatus s{HipError::SubmissionFailed, 0};
+    if (bytes <= ring_.capacity() / 2) {
+        {
+            std::lock_guard<std::mutex> lock(launch_mutex_);
+            void* d = ring_.stage(jobs.data(), bytes, stream);
+            if (d != nullptr) {
+                s = mapStatus(kimkv_append_batch(storage_, static_cast<kimkv_append_job const*>(d),
+                                                 static_cast<std::uint32_t>(jobs.size()), layout_.layer_count,
+                                                 stream),
+                              HipError::SubmissionFailed);
+            } else {
+                s = HipStatus{HipError::SubmissionFailed, kimkv_last_native_error()};
+            }
+            ring_.fence(stream);
+        }
+        return finish(stream, s);
+    }
+    TempDevice dev;   // larger than the staging ring: a one-off device copy
+    if (!dev.upload(jobs.data(), bytes, stream)) {
         return finish(stream, HipStatus{HipError::SubmissionFailed, kimkv_last_native_error()});
     }
-    HipStatus const s = mapStatus(kimkv_append_batch(storage_, static_cast<kimkv_append_job const*>(dev.mem.get()),
-                                                     static_cast<std::uint32_t>(jobs.size()), layout_.layer_count,
-                                                     stream),
-                                  HipError::SubmissionFailed);
+    s = mapStatus(kimkv_append_batch(storage_, static_cast<kimkv_append_job const*>(dev.mem.get()),
+                                     static_cast<std::uint32_t>(jobs.size()), layout_.layer_count, stream),
+                  HipError::SubmissionFailed);
     return finish(stream, s);
+}
+
+HipStatus HipKvStorage::append(BlockTable const& before, BlockTable const& after, std::uint32_t begin,
+                               std::uint32_t count, KvScalar const* input, HipStream stream)
+{
+    if (!status_.ok()) return status_;
+    if (consumeFailure(HipFailurePoint::Submission)) return HipStatus{HipError::SubmissionFailed, 0};
+    std::vector<kimkv_append_job> jobs;
+    if (!appendJobs(before, after, begin, count, input, jobs)) return HipStatus{HipError::InvalidArgument, 0};
+    return launchAppendJobs(jobs, stream);
+}
+
+HipStatus HipKvStorage::appendMany(std::vector<AppendPlan> const& plans, HipStream stream)
+{
+    if (!status_.ok()) return status_;
+    if (consumeFailure(HipFailurePoint::Submission)) return HipStatus{HipError::SubmissionFailed, 0};
+    std::vector<kimkv_append_job> jobs;
+    for (AppendPlan const& p : plans) {
+        if (!appendJobs(*p.before, *p.after, p.begin, p.count, p.input, jobs)) {
+            return HipStatus{HipError::InvalidArgument, 0};
+        }
+    }
+    if (jobs.empty()) return HipStatus{HipError::InvalidArgument, 0};
+    return launchAppendJobs(jobs, stream);
 }
 
 HipStatus HipKvStorage::gather(BlockTable const& table, KvScalar* out, HipStream stream)

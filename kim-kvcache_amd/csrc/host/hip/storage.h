@@ -42,9 +42,13 @@ private:
     std::size_t bytes_{0};
 };
 
-// Pinned host ring + device ring of the same size.  upload() copies host bytes
-// into the ring and enqueues the H2D copy; fence() records an event after the
-// work that consumes the uploaded bytes so the region is only reused after it.
+// Pinned host ring (+ a device ring of the same size for upload()).  stage()
+// hands kernels the pinned bytes directly; upload() / uploadTo() enqueue an
+// H2D copy of them.  Every region remembers the stream whose work consumes
+// it; fence(stream) records one event after that work and attaches it to all
+// of the stream's unfenced regions.  A region is reused only after its event
+// (or, when it was never fenced, its stream) has completed, so callers may
+// fence once after several staged launches on the same stream.
 class StagingRing final {
 public:
     explicit StagingRing(std::size_t bytes);
@@ -53,6 +57,12 @@ public:
     StagingRing& operator=(StagingRing const&) = delete;
 
     [[nodiscard]] bool ok() const noexcept { return host_ != nullptr && device_.get() != nullptr; }
+    [[nodiscard]] std::size_t capacity() const noexcept { return size_; }
+    // Copies `bytes` into the pinned ring and returns that host address, which
+    // kernels read directly (mapped, coherent host memory: no copy command on
+    // the stream).  For small per-launch argument arrays read once per
+    // workgroup.  nullptr on failure.
+    [[nodiscard]] void* stage(void const* data, std::size_t bytes, HipStream stream);
     // Returns the device address of the staged copy, or nullptr on failure.
     [[nodiscard]] void* upload(void const* data, std::size_t bytes, HipStream stream);
     // Host staging only (the caller names the device destination).
@@ -63,15 +73,20 @@ private:
     struct Region {
         std::size_t begin;
         std::size_t end;
-        void* event;   // nullptr until fenced
+        HipStream stream;   // the stream whose work consumes the region
+        void* event;        // nullptr until fenced; shared by the regions one fence covered
+        bool done;          // consumer known complete (stream drained)
     };
-    [[nodiscard]] std::size_t reserve(std::size_t bytes);
+    [[nodiscard]] std::size_t reserve(std::size_t bytes, HipStream stream);
+    void dropRef(void* event);
 
     std::size_t size_;
     std::size_t head_{0};
     unsigned char* host_{nullptr};
+    unsigned char* view_{nullptr};   // device address of host_ (mapped, coherent)
     DeviceMemory device_;
     std::deque<Region> live_;
+    std::vector<std::pair<void*, int>> event_refs_;   // fence events and how many live regions use each
     std::vector<void*> spare_events_;
     std::mutex mutex_;
 };
@@ -118,6 +133,9 @@ public:
     void injectFailureOnce(HipFailurePoint point) noexcept;
 
     StagingRing& ring() noexcept { return ring_; }
+    // Held around every staged upload + launch + fence on this storage, so a
+    // fence always covers the regions staged just before it.
+    std::mutex& launchMutex() noexcept { return launch_mutex_; }
     DeviceBufferCache& buffers() noexcept { return buffers_; }
 
     // Synchronous data-path operations used by HipKvCache: enqueue on
@@ -125,6 +143,15 @@ public:
     [[nodiscard]] HipStatus append(BlockTable const& before, BlockTable const& after,
                                    std::uint32_t append_token_begin, std::uint32_t token_count,
                                    KvScalar const* device_input, HipStream stream);
+    // Several requests' appends in one launch.
+    struct AppendPlan {
+        BlockTable const* before;
+        BlockTable const* after;
+        std::uint32_t begin;
+        std::uint32_t count;
+        KvScalar const* input;
+    };
+    [[nodiscard]] HipStatus appendMany(std::vector<AppendPlan> const& plans, HipStream stream);
     [[nodiscard]] HipStatus gather(BlockTable const& table, KvScalar* device_output, HipStream stream);
     [[nodiscard]] HipStatus promote(PromotionPrepareResult const& promotion, HipStream stream);
     [[nodiscard]] HipStatus promoteBatch(std::vector<PromotionPrepareResult> const& promotions, HipStream stream);
@@ -133,6 +160,11 @@ public:
 
 private:
     [[nodiscard]] HipStatus finish(HipStream stream, HipStatus submitted) noexcept;
+    // Jobs of one request's append (validates both tables and the COW rule).
+    [[nodiscard]] bool appendJobs(BlockTable const& before, BlockTable const& after, std::uint32_t begin,
+                                  std::uint32_t count, KvScalar const* input,
+                                  std::vector<kimkv_append_job>& jobs) const;
+    [[nodiscard]] HipStatus launchAppendJobs(std::vector<kimkv_append_job> const& jobs, HipStream stream);
 
     KvLayout layout_{};
     std::uint32_t micro_capacity_{0};
@@ -142,6 +174,7 @@ private:
     kimkv_storage* storage_{nullptr};
     HipStatus status_{};
     StagingRing ring_;
+    std::mutex launch_mutex_;
     DeviceBufferCache buffers_;
     // Per-slot visit stamps for the O(entries) duplicate-page check.
     mutable std::mutex stamp_mutex_;

@@ -82,6 +82,8 @@ _SIGNATURES = {
     "kimkv_device_free": (ctypes.c_int, [ctypes.c_void_p]),
     "kimkv_host_malloc_pinned": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]),
     "kimkv_host_free_pinned": (ctypes.c_int, [ctypes.c_void_p]),
+    "kimkv_host_malloc_mapped": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p),
+                                                ctypes.c_size_t]),
     "kimkv_memcpy_h2d_async": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "kimkv_memcpy_d2h_async": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "kimkv_memcpy_d2d_async": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),

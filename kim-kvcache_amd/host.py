@@ -109,6 +109,7 @@ _SIG = {
     "kimkv_cache_manager": (P, [P]),
     "kimkv_cache_storage": (P, [P]),
     "kimkv_cache_append": (CacheResult, [P, U64, U32, P, P]),
+    "kimkv_cache_append_batch": (None, [P, P, U32, U32, P, P, P]),
     "kimkv_cache_promote": (CacheResult, [P, U64, U32, P]),
     "kimkv_cache_gather": (CacheResult, [P, U64, P, P]),
     "kimkv_cache_reference_attention": (CacheResult, [P, U64, P, P, P]),
@@ -321,6 +322,17 @@ class Cache:
     def append(self, rid, n, input_ptr, stream: Optional[device.Stream] = None) -> CacheResult:
         return lib().kimkv_cache_append(self.h, rid, n, input_ptr, stream.handle if stream else None)
 
+    def append_batch(self, ids_array, token_count, inputs_array, results_array,
+                     stream: Optional[device.Stream] = None) -> None:
+        """ids_array: uint64[n]; inputs_array: uint64[n] device addresses; results_array:
+        (CacheResult * n) receiving each request's result."""
+        lib().kimkv_cache_append_batch(self.h, ids_array.ctypes.data_as(ctypes.c_void_p), len(ids_array),
+                                       token_count, inputs_array.ctypes.data_as(ctypes.c_void_p),
+                                       stream.handle if stream else None, results_array)
+
+    def permute_free_slots(self, kind: int, seed: int) -> int:
+        return lib().kimkv_manager_permute_free_slots(self.mgr, kind, seed)
+
     def promote(self, rid, begin, stream: Optional[device.Stream] = None) -> CacheResult:
         return lib().kimkv_cache_promote(self.h, rid, begin, stream.handle if stream else None)
 
@@ -419,26 +431,42 @@ class LaneBatch:
     def _p(a):
         return a.ctypes.data_as(ctypes.c_void_p)
 
+    def _bind(self):
+        """Argument pointers, built once (the arrays are updated in place)."""
+        if getattr(self, "_args", None) is None:
+            P_ = ctypes.POINTER(P)
+            self._args = {
+                "txns": ctypes.cast(self._p(self.txns), P_),
+                "status": ctypes.cast(self._p(self.status), ctypes.POINTER(I)),
+                "layers": [ctypes.cast(self._p(self.layer_ids[l]), ctypes.POINTER(U32)) for l in range(self.L)],
+                "keys": [ctypes.cast(self._p(self.keys[l]), P_) for l in range(self.L)],
+                "values": [ctypes.cast(self._p(self.values[l]), P_) for l in range(self.L)],
+                "reqs": [ctypes.cast(ctypes.c_void_p(self._req_base + l * self._req_stride),
+                                     ctypes.POINTER(DecodeRequest)) for l in range(self.L)],
+                "ids": self._p(self.ids), "expected": self._p(self.expected),
+                "txns_v": self._p(self.txns), "status_v": self._p(self.status),
+            }
+        return self._args
+
     def reserve(self, expected) -> None:
+        a = self._bind()
         self.expected[:] = expected
-        lib().kimkv_engine_reserve_batch(self.engine.h, self._p(self.ids), self._p(self.expected), self.n,
-                                         self.stream, self._p(self.txns), self._p(self.status))
+        lib().kimkv_engine_reserve_batch(self.engine.h, a["ids"], a["expected"], self.n, self.stream, a["txns_v"],
+                                         a["status_v"])
 
     def write(self, layer: int) -> None:
-        lib().kimkv_write_layer_batch(ctypes.cast(self._p(self.txns), ctypes.POINTER(P)),
-                                      ctypes.cast(self._p(self.layer_ids[layer]), ctypes.POINTER(U32)),
-                                      ctypes.cast(self._p(self.keys[layer]), ctypes.POINTER(P)),
-                                      ctypes.cast(self._p(self.values[layer]), ctypes.POINTER(P)),
-                                      self.n, ctypes.cast(self._p(self.status), ctypes.POINTER(I)))
+        a = self._bind()
+        lib().kimkv_write_layer_batch(a["txns"], a["layers"][layer], a["keys"][layer], a["values"][layer], self.n,
+                                      a["status"])
 
     def attend(self, layer: int) -> None:
-        reqs = ctypes.cast(ctypes.c_void_p(self._req_base + layer * self._req_stride), ctypes.POINTER(DecodeRequest))
-        lib().kimkv_attend_layer_batch(ctypes.cast(self._p(self.txns), ctypes.POINTER(P)), reqs, self.n,
-                                       self.device_items.ptr, self.n,
-                                       ctypes.cast(self._p(self.status), ctypes.POINTER(I)))
+        a = self._bind()
+        lib().kimkv_attend_layer_batch(a["txns"], a["reqs"][layer], self.n, self.device_items.ptr, self.n,
+                                       a["status"])
 
     def commit(self) -> None:
-        lib().kimkv_txn_commit_batch(self._p(self.txns), self.n, self._p(self.status))
+        a = self._bind()
+        lib().kimkv_txn_commit_batch(a["txns_v"], self.n, a["status_v"])
 
     def failed(self) -> bool:
         return bool(self.status.any())
