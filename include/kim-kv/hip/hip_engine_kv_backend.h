@@ -52,6 +52,60 @@ namespace kimkvcache {
 // kim-kv/runtime/pool_permutation.h).
 [[nodiscard]] EngineKvStatus permuteEngineFreeSlots(EngineKvBackend& backend, PageKind kind, std::uint64_t seed);
 
+// A chunk of n prompt positions of one request, written and attended layer
+// by layer (no reference counterpart: the reference advances a prompt one
+// position per token transaction).  beginPrefillChunk appends the n tokens to
+// the request's table at once; then, for every layer in order, writeLayer
+// stores the chunk's K/V ([n][kv_heads][head_dim] fp16 each) and attendLayer
+// runs causal GQA attention of the chunk's queries ([n][query_heads][dim])
+// over the request's tokens: output row i equals a decode of the first
+// T0 + i + 1 tokens.  finish() waits for the work; a failure cancels the
+// request (its table already holds the chunk).  Calls only enqueue work on
+// the chunk's stream until finish().
+class PrefillChunk final {
+public:
+    struct Impl;
+    PrefillChunk() noexcept;
+    explicit PrefillChunk(std::unique_ptr<Impl> impl) noexcept;
+    ~PrefillChunk();
+    PrefillChunk(PrefillChunk&&) noexcept;
+    PrefillChunk& operator=(PrefillChunk&&) noexcept;
+    PrefillChunk(PrefillChunk const&) = delete;
+    PrefillChunk& operator=(PrefillChunk const&) = delete;
+
+    [[nodiscard]] bool valid() const noexcept { return impl_ != nullptr; }
+    [[nodiscard]] std::uint32_t tokenBegin() const noexcept;   // T0
+    [[nodiscard]] std::uint32_t tokenCount() const noexcept;   // n
+    [[nodiscard]] EngineKvStatus writeLayer(std::uint32_t layer, KvScalar const* device_key,
+                                            KvScalar const* device_value);
+    [[nodiscard]] EngineKvStatus attendLayer(std::uint32_t layer, KvScalar const* device_query,
+                                             KvScalar* device_output, float attention_scale);
+    [[nodiscard]] EngineKvStatus finish();
+    Impl* impl() noexcept { return impl_.get(); }
+
+private:
+    std::unique_ptr<Impl> impl_;
+};
+
+struct PrefillChunkResult final {
+    EngineKvStatus status{EngineKvError::InternalError};
+    PrefillChunk chunk;
+    [[nodiscard]] bool ok() const noexcept { return status.ok() && chunk.valid(); }
+};
+
+[[nodiscard]] PrefillChunkResult beginPrefillChunk(EngineKvBackend& backend, RequestId request_id,
+                                                   std::uint32_t expected_committed_tokens, std::uint32_t token_count,
+                                                   HipStream stream);
+
+// The layer step of several chunks of one backend and stream with one launch
+// each (write: one append kernel; attend: one prefill kernel).
+void writePrefillBatch(PrefillChunk* const* chunks, std::size_t count, std::uint32_t layer,
+                       KvScalar const* const* device_keys, KvScalar const* const* device_values,
+                       EngineKvStatus* statuses);
+void attendPrefillBatch(PrefillChunk* const* chunks, std::size_t count, std::uint32_t layer,
+                        KvScalar const* const* device_queries, KvScalar* const* device_outputs, float attention_scale,
+                        EngineKvStatus* statuses);
+
 // Committed block table of a request (diagnostics and tests).
 [[nodiscard]] bool engineBlockTable(EngineKvBackend const& backend, RequestId request_id, BlockTable& out);
 

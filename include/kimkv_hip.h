@@ -81,6 +81,23 @@ typedef struct kimkv_decode_item {
     float attention_scale;
 } kimkv_decode_item;
 
+/* One request's chunk of a multi-token causal prefill: the table holds
+ * token_count tokens, of which the last new_tokens are the chunk; new token i
+ * attends keys [0, token_count - new_tokens + i].  query / output are
+ * [new_tokens][query_heads][head_dim] fp16.  No reference counterpart (the
+ * reference advances a prompt chunk one position at a time). */
+typedef struct kimkv_prefill_item {
+    const kimkv_block_desc* descriptors;
+    uint32_t descriptor_count;
+    uint32_t token_count;
+    uint32_t new_tokens;
+    uint32_t layer;
+    const uint16_t* query;
+    uint16_t* output;
+    float attention_scale;
+    uint32_t reserved;
+} kimkv_prefill_item;
+
 /* One lane's append.  Writes `token_count` tokens of layers
  * [layer_begin, layer_begin+layer_count) into page (dst_kind, dst_slot) at
  * page token `dst_token`.  Source element (l, t, h, d) of K is read at
@@ -198,7 +215,7 @@ kimkv_status kimkv_promote_batch(const kimkv_storage* storage,
                                  kimkv_stream_t stream);
 
 /* Split-K planning for a ragged decode batch.  Given the lanes' token counts
- * (host array), picks the chunk length (a multiple of 64 tokens, >= 128) and
+ * (host array), picks the chunk length (a multiple of 64 tokens, 256..8192) and
  * fills chunk_prefix[0..lane_count] (host array) with the running chunk count.
  * Returns the total chunk count in *total_chunks. */
 kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* token_counts,
@@ -218,13 +235,29 @@ size_t kimkv_decode_workspace_bytes(uint32_t token_count, uint32_t chunk_tokens,
  * (kernels.cuh:119-143; paged_decode_kernels.cu:132-474,533-617).
  * q head j reads kv head j / (query_heads / kv_heads); s = (q.k) * scale with
  * fp32 accumulation; softmax; fp16 round-to-nearest-even output.
- * `device_items` and `device_chunk_prefix` live in DEVICE memory. */
+ * `device_items` and `device_chunk_prefix` live in memory the device reads
+ * (device memory, or mapped host memory as the engine stages them). */
 kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage,
                                       const kimkv_decode_item* device_items,
                                       const uint32_t* device_chunk_prefix,
                                       uint32_t lane_count, uint32_t total_chunks,
                                       uint32_t chunk_tokens, uint32_t query_heads,
                                       kimkv_stream_t stream);
+
+/* New tokens handled by one prefill workgroup (per KV head) for this
+ * storage's shape and query head count: items need
+ * ceil(new_tokens / this) workgroups each.  0 for an invalid head count. */
+uint32_t kimkv_prefill_tokens_per_block(const kimkv_storage* storage, uint32_t query_heads);
+
+/* Multi-token causal GQA paged attention (chunked prefill) for a batch of
+ * items: block_prefix[0..item_count] is the running workgroup count
+ * (kimkv_prefill_tokens_per_block), total_blocks its last entry.  Same
+ * arithmetic as kimkv_paged_decode_batch applied to each new token: the
+ * output of new token i equals a decode of the first
+ * token_count - new_tokens + i + 1 tokens with that token's query. */
+kimkv_status kimkv_paged_prefill_batch(const kimkv_storage* storage, const kimkv_prefill_item* device_items,
+                                       const uint32_t* device_block_prefix, uint32_t item_count,
+                                       uint32_t total_blocks, uint32_t query_heads, kimkv_stream_t stream);
 
 /* Reference attention over one table (the comparator of the reference's
  * launchAttentionScores / launchAttentionOutput, kernels.cuh:77-95, and of the

@@ -224,6 +224,35 @@ void kimkv_attend_layer_batch(kimkv_txn** txns, const kimkv_decode_request* requ
 void kimkv_write_layer_batch(kimkv_txn** txns, const uint32_t* layers, const uint16_t* const* keys,
                              const uint16_t* const* values, uint32_t count, int* statuses);
 
+/* ---- chunked prefill (no reference counterpart: the reference advances a
+ * prompt one position per token transaction) ------------------------------
+ * kimkv_engine_prefill_begin appends token_count positions to a committed
+ * request whose committed length is expected_committed_tokens and returns a
+ * chunk handle.  Then, for layer 0, 1, ... in order: write the chunk's K/V
+ * (each [token_count][kv_heads][head_dim] fp16, device memory), then attend
+ * its queries ([token_count][query_heads][head_dim]) causally over the
+ * request's tokens, output row i = decode of the first T0 + i + 1 tokens.
+ * kimkv_prefill_finish waits for the chunk's work and commits the tokens; a
+ * failure (or a chunk abandoned before its last layer) cancels the request.
+ * While a chunk is open, the request refuses reservation, fork, promotion and
+ * release (EngineKvError::InvalidState).  Calls only enqueue work on the
+ * chunk's stream before finish. */
+typedef struct kimkv_prefill_chunk kimkv_prefill_chunk;
+int kimkv_engine_prefill_begin(kimkv_engine* e, uint64_t request_id, uint32_t expected_committed_tokens,
+                               uint32_t token_count, kimkv_stream_t stream, kimkv_prefill_chunk** chunk);
+int kimkv_prefill_write_layer(kimkv_prefill_chunk* c, uint32_t layer, const uint16_t* key, const uint16_t* value);
+int kimkv_prefill_attend_layer(kimkv_prefill_chunk* c, uint32_t layer, const uint16_t* query, uint16_t* output,
+                               float attention_scale);
+int kimkv_prefill_finish(kimkv_prefill_chunk* c);
+void kimkv_prefill_destroy(kimkv_prefill_chunk* c);   /* finishes first when still open */
+/* One layer step of `count` chunks of one engine and stream: one append
+ * launch (write) or one prefill-attention launch (attend) for all of them. */
+void kimkv_prefill_write_batch(kimkv_prefill_chunk** chunks, uint32_t count, uint32_t layer,
+                               const uint16_t* const* keys, const uint16_t* const* values, int* statuses);
+void kimkv_prefill_attend_batch(kimkv_prefill_chunk** chunks, uint32_t count, uint32_t layer,
+                                const uint16_t* const* queries, uint16_t* const* outputs, float attention_scale,
+                                int* statuses);
+
 /* ---- CudaKvCache equivalent (include/kim-kv/cuda/cuda_kv_cache.h:33-100) --- */
 typedef struct kimkv_cache kimkv_cache;
 

@@ -22,6 +22,10 @@ struct kimkv_txn {
     TokenTransaction t;
 };
 
+struct kimkv_prefill_chunk {
+    PrefillChunk c;
+};
+
 struct kimkv_cache {
     HipKvCache cache;
     kimkv_manager view;
@@ -258,6 +262,59 @@ void kimkv_write_layer_batch(kimkv_txn** txns, const uint32_t* layers, const uin
     LayerKvWriteBatch batch{items.data(), count};
     writeLayerBatch(batch);
     for (uint32_t i = 0; i < count; ++i) statuses[i] = code(items[i].status);
+}
+
+int kimkv_engine_prefill_begin(kimkv_engine* e, uint64_t id, uint32_t expected, uint32_t n, kimkv_stream_t stream,
+                               kimkv_prefill_chunk** chunk)
+{
+    if (chunk == nullptr) return static_cast<int>(EngineKvError::InvalidArgument);
+    *chunk = nullptr;
+    PrefillChunkResult r = beginPrefillChunk(*e->backend, id, expected, n, stream);
+    if (!r.ok()) return code(r.status);
+    auto* c = new (std::nothrow) kimkv_prefill_chunk{std::move(r.chunk)};
+    if (c == nullptr) return static_cast<int>(EngineKvError::ResourceExhausted);   // r.chunk's dtor cancelled it
+    *chunk = c;
+    return 0;
+}
+
+int kimkv_prefill_write_layer(kimkv_prefill_chunk* c, uint32_t layer, const uint16_t* key, const uint16_t* value)
+{
+    return code(c->c.writeLayer(layer, key, value));
+}
+
+int kimkv_prefill_attend_layer(kimkv_prefill_chunk* c, uint32_t layer, const uint16_t* query, uint16_t* output,
+                               float attention_scale)
+{
+    return code(c->c.attendLayer(layer, query, output, attention_scale));
+}
+
+int kimkv_prefill_finish(kimkv_prefill_chunk* c) { return code(c->c.finish()); }
+void kimkv_prefill_destroy(kimkv_prefill_chunk* c) { delete c; }
+
+void kimkv_prefill_write_batch(kimkv_prefill_chunk** chunks, uint32_t count, uint32_t layer,
+                               const uint16_t* const* keys, const uint16_t* const* values, int* statuses)
+{
+    if (count == 0) return;
+    thread_local std::vector<PrefillChunk*> list;
+    thread_local std::vector<EngineKvStatus> st;
+    list.resize(count);
+    st.assign(count, EngineKvStatus{});
+    for (uint32_t i = 0; i < count; ++i) list[i] = chunks[i] != nullptr ? &chunks[i]->c : nullptr;
+    writePrefillBatch(list.data(), count, layer, keys, values, st.data());
+    for (uint32_t i = 0; i < count; ++i) statuses[i] = code(st[i]);
+}
+
+void kimkv_prefill_attend_batch(kimkv_prefill_chunk** chunks, uint32_t count, uint32_t layer,
+                                const uint16_t* const* queries, uint16_t* const* outputs, float scale, int* statuses)
+{
+    if (count == 0) return;
+    thread_local std::vector<PrefillChunk*> list;
+    thread_local std::vector<EngineKvStatus> st;
+    list.resize(count);
+    st.assign(count, EngineKvStatus{});
+    for (uint32_t i = 0; i < count; ++i) list[i] = chunks[i] != nullptr ? &chunks[i]->c : nullptr;
+    attendPrefillBatch(list.data(), count, layer, queries, outputs, scale, st.data());
+    for (uint32_t i = 0; i < count; ++i) statuses[i] = code(st[i]);
 }
 
 kimkv_cache* kimkv_cache_create(kimkv_layout layout, uint32_t micro_capacity, uint32_t extent_capacity)

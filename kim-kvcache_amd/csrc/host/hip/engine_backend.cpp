@@ -15,6 +15,7 @@
 #include "kim-kv/runtime/pool_permutation.h"
 #include "storage.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstddef>
 #include <cstring>
@@ -22,6 +23,7 @@
 #include <memory>
 #include <mutex>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 namespace kimkvcache {
@@ -62,6 +64,9 @@ struct BackendState final {
     KvCacheManager manager;
     HipKvStorage storage;
     std::unordered_map<RequestId, std::uint32_t> committed_lengths;
+    // Requests with an unfinished PrefillChunk: their table already holds the
+    // chunk, so every other mutation of them is refused until finish().
+    std::unordered_set<RequestId> prefilling;
     std::uint64_t active_transactions{0};
     std::atomic<std::uint64_t> batched_attention_submissions{0};
     std::atomic<std::uint64_t> batched_attention_lanes{0};
@@ -579,6 +584,296 @@ private:
     bool resolved_{false};
 };
 
+}  // namespace
+
+// ---- chunked prefill ------------------------------------------------------------
+
+struct PrefillChunk::Impl {
+    std::shared_ptr<BackendState> owner;
+    RequestId request{kInvalidRequestId};
+    std::uint32_t begin{0};
+    std::uint32_t count{0};
+    HipStream stream{nullptr};
+    PageLeaseId lease_before{kInvalidPageLeaseId};
+    PageLeaseId lease_after{kInvalidPageLeaseId};
+    std::shared_ptr<DescriptorArena> arena;
+    kimkv_block_desc const* descriptors{nullptr};
+    std::uint32_t desc_count{0};
+    std::vector<kimkv_append_job> jobs;       // per-layer template: destinations and COW source
+    std::vector<std::uint32_t> offsets;       // each job's first token relative to `begin`
+    std::uint32_t next_layer{0};
+    bool wrote{false};
+    HipStatus submission{};
+    bool finished{false};
+    EngineKvStatus final_status{};
+    std::shared_ptr<CompletionMark> mark;
+    bool dirty{true};
+
+    ~Impl() { static_cast<void>(finish()); }
+
+    EngineKvStatus check(std::uint32_t layer, bool want_written) const
+    {
+        if (finished) return {EngineKvError::InvalidState};
+        if (!submission.ok()) return mapDevice(submission);
+        if (layer != next_layer || wrote != want_written) return {EngineKvError::LayerOutOfOrder};
+        return {};
+    }
+
+    // Appends this chunk's layer jobs (sources set) to `out`.
+    void layerJobs(std::uint32_t layer, KvScalar const* key, KvScalar const* value,
+                   std::vector<kimkv_append_job>& out) const
+    {
+        std::size_t const hd = static_cast<std::size_t>(owner->config.kv_layout.kv_head_count)
+            * owner->config.kv_layout.head_dimension;
+        for (std::size_t k = 0; k < jobs.size(); ++k) {
+            kimkv_append_job j = jobs[k];
+            std::size_t const off = static_cast<std::size_t>(offsets[k]) * hd;
+            j.src_key = key + off;
+            j.src_value = value + off;
+            j.src_layer_stride = 0;
+            j.src_token_stride = static_cast<std::uint32_t>(hd);
+            j.layer_begin = layer;
+            j.layer_count = 1;
+            out.push_back(j);
+        }
+    }
+
+    kimkv_prefill_item item(std::uint32_t layer, KvScalar const* query, KvScalar* output, float scale) const
+    {
+        kimkv_prefill_item it{};
+        it.descriptors = descriptors;
+        it.descriptor_count = desc_count;
+        it.token_count = begin + count;
+        it.new_tokens = count;
+        it.layer = layer;
+        it.query = query;
+        it.output = output;
+        it.attention_scale = scale;
+        return it;
+    }
+
+    void fail(int native) { submission = HipStatus{HipError::SubmissionFailed, native}; }
+
+    EngineKvStatus finish()
+    {
+        if (finished || owner == nullptr) return final_status;
+        kimkv_status waited = KIMKV_OK;
+        if (!submission.ok()) {
+            static_cast<void>(kimkv_stream_synchronize(stream));
+        } else {
+            waited = mark != nullptr && !dirty ? kimkv_event_synchronize(mark->event) : kimkv_stream_synchronize(stream);
+        }
+        bool const all_layers = next_layer == owner->config.kv_layout.layer_count;
+        if (!submission.ok()) {
+            final_status = mapDevice(submission);
+        } else if (waited != KIMKV_OK) {
+            final_status = {EngineKvError::ExecutionFailed};
+        } else if (owner->storage.consumeFailure(HipFailurePoint::Completion)) {
+            final_status = {EngineKvError::ExecutionFailed};
+        } else if (!all_layers) {
+            final_status = {EngineKvError::InvalidState};   // abandoned before its last layer
+        } else {
+            final_status = {};
+        }
+        {
+            std::lock_guard<std::mutex> lock(owner->mutex);
+            KvCacheManager& m = owner->manager;
+            owner->prefilling.erase(request);
+            if (lease_after != kInvalidPageLeaseId) static_cast<void>(m.releasePageLease(lease_after));
+            if (lease_before != kInvalidPageLeaseId) static_cast<void>(m.releasePageLease(lease_before));
+            if (final_status.ok()) {
+                auto len = owner->committed_lengths.find(request);
+                if (len != owner->committed_lengths.end()) len->second += count;
+            } else {
+                // The table already names the chunk's pages: cancel rather than expose them.
+                static_cast<void>(m.releaseRequest(request));
+                owner->committed_lengths.erase(request);
+            }
+        }
+        arena.reset();
+        mark.reset();
+        finished = true;
+        return final_status;
+    }
+};
+
+PrefillChunk::PrefillChunk() noexcept = default;
+PrefillChunk::PrefillChunk(std::unique_ptr<Impl> impl) noexcept : impl_(std::move(impl)) {}
+PrefillChunk::~PrefillChunk() = default;
+PrefillChunk::PrefillChunk(PrefillChunk&&) noexcept = default;
+PrefillChunk& PrefillChunk::operator=(PrefillChunk&&) noexcept = default;
+
+std::uint32_t PrefillChunk::tokenBegin() const noexcept { return impl_ ? impl_->begin : 0; }
+std::uint32_t PrefillChunk::tokenCount() const noexcept { return impl_ ? impl_->count : 0; }
+
+EngineKvStatus PrefillChunk::writeLayer(std::uint32_t layer, KvScalar const* key, KvScalar const* value)
+{
+    PrefillChunk* self = this;
+    EngineKvStatus st{};
+    writePrefillBatch(&self, 1, layer, &key, &value, &st);
+    return st;
+}
+
+EngineKvStatus PrefillChunk::attendLayer(std::uint32_t layer, KvScalar const* query, KvScalar* output, float scale)
+{
+    PrefillChunk* self = this;
+    EngineKvStatus st{};
+    attendPrefillBatch(&self, 1, layer, &query, &output, scale, &st);
+    return st;
+}
+
+EngineKvStatus PrefillChunk::finish()
+{
+    if (impl_ == nullptr) return {EngineKvError::InvalidState};
+    return impl_->finish();
+}
+
+void writePrefillBatch(PrefillChunk* const* chunks, std::size_t count, std::uint32_t layer,
+                       KvScalar const* const* keys, KvScalar const* const* values, EngineKvStatus* statuses)
+{
+    thread_local std::vector<kimkv_append_job> jobs;
+    jobs.clear();
+    std::vector<PrefillChunk::Impl*> launched;
+    BackendState* owner = nullptr;
+    HipStream stream = nullptr;
+    for (std::size_t i = 0; i < count; ++i) {
+        PrefillChunk::Impl* c = chunks[i] != nullptr ? chunks[i]->impl() : nullptr;
+        if (c == nullptr) {
+            statuses[i] = {EngineKvError::InvalidArgument};
+            continue;
+        }
+        statuses[i] = c->check(layer, false);
+        if (!statuses[i].ok()) continue;
+        if (keys[i] == nullptr || values[i] == nullptr
+            || (owner != nullptr && (c->owner.get() != owner || c->stream != stream))) {
+            statuses[i] = {EngineKvError::InvalidArgument};
+            continue;
+        }
+        if (c->owner->storage.consumeFailure(HipFailurePoint::Submission)) {
+            c->fail(0);
+            statuses[i] = {EngineKvError::SubmissionFailed};
+            continue;
+        }
+        owner = c->owner.get();
+        stream = c->stream;
+        c->layerJobs(layer, keys[i], values[i], jobs);
+        launched.push_back(c);
+    }
+    if (launched.empty()) return;
+    HipKvStorage& st = owner->storage;
+    kimkv_status k = KIMKV_SUBMISSION_FAILED;
+    {
+        std::lock_guard<std::mutex> lock(st.launchMutex());
+        void* d = st.ring().stage(jobs.data(), jobs.size() * sizeof(kimkv_append_job), stream);
+        if (d != nullptr) {
+            k = kimkv_append_batch(st.handle(), static_cast<kimkv_append_job const*>(d),
+                                   static_cast<std::uint32_t>(jobs.size()), 1, stream);
+        }
+    }
+    int const native = k == KIMKV_OK ? 0 : kimkv_last_native_error();
+    for (std::size_t i = 0; i < count; ++i) {
+        PrefillChunk::Impl* c = chunks[i] != nullptr ? chunks[i]->impl() : nullptr;
+        if (c == nullptr || std::find(launched.begin(), launched.end(), c) == launched.end()) continue;
+        c->dirty = true;
+        if (k != KIMKV_OK) {
+            c->fail(native);
+            statuses[i] = {EngineKvError::SubmissionFailed};
+        } else {
+            c->wrote = true;
+        }
+    }
+}
+
+void attendPrefillBatch(PrefillChunk* const* chunks, std::size_t count, std::uint32_t layer,
+                        KvScalar const* const* queries, KvScalar* const* outputs, float scale,
+                        EngineKvStatus* statuses)
+{
+    thread_local std::vector<kimkv_prefill_item> items;
+    items.clear();
+    std::vector<std::uint32_t> prefix(1, 0);
+    std::vector<PrefillChunk::Impl*> launched;
+    BackendState* owner = nullptr;
+    HipStream stream = nullptr;
+    std::uint32_t per = 0;
+    for (std::size_t i = 0; i < count; ++i) {
+        PrefillChunk::Impl* c = chunks[i] != nullptr ? chunks[i]->impl() : nullptr;
+        if (c == nullptr) {
+            statuses[i] = {EngineKvError::InvalidArgument};
+            continue;
+        }
+        statuses[i] = c->check(layer, true);
+        if (!statuses[i].ok()) continue;
+        if (queries[i] == nullptr || outputs[i] == nullptr || !(scale > 0.0f)
+            || (owner != nullptr && (c->owner.get() != owner || c->stream != stream))) {
+            statuses[i] = {EngineKvError::InvalidArgument};
+            continue;
+        }
+        if (c->owner->storage.consumeFailure(HipFailurePoint::Submission)) {
+            c->fail(0);
+            statuses[i] = {EngineKvError::SubmissionFailed};
+            continue;
+        }
+        if (owner == nullptr) {
+            owner = c->owner.get();
+            stream = c->stream;
+            per = kimkv_prefill_tokens_per_block(owner->storage.handle(), owner->config.query_head_count);
+        }
+        if (per == 0) {
+            statuses[i] = {EngineKvError::InvalidArgument};
+            continue;
+        }
+        items.push_back(c->item(layer, queries[i], outputs[i], scale));
+        prefix.push_back(prefix.back() + (c->count + per - 1) / per);
+        launched.push_back(c);
+    }
+    if (launched.empty()) return;
+    HipKvStorage& st = owner->storage;
+    std::size_t const items_bytes = (items.size() * sizeof(kimkv_prefill_item) + 15) & ~std::size_t{15};
+    thread_local std::vector<unsigned char> staging;
+    staging.resize(items_bytes + prefix.size() * 4);
+    std::memcpy(staging.data(), items.data(), items.size() * sizeof(kimkv_prefill_item));
+    std::memcpy(staging.data() + items_bytes, prefix.data(), prefix.size() * 4);
+    kimkv_status k = KIMKV_SUBMISSION_FAILED;
+    {
+        std::lock_guard<std::mutex> lock(st.launchMutex());
+        auto* d = static_cast<unsigned char*>(st.ring().stage(staging.data(), staging.size(), stream));
+        if (d != nullptr) {
+            k = kimkv_paged_prefill_batch(st.handle(), reinterpret_cast<kimkv_prefill_item const*>(d),
+                                          reinterpret_cast<std::uint32_t const*>(d + items_bytes),
+                                          static_cast<std::uint32_t>(items.size()), prefix.back(),
+                                          owner->config.query_head_count, stream);
+        }
+        st.ring().fence(stream);
+    }
+    bool const last = layer + 1 == owner->config.kv_layout.layer_count;
+    std::shared_ptr<CompletionMark> mark;
+    if (k == KIMKV_OK && last) {
+        for (PrefillChunk::Impl* c : launched) {
+            mark = markLaunch(c->owner, stream);
+            break;
+        }
+    }
+    int const native = k == KIMKV_OK ? 0 : kimkv_last_native_error();
+    for (std::size_t i = 0; i < count; ++i) {
+        PrefillChunk::Impl* c = chunks[i] != nullptr ? chunks[i]->impl() : nullptr;
+        if (c == nullptr || std::find(launched.begin(), launched.end(), c) == launched.end()) continue;
+        c->dirty = true;
+        if (k != KIMKV_OK) {
+            c->fail(native);
+            statuses[i] = {EngineKvError::SubmissionFailed};
+            continue;
+        }
+        c->wrote = false;
+        ++c->next_layer;
+        if (last && mark != nullptr) {
+            c->mark = mark;
+            c->dirty = false;
+        }
+    }
+}
+
+namespace {
+
 class HipEngineKvBackend final : public EngineKvBackend {
 public:
     explicit HipEngineKvBackend(std::shared_ptr<BackendState> s) : state_(std::move(s)) {}
@@ -600,6 +895,7 @@ public:
         std::lock_guard<std::mutex> lock(state_->mutex);
         auto it = state_->committed_lengths.find(source);
         if (it == state_->committed_lengths.end()) return {EngineKvError::RequestNotFound};
+        if (state_->prefilling.count(source) != 0) return {EngineKvError::InvalidState};
         KvCacheError const e = state_->manager.forkRequest(source, child);
         if (e == KvCacheError::None) state_->committed_lengths.emplace(child, it->second);
         return mapMetadata(e);
@@ -608,6 +904,7 @@ public:
     EngineKvStatus releaseRequest(RequestId request_id) override
     {
         std::lock_guard<std::mutex> lock(state_->mutex);
+        if (state_->prefilling.count(request_id) != 0) return {EngineKvError::InvalidState};
         KvCacheError const e = state_->manager.releaseRequest(request_id);
         if (e == KvCacheError::None) state_->committed_lengths.erase(request_id);
         return mapMetadata(e);
@@ -652,6 +949,10 @@ public:
             }
             if (state_->committed_lengths.find(request.request_id) == state_->committed_lengths.end()) {
                 result.status = {EngineKvError::RequestNotFound};
+                continue;
+            }
+            if (state_->prefilling.count(request.request_id) != 0) {
+                result.status = {EngineKvError::InvalidState};
                 continue;
             }
             TokenReservationResult r = m.reserveToken(request.request_id, request.expected_committed_tokens);
@@ -794,6 +1095,7 @@ public:
         KvCacheManager& m = state_->manager;
         std::optional<BlockTable> t = m.blockTable(request_id);
         if (!t.has_value()) return {EngineKvError::RequestNotFound};
+        if (state_->prefilling.count(request_id) != 0) return {EngineKvError::InvalidState};
         std::vector<std::uint32_t> runs;
         auto const& e = t->entries();
         for (std::size_t i = 0; i + kPromotionSourcePageCount <= e.size();) {
@@ -861,6 +1163,7 @@ public:
             if (!state_->storage.status().ok()) return mapDevice(state_->storage.status());
             auto len = state_->committed_lengths.find(request_id);
             if (len == state_->committed_lengths.end()) return {EngineKvError::RequestNotFound};
+            if (state_->prefilling.count(request_id) != 0) return {EngineKvError::InvalidState};
             KvCacheManager& m = state_->manager;
             before = m.acquireRequestReadLease(request_id);
             if (!before.ok()) return mapMetadata(before.error);
@@ -900,6 +1203,94 @@ public:
             }
         }
         return promote_runs ? promote(request_id, stream, promoted) : EngineKvStatus{};
+    }
+
+    PrefillChunkResult beginPrefill(RequestId request_id, std::uint32_t expected, std::uint32_t n, HipStream stream)
+    {
+        PrefillChunkResult result;
+        if (request_id == kInvalidRequestId || n == 0) {
+            result.status = {EngineKvError::InvalidArgument};
+            return result;
+        }
+        auto impl = std::make_unique<PrefillChunk::Impl>();
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        HipKvStorage& st = state_->storage;
+        KvCacheManager& m = state_->manager;
+        if (!st.status().ok()) {
+            result.status = mapDevice(st.status());
+            return result;
+        }
+        auto len = state_->committed_lengths.find(request_id);
+        if (len == state_->committed_lengths.end()) {
+            result.status = {EngineKvError::RequestNotFound};
+            return result;
+        }
+        if (len->second != expected || state_->prefilling.count(request_id) != 0) {
+            result.status = {EngineKvError::InvalidState};
+            return result;
+        }
+        PageLeaseAcquireResult before = m.acquireRequestReadLease(request_id);
+        if (!before.ok()) {
+            result.status = mapMetadata(before.error);
+            return result;
+        }
+        if (before.table.tokenCount() != expected) {
+            static_cast<void>(m.releasePageLease(before.lease_id));
+            result.status = {EngineKvError::InvalidState};
+            return result;
+        }
+        KvCacheError const appended = m.append(request_id, n);
+        if (appended != KvCacheError::None) {
+            static_cast<void>(m.releasePageLease(before.lease_id));
+            result.status = mapMetadata(appended);
+            return result;
+        }
+        PageLeaseAcquireResult after = m.acquireRequestReadLease(request_id);
+        auto cancel = [&](EngineKvStatus why) {
+            if (after.ok()) static_cast<void>(m.releasePageLease(after.lease_id));
+            static_cast<void>(m.releasePageLease(before.lease_id));
+            static_cast<void>(m.releaseRequest(request_id));
+            state_->committed_lengths.erase(request_id);
+            result.status = why;
+            return std::move(result);
+        };
+        if (!after.ok()) return cancel(mapMetadata(after.error));
+        if (!st.appendSegments(before.table, after.table, expected, n, impl->jobs, impl->offsets)) {
+            return cancel({EngineKvError::InvalidArgument});
+        }
+        if (st.consumeFailure(HipFailurePoint::Submission)) return cancel({EngineKvError::SubmissionFailed});
+        std::vector<kimkv_block_desc> d;
+        st.descriptors(after.table, d);
+        std::size_t const bytes = d.size() * sizeof(kimkv_block_desc);
+        std::size_t granted = 0;
+        void* mem = st.buffers().acquire(bytes, granted);
+        if (mem == nullptr) return cancel({EngineKvError::ResourceExhausted});
+        try {
+            impl->arena = std::make_shared<DescriptorArena>(state_, mem, granted);
+        } catch (...) {
+            st.buffers().release(mem, granted);
+            return cancel({EngineKvError::ResourceExhausted});
+        }
+        {
+            // Fenced by the chunk's first attention launch on this stream.
+            std::lock_guard<std::mutex> launch(st.launchMutex());
+            if (!st.ring().uploadTo(impl->arena->ptr, d.data(), bytes, stream)) {
+                return cancel({EngineKvError::SubmissionFailed});
+            }
+        }
+        state_->prefilling.insert(request_id);
+        impl->owner = state_;
+        impl->request = request_id;
+        impl->begin = expected;
+        impl->count = n;
+        impl->stream = stream;
+        impl->lease_before = before.lease_id;
+        impl->lease_after = after.lease_id;
+        impl->descriptors = static_cast<kimkv_block_desc const*>(impl->arena->ptr);
+        impl->desc_count = static_cast<std::uint32_t>(d.size());
+        result.chunk = PrefillChunk(std::move(impl));
+        result.status = {};
+        return result;
     }
 
     // Shuffles a pool's free list with a seeded permutation (benchmarks: page
@@ -975,6 +1366,18 @@ bool reserveTokenBatch(EngineKvBackend& backend, ReserveTokenRequest const* requ
     if (b == nullptr) return false;
     b->reserveBatch(requests, count, results);
     return true;
+}
+
+PrefillChunkResult beginPrefillChunk(EngineKvBackend& backend, RequestId request_id, std::uint32_t expected,
+                                     std::uint32_t token_count, HipStream stream)
+{
+    auto* b = dynamic_cast<HipEngineKvBackend*>(&backend);
+    if (b == nullptr) {
+        PrefillChunkResult r;
+        r.status = {EngineKvError::InvalidArgument};
+        return r;
+    }
+    return b->beginPrefill(request_id, expected, token_count, stream);
 }
 
 EngineKvStatus permuteEngineFreeSlots(EngineKvBackend& backend, PageKind kind, std::uint64_t seed)

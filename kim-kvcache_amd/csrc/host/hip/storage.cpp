@@ -356,15 +356,15 @@ struct TempDevice {
 
 }  // namespace
 
-bool HipKvStorage::appendJobs(BlockTable const& before, BlockTable const& after, std::uint32_t begin,
-                              std::uint32_t count, KvScalar const* input, std::vector<kimkv_append_job>& jobs) const
+bool HipKvStorage::appendSegments(BlockTable const& before, BlockTable const& after, std::uint32_t begin,
+                                  std::uint32_t count, std::vector<kimkv_append_job>& jobs,
+                                  std::vector<std::uint32_t>& token_offsets) const
 {
     std::uint64_t const end = static_cast<std::uint64_t>(begin) + count;
-    if (input == nullptr || count == 0 || end > 0xFFFFFFFFull || !validTable(before) || !validTable(after)
+    if (count == 0 || end > 0xFFFFFFFFull || !validTable(before) || !validTable(after)
         || before.tokenCount() != begin || after.tokenCount() != end) {
         return false;
     }
-    std::size_t const hd = static_cast<std::size_t>(layout_.kv_head_count) * layout_.head_dimension;
     // Copy-on-write source of the replaced partial tail, if any.
     PageHandle cow_src = PageHandle::invalid();
     std::uint16_t cow_tokens = 0;
@@ -390,14 +390,8 @@ bool HipKvStorage::appendJobs(BlockTable const& before, BlockTable const& after,
         std::uint32_t const se = std::min(static_cast<std::uint32_t>(end), e.logicalTokenEnd());
         if (sb >= se) continue;
         kimkv_append_job j{};
-        std::size_t const off = static_cast<std::size_t>(sb - begin) * hd;
-        j.src_key = input + off;
-        j.src_value = input + static_cast<std::size_t>(count) * hd + off;
-        j.src_layer_stride = 2ull * count * hd;
-        j.src_token_stride = static_cast<std::uint32_t>(hd);
-        j.layer_begin = 0;
-        j.layer_count = layout_.layer_count;
         j.token_count = se - sb;
+        token_offsets.push_back(sb - begin);
         j.dst_slot = e.handle.slot;
         j.dst_kind = static_cast<std::uint8_t>(e.kind);
         j.dst_token = static_cast<std::uint16_t>(sb - e.logical_token_begin);
@@ -409,6 +403,27 @@ bool HipKvStorage::appendJobs(BlockTable const& before, BlockTable const& after,
         jobs.push_back(j);
     }
     return jobs.size() > first;
+}
+
+bool HipKvStorage::appendJobs(BlockTable const& before, BlockTable const& after, std::uint32_t begin,
+                              std::uint32_t count, KvScalar const* input, std::vector<kimkv_append_job>& jobs) const
+{
+    if (input == nullptr) return false;
+    std::size_t const first = jobs.size();
+    std::vector<std::uint32_t> offsets;
+    if (!appendSegments(before, after, begin, count, jobs, offsets)) return false;
+    std::size_t const hd = static_cast<std::size_t>(layout_.kv_head_count) * layout_.head_dimension;
+    for (std::size_t k = first; k < jobs.size(); ++k) {
+        kimkv_append_job& j = jobs[k];
+        std::size_t const off = static_cast<std::size_t>(offsets[k - first]) * hd;
+        j.src_key = input + off;
+        j.src_value = input + static_cast<std::size_t>(count) * hd + off;
+        j.src_layer_stride = 2ull * count * hd;
+        j.src_token_stride = static_cast<std::uint32_t>(hd);
+        j.layer_begin = 0;
+        j.layer_count = layout_.layer_count;
+    }
+    return true;
 }
 
 HipStatus HipKvStorage::launchAppendJobs(std::vector<kimkv_append_job> const& jobs, HipStream stream)

@@ -160,7 +160,18 @@ public:
 
 private:
     [[nodiscard]] HipStatus finish(HipStream stream, HipStatus submitted) noexcept;
-    // Jobs of one request's append (validates both tables and the COW rule).
+public:
+    // Segments of one request's append [begin, begin + count): one job per
+    // touched entry with destination, token count and copy-on-write source
+    // filled in (validates both tables and the COW rule); token_offsets gets
+    // each job's first token relative to `begin`.  Sources are left to the
+    // caller.
+    [[nodiscard]] bool appendSegments(BlockTable const& before, BlockTable const& after, std::uint32_t begin,
+                                      std::uint32_t count, std::vector<kimkv_append_job>& jobs,
+                                      std::vector<std::uint32_t>& token_offsets) const;
+
+private:
+    // Jobs of one request's append from a [layer][K/V][count][head][dim] input.
     [[nodiscard]] bool appendJobs(BlockTable const& before, BlockTable const& after, std::uint32_t begin,
                                   std::uint32_t count, KvScalar const* input,
                                   std::vector<kimkv_append_job>& jobs) const;

@@ -45,6 +45,13 @@ APPEND_JOB = np.dtype({
     "offsets": [0, 8, 16, 24, 28, 32, 36, 40, 44, 48, 50, 52, 53],
     "itemsize": 56,
 })
+PREFILL_ITEM = np.dtype({
+    "names": ["descriptors", "descriptor_count", "token_count", "new_tokens", "layer", "query", "output",
+              "attention_scale"],
+    "formats": ["<u8", "<u4", "<u4", "<u4", "<u4", "<u8", "<u8", "<f4"],
+    "offsets": [0, 8, 12, 16, 20, 24, 32, 40],
+    "itemsize": 48,
+})
 PROMOTION_JOB = np.dtype({
     "names": ["micro_slots", "extent_slot"],
     "formats": [("<u4", (8,)), "<u4"],
@@ -115,6 +122,9 @@ _SIGNATURES = {
     "kimkv_paged_decode_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                 ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                 ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_prefill_tokens_per_block": (ctypes.c_uint32, [ctypes.c_void_p, ctypes.c_uint32]),
+    "kimkv_paged_prefill_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
+                                                 ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]),
     "kimkv_reference_attention": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "kimkv_decode_timing": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
@@ -338,6 +348,21 @@ class Storage:
         check(lib().kimkv_paged_decode_batch(self.h, ctypes.c_void_p(items_ptr), ctypes.c_void_p(prefix_ptr),
                                              lanes, total_chunks, chunk_tokens, query_heads, _sh(stream)),
               "paged_decode_batch")
+
+    def prefill_plan(self, new_token_counts, query_heads: int):
+        """(tokens per workgroup, workgroup prefix over items, total workgroups)."""
+        per = int(lib().kimkv_prefill_tokens_per_block(self.h, query_heads))
+        if per == 0:
+            raise KimkvError("prefill_tokens_per_block", 1)
+        counts = np.asarray(new_token_counts, dtype=np.uint64)
+        prefix = np.zeros(len(counts) + 1, dtype=np.uint32)
+        prefix[1:] = np.cumsum((counts + per - 1) // per)
+        return per, prefix, int(prefix[-1])
+
+    def prefill_launch(self, items_ptr: int, prefix_ptr: int, item_count: int, total_blocks: int, query_heads: int,
+                       stream: Optional[Stream] = None) -> None:
+        check(lib().kimkv_paged_prefill_batch(self.h, ctypes.c_void_p(items_ptr), ctypes.c_void_p(prefix_ptr),
+                                              item_count, total_blocks, query_heads, _sh(stream)), "paged_prefill_batch")
 
     def destroy(self) -> None:
         if self.handle:

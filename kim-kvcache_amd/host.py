@@ -103,6 +103,15 @@ _SIG = {
                                         ctypes.POINTER(I)]),
     "kimkv_write_layer_batch": (None, [ctypes.POINTER(P), ctypes.POINTER(U32), ctypes.POINTER(P), ctypes.POINTER(P),
                                        U32, ctypes.POINTER(I)]),
+    "kimkv_engine_prefill_begin": (I, [P, U64, U32, U32, P, ctypes.POINTER(P)]),
+    "kimkv_prefill_write_layer": (I, [P, U32, P, P]),
+    "kimkv_prefill_attend_layer": (I, [P, U32, P, P, ctypes.c_float]),
+    "kimkv_prefill_finish": (I, [P]),
+    "kimkv_prefill_destroy": (None, [P]),
+    "kimkv_prefill_write_batch": (None, [ctypes.POINTER(P), U32, U32, ctypes.POINTER(P), ctypes.POINTER(P),
+                                         ctypes.POINTER(I)]),
+    "kimkv_prefill_attend_batch": (None, [ctypes.POINTER(P), U32, U32, ctypes.POINTER(P), ctypes.POINTER(P),
+                                          ctypes.c_float, ctypes.POINTER(I)]),
     "kimkv_cache_create": (P, [device.Layout, U32, U32]),
     "kimkv_cache_destroy": (None, [P]),
     "kimkv_cache_status": (I, [P]),
@@ -231,6 +240,48 @@ def write_layer_batch(txns: Sequence[Transaction], layers, keys, values) -> List
     return list(st)
 
 
+class PrefillChunk:
+    """A multi-token prompt chunk of one request (kimkv_engine_prefill_begin)."""
+
+    def __init__(self, handle: int, begin: int, count: int):
+        self.h, self.begin, self.count = handle, begin, count
+
+    def write_layer(self, layer: int, key: int, value: int) -> int:
+        return lib().kimkv_prefill_write_layer(self.h, layer, key, value)
+
+    def attend_layer(self, layer: int, query: int, output: int, scale: float) -> int:
+        return lib().kimkv_prefill_attend_layer(self.h, layer, query, output, scale)
+
+    def finish(self) -> int:
+        return lib().kimkv_prefill_finish(self.h)
+
+    def close(self) -> None:
+        if self.h:
+            lib().kimkv_prefill_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def prefill_write_batch(chunks: Sequence[PrefillChunk], layer: int, keys, values) -> List[int]:
+    n = len(chunks)
+    st = (I * n)()
+    lib().kimkv_prefill_write_batch((P * n)(*[c.h for c in chunks]), n, layer, (P * n)(*keys), (P * n)(*values), st)
+    return list(st)
+
+
+def prefill_attend_batch(chunks: Sequence[PrefillChunk], layer: int, queries, outputs, scale: float) -> List[int]:
+    n = len(chunks)
+    st = (I * n)()
+    lib().kimkv_prefill_attend_batch((P * n)(*[c.h for c in chunks]), n, layer, (P * n)(*queries),
+                                     (P * n)(*outputs), scale, st)
+    return list(st)
+
+
 class Engine:
     """createHeterogeneousHipEngineKvBackend through the C facade."""
 
@@ -260,6 +311,12 @@ class Engine:
         s = EngineSnapshot()
         lib().kimkv_engine_get_snapshot(self.h, ctypes.byref(s))
         return s
+
+    def prefill_begin(self, rid, expected, token_count, stream: Optional[device.Stream] = None):
+        out = P()
+        rc = lib().kimkv_engine_prefill_begin(self.h, rid, expected, token_count,
+                                              stream.handle if stream else None, ctypes.byref(out))
+        return rc, (PrefillChunk(out.value, expected, token_count) if rc == 0 else None)
 
     def append_prefill(self, rid, token_count, device_kv, stream: Optional[device.Stream] = None, promote=True):
         n = U32()

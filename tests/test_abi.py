@@ -33,6 +33,7 @@ def test_struct_layouts_match_reference_sizes(kimkv):
     assert d.DECODE_ITEM.itemsize == 56     # DevicePagedDecodeBatchItem (engine_kv.h:172-191)
     assert d.APPEND_JOB.itemsize == 56
     assert d.PROMOTION_JOB.itemsize == 36   # PromotionSlots + target slot
+    assert d.PREFILL_ITEM.itemsize == 48
 
 
 def test_host_synth_matches_oracle(kimkv):

@@ -464,3 +464,182 @@ def test_engine_prefill_promotion_then_decode(host, dev):
     assert engine.release_request(5) == 0
     assert engine.check_invariants()
     stream.destroy()
+
+
+# --- chunked prefill through the engine -------------------------------------------------------------------
+
+def _causal_oracle(K, V, Q, t0, scale, G):
+    """fp64 causal GQA: K, V [T][kv][D] f32, Q [n][QH][D] f32; row i attends the first t0 + i + 1 tokens."""
+    n = Q.shape[0]
+    T = K.shape[0]
+    out = np.zeros(Q.shape, dtype=np.float64)
+    Kd, Vd, Qd = K.astype(np.float64), V.astype(np.float64), Q.astype(np.float64)
+    for h in range(Q.shape[1]):
+        s = Qd[:, h, :] @ Kd[:, h // G, :].T * scale                     # [n][T]
+        s[np.arange(T)[None, :] > (t0 + np.arange(n))[:, None]] = -np.inf
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h, :] = (p @ Vd[:, h // G, :]) / p.sum(axis=1, keepdims=True)
+    return out
+
+
+def test_engine_prefill_chunks_batched(host, dev):
+    """Chunks of 37 / 64 / 200 prompt tokens on contexts of 0 / 100 / 1000 tokens
+    and on a fork child sharing a partial tail (COW), advanced layer by layer with
+    one write launch and one attention launch per layer for all chunks.  Every
+    output row matches an fp64 causal GQA (2e-3 abs + 1e-3 rel), the gathered
+    KV is bit-exact afterwards and a decode token then matches the oracle."""
+    L, H, D, QH = 3, 4, 64, 32
+    G = QH // H
+    scale = 1.0 / math.sqrt(D)
+    engine = host.Engine(L, H, D, QH, 1 << 16, 512, 64)
+    assert engine.permute_free_slots(1, 5) == 0 and engine.permute_free_slots(0, 6) == 0
+    rng = np.random.default_rng(17)
+    stream = dev.Stream()
+    contexts = {1: 0, 2: 100, 3: 1000}
+    kv = {}
+    keep = []
+    for rid, t0 in contexts.items():
+        assert engine.create_request(rid) == 0
+        kv[rid] = f16(*rng.uniform(-1, 1, L * 2 * t0 * H * D)).reshape(L, 2, t0, H, D)
+        if t0:
+            src = dev.upload(kv[rid].reshape(-1), stream)
+            keep.append(src)
+            rc, _ = engine.append_prefill(rid, t0, src.ptr, stream, promote=True)
+            assert rc == 0, host.ENGINE_ERRORS[rc]
+    assert engine.fork_request(2, 4) == 0            # shares request 2's partial micro tail
+    kv[4] = kv[2].copy()
+    contexts[4] = 100
+    chunk_tokens = {1: 37, 2: 64, 3: 200, 4: 45}
+
+    chunks, new_kv, queries, outs = {}, {}, {}, {}
+    for rid, n in chunk_tokens.items():
+        rc, c = engine.prefill_begin(rid, contexts[rid], n, stream)
+        assert rc == 0, host.ENGINE_ERRORS[rc]
+        chunks[rid] = c
+        new_kv[rid] = f16(*rng.uniform(-1, 1, L * 2 * n * H * D)).reshape(L, 2, n, H, D)
+        queries[rid] = f16(*rng.uniform(-1, 1, L * n * QH * D)).reshape(L, n, QH, D)
+        outs[rid] = [dev.DeviceBuffer(n * QH * D * 2) for _ in range(L)]
+    # An open chunk blocks every other mutation of its request.
+    rc, _ = engine.reserve_token(3, 1000 + 200, stream)
+    assert host.ENGINE_ERRORS[rc] == "invalid_state"
+    assert host.ENGINE_ERRORS[engine.release_request(3)] == "invalid_state"
+    assert host.ENGINE_ERRORS[engine.fork_request(3, 9)] == "invalid_state"
+    rc, _ = engine.prefill_begin(3, 1000, 8, stream)
+    assert host.ENGINE_ERRORS[rc] == "invalid_state"
+
+    order = list(chunk_tokens)
+    dkv = {rid: dev.upload(new_kv[rid].reshape(-1), stream) for rid in order}
+    dq = {rid: dev.upload(queries[rid].reshape(-1), stream) for rid in order}
+    per_layer = {rid: chunk_tokens[rid] * H * D * 2 for rid in order}
+    for layer in range(L):
+        keys = [dkv[r].ptr + (layer * 2) * per_layer[r] for r in order]
+        values = [dkv[r].ptr + (layer * 2 + 1) * per_layer[r] for r in order]
+        st = host.prefill_write_batch([chunks[r] for r in order], layer, keys, values)
+        assert st == [0] * len(order), st
+        qs = [dq[r].ptr + layer * chunk_tokens[r] * QH * D * 2 for r in order]
+        st = host.prefill_attend_batch([chunks[r] for r in order], layer, qs, [outs[r][layer].ptr for r in order],
+                                       scale)
+        assert st == [0] * len(order), st
+    for rid in order:
+        assert chunks[rid].finish() == 0
+        chunks[rid].close()
+    assert engine.check_invariants()
+    assert engine.snapshot().committed_token_count == sum(contexts[r] + chunk_tokens[r] for r in order)
+
+    worst = 0.0
+    for rid in order:
+        t0, n = contexts[rid], chunk_tokens[rid]
+        full = np.concatenate([kv[rid], new_kv[rid]], axis=2)            # [L][2][T][H][D]
+        for layer in range(L):
+            want = _causal_oracle(to_f32(full[layer, 0]), to_f32(full[layer, 1]), to_f32(queries[rid][layer]),
+                                  t0, scale, G)
+            got = to_f32(dev.download(outs[rid][layer].ptr, (n, QH, D), np.uint16))
+            err = np.abs(got - want)
+            assert np.all(err <= 2e-3 + 1e-3 * np.abs(want)), (rid, layer, float(err.max()))
+            worst = max(worst, float(err.max()))
+        _, entries = engine.block_table(rid)
+        descs = host.descriptors_from_entries(entries)
+        d = dev.upload(descs, stream)
+        T = t0 + n
+        out = dev.DeviceBuffer(full.nbytes)
+        dev.check(dev.lib().kimkv_gather(ctypes.c_void_p(engine.storage_handle()), ctypes.c_void_p(d.ptr),
+                                         len(descs), T, ctypes.c_void_p(out.ptr), ctypes.c_void_p(stream.handle)),
+                  "gather")
+        assert np.array_equal(dev.download(out.ptr, full.shape, np.uint16, stream), full), rid
+        kv[rid] = full
+    print(f"engine prefill chunks max_err={worst:.2e}", flush=True)
+
+    # A decode token after the prompt chunks (request 3, 1200 tokens).
+    buf = Buffers(dev, layers=L, kv=H, qh=QH, dim=D, workspace=1 << 16)
+    rc, txn = engine.reserve_token(3, 1200, stream)
+    assert rc == 0, host.ENGINE_ERRORS[rc]
+    new = [(f16(*rng.uniform(-1, 1, H * D)), f16(*rng.uniform(-1, 1, H * D))) for _ in range(L)]
+    q = f16(*rng.uniform(-1, 1, QH * D))
+    dev.copy_to_device(buf.query.ptr, q, stream)
+    for layer in range(L):
+        dev.copy_to_device(buf.keys[layer].ptr, new[layer][0], stream)
+        dev.copy_to_device(buf.values[layer].ptr, new[layer][1], stream)
+        assert txn.write_layer(layer, buf.keys[layer].ptr, buf.values[layer].ptr) == 0
+        assert txn.attend_layer(layer, buf.query.ptr, buf.output.ptr, buf.workspace.ptr, buf.workspace_bytes,
+                                scale) == 0
+    assert txn.commit() == 0
+    hist = [[(kv[3][l, 0, t].reshape(-1), kv[3][l, 1, t].reshape(-1)) for l in range(L)] for t in range(1200)]
+    want = _oracle_lane(hist + [new], L - 1, q, QH, H, D, scale)
+    got = to_f32(dev.download(buf.output.ptr, (QH * D,), np.uint16))
+    assert np.all(np.abs(got - want) <= 2e-3 + 1e-3 * np.abs(want))
+    for rid in order:
+        assert engine.release_request(rid) == 0
+    snap = engine.snapshot()
+    assert snap.request_count == 0 and snap.allocated_primary_pages == 0 and snap.allocated_secondary_pages == 0
+    stream.destroy()
+
+
+def test_engine_prefill_chunk_errors(host, dev):
+    """Layer order, an abandoned chunk and an injected submission failure: the
+    last two cancel the request, exactly like a failed bulk append."""
+    L, H, D, QH = 2, 2, 64, 4
+    engine = host.Engine(L, H, D, QH, 1 << 16, 64, 8)
+    stream = dev.Stream()
+    n = 20
+    k = dev.upload(f16(*np.linspace(-1, 1, n * H * D)), stream)
+    q = dev.upload(f16(*np.linspace(1, -1, n * QH * D)), stream)
+    o = dev.DeviceBuffer(n * QH * D * 2)
+    assert engine.create_request(1) == 0
+    rc, c = engine.prefill_begin(1, 5, n, stream)
+    assert host.ENGINE_ERRORS[rc] == "invalid_state"          # committed length is 0
+    rc, c = engine.prefill_begin(1, 0, n, stream)
+    assert rc == 0
+    assert host.ENGINE_ERRORS[c.attend_layer(0, q.ptr, o.ptr, 0.125)] == "layer_out_of_order"
+    assert host.ENGINE_ERRORS[c.write_layer(1, k.ptr, k.ptr)] == "layer_out_of_order"
+    assert c.write_layer(0, k.ptr, k.ptr) == 0
+    assert host.ENGINE_ERRORS[c.write_layer(0, k.ptr, k.ptr)] == "layer_out_of_order"
+    assert c.attend_layer(0, q.ptr, o.ptr, 0.125) == 0
+    assert host.ENGINE_ERRORS[c.finish()] == "invalid_state"  # abandoned after layer 0
+    c.close()
+    assert host.ENGINE_ERRORS[engine.release_request(1)] == "request_not_found"
+    assert engine.snapshot().allocated_primary_pages == 0
+
+    assert engine.create_request(2) == 0
+    rc, c = engine.prefill_begin(2, 0, n, stream)
+    assert rc == 0
+    assert engine.inject_failure_once("submission")
+    assert c.write_layer(0, k.ptr, k.ptr) == SUBMISSION_FAILED
+    assert c.finish() == SUBMISSION_FAILED
+    c.close()
+    assert host.ENGINE_ERRORS[engine.release_request(2)] == "request_not_found"
+
+    assert engine.create_request(3) == 0
+    rc, c = engine.prefill_begin(3, 0, n, stream)
+    assert rc == 0
+    for layer in range(L):
+        assert c.write_layer(layer, k.ptr, k.ptr) == 0
+        assert c.attend_layer(layer, q.ptr, o.ptr, 0.125) == 0
+    assert c.finish() == 0
+    assert c.finish() == 0                                      # idempotent
+    c.close()
+    assert engine.snapshot().committed_token_count == n
+    assert engine.release_request(3) == 0
+    assert engine.check_invariants()
+    snap = engine.snapshot()
+    assert snap.request_count == 0 and snap.allocated_primary_pages == 0
+    stream.destroy()

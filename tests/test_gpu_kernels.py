@@ -236,3 +236,70 @@ def test_fill_kv_block_matches_oracle(dev):
         for c in range(2):
             want = oracle.synth_rows(T * cols, seed, oracle.kv_row(sid, l, c, t0), cols).reshape(T, cols)
             assert np.array_equal(got[l, c], want)
+
+
+# ---- chunked prefill ---------------------------------------------------------------
+
+def _prefill_case(dev, shape, cases, G, micro_tokens=8, extent_tokens=64, seed=21, uniform_pages=False):
+    """cases: list of (T0, n): a table of T0 + n tokens whose last n are the chunk.  Every new token's
+    output must match the oracle's decode of the first T0 + i + 1 tokens with that token's query."""
+    L, H, D = shape
+    QH = H * G
+    totals = [t0 + n for t0, n in cases]
+    micro_cap = sum(t // micro_tokens + 2 for t in totals) + 8
+    ext_cap = sum(t // extent_tokens + 1 for t in totals) + 2
+    storage = dev.Storage(L, H, D, micro_cap, ext_cap, micro_tokens, extent_tokens)
+    pools = oracle.HostPools(L, H, D, micro_cap, ext_cap, micro_tokens, extent_tokens)
+    alloc = helpers.SlotAllocator(micro_cap, ext_cap, seed=seed, micro_tokens=micro_tokens,
+                                  extent_tokens=extent_tokens)
+    per, prefix, total = storage.prefill_plan([n for _, n in cases], QH)
+    items = np.zeros(len(cases), dtype=dev.PREFILL_ITEM)
+    keep, outs, lanes = [], [], []
+    scale = 1.0 / math.sqrt(D)
+    for i, (t0, n) in enumerate(cases):
+        T = t0 + n
+        table = helpers.uniform_table(T, micro_tokens, alloc) if uniform_pages else helpers.hetero_table(T, alloc)
+        inp = _input(L, H, D, T, seed=seed * 100 + i)
+        keep.append(_populate(dev, storage, pools, table, inp))
+        q = oracle.synth_rows(n * QH * D, seed * 1000 + i, 0, D)
+        layer = (i * 5) % L
+        dbuf, qbuf = dev.upload(table), dev.upload(q)
+        obuf = dev.DeviceBuffer(n * QH * D * 2)
+        items[i] = (dbuf.ptr, len(table), T, n, layer, qbuf.ptr, obuf.ptr, scale)
+        keep += [dbuf, qbuf]
+        outs.append(obuf)
+        lanes.append((table, t0, n, layer, q))
+    ibuf, pbuf = dev.upload(items), dev.upload(prefix)
+    storage.prefill_launch(ibuf.ptr, pbuf.ptr, len(cases), total, QH)
+    dev.sync()
+    worst = 0.0
+    for (table, t0, n, layer, q), obuf in zip(lanes, outs):
+        got = dev.download(obuf.ptr, (n, QH * D), np.uint16)
+        for i in range(n):
+            want = pools.paged_decode(table, t0 + i + 1, layer, QH, q[i * QH * D:(i + 1) * QH * D], scale, f32=True)
+            worst = max(worst, helpers.assert_attention_close(got[i], want))
+    print(f"prefill shape={shape} G={G} cases={cases} per_block={per} blocks={total} max_err={worst:.2e}",
+          flush=True)
+
+
+def test_prefill_causal_matches_per_token_decode(dev):
+    """TinyLlama GQA (G=8): chunks at the start of a context, after micro and extent pages, ragged."""
+    _prefill_case(dev, (2, 4, 64), [(0, 1), (0, 37), (100, 64), (1000, 200), (5, 7), (64, 130)], G=8)
+
+
+def test_prefill_group_sizes(dev):
+    _prefill_case(dev, (2, 4, 64), [(30, 50), (200, 17)], G=1, seed=22)
+    _prefill_case(dev, (2, 2, 64), [(70, 33), (0, 20)], G=4, seed=23)
+    _prefill_case(dev, (2, 2, 64), [(129, 40)], G=16, seed=24)
+
+
+def test_prefill_long_context_segments(dev):
+    """Keys beyond one 8192-token group-table segment."""
+    _prefill_case(dev, (1, 4, 64), [(9000, 40)], G=8, seed=25)
+
+
+def test_prefill_generic_paths(dev):
+    _prefill_case(dev, (2, 2, 128), [(90, 20)], G=2, seed=26)                 # D != 64
+    _prefill_case(dev, (2, 1, 64), [(50, 9)], G=3, seed=27)                   # G does not divide 16
+    _prefill_case(dev, (2, 4, 64), [(17, 30)], G=8, micro_tokens=6, extent_tokens=48, seed=28,
+                  uniform_pages=True)                                          # unaligned pages
