@@ -709,6 +709,136 @@ def run_shared(kimkv, dev, args) -> int:
     return 0 if ok else 1
 
 
+PEAK_MFMA_F16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+
+
+def run_prefill(kimkv, dev, args) -> int:
+    """Chunked prefill through the engine: --prefill-lanes requests whose
+    contexts hold T0 ~ U[256, 2048] (seeded) prompt tokens take one
+    --prefill-chunk-token chunk each per step.  Each step forks every base
+    request (the fork's partial tail is copied on write), then per layer one
+    batched K/V write and one batched causal GQA prefill-attention launch for
+    all chunks, finishes the chunks and releases the forks, so every step does
+    the same work.  Roofline: attention FLOPs per launch (4 * QH * D per
+    (query, visible key) pair) over the prefill kernel's event-timed duration,
+    against dense fp16 MFMA peak."""
+    import importlib
+    host = importlib.import_module(kimkv.__name__ + ".host")
+    L, H, D, QH = args.layers, 4, 64, 32
+    HD, QD = H * D, QH * D
+    lanes, n = args.prefill_lanes, args.prefill_chunk
+    rng = np.random.default_rng(args.seed)
+    T0 = rng.integers(256, 2049, lanes)
+    if args.prefill_context:
+        T0[:] = args.prefill_context
+    total_steps = args.warmup + args.steps
+    n_ext = int(sum((T0 + n) // 64)) * 2 + 16
+    n_micro = 1024 + lanes * (n // 8 + 4) * 2
+    engine = host.Engine(L, H, D, QH, 1 << 16, n_micro, n_ext)
+    for kind, sd in ((1, args.seed), (0, args.seed + 1)):
+        assert engine.permute_free_slots(kind, sd) == 0
+    stream = dev.Stream()
+    stage = dev.DeviceBuffer(L * 2 * int(T0.max()) * HD * 2)
+    for i in range(lanes):
+        assert engine.create_request(i + 1) == 0
+        dev.fill_kv(stage.ptr, L, int(T0[i]), HD, args.seed, i, 0, stream)
+        rc, _ = engine.append_prefill(i + 1, int(T0[i]), stage.ptr, stream, promote=True)
+        assert rc == 0, host.ENGINE_ERRORS[rc]
+    # Chunk inputs: K/V [lane][L][2][n][HD] (rows kv_row(lane, l, c, T0 + t)), queries [lane][L][n][QD].
+    kv = dev.DeviceBuffer(lanes * L * 2 * n * HD * 2)
+    q = dev.DeviceBuffer(lanes * L * n * QD * 2)
+    out = dev.DeviceBuffer(lanes * L * n * QD * 2)
+    qseed = args.seed ^ 0x5155455259
+    for i in range(lanes):
+        dev.fill_kv(kv.ptr + i * L * 2 * n * HD * 2, L, n, HD, args.seed, i, int(T0[i]), stream)
+        for l in range(L):
+            dev.fill_rows(q.ptr + ((i * L + l) * n * QD) * 2, n * QD, qseed, dev.synth_kv_row(i, l, 0, 0), QD)
+    stream.synchronize()
+    scale = 1.0 / math.sqrt(D)
+
+    def kv_ptr(i, l, c):
+        return kv.ptr + (((i * L + l) * 2 + c) * n * HD) * 2
+
+    def step(s_):
+        base = 1000 * (s_ + 1)
+        chunks = []
+        for i in range(lanes):
+            assert engine.fork_request(i + 1, base + i) == 0
+            rc, c = engine.prefill_begin(base + i, int(T0[i]), n, stream)
+            assert rc == 0, host.ENGINE_ERRORS[rc]
+            chunks.append(c)
+        for l in range(L):
+            st = host.prefill_write_batch(chunks, l, [kv_ptr(i, l, 0) for i in range(lanes)],
+                                          [kv_ptr(i, l, 1) for i in range(lanes)])
+            assert st == [0] * lanes, st
+            st = host.prefill_attend_batch(chunks, l, [q.ptr + ((i * L + l) * n * QD) * 2 for i in range(lanes)],
+                                           [out.ptr + ((i * L + l) * n * QD) * 2 for i in range(lanes)], scale)
+            assert st == [0] * lanes, st
+        for i, c in enumerate(chunks):
+            assert c.finish() == 0
+            c.close()
+            assert engine.release_request(base + i) == 0
+
+    for s_ in range(args.warmup):
+        step(s_)
+    stream.synchronize()
+    start, stop = dev.Event(), dev.Event()
+    dev.prefill_timing(True)
+    t_wall = time.perf_counter()
+    start.record(stream)
+    for s_ in range(args.warmup, total_steps):
+        step(s_)
+    stop.record(stream)
+    stop.synchronize()
+    wall_ms = (time.perf_counter() - t_wall) * 1000.0
+    pf_ms, pf_n = dev.prefill_timing(False)
+    ms_per_step = max(start.elapsed_ms(stop), wall_ms) / args.steps
+    kernel_ms = pf_ms / max(pf_n, 1)
+    pairs = float(sum(n * int(t) + n * (n + 1) // 2 for t in T0))     # (query, visible key) pairs per layer
+    flops = 4.0 * QH * D * pairs
+    kv_bytes = float(sum(int(t) + n for t in T0)) * 2 * HD * 2 + 2 * lanes * n * QD * 2
+    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    # Check sampled rows of layers 0 and L-1 against the oracle's decode of the first T0 + r + 1 tokens.
+    import oracle
+    worst, ok, rows = 0.0, True, 0
+    for i in range(lanes):
+        t0 = int(T0[i])
+        for l in (0, L - 1):
+            kvl = np.empty((2, t0 + n, H, D), dtype=np.uint16)
+            for c in range(2):
+                kvl[c, :t0] = oracle.synth_rows(t0 * HD, args.seed, oracle.kv_row(i, l, c, 0), HD).reshape(t0, H, D)
+                kvl[c, t0:] = oracle.synth_rows(n * HD, args.seed, oracle.kv_row(i, l, c, t0), HD).reshape(n, H, D)
+            ql = oracle.synth_rows(n * QD, qseed, oracle.kv_row(i, l, 0, 0), QD).reshape(n, QD)
+            got = dev.download(out.ptr + ((i * L + l) * n * QD) * 2, (n, QD), np.uint16)
+            for r in (0, n // 2, n - 1):
+                T = t0 + r + 1
+                ref = oracle_decode_layer(kvl[:, :T], T, ql[r], QH, D)
+                err = np.abs(got[r].view(np.float16).astype(np.float32) - ref)
+                worst = max(worst, float(err.max()))
+                ok = ok and bool(np.all(err <= 2e-3 + 1e-3 * np.abs(ref)))
+                rows += 1
+    print(json.dumps({
+        "metric": "chunked-prefill causal paged GQA attention (MFMA) TFLOP/s",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "higher_is_better": True,
+        "prompt_tokens_per_s": round(lanes * n / (ms_per_step * 1e-3), 1),
+        "ms_per_step": round(ms_per_step, 3), "us_per_layer": round(ms_per_step * 1000.0 / L, 2),
+        "prefill_kernel_avg_us": round(kernel_ms * 1000, 2), "prefill_launches": pf_n,
+        "dtype": "f16 in, f32 accumulate",
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None,
+                     "flops_per_launch": flops,
+                     "kv_q_o_bytes_per_launch": kv_bytes,
+                     "hbm_gb_per_s_if_read_once": round(kv_bytes / (kernel_ms * 1e-3) / 1e9, 1)},
+        "config": {"workload": f"{lanes} x {n}-token prefill chunks on contexts "
+                               f"{'U[256, 2048]' if not args.prefill_context else 'of'} "
+                               f"({', '.join(str(int(t)) for t in T0)}), {L} layers TinyLlama GQA 32q/4kv/64d fp16, "
+                               f"forked per step (partial-tail COW), through the engine"},
+        "steps": args.steps, "warmup": args.warmup,
+        "check": {"rows": rows, "layers": [0, L - 1], "max_abs_err": worst, "within_tolerance": ok,
+                  "tolerance": "2e-3 + 1e-3*|ref|"}}), flush=True)
+    return 0 if ok else 1
+
+
 def run_copy(dev, args) -> int:
     """Plain device-to-device copy of a known size: the achievable copy
     bandwidth of the box and the calibration run for the FETCH_SIZE /
@@ -765,10 +895,12 @@ def profiled_traffic(lanes_per_launch: int, context: int, layers: int):
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", choices=["decode", "gather", "append", "shared", "copy"], default="decode",
+    ap.add_argument("--config", choices=["decode", "gather", "append", "shared", "prefill", "copy"],
+                    default="decode",
                     help="decode: HBM-scale decode+append (the headline line); gather: long-sequence gather; "
                          "append: ragged one-token append with tail allocation; shared: fork/COW shared-prefix "
-                         "decode; copy: plain device copy (bandwidth and counter calibration)")
+                         "decode; prefill: chunked-prefill attention through the engine; copy: plain device copy (bandwidth "
+                         "and counter calibration)")
     ap.add_argument("--shared-check", type=int, default=4, help="lanes of the shared config checked")
     ap.add_argument("--append-lanes", type=int, default=64)
     ap.add_argument("--append-check", type=int, default=4, help="lanes gathered and compared bit-exactly")
@@ -779,6 +911,10 @@ def main() -> int:
                     help="engine path: lane groups pipelined against each other (1 = one batch per step)")
     ap.add_argument("--slots", choices=["permuted", "sequential"], default="permuted",
                     help="kernel path: page slots in seeded-permutation order (default) or in pool order")
+    ap.add_argument("--prefill-lanes", type=int, default=4)
+    ap.add_argument("--prefill-chunk", type=int, default=512)
+    ap.add_argument("--prefill-context", type=int, default=0,
+                    help="prefill: the same context for every lane instead of U[256, 2048]")
     ap.add_argument("--copy-mib", type=int, default=4096)
     ap.add_argument("--gather-tokens", type=int, default=16384)
     ap.add_argument("--gpus", type=int, default=1)
@@ -809,6 +945,8 @@ def main() -> int:
         return run_append(kimkv, dev, args)
     if args.config == "shared":
         return run_shared(kimkv, dev, args)
+    if args.config == "prefill":
+        return run_prefill(kimkv, dev, args)
     H, D, QH = 4, 64, 32
     total_steps = args.warmup + args.steps
     if args.path == "engine":

@@ -84,7 +84,8 @@ typedef struct kimkv_decode_item {
 /* One request's chunk of a multi-token causal prefill: the table holds
  * token_count tokens, of which the last new_tokens are the chunk; new token i
  * attends keys [0, token_count - new_tokens + i].  query / output are
- * [new_tokens][query_heads][head_dim] fp16.  No reference counterpart (the
+ * [new_tokens][query_heads][head_dim] fp16; query 16-byte and output 8-byte
+ * aligned (the kernel's vector accesses).  No reference counterpart (the
  * reference advances a prompt chunk one position at a time). */
 typedef struct kimkv_prefill_item {
     const kimkv_block_desc* descriptors;
@@ -272,6 +273,8 @@ kimkv_status kimkv_reference_attention(const kimkv_storage* storage,
 /* Average duration (ms) of the decode kernels launched since the last reset,
  * measured with events on the launch stream; for the benchmark's roofline. */
 kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launches);
+/* The same for the chunked-prefill attention kernel. */
+kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launches);
 
 /* ---- synthetic inputs (benchmarks and tests) ----------------------------- */
 

@@ -639,10 +639,10 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage, const kimkv_
     hipStream_t const s = native(stream);
     dim3 const grid(total_chunks, (storage->layout.kv_heads + kHeadsPerBlock - 1) / kHeadsPerBlock);
     void* start = nullptr;
-    decode_timing_begin(s, &start);
+    kernel_timing_begin(TimedKernel::Decode, s, &start);
     decode_kernel<<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix, lane_count,
                                           chunk_tokens, query_heads);
-    decode_timing_end(s, start);
+    kernel_timing_end(TimedKernel::Decode, s, start);
     kimkv_status const status = launch_status();
     if (status != KIMKV_OK) return status;
     if (total_chunks > lane_count) {

@@ -9,16 +9,21 @@
 // token i (0 <= i < n, position T - n + i of a table of T tokens whose last n
 // tokens are the chunk) attends keys [0, T - n + i] of its KV head.
 //
-// Work: block = (item, KV head, block of 4*tpw new tokens), one wave per tpw
-// tokens, where a wave's 16 MFMA columns are tpw tokens x G query heads
-// (tpw = 16 / G).  Each wave streams the keys up to its last token's position
-// in 64-token steps: S^T = K.Q^T and O^T += V^T.P^T on
-// v_mfma_f32_16x16x32_f16 (same operand layout as the decode kernel), online
-// softmax in base 2, fp32 accumulation, fp16 output.  Keys past a column's
-// causal limit are masked per column.  The group table (8-token groups of the
-// key range) is built in LDS one 8192-token segment at a time.  Tables that
-// do not keep 8-token groups aligned, head dims other than 64 and group sizes
-// that do not divide 16 take a one-row-at-a-time generic path.
+// Work: block = (item, KV head, 8 * tpw new tokens), 4 waves, each wave two
+// 16-column MFMA blocks whose columns are tpw tokens x G query heads
+// (tpw = 16 / G; TinyLlama's G = 8 gives 16 tokens = 256 query rows per
+// block).  The block walks the keys up to its last token's position in
+// 64-key tiles: all 256 threads load a tile's K and V^T (16 KiB) once into a
+// double-buffered, bank-swizzled LDS stage, and every wave runs
+// S^T = K.Q^T and O^T += V^T.P^T for its 32 columns on
+// v_mfma_f32_16x16x32_f16 (same operand layout as the decode kernel), with an
+// online softmax in base 2, fp32 accumulation and fp16 output, while the next
+// tile's loads are in flight.  Keys past a column's causal limit are masked
+// per column (only on the diagonal tiles).  The group table (8-token groups
+// of the key range, resolved to K and V^T pointers of the block's head) is
+// built in LDS one 4096-key segment at a time.
+// Tables that do not keep 8-token groups aligned, head dims other than 64 and
+// group sizes that do not divide 16 take a one-row-at-a-time generic path.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -31,184 +36,333 @@ namespace kimkv {
 namespace {
 
 constexpr unsigned kBlock = 256;   // 4 waves
+constexpr unsigned kWaves = kBlock / 64;
+constexpr unsigned kColBlocks = 2;  // 16-column MFMA blocks per wave
+constexpr unsigned kTileKeys = 64;
+constexpr float kLazyRescaleLog2 = 8.0f;
 
 struct PrefillShape {
-    uint32_t tpw;        // new tokens per wave
+    uint32_t tpw;        // new tokens per 16-column block
     uint32_t G;          // query heads per KV head
     bool mfma;           // D == 64 and G divides 16
 };
 
-__device__ inline PrefillShape prefill_shape(uint32_t QH, uint32_t H, uint32_t D)
+__host__ __device__ inline PrefillShape prefill_shape(uint32_t QH, uint32_t H, uint32_t D)
 {
     uint32_t const G = QH / H;
     bool const mfma = D == 64 && G >= 1 && G <= 16 && 16 % G == 0;
     return PrefillShape{mfma ? 16 / G : 1, G, mfma};
 }
 
-// One wave, fast path: new tokens [i0, i0 + tpw) x the G query heads of KV
-// head h; keys [s0, s1) of the current segment, whose groups are in `groups`
-// (group g covers keys s0 + 8g ..).
-struct PrefillWave {
-    uint32_t l, a, r, x;
-    bool qvalid;
-    uint32_t limit;          // last key this lane's column may see
-    uint64_t head_unit;
-    half8_t qb0, qb1;
-    float scale2;
-    float m_run, l_part;
-    float4_t acc[4];
+__host__ __device__ inline uint32_t prefill_block_tokens(PrefillShape s)
+{
+    return s.mfma ? kWaves * kColBlocks * s.tpw : kWaves;
+}
+
+// One 64-key tile of one KV head (D = 64) staged in LDS, in 16-byte units:
+//   K   unit (key t, dim octet o) at t * 8 + (o ^ k_swizzle(t))
+//   V^T unit (dim d, key octet c) at d * 8 + (c ^ (d & 7))
+// The swizzles put the eight 16-byte reads that one LDS cycle serves (lanes
+// 8j .. 8j + 7 of an MFMA operand read) on eight different bank groups.
+struct KvTile {
+    half8_t k[kTileKeys * 8];
+    half8_t v[64 * 8];
 };
 
-__device__ void prefill_wave_init(PrefillWave& w, const kimkv_prefill_item& item, uint32_t h, uint32_t G, uint32_t QH,
-                                  uint32_t i0)
+__device__ inline uint32_t k_swizzle(uint32_t t) { return (t & 3u) | (((t >> 3) & 1u) << 2); }
+__device__ inline uint32_t k_unit(uint32_t t, uint32_t o) { return t * 8u + (o ^ k_swizzle(t)); }
+__device__ inline uint32_t v_unit(uint32_t d, uint32_t c) { return d * 8u + (c ^ (d & 7u)); }
+
+// Keys per group-table segment of the prefill kernel (multiple of 64).
+constexpr unsigned kSegmentKeys = 4096;
+constexpr unsigned kSegmentGroups = kSegmentKeys / 8;
+
+// One 8-key group of the segment resolved for the block's layer and KV head:
+// k points at the group's first key in K panel 0 (panel 1, dims 32..63, is
+// kpanel elements further), v at the group's first key in V^T row 0 (dim d is
+// d * vw elements further).
+struct HeadGroup {
+    const uint16_t* k;
+    const uint16_t* v;
+    uint32_t kpanel;
+    uint32_t vw;
+    uint64_t pad;
+};
+
+// Records the 8-key groups of [c0, c1) that entry `e` covers, for layer /
+// head.  An entry whose pages do not keep 8-token groups aligned (or that
+// names no page of the storage) switches the block to the generic path.
+__device__ inline void add_head_groups(const PoolView& P, kimkv_block_desc const& e, uint32_t layer, uint32_t h,
+                                       uint32_t c0, uint32_t c1, uint32_t T, HeadGroup* groups, uint32_t* s_generic)
+{
+    uint32_t const b = e.logical_token_begin;
+    uint32_t const end = b + e.valid_tokens;
+    uint32_t const lo = max(b, c0);
+    uint32_t const hi = min(end, c1);
+    if (lo >= hi) return;
+    uint32_t const cap = e.page_token_capacity;
+    const uint16_t* page = page_base(P, e.kind, e.slot, cap);
+    bool const aligned = (b & 7u) == 0 && (cap & 7u) == 0 && e.valid_tokens <= cap
+        && ((end & 7u) == 0 || end >= T) && page != nullptr;
+    if (!aligned) {
+        *s_generic = 1;
+        return;
+    }
+    const uint16_t* hb = page + head_block(P, cap, layer, h);
+    uint32_t const vw = v_width(cap);
+    for (uint32_t g = (lo - c0) >> 3; g < (hi - c0 + 7) >> 3; ++g) {
+        uint32_t const pt0 = c0 + 8 * g - b;
+        groups[g] = HeadGroup{hb + k_offset(cap, 64, pt0, 0), hb + v_offset(cap, 64, pt0, 0), cap * 32u, vw, 0};
+    }
+}
+
+// A thread's share of one tile in flight: two K units and two V^T units.
+//   K unit j:   chunk c = tid + 256 j -> group c / 64, panel (c / 32) % 2, key (c / 4) % 8, octet c % 4
+//               (a wave reads one 8-key group: two contiguous 512-byte runs of the page)
+//   V^T unit j: key octet 4 j + tid % 4, dim tid / 4
+//               (four consecutive lanes read one dim row of a 32-key V^T panel: 64 contiguous bytes)
+struct TileLoad {
+    half8_t k[2];
+    half8_t v[2];
+};
+
+// kFull: all 64 keys of the tile are below nvalid and every group of the
+// segment names a page, so no lane needs a check.
+template <bool kFull>
+__device__ inline void tile_fetch(TileLoad& r, const HeadGroup* groups, uint32_t tg, uint32_t nvalid, uint32_t tid)
+{
+    half8_t const zero8 = {};
+#pragma unroll
+    for (uint32_t j = 0; j < 2; ++j) {
+        uint32_t const c = tid + kBlock * j;
+        uint32_t const g = c >> 6;
+        uint32_t const tk = (c >> 2) & 7u;
+        if (kFull) {
+            HeadGroup const e = groups[tg + g];
+            r.k[j] = load_half8_stream(e.k + ((c >> 5) & 1u) * e.kpanel + tk * 32 + (c & 3u) * 8);
+        } else {
+            r.k[j] = zero8;
+            if (8 * g + tk < nvalid) {
+                HeadGroup const e = groups[tg + g];
+                if (e.k != nullptr) r.k[j] = load_half8_stream(e.k + ((c >> 5) & 1u) * e.kpanel + tk * 32 + (c & 3u) * 8);
+            }
+        }
+        uint32_t const ko = 4 * j + (tid & 3u);
+        if (kFull) {
+            HeadGroup const e = groups[tg + ko];
+            r.v[j] = load_half8_stream(e.v + (tid >> 2) * e.vw);
+        } else {
+            r.v[j] = zero8;
+            if (8 * ko < nvalid) {
+                HeadGroup const e = groups[tg + ko];
+                if (e.v != nullptr) {
+                    r.v[j] = load_half8_stream(e.v + (tid >> 2) * e.vw);
+                    if (8 * ko + 8 > nvalid) {
+                        uint32_t const keep = nvalid - 8 * ko;
+#pragma unroll
+                        for (uint32_t q = 0; q < 8; ++q) {
+                            if (q >= keep) r.v[j][q] = static_cast<_Float16>(0.0f);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+__device__ inline void tile_store(KvTile& t, const TileLoad& r, uint32_t tid)
+{
+#pragma unroll
+    for (uint32_t j = 0; j < 2; ++j) {
+        uint32_t const c = tid + kBlock * j;
+        uint32_t const key = 8 * (c >> 6) + ((c >> 2) & 7u);
+        t.k[k_unit(key, 4 * ((c >> 5) & 1u) + (c & 3u))] = r.k[j];
+        t.v[v_unit(tid >> 2, 4 * j + (tid & 3u))] = r.v[j];
+    }
+}
+
+// Cross-row exchanges of a wave64 on the VALU (v_permlane16/32_swap): the
+// value of lane l ^ 16 and of lane l ^ 32.
+__device__ inline float xor16(float v)
+{
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 16u) ? r[0] : r[1]);
+}
+
+__device__ inline float xor32(float v)
+{
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 32u) ? r[0] : r[1]);
+}
+
+// One wave of the fast path: kColBlocks column blocks of 16 columns, each
+// tpw new tokens x the G query heads of KV head h.  S^T = K.Q^T and
+// O^T += V^T.P^T per 64-key tile, with the keys of a 32-key half permuted
+// so that the S^T accumulator layout is the P^T operand layout (lane l holds
+// keys 8 (l / 16) .. + 7 of its column).
+struct PrefillWave {
+    uint32_t l, a, r, x;
+    uint32_t i0;                       // first new token of the wave
+    half8_t qb[kColBlocks][2];
+    uint32_t limit[kColBlocks];        // last key this lane's column may see
+    float scale2;
+    float m_run[kColBlocks];
+    // acc[0..3]: O^T dims 16 db .. 16 db + 15; acc[4] row 0: the softmax
+    // denominator, accumulated by the MFMA from a ones row of V^T.
+    float4_t acc[5][kColBlocks];
+    half8_t ones;
+};
+
+__device__ void prefill_wave_init(PrefillWave& w, const kimkv_prefill_item& item, uint32_t h, PrefillShape shape,
+                                  uint32_t QH, uint32_t i0)
 {
     constexpr uint32_t D = 64;
     w.l = threadIdx.x & 63u;
     w.a = w.l >> 4;
     w.r = w.l & 15u;
     w.x = (w.l >> 2) & 3u;
-    uint32_t const i = i0 + w.r / G;                     // new-token index of this lane's column
-    uint32_t const q = h * G + w.r % G;
-    w.qvalid = i < item.new_tokens;
-    w.limit = item.token_count - item.new_tokens + (w.qvalid ? i : 0);
-    w.head_unit = static_cast<uint64_t>(h) * 2u * D;
+    w.i0 = i0;
+    uint32_t const T0 = item.token_count - item.new_tokens;
     half8_t const zero8 = {};
-    w.qb0 = zero8;
-    w.qb1 = zero8;
-    if (w.qvalid) {
-        const uint16_t* qrow = item.query + (static_cast<uint64_t>(i) * QH + q) * D;
-        w.qb0 = *reinterpret_cast<const half8_t*>(qrow + w.a * 8);
-        w.qb1 = *reinterpret_cast<const half8_t*>(qrow + 32 + w.a * 8);
+#pragma unroll
+    for (uint32_t cb = 0; cb < kColBlocks; ++cb) {
+        uint32_t const i = i0 + cb * shape.tpw + w.r / shape.G;
+        uint32_t const q = h * shape.G + w.r % shape.G;
+        bool const valid = i < item.new_tokens;
+        w.limit[cb] = T0 + (valid ? i : 0);
+        w.qb[cb][0] = zero8;
+        w.qb[cb][1] = zero8;
+        if (valid) {
+            const uint16_t* qrow = item.query + (static_cast<uint64_t>(i) * QH + q) * D;
+            w.qb[cb][0] = *reinterpret_cast<const half8_t*>(qrow + w.a * 8);
+            w.qb[cb][1] = *reinterpret_cast<const half8_t*>(qrow + 32 + w.a * 8);
+        }
+        w.m_run[cb] = -INFINITY;
+#pragma unroll
+        for (uint32_t db = 0; db < 5; ++db) w.acc[db][cb] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
     w.scale2 = item.attention_scale * kLog2e;
-    w.m_run = -INFINITY;
-    w.l_part = 0.0f;
-#pragma unroll
-    for (uint32_t db = 0; db < 4; ++db) w.acc[db] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    _Float16 const one = static_cast<_Float16>(w.r == 0 ? 1.0f : 0.0f);
+    w.ones = half8_t{one, one, one, one, one, one, one, one};
 }
 
-// Keys [t0, t0 + 64) of the segment starting at s0 (ending at s1).
-__device__ void prefill_wave_step(PrefillWave& w, const GroupEntry* groups, uint32_t s0, uint32_t s1, uint32_t t0)
+// Keys [t0, t0 + 64) from the staged tile; nvalid = valid keys from t0 on.
+// kMasked: some key of the tile is past nvalid or past a column's limit.
+template <bool kMasked>
+__device__ inline void prefill_wave_step(PrefillWave& w, const KvTile& tile, uint32_t t0, uint32_t nvalid)
 {
-    constexpr uint32_t D = 64;
-    half8_t const zero8 = {};
-    uint32_t const tg = (t0 - s0) >> 3;
-    uint32_t const nvalid = s1 - t0;
+    // Column block 0's scores are issued first, so its softmax (VALU) runs
+    // while block 1's score MFMAs execute, and block 1's softmax while block
+    // 0's output MFMAs execute.
     half8_t kop[2][2][2];
+#pragma unroll
+    for (uint32_t kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (uint32_t e = 0; e < 2; ++e) {
+            uint32_t const t = 32 * kb + 8 * w.x + 4 * e + (w.l & 3u);
+            kop[kb][e][0] = tile.k[k_unit(t, w.a)];
+            kop[kb][e][1] = tile.k[k_unit(t, 4 + w.a)];
+        }
+    }
+    float4_t s[kColBlocks][2][2];
+#pragma unroll
+    for (uint32_t cb = 0; cb < kColBlocks; ++cb) {
+#pragma unroll
+        for (uint32_t kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (uint32_t e = 0; e < 2; ++e) {
+                float4_t z = {};
+                z = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][0], w.qb[cb][0], z, 0, 0, 0);
+                s[cb][kb][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][1], w.qb[cb][1], z, 0, 0, 0);
+            }
+        }
+    }
     half8_t vop[2][4];
 #pragma unroll
     for (uint32_t kb = 0; kb < 2; ++kb) {
-        GroupEntry const gk = groups[tg + 4 * kb + w.x];
 #pragma unroll
-        for (uint32_t e = 0; e < 2; ++e) {
-            uint32_t const tt = 32 * kb + 8 * w.x + 4 * e + (w.l & 3u);
-            if (tt < nvalid && gk.base != nullptr) {
-                const uint16_t* row = gk.base + gk.cap * w.head_unit
-                    + static_cast<uint64_t>(gk.pt0 + 4 * e + (w.l & 3u)) * 32 + w.a * 8;
-                kop[kb][e][0] = load_half8_stream(row);
-                kop[kb][e][1] = load_half8_stream(row + static_cast<uint64_t>(gk.cap) * 32);
-            } else {
-                kop[kb][e][0] = zero8;
-                kop[kb][e][1] = zero8;
-            }
-        }
-        GroupEntry const gv = groups[tg + 4 * kb + w.a];
-        uint32_t const vt0 = 32 * kb + 8 * w.a;
-        if (vt0 < nvalid && gv.base != nullptr) {
-            uint32_t const vw = v_width(gv.cap);
-            const uint16_t* vt = gv.base + gv.cap * w.head_unit + v_offset(gv.cap, D, gv.pt0, w.r);
+        for (uint32_t db = 0; db < 4; ++db) vop[kb][db] = tile.v[v_unit(16 * db + w.r, 4 * kb + w.a)];
+    }
 #pragma unroll
-            for (uint32_t db = 0; db < 4; ++db) vop[kb][db] = load_half8_stream(vt + static_cast<uint64_t>(db * 16) * vw);
-            if (vt0 + 8 > nvalid) {
-                uint32_t const keep = nvalid - vt0;
+    for (uint32_t cb = 0; cb < kColBlocks; ++cb) {
+        // Element i of s[cb][kb][e] is key t0 + 32 kb + 8 a + 4 e + i of this lane's column.  The max is
+        // taken on the unscaled dots (scale2 > 0 keeps the order and rounding is monotonic).
+        float mx = -INFINITY;
 #pragma unroll
-                for (uint32_t db = 0; db < 4; ++db) {
+        for (uint32_t kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                    for (uint32_t j = 0; j < 8; ++j) {
-                        if (j >= keep) vop[kb][db][j] = static_cast<_Float16>(0.0f);
+            for (uint32_t e = 0; e < 2; ++e) {
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i) {
+                    if (kMasked) {
+                        uint32_t const tt = 32 * kb + 8 * w.a + 4 * e + i;
+                        if (!(tt < nvalid && t0 + tt <= w.limit[cb])) s[cb][kb][e][i] = -INFINITY;
                     }
+                    mx = fmaxf(mx, s[cb][kb][e][i]);
                 }
             }
-        } else {
-#pragma unroll
-            for (uint32_t db = 0; db < 4; ++db) vop[kb][db] = zero8;
         }
-    }
-
-    float4_t s[2][2];
+        mx = fmaxf(mx, xor16(mx));
+        mx = fmaxf(mx, xor32(mx));
+        // Lazy running max: the reference point moves (and the accumulators
+        // are rescaled) only when a score exceeds it by more than 2^8, so
+        // p <= 256 stays well inside fp16 and most tiles skip the rescale.
+        // A column whose keys so far are all masked keeps m = -inf.
+        float const m_cand = fmaxf(w.m_run[cb], mx * w.scale2);
+        bool const grow = m_cand > w.m_run[cb] + kLazyRescaleLog2;
+        if (__any(grow)) {
+            float const alpha = grow ? __builtin_amdgcn_exp2f(w.m_run[cb] - m_cand) : 1.0f;
+            if (grow) w.m_run[cb] = m_cand;
 #pragma unroll
-    for (uint32_t kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (uint32_t e = 0; e < 2; ++e) {
-            float4_t z = {};
-            z = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][0], w.qb0, z, 0, 0, 0);
-            s[kb][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][1], w.qb1, z, 0, 0, 0);
+            for (uint32_t db = 0; db < 5; ++db) w.acc[db][cb] *= alpha;
         }
-    }
-    // Element i of s[kb][e] is key t0 + 32kb + 8a + 4e + i for this lane's column.
-    float mx = -INFINITY;
+        float const mref = w.m_run[cb];
+        bool const empty = kMasked && mref == -INFINITY;
+        half8_t pb[2];
 #pragma unroll
-    for (uint32_t kb = 0; kb < 2; ++kb) {
+        for (uint32_t kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (uint32_t e = 0; e < 2; ++e) {
+            for (uint32_t e = 0; e < 2; ++e) {
 #pragma unroll
-            for (uint32_t i = 0; i < 4; ++i) {
-                uint32_t const tt = 32 * kb + 8 * w.a + 4 * e + i;
-                bool const ok = tt < nvalid && t0 + tt <= w.limit;
-                float const v = ok ? s[kb][e][i] * w.scale2 : -INFINITY;
-                s[kb][e][i] = v;
-                mx = fmaxf(mx, v);
+                for (uint32_t i = 0; i < 4; ++i) {
+                    float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[cb][kb][e][i], w.scale2, -mref));
+                    if (kMasked && empty) p = 0.0f;
+                    pb[kb][4 * e + i] = static_cast<_Float16>(p);
+                }
             }
         }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    float const m_new = fmaxf(w.m_run, mx);
-    // A column whose keys in this step are all masked keeps its state.
-    float const alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(w.m_run - m_new);
-    w.m_run = m_new;
-    half8_t pb[2];
-    float psum = 0.0f;
 #pragma unroll
-    for (uint32_t kb = 0; kb < 2; ++kb) {
+        for (uint32_t kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (uint32_t e = 0; e < 2; ++e) {
-#pragma unroll
-            for (uint32_t i = 0; i < 4; ++i) {
-                float const p = m_new == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[kb][e][i] - m_new);
-                psum += p;
-                pb[kb][4 * e + i] = static_cast<_Float16>(p);
+            for (uint32_t db = 0; db < 4; ++db) {
+                w.acc[db][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[kb][db], pb[kb], w.acc[db][cb], 0, 0, 0);
             }
-        }
-    }
-    w.l_part = w.l_part * alpha + psum;
-#pragma unroll
-    for (uint32_t db = 0; db < 4; ++db) w.acc[db] *= alpha;
-#pragma unroll
-    for (uint32_t kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (uint32_t db = 0; db < 4; ++db) {
-            w.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[kb][db], pb[kb], w.acc[db], 0, 0, 0);
+            w.acc[4][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w.ones, pb[kb], w.acc[4][cb], 0, 0, 0);
         }
     }
 }
 
-__device__ void prefill_wave_store(PrefillWave& w, const kimkv_prefill_item& item, uint32_t h, uint32_t G,
-                                   uint32_t QH, uint32_t i0)
+__device__ void prefill_wave_store(PrefillWave& w, const kimkv_prefill_item& item, uint32_t h, PrefillShape shape,
+                                   uint32_t QH)
 {
     constexpr uint32_t D = 64;
-    float l_tot = w.l_part + __shfl_xor(w.l_part, 16);
-    l_tot += __shfl_xor(l_tot, 32);
-    if (!w.qvalid) return;
-    uint32_t const i = i0 + w.r / G;
-    uint32_t const q = h * G + w.r % G;
-    float const inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    uint16_t* out = item.output + (static_cast<uint64_t>(i) * QH + q) * D;
 #pragma unroll
-    for (uint32_t db = 0; db < 4; ++db) {
+    for (uint32_t cb = 0; cb < kColBlocks; ++cb) {
+        // Row 0 of acc[4] (element 0 on lanes 0..15) is the denominator; the other lanes hold zeros.
+        float l_tot = w.acc[4][cb][0] + xor16(w.acc[4][cb][0]);
+        l_tot += xor32(l_tot);
+        uint32_t const i = w.i0 + cb * shape.tpw + w.r / shape.G;
+        if (i >= item.new_tokens) continue;
+        uint32_t const q = h * shape.G + w.r % shape.G;
+        float const inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        uint16_t* out = item.output + (static_cast<uint64_t>(i) * QH + q) * D;
 #pragma unroll
-        for (uint32_t k = 0; k < 4; ++k) {
-            out[db * 16 + 4 * w.a + k] = __half_as_ushort(__float2half_rn(w.acc[db][k] * inv));
+        for (uint32_t db = 0; db < 4; ++db) {
+            uint32_t lo = static_cast<uint32_t>(__half_as_ushort(__float2half_rn(w.acc[db][cb][0] * inv)))
+                | (static_cast<uint32_t>(__half_as_ushort(__float2half_rn(w.acc[db][cb][1] * inv))) << 16);
+            uint32_t hi = static_cast<uint32_t>(__half_as_ushort(__float2half_rn(w.acc[db][cb][2] * inv)))
+                | (static_cast<uint32_t>(__half_as_ushort(__float2half_rn(w.acc[db][cb][3] * inv))) << 16);
+            *reinterpret_cast<uint2*>(out + db * 16 + 4 * w.a) = make_uint2(lo, hi);
         }
     }
 }
@@ -300,14 +454,16 @@ __device__ void prefill_row_generic(const PoolView& P, const kimkv_prefill_item&
     }
 }
 
-__global__ __launch_bounds__(kBlock) void prefill_kernel(PoolView P, const kimkv_prefill_item* items,
-                                                         const uint32_t* block_prefix, uint32_t item_count,
-                                                         uint32_t QH)
+__global__ __launch_bounds__(kBlock, 2) void prefill_kernel(PoolView P, const kimkv_prefill_item* items,
+                                                            const uint32_t* block_prefix, uint32_t item_count,
+                                                            uint32_t QH)
 {
-    __shared__ GroupEntry groups[kMaxGroups];
-    __shared__ GenericScratch scratch[4];
+    __shared__ HeadGroup groups[kSegmentGroups];
+    __shared__ KvTile tiles[2];
+    __shared__ GenericScratch scratch[kWaves];
     __shared__ uint32_t s_item;
     __shared__ uint32_t s_generic;
+    __shared__ uint32_t s_holes;
 
     uint32_t const tid = threadIdx.x;
     uint32_t const block = blockIdx.x;
@@ -333,43 +489,91 @@ __global__ __launch_bounds__(kBlock) void prefill_kernel(PoolView P, const kimkv
     }
     PrefillShape const shape = prefill_shape(QH, H, D);
     uint32_t const wave = tid >> 6;
-    uint32_t const per_block = 4 * shape.tpw;
-    uint32_t const i_block = (block - block_prefix[it]) * per_block;
-    uint32_t const i0 = i_block + wave * shape.tpw;          // this wave's first new token
+    uint32_t const per_block = prefill_block_tokens(shape);
+    // Blocks of an item run from its last tokens (most keys) to its first.
+    uint32_t const nb = block_prefix[it + 1] - block_prefix[it];
+    uint32_t const i_block = (nb - 1 - (block - block_prefix[it])) * per_block;
     uint32_t const T0 = item.token_count - item.new_tokens;
     // Keys the whole block needs: [0, T0 + last token of the block].
     uint32_t const last = min(i_block + per_block, item.new_tokens) - 1;
     uint32_t const kend = T0 + last + 1;
 
-    PrefillWave w;
-    if (shape.mfma) prefill_wave_init(w, item, h, shape.G, QH, i0);
-    bool const wave_has_rows = i0 < item.new_tokens;
-    uint32_t const wave_kend = wave_has_rows ? T0 + min(i0 + shape.tpw, item.new_tokens) : 0;   // exclusive
-
-    for (uint32_t s0 = 0; s0 < kend; s0 += kMaxChunk) {
-        uint32_t const s1 = min(s0 + kMaxChunk, kend);
-        uint32_t const ngroups = (s1 - s0 + 7) / 8;
-        for (uint32_t g = tid; g < ngroups; g += kBlock) groups[g] = GroupEntry{nullptr, 0, 0};
-        __syncthreads();
-        if (shape.mfma) {
+    if (shape.mfma) {
+        uint32_t const wave_tokens = kColBlocks * shape.tpw;
+        uint32_t const i0 = i_block + wave * wave_tokens;
+        PrefillWave w;
+        prefill_wave_init(w, item, h, shape, QH, i0);
+        bool const wave_has_rows = i0 < item.new_tokens;
+        // Keys up to the wave's last token (exclusive end) and its first token's limit.
+        uint32_t const wave_kend = wave_has_rows ? T0 + min(i0 + wave_tokens, item.new_tokens) : 0;
+        uint32_t const wave_full = T0 + i0;   // keys below this need no causal mask
+        for (uint32_t s0 = 0; s0 < kend; s0 += kSegmentKeys) {
+            uint32_t const s1 = min(s0 + kSegmentKeys, kend);
+            uint32_t const ngroups = (s1 - s0 + 7) / 8;
+            for (uint32_t g = tid; g < ngroups; g += kBlock) groups[g] = HeadGroup{nullptr, nullptr, 0, 0, 0};
+            __syncthreads();
             uint32_t const idx0 = find_descriptor_wave(item.descriptors, item.descriptor_count, s0);
             for (uint32_t j = tid; j <= ngroups && idx0 + j < item.descriptor_count; j += kBlock) {
-                add_groups(P, item.descriptors[idx0 + j], item.layer, s0, s1, item.token_count, groups, &s_generic);
+                add_head_groups(P, item.descriptors[idx0 + j], item.layer, h, s0, s1, item.token_count, groups,
+                                &s_generic);
+            }
+            __syncthreads();
+            if (s_generic != 0) break;
+            // A group no entry covers (a table with a hole) keeps every tile on the checked loads.
+            if (tid == 0) s_holes = 0;
+            __syncthreads();
+            for (uint32_t g = tid; g < ngroups; g += kBlock) {
+                if (groups[g].k == nullptr) s_holes = 1;
+            }
+            __syncthreads();
+            bool const holes = s_holes != 0;
+            uint32_t const ntiles = (s1 - s0 + kTileKeys - 1) / kTileKeys;
+            // Tile j is computed from tiles[j % 2] while tile j + 1 sits in the
+            // other register set and tile j + 2's loads are issued: each tile's
+            // loads have two compute phases to land.
+            auto compute = [&](const KvTile& tile, uint32_t j) {
+                uint32_t const t0 = s0 + j * kTileKeys;
+                if (t0 >= wave_kend) return;
+                if (t0 + kTileKeys <= s1 && t0 + kTileKeys <= wave_full) {
+                    prefill_wave_step<false>(w, tile, t0, s1 - t0);
+                } else {
+                    prefill_wave_step<true>(w, tile, t0, s1 - t0);
+                }
+            };
+            auto fetch = [&](TileLoad& ld, uint32_t j) {
+                uint32_t const nvalid = s1 - s0 - j * kTileKeys;
+                if (!holes && nvalid >= kTileKeys) {
+                    tile_fetch<true>(ld, groups, j * (kTileKeys / 8), nvalid, tid);
+                } else {
+                    tile_fetch<false>(ld, groups, j * (kTileKeys / 8), nvalid, tid);
+                }
+            };
+            TileLoad la, lb;
+            fetch(la, 0);
+            tile_store(tiles[0], la, tid);
+            if (ntiles > 1) fetch(lb, 1);
+            __syncthreads();
+            for (uint32_t j = 0; j < ntiles; j += 2) {
+                if (j + 2 < ntiles) fetch(la, j + 2);
+                compute(tiles[0], j);
+                if (j + 1 < ntiles) tile_store(tiles[1], lb, tid);
+                __syncthreads();
+                if (j + 1 >= ntiles) break;
+                if (j + 3 < ntiles) fetch(lb, j + 3);
+                compute(tiles[1], j + 1);
+                if (j + 2 < ntiles) tile_store(tiles[0], la, tid);
+                __syncthreads();
             }
         }
-        __syncthreads();
-        if (shape.mfma && s_generic == 0) {
-            uint32_t const stop = min(s1, wave_kend);
-            for (uint32_t t0 = s0; t0 < stop; t0 += 64) prefill_wave_step(w, groups, s0, s1, t0);
+        if (s_generic == 0) {
+            if (wave_has_rows) prefill_wave_store(w, item, h, shape, QH);
+            return;
         }
-        __syncthreads();
-    }
-    if (shape.mfma && s_generic == 0) {
-        prefill_wave_store(w, item, h, shape.G, QH, i0);
-        return;
     }
     // Generic path: this wave's new tokens x the G query heads, one row at a time.
-    for (uint32_t i = i0; i < min(i0 + shape.tpw, item.new_tokens); ++i) {
+    uint32_t const g0 = i_block + wave * (per_block / kWaves);
+    uint32_t const g1 = min(g0 + per_block / kWaves, item.new_tokens);
+    for (uint32_t i = g0; i < g1; ++i) {
         for (uint32_t g = 0; g < shape.G; ++g) {
             prefill_row_generic(P, item, h, h * shape.G + g, i, QH, &scratch[wave]);
         }
@@ -389,9 +593,7 @@ uint32_t kimkv_prefill_tokens_per_block(const kimkv_storage* storage, uint32_t q
         || query_heads % storage->layout.kv_heads != 0) {
         return 0;
     }
-    uint32_t const G = query_heads / storage->layout.kv_heads;
-    bool const mfma = storage->layout.head_dim == 64 && G <= 16 && 16 % G == 0;
-    return 4 * (mfma ? 16 / G : 1);
+    return prefill_block_tokens(prefill_shape(query_heads, storage->layout.kv_heads, storage->layout.head_dim));
 }
 
 kimkv_status kimkv_paged_prefill_batch(const kimkv_storage* storage, const kimkv_prefill_item* device_items,
@@ -405,9 +607,13 @@ kimkv_status kimkv_paged_prefill_batch(const kimkv_storage* storage, const kimkv
     }
     if (total_blocks == 0 || item_count == 0) return KIMKV_OK;
     dim3 const grid(total_blocks, storage->layout.kv_heads);
+    void* start = nullptr;
+    kernel_timing_begin(TimedKernel::Prefill, native(stream), &start);
     prefill_kernel<<<grid, kBlock, 0, native(stream)>>>(pool_view(*storage), device_items, device_block_prefix,
                                                         item_count, query_heads);
-    return launch_status();
+    kimkv_status const st = launch_status();
+    kernel_timing_end(TimedKernel::Prefill, native(stream), start);
+    return st;
 }
 
 }  // extern "C"

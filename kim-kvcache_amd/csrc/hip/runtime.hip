@@ -26,10 +26,10 @@ struct DecodeTiming {
     uint64_t launches{0};
 };
 
-DecodeTiming& timing()
+DecodeTiming& timing(TimedKernel kind = TimedKernel::Decode)
 {
-    static DecodeTiming instance;
-    return instance;
+    static DecodeTiming instances[2];
+    return instances[static_cast<int>(kind)];
 }
 
 void drain_locked(DecodeTiming& t)
@@ -58,10 +58,10 @@ kimkv_status record_error(hipError_t error, kimkv_status failure)
     return failure;
 }
 
-void decode_timing_begin(hipStream_t stream, void** start)
+void kernel_timing_begin(TimedKernel kind, hipStream_t stream, void** start)
 {
     *start = nullptr;
-    DecodeTiming& t = timing();
+    DecodeTiming& t = timing(kind);
     std::lock_guard<std::mutex> lock(t.mutex);
     if (!t.enabled) {
         return;
@@ -74,12 +74,12 @@ void decode_timing_begin(hipStream_t stream, void** start)
     }
 }
 
-void decode_timing_end(hipStream_t stream, void* start)
+void kernel_timing_end(TimedKernel kind, hipStream_t stream, void* start)
 {
     if (start == nullptr) {
         return;
     }
-    DecodeTiming& t = timing();
+    DecodeTiming& t = timing(kind);
     std::lock_guard<std::mutex> lock(t.mutex);
     hipEvent_t stop = nullptr;
     if (hipEventCreate(&stop) == hipSuccess && hipEventRecord(stop, stream) == hipSuccess) {
@@ -360,9 +360,10 @@ uint64_t kimkv_synth_kv_row(uint32_t stream, uint32_t layer, uint32_t component,
     return kimkv::kv_row(stream, layer, component, token);
 }
 
-kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launches)
+namespace {
+kimkv_status kernel_timing(kimkv::TimedKernel kind, int enable, double* total_ms, uint64_t* launches)
 {
-    kimkv::DecodeTiming& t = kimkv::timing();
+    kimkv::DecodeTiming& t = kimkv::timing(kind);
     std::lock_guard<std::mutex> lock(t.mutex);
     kimkv::drain_locked(t);
     if (total_ms != nullptr) *total_ms = t.total_ms;
@@ -371,6 +372,17 @@ kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launche
     t.launches = 0;
     t.enabled = enable != 0;
     return KIMKV_OK;
+}
+}  // namespace
+
+kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launches)
+{
+    return kernel_timing(kimkv::TimedKernel::Decode, enable, total_ms, launches);
+}
+
+kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launches)
+{
+    return kernel_timing(kimkv::TimedKernel::Prefill, enable, total_ms, launches);
 }
 
 }  // extern "C"

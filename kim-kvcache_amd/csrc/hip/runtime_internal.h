@@ -18,8 +18,11 @@ inline kimkv_status launch_status()
 
 inline hipStream_t native(kimkv_stream_t stream) { return static_cast<hipStream_t>(stream); }
 
-// Decode-kernel event timing used by the benchmark (kimkv_decode_timing).
-void decode_timing_begin(hipStream_t stream, void** start);
-void decode_timing_end(hipStream_t stream, void* start);
+// Kernel event timing used by the benchmark (kimkv_decode_timing,
+// kimkv_prefill_timing): events recorded on the launch stream around each
+// launch while enabled.
+enum class TimedKernel : int { Decode = 0, Prefill = 1 };
+void kernel_timing_begin(TimedKernel kind, hipStream_t stream, void** start);
+void kernel_timing_end(TimedKernel kind, hipStream_t stream, void* start);
 
 }  // namespace kimkv

@@ -803,7 +803,10 @@ void attendPrefillBatch(PrefillChunk* const* chunks, std::size_t count, std::uin
         }
         statuses[i] = c->check(layer, true);
         if (!statuses[i].ok()) continue;
+        // The kernel reads query rows as 16-byte vectors and stores 8-byte output pieces.
         if (queries[i] == nullptr || outputs[i] == nullptr || !(scale > 0.0f)
+            || (reinterpret_cast<std::uintptr_t>(queries[i]) & 15u) != 0
+            || (reinterpret_cast<std::uintptr_t>(outputs[i]) & 7u) != 0
             || (owner != nullptr && (c->owner.get() != owner || c->stream != stream))) {
             statuses[i] = {EngineKvError::InvalidArgument};
             continue;

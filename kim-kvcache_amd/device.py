@@ -129,6 +129,8 @@ _SIGNATURES = {
                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "kimkv_decode_timing": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                            ctypes.POINTER(ctypes.c_uint64)]),
+    "kimkv_prefill_timing": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                            ctypes.POINTER(ctypes.c_uint64)]),
     "kimkv_synth_value": (ctypes.c_uint16, [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32]),
     "kimkv_synth_kv_row": (ctypes.c_uint64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
     "kimkv_fill_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
@@ -397,4 +399,12 @@ def decode_timing(enable: bool):
     launches = ctypes.c_uint64()
     check(lib().kimkv_decode_timing(1 if enable else 0, ctypes.byref(total), ctypes.byref(launches)),
           "decode_timing")
+    return float(total.value), int(launches.value)
+
+
+def prefill_timing(enable: bool):
+    total = ctypes.c_double()
+    launches = ctypes.c_uint64()
+    check(lib().kimkv_prefill_timing(1 if enable else 0, ctypes.byref(total), ctypes.byref(launches)),
+          "prefill_timing")
     return float(total.value), int(launches.value)
