@@ -4,7 +4,9 @@ Outputs (git-ignored, shipped with the tree):
   kim-kvcache_amd/_lib/libkimkv_hip.so  -- gfx950 kernels + the C-ABI of include/kimkv_hip.h
   kim-kvcache_amd/_lib/libkimkv.so      -- C++ host layer (page pool, block tables,
                                            KvCacheManager, token transactions, HIP engine
-                                           backend) + the C facade of include/kimkv_host.h
+                                           backend, generation runtime, iteration scheduler)
+                                           + the C facade of include/kimkv_host.h
+  kim-kvcache_amd/_lib/tests/*          -- C++ contract tests (tests/cpp), run by pytest
 """
 from __future__ import annotations
 
@@ -96,6 +98,20 @@ def build_host() -> str | None:
     return out
 
 
+TEST_SRC = os.path.join(REPO, "tests", "cpp")
+TEST_BIN = os.path.join(LIB_DIR, "tests")
+
+
+def build_tests() -> list[str]:
+    """Compile the C++ contract tests (tests/cpp/*.cpp) against libkimkv.so."""
+    srcs = _sources(TEST_SRC, (".cpp",)) if os.path.isdir(TEST_SRC) else []
+    os.makedirs(TEST_BIN, exist_ok=True)
+    outs = [os.path.join(TEST_BIN, os.path.splitext(os.path.basename(s))[0]) for s in srcs]
+    _parallel([[CXX, *HOST_FLAGS, f"-I{INCLUDE}", s, f"-L{LIB_DIR}", "-lkimkv", "-lkimkv_hip",
+                "-Wl,-rpath,$ORIGIN/..", "-pthread", "-o", o] for s, o in zip(srcs, outs)])
+    return outs
+
+
 def build_all() -> list[str]:
     if os.path.isdir(OBJ_DIR):
         shutil.rmtree(OBJ_DIR)
@@ -103,6 +119,7 @@ def build_all() -> list[str]:
     host = build_host()
     if host:
         built.append(host)
+        built.extend(build_tests())
     shutil.rmtree(OBJ_DIR, ignore_errors=True)
     return built
 

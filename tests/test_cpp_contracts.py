@@ -1,0 +1,18 @@
+"""Runs the C++ contract tests built from tests/cpp (CPU only: fake KV backend
+and fake model).  They mirror the reference's tests/engine scenarios for the
+single-request generation runtime and the iteration scheduler."""
+import os
+import subprocess
+
+import pytest
+
+BIN = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "kim-kvcache_amd", "_lib", "tests")
+
+
+@pytest.mark.parametrize("name", ["generation_contract_test"])
+def test_cpp_contract(name):
+    path = os.path.join(BIN, name)
+    if not os.path.exists(path):
+        pytest.fail(f"{path} is missing: run __graft_entry__.build() first")
+    proc = subprocess.run([path], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=120)
+    assert proc.returncode == 0, proc.stdout
