@@ -276,6 +276,43 @@ kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launche
 /* The same for the chunked-prefill attention kernel. */
 kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launches);
 
+/* ---- dense TinyLlama layers (the model runner's device side) --------------
+ * Counterparts of src/cuda/model/kernels.cuh:11-119 and the cuBLAS calls of
+ * src/cuda/model/runner_support.cpp:207-250.  Activations are fp16 rows,
+ * stored with round-to-nearest-even; all accumulation is fp32. */
+
+/* y[rows][out] = x[rows][in] . weight[out][in]^T + beta * y (rocBLAS, fp32
+ * accumulate).  y is fp16 (y_f32 = 0) or fp32 (y_f32 != 0); beta = 1 with
+ * y = the residual stream fuses the residual add. */
+kimkv_status kimkv_linear(const uint16_t* x, uint32_t rows, uint32_t in_features, const uint16_t* weight,
+                          uint32_t out_features, void* y, int y_f32, float beta, kimkv_stream_t stream);
+/* out[r] = table[ids[r]] (launchEmbeddingBatch, kernels.cuh:19-26). */
+kimkv_status kimkv_model_embed(const uint16_t* table, const uint32_t* device_ids, uint32_t rows, uint32_t hidden,
+                               uint16_t* out, kimkv_stream_t stream);
+/* RMSNorm (launchRmsNormBatch, kernels.cuh:37-45): out[r] = x[src] * rsqrt(mean(x[src]^2) + eps) * weight,
+ * src = device_rows ? device_rows[r] : r (row selection for the last position of each request). */
+kimkv_status kimkv_model_rmsnorm(const uint16_t* x, const uint32_t* device_rows, uint32_t rows, const uint16_t* weight,
+                                 uint32_t hidden, float eps, uint16_t* out, kimkv_stream_t stream);
+/* RoPE (launchRopeBatch, kernels.cuh:58-68) fused with the q / k / v split of a
+ * [rows][(QH + 2 KVH) * D] projection: q_out [rows][QH*D] and k_out
+ * [rows][KVH*D] rotated by positions[r] (pairs (d, d + D/2), angle =
+ * pos * theta^(-2d/D)), v_out [rows][KVH*D] copied. */
+kimkv_status kimkv_model_rope_split(const uint16_t* qkv, const uint32_t* device_positions, uint32_t rows,
+                                    uint32_t query_heads, uint32_t kv_heads, uint32_t head_dim, float theta,
+                                    uint16_t* q_out, uint16_t* k_out, uint16_t* v_out, kimkv_stream_t stream);
+/* SwiGLU (launchSwiGluBatch, kernels.cuh:95-102) of a fused [rows][2*inter]
+ * gate|up projection: out[r][i] = silu(gate) * up. */
+kimkv_status kimkv_model_swiglu(const uint16_t* gate_up, uint32_t rows, uint32_t intermediate, uint16_t* out,
+                                kimkv_stream_t stream);
+/* First index of each row's maximum (launchArgmaxBatch, kernels.cuh:111-117). */
+kimkv_status kimkv_model_argmax(const float* logits, uint32_t rows, uint32_t vocabulary, uint32_t* device_out,
+                                kimkv_stream_t stream);
+/* Seeded weights: out[i] = fp16(float(synth(seed, row0 + i / cols, i % cols)) * scale). */
+kimkv_status kimkv_fill_rows_scaled(uint16_t* device_out, uint64_t count, uint64_t seed, uint64_t row0, uint32_t cols,
+                                    float scale, kimkv_stream_t stream);
+/* out[i] = bits. */
+kimkv_status kimkv_fill_f16(uint16_t* device_out, uint64_t count, uint16_t bits, kimkv_stream_t stream);
+
 /* ---- synthetic inputs (benchmarks and tests) ----------------------------- */
 
 /* Deterministic pseudo-normal fp16 value used for every synthetic tensor:

@@ -253,6 +253,92 @@ void kimkv_prefill_attend_batch(kimkv_prefill_chunk** chunks, uint32_t count, ui
                                 const uint16_t* const* queries, uint16_t* const* outputs, float attention_scale,
                                 int* statuses);
 
+/* ---- model runner and iteration scheduler ----------------------------------
+ * HipTinyLlamaRunner (include/kim-kv/hip/hip_model_runner.h; counterpart of
+ * createCudaTinyLlamaModelRunner, include/kim-kv/cuda/cuda_model_runner.h)
+ * and IterationSchedulerRuntime (include/kim-kv/engine/iteration_scheduler.h:
+ * 132-180) over an engine.  Weights are seeded N(0, 0.02) fp16. */
+typedef struct kimkv_runner kimkv_runner;
+typedef struct kimkv_scheduler kimkv_scheduler;
+
+/* TinyLlamaConfig (include/kim-kv/model/tinyllama_config.h). */
+typedef struct kimkv_model_config {
+    uint32_t hidden_size;
+    uint32_t intermediate_size;
+    uint32_t layer_count;
+    uint32_t attention_head_count;
+    uint32_t kv_head_count;
+    uint32_t head_dimension;
+    uint32_t vocabulary_size;
+    uint32_t max_position_embeddings;
+    uint32_t bos_token_id;
+    uint32_t eos_token_id;
+    float rms_norm_epsilon;
+    float rope_theta;
+} kimkv_model_config;
+
+/* NULL on a shape mismatch with the engine or an allocation failure. */
+kimkv_runner* kimkv_runner_create(kimkv_engine* e, const kimkv_model_config* model, uint64_t weight_seed,
+                                  uint32_t max_positions, uint32_t max_spans, kimkv_stream_t stream);
+void kimkv_runner_destroy(kimkv_runner* r);
+uint64_t kimkv_runner_weight_bytes(const kimkv_runner* r);
+/* One forward over span_count spans (span i: request_ids[i], positions
+ * [first_positions[i], + token_counts[i]), its tokens next in `tokens`).
+ * next_tokens[i] = greedy token after the span; step_ok[i] = 1 if the span
+ * succeeded; logits (nullable) receives [span_count][vocabulary] fp32.
+ * Returns 0 when the call ran (per-span failures in step_ok), else -1. */
+int kimkv_runner_forward(kimkv_runner* r, uint32_t span_count, const uint64_t* request_ids,
+                         const uint32_t* first_positions, const uint32_t* token_counts, const uint32_t* tokens,
+                         uint32_t* next_tokens, int* step_ok, float* logits);
+
+/* IterationSchedulerConfig. */
+typedef struct kimkv_scheduler_config {
+    uint32_t max_active_requests;
+    uint32_t max_batched_tokens;
+    uint64_t max_kv_tokens;
+    uint32_t prefill_chunk_size;
+} kimkv_scheduler_config;
+
+/* SchedulerIterationResult. */
+typedef struct kimkv_iteration_result {
+    uint64_t iteration;
+    uint32_t model_forward_tokens;
+    uint32_t model_forward_batches;
+    uint32_t prefill_tokens;
+    uint32_t decode_tokens;
+    uint32_t terminals_produced;
+} kimkv_iteration_result;
+
+/* GenerationTerminal without its token list (kimkv_scheduler_terminal_tokens). */
+typedef struct kimkv_terminal_info {
+    uint64_t request_id;
+    uint32_t reason;               /* GenerationTerminalReason */
+    uint32_t error;                /* GenerationError */
+    uint32_t prompt_tokens;
+    uint32_t completion_tokens;
+    uint64_t ttft_ns;
+    uint64_t tpot_ns;
+    uint64_t e2e_ns;
+} kimkv_terminal_info;
+
+kimkv_scheduler* kimkv_scheduler_create(kimkv_engine* e, kimkv_runner* r, const kimkv_scheduler_config* config);
+void kimkv_scheduler_destroy(kimkv_scheduler* s);   /* stops and reclaims active requests */
+/* submit(): returns SchedulerAdmissionError; eos_token_id < 0 = the model's EOS. */
+int kimkv_scheduler_submit(kimkv_scheduler* s, uint64_t request_id, const uint32_t* prompt, uint32_t prompt_length,
+                           uint32_t max_new_tokens, int64_t eos_token_id);
+int kimkv_scheduler_cancel(kimkv_scheduler* s, uint64_t request_id);
+void kimkv_scheduler_run_iteration(kimkv_scheduler* s, kimkv_iteration_result* out);
+/* drain() / takeTerminals(): terminals move to the handle's delivery list;
+ * both return the list's new length. */
+uint32_t kimkv_scheduler_drain(kimkv_scheduler* s);
+uint32_t kimkv_scheduler_collect(kimkv_scheduler* s);
+/* Reads delivered terminal `index`; its tokens go to `tokens` (up to
+ * capacity); returns the token count, or -1 for a bad index. */
+int kimkv_scheduler_terminal(const kimkv_scheduler* s, uint32_t index, kimkv_terminal_info* info, uint32_t* tokens,
+                             uint32_t capacity);
+void kimkv_scheduler_clear_terminals(kimkv_scheduler* s);
+int kimkv_scheduler_idle(const kimkv_scheduler* s);
+
 /* ---- CudaKvCache equivalent (include/kim-kv/cuda/cuda_kv_cache.h:33-100) --- */
 typedef struct kimkv_cache kimkv_cache;
 

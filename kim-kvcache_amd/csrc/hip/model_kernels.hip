@@ -1,0 +1,310 @@
+// model_kernels.hip -- the dense side of a TinyLlama forward for gfx950:
+// embedding gather, RMSNorm, RoPE (fused with the q / k / v split), SwiGLU,
+// greedy argmax, seeded weight initialisation, and the linear layers on
+// rocBLAS (fp16 in, fp32 accumulate).
+//
+// Counterparts: src/cuda/model/kernels.cuh:11-119 (launchEmbeddingBatch,
+// launchRmsNormBatch, launchRopeBatch, launchResidualAddBatch,
+// launchSwiGluBatch, launchArgmaxBatch) and the cuBLAS GEMMs of
+// src/cuda/model/runner_support.cpp:207-250.  Rounding points follow the
+// reference: every activation is stored as fp16 (round to nearest even), the
+// logits stay fp32.  Residual adds are fused into the output GEMM (beta = 1),
+// which rounds x + W.a once instead of twice.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <rocblas/rocblas.h>
+
+#include <cmath>
+#include <mutex>
+#include <unordered_map>
+
+#include "device_common.h"
+#include "runtime_internal.h"
+
+namespace kimkv {
+namespace {
+
+constexpr unsigned kBlock = 256;
+
+__device__ inline float h2f(uint16_t v) { return __half2float(__ushort_as_half(v)); }
+__device__ inline uint16_t f2h(float v) { return __half_as_ushort(__float2half_rn(v)); }
+
+__global__ __launch_bounds__(kBlock) void fill_scaled_kernel(uint16_t* out, uint64_t count, uint64_t seed,
+                                                             uint64_t row0, uint32_t cols, float scale)
+{
+    uint64_t const stride = static_cast<uint64_t>(gridDim.x) * kBlock;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; i < count; i += stride) {
+        out[i] = f2h(h2f(synth_f16(seed, row0 + i / cols, static_cast<uint32_t>(i % cols))) * scale);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void fill_const_kernel(uint16_t* out, uint64_t count, uint16_t bits)
+{
+    uint64_t const stride = static_cast<uint64_t>(gridDim.x) * kBlock;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; i < count; i += stride) out[i] = bits;
+}
+
+// One row per workgroup: out[r] = table[ids[r]] (ids checked by the host).
+__global__ __launch_bounds__(kBlock) void embed_kernel(const uint16_t* table, const uint32_t* ids, uint32_t hidden,
+                                                       uint16_t* out)
+{
+    uint32_t const r = blockIdx.x;
+    const uint16_t* src = table + static_cast<uint64_t>(ids[r]) * hidden;
+    uint16_t* dst = out + static_cast<uint64_t>(r) * hidden;
+    for (uint32_t i = threadIdx.x; i < hidden; i += kBlock) dst[i] = src[i];
+}
+
+__device__ inline float block_sum(float v, float* scratch)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    uint32_t const wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63u) == 0) scratch[wave] = v;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (uint32_t w = 0; w < kBlock / 64; ++w) total += scratch[w];
+    __syncthreads();
+    return total;
+}
+
+// out[r] = fp16(x[src_r] * rsqrt(mean(x[src_r]^2) + eps) * w), src_r = rows ? rows[r] : r.
+__global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const uint16_t* x, const uint32_t* rows, const uint16_t* w,
+                                                         uint32_t hidden, float eps, uint16_t* out)
+{
+    __shared__ float scratch[kBlock / 64];
+    uint32_t const r = blockIdx.x;
+    uint32_t const src = rows != nullptr ? rows[r] : r;
+    const uint16_t* in = x + static_cast<uint64_t>(src) * hidden;
+    float sq = 0.0f;
+    for (uint32_t i = threadIdx.x; i < hidden; i += kBlock) {
+        float const v = h2f(in[i]);
+        sq += v * v;
+    }
+    float const scale = 1.0f / sqrtf(block_sum(sq, scratch) / static_cast<float>(hidden) + eps);
+    uint16_t* o = out + static_cast<uint64_t>(r) * hidden;
+    for (uint32_t i = threadIdx.x; i < hidden; i += kBlock) o[i] = f2h(h2f(in[i]) * scale * h2f(w[i]));
+}
+
+// qkv row = [q: QH*D | k: KVH*D | v: KVH*D].  Rotates q and k by the row's
+// position (pairs (d, d + D/2), angle = pos * theta^(-2d/D)) into q_out / k_out
+// and copies v to v_out; each output is [rows][heads * D].
+__global__ __launch_bounds__(kBlock) void rope_split_kernel(const uint16_t* qkv, const uint32_t* positions,
+                                                            uint32_t QH, uint32_t KVH, uint32_t D, float theta,
+                                                            uint16_t* q_out, uint16_t* k_out, uint16_t* v_out)
+{
+    uint32_t const r = blockIdx.x;
+    uint32_t const half = D / 2;
+    uint64_t const width = static_cast<uint64_t>(QH + 2 * KVH) * D;
+    const uint16_t* row = qkv + r * width;
+    float const pos = static_cast<float>(positions[r]);
+    uint32_t const pairs = (QH + KVH) * half;
+    for (uint32_t p = threadIdx.x; p < pairs; p += kBlock) {
+        uint32_t const head = p / half;
+        uint32_t const d = p - head * half;
+        float const angle = pos * powf(theta, -2.0f * static_cast<float>(d) / static_cast<float>(D));
+        float const c = cosf(angle);
+        float const s = sinf(angle);
+        bool const is_q = head < QH;
+        uint32_t const h = is_q ? head : head - QH;
+        const uint16_t* src = row + (is_q ? 0 : static_cast<uint64_t>(QH) * D) + static_cast<uint64_t>(h) * D;
+        uint16_t* dst = (is_q ? q_out + static_cast<uint64_t>(r) * QH * D : k_out + static_cast<uint64_t>(r) * KVH * D)
+            + static_cast<uint64_t>(h) * D;
+        float const a = h2f(src[d]);
+        float const b = h2f(src[d + half]);
+        dst[d] = f2h(a * c - b * s);
+        dst[d + half] = f2h(b * c + a * s);
+    }
+    const uint16_t* v = row + static_cast<uint64_t>(QH + KVH) * D;
+    uint16_t* vo = v_out + static_cast<uint64_t>(r) * KVH * D;
+    for (uint32_t i = threadIdx.x; i < KVH * D; i += kBlock) vo[i] = v[i];
+}
+
+// gu row = [gate: inter | up: inter]; out = fp16(silu(gate) * up).
+__global__ __launch_bounds__(kBlock) void swiglu_kernel(const uint16_t* gu, uint32_t inter, uint16_t* out)
+{
+    uint32_t const r = blockIdx.y;
+    uint32_t const i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= inter) return;
+    const uint16_t* row = gu + static_cast<uint64_t>(r) * 2u * inter;
+    float const g = h2f(row[i]);
+    out[static_cast<uint64_t>(r) * inter + i] = f2h(g / (1.0f + expf(-g)) * h2f(row[inter + i]));
+}
+
+// First index of the row maximum (std::max_element order; NaN never wins).
+__global__ __launch_bounds__(kBlock) void argmax_kernel(const float* logits, uint32_t V, uint32_t* out)
+{
+    __shared__ float sv[kBlock / 64];
+    __shared__ uint32_t si[kBlock / 64];
+    uint32_t const r = blockIdx.x;
+    const float* row = logits + static_cast<uint64_t>(r) * V;
+    float best = -INFINITY;
+    uint32_t idx = 0xFFFFFFFFu;
+    for (uint32_t i = threadIdx.x; i < V; i += kBlock) {
+        float const v = row[i];
+        if (v > best || (idx == 0xFFFFFFFFu && v == v)) {
+            best = v;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        float const ov = __shfl_xor(best, m);
+        uint32_t const oi = __shfl_xor(idx, m);
+        if (oi != 0xFFFFFFFFu && (idx == 0xFFFFFFFFu || ov > best || (ov == best && oi < idx))) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    uint32_t const wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63u) == 0) {
+        sv[wave] = best;
+        si[wave] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < kBlock / 64; ++w) {
+            if (si[w] != 0xFFFFFFFFu && (idx == 0xFFFFFFFFu || sv[w] > best || (sv[w] == best && si[w] < idx))) {
+                best = sv[w];
+                idx = si[w];
+            }
+        }
+        out[r] = idx == 0xFFFFFFFFu ? 0u : idx;
+    }
+}
+
+unsigned grid_for(uint64_t count)
+{
+    uint64_t const b = (count + kBlock - 1) / kBlock;
+    return static_cast<unsigned>(b < 65536 ? (b == 0 ? 1 : b) : 65536);
+}
+
+// One rocBLAS handle per stream (created on first use, kept for the process).
+struct BlasHandles {
+    std::mutex mutex;
+    std::unordered_map<hipStream_t, rocblas_handle> by_stream;
+};
+
+BlasHandles& blas()
+{
+    static BlasHandles instance;
+    return instance;
+}
+
+rocblas_handle handle_for(hipStream_t stream)
+{
+    BlasHandles& b = blas();
+    std::lock_guard<std::mutex> lock(b.mutex);
+    auto it = b.by_stream.find(stream);
+    if (it != b.by_stream.end()) return it->second;
+    rocblas_handle h = nullptr;
+    if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
+    if (rocblas_set_stream(h, stream) != rocblas_status_success) {
+        rocblas_destroy_handle(h);
+        return nullptr;
+    }
+    b.by_stream.emplace(stream, h);
+    return h;
+}
+
+}  // namespace
+}  // namespace kimkv
+
+using namespace kimkv;
+
+extern "C" {
+
+kimkv_status kimkv_fill_rows_scaled(uint16_t* device_out, uint64_t count, uint64_t seed, uint64_t row0, uint32_t cols,
+                                    float scale, kimkv_stream_t stream)
+{
+    if (device_out == nullptr || cols == 0) return KIMKV_INVALID_ARGUMENT;
+    if (count == 0) return KIMKV_OK;
+    fill_scaled_kernel<<<grid_for(count), kBlock, 0, native(stream)>>>(device_out, count, seed, row0, cols, scale);
+    return launch_status();
+}
+
+kimkv_status kimkv_fill_f16(uint16_t* device_out, uint64_t count, uint16_t bits, kimkv_stream_t stream)
+{
+    if (device_out == nullptr) return KIMKV_INVALID_ARGUMENT;
+    if (count == 0) return KIMKV_OK;
+    fill_const_kernel<<<grid_for(count), kBlock, 0, native(stream)>>>(device_out, count, bits);
+    return launch_status();
+}
+
+kimkv_status kimkv_model_embed(const uint16_t* table, const uint32_t* device_ids, uint32_t rows, uint32_t hidden,
+                               uint16_t* out, kimkv_stream_t stream)
+{
+    if (table == nullptr || device_ids == nullptr || out == nullptr || hidden == 0) return KIMKV_INVALID_ARGUMENT;
+    if (rows == 0) return KIMKV_OK;
+    embed_kernel<<<rows, kBlock, 0, native(stream)>>>(table, device_ids, hidden, out);
+    return launch_status();
+}
+
+kimkv_status kimkv_model_rmsnorm(const uint16_t* x, const uint32_t* device_rows, uint32_t rows, const uint16_t* weight,
+                                 uint32_t hidden, float eps, uint16_t* out, kimkv_stream_t stream)
+{
+    if (x == nullptr || weight == nullptr || out == nullptr || hidden == 0 || !(eps > 0.0f)) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    if (rows == 0) return KIMKV_OK;
+    rmsnorm_kernel<<<rows, kBlock, 0, native(stream)>>>(x, device_rows, weight, hidden, eps, out);
+    return launch_status();
+}
+
+kimkv_status kimkv_model_rope_split(const uint16_t* qkv, const uint32_t* device_positions, uint32_t rows,
+                                    uint32_t query_heads, uint32_t kv_heads, uint32_t head_dim, float theta,
+                                    uint16_t* q_out, uint16_t* k_out, uint16_t* v_out, kimkv_stream_t stream)
+{
+    if (qkv == nullptr || device_positions == nullptr || q_out == nullptr || k_out == nullptr || v_out == nullptr
+        || query_heads == 0 || kv_heads == 0 || head_dim == 0 || head_dim % 2 != 0 || !(theta > 0.0f)) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    if (rows == 0) return KIMKV_OK;
+    rope_split_kernel<<<rows, kBlock, 0, native(stream)>>>(qkv, device_positions, query_heads, kv_heads, head_dim,
+                                                           theta, q_out, k_out, v_out);
+    return launch_status();
+}
+
+kimkv_status kimkv_model_swiglu(const uint16_t* gate_up, uint32_t rows, uint32_t intermediate, uint16_t* out,
+                                kimkv_stream_t stream)
+{
+    if (gate_up == nullptr || out == nullptr || intermediate == 0 || rows > 65535) return KIMKV_INVALID_ARGUMENT;
+    if (rows == 0) return KIMKV_OK;
+    dim3 const grid((intermediate + kBlock - 1) / kBlock, rows);
+    swiglu_kernel<<<grid, kBlock, 0, native(stream)>>>(gate_up, intermediate, out);
+    return launch_status();
+}
+
+kimkv_status kimkv_model_argmax(const float* logits, uint32_t rows, uint32_t vocabulary, uint32_t* device_out,
+                                kimkv_stream_t stream)
+{
+    if (logits == nullptr || device_out == nullptr || vocabulary == 0) return KIMKV_INVALID_ARGUMENT;
+    if (rows == 0) return KIMKV_OK;
+    argmax_kernel<<<rows, kBlock, 0, native(stream)>>>(logits, vocabulary, device_out);
+    return launch_status();
+}
+
+kimkv_status kimkv_linear(const uint16_t* x, uint32_t rows, uint32_t in_features, const uint16_t* weight,
+                          uint32_t out_features, void* y, int y_f32, float beta, kimkv_stream_t stream)
+{
+    if (x == nullptr || weight == nullptr || y == nullptr || in_features == 0 || out_features == 0
+        || in_features > 0x7FFFFFFFu || out_features > 0x7FFFFFFFu || rows > 0x7FFFFFFFu) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    if (rows == 0) return KIMKV_OK;
+    rocblas_handle h = handle_for(native(stream));
+    if (h == nullptr) return KIMKV_RUNTIME_UNAVAILABLE;
+    // Row-major y[rows][out] = x[rows][in] . W[out][in]^T  ==  column-major
+    // y^T (out x rows) = op(W_cm) . x_cm with W_cm = W^T (in x out, ld = in).
+    float const alpha = 1.0f;
+    rocblas_datatype const yt = y_f32 ? rocblas_datatype_f32_r : rocblas_datatype_f16_r;
+    rocblas_status const st = rocblas_gemm_ex(
+        h, rocblas_operation_transpose, rocblas_operation_none, static_cast<rocblas_int>(out_features),
+        static_cast<rocblas_int>(rows), static_cast<rocblas_int>(in_features), &alpha, weight, rocblas_datatype_f16_r,
+        static_cast<rocblas_int>(in_features), x, rocblas_datatype_f16_r, static_cast<rocblas_int>(in_features), &beta,
+        y, yt, static_cast<rocblas_int>(out_features), y, yt, static_cast<rocblas_int>(out_features),
+        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    return st == rocblas_status_success ? KIMKV_OK : KIMKV_SUBMISSION_FAILED;
+}
+
+}  // extern "C"

@@ -14,10 +14,6 @@
 
 using namespace kimkvcache;
 
-struct kimkv_engine {
-    std::unique_ptr<EngineKvBackend> backend;
-};
-
 struct kimkv_txn {
     TokenTransaction t;
 };

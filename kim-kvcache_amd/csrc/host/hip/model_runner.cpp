@@ -1,0 +1,473 @@
+// TinyLlama runner over the HIP engine backend (counterpart of
+// src/cuda/model/runner.cpp:410-848 and runner_factory.cpp:56-196).
+//
+// One forward call = one iteration's spans.  Per call: token ids / positions
+// / last-row indices go up in one staged copy; decode steps reserve token
+// transactions in one batch, prompt chunks open PrefillChunks; then per layer
+//   RMSNorm -> QKV GEMM -> RoPE + split -> K/V writes (one append launch for
+//   the decode lanes, one for the chunks) -> attention (one decode launch,
+//   one chunked-prefill launch) -> O GEMM (+ residual) -> RMSNorm ->
+//   gate|up GEMM -> SwiGLU -> down GEMM (+ residual);
+// finally RMSNorm of each span's last row, the LM head (fp32 logits) and the
+// argmax.  Commits / finishes are the call's completion point.
+#include "kim-kv/hip/hip_model_runner.h"
+
+#include "kim-kv/hip/hip_engine_kv_backend.h"
+#include "kimkv_hip.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <utility>
+
+namespace kimkvcache {
+
+namespace {
+
+// N(0, 0.02) from the synthetic generator (std 2 / sqrt(3)): scale = 0.02 * sqrt(3) / 2.
+constexpr float kWeightScale = 0.017320508f;
+constexpr std::uint16_t kOneF16 = 0x3C00;
+
+// Row ids of the seeded weights: tensor `kind` of layer `layer` (layer ==
+// layer_count for the embedding, final norm and LM head) starts at row
+// (layer + 1) << 40 | kind << 32.
+enum WeightKind : std::uint32_t { kQ = 1, kK, kV, kO, kGate, kUp, kDown, kEmbed, kHead };
+
+std::uint64_t weightRow(std::uint32_t layer, std::uint32_t kind)
+{
+    return (static_cast<std::uint64_t>(layer + 1) << 40) | (static_cast<std::uint64_t>(kind) << 32);
+}
+
+std::size_t align256(std::size_t n) { return (n + 255) & ~std::size_t{255}; }
+
+}  // namespace
+
+struct HipTinyLlamaRunner::Impl {
+    EngineKvBackend* kv{nullptr};
+    HipModelRunnerConfig cfg{};
+    HipStream stream{nullptr};
+    std::uint32_t QD{0}, KD{0}, W_qkv{0};
+    std::size_t ws_lane{0};   // decode split-K workspace per lane
+
+    // Device memory: one block for weights, one for activations.
+    void* weights{nullptr};
+    std::uint64_t weight_bytes{0};
+    void* work{nullptr};
+    std::uint64_t work_bytes{0};
+    void* pinned{nullptr};   // ids / positions / last rows up, tokens down
+
+    struct Layer {
+        std::uint16_t *ln1, *wqkv, *wo, *ln2, *wgu, *wdown;
+    };
+    std::vector<Layer> layers;
+    std::uint16_t *embed{nullptr}, *final_norm{nullptr}, *head{nullptr};
+
+    // Activations.
+    std::uint16_t *x{nullptr}, *h{nullptr}, *qkv{nullptr}, *q{nullptr}, *k{nullptr}, *v{nullptr}, *attn{nullptr},
+        *gu{nullptr}, *act{nullptr}, *hf{nullptr};
+    float* logits{nullptr};
+    std::uint32_t *d_ids{nullptr}, *d_pos{nullptr}, *d_last{nullptr}, *d_tokens{nullptr};
+    std::uint8_t* decode_ws{nullptr};
+    DevicePagedDecodeBatchItem* d_items{nullptr};
+
+    ~Impl()
+    {
+        if (weights) kimkv_device_free(weights);
+        if (work) kimkv_device_free(work);
+        if (pinned) kimkv_host_free_pinned(pinned);
+    }
+
+    bool allocate(std::string* error)
+    {
+        TinyLlamaConfig const& m = cfg.model;
+        std::uint64_t const H = m.hidden_size, I = m.intermediate_size, V = m.vocabulary_size;
+        std::uint64_t per_layer = 0;
+        per_layer += align256(H * 2) * 2;                              // ln1, ln2
+        per_layer += align256(std::uint64_t{W_qkv} * H * 2);           // q|k|v
+        per_layer += align256(H * H * 2);                              // o
+        per_layer += align256(2 * I * H * 2);                          // gate|up
+        per_layer += align256(H * I * 2);                              // down
+        weight_bytes = per_layer * m.layer_count + align256(V * H * 2) * 2 + align256(H * 2);
+        if (kimkv_device_malloc(&weights, weight_bytes) != KIMKV_OK) {
+            if (error) *error = "weight allocation failed";
+            return false;
+        }
+        auto* p = static_cast<std::uint8_t*>(weights);
+        auto take = [&p](std::uint64_t bytes) {
+            auto* r = reinterpret_cast<std::uint16_t*>(p);
+            p += align256(bytes);
+            return r;
+        };
+        layers.resize(m.layer_count);
+        for (Layer& L : layers) {
+            L.ln1 = take(H * 2);
+            L.wqkv = take(std::uint64_t{W_qkv} * H * 2);
+            L.wo = take(H * H * 2);
+            L.ln2 = take(H * 2);
+            L.wgu = take(2 * I * H * 2);
+            L.wdown = take(H * I * 2);
+        }
+        embed = take(V * H * 2);
+        final_norm = take(H * 2);
+        head = take(V * H * 2);
+
+        std::uint64_t const P = cfg.max_positions, S = cfg.max_spans;
+        std::uint64_t sizes[] = {
+            P * H * 2, P * H * 2, P * W_qkv * 2, P * QD * 2, P * KD * 2, P * KD * 2, P * QD * 2,
+            P * 2 * I * 2, P * I * 2, S * H * 2, S * V * 4, P * 4, P * 4, S * 4, S * 4,
+            S * ws_lane, S * sizeof(DevicePagedDecodeBatchItem)};
+        work_bytes = 0;
+        for (std::uint64_t s : sizes) work_bytes += align256(s);
+        if (kimkv_device_malloc(&work, work_bytes) != KIMKV_OK) {
+            if (error) *error = "workspace allocation failed";
+            return false;
+        }
+        p = static_cast<std::uint8_t*>(work);
+        x = take(sizes[0]);
+        h = take(sizes[1]);
+        qkv = take(sizes[2]);
+        q = take(sizes[3]);
+        k = take(sizes[4]);
+        v = take(sizes[5]);
+        attn = take(sizes[6]);
+        gu = take(sizes[7]);
+        act = take(sizes[8]);
+        hf = take(sizes[9]);
+        logits = reinterpret_cast<float*>(take(sizes[10]));
+        d_ids = reinterpret_cast<std::uint32_t*>(take(sizes[11]));
+        d_pos = reinterpret_cast<std::uint32_t*>(take(sizes[12]));
+        d_last = reinterpret_cast<std::uint32_t*>(take(sizes[13]));
+        d_tokens = reinterpret_cast<std::uint32_t*>(take(sizes[14]));
+        decode_ws = reinterpret_cast<std::uint8_t*>(take(sizes[15]));
+        d_items = reinterpret_cast<DevicePagedDecodeBatchItem*>(take(sizes[16]));
+        if (kimkv_host_malloc_pinned(&pinned, (2 * P + 2 * S) * 4) != KIMKV_OK) {
+            if (error) *error = "pinned staging allocation failed";
+            return false;
+        }
+        return true;
+    }
+
+    bool initWeights()
+    {
+        TinyLlamaConfig const& m = cfg.model;
+        std::uint64_t const H = m.hidden_size, I = m.intermediate_size, V = m.vocabulary_size;
+        std::uint64_t const seed = cfg.weight_seed;
+        bool ok = true;
+        auto fill = [&](std::uint16_t* dst, std::uint64_t rows, std::uint64_t cols, std::uint64_t row0) {
+            ok = ok && kimkv_fill_rows_scaled(dst, rows * cols, seed, row0, static_cast<std::uint32_t>(cols),
+                                              kWeightScale, stream) == KIMKV_OK;
+        };
+        auto ones = [&](std::uint16_t* dst, std::uint64_t n) {
+            ok = ok && kimkv_fill_f16(dst, n, kOneF16, stream) == KIMKV_OK;
+        };
+        for (std::uint32_t l = 0; l < m.layer_count; ++l) {
+            Layer const& L = layers[l];
+            ones(L.ln1, H);
+            ones(L.ln2, H);
+            fill(L.wqkv, QD, H, weightRow(l, kQ));
+            fill(L.wqkv + std::uint64_t{QD} * H, KD, H, weightRow(l, kK));
+            fill(L.wqkv + std::uint64_t{QD + KD} * H, KD, H, weightRow(l, kV));
+            fill(L.wo, H, H, weightRow(l, kO));
+            fill(L.wgu, I, H, weightRow(l, kGate));
+            fill(L.wgu + I * H, I, H, weightRow(l, kUp));
+            fill(L.wdown, H, I, weightRow(l, kDown));
+        }
+        fill(embed, V, H, weightRow(m.layer_count, kEmbed));
+        ones(final_norm, H);
+        fill(head, V, H, weightRow(m.layer_count, kHead));
+        return ok && kimkv_stream_synchronize(stream) == KIMKV_OK;
+    }
+
+    GenerationBatchResult forward(std::vector<GenerationSpan> const& spans, float* host_logits);
+};
+
+GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSpan> const& spans, float* host_logits)
+{
+    GenerationBatchResult result;
+    TinyLlamaConfig const& m = cfg.model;
+    std::size_t const S = spans.size();
+    if (S == 0 || S > cfg.max_spans) {
+        result.detail = "span count is zero or above the runner's max_spans";
+        return result;
+    }
+    std::uint32_t P = 0;
+    for (GenerationSpan const& s : spans) {
+        if (s.token_ids.empty() || s.request_id == kInvalidRequestId) {
+            result.detail = "span without tokens or request id";
+            return result;
+        }
+        for (std::uint32_t t : s.token_ids) {
+            if (t >= m.vocabulary_size) {
+                result.detail = "token id outside the vocabulary";
+                return result;
+            }
+        }
+        if (static_cast<std::uint64_t>(s.first_position) + s.token_ids.size() > m.max_position_embeddings) {
+            result.detail = "span runs past max_position_embeddings";
+            return result;
+        }
+        P += static_cast<std::uint32_t>(s.token_ids.size());
+    }
+    if (P > cfg.max_positions) {
+        result.detail = "span positions exceed the runner's max_positions";
+        return result;
+    }
+
+    // Host staging: ids[P], positions[P], last rows[S].
+    auto* st = static_cast<std::uint32_t*>(pinned);
+    std::uint32_t* ids = st;
+    std::uint32_t* pos = st + cfg.max_positions;
+    std::uint32_t* last = st + 2 * cfg.max_positions;
+    std::uint32_t* tokens_out = last + cfg.max_spans;
+    std::vector<std::uint32_t> first_row(S);
+    std::uint32_t r = 0;
+    for (std::size_t i = 0; i < S; ++i) {
+        first_row[i] = r;
+        for (std::size_t t = 0; t < spans[i].token_ids.size(); ++t, ++r) {
+            ids[r] = spans[i].token_ids[t];
+            pos[r] = spans[i].first_position + static_cast<std::uint32_t>(t);
+        }
+        last[i] = r - 1;
+    }
+    bool ok = kimkv_memcpy_h2d_async(d_ids, ids, P * 4ull, stream) == KIMKV_OK
+        && kimkv_memcpy_h2d_async(d_pos, pos, P * 4ull, stream) == KIMKV_OK
+        && kimkv_memcpy_h2d_async(d_last, last, S * 4ull, stream) == KIMKV_OK;
+
+    // KV side: token transactions for single positions, prefill chunks for the rest.
+    std::vector<GenerationStepResult> steps(S, GenerationStepResult{true, 0, {}});
+    std::vector<std::size_t> dec, pre;
+    for (std::size_t i = 0; i < S; ++i) (spans[i].token_ids.size() == 1 ? dec : pre).push_back(i);
+    std::vector<ReserveTokenRequest> reqs(dec.size());
+    std::vector<TokenReserveResult> reserved(dec.size());
+    for (std::size_t j = 0; j < dec.size(); ++j) {
+        reqs[j] = ReserveTokenRequest{spans[dec[j]].request_id, spans[dec[j]].first_position, stream};
+    }
+    if (!dec.empty() && !reserveTokenBatch(*kv, reqs.data(), reqs.size(), reserved.data())) {
+        for (std::size_t j = 0; j < dec.size(); ++j) reserved[j].status = {EngineKvError::InvalidArgument};
+    }
+    auto fail = [&steps](std::size_t i, std::string text) {
+        if (steps[i].success) steps[i] = GenerationStepResult{false, 0, std::move(text)};
+    };
+    for (std::size_t j = 0; j < dec.size(); ++j) {
+        if (!reserved[j].ok()) fail(dec[j], "token reservation failed: " + std::string(toString(reserved[j].status.error)));
+    }
+    std::vector<PrefillChunk> chunks(pre.size());
+    for (std::size_t j = 0; j < pre.size(); ++j) {
+        GenerationSpan const& s = spans[pre[j]];
+        PrefillChunkResult c = beginPrefillChunk(*kv, s.request_id, s.first_position,
+                                                 static_cast<std::uint32_t>(s.token_ids.size()), stream);
+        if (c.ok()) {
+            chunks[j] = std::move(c.chunk);
+        } else {
+            fail(pre[j], "prefill chunk refused: " + std::string(toString(c.status.error)));
+        }
+    }
+
+    float const scale = 1.0f / std::sqrt(static_cast<float>(m.head_dimension));
+    std::vector<LayerKvWriteBatchItem> wr;
+    std::vector<PagedDecodeBatchItem> at;
+    std::vector<DevicePagedDecodeBatchItem> at_host(dec.size());
+    std::vector<PrefillChunk*> live_chunks;
+    std::vector<std::size_t> live_pre;
+    std::vector<KvScalar const*> pk, pv, pq;
+    std::vector<KvScalar*> po;
+    std::vector<EngineKvStatus> pst;
+
+    ok = ok && kimkv_model_embed(embed, d_ids, P, m.hidden_size, x, stream) == KIMKV_OK;
+    for (std::uint32_t l = 0; l < m.layer_count && ok; ++l) {
+        Layer const& L = layers[l];
+        ok = kimkv_model_rmsnorm(x, nullptr, P, L.ln1, m.hidden_size, m.rms_norm_epsilon, h, stream) == KIMKV_OK
+            && kimkv_linear(h, P, m.hidden_size, L.wqkv, W_qkv, qkv, 0, 0.0f, stream) == KIMKV_OK
+            && kimkv_model_rope_split(qkv, d_pos, P, m.attention_head_count, m.kv_head_count, m.head_dimension,
+                                      m.rope_theta, q, k, v, stream) == KIMKV_OK;
+        if (!ok) break;
+        // Writes.
+        wr.clear();
+        std::vector<std::size_t> wr_owner;
+        for (std::size_t j = 0; j < dec.size(); ++j) {
+            if (!steps[dec[j]].success) continue;
+            std::uint64_t const row = first_row[dec[j]];
+            LayerKvWriteBatchItem it;
+            it.transaction = &reserved[j].transaction;
+            it.write = LayerKvWrite{l, k + row * KD, v + row * KD};
+            wr.push_back(it);
+            wr_owner.push_back(dec[j]);
+        }
+        if (!wr.empty()) {
+            LayerKvWriteBatch b{wr.data(), wr.size()};
+            writeLayerBatch(b);
+        }
+        live_chunks.clear();
+        live_pre.clear();
+        pk.clear();
+        pv.clear();
+        for (std::size_t j = 0; j < pre.size(); ++j) {
+            if (!steps[pre[j]].success) continue;
+            std::uint64_t const row = first_row[pre[j]];
+            live_chunks.push_back(&chunks[j]);
+            live_pre.push_back(pre[j]);
+            pk.push_back(k + row * KD);
+            pv.push_back(v + row * KD);
+        }
+        pst.assign(live_chunks.size(), EngineKvStatus{});
+        if (!live_chunks.empty()) {
+            writePrefillBatch(live_chunks.data(), live_chunks.size(), l, pk.data(), pv.data(), pst.data());
+        }
+        for (std::size_t w = 0; w < wr.size(); ++w) {
+            if (!wr[w].status.ok()) fail(wr_owner[w], "K/V write failed: " + std::string(toString(wr[w].status.error)));
+        }
+        for (std::size_t c = 0; c < live_pre.size(); ++c) {
+            if (!pst[c].ok()) fail(live_pre[c], "chunk K/V write failed: " + std::string(toString(pst[c].error)));
+        }
+        // Attention.
+        at.clear();
+        std::vector<std::size_t> at_owner;
+        for (std::size_t j = 0; j < dec.size(); ++j) {
+            if (!steps[dec[j]].success) continue;
+            std::uint64_t const row = first_row[dec[j]];
+            PagedDecodeBatchItem it;
+            it.transaction = &reserved[j].transaction;
+            it.request = PagedDecodeRequest{l, q + row * QD, attn + row * QD, decode_ws + at.size() * ws_lane, ws_lane,
+                                            scale};
+            at.push_back(it);
+            at_owner.push_back(dec[j]);
+        }
+        if (!at.empty()) {
+            PagedDecodeBatch b{at.data(), at.size(), at_host.data(), d_items, dec.size()};
+            attendLayerBatch(b);
+            for (std::size_t a = 0; a < at.size(); ++a) {
+                if (!at[a].status.ok()) fail(at_owner[a], "decode attention failed: " + std::string(toString(at[a].status.error)));
+            }
+        }
+        live_chunks.clear();
+        live_pre.clear();
+        pq.clear();
+        po.clear();
+        for (std::size_t j = 0; j < pre.size(); ++j) {
+            if (!steps[pre[j]].success) continue;
+            std::uint64_t const row = first_row[pre[j]];
+            live_chunks.push_back(&chunks[j]);
+            live_pre.push_back(pre[j]);
+            pq.push_back(q + row * QD);
+            po.push_back(attn + row * QD);
+        }
+        pst.assign(live_chunks.size(), EngineKvStatus{});
+        if (!live_chunks.empty()) {
+            attendPrefillBatch(live_chunks.data(), live_chunks.size(), l, pq.data(), po.data(), scale, pst.data());
+            for (std::size_t c = 0; c < live_pre.size(); ++c) {
+                if (!pst[c].ok()) fail(live_pre[c], "chunk attention failed: " + std::string(toString(pst[c].error)));
+            }
+        }
+        // Output projection + residual, MLP + residual.
+        ok = kimkv_linear(attn, P, m.hidden_size, L.wo, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK
+            && kimkv_model_rmsnorm(x, nullptr, P, L.ln2, m.hidden_size, m.rms_norm_epsilon, h, stream) == KIMKV_OK
+            && kimkv_linear(h, P, m.hidden_size, L.wgu, 2 * m.intermediate_size, gu, 0, 0.0f, stream) == KIMKV_OK
+            && kimkv_model_swiglu(gu, P, m.intermediate_size, act, stream) == KIMKV_OK
+            && kimkv_linear(act, P, m.intermediate_size, L.wdown, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK;
+    }
+    ok = ok && kimkv_model_rmsnorm(x, d_last, static_cast<std::uint32_t>(S), final_norm, m.hidden_size,
+                                   m.rms_norm_epsilon, hf, stream) == KIMKV_OK
+        && kimkv_linear(hf, static_cast<std::uint32_t>(S), m.hidden_size, head, m.vocabulary_size, logits, 1, 0.0f,
+                        stream) == KIMKV_OK
+        && kimkv_model_argmax(logits, static_cast<std::uint32_t>(S), m.vocabulary_size, d_tokens, stream) == KIMKV_OK
+        && kimkv_memcpy_d2h_async(tokens_out, d_tokens, S * 4ull, stream) == KIMKV_OK;
+    if (ok && host_logits != nullptr) {
+        ok = kimkv_memcpy_d2h_async(host_logits, logits, S * std::uint64_t{m.vocabulary_size} * 4, stream) == KIMKV_OK;
+    }
+
+    // Completion: commit / finish (each waits for its work), then the stream.
+    for (std::size_t j = 0; j < dec.size(); ++j) {
+        if (!reserved[j].transaction.valid()) continue;
+        if (steps[dec[j]].success && ok) {
+            EngineKvStatus const c = reserved[j].transaction.commit();
+            if (!c.ok()) fail(dec[j], "commit failed: " + std::string(toString(c.error)));
+        } else {
+            static_cast<void>(reserved[j].transaction.rollback());
+        }
+    }
+    for (std::size_t j = 0; j < pre.size(); ++j) {
+        if (!chunks[j].valid()) continue;
+        EngineKvStatus const f = chunks[j].finish();
+        if (!f.ok()) fail(pre[j], "prefill chunk finish failed: " + std::string(toString(f.error)));
+    }
+    if (kimkv_stream_synchronize(stream) != KIMKV_OK) ok = false;
+    if (!ok) {
+        result.detail = "device submission failed in the model forward";
+        return result;
+    }
+    for (std::size_t i = 0; i < S; ++i) {
+        if (steps[i].success) steps[i].greedy_token_id = tokens_out[i];
+    }
+    result.steps = std::move(steps);
+    result.success = true;
+    return result;
+}
+
+// ---- public surface ---------------------------------------------------------------------
+
+std::unique_ptr<HipTinyLlamaRunner> HipTinyLlamaRunner::create(EngineKvBackend& kv, HipModelRunnerConfig const& config,
+                                                               HipStream stream, std::string* error)
+{
+    TinyLlamaConfig const& m = config.model;
+    EngineKvConfig const e = kv.config();
+    if (!m.valid() || config.max_positions == 0 || config.max_spans == 0) {
+        if (error) *error = "invalid model or runner configuration";
+        return nullptr;
+    }
+    if (e.kv_layout.layer_count != m.layer_count || e.kv_layout.kv_head_count != m.kv_head_count
+        || e.kv_layout.head_dimension != m.head_dimension || e.query_head_count != m.attention_head_count) {
+        if (error) *error = "KV backend layout does not match the model";
+        return nullptr;
+    }
+    auto impl = std::make_unique<Impl>();
+    impl->kv = &kv;
+    impl->cfg = config;
+    impl->stream = stream;
+    impl->QD = m.attention_head_count * m.head_dimension;
+    impl->KD = m.kv_head_count * m.head_dimension;
+    impl->W_qkv = impl->QD + 2 * impl->KD;
+    impl->ws_lane = (e.attention_workspace_bytes + 255) & ~std::size_t{255};
+    if (!impl->allocate(error)) return nullptr;
+    if (!impl->initWeights()) {
+        if (error) *error = "weight initialisation failed";
+        return nullptr;
+    }
+    return std::unique_ptr<HipTinyLlamaRunner>(new HipTinyLlamaRunner(std::move(impl)));
+}
+
+HipTinyLlamaRunner::HipTinyLlamaRunner(std::unique_ptr<Impl> impl) noexcept : impl_(std::move(impl)) {}
+HipTinyLlamaRunner::~HipTinyLlamaRunner() = default;
+
+TinyLlamaConfig HipTinyLlamaRunner::generationConfig() const noexcept { return impl_->cfg.model; }
+std::uint32_t HipTinyLlamaRunner::generationMaxBatchSize() const noexcept { return impl_->cfg.max_positions; }
+std::uint64_t HipTinyLlamaRunner::deviceWeightBytes() const noexcept { return impl_->weight_bytes; }
+std::uint64_t HipTinyLlamaRunner::deviceWorkspaceBytes() const noexcept { return impl_->work_bytes; }
+
+GenerationStepResult HipTinyLlamaRunner::generationForwardToken(RequestId request_id, std::uint32_t token_id,
+                                                                std::uint32_t expected_position)
+{
+    GenerationBatchResult r = impl_->forward({GenerationSpan{request_id, expected_position, {token_id}}}, nullptr);
+    if (!r.success) return GenerationStepResult{false, 0, std::move(r.detail)};
+    return std::move(r.steps.front());
+}
+
+GenerationBatchResult HipTinyLlamaRunner::generationForwardBatch(std::vector<GenerationBatchItem> const& batch)
+{
+    std::vector<GenerationSpan> spans;
+    spans.reserve(batch.size());
+    for (GenerationBatchItem const& it : batch) spans.push_back({it.request_id, it.expected_position, {it.token_id}});
+    return impl_->forward(spans, nullptr);
+}
+
+GenerationBatchResult HipTinyLlamaRunner::generationForwardSpans(std::vector<GenerationSpan> const& spans)
+{
+    return impl_->forward(spans, nullptr);
+}
+
+GenerationBatchResult HipTinyLlamaRunner::forwardSpans(std::vector<GenerationSpan> const& spans, float* host_logits)
+{
+    return impl_->forward(spans, host_logits);
+}
+
+}  // namespace kimkvcache

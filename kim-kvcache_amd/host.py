@@ -67,6 +67,36 @@ class ManagerSnapshot(ctypes.Structure):
                 ("token_reservation_count", U64), ("micro_pool", PoolSnapshot), ("extent_pool", PoolSnapshot)]
 
 
+class ModelConfig(ctypes.Structure):
+    _fields_ = [("hidden_size", U32), ("intermediate_size", U32), ("layer_count", U32),
+                ("attention_head_count", U32), ("kv_head_count", U32), ("head_dimension", U32),
+                ("vocabulary_size", U32), ("max_position_embeddings", U32), ("bos_token_id", U32),
+                ("eos_token_id", U32), ("rms_norm_epsilon", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+
+class SchedulerConfig(ctypes.Structure):
+    _fields_ = [("max_active_requests", U32), ("max_batched_tokens", U32), ("max_kv_tokens", U64),
+                ("prefill_chunk_size", U32)]
+
+
+class IterationResult(ctypes.Structure):
+    _fields_ = [("iteration", U64), ("model_forward_tokens", U32), ("model_forward_batches", U32),
+                ("prefill_tokens", U32), ("decode_tokens", U32), ("terminals_produced", U32)]
+
+
+class TerminalInfo(ctypes.Structure):
+    _fields_ = [("request_id", U64), ("reason", U32), ("error", U32), ("prompt_tokens", U32),
+                ("completion_tokens", U32), ("ttft_ns", U64), ("tpot_ns", U64), ("e2e_ns", U64)]
+
+
+# GenerationTerminalReason / GenerationError / SchedulerAdmissionError (include/kim-kv/engine/*.h).
+TERMINAL_REASONS = ["eos_token", "max_new_tokens", "cancelled", "runtime_stopped", "failed"]
+GENERATION_ERRORS = ["none", "invalid_argument", "runtime_stopped", "model_failed", "kv_backend_failed",
+                     "internal_error"]
+ADMISSION_ERRORS = ["none", "invalid_argument", "runtime_stopped", "duplicate_request", "max_active_requests",
+                    "kv_token_budget", "internal_error"]
+
+
 class CacheResult(ctypes.Structure):
     _fields_ = [("metadata_error", I), ("device_status", I)]
 
@@ -112,6 +142,20 @@ _SIG = {
                                          ctypes.POINTER(I)]),
     "kimkv_prefill_attend_batch": (None, [ctypes.POINTER(P), U32, U32, ctypes.POINTER(P), ctypes.POINTER(P),
                                           ctypes.c_float, ctypes.POINTER(I)]),
+    "kimkv_runner_create": (P, [P, ctypes.POINTER(ModelConfig), U64, U32, U32, P]),
+    "kimkv_runner_destroy": (None, [P]),
+    "kimkv_runner_weight_bytes": (U64, [P]),
+    "kimkv_runner_forward": (I, [P, U32, P, P, P, P, P, P, P]),
+    "kimkv_scheduler_create": (P, [P, P, ctypes.POINTER(SchedulerConfig)]),
+    "kimkv_scheduler_destroy": (None, [P]),
+    "kimkv_scheduler_submit": (I, [P, U64, P, U32, U32, ctypes.c_int64]),
+    "kimkv_scheduler_cancel": (I, [P, U64]),
+    "kimkv_scheduler_run_iteration": (None, [P, ctypes.POINTER(IterationResult)]),
+    "kimkv_scheduler_drain": (U32, [P]),
+    "kimkv_scheduler_collect": (U32, [P]),
+    "kimkv_scheduler_terminal": (I, [P, U32, ctypes.POINTER(TerminalInfo), P, U32]),
+    "kimkv_scheduler_clear_terminals": (None, [P]),
+    "kimkv_scheduler_idle": (I, [P]),
     "kimkv_cache_create": (P, [device.Layout, U32, U32]),
     "kimkv_cache_destroy": (None, [P]),
     "kimkv_cache_status": (I, [P]),
@@ -527,3 +571,108 @@ class LaneBatch:
 
     def failed(self) -> bool:
         return bool(self.status.any())
+
+
+class Runner:
+    """HipTinyLlamaRunner (seeded N(0, 0.02) fp16 weights) on an Engine."""
+
+    def __init__(self, engine: "Engine", model: ModelConfig, seed: int, max_positions: int, max_spans: int,
+                 stream: Optional[device.Stream] = None):
+        self.engine, self.model = engine, model
+        self.h = lib().kimkv_runner_create(engine.h, ctypes.byref(model), seed, max_positions, max_spans,
+                                           stream.handle if stream else None)
+        if not self.h:
+            raise RuntimeError("model runner creation failed")
+
+    def weight_bytes(self) -> int:
+        return lib().kimkv_runner_weight_bytes(self.h)
+
+    def forward(self, spans, want_logits: bool = False):
+        """spans: list of (request_id, first_position, [token ids]).  Returns
+        (next_tokens, step_ok, logits or None)."""
+        import numpy as np
+        n = len(spans)
+        ids = np.array([s[0] for s in spans], dtype=np.uint64)
+        first = np.array([s[1] for s in spans], dtype=np.uint32)
+        counts = np.array([len(s[2]) for s in spans], dtype=np.uint32)
+        tokens = np.concatenate([np.asarray(s[2], dtype=np.uint32) for s in spans])
+        nxt = np.zeros(n, dtype=np.uint32)
+        ok = np.zeros(n, dtype=np.int32)
+        logits = np.zeros((n, self.model.vocabulary_size), dtype=np.float32) if want_logits else None
+        rc = lib().kimkv_runner_forward(self.h, n, ids.ctypes.data, first.ctypes.data, counts.ctypes.data,
+                                        tokens.ctypes.data, nxt.ctypes.data, ok.ctypes.data,
+                                        logits.ctypes.data if logits is not None else None)
+        if rc != 0:
+            raise RuntimeError("model forward failed")
+        return nxt, ok.astype(bool), logits
+
+    def close(self):
+        if self.h:
+            lib().kimkv_runner_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Scheduler:
+    """IterationSchedulerRuntime over an Engine and a Runner."""
+
+    def __init__(self, engine: "Engine", runner: Runner, max_active: int, max_batched_tokens: int,
+                 max_kv_tokens: int, prefill_chunk: int):
+        self.engine, self.runner = engine, runner
+        cfg = SchedulerConfig(max_active, max_batched_tokens, max_kv_tokens, prefill_chunk)
+        self.h = lib().kimkv_scheduler_create(engine.h, runner.h, ctypes.byref(cfg))
+        if not self.h:
+            raise RuntimeError("scheduler creation failed")
+
+    def submit(self, rid: int, prompt, max_new_tokens: int, eos: int = -1) -> str:
+        import numpy as np
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.uint32))
+        rc = lib().kimkv_scheduler_submit(self.h, rid, p.ctypes.data if p.size else None, p.size, max_new_tokens, eos)
+        return ADMISSION_ERRORS[rc]
+
+    def cancel(self, rid: int) -> bool:
+        return lib().kimkv_scheduler_cancel(self.h, rid) == 1
+
+    def run_iteration(self) -> IterationResult:
+        r = IterationResult()
+        lib().kimkv_scheduler_run_iteration(self.h, ctypes.byref(r))
+        return r
+
+    def idle(self) -> bool:
+        return lib().kimkv_scheduler_idle(self.h) == 1
+
+    def _take(self, count: int):
+        out = []
+        for i in range(count):
+            info = TerminalInfo()
+            n = lib().kimkv_scheduler_terminal(self.h, i, ctypes.byref(info), None, 0)
+            toks = (U32 * max(n, 1))()
+            lib().kimkv_scheduler_terminal(self.h, i, ctypes.byref(info), toks, n)
+            out.append({"request_id": info.request_id, "reason": TERMINAL_REASONS[info.reason],
+                        "error": GENERATION_ERRORS[info.error], "prompt_tokens": info.prompt_tokens,
+                        "completion_tokens": info.completion_tokens, "tokens": list(toks[:n]),
+                        "ttft_ns": info.ttft_ns, "tpot_ns": info.tpot_ns, "e2e_ns": info.e2e_ns})
+        lib().kimkv_scheduler_clear_terminals(self.h)
+        return out
+
+    def drain(self):
+        return self._take(lib().kimkv_scheduler_drain(self.h))
+
+    def take_terminals(self):
+        return self._take(lib().kimkv_scheduler_collect(self.h))
+
+    def close(self):
+        if self.h:
+            lib().kimkv_scheduler_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,151 @@
+"""TinyLlama-shaped CPU reference forward -- TEST INFRASTRUCTURE ONLY.
+
+A numpy restatement of the reference's CPU ReferenceModel
+(tests/cuda/cuda_model_runner_test.cpp:213-441): fp32 arithmetic with every
+activation rounded to fp16 (round to nearest even, the oracle's pinned codec)
+at the same points -- matvec outputs (q, k, v, o, gate, up, down), RMSNorm
+outputs, RoPE outputs, attention outputs, SwiGLU outputs and residual sums --
+and fp32 logits.  Weights are the runner's seeded ones: element (r, c) of the
+tensor with first row row0 is fp16(float(synth(seed, row0 + r, c)) * 0.017320508)
+(N(0, 0.02) from the synthetic generator, whose std is 2/sqrt(3)); RMSNorm
+weights are one.  Row ids: (layer + 1) << 40 | kind << 32, with layer ==
+layer_count for the embedding and the LM head.
+
+Only tests/ and bench.py's check may import this module.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import f16_to_f32, f32_to_f16, synth_rows
+
+WEIGHT_SCALE = np.float32(0.017320508)
+KIND = {"q": 1, "k": 2, "v": 3, "o": 4, "gate": 5, "up": 6, "down": 7, "embed": 8, "head": 9}
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    hidden_size: int
+    intermediate_size: int
+    layer_count: int
+    attention_head_count: int
+    kv_head_count: int
+    head_dimension: int
+    vocabulary_size: int
+    max_position_embeddings: int
+    bos_token_id: int = 1
+    eos_token_id: int = 2
+    rms_norm_epsilon: float = 1e-5
+    rope_theta: float = 10000.0
+
+
+def rounded(x) -> np.ndarray:
+    """fp32 -> fp16 (RNE) -> fp32 through the oracle's codec."""
+    return f16_to_f32(f32_to_f16(np.asarray(x, dtype=np.float32)))
+
+
+def weight_row(layer: int, kind: str) -> int:
+    return ((layer + 1) << 40) | (KIND[kind] << 32)
+
+
+def seeded_weight(seed: int, rows: int, cols: int, row0: int) -> np.ndarray:
+    codes = synth_rows(rows * cols, seed, row0, cols)
+    return rounded(f16_to_f32(codes) * WEIGHT_SCALE).reshape(rows, cols)
+
+
+def matvec(w: np.ndarray, x: np.ndarray, round_output: bool = True) -> np.ndarray:
+    y = (w.astype(np.float64) @ x.astype(np.float64)).astype(np.float32)
+    return rounded(y) if round_output else y
+
+
+def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    sq = np.float32(np.sum(x.astype(np.float64) ** 2))
+    scale = np.float32(1.0) / np.sqrt(sq / np.float32(x.size) + np.float32(eps), dtype=np.float32)
+    return rounded(x * scale * weight)
+
+
+def apply_rope(v: np.ndarray, heads: int, dim: int, position: int, theta: float) -> np.ndarray:
+    half = dim // 2
+    out = v.copy().reshape(heads, dim)
+    d = np.arange(half, dtype=np.float32)
+    angle = np.float32(position) * np.power(np.float32(theta), np.float32(-2.0) * d / np.float32(dim),
+                                             dtype=np.float32)
+    c, s = np.cos(angle).astype(np.float32), np.sin(angle).astype(np.float32)
+    left, right = out[:, :half].copy(), out[:, half:].copy()
+    out[:, :half] = rounded(left * c - right * s)
+    out[:, half:] = rounded(right * c + left * s)
+    return out.reshape(-1)
+
+
+class ReferenceModel:
+    """Token-at-a-time forward with its own KV history (positions in order)."""
+
+    def __init__(self, cfg: ModelConfig, seed: int):
+        self.cfg = cfg
+        H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocabulary_size
+        QD = cfg.attention_head_count * cfg.head_dimension
+        KD = cfg.kv_head_count * cfg.head_dimension
+        self.layers = []
+        for l in range(cfg.layer_count):
+            self.layers.append({
+                "q": seeded_weight(seed, QD, H, weight_row(l, "q")),
+                "k": seeded_weight(seed, KD, H, weight_row(l, "k")),
+                "v": seeded_weight(seed, KD, H, weight_row(l, "v")),
+                "o": seeded_weight(seed, H, H, weight_row(l, "o")),
+                "gate": seeded_weight(seed, I, H, weight_row(l, "gate")),
+                "up": seeded_weight(seed, I, H, weight_row(l, "up")),
+                "down": seeded_weight(seed, H, I, weight_row(l, "down")),
+                "ln1": np.ones(H, dtype=np.float32),
+                "ln2": np.ones(H, dtype=np.float32),
+            })
+        L = cfg.layer_count
+        self.embed = seeded_weight(seed, V, H, weight_row(L, "embed"))
+        self.head = seeded_weight(seed, V, H, weight_row(L, "head"))
+        self.final_norm = np.ones(H, dtype=np.float32)
+        self.keys = [[] for _ in range(L)]
+        self.values = [[] for _ in range(L)]
+        self.final_hidden = None
+
+    def forward(self, token: int, position: int) -> np.ndarray:
+        cfg = self.cfg
+        D, QH, KVH = cfg.head_dimension, cfg.attention_head_count, cfg.kv_head_count
+        G = QH // KVH
+        scale = np.float32(1.0) / np.sqrt(np.float32(D))
+        hidden = self.embed[token].copy()
+        for l, W in enumerate(self.layers):
+            x = rms_norm(hidden, W["ln1"], cfg.rms_norm_epsilon)
+            q = apply_rope(matvec(W["q"], x), QH, D, position, cfg.rope_theta)
+            k = apply_rope(matvec(W["k"], x), KVH, D, position, cfg.rope_theta)
+            v = matvec(W["v"], x)
+            self.keys[l].append(k)
+            self.values[l].append(v)
+            K = np.stack(self.keys[l]).reshape(-1, KVH, D).astype(np.float64)
+            Vv = np.stack(self.values[l]).reshape(-1, KVH, D).astype(np.float64)
+            attn = np.zeros(QH * D, dtype=np.float32)
+            for h in range(QH):
+                s = (K[:, h // G, :] @ q[h * D:(h + 1) * D].astype(np.float64)).astype(np.float32) * scale
+                p = np.exp((s - s.max()).astype(np.float64))
+                attn[h * D:(h + 1) * D] = rounded(((p / p.sum()) @ Vv[:, h // G, :]).astype(np.float32))
+            hidden = rounded(hidden + matvec(W["o"], attn))
+            x = rms_norm(hidden, W["ln2"], cfg.rms_norm_epsilon)
+            gate, up = matvec(W["gate"], x), matvec(W["up"], x)
+            act = rounded(gate / (np.float32(1.0) + np.exp(-gate)) * up)
+            hidden = rounded(hidden + matvec(W["down"], act))
+        self.final_hidden = rms_norm(hidden, self.final_norm, cfg.rms_norm_epsilon)
+        return matvec(self.head, self.final_hidden, round_output=False)
+
+    def generate(self, prompt, max_new_tokens: int, eos: int | None = None):
+        """Greedy generation (tests/cuda/cuda_model_runner_test.cpp:423-443)."""
+        logits = None
+        for p, t in enumerate(prompt):
+            logits = self.forward(int(t), p)
+        out = []
+        for g in range(max_new_tokens):
+            nxt = int(np.argmax(logits))
+            out.append(nxt)
+            if (eos is not None and nxt == eos) or g + 1 == max_new_tokens:
+                break
+            logits = self.forward(nxt, len(prompt) + g)
+        return out

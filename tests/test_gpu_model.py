@@ -1,0 +1,140 @@
+"""GPU tests of the TinyLlama-shaped model runner and the iteration scheduler
+on the HIP engine (scenarios of the reference's
+tests/cuda/cuda_model_runner_test.cpp:445-560 and the scheduler e2e path).
+The checker is the oracle's CPU forward (oracle/model.py, pinned by
+tests/test_model_oracle.py) with the same seeded weights: logits within
+0.035 max-abs (the reference's bar) and every greedy token the oracle's
+argmax up to that tolerance.  Generation is teacher-forced with the GPU's
+tokens so a near-tie cannot make the sequences diverge."""
+import numpy as np
+import pytest
+
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+
+CFG = om.ModelConfig(hidden_size=256, intermediate_size=512, layer_count=2, attention_head_count=4,
+                     kv_head_count=2, head_dimension=64, vocabulary_size=512, max_position_embeddings=1024)
+SEED = 1234
+TOL = 0.035
+
+
+@pytest.fixture(scope="module")
+def host(kimkv, dev):
+    import importlib
+    return importlib.import_module(kimkv.__name__ + ".host")
+
+
+def model_config(host):
+    c = CFG
+    return host.ModelConfig(c.hidden_size, c.intermediate_size, c.layer_count, c.attention_head_count,
+                            c.kv_head_count, c.head_dimension, c.vocabulary_size, c.max_position_embeddings,
+                            c.bos_token_id, c.eos_token_id, c.rms_norm_epsilon, c.rope_theta)
+
+
+def make(host, dev, max_positions=256, max_spans=8):
+    engine = host.Engine(CFG.layer_count, CFG.kv_head_count, CFG.head_dimension, CFG.attention_head_count, 1 << 20,
+                         1024, 64)
+    stream = dev.Stream()
+    runner = host.Runner(engine, model_config(host), SEED, max_positions, max_spans, stream)
+    return engine, runner, stream
+
+
+def check_logits(got, want, tag):
+    err = float(np.max(np.abs(got - want)))
+    assert err < TOL, (tag, err)
+    return err
+
+
+def check_token(token, want_logits, tag):
+    """The GPU's greedy token is the oracle's argmax up to the logit tolerance."""
+    assert want_logits[token] >= want_logits.max() - TOL, (tag, int(token), int(np.argmax(want_logits)))
+
+
+def test_runner_spans_match_oracle(host, dev):
+    engine, runner, stream = make(host, dev)
+    rng = np.random.default_rng(5)
+    pa = [int(t) for t in rng.integers(0, CFG.vocabulary_size, 37)]
+    pb = [int(t) for t in rng.integers(0, CFG.vocabulary_size, 30)]
+    assert engine.create_request(1) == 0 and engine.create_request(2) == 0
+    ra, rb = om.ReferenceModel(CFG, SEED), om.ReferenceModel(CFG, SEED)
+    worst = 0.0
+
+    # A: 37-token prompt chunk.
+    nxt, ok, logits = runner.forward([(1, 0, pa)], want_logits=True)
+    assert ok.all()
+    for p, t in enumerate(pa):
+        want = ra.forward(t, p)
+    worst = max(worst, check_logits(logits[0], want, "A chunk"))
+    check_token(nxt[0], want, "A chunk")
+    ga = int(nxt[0])
+
+    # A decodes one token while B's first 9 prompt tokens go as a chunk.
+    nxt, ok, logits = runner.forward([(1, 37, [ga]), (2, 0, pb[:9])], want_logits=True)
+    assert ok.all()
+    wa = ra.forward(ga, 37)
+    for p in range(9):
+        wb = rb.forward(pb[p], p)
+    worst = max(worst, check_logits(logits[0], wa, "A decode"), check_logits(logits[1], wb, "B chunk"))
+    check_token(nxt[0], wa, "A decode")
+    ga = int(nxt[0])
+
+    # Single positions for both (B still in its prompt).
+    nxt, ok, logits = runner.forward([(2, 9, [pb[9]]), (1, 38, [ga])], want_logits=True)
+    assert ok.all()
+    wb, wa = rb.forward(pb[9], 9), ra.forward(ga, 38)
+    worst = max(worst, check_logits(logits[0], wb, "B single"), check_logits(logits[1], wa, "A decode 2"))
+
+    # B's next 20 prompt tokens as a chunk after a 10-token context (partial micro tail).
+    nxt, ok, logits = runner.forward([(2, 10, pb[10:30])], want_logits=True)
+    assert ok.all()
+    for p in range(10, 30):
+        wb = rb.forward(pb[p], p)
+    worst = max(worst, check_logits(logits[0], wb, "B chunk 2"))
+    check_token(nxt[0], wb, "B chunk 2")
+
+    snap = engine.snapshot()
+    assert snap.committed_token_count == 39 + 30 and snap.active_transaction_count == 0
+    assert engine.check_invariants()
+    # A position that is not the committed length fails for its request only.
+    nxt, ok, _ = runner.forward([(1, 5, [3]), (2, 30, [int(nxt[0])])])
+    assert list(ok) == [False, True]
+    print(f"runner spans max logit err {worst:.2e}", flush=True)
+    assert engine.release_request(1) == 0 and engine.release_request(2) == 0
+    runner.close()
+    stream.destroy()
+
+
+def test_scheduler_generation_matches_oracle(host, dev):
+    engine, runner, stream = make(host, dev, max_positions=192, max_spans=8)
+    sched = host.Scheduler(engine, runner, max_active=8, max_batched_tokens=128, max_kv_tokens=1 << 16,
+                           prefill_chunk=32)
+    rng = np.random.default_rng(9)
+    prompts = {10: 45, 11: 20, 12: 70, 13: 3}
+    sent = {}
+    for rid, n in prompts.items():
+        sent[rid] = [int(t) for t in rng.integers(3, CFG.vocabulary_size, n)]
+        assert sched.submit(rid, sent[rid], 6) == "none"
+    first = sched.run_iteration()
+    # Every request's first chunk (32 positions max) in one call.
+    assert first.model_forward_batches == 1 and first.prefill_tokens == 32 + 20 + 32 + 3
+    done = {t["request_id"]: t for t in sched.drain()}
+    assert sorted(done) == sorted(prompts)
+    for rid, t in done.items():
+        assert t["error"] == "none", t
+        toks = t["tokens"]
+        assert t["prompt_tokens"] == prompts[rid] and t["completion_tokens"] == len(toks)
+        assert (t["reason"] == "eos_token" and toks[-1] == CFG.eos_token_id) or \
+            (t["reason"] == "max_new_tokens" and len(toks) == 6)
+        ref = om.ReferenceModel(CFG, SEED)
+        for p, tok in enumerate(sent[rid]):
+            logits = ref.forward(tok, p)
+        for g, tok in enumerate(toks):
+            check_token(tok, logits, f"request {rid} token {g}")
+            if g + 1 < len(toks):
+                logits = ref.forward(tok, prompts[rid] + g)
+    assert engine.snapshot().request_count == 0
+    assert engine.check_invariants()
+    sched.close()
+    runner.close()
+    stream.destroy()

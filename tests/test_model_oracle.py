@@ -1,0 +1,97 @@
+"""Pins the model oracle (oracle/model.py) before it is used as the checker of
+the GPU model runner:
+  * RoPE at position 0 is the identity, and it preserves each pair's norm;
+  * the first position's attention output is its own V (softmax over one key);
+  * an independent float64 Llama forward written with torch library routines
+    (F.rms_norm, rotate-half RoPE, F.scaled_dot_product_attention with causal
+    mask and grouped KV heads, F.silu) and no fp16 rounding agrees with the
+    oracle's logits to within the fp16 rounding noise at every position.
+A dropped term (residual, norm weight), a wrong RoPE pairing, a wrong GQA
+head mapping or a non-causal mask each fail the last check by far more."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import model as om
+
+CFG = om.ModelConfig(hidden_size=128, intermediate_size=256, layer_count=2, attention_head_count=4,
+                     kv_head_count=2, head_dimension=32, vocabulary_size=96, max_position_embeddings=64)
+SEED = 77
+
+
+def test_rope_identity_and_norm():
+    v = om.rounded(np.random.default_rng(0).standard_normal(4 * 32).astype(np.float32))
+    assert np.array_equal(om.apply_rope(v, 4, 32, 0, 10000.0), v)
+    r = om.apply_rope(v, 4, 32, 9, 10000.0).reshape(4, 2, 16)
+    x = v.reshape(4, 2, 16)
+    assert np.allclose(np.hypot(r[:, 0], r[:, 1]), np.hypot(x[:, 0], x[:, 1]), rtol=2e-3, atol=2e-3)
+
+
+def test_seeded_weights_statistics():
+    w = om.seeded_weight(SEED, 256, 256, om.weight_row(0, "q"))
+    assert abs(float(w.mean())) < 1e-3 and abs(float(w.std()) - 0.02) < 1e-3
+    assert not np.array_equal(w, om.seeded_weight(SEED, 256, 256, om.weight_row(0, "k")))
+
+
+def _torch_logits(ref: om.ReferenceModel, tokens):
+    """Float64 Llama forward over the whole sequence, no intermediate rounding."""
+    c = ref.cfg
+    D, QH, KVH = c.head_dimension, c.attention_head_count, c.kv_head_count
+    t = lambda a: torch.from_numpy(np.asarray(a, dtype=np.float64))
+    n = len(tokens)
+    x = t(ref.embed[np.asarray(tokens)])                                        # [n][H]
+    pos = torch.arange(n, dtype=torch.float64)
+    inv = c.rope_theta ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)   # [D/2]
+    ang = pos[:, None] * inv[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], -1)[None, :, None, :]
+    sin = torch.cat([ang.sin(), ang.sin()], -1)[None, :, None, :]
+
+    def rot(v):                                                                 # [1][n][h][D]
+        half = torch.cat([-v[..., D // 2:], v[..., :D // 2]], -1)
+        return v * cos + half * sin
+
+    for W in ref.layers:
+        h = F.rms_norm(x, (c.hidden_size,), weight=t(W["ln1"]), eps=c.rms_norm_epsilon)
+        q = rot((h @ t(W["q"]).T).view(1, n, QH, D)).transpose(1, 2)
+        k = rot((h @ t(W["k"]).T).view(1, n, KVH, D)).transpose(1, 2)
+        v = (h @ t(W["v"]).T).view(1, n, KVH, D).transpose(1, 2)
+        a = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+        x = x + a.transpose(1, 2).reshape(n, -1) @ t(W["o"]).T
+        h = F.rms_norm(x, (c.hidden_size,), weight=t(W["ln2"]), eps=c.rms_norm_epsilon)
+        x = x + (F.silu(h @ t(W["gate"]).T) * (h @ t(W["up"]).T)) @ t(W["down"]).T
+    h = F.rms_norm(x, (c.hidden_size,), weight=t(ref.final_norm), eps=c.rms_norm_epsilon)
+    return (h @ t(ref.head).T).numpy()
+
+
+def test_oracle_matches_independent_float64_llama():
+    ref = om.ReferenceModel(CFG, SEED)
+    tokens = [5, 17, 3, 88, 41, 0, 63, 12, 9, 50]
+    want = _torch_logits(ref, tokens)
+    scale = float(np.abs(want).max())
+    for p, tok in enumerate(tokens):
+        got = ref.forward(tok, p)
+        assert np.max(np.abs(got - want[p])) < 0.004 * scale + 1e-3, p   # measured 4e-4 at scale 0.8
+
+
+def test_first_position_attention_is_value():
+    ref = om.ReferenceModel(CFG, SEED)
+    ref.forward(7, 0)
+    # One key: every query head's output is its KV head's value row; the
+    # first layer's stored V equals W_v . rmsnorm(embedding).
+    x = om.rms_norm(ref.embed[7].copy(), ref.layers[0]["ln1"], CFG.rms_norm_epsilon)
+    assert np.array_equal(ref.values[0][0], om.matvec(ref.layers[0]["v"], x))
+    assert np.array_equal(ref.keys[0][0], om.matvec(ref.layers[0]["k"], x))   # RoPE at 0 is the identity
+
+
+def test_wrong_structure_is_detected():
+    """A planted mistake in the oracle (layer 0's attention output dropped)
+    breaks the agreement with the float64 forward."""
+    ref = om.ReferenceModel(CFG, SEED)
+    tokens = [5, 17, 3, 88]
+    want = _torch_logits(ref, tokens)
+    # Plant the mistake: drop layer 0's output projection.
+    ref.layers[0]["o"] = np.zeros_like(ref.layers[0]["o"])
+    got = [ref.forward(tk, p) for p, tk in enumerate(tokens)]
+    err = max(float(np.max(np.abs(g - w))) for g, w in zip(got, want))
+    assert err > 0.05 * float(np.abs(want).max())
