@@ -839,6 +839,126 @@ def run_prefill(kimkv, dev, args) -> int:
     return 0 if ok else 1
 
 
+def run_e2e(kimkv, dev, args) -> int:
+    """End-to-end TinyLlama-1.1B-shaped fp16 model (seeded N(0, 0.02) weights,
+    RMSNorm weights one) under the iteration scheduler, in the steady state of
+    --e2e-prefill requests doing --prefill-chunk-token chunked prefill (prompts
+    U[256, 2048]) beside --e2e-decode decode lanes.  Setup (untimed): the
+    decode lanes (prompts U[256, 1536], enough new tokens to outlive the run)
+    are prefilled until every one is decoding.  Each timed step is one
+    scheduler iteration under a budget of prefill * chunk + decode positions:
+    one model call with every decode lane's next token and each prefilling
+    request's next chunk; a prefilling request asks for one new token, so it
+    leaves when its prompt completes and is replaced, keeping the mix fixed.
+    Check: a short request through the same scheduler, teacher-forced through
+    the oracle's CPU forward of the same model (every GPU token within 0.035
+    of the oracle's max logit)."""
+    import importlib
+    host = importlib.import_module(kimkv.__name__ + ".host")
+    L, KVH, D, QH, HID, INTER, VOC, MAXPOS = 22, 4, 64, 32, 2048, 5632, 32000, 2048
+    n_dec, n_pre, chunk = args.e2e_decode, args.e2e_prefill, args.prefill_chunk
+    budget = n_pre * chunk + n_dec
+    rng = np.random.default_rng(args.seed)
+    micro_cap = (n_dec * 2048 + (2 * n_pre + 2) * 2048) // 8 + 256
+    engine = host.Engine(L, KVH, D, QH, 1 << 20, micro_cap, 16)
+    assert engine.permute_free_slots(0, args.seed) == 0
+    stream = dev.Stream()
+    model = host.ModelConfig(HID, INTER, L, QH, KVH, D, VOC, MAXPOS, 1, 2, 1e-5, 10000.0)
+    t0 = time.time()
+    runner = host.Runner(engine, model, args.seed, budget + 64, n_dec + n_pre + 8, stream)
+    sched = host.Scheduler(engine, runner, max_active=n_dec + n_pre + 8, max_batched_tokens=budget,
+                           max_kv_tokens=1 << 40, prefill_chunk=chunk)
+    log(f"model ready ({runner.weight_bytes() / 2**30:.2f} GiB of weights) in {time.time() - t0:.1f}s")
+    next_id = [1]
+
+    def submit(lo, hi, max_new):
+        rid = next_id[0]
+        next_id[0] += 1
+        n = int(rng.integers(lo, hi + 1))
+        assert sched.submit(rid, rng.integers(3, VOC, n), max_new) == "none"
+        return rid
+
+    decoders = [submit(256, 1536, 400) for _ in range(n_dec)]
+    t0 = time.time()
+    setup_iters = 0
+    while True:
+        r = sched.run_iteration()
+        setup_iters += 1
+        if r.prefill_tokens == 0:
+            break
+    finished = sched.take_terminals()
+    assert not finished, finished[:1]
+    log(f"{n_dec} decode lanes prefilled in {setup_iters} iterations ({time.time() - t0:.1f}s)")
+    prefilling = set()
+
+    def step():
+        while len(prefilling) < n_pre:
+            prefilling.add(submit(256, 2048, 1))
+        r = sched.run_iteration()
+        for t in sched.take_terminals():
+            assert t["error"] == "none", t
+            prefilling.discard(t["request_id"])
+        return r
+
+    for _ in range(args.warmup):
+        step()
+    dev.prefill_timing(True)
+    dev.decode_timing(True)
+    tok_pre = tok_dec = 0
+    t_wall = time.perf_counter()
+    for _ in range(args.steps):
+        r = step()
+        tok_pre += r.prefill_tokens
+        tok_dec += r.decode_tokens
+    wall = time.perf_counter() - t_wall
+    pf_ms, pf_n = dev.prefill_timing(False)
+    dc_ms, dc_n = dev.decode_timing(False)
+    ms_per_step = wall * 1000.0 / args.steps
+
+    # Correctness sample: a short request through the same scheduler.
+    import oracle.model as om
+    prompt = [int(t) for t in rng.integers(3, VOC, 6)]
+    rid = next_id[0]
+    assert sched.submit(rid, prompt, 3) == "none"
+    out = []
+    for _ in range(64):
+        sched.run_iteration()
+        got = [t for t in sched.take_terminals() if t["request_id"] == rid]
+        if got:
+            out = got[0]["tokens"]
+            break
+    t0 = time.time()
+    ref = om.ReferenceModel(om.ModelConfig(HID, INTER, L, QH, KVH, D, VOC, MAXPOS), args.seed)
+    for p, t in enumerate(prompt):
+        logits = ref.forward(t, p)
+    ok, margin = len(out) == 3, 0.0
+    for g, tok in enumerate(out):
+        margin = max(margin, float(logits.max() - logits[tok]))
+        ok = ok and bool(logits[tok] >= logits.max() - 0.035)
+        if g + 1 < len(out):
+            logits = ref.forward(tok, len(prompt) + g)
+    log(f"oracle check in {time.time() - t0:.1f}s")
+    sched.close()
+    runner.close()
+    total = tok_pre + tok_dec
+    print(json.dumps({
+        "metric": "e2e TinyLlama chunked prefill + decode tokens/s (iteration scheduler)",
+        "value": round(total / wall, 1), "unit": "tokens/s", "higher_is_better": True,
+        "decode_tokens_per_s": round(tok_dec / wall, 1), "prefill_tokens_per_s": round(tok_pre / wall, 1),
+        "ms_per_step": round(ms_per_step, 3), "tokens_per_step": round(total / args.steps, 1),
+        "attention_ms_per_step": {"prefill_kernel": round(pf_ms / args.steps, 3),
+                                  "decode_kernel": round(dc_ms / args.steps, 3)},
+        "dtype": "f16 in, f32 accumulate",
+        "config": {"workload": f"TinyLlama-1.1B-shaped fp16 (22 layers, hidden 2048, SwiGLU 5632, 32q/4kv x 64, "
+                               f"vocab 32000), seeded N(0, 0.02) weights; {n_pre} requests in {chunk}-token chunked "
+                               f"prefill (prompts U[256, 2048]) + {n_dec} decode lanes per iteration, greedy",
+                   "max_batched_tokens": budget},
+        "steps": args.steps, "warmup": args.warmup, "data": "synthetic (random token ids, seeded weights)",
+        "check": {"request_prompt": 6, "tokens": len(out), "all_near_argmax": ok,
+                  "max_logit_gap_to_oracle_max": margin, "tolerance": 0.035}}), flush=True)
+    return 0 if ok else 1
+
+
 def run_copy(dev, args) -> int:
     """Plain device-to-device copy of a known size: the achievable copy
     bandwidth of the box and the calibration run for the FETCH_SIZE /
@@ -895,12 +1015,12 @@ def profiled_traffic(lanes_per_launch: int, context: int, layers: int):
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", choices=["decode", "gather", "append", "shared", "prefill", "copy"],
+    ap.add_argument("--config", choices=["decode", "gather", "append", "shared", "prefill", "e2e", "copy"],
                     default="decode",
                     help="decode: HBM-scale decode+append (the headline line); gather: long-sequence gather; "
                          "append: ragged one-token append with tail allocation; shared: fork/COW shared-prefix "
-                         "decode; prefill: chunked-prefill attention through the engine; copy: plain device copy (bandwidth "
-                         "and counter calibration)")
+                         "decode; prefill: chunked-prefill attention through the engine; e2e: TinyLlama under the iteration "
+                         "scheduler; copy: plain device copy (bandwidth and counter calibration)")
     ap.add_argument("--shared-check", type=int, default=4, help="lanes of the shared config checked")
     ap.add_argument("--append-lanes", type=int, default=64)
     ap.add_argument("--append-check", type=int, default=4, help="lanes gathered and compared bit-exactly")
@@ -912,6 +1032,8 @@ def main() -> int:
     ap.add_argument("--slots", choices=["permuted", "sequential"], default="permuted",
                     help="kernel path: page slots in seeded-permutation order (default) or in pool order")
     ap.add_argument("--prefill-lanes", type=int, default=4)
+    ap.add_argument("--e2e-decode", type=int, default=60)
+    ap.add_argument("--e2e-prefill", type=int, default=4)
     ap.add_argument("--prefill-chunk", type=int, default=512)
     ap.add_argument("--prefill-context", type=int, default=0,
                     help="prefill: the same context for every lane instead of U[256, 2048]")
@@ -947,6 +1069,8 @@ def main() -> int:
         return run_shared(kimkv, dev, args)
     if args.config == "prefill":
         return run_prefill(kimkv, dev, args)
+    if args.config == "e2e":
+        return run_e2e(kimkv, dev, args)
     H, D, QH = 4, 64, 32
     total_steps = args.warmup + args.steps
     if args.path == "engine":

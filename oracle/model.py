@@ -56,7 +56,8 @@ def seeded_weight(seed: int, rows: int, cols: int, row0: int) -> np.ndarray:
 
 
 def matvec(w: np.ndarray, x: np.ndarray, round_output: bool = True) -> np.ndarray:
-    y = (w.astype(np.float64) @ x.astype(np.float64)).astype(np.float32)
+    """fp32 matrix-vector product (fp32 accumulation, like the reference's loop)."""
+    y = np.dot(w, x.astype(np.float32)).astype(np.float32)
     return rounded(y) if round_output else y
 
 
