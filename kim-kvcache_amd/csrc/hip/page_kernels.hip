@@ -115,109 +115,230 @@ __global__ __launch_bounds__(kBlock) void append_kernel(PoolView P, const kimkv_
 }
 
 // ---------------------------------------------------------------------------
-// Gather: block = (64-token tile, layer, component); output [L][2][T][H][D].
-// K rows are copied with 16-byte vectors; V is transposed through LDS.
+// Gather: block = (64-token tile, group of layers); output [L][2][T][H][D].
+// Fast path (full tile whose 8-token groups each sit 8-aligned in one page,
+// D % 8 == 0): every thread issues all its 16-byte non-temporal loads before
+// any store.  K rows are copied straight; V^T is transposed through LDS
+// (16-byte chunks of 8 tokens of one dim row in, 16-byte chunks of 8 dims of
+// one token out; the chunk column is XOR-swizzled by the token's group so the
+// scattered 2-byte writes of one instruction spread over the banks).  Other
+// tiles take the element-wise path.
 // ---------------------------------------------------------------------------
-constexpr unsigned kRowChunk = 256;   // V rows staged per pass
+constexpr unsigned kRowChunk = 256;            // V rows (head x dim) per pass
+constexpr unsigned kStageRow = kRowChunk + 8;  // u16 per staged token row (16-byte multiple)
+constexpr unsigned kGatherLoads = 8;           // 16-byte loads in flight per thread
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4_t global_u32x4_t;
+typedef __attribute__((address_space(1))) u32x4_t global_u32x4_out_t;
+
+__device__ inline u32x4_t load16_nt(const uint16_t* p)
+{
+    return __builtin_nontemporal_load((global_u32x4_t*)(p));
+}
+
+__device__ inline void store16_nt(uint16_t* p, u32x4_t v)
+{
+    __builtin_nontemporal_store(v, (global_u32x4_out_t*)(p));
+}
+
+__device__ inline uint32_t stage_col(uint32_t t, uint32_t r)
+{
+    return (((r >> 3) ^ ((t >> 3) & 3u)) << 3) | (r & 7u);
+}
+
+// K rows of one (tile, layer): straight 16-byte copies, all loads first.
+__device__ inline void gather_k_fast(const PoolView& P, const TokEntry* tab, uint32_t layer, uint16_t* out_base)
+{
+    uint32_t const tid = threadIdx.x;
+    uint32_t const D = P.dim;
+    uint32_t const dchunks = D / 8;
+    uint32_t const per_token = P.heads * dchunks;
+    uint32_t const total = kTile * per_token;
+    for (uint32_t base = 0; base < total; base += kBlock * kGatherLoads) {
+        u32x4_t v[kGatherLoads];
+#pragma unroll
+        for (uint32_t k = 0; k < kGatherLoads; ++k) {
+            uint32_t const i = base + k * kBlock + tid;
+            if (i < total) {
+                uint32_t const t = i / per_token;
+                uint32_t const c = i - t * per_token;
+                uint32_t const h = c / dchunks;
+                TokEntry const e = tab[t];
+                v[k] = load16_nt(e.page + head_block(P, e.cap, layer, h) + k_offset(e.cap, D, e.pt, (c - h * dchunks) * 8));
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kGatherLoads; ++k) {
+            uint32_t const i = base + k * kBlock + tid;
+            if (i < total) store16_nt(out_base + static_cast<uint64_t>(i) * 8, v[k]);
+        }
+    }
+}
+
+// V^T rows of one (tile, layer) transposed through LDS.
+__device__ inline void gather_v_fast(const PoolView& P, const TokEntry* tab, uint32_t layer, uint16_t* out_base,
+                                     uint16_t* stage)
+{
+    uint32_t const tid = threadIdx.x;
+    uint32_t const D = P.dim;
+    uint32_t const HD = P.heads * D;
+    for (uint32_t r0 = 0; r0 < HD; r0 += kRowChunk) {
+        uint32_t const rows = min(kRowChunk, HD - r0);
+        uint32_t const chunks = rows * 8;   // (row, 8-token group) pairs
+        // Chunk q: group (q & 3) + 4 * ((q >> 2) / rows), row (q >> 2) % rows: four consecutive
+        // lanes read one 64-byte dim row of a 32-token V^T panel.
+        for (uint32_t base = 0; base < chunks; base += kBlock * kGatherLoads) {
+            u32x4_t v[kGatherLoads];
+#pragma unroll
+            for (uint32_t k = 0; k < kGatherLoads; ++k) {
+                uint32_t const q = base + k * kBlock + tid;
+                if (q < chunks) {
+                    uint32_t const rr = (q >> 2) % rows;
+                    uint32_t const g = (q & 3u) + 4u * ((q >> 2) / rows);
+                    uint32_t const r = r0 + rr;
+                    uint32_t const h = r / D;
+                    TokEntry const e = tab[8 * g];
+                    v[k] = load16_nt(e.page + head_block(P, e.cap, layer, h) + v_offset(e.cap, D, e.pt, r - h * D));
+                }
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kGatherLoads; ++k) {
+                uint32_t const q = base + k * kBlock + tid;
+                if (q < chunks) {
+                    uint32_t const rr = (q >> 2) % rows;
+                    uint32_t const g = (q & 3u) + 4u * ((q >> 2) / rows);
+#pragma unroll
+                    for (uint32_t j = 0; j < 8; ++j) {
+                        uint32_t const t = 8 * g + j;
+                        uint32_t const word = v[k][j >> 1];
+                        stage[t * kStageRow + stage_col(t, rr)] =
+                            static_cast<uint16_t>((j & 1u) ? (word >> 16) : (word & 0xFFFFu));
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        uint32_t const per_token = rows / 8;
+        for (uint32_t i = tid; i < kTile * per_token; i += kBlock) {
+            uint32_t const t = i / per_token;
+            uint32_t const c = i - t * per_token;
+            u32x4_t const w = *reinterpret_cast<const u32x4_t*>(&stage[t * kStageRow + stage_col(t, c * 8)]);
+            store16_nt(out_base + static_cast<uint64_t>(t) * HD + r0 + c * 8, w);
+        }
+        __syncthreads();
+    }
+}
+
+// One (tile, layer) with H * D == kRowChunk: the K and V^T loads of the
+// layer (8 + 8 per thread) are all in flight before the first store.
+__device__ inline void gather_kv_fast(const PoolView& P, const TokEntry* tab, uint32_t layer, uint16_t* k_base,
+                                      uint16_t* v_base, uint16_t* stage)
+{
+    constexpr uint32_t rows = kRowChunk;
+    constexpr uint32_t per = kTile * rows / 8 / kBlock;   // 16-byte chunks per thread, each of K and V
+    uint32_t const tid = threadIdx.x;
+    uint32_t const D = P.dim;
+    uint32_t const dchunks = D / 8;
+    constexpr uint32_t per_token = rows / 8;
+    u32x4_t kv[per], vv[per];
+#pragma unroll
+    for (uint32_t k = 0; k < per; ++k) {
+        uint32_t const i = k * kBlock + tid;
+        uint32_t const t = i / per_token;
+        uint32_t const c = i - t * per_token;
+        uint32_t const h = c / dchunks;
+        TokEntry const e = tab[t];
+        kv[k] = load16_nt(e.page + head_block(P, e.cap, layer, h) + k_offset(e.cap, D, e.pt, (c - h * dchunks) * 8));
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < per; ++k) {
+        uint32_t const q = k * kBlock + tid;
+        uint32_t const rr = (q >> 2) % rows;
+        uint32_t const g = (q & 3u) + 4u * ((q >> 2) / rows);
+        uint32_t const h = rr / D;
+        TokEntry const e = tab[8 * g];
+        vv[k] = load16_nt(e.page + head_block(P, e.cap, layer, h) + v_offset(e.cap, D, e.pt, rr - h * D));
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < per; ++k) store16_nt(k_base + static_cast<uint64_t>(k * kBlock + tid) * 8, kv[k]);
+#pragma unroll
+    for (uint32_t k = 0; k < per; ++k) {
+        uint32_t const q = k * kBlock + tid;
+        uint32_t const rr = (q >> 2) % rows;
+        uint32_t const g = (q & 3u) + 4u * ((q >> 2) / rows);
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            uint32_t const t = 8 * g + j;
+            uint32_t const word = vv[k][j >> 1];
+            stage[t * kStageRow + stage_col(t, rr)] = static_cast<uint16_t>((j & 1u) ? (word >> 16) : (word & 0xFFFFu));
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = 0; k < per; ++k) {
+        uint32_t const i = k * kBlock + tid;
+        uint32_t const t = i / per_token;
+        uint32_t const c = i - t * per_token;
+        u32x4_t const w = *reinterpret_cast<const u32x4_t*>(&stage[t * kStageRow + stage_col(t, c * 8)]);
+        store16_nt(v_base + static_cast<uint64_t>(t) * rows + c * 8, w);
+    }
+    __syncthreads();
+}
+
+// Block = (64-token tile, group of layers_per_block layers): the tile's page
+// table is resolved once for all its layers and both components.
 __global__ __launch_bounds__(kBlock) void gather_kernel(PoolView P, const kimkv_block_desc* desc,
-                                                        uint32_t count, uint32_t T, uint16_t* out)
+                                                        uint32_t count, uint32_t T, uint32_t layers_per_block,
+                                                        uint16_t* out)
 {
     __shared__ TokEntry tab[kTile];
     __shared__ uint32_t s_idx;
-    __shared__ __align__(16) uint16_t stage[kTile * kRowChunk];
+    __shared__ __align__(16) uint16_t stage[kTile * kStageRow];
 
     uint32_t const t0 = blockIdx.x * kTile;
     uint32_t const n = min(kTile, T - t0);
-    uint32_t const layer = blockIdx.y;
-    uint32_t const comp = blockIdx.z;
     build_tile_table(P, desc, count, t0, n, tab, &s_idx);
 
     uint32_t const D = P.dim;
     uint32_t const HD = P.heads * D;
-    uint16_t* out_base = out + (static_cast<uint64_t>(layer * 2 + comp) * T + t0) * HD;
     uint32_t const tid = threadIdx.x;
+    uint32_t const l0 = blockIdx.y * layers_per_block;
+    uint32_t const l1 = min(P.layers, l0 + layers_per_block);
 
-    if (comp == 0) {
-        if ((D & 7u) == 0) {
-            uint32_t const dchunks = D / 8;
-            uint32_t const per_token = HD / 8;
-            for (uint32_t i = tid; i < n * per_token; i += kBlock) {
-                uint32_t const t = i / per_token;
-                uint32_t const c = i - t * per_token;
-                TokEntry const e = tab[t];
-                if (e.page == nullptr) continue;
-                uint32_t const h = c / dchunks;
-                uint32_t const dc = c - h * dchunks;
-                uint4 const* src = reinterpret_cast<uint4 const*>(
-                    e.page + head_block(P, e.cap, layer, h) + k_offset(e.cap, D, e.pt, dc * 8));
-                reinterpret_cast<uint4*>(out_base)[i] = *src;
-            }
-        } else {
-            for (uint32_t i = tid; i < n * HD; i += kBlock) {
-                uint32_t const t = i / HD;
-                uint32_t const r = i - t * HD;
-                TokEntry const e = tab[t];
-                if (e.page == nullptr) continue;
-                uint32_t const h = r / D;
-                uint32_t const d = r - h * D;
-                out_base[i] = e.page[head_block(P, e.cap, layer, h) + k_offset(e.cap, D, e.pt, d)];
-            }
-        }
-        return;
+    int group_ok = 1;
+    if (tid < kTile / 8) {
+        TokEntry const a = tab[8 * tid];
+        TokEntry const b = tab[8 * tid + 7];
+        group_ok = a.page != nullptr && b.page == a.page && (a.pt & 7u) == 0 && b.pt == a.pt + 7
+            && (a.cap & 7u) == 0;
     }
+    bool const fast = __syncthreads_and(group_ok) && n == kTile && (D & 7u) == 0;
 
-    for (uint32_t r0 = 0; r0 < HD; r0 += kRowChunk) {
-        uint32_t const rows = min(kRowChunk, HD - r0);
-        if (tid < rows) {
-            uint32_t const r = r0 + tid;
+    for (uint32_t layer = l0; layer < l1; ++layer) {
+        uint16_t* k_base = out + (static_cast<uint64_t>(layer * 2) * T + t0) * HD;
+        uint16_t* v_base = out + (static_cast<uint64_t>(layer * 2 + 1) * T + t0) * HD;
+        if (fast && HD == kRowChunk) {
+            gather_kv_fast(P, tab, layer, k_base, v_base, stage);
+            continue;
+        }
+        if (fast) {
+            gather_k_fast(P, tab, layer, k_base);
+            gather_v_fast(P, tab, layer, v_base, stage);
+            continue;
+        }
+        // Element-wise path: partial tiles, unaligned groups, D % 8 != 0.
+        for (uint32_t i = tid; i < n * HD; i += kBlock) {
+            uint32_t const t = i / HD;
+            uint32_t const r = i - t * HD;
+            TokEntry const e = tab[t];
+            if (e.page == nullptr) continue;
             uint32_t const h = r / D;
             uint32_t const d = r - h * D;
-            uint32_t t = 0;
-            while (t < n) {
-                TokEntry const e = tab[t];
-                if (e.page == nullptr) {
-                    stage[t * kRowChunk + tid] = 0;
-                    ++t;
-                    continue;
-                }
-                uint16_t const* hb = e.page + head_block(P, e.cap, layer, h);
-                bool const vec = (t & 7u) == 0 && t + 8 <= n && (e.pt & 7u) == 0 && (e.cap & 7u) == 0
-                    && e.pt + 8 <= e.cap && tab[t + 7].page == e.page && tab[t + 7].pt == e.pt + 7;
-                if (vec) {
-                    uint4 const v = *reinterpret_cast<uint4 const*>(hb + v_offset(e.cap, D, e.pt, d));
-                    uint32_t const w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (uint32_t j = 0; j < 4; ++j) {
-                        stage[(t + 2 * j) * kRowChunk + tid] = static_cast<uint16_t>(w[j] & 0xFFFFu);
-                        stage[(t + 2 * j + 1) * kRowChunk + tid] = static_cast<uint16_t>(w[j] >> 16);
-                    }
-                    t += 8;
-                } else {
-                    stage[t * kRowChunk + tid] = hb[v_offset(e.cap, D, e.pt, d)];
-                    ++t;
-                }
-            }
+            uint16_t const* hb = e.page + head_block(P, e.cap, layer, h);
+            k_base[i] = hb[k_offset(e.cap, D, e.pt, d)];
+            v_base[i] = hb[v_offset(e.cap, D, e.pt, d)];
         }
-        __syncthreads();
-        if ((rows & 7u) == 0) {
-            uint32_t const per_token = rows / 8;
-            for (uint32_t i = tid; i < n * per_token; i += kBlock) {
-                uint32_t const t = i / per_token;
-                uint32_t const c = (i - t * per_token) * 8;
-                if (tab[t].page == nullptr) continue;
-                *reinterpret_cast<uint4*>(out_base + static_cast<uint64_t>(t) * HD + r0 + c) =
-                    *reinterpret_cast<uint4 const*>(&stage[t * kRowChunk + c]);
-            }
-        } else {
-            for (uint32_t i = tid; i < n * rows; i += kBlock) {
-                uint32_t const t = i / rows;
-                uint32_t const c = i - t * rows;
-                if (tab[t].page == nullptr) continue;
-                out_base[static_cast<uint64_t>(t) * HD + r0 + c] = stage[t * kRowChunk + c];
-            }
-        }
-        __syncthreads();
     }
 }
 
@@ -405,9 +526,15 @@ kimkv_status kimkv_gather(const kimkv_storage* storage, const kimkv_block_desc* 
         || descriptor_count == 0 || total_tokens == 0) {
         return KIMKV_INVALID_ARGUMENT;
     }
-    dim3 const grid(ceil_div(total_tokens, kTile), storage->layout.layers, 2);
+    // Enough workgroups to fill the chip (~8 per CU) with as few table
+    // resolutions as possible: layers are grouped per workgroup.
+    uint32_t const tiles = ceil_div(total_tokens, kTile);
+    uint32_t const L = storage->layout.layers;
+    uint32_t per = 1;
+    while (per < L && static_cast<uint64_t>(tiles) * ceil_div(L, per * 2) >= 2048) per *= 2;
+    dim3 const grid(tiles, ceil_div(L, per));
     gather_kernel<<<grid, kBlock, 0, native(stream)>>>(pool_view(*storage), device_descriptors,
-                                                       descriptor_count, total_tokens, device_output);
+                                                       descriptor_count, total_tokens, per, device_output);
     return launch_status();
 }
 

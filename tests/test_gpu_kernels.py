@@ -50,7 +50,8 @@ def _populate(dev, storage, pools, table, inp):
     return buf
 
 
-@pytest.mark.parametrize("shape,T", [((2, 2, 8), 70), ((22, 4, 64), 300), ((3, 1, 12), 9)])
+@pytest.mark.parametrize("shape,T", [((2, 2, 8), 70), ((22, 4, 64), 300), ((3, 1, 12), 9), ((2, 8, 64), 130),
+                                     ((2, 2, 64), 200)])
 def test_append_gather_bit_exact(dev, shape, T):
     L, H, D = shape
     print(f"append/gather L={L} H={H} D={D} T={T}", flush=True)
