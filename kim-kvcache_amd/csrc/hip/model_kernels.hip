@@ -68,7 +68,17 @@ __device__ inline float block_sum(float v, float* scratch)
     return total;
 }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ inline float lo_f(uint32_t w) { return h2f(static_cast<uint16_t>(w & 0xFFFFu)); }
+__device__ inline float hi_f(uint32_t w) { return h2f(static_cast<uint16_t>(w >> 16)); }
+__device__ inline uint32_t pack2(float a, float b)
+{
+    return static_cast<uint32_t>(f2h(a)) | (static_cast<uint32_t>(f2h(b)) << 16);
+}
+
 // out[r] = fp16(x[src_r] * rsqrt(mean(x[src_r]^2) + eps) * w), src_r = rows ? rows[r] : r.
+// 16-byte vectors when hidden % 8 == 0 (every TinyLlama shape), else scalar.
 __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const uint16_t* x, const uint32_t* rows, const uint16_t* w,
                                                          uint32_t hidden, float eps, uint16_t* out)
 {
@@ -76,35 +86,64 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const uint16_t* x, cons
     uint32_t const r = blockIdx.x;
     uint32_t const src = rows != nullptr ? rows[r] : r;
     const uint16_t* in = x + static_cast<uint64_t>(src) * hidden;
+    uint16_t* o = out + static_cast<uint64_t>(r) * hidden;
+    if ((hidden & 7u) == 0) {
+        uint32_t const nv = hidden / 8;
+        float sq = 0.0f;
+        for (uint32_t i = threadIdx.x; i < nv; i += kBlock) {
+            u32x4_t const v = reinterpret_cast<const u32x4_t*>(in)[i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sq += lo_f(v[j]) * lo_f(v[j]) + hi_f(v[j]) * hi_f(v[j]);
+        }
+        float const scale = 1.0f / sqrtf(block_sum(sq, scratch) / static_cast<float>(hidden) + eps);
+        for (uint32_t i = threadIdx.x; i < nv; i += kBlock) {
+            u32x4_t const v = reinterpret_cast<const u32x4_t*>(in)[i];
+            u32x4_t const g = reinterpret_cast<const u32x4_t*>(w)[i];
+            u32x4_t y;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y[j] = pack2(lo_f(v[j]) * scale * lo_f(g[j]), hi_f(v[j]) * scale * hi_f(g[j]));
+            reinterpret_cast<u32x4_t*>(o)[i] = y;
+        }
+        return;
+    }
     float sq = 0.0f;
     for (uint32_t i = threadIdx.x; i < hidden; i += kBlock) {
         float const v = h2f(in[i]);
         sq += v * v;
     }
     float const scale = 1.0f / sqrtf(block_sum(sq, scratch) / static_cast<float>(hidden) + eps);
-    uint16_t* o = out + static_cast<uint64_t>(r) * hidden;
     for (uint32_t i = threadIdx.x; i < hidden; i += kBlock) o[i] = f2h(h2f(in[i]) * scale * h2f(w[i]));
 }
 
 // qkv row = [q: QH*D | k: KVH*D | v: KVH*D].  Rotates q and k by the row's
 // position (pairs (d, d + D/2), angle = pos * theta^(-2d/D)) into q_out / k_out
-// and copies v to v_out; each output is [rows][heads * D].
+// and copies v to v_out; each output is [rows][heads * D].  The D/2 angles
+// of a row are computed once (LDS) and shared by its QH + KVH heads.
+constexpr uint32_t kMaxRopeHalf = 256;
+
 __global__ __launch_bounds__(kBlock) void rope_split_kernel(const uint16_t* qkv, const uint32_t* positions,
                                                             uint32_t QH, uint32_t KVH, uint32_t D, float theta,
                                                             uint16_t* q_out, uint16_t* k_out, uint16_t* v_out)
 {
+    __shared__ float s_cos[kMaxRopeHalf];
+    __shared__ float s_sin[kMaxRopeHalf];
     uint32_t const r = blockIdx.x;
     uint32_t const half = D / 2;
     uint64_t const width = static_cast<uint64_t>(QH + 2 * KVH) * D;
     const uint16_t* row = qkv + r * width;
     float const pos = static_cast<float>(positions[r]);
+    for (uint32_t d = threadIdx.x; d < half; d += kBlock) {
+        float const angle = pos * powf(theta, -2.0f * static_cast<float>(d) / static_cast<float>(D));
+        s_cos[d] = cosf(angle);
+        s_sin[d] = sinf(angle);
+    }
+    __syncthreads();
     uint32_t const pairs = (QH + KVH) * half;
     for (uint32_t p = threadIdx.x; p < pairs; p += kBlock) {
         uint32_t const head = p / half;
         uint32_t const d = p - head * half;
-        float const angle = pos * powf(theta, -2.0f * static_cast<float>(d) / static_cast<float>(D));
-        float const c = cosf(angle);
-        float const s = sinf(angle);
+        float const c = s_cos[d];
+        float const s = s_sin[d];
         bool const is_q = head < QH;
         uint32_t const h = is_q ? head : head - QH;
         const uint16_t* src = row + (is_q ? 0 : static_cast<uint64_t>(QH) * D) + static_cast<uint64_t>(h) * D;
@@ -117,18 +156,39 @@ __global__ __launch_bounds__(kBlock) void rope_split_kernel(const uint16_t* qkv,
     }
     const uint16_t* v = row + static_cast<uint64_t>(QH + KVH) * D;
     uint16_t* vo = v_out + static_cast<uint64_t>(r) * KVH * D;
-    for (uint32_t i = threadIdx.x; i < KVH * D; i += kBlock) vo[i] = v[i];
+    if (((KVH * D) & 7u) == 0 && ((QH + KVH) * D & 7u) == 0 && (width & 7u) == 0) {
+        for (uint32_t i = threadIdx.x; i < KVH * D / 8; i += kBlock) {
+            reinterpret_cast<u32x4_t*>(vo)[i] = reinterpret_cast<const u32x4_t*>(v)[i];
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < KVH * D; i += kBlock) vo[i] = v[i];
+    }
 }
 
-// gu row = [gate: inter | up: inter]; out = fp16(silu(gate) * up).
+// gu row = [gate: inter | up: inter]; out = fp16(silu(gate) * up); 8 elements per thread.
 __global__ __launch_bounds__(kBlock) void swiglu_kernel(const uint16_t* gu, uint32_t inter, uint16_t* out)
 {
     uint32_t const r = blockIdx.y;
+    const uint16_t* row = gu + static_cast<uint64_t>(r) * 2u * inter;
+    uint16_t* o = out + static_cast<uint64_t>(r) * inter;
+    if ((inter & 7u) == 0) {
+        uint32_t const i = blockIdx.x * kBlock + threadIdx.x;
+        if (i >= inter / 8) return;
+        u32x4_t const g = reinterpret_cast<const u32x4_t*>(row)[i];
+        u32x4_t const u = reinterpret_cast<const u32x4_t*>(row + inter)[i];
+        u32x4_t y;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float const g0 = lo_f(g[j]), g1 = hi_f(g[j]);
+            y[j] = pack2(g0 / (1.0f + expf(-g0)) * lo_f(u[j]), g1 / (1.0f + expf(-g1)) * hi_f(u[j]));
+        }
+        reinterpret_cast<u32x4_t*>(o)[i] = y;
+        return;
+    }
     uint32_t const i = blockIdx.x * kBlock + threadIdx.x;
     if (i >= inter) return;
-    const uint16_t* row = gu + static_cast<uint64_t>(r) * 2u * inter;
     float const g = h2f(row[i]);
-    out[static_cast<uint64_t>(r) * inter + i] = f2h(g / (1.0f + expf(-g)) * h2f(row[inter + i]));
+    o[i] = f2h(g / (1.0f + expf(-g)) * h2f(row[inter + i]));
 }
 
 // First index of the row maximum (std::max_element order; NaN never wins).
@@ -256,7 +316,8 @@ kimkv_status kimkv_model_rope_split(const uint16_t* qkv, const uint32_t* device_
                                     uint16_t* q_out, uint16_t* k_out, uint16_t* v_out, kimkv_stream_t stream)
 {
     if (qkv == nullptr || device_positions == nullptr || q_out == nullptr || k_out == nullptr || v_out == nullptr
-        || query_heads == 0 || kv_heads == 0 || head_dim == 0 || head_dim % 2 != 0 || !(theta > 0.0f)) {
+        || query_heads == 0 || kv_heads == 0 || head_dim == 0 || head_dim % 2 != 0 || head_dim / 2 > kMaxRopeHalf
+        || !(theta > 0.0f)) {
         return KIMKV_INVALID_ARGUMENT;
     }
     if (rows == 0) return KIMKV_OK;
@@ -270,7 +331,8 @@ kimkv_status kimkv_model_swiglu(const uint16_t* gate_up, uint32_t rows, uint32_t
 {
     if (gate_up == nullptr || out == nullptr || intermediate == 0 || rows > 65535) return KIMKV_INVALID_ARGUMENT;
     if (rows == 0) return KIMKV_OK;
-    dim3 const grid((intermediate + kBlock - 1) / kBlock, rows);
+    uint32_t const lanes = (intermediate & 7u) == 0 ? intermediate / 8 : intermediate;
+    dim3 const grid((lanes + kBlock - 1) / kBlock, rows);
     swiglu_kernel<<<grid, kBlock, 0, native(stream)>>>(gate_up, intermediate, out);
     return launch_status();
 }
