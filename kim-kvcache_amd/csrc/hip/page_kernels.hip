@@ -18,6 +18,8 @@ namespace {
 constexpr unsigned kBlock = 256;
 constexpr unsigned kTile = 64;   // tokens per gather/fill tile
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 struct TokEntry {
     uint16_t* page;
     uint32_t cap;
@@ -101,6 +103,56 @@ __global__ __launch_bounds__(kBlock) void append_kernel(PoolView P, const kimkv_
     uint32_t const HD = H * D;
     uint32_t const total = job.token_count * HD;
     uint64_t const layer_off = static_cast<uint64_t>(li) * job.src_layer_stride;
+    const uint16_t* sk = job.src_key + layer_off;
+    const uint16_t* sv = job.src_value + layer_off;
+    uint32_t const stride = job.src_token_stride;
+    bool const src_aligned = (D & 7u) == 0 && (stride & 7u) == 0
+        && ((reinterpret_cast<uintptr_t>(sk) | reinterpret_cast<uintptr_t>(sv)) & 15u) == 0;
+    if (src_aligned) {
+        // K: 16-byte pieces of 8 dims of one token (contiguous in source and page).
+        uint32_t const dchunks = D / 8;
+        uint32_t const kchunks = job.token_count * H * dchunks;
+        for (uint32_t i = tid; i < kchunks; i += kBlock) {
+            uint32_t const t = i / (H * dchunks);
+            uint32_t const rem = i - t * (H * dchunks);
+            uint32_t const h = rem / dchunks;
+            uint32_t const dc = rem - h * dchunks;
+            u32x4_t const v = *reinterpret_cast<const u32x4_t*>(sk + static_cast<uint64_t>(t) * stride + h * D + dc * 8);
+            *reinterpret_cast<u32x4_t*>(dst + head_block(P, dcap, layer, h)
+                                        + k_offset(dcap, D, job.dst_token + t, dc * 8)) = v;
+        }
+        // V^T: 16-byte pieces of 8 tokens of one dim when the tokens sit in
+        // 8-aligned groups of the page, else one element at a time.
+        bool const v_groups = (job.token_count & 7u) == 0 && (job.dst_token & 7u) == 0 && (dcap & 7u) == 0;
+        if (v_groups) {
+            uint32_t const vchunks = (job.token_count / 8) * HD;
+            for (uint32_t i = tid; i < vchunks; i += kBlock) {
+                uint32_t const g = i / HD;
+                uint32_t const r = i - g * HD;
+                uint32_t const h = r / D;
+                uint32_t const d = r - h * D;
+                const uint16_t* src = sv + static_cast<uint64_t>(8 * g) * stride + r;
+                u32x4_t w;
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j) {
+                    w[j] = static_cast<uint32_t>(src[static_cast<uint64_t>(2 * j) * stride])
+                        | (static_cast<uint32_t>(src[static_cast<uint64_t>(2 * j + 1) * stride]) << 16);
+                }
+                *reinterpret_cast<u32x4_t*>(dst + head_block(P, dcap, layer, h)
+                                            + v_offset(dcap, D, job.dst_token + 8 * g, d)) = w;
+            }
+            return;
+        }
+        for (uint32_t i = tid; i < total; i += kBlock) {
+            uint32_t const t = i / HD;
+            uint32_t const rem = i - t * HD;
+            uint32_t const h = rem / D;
+            uint32_t const d = rem - h * D;
+            dst[head_block(P, dcap, layer, h) + v_offset(dcap, D, job.dst_token + t, d)] =
+                sv[static_cast<uint64_t>(t) * stride + rem];
+        }
+        return;
+    }
     for (uint32_t i = tid; i < total; i += kBlock) {
         uint32_t const t = i / HD;
         uint32_t const rem = i - t * HD;
@@ -128,7 +180,6 @@ constexpr unsigned kRowChunk = 256;            // V rows (head x dim) per pass
 constexpr unsigned kStageRow = kRowChunk + 8;  // u16 per staged token row (16-byte multiple)
 constexpr unsigned kGatherLoads = 8;           // 16-byte loads in flight per thread
 
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(1))) u32x4_t global_u32x4_t;
 typedef __attribute__((address_space(1))) u32x4_t global_u32x4_out_t;
 
