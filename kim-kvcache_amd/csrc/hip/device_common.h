@@ -108,6 +108,22 @@ __host__ __device__ inline uint64_t v_offset(uint32_t cap, uint32_t D, uint32_t 
         + t % vw;
 }
 
+// ---- XCD-aware workgroup order ----------------------------------------------
+// MI355X dispatches the workgroups of a launch round-robin over its 8 XCDs
+// (workgroup w runs on XCD w % 8), each with its own L2.  This maps dispatch
+// index w of an n-workgroup grid to a logical index such that XCD x receives
+// one contiguous logical range (the first n % 8 XCDs one element longer), so
+// workgroups that read the same data share an L2.  A bijection on [0, n).
+constexpr unsigned kXcds = 8;
+__host__ __device__ inline uint32_t xcd_logical_index(uint32_t w, uint32_t n)
+{
+    uint32_t const per = (n + kXcds - 1) / kXcds;
+    uint32_t const tall = n % kXcds == 0 ? kXcds : n % kXcds;
+    uint32_t const x = w % kXcds;
+    uint32_t const local = w / kXcds;
+    return x < tall ? x * per + local : tall * per + (x - tall) * (per - 1) + local;
+}
+
 // ---- synthetic generator (bit-identical to kimkv_synth_value) -------------
 __host__ __device__ inline uint64_t mix64(uint64_t z)
 {

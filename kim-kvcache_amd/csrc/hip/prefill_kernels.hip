@@ -456,7 +456,7 @@ __device__ void prefill_row_generic(const PoolView& P, const kimkv_prefill_item&
 
 __global__ __launch_bounds__(kBlock, 2) void prefill_kernel(PoolView P, const kimkv_prefill_item* items,
                                                             const uint32_t* block_prefix, uint32_t item_count,
-                                                            uint32_t QH)
+                                                            uint32_t total_blocks, uint32_t QH)
 {
     __shared__ HeadGroup groups[kSegmentGroups];
     __shared__ KvTile tiles[2];
@@ -466,8 +466,11 @@ __global__ __launch_bounds__(kBlock, 2) void prefill_kernel(PoolView P, const ki
     __shared__ uint32_t s_holes;
 
     uint32_t const tid = threadIdx.x;
-    uint32_t const block = blockIdx.x;
-    uint32_t const h = blockIdx.y;
+    // Head-major logical order, XCD-contiguous: the blocks of one (item, KV
+    // head) run on one XCD and read that head's pages through one L2.
+    uint32_t const logical = xcd_logical_index(blockIdx.x, gridDim.x);
+    uint32_t const block = logical % total_blocks;
+    uint32_t const h = logical / total_blocks;
     if (tid == 0) {
         s_item = 0xFFFFFFFFu;
         s_generic = 0;
@@ -606,11 +609,12 @@ kimkv_status kimkv_paged_prefill_batch(const kimkv_storage* storage, const kimkv
         return KIMKV_INVALID_ARGUMENT;
     }
     if (total_blocks == 0 || item_count == 0) return KIMKV_OK;
-    dim3 const grid(total_blocks, storage->layout.kv_heads);
+    if (static_cast<uint64_t>(total_blocks) * storage->layout.kv_heads > 0x7FFFFFFFull) return KIMKV_INVALID_ARGUMENT;
+    dim3 const grid(total_blocks * storage->layout.kv_heads);
     void* start = nullptr;
     kernel_timing_begin(TimedKernel::Prefill, native(stream), &start);
     prefill_kernel<<<grid, kBlock, 0, native(stream)>>>(pool_view(*storage), device_items, device_block_prefix,
-                                                        item_count, query_heads);
+                                                        item_count, total_blocks, query_heads);
     kimkv_status const st = launch_status();
     kernel_timing_end(TimedKernel::Prefill, native(stream), start);
     return st;
