@@ -459,15 +459,18 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 }
 
 // Merges the per-chunk partials of every multi-chunk lane.  Block = (lane,
-// 4 query heads), one wave per head: the max and denominator are wave
-// reductions over the chunks (lane k takes chunks k, k+64, ...); the output
-// pass streams one 64-float partial row per chunk with all lanes loading
-// consecutive floats, unrolled so several rows are in flight.
+// 4 query heads), one wave per head.  Chunks are taken 64 at a time: lane k
+// reads chunk k's (m, l) and every lane reads its kDims dims of the chunks'
+// partial rows in the same round of loads, so a lane with up to 64 chunks
+// (and D <= 64) is merged after a single memory round trip; rounds of 64
+// chunks fold into the running (M, den, acc) like an online softmax.
 constexpr unsigned kCombineHeads = 4;
 
+template <uint32_t kDims>
 __global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(const kimkv_decode_item* items,
                                                                     const uint32_t* prefix, uint32_t QH, uint32_t D)
 {
+    constexpr uint32_t kBatch = 64 / kDims;   // partial rows held in registers at once
     uint32_t const lane = blockIdx.x;
     uint32_t const q = blockIdx.y * kCombineHeads + (threadIdx.x >> 6);
     uint32_t const l = threadIdx.x & 63u;
@@ -478,26 +481,52 @@ __global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(const kimkv
     if (item.workspace == nullptr || item.output == nullptr) return;
     uint64_t const stride = static_cast<uint64_t>(QH) * (D + 2);
     const float* ws = item.workspace + static_cast<uint64_t>(q) * (D + 2);
-    float m = -INFINITY;
-    for (uint32_t k = l; k < n; k += 64) m = fmaxf(m, ws[k * stride + D]);
-    float const M = wave_max(m);
+    float M = -INFINITY;
     float den = 0.0f;
-    for (uint32_t k = l; k < n; k += 64) den += exp2f(ws[k * stride + D] - M) * ws[k * stride + D + 1];
-    den = wave_sum(den);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-    for (uint32_t k = 0; k < n; ++k) {
-        const float* part = ws + k * stride;
-        float const w = exp2f(part[D] - M);
+    float acc[kDims];
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            uint32_t const d = l + 64u * j;
-            if (d < D) acc[j] += w * part[d];
+    for (uint32_t j = 0; j < kDims; ++j) acc[j] = 0.0f;
+    float row[kBatch][kDims];
+    auto load_rows = [&](const float* blk, uint32_t b, uint32_t kn) {
+#pragma unroll
+        for (uint32_t i = 0; i < kBatch; ++i) {
+#pragma unroll
+            for (uint32_t j = 0; j < kDims; ++j) {
+                uint32_t const d = l + 64u * j;
+                row[i][j] = b + i < kn && d < D ? blk[static_cast<uint64_t>(b + i) * stride + d] : 0.0f;
+            }
+        }
+    };
+    for (uint32_t k0 = 0; k0 < n; k0 += 64) {
+        uint32_t const kn = min(64u, n - k0);
+        const float* blk = ws + static_cast<uint64_t>(k0) * stride;
+        float mk = -INFINITY;
+        float lk = 0.0f;
+        if (l < kn) {
+            mk = blk[static_cast<uint64_t>(l) * stride + D];
+            lk = blk[static_cast<uint64_t>(l) * stride + D + 1];
+        }
+        load_rows(blk, 0, kn);
+        float const m_new = fmaxf(M, wave_max(mk));
+        float const c = M == -INFINITY ? 0.0f : exp2f(M - m_new);
+        M = m_new;
+        float const w = l < kn ? exp2f(mk - M) : 0.0f;
+        den = den * c + wave_sum(w * lk);
+#pragma unroll
+        for (uint32_t j = 0; j < kDims; ++j) acc[j] *= c;
+        for (uint32_t b = 0; b < kn; b += kBatch) {
+            if (b != 0) load_rows(blk, b, kn);
+#pragma unroll
+            for (uint32_t i = 0; i < kBatch; ++i) {
+                float const wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), static_cast<int>(b + i)));
+#pragma unroll
+                for (uint32_t j = 0; j < kDims; ++j) acc[j] += wk * row[i][j];
+            }
         }
     }
     float const inv = 1.0f / den;
 #pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
+    for (uint32_t j = 0; j < kDims; ++j) {
         uint32_t const d = l + 64u * j;
         if (d < D) item.output[static_cast<uint64_t>(q) * D + d] = __half_as_ushort(__float2half_rn(acc[j] * inv));
     }
@@ -647,8 +676,14 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage, const kimkv_
     if (status != KIMKV_OK) return status;
     if (total_chunks > lane_count) {
         dim3 const cgrid(lane_count, (query_heads + kCombineHeads - 1) / kCombineHeads);
-        combine_kernel<<<cgrid, 64 * kCombineHeads, 0, s>>>(device_items, device_chunk_prefix, query_heads,
-                                                            storage->layout.head_dim);
+        uint32_t const D = storage->layout.head_dim;
+        if (D <= 64) {
+            combine_kernel<1><<<cgrid, 64 * kCombineHeads, 0, s>>>(device_items, device_chunk_prefix, query_heads, D);
+        } else if (D <= 128) {
+            combine_kernel<2><<<cgrid, 64 * kCombineHeads, 0, s>>>(device_items, device_chunk_prefix, query_heads, D);
+        } else {
+            combine_kernel<4><<<cgrid, 64 * kCombineHeads, 0, s>>>(device_items, device_chunk_prefix, query_heads, D);
+        }
         return launch_status();
     }
     return KIMKV_OK;

@@ -208,6 +208,17 @@ def test_decode_split_k_long_lanes(dev):
     assert total > 4          # several lanes split across chunks -> combine path
 
 
+def test_decode_combine_wide_heads_and_many_chunks(dev):
+    # Split-K merges with 2 and 4 dims per lane (D = 128, 256; generic path)
+    # and a lane of more than 64 chunks (the merge folds rounds of 64).
+    chunk, total = _decode_case(dev, (1, 2, 128), [300, 2600], G=4, seed=13)
+    assert total > 2
+    chunk, total = _decode_case(dev, (1, 1, 256), [700, 2000], G=2, seed=14)
+    assert total > 2
+    chunk, total = _decode_case(dev, (1, 4, 64), [20000, 33], G=8, seed=15)
+    assert (20000 + chunk - 1) // chunk > 64
+
+
 def test_decode_group_sizes_fast_path(dev):
     _decode_case(dev, (2, 2, 64), [130, 700], G=16, seed=6)
     _decode_case(dev, (2, 8, 64), [70, 333], G=1, seed=7)
