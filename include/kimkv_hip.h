@@ -281,11 +281,20 @@ kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launch
  * src/cuda/model/runner_support.cpp:207-250.  Activations are fp16 rows,
  * stored with round-to-nearest-even; all accumulation is fp32. */
 
-/* y[rows][out] = x[rows][in] . weight[out][in]^T + beta * y (rocBLAS, fp32
+/* y[rows][out] = x[rows][in] . weight[out][in]^T + beta * y (hipBLASLt, fp32
  * accumulate).  y is fp16 (y_f32 = 0) or fp32 (y_f32 != 0); beta = 1 with
- * y = the residual stream fuses the residual add. */
+ * y = the residual stream fuses the residual add.  Each exact problem (rows,
+ * in, out, output type, beta != 0) keeps one algorithm per stream: the
+ * library's first heuristic choice unless kimkv_linear_tune chose one. */
 kimkv_status kimkv_linear(const uint16_t* x, uint32_t rows, uint32_t in_features, const uint16_t* weight,
                           uint32_t out_features, void* y, int y_f32, float beta, kimkv_stream_t stream);
+/* Times the library's leading candidates for this exact problem on these
+ * buffers (the stream is synchronized; y is overwritten or accumulated into
+ * several times, so pass scratch contents) and makes the fastest the one
+ * kimkv_linear uses for the problem on this stream.  No counterpart in the
+ * reference (cuBLAS picks its own algorithm). */
+kimkv_status kimkv_linear_tune(const uint16_t* x, uint32_t rows, uint32_t in_features, const uint16_t* weight,
+                               uint32_t out_features, void* y, int y_f32, float beta, kimkv_stream_t stream);
 /* out[r] = table[ids[r]] (launchEmbeddingBatch, kernels.cuh:19-26). */
 kimkv_status kimkv_model_embed(const uint16_t* table, const uint32_t* device_ids, uint32_t rows, uint32_t hidden,
                                uint16_t* out, kimkv_stream_t stream);

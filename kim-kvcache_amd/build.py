@@ -76,7 +76,7 @@ def build_device() -> str:
                for s, o in zip(srcs, objs)])
     out = os.path.join(LIB_DIR, "libkimkv_hip.so")
     tmp = out + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-lrocblas", "-o", tmp])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-lhipblaslt", "-o", tmp])
     os.replace(tmp, out)
     return out
 

@@ -12,10 +12,11 @@
 // which rounds x + W.a once instead of twice.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
-#include <rocblas/rocblas.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <cmath>
 #include <mutex>
+#include <tuple>
 #include <unordered_map>
 
 #include "device_common.h"
@@ -239,32 +240,126 @@ unsigned grid_for(uint64_t count)
     return static_cast<unsigned>(b < 65536 ? (b == 0 ? 1 : b) : 65536);
 }
 
-// One rocBLAS handle per stream (created on first use, kept for the process).
-struct BlasHandles {
-    std::mutex mutex;
-    std::unordered_map<hipStream_t, rocblas_handle> by_stream;
+// hipBLASLt plans.  y^T (out x rows) = W_cm^T . x_cm in column-major terms,
+// W_cm = W^T (in x out, ld = in), x_cm = x^T (in x rows, ld = in).  One
+// context per stream (a workspace is only safe for one stream's GEMMs at a
+// time); every exact problem (rows, in, out, output type, accumulate) keeps
+// one plan: the library's first heuristic choice, or the fastest candidate
+// measured by kimkv_linear_tune.
+constexpr size_t kLtWorkspace = size_t{64} << 20;
+
+struct LtKey {
+    uint32_t rows, in, out;
+    uint8_t f32, accumulate;
+    bool operator==(LtKey const& o) const
+    {
+        return std::tie(rows, in, out, f32, accumulate) == std::tie(o.rows, o.in, o.out, o.f32, o.accumulate);
+    }
 };
 
-BlasHandles& blas()
+struct LtKeyHash {
+    size_t operator()(LtKey const& k) const noexcept
+    {
+        uint64_t h = (uint64_t{k.rows} << 32) ^ (uint64_t{k.in} << 16) ^ k.out ^ (uint64_t{k.f32} << 62)
+            ^ (uint64_t{k.accumulate} << 63);
+        return static_cast<size_t>(mix64(h));
+    }
+};
+
+struct LtPlan {
+    hipblasLtMatmulDesc_t desc{nullptr};
+    hipblasLtMatrixLayout_t a{nullptr}, b{nullptr}, c{nullptr};
+    hipblasLtMatmulAlgo_t algo{};
+};
+
+struct LtContext {
+    void* workspace{nullptr};
+    std::unordered_map<LtKey, LtPlan, LtKeyHash> plans;
+};
+
+struct LtState {
+    std::mutex mutex;
+    hipblasLtHandle_t handle{nullptr};
+    bool failed{false};
+    std::unordered_map<hipStream_t, LtContext> by_stream;
+};
+
+LtState& lt_state()
 {
-    static BlasHandles instance;
+    static LtState instance;
     return instance;
 }
 
-rocblas_handle handle_for(hipStream_t stream)
+// Caller holds the state mutex.
+LtContext* lt_context(LtState& st, hipStream_t stream)
 {
-    BlasHandles& b = blas();
-    std::lock_guard<std::mutex> lock(b.mutex);
-    auto it = b.by_stream.find(stream);
-    if (it != b.by_stream.end()) return it->second;
-    rocblas_handle h = nullptr;
-    if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
-    if (rocblas_set_stream(h, stream) != rocblas_status_success) {
-        rocblas_destroy_handle(h);
-        return nullptr;
+    if (st.handle == nullptr) {
+        if (st.failed || hipblasLtCreate(&st.handle) != HIPBLAS_STATUS_SUCCESS) {
+            st.failed = true;
+            st.handle = nullptr;
+            return nullptr;
+        }
     }
-    b.by_stream.emplace(stream, h);
-    return h;
+    auto it = st.by_stream.find(stream);
+    if (it != st.by_stream.end()) return &it->second;
+    LtContext ctx;
+    if (hipMalloc(&ctx.workspace, kLtWorkspace) != hipSuccess) return nullptr;
+    return &st.by_stream.emplace(stream, std::move(ctx)).first->second;
+}
+
+void lt_destroy(LtPlan& p)
+{
+    if (p.a != nullptr) hipblasLtMatrixLayoutDestroy(p.a);
+    if (p.b != nullptr) hipblasLtMatrixLayoutDestroy(p.b);
+    if (p.c != nullptr) hipblasLtMatrixLayoutDestroy(p.c);
+    if (p.desc != nullptr) hipblasLtMatmulDescDestroy(p.desc);
+    p = LtPlan{};
+}
+
+bool lt_describe(LtKey const& k, LtPlan& p)
+{
+    hipblasOperation_t const ta = HIPBLAS_OP_T;
+    hipblasOperation_t const tb = HIPBLAS_OP_N;
+    bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS
+        && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) == HIPBLAS_STATUS_SUCCESS
+        && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) == HIPBLAS_STATUS_SUCCESS
+        && hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16F, k.in, k.out, k.in) == HIPBLAS_STATUS_SUCCESS
+        && hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16F, k.in, k.rows, k.in) == HIPBLAS_STATUS_SUCCESS
+        && hipblasLtMatrixLayoutCreate(&p.c, k.f32 ? HIP_R_32F : HIP_R_16F, k.out, k.rows, k.out)
+            == HIPBLAS_STATUS_SUCCESS;
+    if (!ok) lt_destroy(p);
+    return ok;
+}
+
+// Up to `want` candidate algorithms for the plan's problem, best first.
+int lt_candidates(LtState& st, LtPlan const& p, hipblasLtMatmulHeuristicResult_t* out, int want)
+{
+    hipblasLtMatmulPreference_t pref = nullptr;
+    if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return 0;
+    size_t ws = kLtWorkspace;
+    int got = 0;
+    if (hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws))
+            != HIPBLAS_STATUS_SUCCESS
+        || hipblasLtMatmulAlgoGetHeuristic(st.handle, p.desc, p.a, p.b, p.c, p.c, pref, want, out, &got)
+            != HIPBLAS_STATUS_SUCCESS) {
+        got = 0;
+    }
+    hipblasLtMatmulPreferenceDestroy(pref);
+    return got;
+}
+
+hipblasStatus_t lt_run(LtState& st, LtContext& ctx, LtPlan const& p, hipblasLtMatmulAlgo_t const& algo,
+                       const uint16_t* x, const uint16_t* w, void* y, float beta, hipStream_t stream)
+{
+    float const alpha = 1.0f;
+    return hipblasLtMatmul(st.handle, p.desc, &alpha, w, p.a, x, p.b, &beta, y, p.c, y, p.c, &algo, ctx.workspace,
+                           kLtWorkspace, stream);
+}
+
+bool lt_args_ok(const uint16_t* x, uint32_t in, const uint16_t* w, uint32_t out, void* y, uint32_t rows)
+{
+    return x != nullptr && w != nullptr && y != nullptr && in != 0 && out != 0 && in <= 0x7FFFFFFFu
+        && out <= 0x7FFFFFFFu && rows <= 0x7FFFFFFFu;
 }
 
 }  // namespace
@@ -349,24 +444,81 @@ kimkv_status kimkv_model_argmax(const float* logits, uint32_t rows, uint32_t voc
 kimkv_status kimkv_linear(const uint16_t* x, uint32_t rows, uint32_t in_features, const uint16_t* weight,
                           uint32_t out_features, void* y, int y_f32, float beta, kimkv_stream_t stream)
 {
-    if (x == nullptr || weight == nullptr || y == nullptr || in_features == 0 || out_features == 0
-        || in_features > 0x7FFFFFFFu || out_features > 0x7FFFFFFFu || rows > 0x7FFFFFFFu) {
-        return KIMKV_INVALID_ARGUMENT;
-    }
+    if (!lt_args_ok(x, in_features, weight, out_features, y, rows)) return KIMKV_INVALID_ARGUMENT;
     if (rows == 0) return KIMKV_OK;
-    rocblas_handle h = handle_for(native(stream));
-    if (h == nullptr) return KIMKV_RUNTIME_UNAVAILABLE;
-    // Row-major y[rows][out] = x[rows][in] . W[out][in]^T  ==  column-major
-    // y^T (out x rows) = op(W_cm) . x_cm with W_cm = W^T (in x out, ld = in).
-    float const alpha = 1.0f;
-    rocblas_datatype const yt = y_f32 ? rocblas_datatype_f32_r : rocblas_datatype_f16_r;
-    rocblas_status const st = rocblas_gemm_ex(
-        h, rocblas_operation_transpose, rocblas_operation_none, static_cast<rocblas_int>(out_features),
-        static_cast<rocblas_int>(rows), static_cast<rocblas_int>(in_features), &alpha, weight, rocblas_datatype_f16_r,
-        static_cast<rocblas_int>(in_features), x, rocblas_datatype_f16_r, static_cast<rocblas_int>(in_features), &beta,
-        y, yt, static_cast<rocblas_int>(out_features), y, yt, static_cast<rocblas_int>(out_features),
-        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    return st == rocblas_status_success ? KIMKV_OK : KIMKV_SUBMISSION_FAILED;
+    LtState& st = lt_state();
+    std::lock_guard<std::mutex> lock(st.mutex);
+    LtContext* ctx = lt_context(st, native(stream));
+    if (ctx == nullptr) return KIMKV_RUNTIME_UNAVAILABLE;
+    LtKey const key{rows, in_features, out_features, static_cast<uint8_t>(y_f32 != 0), static_cast<uint8_t>(beta != 0.0f)};
+    auto it = ctx->plans.find(key);
+    if (it == ctx->plans.end()) {
+        LtPlan p;
+        hipblasLtMatmulHeuristicResult_t cand[1];
+        if (!lt_describe(key, p)) return KIMKV_RUNTIME_UNAVAILABLE;
+        if (lt_candidates(st, p, cand, 1) < 1) {
+            lt_destroy(p);
+            return KIMKV_SUBMISSION_FAILED;
+        }
+        p.algo = cand[0].algo;
+        it = ctx->plans.emplace(key, p).first;
+    }
+    hipblasStatus_t const r = lt_run(st, *ctx, it->second, it->second.algo, x, weight, y, beta, native(stream));
+    return r == HIPBLAS_STATUS_SUCCESS ? KIMKV_OK : KIMKV_SUBMISSION_FAILED;
+}
+
+kimkv_status kimkv_linear_tune(const uint16_t* x, uint32_t rows, uint32_t in_features, const uint16_t* weight,
+                               uint32_t out_features, void* y, int y_f32, float beta, kimkv_stream_t stream)
+{
+    constexpr int kCandidates = 8;
+    constexpr int kReps = 3;
+    if (!lt_args_ok(x, in_features, weight, out_features, y, rows)) return KIMKV_INVALID_ARGUMENT;
+    if (rows == 0) return KIMKV_OK;
+    LtState& st = lt_state();
+    std::lock_guard<std::mutex> lock(st.mutex);
+    hipStream_t const s = native(stream);
+    LtContext* ctx = lt_context(st, s);
+    if (ctx == nullptr) return KIMKV_RUNTIME_UNAVAILABLE;
+    LtKey const key{rows, in_features, out_features, static_cast<uint8_t>(y_f32 != 0), static_cast<uint8_t>(beta != 0.0f)};
+    LtPlan p;
+    if (!lt_describe(key, p)) return KIMKV_RUNTIME_UNAVAILABLE;
+    hipblasLtMatmulHeuristicResult_t cand[kCandidates];
+    int const n = lt_candidates(st, p, cand, kCandidates);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (n < 1 || hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        if (e0 != nullptr) static_cast<void>(hipEventDestroy(e0));
+        lt_destroy(p);
+        return n < 1 ? KIMKV_SUBMISSION_FAILED : KIMKV_RUNTIME_UNAVAILABLE;
+    }
+    int best = -1;
+    float best_ms = 0.0f;
+    for (int a = 0; a < n; ++a) {
+        if (lt_run(st, *ctx, p, cand[a].algo, x, weight, y, beta, s) != HIPBLAS_STATUS_SUCCESS) continue;
+        bool ok = hipEventRecord(e0, s) == hipSuccess;
+        for (int i = 0; i < kReps && ok; ++i) ok = lt_run(st, *ctx, p, cand[a].algo, x, weight, y, beta, s) == HIPBLAS_STATUS_SUCCESS;
+        float ms = 0.0f;
+        ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess
+            && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+        if (ok && (best < 0 || ms < best_ms)) {
+            best = a;
+            best_ms = ms;
+        }
+    }
+    static_cast<void>(hipEventDestroy(e0));
+    static_cast<void>(hipEventDestroy(e1));
+    if (best < 0) {
+        lt_destroy(p);
+        return KIMKV_SUBMISSION_FAILED;
+    }
+    p.algo = cand[best].algo;
+    auto it = ctx->plans.find(key);
+    if (it != ctx->plans.end()) {
+        lt_destroy(it->second);
+        it->second = p;
+    } else {
+        ctx->plans.emplace(key, p);
+    }
+    return KIMKV_OK;
 }
 
 }  // extern "C"

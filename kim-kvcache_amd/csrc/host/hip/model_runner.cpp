@@ -41,6 +41,10 @@ std::uint64_t weightRow(std::uint32_t layer, std::uint32_t kind)
 
 std::size_t align256(std::size_t n) { return (n + 255) & ~std::size_t{255}; }
 
+// Row counts of the per-layer GEMMs are padded to a multiple of this, so a
+// handful of tuned problem sizes covers every forward.
+constexpr std::uint32_t kGemmRowQuantum = 128;
+
 }  // namespace
 
 struct HipTinyLlamaRunner::Impl {
@@ -49,6 +53,7 @@ struct HipTinyLlamaRunner::Impl {
     HipStream stream{nullptr};
     std::uint32_t QD{0}, KD{0}, W_qkv{0};
     std::size_t ws_lane{0};   // decode split-K workspace per lane
+    std::uint32_t gemm_cap{0};   // activation rows: max_positions rounded up to kGemmRowQuantum
 
     // Device memory: one block for weights, one for activations.
     void* weights{nullptr};
@@ -112,7 +117,8 @@ struct HipTinyLlamaRunner::Impl {
         final_norm = take(H * 2);
         head = take(V * H * 2);
 
-        std::uint64_t const P = cfg.max_positions, S = cfg.max_spans;
+        gemm_cap = (cfg.max_positions + kGemmRowQuantum - 1) / kGemmRowQuantum * kGemmRowQuantum;
+        std::uint64_t const P = gemm_cap, S = cfg.max_spans;
         std::uint64_t sizes[] = {
             P * H * 2, P * H * 2, P * W_qkv * 2, P * QD * 2, P * KD * 2, P * KD * 2, P * QD * 2,
             P * 2 * I * 2, P * I * 2, S * H * 2, S * V * 4, P * 4, P * 4, S * 4, S * 4,
@@ -146,6 +152,23 @@ struct HipTinyLlamaRunner::Impl {
             return false;
         }
         return true;
+    }
+
+    // Picks the GEMM algorithm of every padded row count the forward can use
+    // (multiples of kGemmRowQuantum up to gemm_cap) on the activation buffers.
+    bool tuneGemms()
+    {
+        TinyLlamaConfig const& m = cfg.model;
+        bool ok = true;
+        for (std::uint32_t g = kGemmRowQuantum; g <= gemm_cap && ok; g += kGemmRowQuantum) {
+            ok = kimkv_linear_tune(h, g, m.hidden_size, layers[0].wqkv, W_qkv, qkv, 0, 0.0f, stream) == KIMKV_OK
+                && kimkv_linear_tune(attn, g, m.hidden_size, layers[0].wo, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK
+                && kimkv_linear_tune(h, g, m.hidden_size, layers[0].wgu, 2 * m.intermediate_size, gu, 0, 0.0f, stream)
+                    == KIMKV_OK
+                && kimkv_linear_tune(act, g, m.intermediate_size, layers[0].wdown, m.hidden_size, x, 0, 1.0f, stream)
+                    == KIMKV_OK;
+        }
+        return ok && kimkv_stream_synchronize(stream) == KIMKV_OK;
     }
 
     bool initWeights()
@@ -274,11 +297,16 @@ GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSp
     std::vector<KvScalar*> po;
     std::vector<EngineKvStatus> pst;
 
+    // The four per-layer GEMMs run on G >= P rows (P rounded up to the tuned
+    // quantum); rows P..G-1 of their inputs and outputs are scratch that no
+    // other kernel reads.
+    std::uint32_t const G = std::min<std::uint32_t>((P + kGemmRowQuantum - 1) / kGemmRowQuantum * kGemmRowQuantum,
+                                                    gemm_cap);
     ok = ok && kimkv_model_embed(embed, d_ids, P, m.hidden_size, x, stream) == KIMKV_OK;
     for (std::uint32_t l = 0; l < m.layer_count && ok; ++l) {
         Layer const& L = layers[l];
         ok = kimkv_model_rmsnorm(x, nullptr, P, L.ln1, m.hidden_size, m.rms_norm_epsilon, h, stream) == KIMKV_OK
-            && kimkv_linear(h, P, m.hidden_size, L.wqkv, W_qkv, qkv, 0, 0.0f, stream) == KIMKV_OK
+            && kimkv_linear(h, G, m.hidden_size, L.wqkv, W_qkv, qkv, 0, 0.0f, stream) == KIMKV_OK
             && kimkv_model_rope_split(qkv, d_pos, P, m.attention_head_count, m.kv_head_count, m.head_dimension,
                                       m.rope_theta, q, k, v, stream) == KIMKV_OK;
         if (!ok) break;
@@ -360,11 +388,11 @@ GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSp
             }
         }
         // Output projection + residual, MLP + residual.
-        ok = kimkv_linear(attn, P, m.hidden_size, L.wo, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK
+        ok = kimkv_linear(attn, G, m.hidden_size, L.wo, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK
             && kimkv_model_rmsnorm(x, nullptr, P, L.ln2, m.hidden_size, m.rms_norm_epsilon, h, stream) == KIMKV_OK
-            && kimkv_linear(h, P, m.hidden_size, L.wgu, 2 * m.intermediate_size, gu, 0, 0.0f, stream) == KIMKV_OK
+            && kimkv_linear(h, G, m.hidden_size, L.wgu, 2 * m.intermediate_size, gu, 0, 0.0f, stream) == KIMKV_OK
             && kimkv_model_swiglu(gu, P, m.intermediate_size, act, stream) == KIMKV_OK
-            && kimkv_linear(act, P, m.intermediate_size, L.wdown, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK;
+            && kimkv_linear(act, G, m.intermediate_size, L.wdown, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK;
     }
     ok = ok && kimkv_model_rmsnorm(x, d_last, static_cast<std::uint32_t>(S), final_norm, m.hidden_size,
                                    m.rms_norm_epsilon, hf, stream) == KIMKV_OK
@@ -431,6 +459,10 @@ std::unique_ptr<HipTinyLlamaRunner> HipTinyLlamaRunner::create(EngineKvBackend& 
     if (!impl->allocate(error)) return nullptr;
     if (!impl->initWeights()) {
         if (error) *error = "weight initialisation failed";
+        return nullptr;
+    }
+    if (!impl->tuneGemms()) {
+        if (error) *error = "GEMM algorithm selection failed";
         return nullptr;
     }
     return std::unique_ptr<HipTinyLlamaRunner>(new HipTinyLlamaRunner(std::move(impl)));
