@@ -131,6 +131,11 @@ _SIGNATURES = {
                                            ctypes.POINTER(ctypes.c_uint64)]),
     "kimkv_prefill_timing": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_uint64)]),
+    "kimkv_linear": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
+                                    ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_void_p]),
+    "kimkv_linear_tune": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
+                                         ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int, ctypes.c_float,
+                                         ctypes.c_void_p]),
     "kimkv_synth_value": (ctypes.c_uint16, [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32]),
     "kimkv_synth_kv_row": (ctypes.c_uint64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
     "kimkv_fill_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
@@ -392,6 +397,20 @@ def decode_plan(storage_handle: int, token_counts, query_heads: int):
 
 def workspace_bytes(token_count: int, chunk_tokens: int, query_heads: int, head_dim: int) -> int:
     return int(lib().kimkv_decode_workspace_bytes(token_count, chunk_tokens, query_heads, head_dim))
+
+
+def linear(x_ptr: int, rows: int, in_features: int, w_ptr: int, out_features: int, y_ptr: int, y_f32: bool,
+           beta: float, stream: Optional[Stream] = None) -> None:
+    """y[rows][out] = x[rows][in] . w[out][in]^T + beta * y (kimkv_linear)."""
+    check(lib().kimkv_linear(ctypes.c_void_p(x_ptr), rows, in_features, ctypes.c_void_p(w_ptr), out_features,
+                             ctypes.c_void_p(y_ptr), 1 if y_f32 else 0, beta, _sh(stream)), "linear")
+
+
+def linear_tune(x_ptr: int, rows: int, in_features: int, w_ptr: int, out_features: int, y_ptr: int, y_f32: bool,
+                beta: float, stream: Optional[Stream] = None) -> None:
+    """kimkv_linear_tune: times candidates on these buffers (y is clobbered)."""
+    check(lib().kimkv_linear_tune(ctypes.c_void_p(x_ptr), rows, in_features, ctypes.c_void_p(w_ptr), out_features,
+                                  ctypes.c_void_p(y_ptr), 1 if y_f32 else 0, beta, _sh(stream)), "linear_tune")
 
 
 def decode_timing(enable: bool):

@@ -138,3 +138,42 @@ def test_scheduler_generation_matches_oracle(host, dev):
     sched.close()
     runner.close()
     stream.destroy()
+
+
+def _f16(rng, shape, scale):
+    return (rng.standard_normal(shape) * scale).astype(np.float16)
+
+
+def test_linear_matches_fp32_reference(dev):
+    """kimkv_linear (hipBLASLt) against a float64 product of the same fp16
+    operands: fp16 output (plain and with beta = 1 accumulating into y), fp32
+    output, and the same problems again after kimkv_linear_tune picked an
+    algorithm.  Bound: fp32 accumulation + one fp16 rounding of the output."""
+    rng = np.random.default_rng(77)
+    rows, fin, fout = 200, 320, 384
+    x = _f16(rng, (rows, fin), 1.0)
+    w = _f16(rng, (fout, fin), 0.05)
+    y0 = _f16(rng, (rows, fout), 1.0)
+    prod = x.astype(np.float64) @ w.astype(np.float64).T
+    xb, wb = dev.upload(x.view(np.uint16)), dev.upload(w.view(np.uint16))
+    scratch = dev.DeviceBuffer(rows * fout * 4)
+
+    def run(y_f32, beta, tune):
+        init = y0.view(np.uint16) if not y_f32 else y0.astype(np.float32)
+        yb = dev.upload(np.ascontiguousarray(init))
+        if tune:
+            dev.linear_tune(xb.ptr, rows, fin, wb.ptr, fout, scratch.ptr, y_f32, beta)
+        dev.linear(xb.ptr, rows, fin, wb.ptr, fout, yb.ptr, y_f32, beta)
+        dev.sync()
+        if y_f32:
+            return dev.download(yb.ptr, (rows, fout), np.float32).astype(np.float64)
+        return dev.download(yb.ptr, (rows, fout), np.uint16).view(np.float16).astype(np.float64)
+
+    for tune in (False, True):
+        for y_f32, beta in ((False, 0.0), (False, 1.0), (True, 0.0)):
+            want = prod + (beta * y0.astype(np.float64) if beta else 0.0)
+            got = run(y_f32, beta, tune)
+            rel = 1e-5 if y_f32 else 2.0 ** -10
+            err = np.abs(got - want)
+            assert np.all(err <= 1e-4 + rel * np.abs(want)), (tune, y_f32, beta, float(err.max()))
+    print(f"linear {rows}x{fin}x{fout}: within fp32-accumulate + fp16 rounding", flush=True)
