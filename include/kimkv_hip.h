@@ -288,13 +288,16 @@ kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launch
  * library's first heuristic choice unless kimkv_linear_tune chose one. */
 kimkv_status kimkv_linear(const uint16_t* x, uint32_t rows, uint32_t in_features, const uint16_t* weight,
                           uint32_t out_features, void* y, int y_f32, float beta, kimkv_stream_t stream);
-/* Times the library's leading candidates for this exact problem on these
- * buffers (the stream is synchronized; y is overwritten or accumulated into
- * several times, so pass scratch contents) and makes the fastest the one
- * kimkv_linear uses for the problem on this stream.  No counterpart in the
- * reference (cuBLAS picks its own algorithm). */
-kimkv_status kimkv_linear_tune(const uint16_t* x, uint32_t rows, uint32_t in_features, const uint16_t* weight,
-                               uint32_t out_features, void* y, int y_f32, float beta, kimkv_stream_t stream);
+/* Times the library's leading candidates for this exact problem (the stream
+ * is synchronized; y is overwritten or accumulated into several times, so
+ * pass scratch contents) and makes the fastest the one kimkv_linear uses for
+ * the problem on this stream.  Successive timed products cycle through the
+ * weight_count weight matrices (e.g. every layer's), so the weights are read
+ * from HBM as in a forward pass, not from a warm cache.  No counterpart in
+ * the reference (cuBLAS picks its own algorithm). */
+kimkv_status kimkv_linear_tune(const uint16_t* x, uint32_t rows, uint32_t in_features,
+                               const uint16_t* const* weights, uint32_t weight_count, uint32_t out_features, void* y,
+                               int y_f32, float beta, kimkv_stream_t stream);
 /* out[r] = table[ids[r]] (launchEmbeddingBatch, kernels.cuh:19-26). */
 kimkv_status kimkv_model_embed(const uint16_t* table, const uint32_t* device_ids, uint32_t rows, uint32_t hidden,
                                uint16_t* out, kimkv_stream_t stream);

@@ -467,12 +467,17 @@ kimkv_status kimkv_linear(const uint16_t* x, uint32_t rows, uint32_t in_features
     return r == HIPBLAS_STATUS_SUCCESS ? KIMKV_OK : KIMKV_SUBMISSION_FAILED;
 }
 
-kimkv_status kimkv_linear_tune(const uint16_t* x, uint32_t rows, uint32_t in_features, const uint16_t* weight,
-                               uint32_t out_features, void* y, int y_f32, float beta, kimkv_stream_t stream)
+kimkv_status kimkv_linear_tune(const uint16_t* x, uint32_t rows, uint32_t in_features,
+                               const uint16_t* const* weights, uint32_t weight_count, uint32_t out_features, void* y,
+                               int y_f32, float beta, kimkv_stream_t stream)
 {
-    constexpr int kCandidates = 8;
-    constexpr int kReps = 3;
-    if (!lt_args_ok(x, in_features, weight, out_features, y, rows)) return KIMKV_INVALID_ARGUMENT;
+    constexpr int kCandidates = 16;
+    constexpr int kRounds = 3;   // each candidate's time is its best round: one-off interference does not decide
+    constexpr int kReps = 5;
+    if (weights == nullptr || weight_count == 0) return KIMKV_INVALID_ARGUMENT;
+    for (uint32_t i = 0; i < weight_count; ++i) {
+        if (!lt_args_ok(x, in_features, weights[i], out_features, y, rows)) return KIMKV_INVALID_ARGUMENT;
+    }
     if (rows == 0) return KIMKV_OK;
     LtState& st = lt_state();
     std::lock_guard<std::mutex> lock(st.mutex);
@@ -490,19 +495,33 @@ kimkv_status kimkv_linear_tune(const uint16_t* x, uint32_t rows, uint32_t in_fea
         lt_destroy(p);
         return n < 1 ? KIMKV_SUBMISSION_FAILED : KIMKV_RUNTIME_UNAVAILABLE;
     }
-    int best = -1;
-    float best_ms = 0.0f;
+    float time_ms[kCandidates];
+    bool usable[kCandidates];
     for (int a = 0; a < n; ++a) {
-        if (lt_run(st, *ctx, p, cand[a].algo, x, weight, y, beta, s) != HIPBLAS_STATUS_SUCCESS) continue;
-        bool ok = hipEventRecord(e0, s) == hipSuccess;
-        for (int i = 0; i < kReps && ok; ++i) ok = lt_run(st, *ctx, p, cand[a].algo, x, weight, y, beta, s) == HIPBLAS_STATUS_SUCCESS;
-        float ms = 0.0f;
-        ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess
-            && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
-        if (ok && (best < 0 || ms < best_ms)) {
-            best = a;
-            best_ms = ms;
+        time_ms[a] = 0.0f;
+        usable[a] = lt_run(st, *ctx, p, cand[a].algo, x, weights[0], y, beta, s) == HIPBLAS_STATUS_SUCCESS;
+    }
+    for (int round = 0; round < kRounds; ++round) {
+        for (int a = 0; a < n; ++a) {
+            if (!usable[a]) continue;
+            bool ok = hipEventRecord(e0, s) == hipSuccess;
+            for (int i = 0; i < kReps && ok; ++i) {
+                const uint16_t* w = weights[(static_cast<uint32_t>(round * kReps + i) + static_cast<uint32_t>(a)) % weight_count];
+                ok = lt_run(st, *ctx, p, cand[a].algo, x, w, y, beta, s) == HIPBLAS_STATUS_SUCCESS;
+            }
+            float ms = 0.0f;
+            ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess
+                && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+            if (!ok) {
+                usable[a] = false;
+            } else if (round == 0 || ms < time_ms[a]) {
+                time_ms[a] = ms;
+            }
         }
+    }
+    int best = -1;
+    for (int a = 0; a < n; ++a) {
+        if (usable[a] && (best < 0 || time_ms[a] < time_ms[best])) best = a;
     }
     static_cast<void>(hipEventDestroy(e0));
     static_cast<void>(hipEventDestroy(e1));

@@ -155,17 +155,26 @@ struct HipTinyLlamaRunner::Impl {
     }
 
     // Picks the GEMM algorithm of every padded row count the forward can use
-    // (multiples of kGemmRowQuantum up to gemm_cap) on the activation buffers.
+    // (multiples of kGemmRowQuantum up to gemm_cap) on the activation
+    // buffers, timing each candidate over all layers' weights.
     bool tuneGemms()
     {
         TinyLlamaConfig const& m = cfg.model;
+        std::vector<std::uint16_t const*> wqkv, wo, wgu, wdown;
+        for (Layer const& L : layers) {
+            wqkv.push_back(L.wqkv);
+            wo.push_back(L.wo);
+            wgu.push_back(L.wgu);
+            wdown.push_back(L.wdown);
+        }
+        auto const n = static_cast<std::uint32_t>(layers.size());
         bool ok = true;
         for (std::uint32_t g = kGemmRowQuantum; g <= gemm_cap && ok; g += kGemmRowQuantum) {
-            ok = kimkv_linear_tune(h, g, m.hidden_size, layers[0].wqkv, W_qkv, qkv, 0, 0.0f, stream) == KIMKV_OK
-                && kimkv_linear_tune(attn, g, m.hidden_size, layers[0].wo, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK
-                && kimkv_linear_tune(h, g, m.hidden_size, layers[0].wgu, 2 * m.intermediate_size, gu, 0, 0.0f, stream)
+            ok = kimkv_linear_tune(h, g, m.hidden_size, wqkv.data(), n, W_qkv, qkv, 0, 0.0f, stream) == KIMKV_OK
+                && kimkv_linear_tune(attn, g, m.hidden_size, wo.data(), n, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK
+                && kimkv_linear_tune(h, g, m.hidden_size, wgu.data(), n, 2 * m.intermediate_size, gu, 0, 0.0f, stream)
                     == KIMKV_OK
-                && kimkv_linear_tune(act, g, m.intermediate_size, layers[0].wdown, m.hidden_size, x, 0, 1.0f, stream)
+                && kimkv_linear_tune(act, g, m.intermediate_size, wdown.data(), n, m.hidden_size, x, 0, 1.0f, stream)
                     == KIMKV_OK;
         }
         return ok && kimkv_stream_synchronize(stream) == KIMKV_OK;

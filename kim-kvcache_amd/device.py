@@ -134,8 +134,8 @@ _SIGNATURES = {
     "kimkv_linear": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
                                     ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_void_p]),
     "kimkv_linear_tune": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
-                                         ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int, ctypes.c_float,
-                                         ctypes.c_void_p]),
+                                         ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int,
+                                         ctypes.c_float, ctypes.c_void_p]),
     "kimkv_synth_value": (ctypes.c_uint16, [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32]),
     "kimkv_synth_kv_row": (ctypes.c_uint64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
     "kimkv_fill_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
@@ -406,10 +406,12 @@ def linear(x_ptr: int, rows: int, in_features: int, w_ptr: int, out_features: in
                              ctypes.c_void_p(y_ptr), 1 if y_f32 else 0, beta, _sh(stream)), "linear")
 
 
-def linear_tune(x_ptr: int, rows: int, in_features: int, w_ptr: int, out_features: int, y_ptr: int, y_f32: bool,
+def linear_tune(x_ptr: int, rows: int, in_features: int, w_ptrs, out_features: int, y_ptr: int, y_f32: bool,
                 beta: float, stream: Optional[Stream] = None) -> None:
-    """kimkv_linear_tune: times candidates on these buffers (y is clobbered)."""
-    check(lib().kimkv_linear_tune(ctypes.c_void_p(x_ptr), rows, in_features, ctypes.c_void_p(w_ptr), out_features,
+    """kimkv_linear_tune: times candidates cycling through the weight
+    matrices w_ptrs (y is clobbered)."""
+    ws = (ctypes.c_void_p * len(w_ptrs))(*[ctypes.c_void_p(p) for p in w_ptrs])
+    check(lib().kimkv_linear_tune(ctypes.c_void_p(x_ptr), rows, in_features, ws, len(w_ptrs), out_features,
                                   ctypes.c_void_p(y_ptr), 1 if y_f32 else 0, beta, _sh(stream)), "linear_tune")
 
 

@@ -162,7 +162,7 @@ def test_linear_matches_fp32_reference(dev):
         init = y0.view(np.uint16) if not y_f32 else y0.astype(np.float32)
         yb = dev.upload(np.ascontiguousarray(init))
         if tune:
-            dev.linear_tune(xb.ptr, rows, fin, wb.ptr, fout, scratch.ptr, y_f32, beta)
+            dev.linear_tune(xb.ptr, rows, fin, [wb.ptr, wb.ptr], fout, scratch.ptr, y_f32, beta)
         dev.linear(xb.ptr, rows, fin, wb.ptr, fout, yb.ptr, y_f32, beta)
         dev.sync()
         if y_f32:
