@@ -260,6 +260,36 @@ kimkv_status kimkv_paged_prefill_batch(const kimkv_storage* storage, const kimkv
                                        const uint32_t* device_block_prefix, uint32_t item_count,
                                        uint32_t total_blocks, uint32_t query_heads, kimkv_stream_t stream);
 
+/* One workgroup of an ordered prefill launch: new tokens
+ * [block * tokens_per_block, (block + 1) * tokens_per_block) of item `item`
+ * for KV head `head`; item == 0xFFFFFFFF marks an idle slot. */
+typedef struct kimkv_prefill_block {
+    uint32_t item;
+    uint16_t head;
+    uint16_t block;
+} kimkv_prefill_block;
+
+/* Host-side placement of a prefill batch (pure host code): fills
+ * order[0 .. *order_count) with every (item, KV head, block) of the batch,
+ * laid out for kimkv_paged_prefill_ordered so that each XCD (workgroup w of
+ * the launch runs on XCD w % 8) receives a share of (item, head) pairs of
+ * about equal total work (their K/V then stays in one L2), and inside an XCD
+ * the heaviest blocks share compute units with the lightest.  token_counts[i]
+ * and new_tokens[i] are item i's; compute_units is the device's (the
+ * storage's kimkv_storage_info).  KIMKV_INVALID_ARGUMENT when capacity is too
+ * small (*order_count then holds the size needed).  No counterpart in the
+ * reference. */
+kimkv_status kimkv_prefill_order(uint32_t kv_heads, uint32_t head_dim, uint32_t query_heads, uint32_t compute_units,
+                                 const uint32_t* token_counts, const uint32_t* new_tokens, uint32_t item_count,
+                                 kimkv_prefill_block* order, uint32_t capacity, uint32_t* order_count);
+
+/* kimkv_paged_prefill_batch with the workgroup placement of
+ * kimkv_prefill_order (device_order in memory the device reads, order_count
+ * entries; results are identical to the unordered launch). */
+kimkv_status kimkv_paged_prefill_ordered(const kimkv_storage* storage, const kimkv_prefill_item* device_items,
+                                         uint32_t item_count, const kimkv_prefill_block* device_order,
+                                         uint32_t order_count, uint32_t query_heads, kimkv_stream_t stream);
+
 /* Reference attention over one table (the comparator of the reference's
  * launchAttentionScores / launchAttentionOutput, kernels.cuh:77-95, and of the
  * CPU referenceAttention, src/reference/kv_reference.cpp:136-234): MHA with

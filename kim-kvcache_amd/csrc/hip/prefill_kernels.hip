@@ -26,7 +26,9 @@
 // group sizes that do not divide 16 take a one-row-at-a-time generic path.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
+#include <vector>
 
 #include "attention_common.h"
 #include "device_common.h"
@@ -454,8 +456,12 @@ __device__ void prefill_row_generic(const PoolView& P, const kimkv_prefill_item&
     }
 }
 
+// Either order != nullptr (an ordered launch: dispatch index -> XCD-logical
+// index -> order entry) or block_prefix != nullptr (head-major blocks, the
+// blocks of an item from its last tokens to its first).
 __global__ __launch_bounds__(kBlock, 2) void prefill_kernel(PoolView P, const kimkv_prefill_item* items,
-                                                            const uint32_t* block_prefix, uint32_t item_count,
+                                                            const uint32_t* block_prefix,
+                                                            const kimkv_prefill_block* order, uint32_t item_count,
                                                             uint32_t total_blocks, uint32_t QH)
 {
     __shared__ HeadGroup groups[kSegmentGroups];
@@ -469,17 +475,25 @@ __global__ __launch_bounds__(kBlock, 2) void prefill_kernel(PoolView P, const ki
     // Head-major logical order, XCD-contiguous: the blocks of one (item, KV
     // head) run on one XCD and read that head's pages through one L2.
     uint32_t const logical = xcd_logical_index(blockIdx.x, gridDim.x);
-    uint32_t const block = logical % total_blocks;
-    uint32_t const h = logical / total_blocks;
+    uint32_t block = logical % total_blocks;
+    uint32_t h = logical / total_blocks;
     if (tid == 0) {
         s_item = 0xFFFFFFFFu;
         s_generic = 0;
     }
-    __syncthreads();
-    for (uint32_t k = tid; k < item_count; k += kBlock) {
-        if (block_prefix[k] <= block && block < block_prefix[k + 1]) s_item = k;
+    if (order != nullptr) {
+        kimkv_prefill_block const e = order[logical];
+        if (tid == 0 && e.item < item_count) s_item = e.item;
+        h = e.head;
+        block = e.block;
     }
     __syncthreads();
+    if (order == nullptr) {
+        for (uint32_t k = tid; k < item_count; k += kBlock) {
+            if (block_prefix[k] <= block && block < block_prefix[k + 1]) s_item = k;
+        }
+        __syncthreads();
+    }
     uint32_t const it = s_item;
     if (it == 0xFFFFFFFFu) return;
     kimkv_prefill_item const item = items[it];
@@ -493,9 +507,11 @@ __global__ __launch_bounds__(kBlock, 2) void prefill_kernel(PoolView P, const ki
     PrefillShape const shape = prefill_shape(QH, H, D);
     uint32_t const wave = tid >> 6;
     uint32_t const per_block = prefill_block_tokens(shape);
-    // Blocks of an item run from its last tokens (most keys) to its first.
-    uint32_t const nb = block_prefix[it + 1] - block_prefix[it];
-    uint32_t const i_block = (nb - 1 - (block - block_prefix[it])) * per_block;
+    // Unordered: the blocks of an item run from its last tokens (most keys) to its first.
+    uint32_t const i_block = order != nullptr
+        ? block * per_block
+        : (block_prefix[it + 1] - 1 - block) * per_block;
+    if (i_block >= item.new_tokens) return;
     uint32_t const T0 = item.token_count - item.new_tokens;
     // Keys the whole block needs: [0, T0 + last token of the block].
     uint32_t const last = min(i_block + per_block, item.new_tokens) - 1;
@@ -614,7 +630,115 @@ kimkv_status kimkv_paged_prefill_batch(const kimkv_storage* storage, const kimkv
     void* start = nullptr;
     kernel_timing_begin(TimedKernel::Prefill, native(stream), &start);
     prefill_kernel<<<grid, kBlock, 0, native(stream)>>>(pool_view(*storage), device_items, device_block_prefix,
-                                                        item_count, total_blocks, query_heads);
+                                                        nullptr, item_count, total_blocks, query_heads);
+    kimkv_status const st = launch_status();
+    kernel_timing_end(TimedKernel::Prefill, native(stream), start);
+    return st;
+}
+
+kimkv_status kimkv_prefill_order(uint32_t kv_heads, uint32_t head_dim, uint32_t query_heads, uint32_t compute_units,
+                                 const uint32_t* token_counts, const uint32_t* new_tokens, uint32_t item_count,
+                                 kimkv_prefill_block* order, uint32_t capacity, uint32_t* order_count)
+{
+    if (order_count == nullptr || (item_count != 0 && (token_counts == nullptr || new_tokens == nullptr))
+        || query_heads == 0 || kv_heads == 0 || kv_heads > 0xFFFFu || query_heads % kv_heads != 0) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    uint32_t const per = prefill_block_tokens(prefill_shape(query_heads, kv_heads, head_dim));
+    uint32_t const H = kv_heads;
+    struct Unit {
+        uint64_t cost;
+        kimkv_prefill_block b;
+    };
+    struct Pair {
+        uint64_t cost;
+        std::vector<Unit> units;
+    };
+    // A block's work grows with the keys its last token sees.
+    std::vector<Pair> pairs;
+    for (uint32_t i = 0; i < item_count; ++i) {
+        uint32_t const n = new_tokens[i];
+        if (n == 0 || n > token_counts[i]) continue;
+        uint32_t const nb = (n + per - 1) / per;
+        if (nb > 0xFFFFu) return KIMKV_INVALID_ARGUMENT;
+        for (uint32_t h = 0; h < H; ++h) {
+            Pair p{0, {}};
+            for (uint32_t b = nb; b-- > 0;) {
+                uint64_t const keys = static_cast<uint64_t>(token_counts[i]) - n + std::min((b + 1) * per, n);
+                Unit u{(keys + 63) / 64 + 1, kimkv_prefill_block{i, static_cast<uint16_t>(h), static_cast<uint16_t>(b)}};
+                p.cost += u.cost;
+                p.units.push_back(u);
+            }
+            pairs.push_back(std::move(p));
+        }
+    }
+    // Whole (item, head) pairs to XCDs, heaviest first onto the least loaded;
+    // with fewer pairs than XCDs the blocks themselves are spread.
+    std::vector<std::vector<Unit>> xcd(kXcds);
+    std::vector<uint64_t> load(kXcds, 0);
+    auto least = [&] {
+        uint32_t x = 0;
+        for (uint32_t k = 1; k < kXcds; ++k) {
+            if (load[k] < load[x] || (load[k] == load[x] && xcd[k].size() < xcd[x].size())) x = k;
+        }
+        return x;
+    };
+    if (pairs.size() >= kXcds) {
+        std::stable_sort(pairs.begin(), pairs.end(), [](Pair const& a, Pair const& b) { return a.cost > b.cost; });
+        for (Pair& p : pairs) {
+            uint32_t const x = least();
+            load[x] += p.cost;
+            xcd[x].insert(xcd[x].end(), p.units.begin(), p.units.end());
+        }
+    } else {
+        std::vector<Unit> all;
+        for (Pair& p : pairs) all.insert(all.end(), p.units.begin(), p.units.end());
+        std::stable_sort(all.begin(), all.end(), [](Unit const& a, Unit const& b) { return a.cost > b.cost; });
+        for (Unit const& u : all) {
+            uint32_t const x = least();
+            load[x] += u.cost;
+            xcd[x].push_back(u);
+        }
+    }
+    // Inside an XCD: heaviest first; when every block of the XCD is resident
+    // at once (two per compute unit), slot k and slot k + CUs share a compute
+    // unit, so the second half is reversed to pair heavy with light.
+    uint32_t const cus = compute_units >= kXcds ? compute_units / kXcds : 32u;
+    size_t len = 0;
+    for (auto& list : xcd) {
+        std::stable_sort(list.begin(), list.end(), [](Unit const& a, Unit const& b) { return a.cost > b.cost; });
+        size_t const m = list.size();
+        if (m > cus && m <= 2 * static_cast<size_t>(cus)) std::reverse(list.begin() + cus, list.end());
+        len = std::max(len, m);
+    }
+    uint64_t const total = len * kXcds;
+    if (total > 0x7FFFFFFFull) return KIMKV_INVALID_ARGUMENT;
+    *order_count = static_cast<uint32_t>(total);
+    if (capacity < total || (total != 0 && order == nullptr)) return KIMKV_INVALID_ARGUMENT;
+    // XCD x owns logical entries [x * len, (x + 1) * len) (xcd_logical_index
+    // with a multiple of 8 entries); short lists end in idle slots.
+    for (uint32_t x = 0; x < kXcds; ++x) {
+        for (size_t k = 0; k < len; ++k) {
+            order[x * len + k] = k < xcd[x].size() ? xcd[x][k].b : kimkv_prefill_block{0xFFFFFFFFu, 0, 0};
+        }
+    }
+    return KIMKV_OK;
+}
+
+kimkv_status kimkv_paged_prefill_ordered(const kimkv_storage* storage, const kimkv_prefill_item* device_items,
+                                         uint32_t item_count, const kimkv_prefill_block* device_order,
+                                         uint32_t order_count, uint32_t query_heads, kimkv_stream_t stream)
+{
+    if (storage == nullptr || device_items == nullptr || device_order == nullptr || query_heads == 0
+        || storage->layout.kv_heads == 0 || query_heads % storage->layout.kv_heads != 0
+        || storage->layout.head_dim > 256 || order_count > 0x7FFFFFFFu) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    if (order_count == 0 || item_count == 0) return KIMKV_OK;
+    void* start = nullptr;
+    kernel_timing_begin(TimedKernel::Prefill, native(stream), &start);
+    prefill_kernel<<<order_count, kBlock, 0, native(stream)>>>(pool_view(*storage), device_items, nullptr,
+                                                               device_order, item_count, 1u, query_heads);
     kimkv_status const st = launch_status();
     kernel_timing_end(TimedKernel::Prefill, native(stream), start);
     return st;

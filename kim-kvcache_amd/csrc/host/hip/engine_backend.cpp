@@ -790,7 +790,6 @@ void attendPrefillBatch(PrefillChunk* const* chunks, std::size_t count, std::uin
 {
     thread_local std::vector<kimkv_prefill_item> items;
     items.clear();
-    std::vector<std::uint32_t> prefix(1, 0);
     std::vector<PrefillChunk::Impl*> launched;
     BackendState* owner = nullptr;
     HipStream stream = nullptr;
@@ -826,25 +825,48 @@ void attendPrefillBatch(PrefillChunk* const* chunks, std::size_t count, std::uin
             continue;
         }
         items.push_back(c->item(layer, queries[i], outputs[i], scale));
-        prefix.push_back(prefix.back() + (c->count + per - 1) / per);
         launched.push_back(c);
     }
     if (launched.empty()) return;
     HipKvStorage& st = owner->storage;
+    // Workgroup placement (XCD shares of equal work, heavy blocks beside
+    // light ones), planned on the host from the items' token counts.
+    thread_local std::vector<std::uint32_t> totals, news;
+    thread_local std::vector<kimkv_prefill_block> order;
+    totals.clear();
+    news.clear();
+    for (kimkv_prefill_item const& it : items) {
+        totals.push_back(it.token_count);
+        news.push_back(it.new_tokens);
+    }
+    KvLayout const& kl = owner->config.kv_layout;
+    kimkv_storage_info info{};
+    std::uint32_t const units = kimkv_storage_query(st.handle(), &info) == KIMKV_OK && info.compute_units > 0
+        ? static_cast<std::uint32_t>(info.compute_units)
+        : 0u;
+    auto plan = [&](kimkv_prefill_block* out, std::uint32_t capacity, std::uint32_t* n) {
+        return kimkv_prefill_order(kl.kv_head_count, kl.head_dimension, owner->config.query_head_count, units,
+                                   totals.data(), news.data(), static_cast<std::uint32_t>(items.size()), out,
+                                   capacity, n);
+    };
+    std::uint32_t order_count = 0;
+    static_cast<void>(plan(nullptr, 0, &order_count));
+    order.resize(order_count);
+    kimkv_status k = plan(order.data(), order_count, &order_count);
     std::size_t const items_bytes = (items.size() * sizeof(kimkv_prefill_item) + 15) & ~std::size_t{15};
     thread_local std::vector<unsigned char> staging;
-    staging.resize(items_bytes + prefix.size() * 4);
+    staging.resize(items_bytes + order.size() * sizeof(kimkv_prefill_block));
     std::memcpy(staging.data(), items.data(), items.size() * sizeof(kimkv_prefill_item));
-    std::memcpy(staging.data() + items_bytes, prefix.data(), prefix.size() * 4);
-    kimkv_status k = KIMKV_SUBMISSION_FAILED;
-    {
+    std::memcpy(staging.data() + items_bytes, order.data(), order.size() * sizeof(kimkv_prefill_block));
+    if (k == KIMKV_OK) {
+        k = KIMKV_SUBMISSION_FAILED;
         std::lock_guard<std::mutex> lock(st.launchMutex());
         auto* d = static_cast<unsigned char*>(st.ring().stage(staging.data(), staging.size(), stream));
         if (d != nullptr) {
-            k = kimkv_paged_prefill_batch(st.handle(), reinterpret_cast<kimkv_prefill_item const*>(d),
-                                          reinterpret_cast<std::uint32_t const*>(d + items_bytes),
-                                          static_cast<std::uint32_t>(items.size()), prefix.back(),
-                                          owner->config.query_head_count, stream);
+            k = kimkv_paged_prefill_ordered(st.handle(), reinterpret_cast<kimkv_prefill_item const*>(d),
+                                            static_cast<std::uint32_t>(items.size()),
+                                            reinterpret_cast<kimkv_prefill_block const*>(d + items_bytes),
+                                            order_count, owner->config.query_head_count, stream);
         }
         st.ring().fence(stream);
     }

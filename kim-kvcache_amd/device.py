@@ -45,6 +45,8 @@ APPEND_JOB = np.dtype({
     "offsets": [0, 8, 16, 24, 28, 32, 36, 40, 44, 48, 50, 52, 53],
     "itemsize": 56,
 })
+PREFILL_BLOCK = np.dtype([("item", "<u4"), ("head", "<u2"), ("block", "<u2")])
+
 PREFILL_ITEM = np.dtype({
     "names": ["descriptors", "descriptor_count", "token_count", "new_tokens", "layer", "query", "output",
               "attention_scale"],
@@ -125,6 +127,12 @@ _SIGNATURES = {
     "kimkv_prefill_tokens_per_block": (ctypes.c_uint32, [ctypes.c_void_p, ctypes.c_uint32]),
     "kimkv_paged_prefill_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
                                                  ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_prefill_order": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
+                                           ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32)]),
+    "kimkv_paged_prefill_ordered": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
+                                                   ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                                   ctypes.c_void_p]),
     "kimkv_reference_attention": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "kimkv_decode_timing": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
@@ -371,6 +379,12 @@ class Storage:
         check(lib().kimkv_paged_prefill_batch(self.h, ctypes.c_void_p(items_ptr), ctypes.c_void_p(prefix_ptr),
                                               item_count, total_blocks, query_heads, _sh(stream)), "paged_prefill_batch")
 
+    def prefill_ordered_launch(self, items_ptr: int, item_count: int, order_ptr: int, order_count: int,
+                               query_heads: int, stream: Optional[Stream] = None) -> None:
+        check(lib().kimkv_paged_prefill_ordered(self.h, ctypes.c_void_p(items_ptr), item_count,
+                                                ctypes.c_void_p(order_ptr), order_count, query_heads, _sh(stream)),
+              "paged_prefill_ordered")
+
     def destroy(self) -> None:
         if self.handle:
             lib().kimkv_storage_destroy(self.h)
@@ -381,6 +395,21 @@ class Storage:
             self.destroy()
         except Exception:
             pass
+
+
+def prefill_order(kv_heads: int, head_dim: int, query_heads: int, compute_units: int, token_counts, new_tokens):
+    """kimkv_prefill_order: the workgroup placement of an ordered prefill launch."""
+    tc = np.ascontiguousarray(token_counts, dtype=np.uint32)
+    nt = np.ascontiguousarray(new_tokens, dtype=np.uint32)
+    n = ctypes.c_uint32()
+    lib().kimkv_prefill_order(kv_heads, head_dim, query_heads, compute_units, tc.ctypes.data_as(ctypes.c_void_p),
+                              nt.ctypes.data_as(ctypes.c_void_p), len(tc), None, 0, ctypes.byref(n))
+    order = np.zeros(n.value, dtype=PREFILL_BLOCK)
+    check(lib().kimkv_prefill_order(kv_heads, head_dim, query_heads, compute_units,
+                                    tc.ctypes.data_as(ctypes.c_void_p), nt.ctypes.data_as(ctypes.c_void_p), len(tc),
+                                    order.ctypes.data_as(ctypes.c_void_p), n.value, ctypes.byref(n)),
+          "prefill_order")
+    return order
 
 
 def decode_plan(storage_handle: int, token_counts, query_heads: int):

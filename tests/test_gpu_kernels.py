@@ -283,15 +283,25 @@ def _prefill_case(dev, shape, cases, G, micro_tokens=8, extent_tokens=64, seed=2
         lanes.append((table, t0, n, layer, q))
     ibuf, pbuf = dev.upload(items), dev.upload(prefix)
     storage.prefill_launch(ibuf.ptr, pbuf.ptr, len(cases), total, QH)
+    # The same batch as an ordered launch (kimkv_prefill_order placement) into
+    # second output buffers: the placement must not change a single bit.
+    items2 = items.copy()
+    outs2 = [dev.DeviceBuffer(n * QH * D * 2) for _, n in cases]
+    for i, ob in enumerate(outs2):
+        items2[i]["output"] = ob.ptr
+    order = dev.prefill_order(H, D, QH, storage.info().compute_units, totals, [n for _, n in cases])
+    ibuf2, obuf_order = dev.upload(items2), dev.upload(order)
+    storage.prefill_ordered_launch(ibuf2.ptr, len(cases), obuf_order.ptr, len(order), QH)
     dev.sync()
     worst = 0.0
-    for (table, t0, n, layer, q), obuf in zip(lanes, outs):
+    for (table, t0, n, layer, q), obuf, obuf2 in zip(lanes, outs, outs2):
         got = dev.download(obuf.ptr, (n, QH * D), np.uint16)
+        assert np.array_equal(got, dev.download(obuf2.ptr, (n, QH * D), np.uint16)), "ordered launch differs"
         for i in range(n):
             want = pools.paged_decode(table, t0 + i + 1, layer, QH, q[i * QH * D:(i + 1) * QH * D], scale, f32=True)
             worst = max(worst, helpers.assert_attention_close(got[i], want))
-    print(f"prefill shape={shape} G={G} cases={cases} per_block={per} blocks={total} max_err={worst:.2e}",
-          flush=True)
+    print(f"prefill shape={shape} G={G} cases={cases} per_block={per} blocks={total} ordered={len(order)} "
+          f"max_err={worst:.2e}", flush=True)
 
 
 def test_prefill_causal_matches_per_token_decode(dev):
