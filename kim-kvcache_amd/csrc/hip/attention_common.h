@@ -13,7 +13,7 @@ namespace kimkv {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-constexpr unsigned kMaxChunk = 8192;      // tokens per chunk (multiple of 64)
+constexpr unsigned kMaxChunk = 16384;     // tokens per chunk (multiple of 64)
 constexpr unsigned kMaxGroups = kMaxChunk / 8;
 constexpr float kLog2e = 1.4426950408889634f;
 

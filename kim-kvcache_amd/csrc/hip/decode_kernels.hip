@@ -64,7 +64,9 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
     // the current step's compute (two register buffers), so each wave keeps
     // up to two steps of K/V in flight and the compute hides under them.  The
     // tail variants mask tokens past the chunk end; full steps skip every
-    // per-token compare.
+    // per-token compare and load unconditionally (the caller guarantees every
+    // group of the chunk is mapped), so the waits before a compute cover
+    // exactly the older buffer's loads.
     struct Ops {
         half8_t k[2][2][2];
         half8_t v[2][4];
@@ -79,7 +81,7 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
 #pragma unroll
             for (uint32_t e = 0; e < 2; ++e) {
                 uint32_t const tt = 32 * kb + 8 * x + 4 * e + (l & 3u);
-                if ((!kTail || tt < nvalid) && gk.base != nullptr) {
+                if (!kTail || (tt < nvalid && gk.base != nullptr)) {
                     // K column blocks of 32 dims: dims [8a, 8a+8) and [32+8a, 40+8a).
                     const uint16_t* row = gk.base + gk.cap * head_unit
                         + static_cast<uint64_t>(gk.pt0 + 4 * e + (l & 3u)) * 32 + a * 8;
@@ -92,7 +94,7 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
             }
             GroupEntry const gv = groups[tg + 4 * kb + a];
             uint32_t const vt0 = 32 * kb + 8 * a;
-            if ((!kTail || vt0 < nvalid) && gv.base != nullptr) {
+            if (!kTail || (vt0 < nvalid && gv.base != nullptr)) {
                 // V^T column block of vw tokens holding this 8-token group; row d = 16 db + r.
                 uint32_t const vw = v_width(gv.cap);
                 const uint16_t* vt = gv.base + gv.cap * head_unit + v_offset(gv.cap, D, gv.pt0, r);
@@ -185,34 +187,32 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
             }
         }
     };
-    auto load_step = [&](Ops& o, uint32_t t0) {
-        if (c1 - t0 >= 64) {
-            load(o, t0, std::false_type{});
-        } else {
-            load(o, t0, std::true_type{});
-        }
-    };
-    auto compute_step = [&](Ops& o, uint32_t t0) {
-        if (c1 - t0 >= 64) {
-            compute(o, t0, std::false_type{});
-        } else {
-            compute(o, t0, std::true_type{});
-        }
-    };
     Ops buf_a;
     Ops buf_b;
-    uint32_t t0 = c0;
-    load_step(buf_a, t0);
-    while (true) {
-        uint32_t const t1 = t0 + 64;
-        if (t1 < c1) load_step(buf_b, t1);
-        compute_step(buf_a, t0);
-        if (t1 >= c1) break;
-        uint32_t const t2 = t1 + 64;
-        if (t2 < c1) load_step(buf_a, t2);
-        compute_step(buf_b, t1);
-        if (t2 >= c1) break;
-        t0 = t2;
+    std::false_type const full{};
+    uint32_t const nfull = (c1 - c0) >> 6;
+    if (nfull > 0) {
+        // At the top of each round buf_a holds step s - 1 in flight; the body
+        // has no bounds test, so no load in it is conditional.
+        load(buf_a, c0, full);
+        uint32_t s = 1;
+        for (; s + 1 < nfull; s += 2) {
+            load(buf_b, c0 + 64 * s, full);
+            compute(buf_a, c0, full);
+            load(buf_a, c0 + 64 * (s + 1), full);
+            compute(buf_b, c0, full);
+        }
+        if (s < nfull) {
+            load(buf_b, c0 + 64 * s, full);
+            compute(buf_a, c0, full);
+            compute(buf_b, c0, full);
+        } else {
+            compute(buf_a, c0, full);
+        }
+    }
+    if (c0 + 64 * nfull < c1) {
+        load(buf_a, c0 + 64 * nfull, std::true_type{});
+        compute(buf_a, c0 + 64 * nfull, std::true_type{});
     }
 
     float l_tot = l_part + __shfl_xor(l_part, 16);
@@ -448,6 +448,14 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         __syncthreads();
     }
 
+    // The fast path loads full steps without per-group checks: a chunk with
+    // an unmapped 8-token group goes to the generic path, which skips
+    // unmapped tokens.
+    bool hole = false;
+    for (uint32_t g = tid; g < ngroups; g += kBlock) hole |= groups[g].base == nullptr;
+    if (hole) s_generic = 1;
+    __syncthreads();
+
     uint32_t const wave = tid >> 6;
     uint32_t const h = blockIdx.y * kHeadsPerBlock + wave;
     if (h >= H) return;
@@ -622,17 +630,30 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
         return KIMKV_INVALID_ARGUMENT;
     }
     uint64_t total = 0;
-    for (uint32_t i = 0; i < lane_count; ++i) total += token_counts[i];
+    uint64_t longest = 0;
+    for (uint32_t i = 0; i < lane_count; ++i) {
+        total += token_counts[i];
+        longest = token_counts[i] > longest ? token_counts[i] : longest;
+    }
     uint64_t const cus = storage->compute_units > 0 ? static_cast<uint64_t>(storage->compute_units) : 256u;
     uint64_t const heads_per_block = kHeadsPerBlock;
     uint64_t const head_blocks = (storage->layout.kv_heads + heads_per_block - 1) / heads_per_block;
-    // Aim for ~8 workgroups per compute unit: long chunks amortise each
-    // workgroup's prologue and keep the split-K partials (and their merge)
-    // small; measured at 256 x 32k tokens this beats ~32 per CU by 2-3 %.
-    uint64_t target = total * head_blocks / (cus * 8);
-    target = (target + 63) / 64 * 64;
+    // Aim for one round of resident workgroups (two per CU): every extra
+    // workgroup costs a prologue of dependent reads during which its waves
+    // stream nothing, and every extra chunk adds split-K partials to merge.
+    // Then even out the longest lane's chunks, so it has no short last chunk.
+    // Measured at 256 lanes x 32k tokens (one layer): 3 workgroups per CU
+    // 1.254 ms, 4: 1.268, 8: 1.315, 16: 1.375; at 128 lanes 2 per CU
+    // 0.635 ms, 4: 0.653, 8: 0.686.
+    uint64_t target = (total * head_blocks + cus * 2 - 1) / (cus * 2);
     if (target < kMinChunk) target = kMinChunk;
     if (target > kMaxChunk) target = kMaxChunk;
+    if (longest > target) {
+        uint64_t const pieces = (longest + target - 1) / target;
+        target = (longest + pieces - 1) / pieces;
+    }
+    target = (target + 63) / 64 * 64;
+    if (target < kMinChunk) target = kMinChunk;
     uint64_t acc = 0;
     chunk_prefix[0] = 0;
     for (uint32_t i = 0; i < lane_count; ++i) {

@@ -139,10 +139,14 @@ def test_promotion_bit_exact(dev):
 
 # ---- decode ---------------------------------------------------------------------
 
-def _run_decode(dev, storage, lanes, query_heads, stream=None):
-    """lanes: list of (desc array, token_count, layer, query codes, scale)."""
+def _run_decode(dev, storage, lanes, query_heads, stream=None, chunk=None):
+    """lanes: list of (desc array, token_count, layer, query codes, scale); chunk forces the chunk length."""
     counts = [t for (_, t, _, _, _) in lanes]
-    chunk, prefix, total = storage.decode_plan(counts, query_heads)
+    if chunk is None:
+        chunk, prefix, total = storage.decode_plan(counts, query_heads)
+    else:
+        prefix = np.concatenate([[0], np.cumsum([(t + chunk - 1) // chunk for t in counts])]).astype(np.uint32)
+        total = int(prefix[-1])
     keep = []
     items = np.zeros(len(lanes), dtype=dev.DECODE_ITEM)
     outs = []
@@ -163,7 +167,7 @@ def _run_decode(dev, storage, lanes, query_heads, stream=None):
 
 
 def _decode_case(dev, shape, token_counts, G, micro_tokens=8, extent_tokens=64, layer=None, seed=1,
-                 uniform_pages=None):
+                 uniform_pages=None, chunk=None):
     L, H, D = shape
     QH = H * G
     micro_cap = sum(t // micro_tokens + 2 for t in token_counts) + 8
@@ -184,7 +188,7 @@ def _decode_case(dev, shape, token_counts, G, micro_tokens=8, extent_tokens=64, 
         q = oracle.synth_rows(QH * D, seed * 1000 + i, 0, D)
         lay = (i * 7) % L if layer is None else layer
         lanes.append((table, T, lay, q, 1.0 / math.sqrt(D)))
-    outs, chunk, total = _run_decode(dev, storage, lanes, QH)
+    outs, chunk, total = _run_decode(dev, storage, lanes, QH, chunk=chunk)
     worst = 0.0
     for (table, T, lay, q, scale), got in zip(lanes, outs):
         want = pools.paged_decode(table, T, lay, QH, q, scale, f32=True)
@@ -217,6 +221,37 @@ def test_decode_combine_wide_heads_and_many_chunks(dev):
     assert total > 2
     chunk, total = _decode_case(dev, (1, 4, 64), [20000, 33], G=8, seed=15)
     assert (20000 + chunk - 1) // chunk > 64
+
+
+def test_decode_full_step_counts(dev):
+    # Chunks of 1..9 full 64-token steps, odd and even, with and without a tail.
+    _decode_case(dev, (2, 4, 64), [128, 192, 256, 320, 389, 447, 511, 576], G=8, seed=16)
+    _decode_case(dev, (1, 4, 64), [4096 + 64 * 3, 4096 + 77, 8192], G=8, seed=17)
+
+
+def test_decode_plan_balances_long_lanes(dev):
+    storage = dev.Storage(1, 4, 64, 16, 16)
+    cus = storage.info().compute_units
+    for lanes, T in [(256, 32769), (128, 32769), (256, 32768), (60, 1600), (3, 12345), (1, 1)]:
+        chunk, prefix, total = storage.decode_plan([T] * lanes, 32)
+        n = (T + chunk - 1) // chunk
+        assert chunk % 64 == 0 and 256 <= chunk <= 16384
+        assert total == lanes * n and list(prefix) == [i * n for i in range(lanes + 1)]
+        # The lane's chunks are even: the last one is short by less than 64 tokens per chunk.
+        assert n * chunk - T < 64 * n or chunk == 256
+        # About one round of resident workgroups (two per CU) once lanes are long enough.
+        if lanes * T >= 2 * cus * 16384:
+            assert total <= 2 * cus + lanes
+    ragged = [100, 5000, 32769, 7]
+    chunk, prefix, total = storage.decode_plan(ragged, 32)
+    assert total == sum((t + chunk - 1) // chunk for t in ragged)
+
+
+def test_decode_long_chunks(dev):
+    # The longest chunks the kernel takes (16384 tokens: a 2048-entry group
+    # table) and a balanced 3-way split of a 32k lane, with and without split-K.
+    _decode_case(dev, (1, 4, 64), [16384, 16384 + 64 * 5 + 3, 700], G=8, seed=18, chunk=16384)
+    _decode_case(dev, (1, 4, 64), [32769, 10944, 5], G=8, seed=19, chunk=10944)
 
 
 def test_decode_group_sizes_fast_path(dev):
