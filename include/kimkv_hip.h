@@ -215,9 +215,17 @@ kimkv_status kimkv_promote_batch(const kimkv_storage* storage,
                                  const kimkv_promotion_job* device_jobs, uint32_t job_count,
                                  kimkv_stream_t stream);
 
+/* Set by kimkv_decode_plan in *chunk_tokens when each workgroup should take
+ * one KV head and split its chunk over its four waves (merged in the
+ * workgroup) instead of taking four KV heads; the other bits are the chunk
+ * length.  Pass the planned value through to kimkv_paged_decode_batch and
+ * kimkv_decode_workspace_bytes unchanged. */
+#define KIMKV_DECODE_HEAD_SPLIT 0x80000000u
+
 /* Split-K planning for a ragged decode batch.  Given the lanes' token counts
- * (host array), picks the chunk length (a multiple of 64 tokens, 256..8192) and
- * fills chunk_prefix[0..lane_count] (host array) with the running chunk count.
+ * (host array), picks the chunk length (a multiple of 64 tokens, 256..65536,
+ * possibly with KIMKV_DECODE_HEAD_SPLIT set) and fills
+ * chunk_prefix[0..lane_count] (host array) with the running chunk count.
  * Returns the total chunk count in *total_chunks. */
 kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* token_counts,
                                uint32_t lane_count, uint32_t query_heads,

@@ -13,15 +13,47 @@ namespace kimkv {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-constexpr unsigned kMaxChunk = 16384;     // tokens per chunk (multiple of 64)
+constexpr unsigned kMaxChunk = 65536;     // tokens per chunk (multiple of 64)
 constexpr unsigned kMaxGroups = kMaxChunk / 8;
 constexpr float kLog2e = 1.4426950408889634f;
 
-// One 8-token group of the chunk: `base` is the page's (layer, head 0) block.
+// One 8-token group of the chunk, 8 bytes so a 65536-token chunk's table
+// fits in 64 KiB of LDS: `page` is the slot, with kExtentPage set for an
+// extent page (kUnmappedGroup when no descriptor covers the group); `pt0` is
+// the group's first token inside the page, `cap` the page's capacity.
+constexpr uint32_t kExtentPage = 0x80000000u;
+constexpr uint32_t kUnmappedGroup = 0xFFFFFFFFu;
+
 struct GroupEntry {
-    const uint16_t* base;
-    uint32_t cap;
-    uint32_t pt0;
+    uint32_t page;
+    uint16_t pt0;
+    uint16_t cap;
+};
+
+// Resolves group entries to the (layer, head) block of their page for one
+// (layer, KV head): block = pool + slot * page_elements + cap * unit with
+// unit = (layer * H + head) * 2 * D.
+struct GroupResolver {
+    const uint16_t* micro;
+    const uint16_t* extent;
+    uint64_t micro_page_elements;
+    uint64_t extent_page_elements;
+
+    __device__ GroupResolver(const PoolView& P, uint32_t layer, uint32_t head)
+    {
+        uint64_t const unit = (static_cast<uint64_t>(layer) * P.heads + head) * 2ull * P.dim;
+        micro = P.micro + unit * P.micro_tokens;
+        extent = P.extent + unit * P.extent_tokens;
+        micro_page_elements = P.micro_page_elements;
+        extent_page_elements = P.extent_page_elements;
+    }
+
+    __device__ const uint16_t* block(GroupEntry g) const
+    {
+        uint64_t const slot = g.page & ~kExtentPage;
+        return (g.page & kExtentPage) != 0 ? extent + slot * extent_page_elements
+                                           : micro + slot * micro_page_elements;
+    }
 };
 
 __device__ inline float wave_max(float v)
@@ -61,8 +93,8 @@ __device__ inline half8_t load_half8_stream(const uint16_t* p)
 // Records the 8-token groups of [c0, c1) that entry `e` covers.  An entry
 // whose pages do not keep 8-token groups aligned (or names no page of the
 // storage) switches the chunk to the generic path.
-__device__ inline void add_groups(const PoolView& P, kimkv_block_desc const& e, uint32_t layer, uint32_t c0,
-                                  uint32_t c1, uint32_t T, GroupEntry* groups, uint32_t* s_generic)
+__device__ inline void add_groups(const PoolView& P, kimkv_block_desc const& e, uint32_t c0, uint32_t c1,
+                                  uint32_t T, GroupEntry* groups, uint32_t* s_generic)
 {
     uint32_t const b = e.logical_token_begin;
     uint32_t const end = b + e.valid_tokens;
@@ -77,9 +109,9 @@ __device__ inline void add_groups(const PoolView& P, kimkv_block_desc const& e, 
         *s_generic = 1;
         return;
     }
-    const uint16_t* base = page + head_block(P, cap, layer, 0);
+    uint32_t const tag = e.kind == KIMKV_PAGE_EXTENT ? e.slot | kExtentPage : e.slot;
     for (uint32_t g = (lo - c0) >> 3; g < (hi - c0 + 7) >> 3; ++g) {
-        groups[g] = GroupEntry{base, cap, c0 + 8 * g - b};
+        groups[g] = GroupEntry{tag, static_cast<uint16_t>(c0 + 8 * g - b), static_cast<uint16_t>(cap)};
     }
 }
 

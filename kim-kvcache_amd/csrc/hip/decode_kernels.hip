@@ -34,9 +34,20 @@ constexpr unsigned kMinChunk = 256;
 // ---------------------------------------------------------------------------
 // Fast path for one wave: kv head h, head_dim 64, group <= 16.
 // ---------------------------------------------------------------------------
-__device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_item& item,
-                                uint32_t h, uint32_t G, uint32_t QH, uint32_t c0, uint32_t c1,
-                                uint32_t chunk_index, bool single_chunk)
+// Online-softmax state of one wave over its tokens: lane (a, r) holds
+// O^T[d][r] for d = 16 db + 4 a + i in acc[db][i], and the running max m and
+// denominator l of query column r (the same in every lane group a).
+struct WavePartial {
+    float4_t acc[4];
+    float m;
+    float l;
+};
+
+// Tokens [c0, c1) of kv head h; the group table starts at token g0 (c0 - g0
+// is a multiple of 64).
+__device__ WavePartial decode_wave_d64(const GroupEntry* groups, const GroupResolver& res,
+                                       const kimkv_decode_item& item, uint32_t h, uint32_t G, uint32_t g0,
+                                       uint32_t c0, uint32_t c1)
 {
     constexpr uint32_t D = 64;
     uint32_t const l = threadIdx.x & 63u;
@@ -45,7 +56,6 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
     uint32_t const x = (l >> 2) & 3u;     // K-operand row group
     uint32_t const q = h * G + r;
     bool const qvalid = r < G;
-    uint64_t const head_unit = static_cast<uint64_t>(h) * 2u * D;   // x cap = head offset
 
     half8_t qb0 = {};
     half8_t qb1 = {};
@@ -73,7 +83,7 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
     };
     auto load = [&](Ops& o, uint32_t t0, auto tail) {
         constexpr bool kTail = decltype(tail)::value;
-        uint32_t const tg = (t0 - c0) >> 3;
+        uint32_t const tg = (t0 - g0) >> 3;
         uint32_t const nvalid = c1 - t0;
 #pragma unroll
         for (uint32_t kb = 0; kb < 2; ++kb) {
@@ -81,10 +91,10 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
 #pragma unroll
             for (uint32_t e = 0; e < 2; ++e) {
                 uint32_t const tt = 32 * kb + 8 * x + 4 * e + (l & 3u);
-                if (!kTail || (tt < nvalid && gk.base != nullptr)) {
+                if (!kTail || (tt < nvalid && gk.page != kUnmappedGroup)) {
                     // K column blocks of 32 dims: dims [8a, 8a+8) and [32+8a, 40+8a).
-                    const uint16_t* row = gk.base + gk.cap * head_unit
-                        + static_cast<uint64_t>(gk.pt0 + 4 * e + (l & 3u)) * 32 + a * 8;
+                    const uint16_t* row = res.block(gk) + static_cast<uint64_t>(gk.pt0 + 4 * e + (l & 3u)) * 32
+                        + a * 8;
                     o.k[kb][e][0] = load_half8_stream(row);
                     o.k[kb][e][1] = load_half8_stream(row + static_cast<uint64_t>(gk.cap) * 32);
                 } else {
@@ -94,10 +104,10 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
             }
             GroupEntry const gv = groups[tg + 4 * kb + a];
             uint32_t const vt0 = 32 * kb + 8 * a;
-            if (!kTail || (vt0 < nvalid && gv.base != nullptr)) {
+            if (!kTail || (vt0 < nvalid && gv.page != kUnmappedGroup)) {
                 // V^T column block of vw tokens holding this 8-token group; row d = 16 db + r.
                 uint32_t const vw = v_width(gv.cap);
-                const uint16_t* vt = gv.base + gv.cap * head_unit + v_offset(gv.cap, D, gv.pt0, r);
+                const uint16_t* vt = res.block(gv) + v_offset(gv.cap, D, gv.pt0, r);
 #pragma unroll
                 for (uint32_t db = 0; db < 4; ++db) {
                     o.v[kb][db] = load_half8_stream(vt + static_cast<uint64_t>(db * 16) * vw);
@@ -217,27 +227,33 @@ __device__ void decode_wave_d64(const GroupEntry* groups, const kimkv_decode_ite
 
     float l_tot = l_part + __shfl_xor(l_part, 16);
     l_tot += __shfl_xor(l_tot, 32);
-    if (!qvalid) return;
+    WavePartial out;
+#pragma unroll
+    for (uint32_t db = 0; db < 4; ++db) out.acc[db] = acc[db];
+    out.m = m_run;
+    out.l = l_tot;
+    return out;
+}
+
+// Writes dims [d0, d0 + 4) of query head q: the fp16 output when the lane
+// has one chunk, else the chunk's (o, m, l) partial for combine_kernel (m and
+// l by the one caller per row that passes write_ml).
+__device__ inline void store_partial(const kimkv_decode_item& item, uint32_t QH, uint32_t q, uint32_t chunk_index,
+                                     bool single_chunk, float4_t o, uint32_t d0, float m, float l, bool write_ml)
+{
+    constexpr uint32_t D = 64;
     if (single_chunk) {
-        float const inv = 1.0f / l_tot;
-        uint16_t* out = item.output + static_cast<uint64_t>(q) * D;
+        float const inv = 1.0f / l;
+        uint16_t* out = item.output + static_cast<uint64_t>(q) * D + d0;
 #pragma unroll
-        for (uint32_t db = 0; db < 4; ++db) {
-#pragma unroll
-            for (uint32_t i = 0; i < 4; ++i) {
-                out[db * 16 + 4 * a + i] = __half_as_ushort(__float2half_rn(acc[db][i] * inv));
-            }
-        }
+        for (uint32_t i = 0; i < 4; ++i) out[i] = __half_as_ushort(__float2half_rn(o[i] * inv));
     } else {
         float* ws = item.workspace + (static_cast<uint64_t>(chunk_index) * QH + q) * (D + 2);
 #pragma unroll
-        for (uint32_t db = 0; db < 4; ++db) {
-#pragma unroll
-            for (uint32_t i = 0; i < 4; ++i) ws[db * 16 + 4 * a + i] = acc[db][i];
-        }
-        if (a == 0) {
-            ws[D] = m_run;
-            ws[D + 1] = l_tot;
+        for (uint32_t i = 0; i < 4; ++i) ws[d0 + i] = o[i];
+        if (write_ml) {
+            ws[D] = m;
+            ws[D + 1] = l;
         }
     }
 }
@@ -354,12 +370,19 @@ __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& 
 }
 
 // Two waves per SIMD: each wave holds two 64-token steps of K/V operands in
-// registers (256 VGPRs), so a CU keeps as many bytes in flight as four
-// single-buffered waves while the compute of one step hides under the loads
-// of the next.
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(PoolView P, const kimkv_decode_item* items,
-                                                        const uint32_t* prefix, uint32_t lane_count,
-                                                        uint32_t chunk_tokens, uint32_t QH)
+// registers, so a CU keeps as many bytes in flight as four single-buffered
+// waves while the compute of one step hides under the loads of the next.
+//
+// kSplit = false: workgroup = (lane, chunk, four kv heads), wave w takes kv
+//   head 4 blockIdx.y + w over the whole chunk.
+// kSplit = true: workgroup = (lane, chunk, kv head blockIdx.y); the chunk is
+//   cut into four 64-token-aligned quarters, one per wave, and the four
+//   online-softmax states are merged through LDS, so a lane that fits one
+//   chunk writes its output directly and needs no combine launch.
+template <bool kSplit>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
+    PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t chunk_tokens,
+    uint32_t QH)
 {
     __shared__ GroupEntry groups[kMaxGroups];
     __shared__ WaveScratch scratch[kHeadsPerBlock];
@@ -417,7 +440,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     bool const fast_shape = D == 64 && G <= 16;
     uint32_t const ngroups = (c1 - c0 + 7) / 8;
     for (uint32_t g = tid; g < ngroups; g += kBlock) {
-        groups[g] = GroupEntry{nullptr, 0, 0};
+        groups[g] = GroupEntry{kUnmappedGroup, 0, 0};
     }
     __syncthreads();
 
@@ -429,12 +452,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     for (uint32_t j = tid; j <= ngroups && dguess + j < item.descriptor_count; j += kBlock) {
         kimkv_block_desc const e = item.descriptors[dguess + j];
         if (j == 0) s_dok = e.logical_token_begin <= c0 && c0 - e.logical_token_begin < e.valid_tokens ? 1u : 0u;
-        add_groups(P, e, item.layer, c0, c1, T, groups, &s_generic);
+        add_groups(P, e, c0, c1, T, groups, &s_generic);
     }
     __syncthreads();
     if (s_dok == 0) {
         for (uint32_t g = tid; g < ngroups; g += kBlock) {
-            groups[g] = GroupEntry{nullptr, 0, 0};
+            groups[g] = GroupEntry{kUnmappedGroup, 0, 0};
         }
         if (tid < 64) {
             uint32_t const idx0 = find_descriptor_wave(item.descriptors, item.descriptor_count, c0);
@@ -443,7 +466,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         __syncthreads();
         uint32_t const idx0 = s_idx0;
         for (uint32_t j = tid; j <= ngroups && idx0 + j < item.descriptor_count; j += kBlock) {
-            add_groups(P, item.descriptors[idx0 + j], item.layer, c0, c1, T, groups, &s_generic);
+            add_groups(P, item.descriptors[idx0 + j], c0, c1, T, groups, &s_generic);
         }
         __syncthreads();
     }
@@ -452,18 +475,85 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // an unmapped 8-token group goes to the generic path, which skips
     // unmapped tokens.
     bool hole = false;
-    for (uint32_t g = tid; g < ngroups; g += kBlock) hole |= groups[g].base == nullptr;
+    for (uint32_t g = tid; g < ngroups; g += kBlock) hole |= groups[g].page == kUnmappedGroup;
     if (hole) s_generic = 1;
     __syncthreads();
 
     uint32_t const wave = tid >> 6;
-    uint32_t const h = blockIdx.y * kHeadsPerBlock + wave;
-    if (h >= H) return;
-    if (fast_shape && s_generic == 0) {
-        decode_wave_d64(groups, item, h, G, QH, c0, c1, chunk_index, single);
-    } else {
-        decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &scratch[wave]);
+    bool const fast = fast_shape && s_generic == 0;
+    if (!kSplit) {
+        uint32_t const h = blockIdx.y * kHeadsPerBlock + wave;
+        if (h >= H) return;
+        if (!fast) {
+            decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &scratch[wave]);
+            return;
+        }
+        WavePartial const w = decode_wave_d64(groups, GroupResolver(P, item.layer, h), item, h, G, c0, c0, c1);
+        uint32_t const l = tid & 63u;
+        uint32_t const r = l & 15u;
+        if (r >= G) return;
+#pragma unroll
+        for (uint32_t db = 0; db < 4; ++db) {
+            store_partial(item, QH, h * G + r, chunk_index, single, w.acc[db], db * 16 + 4 * (l >> 4), w.m, w.l,
+                          db == 0 && l < 16);
+        }
+        return;
     }
+
+    uint32_t const h = blockIdx.y;
+    if (h >= H) return;
+    if (!fast) {
+        if (wave == 0) decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &scratch[0]);
+        return;
+    }
+    uint32_t const quarter = ((c1 - c0 + 3) / 4 + 63) / 64 * 64;
+    uint32_t const s0 = min(c0 + wave * quarter, c1);
+    uint32_t const s1 = min(s0 + quarter, c1);
+    WavePartial w;
+    if (s0 < s1) {
+        w = decode_wave_d64(groups, GroupResolver(P, item.layer, h), item, h, G, c0, s0, s1);
+    } else {
+#pragma unroll
+        for (uint32_t db = 0; db < 4; ++db) w.acc[db] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        w.m = -INFINITY;
+        w.l = 0.0f;
+    }
+    // Every wave is done with the group table: its LDS holds the four states,
+    // [wave][query column][68 floats: o(64), m, l, pad].
+    constexpr uint32_t kRow = 68;
+    __syncthreads();
+    float* part = reinterpret_cast<float*>(groups);
+    {
+        uint32_t const l = tid & 63u;
+        float* row = part + (wave * 16 + (l & 15u)) * kRow;
+#pragma unroll
+        for (uint32_t db = 0; db < 4; ++db) {
+            *reinterpret_cast<float4_t*>(row + db * 16 + 4 * (l >> 4)) = w.acc[db];
+        }
+        if (l < 16) {
+            row[64] = w.m;
+            row[65] = w.l;
+        }
+    }
+    __syncthreads();
+    // Thread t merges dims [4 (t % 16), +4) of query column t / 16.
+    uint32_t const r = tid >> 4;
+    uint32_t const d0 = (tid & 15u) * 4;
+    if (r >= G) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t v = 0; v < kHeadsPerBlock; ++v) M = fmaxf(M, part[(v * 16 + r) * kRow + 64]);
+    float den = 0.0f;
+    float4_t o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t v = 0; v < kHeadsPerBlock; ++v) {
+        const float* row = part + (v * 16 + r) * kRow;
+        float const m = row[64];
+        float const c = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+        den += c * row[65];
+        o += c * *reinterpret_cast<const float4_t*>(row + d0);
+    }
+    store_partial(item, QH, h * G + r, chunk_index, single, o, d0, M, den, d0 == 0);
 }
 
 // Merges the per-chunk partials of every multi-chunk lane.  Block = (lane,
@@ -636,18 +726,26 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
         longest = token_counts[i] > longest ? token_counts[i] : longest;
     }
     uint64_t const cus = storage->compute_units > 0 ? static_cast<uint64_t>(storage->compute_units) : 256u;
-    uint64_t const heads_per_block = kHeadsPerBlock;
-    uint64_t const head_blocks = (storage->layout.kv_heads + heads_per_block - 1) / heads_per_block;
+    uint64_t const H = storage->layout.kv_heads;
+    uint64_t const head_blocks = (H + kHeadsPerBlock - 1) / kHeadsPerBlock;
     // Aim for one round of resident workgroups (two per CU): every extra
     // workgroup costs a prologue of dependent reads during which its waves
     // stream nothing, and every extra chunk adds split-K partials to merge.
-    // Then even out the longest lane's chunks, so it has no short last chunk.
-    // Measured at 256 lanes x 32k tokens (one layer): 3 workgroups per CU
-    // 1.254 ms, 4: 1.268, 8: 1.315, 16: 1.375; at 128 lanes 2 per CU
-    // 0.635 ms, 4: 0.653, 8: 0.686.
-    uint64_t target = (total * head_blocks + cus * 2 - 1) / (cus * 2);
+    // Measured at 256 lanes x 32k tokens (one layer, four kv heads per
+    // workgroup): 3 workgroups per CU 1.254 ms, 4: 1.268, 8: 1.315,
+    // 16: 1.375; at 128 lanes 2 per CU 0.635 ms, 4: 0.653, 8: 0.686.
+    uint64_t const slots = cus * 2;
+    uint64_t const per_block = (total * head_blocks + slots - 1) / slots;
+    uint64_t const per_head = (total * H + slots - 1) / slots;
+    // When four kv heads per workgroup would need split-K but one kv head per
+    // workgroup would not, take one head per workgroup with its chunk split
+    // over the four waves: same workgroup count, no partials, no merge launch.
+    bool const head_split = per_block < longest && per_head >= longest && storage->layout.head_dim == 64
+        && query_heads % H == 0 && query_heads / H <= 16;
+    uint64_t target = head_split ? longest : per_block;
     if (target < kMinChunk) target = kMinChunk;
     if (target > kMaxChunk) target = kMaxChunk;
+    // Even out the longest lane's chunks, so it has no short last chunk.
     if (longest > target) {
         uint64_t const pieces = (longest + target - 1) / target;
         target = (longest + pieces - 1) / pieces;
@@ -661,7 +759,7 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
         if (acc > 0x7FFFFFFFu) return KIMKV_INVALID_ARGUMENT;
         chunk_prefix[i + 1] = static_cast<uint32_t>(acc);
     }
-    *chunk_tokens = static_cast<uint32_t>(target);
+    *chunk_tokens = static_cast<uint32_t>(target) | (head_split ? KIMKV_DECODE_HEAD_SPLIT : 0u);
     *total_chunks = static_cast<uint32_t>(acc);
     return KIMKV_OK;
 }
@@ -669,6 +767,7 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
 size_t kimkv_decode_workspace_bytes(uint32_t token_count, uint32_t chunk_tokens, uint32_t query_heads,
                                     uint32_t head_dim)
 {
+    chunk_tokens &= ~KIMKV_DECODE_HEAD_SPLIT;
     if (chunk_tokens == 0) return 0;
     uint64_t const chunks = (static_cast<uint64_t>(token_count) + chunk_tokens - 1) / chunk_tokens;
     if (chunks <= 1) return 0;
@@ -677,9 +776,11 @@ size_t kimkv_decode_workspace_bytes(uint32_t token_count, uint32_t chunk_tokens,
 
 kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage, const kimkv_decode_item* device_items,
                                       const uint32_t* device_chunk_prefix, uint32_t lane_count,
-                                      uint32_t total_chunks, uint32_t chunk_tokens, uint32_t query_heads,
+                                      uint32_t total_chunks, uint32_t chunk_flags, uint32_t query_heads,
                                       kimkv_stream_t stream)
 {
+    bool const head_split = (chunk_flags & KIMKV_DECODE_HEAD_SPLIT) != 0;
+    uint32_t const chunk_tokens = chunk_flags & ~KIMKV_DECODE_HEAD_SPLIT;
     if (storage == nullptr || device_items == nullptr || device_chunk_prefix == nullptr || lane_count == 0
         || query_heads == 0 || query_heads % storage->layout.kv_heads != 0 || chunk_tokens == 0
         || chunk_tokens % 64 != 0 || chunk_tokens > kMaxChunk || storage->layout.head_dim > 256) {
@@ -687,11 +788,17 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage, const kimkv_
     }
     if (total_chunks == 0) return KIMKV_OK;
     hipStream_t const s = native(stream);
-    dim3 const grid(total_chunks, (storage->layout.kv_heads + kHeadsPerBlock - 1) / kHeadsPerBlock);
+    uint32_t const H = storage->layout.kv_heads;
+    dim3 const grid(total_chunks, head_split ? H : (H + kHeadsPerBlock - 1) / kHeadsPerBlock);
     void* start = nullptr;
     kernel_timing_begin(TimedKernel::Decode, s, &start);
-    decode_kernel<<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix, lane_count,
-                                          chunk_tokens, query_heads);
+    if (head_split) {
+        decode_kernel<true><<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
+                                                    lane_count, chunk_tokens, query_heads);
+    } else {
+        decode_kernel<false><<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
+                                                     lane_count, chunk_tokens, query_heads);
+    }
     kernel_timing_end(TimedKernel::Decode, s, start);
     kimkv_status const status = launch_status();
     if (status != KIMKV_OK) return status;

@@ -412,8 +412,12 @@ def prefill_order(kv_heads: int, head_dim: int, query_heads: int, compute_units:
     return order
 
 
+DECODE_HEAD_SPLIT = 0x80000000
+
+
 def decode_plan(storage_handle: int, token_counts, query_heads: int):
-    """kimkv_decode_plan: (chunk_tokens, chunk prefix over lanes, total chunks)."""
+    """kimkv_decode_plan: (chunk_tokens, chunk prefix over lanes, total chunks).  chunk_tokens may carry
+    DECODE_HEAD_SPLIT (one kv head per workgroup); pass it to the launch and workspace_bytes unchanged."""
     counts = np.ascontiguousarray(np.asarray(token_counts, dtype=np.uint32))
     prefix = np.zeros(len(counts) + 1, dtype=np.uint32)
     chunk = ctypes.c_uint32()

@@ -145,7 +145,8 @@ def _run_decode(dev, storage, lanes, query_heads, stream=None, chunk=None):
     if chunk is None:
         chunk, prefix, total = storage.decode_plan(counts, query_heads)
     else:
-        prefix = np.concatenate([[0], np.cumsum([(t + chunk - 1) // chunk for t in counts])]).astype(np.uint32)
+        length = chunk & ~dev.DECODE_HEAD_SPLIT
+        prefix = np.concatenate([[0], np.cumsum([(t + length - 1) // length for t in counts])]).astype(np.uint32)
         total = int(prefix[-1])
     keep = []
     items = np.zeros(len(lanes), dtype=dev.DECODE_ITEM)
@@ -193,8 +194,9 @@ def _decode_case(dev, shape, token_counts, G, micro_tokens=8, extent_tokens=64, 
     for (table, T, lay, q, scale), got in zip(lanes, outs):
         want = pools.paged_decode(table, T, lay, QH, q, scale, f32=True)
         worst = max(worst, helpers.assert_attention_close(got, want))
-    print(f"decode shape={shape} G={G} T={token_counts} chunk={chunk} chunks={total} max_err={worst:.2e}",
-          flush=True)
+    split = "+split" if chunk & dev.DECODE_HEAD_SPLIT else ""
+    print(f"decode shape={shape} G={G} T={token_counts} chunk={chunk & ~dev.DECODE_HEAD_SPLIT}{split} chunks={total} "
+          f"max_err={worst:.2e}", flush=True)
     return chunk, total
 
 
@@ -232,26 +234,49 @@ def test_decode_full_step_counts(dev):
 def test_decode_plan_balances_long_lanes(dev):
     storage = dev.Storage(1, 4, 64, 16, 16)
     cus = storage.info().compute_units
-    for lanes, T in [(256, 32769), (128, 32769), (256, 32768), (60, 1600), (3, 12345), (1, 1)]:
-        chunk, prefix, total = storage.decode_plan([T] * lanes, 32)
+    H = 4
+    for lanes, T in [(256, 32769), (128, 32769), (64, 32769), (256, 32768), (60, 1600), (3, 12345), (1, 1),
+                     (4, 200000)]:
+        flags, prefix, total = storage.decode_plan([T] * lanes, 32)
+        split = bool(flags & dev.DECODE_HEAD_SPLIT)
+        chunk = flags & ~dev.DECODE_HEAD_SPLIT
         n = (T + chunk - 1) // chunk
-        assert chunk % 64 == 0 and 256 <= chunk <= 16384
+        assert chunk % 64 == 0 and 256 <= chunk <= 65536
         assert total == lanes * n and list(prefix) == [i * n for i in range(lanes + 1)]
         # The lane's chunks are even: the last one is short by less than 64 tokens per chunk.
         assert n * chunk - T < 64 * n or chunk == 256
-        # About one round of resident workgroups (two per CU) once lanes are long enough.
-        if lanes * T >= 2 * cus * 16384:
-            assert total <= 2 * cus + lanes
+        # About one round of resident workgroups (two per CU): four kv heads per workgroup, or
+        # one head per workgroup when that spares the split-K merge.
+        blocks = total * (H if split else 1)
+        if lanes * T * H >= 2 * cus * T and T <= 65536:
+            assert split and n == 1, (lanes, T, flags)
+        elif lanes * T >= 2 * cus * 256:
+            assert not split and blocks <= 2 * cus + lanes, (lanes, T, flags)
     ragged = [100, 5000, 32769, 7]
-    chunk, prefix, total = storage.decode_plan(ragged, 32)
+    flags, prefix, total = storage.decode_plan(ragged, 32)
+    chunk = flags & ~dev.DECODE_HEAD_SPLIT
     assert total == sum((t + chunk - 1) // chunk for t in ragged)
 
 
 def test_decode_long_chunks(dev):
-    # The longest chunks the kernel takes (16384 tokens: a 2048-entry group
+    # The longest chunks the kernel takes (65536 tokens: an 8192-entry group
     # table) and a balanced 3-way split of a 32k lane, with and without split-K.
-    _decode_case(dev, (1, 4, 64), [16384, 16384 + 64 * 5 + 3, 700], G=8, seed=18, chunk=16384)
+    _decode_case(dev, (1, 4, 64), [65536, 65536 + 64 * 5 + 3, 700], G=8, seed=18, chunk=65536)
     _decode_case(dev, (1, 4, 64), [32769, 10944, 5], G=8, seed=19, chunk=10944)
+
+
+def test_decode_head_split(dev):
+    # One kv head per workgroup, the chunk split over four waves and merged in
+    # LDS: single-chunk lanes (output written directly), lanes with split-K
+    # partials, quarters that are empty or end in a tail, and G = 16 / G = 1.
+    S = dev.DECODE_HEAD_SPLIT
+    _decode_case(dev, (2, 4, 64), [1, 5, 64, 65, 200, 256, 257, 1000], G=8, seed=20, chunk=1024 | S)
+    _decode_case(dev, (1, 4, 64), [32769, 10944, 5, 70000], G=8, seed=21, chunk=32832 | S)
+    _decode_case(dev, (2, 2, 64), [130, 700, 3000], G=16, seed=22, chunk=512 | S)
+    _decode_case(dev, (2, 8, 64), [70, 333, 4100], G=1, seed=23, chunk=4096 | S)
+    # A table that is not 8-aligned takes the generic path in the first wave.
+    _decode_case(dev, (2, 4, 64), [17, 200, 3000], G=8, micro_tokens=6, extent_tokens=48, seed=24,
+                 uniform_pages=True, chunk=1024 | S)
 
 
 def test_decode_group_sizes_fast_path(dev):
