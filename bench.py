@@ -1109,7 +1109,10 @@ def main() -> int:
         w.plan = (chunk, total)
 
     start, stop = dev.Event(), dev.Event()
-    dev.decode_timing(True)
+    # Events bracket every 5th decode launch of the timed steps (5 is prime
+    # to the 44 launches of a step, so the sample walks every layer and lane
+    # group); events around every launch cost the stream ~1 % of a step.
+    dev.decode_timing(True, every=5)
     dev.sync()
     t_wall = time.perf_counter()
     start.record(stream)
@@ -1136,8 +1139,10 @@ def main() -> int:
     step_bytes = (decode_bytes + append_bytes) / args.steps
     value_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
     lanes_per_launch = w.groups[0][0].n if args.path == "engine" else args.lanes
-    # One decode launch per layer per lane group: bytes and time per launch.
-    per_launch_decode_bytes = decode_bytes / max(decode_launches, 1)
+    # One decode launch per layer per lane group: bytes per launch (mean over
+    # all timed launches) and time per launch (mean over the timed sample).
+    launches = args.steps * args.layers * (len(w.groups) if args.path == "engine" else 1)
+    per_launch_decode_bytes = decode_bytes / launches
     decode_avg_ms = decode_ms_total / max(decode_launches, 1)
     achieved = per_launch_decode_bytes / (decode_avg_ms * 1e-3) / 1e9
 
@@ -1189,12 +1194,14 @@ def main() -> int:
                                   else "kernels driven directly"),
                    "path": args.path,
                    "lanes": args.lanes, "context": args.context, "layers": args.layers,
-                   "decode_chunk_tokens": w.plan[0], "decode_chunks_per_launch": w.plan[1],
+                   "decode_chunk_tokens": w.plan[0] & ~dev.DECODE_HEAD_SPLIT,
+                   "decode_head_split": bool(w.plan[0] & dev.DECODE_HEAD_SPLIT), "decode_chunks_per_launch": w.plan[1],
                    "lane_groups": args.groups if args.path == "engine" else 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": profiled_traffic(lanes_per_launch, args.context, args.layers),
                      "kernel": "decode_kernel", "avg_launch_ms": round(decode_avg_ms, 4),
+                     "timed_launches": decode_launches, "launches": launches,
                      "lanes_per_launch": lanes_per_launch,
                      "bytes_per_launch": int(per_launch_decode_bytes)},
         "cpu_baseline": cpu,

@@ -308,8 +308,10 @@ kimkv_status kimkv_reference_attention(const kimkv_storage* storage,
                                        uint32_t total_tokens, const float* device_query, float* device_output,
                                        kimkv_stream_t stream);
 
-/* Average duration (ms) of the decode kernels launched since the last reset,
- * measured with events on the launch stream; for the benchmark's roofline. */
+/* Summed duration (ms) and count of the decode kernels timed since the last
+ * call, measured with events on the launch stream; for the benchmark's
+ * roofline.  `enable` > 0 times every enable-th launch from now on (the events
+ * around a launch cost the stream a few microseconds), 0 stops timing. */
 kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launches);
 /* The same for the chunked-prefill attention kernel. */
 kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launches);

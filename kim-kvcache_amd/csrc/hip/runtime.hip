@@ -21,6 +21,8 @@ thread_local int g_last_native_error = 0;
 struct DecodeTiming {
     std::mutex mutex;
     bool enabled{false};
+    uint32_t every{1};        // time every n-th launch
+    uint64_t seen{0};
     std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
     double total_ms{0.0};
     uint64_t launches{0};
@@ -63,7 +65,7 @@ void kernel_timing_begin(TimedKernel kind, hipStream_t stream, void** start)
     *start = nullptr;
     DecodeTiming& t = timing(kind);
     std::lock_guard<std::mutex> lock(t.mutex);
-    if (!t.enabled) {
+    if (!t.enabled || t.seen++ % t.every != 0) {
         return;
     }
     hipEvent_t event = nullptr;
@@ -370,7 +372,9 @@ kimkv_status kernel_timing(kimkv::TimedKernel kind, int enable, double* total_ms
     if (launches != nullptr) *launches = t.launches;
     t.total_ms = 0.0;
     t.launches = 0;
-    t.enabled = enable != 0;
+    t.enabled = enable > 0;
+    t.every = enable > 0 ? static_cast<uint32_t>(enable) : 1u;
+    t.seen = 0;
     return KIMKV_OK;
 }
 }  // namespace

@@ -448,11 +448,12 @@ def linear_tune(x_ptr: int, rows: int, in_features: int, w_ptrs, out_features: i
                                   ctypes.c_void_p(y_ptr), 1 if y_f32 else 0, beta, _sh(stream)), "linear_tune")
 
 
-def decode_timing(enable: bool):
+def decode_timing(enable, every: int = 1):
+    """Returns (ms, launches) timed since the last call; then times every `every`-th launch if enable."""
     total = ctypes.c_double()
     launches = ctypes.c_uint64()
-    check(lib().kimkv_decode_timing(1 if enable else 0, ctypes.byref(total), ctypes.byref(launches)),
-          "decode_timing")
+    check(lib().kimkv_decode_timing(max(1, int(every)) if enable else 0, ctypes.byref(total),
+                                    ctypes.byref(launches)), "decode_timing")
     return float(total.value), int(launches.value)
 
 
