@@ -916,8 +916,10 @@ def run_e2e(kimkv, dev, args) -> int:
 
     for _ in range(args.warmup):
         step()
-    dev.prefill_timing(True)
-    dev.decode_timing(True)
+    # Events bracket every 5th attention launch (22 per step of each kind),
+    # so the timing costs the iteration little.
+    dev.prefill_timing(True, every=5)
+    dev.decode_timing(True, every=5)
     tok_pre = tok_dec = 0
     t_wall = time.perf_counter()
     for _ in range(args.steps):
@@ -960,8 +962,9 @@ def run_e2e(kimkv, dev, args) -> int:
         "value": round(total / wall, 1), "unit": "tokens/s", "higher_is_better": True,
         "decode_tokens_per_s": round(tok_dec / wall, 1), "prefill_tokens_per_s": round(tok_pre / wall, 1),
         "ms_per_step": round(ms_per_step, 3), "tokens_per_step": round(total / args.steps, 1),
-        "attention_ms_per_step": {"prefill_kernel": round(pf_ms / args.steps, 3),
-                                  "decode_kernel": round(dc_ms / args.steps, 3)},
+        "attention_ms_per_step": {"prefill_kernel": round(pf_ms / max(pf_n, 1) * L, 3),
+                                  "decode_kernel": round(dc_ms / max(dc_n, 1) * L, 3),
+                                  "timed_launches": [pf_n, dc_n]},
         "dtype": "f16 in, f32 accumulate",
         "config": {"workload": f"TinyLlama-1.1B-shaped fp16 (22 layers, hidden 2048, SwiGLU 5632, 32q/4kv x 64, "
                                f"vocab 32000), seeded N(0, 0.02) weights; {n_pre} requests in {chunk}-token chunked "

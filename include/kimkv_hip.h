@@ -313,7 +313,7 @@ kimkv_status kimkv_reference_attention(const kimkv_storage* storage,
  * roofline.  `enable` > 0 times every enable-th launch from now on (the events
  * around a launch cost the stream a few microseconds), 0 stops timing. */
 kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launches);
-/* The same for the chunked-prefill attention kernel. */
+/* The same for the chunked-prefill attention kernel (same `enable`). */
 kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launches);
 
 /* ---- dense TinyLlama layers (the model runner's device side) --------------

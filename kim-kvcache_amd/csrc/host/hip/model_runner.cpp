@@ -266,6 +266,22 @@ GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSp
         && kimkv_memcpy_h2d_async(d_pos, pos, P * 4ull, stream) == KIMKV_OK
         && kimkv_memcpy_h2d_async(d_last, last, S * 4ull, stream) == KIMKV_OK;
 
+    // The four per-layer GEMMs run on G >= P rows (P rounded up to the tuned
+    // quantum); rows P..G-1 of their inputs and outputs are scratch that no
+    // other kernel reads.
+    std::uint32_t const G = std::min<std::uint32_t>((P + kGemmRowQuantum - 1) / kGemmRowQuantum * kGemmRowQuantum,
+                                                    gemm_cap);
+    // Layer l up to its K/V: RMSNorm, QKV projection, RoPE.  The embedding and
+    // layer 0's part go to the device before the token reservations and chunk
+    // begins below, so the device works while the host does those.
+    auto pre_attention = [&](Layer const& L) {
+        return kimkv_model_rmsnorm(x, nullptr, P, L.ln1, m.hidden_size, m.rms_norm_epsilon, h, stream) == KIMKV_OK
+            && kimkv_linear(h, G, m.hidden_size, L.wqkv, W_qkv, qkv, 0, 0.0f, stream) == KIMKV_OK
+            && kimkv_model_rope_split(qkv, d_pos, P, m.attention_head_count, m.kv_head_count, m.head_dimension,
+                                      m.rope_theta, q, k, v, stream) == KIMKV_OK;
+    };
+    ok = ok && kimkv_model_embed(embed, d_ids, P, m.hidden_size, x, stream) == KIMKV_OK && pre_attention(layers[0]);
+
     // KV side: token transactions for single positions, prefill chunks for the rest.
     std::vector<GenerationStepResult> steps(S, GenerationStepResult{true, 0, {}});
     std::vector<std::size_t> dec, pre;
@@ -306,18 +322,9 @@ GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSp
     std::vector<KvScalar*> po;
     std::vector<EngineKvStatus> pst;
 
-    // The four per-layer GEMMs run on G >= P rows (P rounded up to the tuned
-    // quantum); rows P..G-1 of their inputs and outputs are scratch that no
-    // other kernel reads.
-    std::uint32_t const G = std::min<std::uint32_t>((P + kGemmRowQuantum - 1) / kGemmRowQuantum * kGemmRowQuantum,
-                                                    gemm_cap);
-    ok = ok && kimkv_model_embed(embed, d_ids, P, m.hidden_size, x, stream) == KIMKV_OK;
     for (std::uint32_t l = 0; l < m.layer_count && ok; ++l) {
         Layer const& L = layers[l];
-        ok = kimkv_model_rmsnorm(x, nullptr, P, L.ln1, m.hidden_size, m.rms_norm_epsilon, h, stream) == KIMKV_OK
-            && kimkv_linear(h, G, m.hidden_size, L.wqkv, W_qkv, qkv, 0, 0.0f, stream) == KIMKV_OK
-            && kimkv_model_rope_split(qkv, d_pos, P, m.attention_head_count, m.kv_head_count, m.head_dimension,
-                                      m.rope_theta, q, k, v, stream) == KIMKV_OK;
+        if (l > 0) ok = pre_attention(L);
         if (!ok) break;
         // Writes.
         wr.clear();

@@ -457,9 +457,10 @@ def decode_timing(enable, every: int = 1):
     return float(total.value), int(launches.value)
 
 
-def prefill_timing(enable: bool):
+def prefill_timing(enable, every: int = 1):
+    """Returns (ms, launches) timed since the last call; then times every `every`-th launch if enable."""
     total = ctypes.c_double()
     launches = ctypes.c_uint64()
-    check(lib().kimkv_prefill_timing(1 if enable else 0, ctypes.byref(total), ctypes.byref(launches)),
-          "prefill_timing")
+    check(lib().kimkv_prefill_timing(max(1, int(every)) if enable else 0, ctypes.byref(total),
+                                     ctypes.byref(launches)), "prefill_timing")
     return float(total.value), int(launches.value)
