@@ -384,7 +384,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t chunk_tokens,
     uint32_t QH)
 {
-    __shared__ GroupEntry groups[kMaxGroups];
+    __shared__ __attribute__((aligned(16))) GroupEntry groups[kMaxGroups];   // also the merge buffer
     __shared__ WaveScratch scratch[kHeadsPerBlock];
     __shared__ uint32_t s_lane;
     __shared__ uint32_t s_hit;
