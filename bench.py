@@ -1067,7 +1067,7 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1",
+        print(json.dumps({"error": "bench.py measures one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}), flush=True)
         return 2
 

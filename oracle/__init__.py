@@ -6,7 +6,7 @@ oracle/_ref/libkimkv_ref.so (the reference's own CPU sources compiled by
 oracle/build.py, when they were available at build time).
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
-this package, and only as the checker or the CPU baseline.
+this package, and only to compute expected results or the CPU baseline.
 """
 from __future__ import annotations
 

@@ -4,7 +4,8 @@
  * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference's
  * CPU path and of the data semantics of its device kernels.  Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and only
- * as the checker or the CPU baseline: the product path never calls it.
+ * to compute expected results or the CPU baseline: the product path never
+ * calls it.
  *
  * Pools here use the REFERENCE page layout [layer][K/V][token][head][dim]
  * (include/kim-kv/core/kv_layout.h:73-90), not the device layout, so the

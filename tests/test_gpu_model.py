@@ -1,7 +1,7 @@
 """GPU tests of the TinyLlama-shaped model runner and the iteration scheduler
 on the HIP engine (scenarios of the reference's
 tests/cuda/cuda_model_runner_test.cpp:445-560 and the scheduler e2e path).
-The checker is the oracle's CPU forward (oracle/model.py, pinned by
+Expected results come from the oracle's CPU forward (oracle/model.py, pinned by
 tests/test_model_oracle.py) with the same seeded weights: logits within
 0.035 max-abs (the reference's bar) and every greedy token the oracle's
 argmax up to that tolerance.  Generation is teacher-forced with the GPU's

@@ -1,5 +1,5 @@
-"""Pins the model oracle (oracle/model.py) before it is used as the checker of
-the GPU model runner:
+"""Pins the model oracle (oracle/model.py) before it is used to check the GPU
+model runner:
   * RoPE at position 0 is the identity, and it preserves each pair's norm;
   * the first position's attention output is its own V (softmax over one key);
   * an independent float64 Llama forward written with torch library routines
