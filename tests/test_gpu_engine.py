@@ -643,3 +643,73 @@ def test_engine_prefill_chunk_errors(host, dev):
     snap = engine.snapshot()
     assert snap.request_count == 0 and snap.allocated_primary_pages == 0
     stream.destroy()
+
+
+def test_engine_head_split_batch_matches_oracle(host, dev):
+    """256 ragged lanes through reserveBatch + writeLayerBatch + attendLayerBatch + commitBatch: enough
+    (lane, kv head) pairs for the decode planner to take one kv head per workgroup with each lane in one
+    chunk (no split-K merge).  Contexts are built by bulk prefill with promotion of every full 64-token
+    run; every lane's output is checked against the oracle's fp32 GQA decode of its history."""
+    L, H, D, QH, lanes, seed = 2, 4, 64, 32, 256, 77
+    HD = H * D
+    rng = np.random.default_rng(seed)
+    T = [int(t) for t in rng.integers(150, 400, lanes)]
+    engine = host.Engine(L, H, D, QH, 1 << 16, sum(t // 8 + 3 for t in T) + 64, sum(t // 64 for t in T) + 16)
+    stream = dev.Stream()
+    stage = dev.DeviceBuffer(L * 2 * 400 * HD * 2)
+    for i in range(lanes):
+        assert engine.create_request(i + 1) == 0
+        dev.fill_kv(stage.ptr, L, T[i], HD, seed, i, 0, stream)
+        rc, _ = engine.append_prefill(i + 1, T[i], stage.ptr, stream, promote=True)
+        assert rc == 0
+    stream.synchronize()
+    newkv = dev.DeviceBuffer(lanes * L * 2 * HD * 2)
+    query = dev.DeviceBuffer(lanes * L * QH * D * 2)
+    out = dev.DeviceBuffer(lanes * L * QH * D * 2)
+    qseed = seed ^ 0x5155
+    for i in range(lanes):
+        dev.fill_kv(newkv.ptr + i * L * 2 * HD * 2, L, 1, HD, seed, i, T[i], stream)
+        for l in range(L):
+            dev.fill_rows(query.ptr + (i * L + l) * QH * D * 2, QH * D, qseed, dev.synth_kv_row(i, l, 0, T[i]),
+                          QH * D, stream)
+    stream.synchronize()
+    flags, _, _ = dev.decode_plan(engine.storage_handle(), [t + 1 for t in T], QH)
+    assert flags & dev.DECODE_HEAD_SPLIT and (flags & ~dev.DECODE_HEAD_SPLIT) >= max(T) + 1
+    lane = np.arange(lanes, dtype=np.uint64)
+    ws = dev.DeviceBuffer(lanes * 256)
+    b = host.LaneBatch(engine, lane + np.uint64(1), ws.ptr + lane * np.uint64(256), 256, 1.0 / math.sqrt(D), stream)
+    for l in range(L):
+        b.keys[l, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * L) + np.uint64(2 * l))
+        b.values[l, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * L) + np.uint64(2 * l + 1))
+        b.queries[l, :] = query.ptr + np.uint64(2 * QH * D) * (lane * np.uint64(L) + np.uint64(l))
+        b.outputs[l, :] = out.ptr + np.uint64(2 * QH * D) * (lane * np.uint64(L) + np.uint64(l))
+    b.reserve(np.array(T, dtype=np.uint32))
+    assert not b.failed()
+    for l in range(L):
+        b.write(l)
+        b.attend(l)
+    b.commit()
+    assert not b.failed(), sorted(set(b.status.tolist()))
+    got = dev.download(out.ptr, (lanes, L, QH * D), np.uint16)
+    worst = 0.0
+    for i in range(lanes):
+        n = T[i] + 1
+        for l in range(L):
+            kv = np.empty((1, 2, n, H, D), dtype=np.uint16)
+            for c in range(2):
+                kv[0, c, :T[i]] = oracle.synth_rows(T[i] * HD, seed, oracle.kv_row(i, l, c, 0), HD).reshape(T[i], H, D)
+                kv[0, c, T[i]] = oracle.synth_rows(HD, seed, oracle.kv_row(i, l, c, T[i]), HD).reshape(H, D)
+            pages = (n + 7) // 8
+            pools = oracle.HostPools(1, H, D, pages, 1)
+            table = np.zeros(pages, dtype=oracle.DESC)
+            for k in range(pages):
+                table[k] = (k, 1, 8 * k, min(8, n - 8 * k), 8, 0)
+                pools.append_tokens(kv, n, 8 * k, 0, k, 0, min(8, n - 8 * k))
+            q = oracle.synth_rows(QH * D, qseed, oracle.kv_row(i, l, 0, T[i]), QH * D)
+            want = pools.paged_decode(table, n, 0, QH, q, 1.0 / math.sqrt(D), f32=True)
+            a = got[i, l].view(np.float16).astype(np.float32)
+            err = np.abs(a - want)
+            assert np.all(err <= 2e-3 + 1e-3 * np.abs(want)), (i, l, float(err.max()))
+            worst = max(worst, float(err.max()))
+    print(f"engine head-split batch: lanes={lanes} T=[{min(T)},{max(T)}] chunk={flags & ~dev.DECODE_HEAD_SPLIT} "
+          f"max_err={worst:.2e}", flush=True)
