@@ -7,7 +7,6 @@ which registers it as the module `kim_kvcache_amd`.
 Submodules:
   device  -- ctypes binding of include/kimkv_hip.h (gfx950 kernels, libkimkv_hip.so)
   host    -- ctypes binding of include/kimkv_host.h (C++ host layer, libkimkv.so)
-  tables  -- page-table helpers (descriptor arrays from block tables)
 """
 from . import device  # noqa: F401
 
