@@ -107,7 +107,7 @@ def build_tests() -> list[str]:
     srcs = _sources(TEST_SRC, (".cpp",)) if os.path.isdir(TEST_SRC) else []
     os.makedirs(TEST_BIN, exist_ok=True)
     outs = [os.path.join(TEST_BIN, os.path.splitext(os.path.basename(s))[0]) for s in srcs]
-    _parallel([[CXX, *HOST_FLAGS, f"-I{INCLUDE}", s, f"-L{LIB_DIR}", "-lkimkv", "-lkimkv_hip",
+    _parallel([[CXX, *HOST_FLAGS, f"-I{INCLUDE}", f"-I{HOST_SRC}", s, f"-L{LIB_DIR}", "-lkimkv", "-lkimkv_hip",
                 "-Wl,-rpath,$ORIGIN/..", "-pthread", "-o", o] for s, o in zip(srcs, outs)])
     return outs
 

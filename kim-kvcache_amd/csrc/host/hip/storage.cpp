@@ -7,6 +7,7 @@
 #include "storage.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 
@@ -52,7 +53,7 @@ DeviceMemory& DeviceMemory::operator=(DeviceMemory&& o) noexcept
 
 // ---- StagingRing -----------------------------------------------------------------
 
-StagingRing::StagingRing(std::size_t bytes) : size_(bytes), device_()
+StagingRing::StagingRing(std::size_t bytes) : size_(bytes), device_(), regions_(bytes)
 {
     void* host = nullptr;
     void* view = nullptr;
@@ -64,12 +65,12 @@ StagingRing::StagingRing(std::size_t bytes) : size_(bytes), device_()
 
 StagingRing::~StagingRing()
 {
-    for (Region const& r : live_) {
-        if (r.done) continue;
-        if (r.event != nullptr) {
-            static_cast<void>(kimkv_event_synchronize(r.event));
+    for (auto const& r : regions_.live()) {
+        if (r.tag.done) continue;
+        if (r.tag.event != nullptr) {
+            static_cast<void>(kimkv_event_synchronize(r.tag.event));
         } else {
-            static_cast<void>(kimkv_stream_synchronize(r.stream));
+            static_cast<void>(kimkv_stream_synchronize(r.tag.stream));
         }
     }
     for (auto const& e : event_refs_) static_cast<void>(kimkv_event_destroy(e.first));
@@ -91,34 +92,24 @@ void StagingRing::dropRef(void* event)
 
 std::size_t StagingRing::reserve(std::size_t bytes, HipStream stream)
 {
-    bytes = (bytes + 255) & ~std::size_t{255};
-    std::size_t begin = head_;
-    if (begin + bytes > size_) begin = 0;
-    std::size_t const end = begin + bytes;
-    // Regions are handed out in ring order; the oldest one overlapping the
-    // new range is freed by waiting on its own fence event, or, if it was
-    // never fenced, on its stream.
-    while (!live_.empty() && live_.front().begin < end && begin < live_.front().end) {
-        Region const r = live_.front();
-        if (!r.done) {
-            if (r.event != nullptr) {
-                static_cast<void>(kimkv_event_synchronize(r.event));
+    // A region is free again once its own fence event has completed or, if
+    // it was never fenced, once its stream has drained.
+    return regions_.reserve(bytes, Consumer{stream, nullptr, false}, [this](auto const& r) {
+        if (!r.tag.done) {
+            if (r.tag.event != nullptr) {
+                static_cast<void>(kimkv_event_synchronize(r.tag.event));
             } else {
-                static_cast<void>(kimkv_stream_synchronize(r.stream));
+                static_cast<void>(kimkv_stream_synchronize(r.tag.stream));
             }
         }
-        dropRef(r.event);
-        live_.pop_front();
-    }
-    live_.push_back(Region{begin, end, stream, nullptr, false});
-    head_ = end;
-    return begin;
+        dropRef(r.tag.event);
+    });
 }
 
 void* StagingRing::stage(void const* data, std::size_t bytes, HipStream stream)
 {
     std::lock_guard<std::mutex> lock(mutex_);
-    if (host_ == nullptr || view_ == nullptr || bytes > size_ / 2) return nullptr;
+    if (host_ == nullptr || view_ == nullptr || bytes > regions_.maxRequest()) return nullptr;
     std::size_t const off = reserve(bytes, stream);
     std::memcpy(host_ + off, data, bytes);
     return view_ + off;
@@ -127,7 +118,7 @@ void* StagingRing::stage(void const* data, std::size_t bytes, HipStream stream)
 void* StagingRing::upload(void const* data, std::size_t bytes, HipStream stream)
 {
     std::lock_guard<std::mutex> lock(mutex_);
-    if (host_ == nullptr || bytes > size_ / 2) return nullptr;
+    if (host_ == nullptr || bytes > regions_.maxRequest()) return nullptr;
     if (device_.get() == nullptr) device_ = DeviceMemory(size_);
     if (device_.get() == nullptr) return nullptr;
     std::size_t const off = reserve(bytes, stream);
@@ -140,17 +131,29 @@ void* StagingRing::upload(void const* data, std::size_t bytes, HipStream stream)
 bool StagingRing::uploadTo(void* device_dst, void const* data, std::size_t bytes, HipStream stream)
 {
     std::lock_guard<std::mutex> lock(mutex_);
-    if (host_ == nullptr || bytes > size_ / 2) return false;
-    std::size_t const off = reserve(bytes, stream);
-    std::memcpy(host_ + off, data, bytes);
-    return kimkv_memcpy_h2d_async(device_dst, host_ + off, bytes, stream) == KIMKV_OK;
+    if (host_ == nullptr) return false;
+    // An upload larger than one ring request goes in pieces; a piece that
+    // needs the ring space of an earlier one waits for that copy (its region
+    // is unfenced, so reserve drains the stream first).
+    auto const* src = static_cast<unsigned char const*>(data);
+    auto* dst = static_cast<unsigned char*>(device_dst);
+    std::size_t const piece = regions_.maxRequest();
+    for (std::size_t done = 0; done < bytes;) {
+        std::size_t const n = std::min(piece, bytes - done);
+        std::size_t const off = reserve(n, stream);
+        std::memcpy(host_ + off, src + done, n);
+        if (kimkv_memcpy_h2d_async(dst + done, host_ + off, n, stream) != KIMKV_OK) return false;
+        done += n;
+    }
+    return true;
 }
 
 void StagingRing::fence(HipStream stream)
 {
     std::lock_guard<std::mutex> lock(mutex_);
+    auto unfenced = [stream](Consumer const& c) { return !c.done && c.event == nullptr && c.stream == stream; };
     int pending = 0;
-    for (Region const& r : live_) pending += (!r.done && r.event == nullptr && r.stream == stream) ? 1 : 0;
+    for (auto const& r : regions_.live()) pending += unfenced(r.tag) ? 1 : 0;
     if (pending == 0) return;
     void* event = nullptr;
     if (!spare_events_.empty()) {
@@ -166,15 +169,15 @@ void StagingRing::fence(HipStream stream)
     if (event == nullptr) {
         // Cannot fence: drain the stream so its staged regions are free again.
         static_cast<void>(kimkv_stream_synchronize(stream));
-        for (Region& r : live_) {
-            if (!r.done && r.event == nullptr && r.stream == stream) r.done = true;
+        for (auto& r : regions_.live()) {
+            if (unfenced(r.tag)) r.tag.done = true;
         }
         return;
     }
     // One event, recorded after everything staged on this stream so far,
     // covers all of that stream's unfenced regions.
-    for (Region& r : live_) {
-        if (!r.done && r.event == nullptr && r.stream == stream) r.event = event;
+    for (auto& r : regions_.live()) {
+        if (unfenced(r.tag)) r.tag.event = event;
     }
     event_refs_.emplace_back(event, pending);
 }
@@ -221,6 +224,19 @@ void DeviceBufferCache::release(void* ptr, std::size_t granted) noexcept
 
 // ---- HipKvStorage --------------------------------------------------------------------
 
+// 8 MiB by default; KIMKV_STAGING_RING_BYTES overrides it (at least 64 KiB),
+// which tests use to drive uploads through the split and wrap paths.
+static std::size_t stagingRingBytes() noexcept
+{
+    std::size_t bytes = std::size_t{8} << 20;
+    if (char const* env = std::getenv("KIMKV_STAGING_RING_BYTES")) {
+        char* end = nullptr;
+        unsigned long long const v = std::strtoull(env, &end, 10);
+        if (end != env && *end == '\0') bytes = std::max<std::size_t>(std::size_t{64} << 10, v);
+    }
+    return bytes;
+}
+
 HipKvStorage::HipKvStorage(KvLayout layout, std::uint32_t micro_capacity, std::uint32_t extent_capacity,
                            std::uint16_t micro_page_tokens, std::uint16_t extent_page_tokens) noexcept
     : layout_(layout),
@@ -228,7 +244,7 @@ HipKvStorage::HipKvStorage(KvLayout layout, std::uint32_t micro_capacity, std::u
       extent_capacity_(extent_capacity),
       micro_tokens_(micro_page_tokens),
       extent_tokens_(extent_page_tokens),
-      ring_(8u << 20)
+      ring_(stagingRingBytes())
 {
     if (!layout.valid() || micro_page_tokens == 0 || extent_page_tokens == 0) {
         status_ = HipStatus{HipError::InvalidArgument, 0};

@@ -10,10 +10,10 @@
 #include "kim-kv/core/kv_layout.h"
 #include "kim-kv/hip/hip_status.h"
 #include "kim-kv/runtime/promotion.h"
+#include "ring_regions.h"
 
 #include <cstddef>
 #include <cstdint>
-#include <deque>
 #include <map>
 #include <mutex>
 #include <vector>
@@ -65,14 +65,13 @@ public:
     [[nodiscard]] void* stage(void const* data, std::size_t bytes, HipStream stream);
     // Returns the device address of the staged copy, or nullptr on failure.
     [[nodiscard]] void* upload(void const* data, std::size_t bytes, HipStream stream);
-    // Host staging only (the caller names the device destination).
+    // Host staging only (the caller names the device destination).  Any
+    // size: uploads beyond half the ring are split into pieces.
     [[nodiscard]] bool uploadTo(void* device_dst, void const* data, std::size_t bytes, HipStream stream);
     void fence(HipStream stream);
 
 private:
-    struct Region {
-        std::size_t begin;
-        std::size_t end;
+    struct Consumer {
         HipStream stream;   // the stream whose work consumes the region
         void* event;        // nullptr until fenced; shared by the regions one fence covered
         bool done;          // consumer known complete (stream drained)
@@ -81,11 +80,10 @@ private:
     void dropRef(void* event);
 
     std::size_t size_;
-    std::size_t head_{0};
     unsigned char* host_{nullptr};
     unsigned char* view_{nullptr};   // device address of host_ (mapped, coherent)
     DeviceMemory device_;
-    std::deque<Region> live_;
+    RingRegions<Consumer> regions_;
     std::vector<std::pair<void*, int>> event_refs_;   // fence events and how many live regions use each
     std::vector<void*> spare_events_;
     std::mutex mutex_;

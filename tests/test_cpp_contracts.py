@@ -1,6 +1,8 @@
-"""Runs the C++ contract tests built from tests/cpp (CPU only: fake KV backend
-and fake model).  They mirror the reference's tests/engine scenarios for the
-single-request generation runtime and the iteration scheduler."""
+"""Runs the C++ tests built from tests/cpp (CPU only).  generation_contract_test
+uses a fake KV backend and a fake model and mirrors the reference's
+tests/engine scenarios for the single-request generation runtime and the
+iteration scheduler; staging_ring_test replays allocation sequences through
+the staging ring's region bookkeeping."""
 import os
 import subprocess
 
@@ -9,7 +11,7 @@ import pytest
 BIN = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "kim-kvcache_amd", "_lib", "tests")
 
 
-@pytest.mark.parametrize("name", ["generation_contract_test"])
+@pytest.mark.parametrize("name", ["generation_contract_test", "staging_ring_test"])
 def test_cpp_contract(name):
     path = os.path.join(BIN, name)
     if not os.path.exists(path):

@@ -645,16 +645,17 @@ def test_engine_prefill_chunk_errors(host, dev):
     stream.destroy()
 
 
-def test_engine_head_split_batch_matches_oracle(host, dev):
-    """256 ragged lanes through reserveBatch + writeLayerBatch + attendLayerBatch + commitBatch: enough
-    (lane, kv head) pairs for the decode planner to take one kv head per workgroup with each lane in one
-    chunk (no split-K merge).  Contexts are built by bulk prefill with promotion of every full 64-token
-    run; every lane's output is checked against the oracle's fp32 GQA decode of its history."""
-    L, H, D, QH, lanes, seed = 2, 4, 64, 32, 256, 77
+def _engine_lane_batch_case(host, dev, steps=1, seed=77):
+    """256 ragged lanes through reserveBatch + writeLayerBatch + attendLayerBatch + commitBatch for
+    `steps` tokens: enough (lane, kv head) pairs for the decode planner to take one kv head per workgroup
+    with each lane in one chunk (no split-K merge).  Contexts are built by bulk prefill with promotion of
+    every full 64-token run; every lane's output at every step is checked against the oracle's fp32 GQA
+    decode of its history."""
+    L, H, D, QH, lanes = 2, 4, 64, 32, 256
     HD = H * D
     rng = np.random.default_rng(seed)
     T = [int(t) for t in rng.integers(150, 400, lanes)]
-    engine = host.Engine(L, H, D, QH, 1 << 16, sum(t // 8 + 3 for t in T) + 64, sum(t // 64 for t in T) + 16)
+    engine = host.Engine(L, H, D, QH, 1 << 16, sum(t // 8 + 3 + steps for t in T) + 64, sum(t // 64 for t in T) + 16)
     stream = dev.Stream()
     stage = dev.DeviceBuffer(L * 2 * 400 * HD * 2)
     for i in range(lanes):
@@ -667,12 +668,6 @@ def test_engine_head_split_batch_matches_oracle(host, dev):
     query = dev.DeviceBuffer(lanes * L * QH * D * 2)
     out = dev.DeviceBuffer(lanes * L * QH * D * 2)
     qseed = seed ^ 0x5155
-    for i in range(lanes):
-        dev.fill_kv(newkv.ptr + i * L * 2 * HD * 2, L, 1, HD, seed, i, T[i], stream)
-        for l in range(L):
-            dev.fill_rows(query.ptr + (i * L + l) * QH * D * 2, QH * D, qseed, dev.synth_kv_row(i, l, 0, T[i]),
-                          QH * D, stream)
-    stream.synchronize()
     flags, _, _ = dev.decode_plan(engine.storage_handle(), [t + 1 for t in T], QH)
     assert flags & dev.DECODE_HEAD_SPLIT and (flags & ~dev.DECODE_HEAD_SPLIT) >= max(T) + 1
     lane = np.arange(lanes, dtype=np.uint64)
@@ -683,33 +678,53 @@ def test_engine_head_split_batch_matches_oracle(host, dev):
         b.values[l, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * L) + np.uint64(2 * l + 1))
         b.queries[l, :] = query.ptr + np.uint64(2 * QH * D) * (lane * np.uint64(L) + np.uint64(l))
         b.outputs[l, :] = out.ptr + np.uint64(2 * QH * D) * (lane * np.uint64(L) + np.uint64(l))
-    b.reserve(np.array(T, dtype=np.uint32))
-    assert not b.failed()
-    for l in range(L):
-        b.write(l)
-        b.attend(l)
-    b.commit()
-    assert not b.failed(), sorted(set(b.status.tolist()))
-    got = dev.download(out.ptr, (lanes, L, QH * D), np.uint16)
     worst = 0.0
-    for i in range(lanes):
-        n = T[i] + 1
+    for step in range(steps):
+        for i in range(lanes):
+            t = T[i] + step
+            dev.fill_kv(newkv.ptr + i * L * 2 * HD * 2, L, 1, HD, seed, i, t, stream)
+            for l in range(L):
+                dev.fill_rows(query.ptr + (i * L + l) * QH * D * 2, QH * D, qseed, dev.synth_kv_row(i, l, 0, t),
+                              QH * D, stream)
+        stream.synchronize()
+        b.reserve(np.array([t + step for t in T], dtype=np.uint32))
+        assert not b.failed()
         for l in range(L):
-            kv = np.empty((1, 2, n, H, D), dtype=np.uint16)
-            for c in range(2):
-                kv[0, c, :T[i]] = oracle.synth_rows(T[i] * HD, seed, oracle.kv_row(i, l, c, 0), HD).reshape(T[i], H, D)
-                kv[0, c, T[i]] = oracle.synth_rows(HD, seed, oracle.kv_row(i, l, c, T[i]), HD).reshape(H, D)
-            pages = (n + 7) // 8
-            pools = oracle.HostPools(1, H, D, pages, 1)
-            table = np.zeros(pages, dtype=oracle.DESC)
-            for k in range(pages):
-                table[k] = (k, 1, 8 * k, min(8, n - 8 * k), 8, 0)
-                pools.append_tokens(kv, n, 8 * k, 0, k, 0, min(8, n - 8 * k))
-            q = oracle.synth_rows(QH * D, qseed, oracle.kv_row(i, l, 0, T[i]), QH * D)
-            want = pools.paged_decode(table, n, 0, QH, q, 1.0 / math.sqrt(D), f32=True)
-            a = got[i, l].view(np.float16).astype(np.float32)
-            err = np.abs(a - want)
-            assert np.all(err <= 2e-3 + 1e-3 * np.abs(want)), (i, l, float(err.max()))
-            worst = max(worst, float(err.max()))
-    print(f"engine head-split batch: lanes={lanes} T=[{min(T)},{max(T)}] chunk={flags & ~dev.DECODE_HEAD_SPLIT} "
-          f"max_err={worst:.2e}", flush=True)
+            b.write(l)
+            b.attend(l)
+        b.commit()
+        assert not b.failed(), sorted(set(b.status.tolist()))
+        got = dev.download(out.ptr, (lanes, L, QH * D), np.uint16)
+        for i in range(lanes):
+            n = T[i] + step + 1
+            for l in range(L):
+                kv = np.empty((1, 2, n, H, D), dtype=np.uint16)
+                for c in range(2):
+                    kv[0, c] = oracle.synth_rows(n * HD, seed, oracle.kv_row(i, l, c, 0), HD).reshape(n, H, D)
+                pages = (n + 7) // 8
+                pools = oracle.HostPools(1, H, D, pages, 1)
+                table = np.zeros(pages, dtype=oracle.DESC)
+                for k in range(pages):
+                    table[k] = (k, 1, 8 * k, min(8, n - 8 * k), 8, 0)
+                    pools.append_tokens(kv, n, 8 * k, 0, k, 0, min(8, n - 8 * k))
+                q = oracle.synth_rows(QH * D, qseed, oracle.kv_row(i, l, 0, n - 1), QH * D)
+                want = pools.paged_decode(table, n, 0, QH, q, 1.0 / math.sqrt(D), f32=True)
+                a = got[i, l].view(np.float16).astype(np.float32)
+                err = np.abs(a - want)
+                assert np.all(err <= 2e-3 + 1e-3 * np.abs(want)), (step, i, l, float(err.max()))
+                worst = max(worst, float(err.max()))
+    assert engine.check_invariants()
+    print(f"engine lane batch: lanes={lanes} steps={steps} T=[{min(T)},{max(T)}] "
+          f"chunk={flags & ~dev.DECODE_HEAD_SPLIT} max_err={worst:.2e}", flush=True)
+
+
+def test_engine_head_split_batch_matches_oracle(host, dev):
+    _engine_lane_batch_case(host, dev)
+
+
+def test_engine_small_staging_ring(host, dev, monkeypatch):
+    """The same lanes with a 64 KiB staging ring: each reserve's ~50 KB
+    descriptor upload goes in pieces and the ring wraps several times per step
+    (items, jobs and descriptor pieces interleaved), over three steps."""
+    monkeypatch.setenv("KIMKV_STAGING_RING_BYTES", str(64 << 10))
+    _engine_lane_batch_case(host, dev, steps=3, seed=78)
