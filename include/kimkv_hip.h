@@ -194,6 +194,26 @@ kimkv_status kimkv_storage_query(const kimkv_storage* storage, kimkv_storage_inf
  * Returns NULL for an out-of-range slot. */
 uint16_t* kimkv_storage_page(const kimkv_storage* storage, uint32_t kind, uint32_t slot);
 
+/* Fault bits.  A kernel that finds one of its jobs or items invalid (layer
+ * out of range, a page that the storage does not hold, a token range past
+ * the page, a null pointer, a multi-chunk decode lane without workspace, a
+ * chunk prefix that does not cover the grid) skips it, leaving its output
+ * unwritten, and sets the matching bit in the storage's fault word. */
+#define KIMKV_FAULT_APPEND_JOB 0x1u
+#define KIMKV_FAULT_DECODE_ITEM 0x2u
+#define KIMKV_FAULT_PREFILL_ITEM 0x4u
+#define KIMKV_FAULT_PROMOTION_JOB 0x8u
+
+/* Waits for `stream`, then reads and clears (one atomic exchange, ordered
+ * on `stream` after its earlier work) the storage's fault word into *faults
+ * (may be NULL).  Returns KIMKV_INVALID_ARGUMENT when any bit was set, so a
+ * direct caller of the launch entry points checks a batch with one call.
+ * The word is shared by every stream using the storage: bits set by work on
+ * other streams are reported by whichever call reads them first.  No
+ * counterpart in the reference (its kernels skip invalid input silently,
+ * src/cuda/attention/paged_decode_kernels.cu:101-130). */
+kimkv_status kimkv_storage_faults(kimkv_storage* storage, kimkv_stream_t stream, uint32_t* faults);
+
 /* ---- data-path kernels ---------------------------------------------------- */
 
 /* Batched append of `job_count` jobs held in DEVICE memory.  `max_layer_count`

@@ -8,7 +8,8 @@
 // Fast path (head_dim 64, group <= 16, page-aligned table): per 64-token tile
 //   S^T[token][q] = K[token][:] . Q[q][:]   -> 4 x 2 MFMA 16x16x32 f16
 //   online softmax (base 2) on the 16 scores each lane holds
-//   O^T[d][q]    += V^T[d][token] . P[q][token] -> 2 x 4 MFMA 16x16x32 f16
+//   O^T[d][q]    += V^T[d][token] . P[q][token] -> 2 x 4 x 2 MFMA 16x16x32 f16
+//                   (P split into fp16 hi and lo parts: ~fp32 weights)
 // K rows and V^T rows (V is stored transposed in the page) are read with
 // 16-byte loads straight into MFMA operand registers; the token order inside
 // each 32-token k-block is permuted so that the score layout MFMA produces is
@@ -30,6 +31,11 @@ namespace {
 constexpr unsigned kBlock = 256;          // 4 waves
 constexpr unsigned kHeadsPerBlock = 4;
 constexpr unsigned kMinChunk = 256;
+// Softmax weights of the fast path are 2^(s - m + kWeightShift): the largest
+// is 2^15 (fp16 max 65504), and weights down to 2^-29 of the largest stay
+// fp16 normal numbers.  o and l carry the same factor, so it cancels in the
+// output and in every merge of partials.
+constexpr float kWeightShift = 15.0f;
 
 // ---------------------------------------------------------------------------
 // Fast path for one wave: kv head h, head_dim 64, group <= 16.
@@ -170,7 +176,14 @@ __device__ WavePartial decode_wave_d64(const GroupEntry* groups, const GroupReso
         float const alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         m_run = m_new;
 
+        // Weights p = 2^(s - m + kWeightShift) <= 2^15 go to the MFMA as two
+        // fp16 parts, p = hi + lo (hi = fp16(p), lo = fp16(p - hi)), so the
+        // products with V carry ~22 significant bits, like the fp32 weights
+        // of the reference, and the denominator sums the same p.  The shift
+        // keeps small weights in fp16's normal range; it cancels in o / l.
+        float const m_ref = m_new - kWeightShift;
         half8_t pb[2];
+        half8_t pl[2];
         float psum = 0.0f;
 #pragma unroll
         for (uint32_t kb = 0; kb < 2; ++kb) {
@@ -178,9 +191,11 @@ __device__ WavePartial decode_wave_d64(const GroupEntry* groups, const GroupReso
             for (uint32_t e = 0; e < 2; ++e) {
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i) {
-                    float const p = __builtin_amdgcn_exp2f(s[kb][e][i] - m_new);
+                    float const p = __builtin_amdgcn_exp2f(s[kb][e][i] - m_ref);
+                    _Float16 const hi = static_cast<_Float16>(p);
                     psum += p;
-                    pb[kb][4 * e + i] = static_cast<_Float16>(p);
+                    pb[kb][4 * e + i] = hi;
+                    pl[kb][4 * e + i] = static_cast<_Float16>(p - static_cast<float>(hi));
                 }
             }
         }
@@ -188,12 +203,13 @@ __device__ WavePartial decode_wave_d64(const GroupEntry* groups, const GroupReso
 #pragma unroll
         for (uint32_t db = 0; db < 4; ++db) acc[db] *= alpha;
 
-        // ---- O^T += V^T . P^T ----
+        // ---- O^T += V^T . (P_hi + P_lo)^T ----
 #pragma unroll
         for (uint32_t kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (uint32_t db = 0; db < 4; ++db) {
                 acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.v[kb][db], pb[kb], acc[db], 0, 0, 0);
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.v[kb][db], pl[kb], acc[db], 0, 0, 0);
             }
         }
     };
@@ -316,7 +332,9 @@ __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& 
             }
             float const m_new = fmaxf(m_run, wave_max(s));
             float const alpha = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
-            float const p = (page != nullptr && m_new != -INFINITY) ? exp2f(s - m_new) : 0.0f;
+            // Same weight shift as the fast path: partials of one lane may
+            // come from both paths and are merged as they are.
+            float const p = (page != nullptr && m_new != -INFINITY) ? exp2f(s - m_new + kWeightShift) : 0.0f;
             l_run = l_run * alpha + wave_sum(p);
             m_run = m_new;
 #pragma unroll
@@ -369,6 +387,16 @@ __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& 
     }
 }
 
+// The per-lane conditions decode_kernel checks before touching a lane (the
+// merge skips the same lanes, so a rejected lane's output stays unwritten).
+__device__ inline bool decode_item_valid(const PoolView& P, const kimkv_decode_item& item, uint32_t QH,
+                                         uint32_t nchunks)
+{
+    return item.token_count != 0 && item.descriptors != nullptr && item.descriptor_count != 0
+        && item.query != nullptr && item.output != nullptr && item.layer < P.layers && QH != 0
+        && QH % P.heads == 0 && P.dim <= 256 && (nchunks <= 1 || item.workspace != nullptr);
+}
+
 // Two waves per SIMD: each wave holds two 64-token steps of K/V operands in
 // registers, so a CU keeps as many bytes in flight as four single-buffered
 // waves while the compute of one step hides under the loads of the next.
@@ -418,7 +446,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         }
         __syncthreads();
         lane = s_lane;
-        if (lane == 0xFFFFFFFFu) return;
+        if (lane == 0xFFFFFFFFu) {   // the chunk prefix does not cover this workgroup
+            report_fault(P, KIMKV_FAULT_DECODE_ITEM);
+            return;
+        }
         item = items[lane];
     }
 
@@ -428,10 +459,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t const nchunks = prefix[lane + 1] - prefix[lane];
     uint32_t const T = item.token_count;
     uint32_t const c0 = chunk_index * chunk_tokens;
-    if (T == 0 || c0 >= T || item.descriptors == nullptr || item.descriptor_count == 0
-        || item.query == nullptr || item.output == nullptr || item.layer >= P.layers
-        || QH == 0 || QH % H != 0 || D > 256 || chunk_tokens > kMaxChunk
-        || (nchunks > 1 && item.workspace == nullptr)) {
+    if (!decode_item_valid(P, item, QH, nchunks) || c0 >= T || chunk_tokens > kMaxChunk) {
+        report_fault(P, KIMKV_FAULT_DECODE_ITEM);
         return;
     }
     uint32_t const c1 = min(c0 + chunk_tokens, T);
@@ -565,7 +594,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 constexpr unsigned kCombineHeads = 4;
 
 template <uint32_t kDims>
-__global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(const kimkv_decode_item* items,
+__global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(PoolView P, const kimkv_decode_item* items,
                                                                     const uint32_t* prefix, uint32_t QH, uint32_t D)
 {
     constexpr uint32_t kBatch = 64 / kDims;   // partial rows held in registers at once
@@ -576,7 +605,7 @@ __global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(const kimkv
     uint32_t const n = prefix[lane + 1] - prefix[lane];
     if (n <= 1) return;
     kimkv_decode_item const item = items[lane];
-    if (item.workspace == nullptr || item.output == nullptr) return;
+    if (!decode_item_valid(P, item, QH, n)) return;   // decode_kernel reported it
     uint64_t const stride = static_cast<uint64_t>(QH) * (D + 2);
     const float* ws = item.workspace + static_cast<uint64_t>(q) * (D + 2);
     float M = -INFINITY;
@@ -806,11 +835,14 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage, const kimkv_
         dim3 const cgrid(lane_count, (query_heads + kCombineHeads - 1) / kCombineHeads);
         uint32_t const D = storage->layout.head_dim;
         if (D <= 64) {
-            combine_kernel<1><<<cgrid, 64 * kCombineHeads, 0, s>>>(device_items, device_chunk_prefix, query_heads, D);
+            combine_kernel<1><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
+                                                                     device_chunk_prefix, query_heads, D);
         } else if (D <= 128) {
-            combine_kernel<2><<<cgrid, 64 * kCombineHeads, 0, s>>>(device_items, device_chunk_prefix, query_heads, D);
+            combine_kernel<2><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
+                                                                     device_chunk_prefix, query_heads, D);
         } else {
-            combine_kernel<4><<<cgrid, 64 * kCombineHeads, 0, s>>>(device_items, device_chunk_prefix, query_heads, D);
+            combine_kernel<4><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
+                                                                     device_chunk_prefix, query_heads, D);
         }
         return launch_status();
     }

@@ -22,6 +22,9 @@ struct kimkv_storage {
     uint64_t extent_page_elements{0};
     uint16_t* micro{nullptr};
     uint16_t* extent{nullptr};
+    uint32_t* faults{nullptr};        // device word, KIMKV_FAULT_* bits
+    uint32_t* fault_host{nullptr};    // mapped pinned word kimkv_storage_faults reads
+    uint32_t* fault_view{nullptr};    // its device address
     int device{0};
     int compute_units{0};
 };
@@ -43,13 +46,23 @@ struct PoolView {
     uint32_t layers;
     uint32_t heads;
     uint32_t dim;
+    uint32_t* faults;
 };
 
 inline PoolView pool_view(const kimkv_storage& s)
 {
     return PoolView{s.micro, s.extent, s.micro_page_elements, s.extent_page_elements,
                     s.micro_capacity, s.extent_capacity, s.micro_tokens, s.extent_tokens,
-                    s.layout.layers, s.layout.kv_heads, s.layout.head_dim};
+                    s.layout.layers, s.layout.kv_heads, s.layout.head_dim, s.faults};
+}
+
+// A workgroup that skips its job or item because the job or item is invalid
+// records why in the storage's fault word (read and cleared by
+// kimkv_storage_faults).  Called with a workgroup-uniform condition; one
+// thread writes, with a device-scope atomic.
+__device__ inline void report_fault(const PoolView& p, uint32_t bit)
+{
+    if (threadIdx.x == 0 && p.faults != nullptr) atomicOr(p.faults, bit);
 }
 
 // Page base for a (kind, slot), or nullptr when the handle does not name a page

@@ -70,14 +70,17 @@ __global__ __launch_bounds__(kBlock) void append_kernel(PoolView P, const kimkv_
     if (blockIdx.x >= job_count) return;
     kimkv_append_job const job = jobs[blockIdx.x];
     uint32_t const li = blockIdx.y;
-    if (li >= job.layer_count) return;
+    if (li >= job.layer_count) return;   // a shorter job of a launch sized for the longest
     uint32_t const layer = job.layer_begin + li;
-    if (layer >= P.layers) return;
     uint32_t const H = P.heads;
     uint32_t const D = P.dim;
     uint32_t const dcap = pool_tokens(P, job.dst_kind);
     uint16_t* dst = page_base(P, job.dst_kind, job.dst_slot, dcap);
-    if (dst == nullptr || static_cast<uint32_t>(job.dst_token) + job.token_count > dcap) return;
+    if (layer >= P.layers || dst == nullptr || static_cast<uint32_t>(job.dst_token) + job.token_count > dcap
+        || job.src_key == nullptr || job.src_value == nullptr) {
+        report_fault(P, KIMKV_FAULT_APPEND_JOB);
+        return;
+    }
     uint32_t const tid = threadIdx.x;
 
     if (job.cow_tokens != 0) {
@@ -404,14 +407,17 @@ __global__ __launch_bounds__(kBlock) void promote_kernel(PoolView P, const kimkv
     uint32_t const layer = blockIdx.y;
     uint32_t const mt = P.micro_tokens;
     uint32_t const et = P.extent_tokens;
-    if (mt * 8 != et || layer >= P.layers) return;
     uint16_t* dst = page_base(P, KIMKV_PAGE_EXTENT, job.extent_slot, et);
-    if (dst == nullptr) return;
     uint16_t const* src[8];
+    bool ok = mt * 8 == et && layer < P.layers && dst != nullptr;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         src[k] = page_base(P, KIMKV_PAGE_MICRO, job.micro_slots[k], mt);
-        if (src[k] == nullptr) return;
+        ok = ok && src[k] != nullptr;
+    }
+    if (!ok) {
+        report_fault(P, KIMKV_FAULT_PROMOTION_JOB);
+        return;
     }
     uint32_t const H = P.heads;
     uint32_t const D = P.dim;

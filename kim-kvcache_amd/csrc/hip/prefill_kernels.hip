@@ -502,6 +502,7 @@ __global__ __launch_bounds__(kBlock, 2) void prefill_kernel(PoolView P, const ki
     if (h >= H || item.new_tokens == 0 || item.new_tokens > item.token_count || item.descriptors == nullptr
         || item.descriptor_count == 0 || item.query == nullptr || item.output == nullptr || item.layer >= P.layers
         || QH == 0 || QH % H != 0 || D > 256) {
+        report_fault(P, KIMKV_FAULT_PREFILL_ITEM);
         return;
     }
     PrefillShape const shape = prefill_shape(QH, H, D);

@@ -51,6 +51,13 @@ void drain_locked(DecodeTiming& t)
 }
 }  // namespace
 
+// Moves the fault word to the mapped host word and clears it in one atomic
+// exchange, so bits set by concurrent work are never lost.
+__global__ __launch_bounds__(64) void take_faults_kernel(uint32_t* faults, uint32_t* host_word)
+{
+    if (threadIdx.x == 0) *host_word = atomicExch(faults, 0u);
+}
+
 kimkv_status record_error(hipError_t error, kimkv_status failure)
 {
     if (error == hipSuccess) {
@@ -299,11 +306,21 @@ kimkv_status kimkv_storage_create(kimkv_storage** out, kimkv_layout layout, uint
         e = hipMalloc(reinterpret_cast<void**>(&s->extent), extent_bytes);
         if (e == hipSuccess) e = hipMemset(s->extent, 0, extent_bytes);
     }
+    if (e == hipSuccess) {
+        e = hipMalloc(reinterpret_cast<void**>(&s->faults), 256);
+        if (e == hipSuccess) e = hipMemset(s->faults, 0, 256);
+    }
+    if (e == hipSuccess) {
+        e = hipHostMalloc(reinterpret_cast<void**>(&s->fault_host), 256, hipHostMallocMapped | hipHostMallocCoherent);
+        if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void**>(&s->fault_view), s->fault_host, 0);
+    }
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         record_error(e, KIMKV_ALLOCATION_FAILED);
         if (s->micro) static_cast<void>(hipFree(s->micro));
         if (s->extent) static_cast<void>(hipFree(s->extent));
+        if (s->faults) static_cast<void>(hipFree(s->faults));
+        if (s->fault_host) static_cast<void>(hipHostFree(s->fault_host));
         delete s;
         return KIMKV_ALLOCATION_FAILED;
     }
@@ -318,8 +335,30 @@ kimkv_status kimkv_storage_destroy(kimkv_storage* storage)
     static_cast<void>(hipDeviceSynchronize());
     if (storage->micro) static_cast<void>(hipFree(storage->micro));
     if (storage->extent) static_cast<void>(hipFree(storage->extent));
+    if (storage->faults) static_cast<void>(hipFree(storage->faults));
+    if (storage->fault_host) static_cast<void>(hipHostFree(storage->fault_host));
     delete storage;
     return KIMKV_OK;
+}
+
+kimkv_status kimkv_storage_faults(kimkv_storage* storage, kimkv_stream_t stream, uint32_t* faults)
+{
+    if (faults != nullptr) *faults = 0;
+    if (storage == nullptr || storage->faults == nullptr || storage->fault_view == nullptr) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    // One reader of the mapped word at a time.
+    static std::mutex mutex;
+    std::lock_guard<std::mutex> lock(mutex);
+    *reinterpret_cast<volatile uint32_t*>(storage->fault_host) = 0;
+    kimkv::take_faults_kernel<<<1, 64, 0, kimkv::native(stream)>>>(storage->faults, storage->fault_view);
+    kimkv_status const launched = kimkv::launch_status();
+    if (launched != KIMKV_OK) return launched;
+    kimkv_status const done = record_error(hipStreamSynchronize(kimkv::native(stream)), KIMKV_EXECUTION_FAILED);
+    if (done != KIMKV_OK) return done;
+    uint32_t const bits = *reinterpret_cast<volatile uint32_t*>(storage->fault_host);
+    if (faults != nullptr) *faults = bits;
+    return bits != 0 ? KIMKV_INVALID_ARGUMENT : KIMKV_OK;
 }
 
 kimkv_status kimkv_storage_query(const kimkv_storage* s, kimkv_storage_info* info)

@@ -111,6 +111,7 @@ _SIGNATURES = {
     "kimkv_storage_destroy": (ctypes.c_int, [ctypes.c_void_p]),
     "kimkv_storage_query": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(StorageInfo)]),
     "kimkv_storage_page": (ctypes.c_void_p, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32]),
+    "kimkv_storage_faults": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32)]),
     "kimkv_append_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                           ctypes.c_void_p]),
     "kimkv_gather": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
@@ -324,6 +325,12 @@ class Storage:
     def page(self, kind: int, slot: int) -> int:
         return lib().kimkv_storage_page(self.h, kind, slot) or 0
 
+    def faults(self, stream: Optional[Stream] = None) -> tuple[int, int]:
+        """kimkv_storage_faults: (status, FAULT_* bits) after waiting for `stream`; clears the word."""
+        bits = ctypes.c_uint32()
+        status = lib().kimkv_storage_faults(self.h, _sh(stream), ctypes.byref(bits))
+        return int(status), int(bits.value)
+
     def append_batch(self, jobs: np.ndarray, stream: Optional[Stream] = None) -> None:
         jobs = np.ascontiguousarray(jobs, dtype=APPEND_JOB)
         if len(jobs) == 0:
@@ -413,6 +420,12 @@ def prefill_order(kv_heads: int, head_dim: int, query_heads: int, compute_units:
 
 
 DECODE_HEAD_SPLIT = 0x80000000
+
+# Fault bits of kimkv_storage_faults (include/kimkv_hip.h).
+FAULT_APPEND_JOB = 0x1
+FAULT_DECODE_ITEM = 0x2
+FAULT_PREFILL_ITEM = 0x4
+FAULT_PROMOTION_JOB = 0x8
 
 
 def decode_plan(storage_handle: int, token_counts, query_heads: int):

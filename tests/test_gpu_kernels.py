@@ -297,6 +297,158 @@ def test_decode_unaligned_pages_generic(dev):
                  uniform_pages=True)
 
 
+def _exact_score_inputs(rng, T, H, D, G, values):
+    """Q and K with one nonzero dim (d = 0), so every score q.k * scale is exact
+    in fp32 on both sides; `values(t, h)` gives V rows [D] (float)."""
+    inp = np.zeros((1, 2, T, H, D), dtype=np.float32)
+    inp[0, 0, :, :, 0] = rng.integers(-6, 7, size=(T, H)) * 0.5        # k_t[0]
+    inp[0, 0, rng.integers(0, T), :, 0] = 8.0                            # a dominant key
+    for t in range(T):
+        for h in range(H):
+            inp[0, 1, t, h] = values(t, h)
+    q = np.zeros((H * G, D), dtype=np.float32)
+    q[:, 0] = rng.integers(1, 9, size=H * G) * 0.5                       # scores up to 8 * 4 / 8
+    return inp.astype(np.float16).view(np.uint16), q.astype(np.float16).view(np.uint16).reshape(-1)
+
+
+def _decode_fixed(dev, lanes_inputs, H, D, G, chunk=None):
+    """Decodes lanes given as (input codes [1][2][T][H][D], query codes) and returns
+    (outputs, oracle fp32 references)."""
+    QH = H * G
+    counts = [inp.shape[2] for inp, _ in lanes_inputs]
+    micro_cap = sum(t // 8 + 2 for t in counts) + 8
+    ext_cap = sum(t // 64 + 1 for t in counts) + 2
+    storage = dev.Storage(1, H, D, micro_cap, ext_cap)
+    pools = oracle.HostPools(1, H, D, micro_cap, ext_cap)
+    alloc = helpers.SlotAllocator(micro_cap, ext_cap, seed=len(counts))
+    lanes, keep = [], []
+    for inp, q in lanes_inputs:
+        T = inp.shape[2]
+        table = helpers.hetero_table(T, alloc)
+        keep.append(_populate(dev, storage, pools, table, inp))
+        lanes.append((table, T, 0, q, 0.125))
+    outs, _, _ = _run_decode(dev, storage, lanes, QH, chunk=chunk)
+    refs = [pools.paged_decode(t, T, 0, QH, q, scale, f32=True) for (t, T, _, q, scale) in lanes]
+    return outs, refs
+
+
+def test_decode_constant_value_lanes_return_value_exactly(dev):
+    """softmax weights sum to one: a lane whose V rows are all equal must return
+    that row bit-exactly, for any scores, chunking and merge path."""
+    rng = np.random.default_rng(31)
+    H, D, G = 4, 64, 8
+    rows = (rng.uniform(-4, 4, size=(H, D))).astype(np.float16).astype(np.float32)
+    lanes = []
+    for T in [1, 2, 5, 8, 9, 64, 100, 1000, 4000, 9000]:
+        lanes.append(_exact_score_inputs(rng, T, H, D, G, lambda t, h: rows[h]))
+    for chunk in [None, 1024, 2048 | dev.DECODE_HEAD_SPLIT]:
+        outs, _ = _decode_fixed(dev, lanes, H, D, G, chunk=chunk)
+        want = np.repeat(rows, G, axis=0).astype(np.float16).view(np.uint16).reshape(-1)
+        for (inp, _), got in zip(lanes, outs):
+            assert np.array_equal(got, want), (inp.shape[2], chunk, np.abs(helpers.to_f32(got) - helpers.to_f32(want)).max())
+
+
+def test_decode_near_cancelling_values_dominant_weight(dev):
+    """|v| at the generator's bound (4), V rows chosen so that the weighted sum
+    of each dim nearly cancels for one query head of the group, one dominant
+    key: the output must stay within one fp16 ulp (+1e-5) of the fp32 oracle
+    (fp16-rounded weights would be off by up to 4 * 2^-11), and within the
+    decode tolerance 2e-3 + 1e-3*|ref|."""
+    rng = np.random.default_rng(32)
+    H, D, G = 4, 64, 8
+    lanes = []
+    for trial in range(24):
+        T = 2 + trial % 7
+        inp, q = _exact_score_inputs(rng, T, H, D, G, lambda t, h: np.zeros(D))
+        k0 = helpers.to_f32(inp[0, 0, :, :, 0])                            # [T][H]
+        q0 = helpers.to_f32(q.reshape(H * G, D)[:, 0])
+        v = rng.choice([-4.0, 4.0], size=(T, H, D)) * rng.uniform(0.9, 1.0, size=(T, H, D))
+        for h in range(H):
+            s = q0[h * G] * k0[:, h] * 0.125
+            w = np.exp(s - s.max())
+            w /= w.sum()
+            last = int(np.argmin(w))
+            rest = np.delete(np.arange(T), last)
+            v[last, h] = np.clip(-(w[rest, None] * v[rest, h]).sum(0) / w[last], -4.0, 4.0)
+        vals = v.astype(np.float16).astype(np.float32)
+        inp_f = helpers.to_f32(inp).reshape(1, 2, T, H, D).copy()
+        inp_f[0, 1] = vals
+        lanes.append((inp_f.astype(np.float16).view(np.uint16), q))
+    outs, refs = _decode_fixed(dev, lanes, H, D, G)
+    worst = 0.0
+    for got, ref in zip(outs, refs):
+        helpers.assert_attention_close(got, ref)
+        g = helpers.to_f32(got)
+        ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32)
+        err = np.abs(g - ref)
+        assert np.all(err <= ulp + 1e-5), float((err - ulp).max())
+        worst = max(worst, float(err.max()))
+    print(f"near-cancelling decode: max |err| {worst:.2e}", flush=True)
+
+
+def test_invalid_items_are_reported_not_run(dev):
+    """Jobs and items the kernels reject (bad layer index, a multi-chunk lane
+    with no workspace, a slot the storage does not hold, a null output) are
+    skipped, leave their outputs untouched, and set their bit in the storage's
+    fault word, which kimkv_storage_faults returns as KIMKV_INVALID_ARGUMENT
+    and clears; valid lanes of the same launch are unaffected."""
+    L, H, D, G = 2, 4, 64, 8
+    QH = H * G
+    storage = dev.Storage(L, H, D, 64, 64)
+    pools = oracle.HostPools(L, H, D, 64, 64)
+    assert storage.faults() == (0, 0)
+    alloc = helpers.SlotAllocator(64, 64, seed=40)
+    T = 3000
+    table = helpers.hetero_table(T, alloc)
+    keep = [_populate(dev, storage, pools, table, _input(L, H, D, T, seed=41))]
+    q = oracle.synth_rows(QH * D, 42, 0, D)
+    dbuf, qbuf = dev.upload(table), dev.upload(q)
+    chunk = 1024                                    # 3 chunks per lane: split-K partials needed
+    n = (T + chunk - 1) // chunk
+    ws = dev.DeviceBuffer(dev.workspace_bytes(T, chunk, QH, D))
+    sentinel = np.full(QH * D, 0x7E00, dtype=np.uint16)              # fp16 NaN
+    outs = [dev.upload(sentinel) for _ in range(3)]
+    items = np.zeros(3, dtype=dev.DECODE_ITEM)
+    items[0] = (dbuf.ptr, len(table), T, 1, qbuf.ptr, ws.ptr, outs[0].ptr, 0.125)   # valid
+    items[1] = (dbuf.ptr, len(table), T, L, qbuf.ptr, ws.ptr, outs[1].ptr, 0.125)   # layer out of range
+    items[2] = (dbuf.ptr, len(table), T, 0, qbuf.ptr, 0, outs[2].ptr, 0.125)        # no workspace
+    prefix = np.array([0, n, 2 * n, 3 * n], dtype=np.uint32)
+    ibuf, pbuf = dev.upload(items), dev.upload(prefix)
+    storage.decode_launch(ibuf.ptr, pbuf.ptr, 3, 3 * n, chunk, QH)
+    status, bits = storage.faults()
+    assert status == 1 and bits == dev.FAULT_DECODE_ITEM, (status, bits)
+    assert storage.faults() == (0, 0)                                  # cleared
+    got = [dev.download(o.ptr, (QH * D,), np.uint16) for o in outs]
+    helpers.assert_attention_close(got[0], pools.paged_decode(table, T, 1, QH, q, 0.125, f32=True))
+    assert np.array_equal(got[1], sentinel) and np.array_equal(got[2], sentinel)
+
+    # Append: a job naming layer L and one naming a slot past the pool.
+    src = dev.upload(np.zeros(2 * H * D, dtype=np.uint16))
+    jobs = np.zeros(2, dtype=dev.APPEND_JOB)
+    jobs[0] = (src.ptr, src.ptr + 2 * H * D, 0, H * D, L, 1, 1, 5, 0, 0, 0, 0, 0)
+    jobs[1] = (src.ptr, src.ptr + 2 * H * D, 0, H * D, 0, 1, 1, 64, 0, 0, 0, 0, 0)
+    storage.append_batch(jobs)
+    assert storage.faults() == (1, dev.FAULT_APPEND_JOB)
+    # Promotion: a micro slot the storage does not hold.
+    pj = np.zeros(1, dtype=dev.PROMOTION_JOB)
+    pj[0]["micro_slots"] = [1, 2, 3, 4, 5, 6, 7, 64]
+    pj[0]["extent_slot"] = 9
+    storage.promote_batch(pj)
+    assert storage.faults() == (1, dev.FAULT_PROMOTION_JOB)
+    # The pages the rejected jobs named are unchanged.
+    assert np.array_equal(storage.gather(table, T), pools.gather(table, T))
+
+    # Prefill: an item with a null output.
+    per, pre, total = storage.prefill_plan([20], QH)
+    pq = dev.upload(oracle.synth_rows(20 * QH * D, 43, 0, D))
+    pitems = np.zeros(1, dtype=dev.PREFILL_ITEM)
+    pitems[0] = (dbuf.ptr, len(table), T, 20, 0, pq.ptr, 0, 0.125)
+    pib, ppb = dev.upload(pitems), dev.upload(pre)
+    storage.prefill_launch(pib.ptr, ppb.ptr, 1, total, QH)
+    assert storage.faults() == (1, dev.FAULT_PREFILL_ITEM)
+    del keep
+
+
 def test_fill_kv_block_matches_oracle(dev):
     """kimkv_fill_kv: [L][2][T][cols] block with rows synth_kv_row(stream, l, c, token0 + t)."""
     L, T, cols, seed, sid, t0 = 3, 37, 96, 99, 5, 1000
