@@ -273,6 +273,30 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage,
                                       uint32_t chunk_tokens, uint32_t query_heads,
                                       kimkv_stream_t stream);
 
+/* Size of the device scratch array of kimkv_paged_decode_batch_noalloc. */
+#define KIMKV_DECODE_SCRATCH_BYTES (16u << 20)
+
+/* kimkv_paged_decode_batch for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, kernels and
+ * results; the items' `workspace` pointers are ignored: split-K partials go
+ * to a file-scope device array of KIMKV_DECODE_SCRATCH_BYTES bytes (one per
+ * device, held until the process ends), which a batch needs only when some
+ * lane has several chunks, then total_chunks * query_heads * (head_dim + 2)
+ * * 4 bytes of it (16 MiB = 1985 chunks at 32 query heads x 64 dims).
+ * KIMKV_INVALID_ARGUMENT for a larger batch or when the storage's device is
+ * not the current device; nothing is launched then.  Calls no allocating
+ * routine.  Every call on a device shares its array, so calls that overlap
+ * on one device (different streams, or threads) race: serialize them.  The
+ * array keeps the last call's partials; nothing in it needs clearing (every
+ * chunk writes its whole partial before the merge reads it). */
+kimkv_status kimkv_paged_decode_batch_noalloc(const kimkv_storage* storage,
+                                              const kimkv_decode_item* device_items,
+                                              const uint32_t* device_chunk_prefix,
+                                              uint32_t lane_count, uint32_t total_chunks,
+                                              uint32_t chunk_tokens, uint32_t query_heads,
+                                              kimkv_stream_t stream);
+
 /* New tokens handled by one prefill workgroup (per KV head) for this
  * storage's shape and query head count: items need
  * ceil(new_tokens / this) workgroups each.  0 for an invalid head count. */

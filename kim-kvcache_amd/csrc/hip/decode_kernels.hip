@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 #include "attention_common.h"
@@ -278,7 +279,7 @@ __device__ inline void store_partial(const kimkv_decode_item& item, uint32_t QH,
 // Generic path for one wave: any head_dim <= 256, any group size, any table.
 // One query head at a time; lanes own tokens for scores and dims for output.
 // ---------------------------------------------------------------------------
-struct WaveScratch {
+struct WaveTokens {
     float p[64];
     const uint16_t* head[64];   // (layer, head) block of the token's page
     uint32_t cap[64];
@@ -287,7 +288,7 @@ struct WaveScratch {
 
 __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& item, uint32_t h,
                                     uint32_t G, uint32_t QH, uint32_t c0, uint32_t c1,
-                                    uint32_t chunk_index, bool single_chunk, WaveScratch* scratch)
+                                    uint32_t chunk_index, bool single_chunk, WaveTokens* tokens)
 {
     uint32_t const lane = threadIdx.x & 63u;
     uint32_t const D = P.dim;
@@ -339,19 +340,19 @@ __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& 
             m_run = m_new;
 #pragma unroll
             for (int k = 0; k < 4; ++k) o[k] *= alpha;
-            scratch->p[lane] = p;
-            scratch->head[lane] = hb;
-            scratch->cap[lane] = cap;
-            scratch->pt[lane] = pt;
+            tokens->p[lane] = p;
+            tokens->head[lane] = hb;
+            tokens->cap[lane] = cap;
+            tokens->pt[lane] = pt;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             uint32_t const nt = min(64u, c1 - t0);
             for (uint32_t tt = 0; tt < nt; ++tt) {
-                float const pp = scratch->p[tt];
-                const uint16_t* vb = scratch->head[tt];
-                uint32_t const vc = scratch->cap[tt];
-                uint32_t const vp = scratch->pt[tt];
+                float const pp = tokens->p[tt];
+                const uint16_t* vb = tokens->head[tt];
+                uint32_t const vc = tokens->cap[tt];
+                uint32_t const vp = tokens->pt[tt];
                 if (vb == nullptr || pp == 0.0f) continue;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
@@ -407,13 +408,16 @@ __device__ inline bool decode_item_valid(const PoolView& P, const kimkv_decode_i
 //   cut into four 64-token-aligned quarters, one per wave, and the four
 //   online-softmax states are merged through LDS, so a lane that fits one
 //   chunk writes its output directly and needs no combine launch.
+//
+// partials: when non-null, split-K partials of global chunk c go to
+// partials + c * QH * (D + 2) instead of the lanes' own workspaces.
 template <bool kSplit>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
     PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t chunk_tokens,
-    uint32_t QH)
+    uint32_t QH, float* partials)
 {
     __shared__ __attribute__((aligned(16))) GroupEntry groups[kMaxGroups];   // also the merge buffer
-    __shared__ WaveScratch scratch[kHeadsPerBlock];
+    __shared__ WaveTokens wave_tokens[kHeadsPerBlock];
     __shared__ uint32_t s_lane;
     __shared__ uint32_t s_hit;
     __shared__ uint32_t s_idx0;
@@ -455,8 +459,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
     uint32_t const H = P.heads;
     uint32_t const D = P.dim;
-    uint32_t const chunk_index = chunk_id - prefix[lane];
-    uint32_t const nchunks = prefix[lane + 1] - prefix[lane];
+    uint32_t const lane_first = prefix[lane];
+    uint32_t const chunk_index = chunk_id - lane_first;
+    uint32_t const nchunks = prefix[lane + 1] - lane_first;
+    if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(lane_first) * QH * (D + 2);
     uint32_t const T = item.token_count;
     uint32_t const c0 = chunk_index * chunk_tokens;
     if (!decode_item_valid(P, item, QH, nchunks) || c0 >= T || chunk_tokens > kMaxChunk) {
@@ -514,7 +520,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         uint32_t const h = blockIdx.y * kHeadsPerBlock + wave;
         if (h >= H) return;
         if (!fast) {
-            decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &scratch[wave]);
+            decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &wave_tokens[wave]);
             return;
         }
         WavePartial const w = decode_wave_d64(groups, GroupResolver(P, item.layer, h), item, h, G, c0, c0, c1);
@@ -532,7 +538,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t const h = blockIdx.y;
     if (h >= H) return;
     if (!fast) {
-        if (wave == 0) decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &scratch[0]);
+        if (wave == 0) decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &wave_tokens[0]);
         return;
     }
     uint32_t const quarter = ((c1 - c0 + 3) / 4 + 63) / 64 * 64;
@@ -595,7 +601,8 @@ constexpr unsigned kCombineHeads = 4;
 
 template <uint32_t kDims>
 __global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(PoolView P, const kimkv_decode_item* items,
-                                                                    const uint32_t* prefix, uint32_t QH, uint32_t D)
+                                                                    const uint32_t* prefix, uint32_t QH, uint32_t D,
+                                                                    float* partials)
 {
     constexpr uint32_t kBatch = 64 / kDims;   // partial rows held in registers at once
     uint32_t const lane = blockIdx.x;
@@ -604,7 +611,8 @@ __global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(PoolView P,
     if (q >= QH) return;
     uint32_t const n = prefix[lane + 1] - prefix[lane];
     if (n <= 1) return;
-    kimkv_decode_item const item = items[lane];
+    kimkv_decode_item item = items[lane];
+    if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(prefix[lane]) * QH * (D + 2);
     if (!decode_item_valid(P, item, QH, n)) return;   // decode_kernel reported it
     uint64_t const stride = static_cast<uint64_t>(QH) * (D + 2);
     const float* ws = item.workspace + static_cast<uint64_t>(q) * (D + 2);
@@ -664,7 +672,7 @@ __global__ __launch_bounds__(64) void reference_attention_kernel(PoolView P, con
                                                                  uint32_t count, uint32_t T, const float* query,
                                                                  float* output)
 {
-    __shared__ WaveScratch scratch;
+    __shared__ WaveTokens tokens;
     uint32_t const h = blockIdx.x;
     uint32_t const layer = blockIdx.y;
     uint32_t const lane = threadIdx.x;
@@ -705,17 +713,17 @@ __global__ __launch_bounds__(64) void reference_attention_kernel(PoolView P, con
         m_run = m_new;
 #pragma unroll
         for (int k = 0; k < 4; ++k) o[k] *= alpha;
-        scratch.p[lane] = p;
-        scratch.head[lane] = hb;
-        scratch.cap[lane] = cap;
-        scratch.pt[lane] = pt;
+        tokens.p[lane] = p;
+        tokens.head[lane] = hb;
+        tokens.cap[lane] = cap;
+        tokens.pt[lane] = pt;
         __syncthreads();
         uint32_t const nt = min(64u, T - t0);
         for (uint32_t tt = 0; tt < nt; ++tt) {
-            float const pp = scratch.p[tt];
-            const uint16_t* vb = scratch.head[tt];
-            uint32_t const vc = scratch.cap[tt];
-            uint32_t const vp = scratch.pt[tt];
+            float const pp = tokens.p[tt];
+            const uint16_t* vb = tokens.head[tt];
+            uint32_t const vc = tokens.cap[tt];
+            uint32_t const vp = tokens.pt[tt];
             if (vb == nullptr || pp == 0.0f) continue;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -731,6 +739,91 @@ __global__ __launch_bounds__(64) void reference_attention_kernel(PoolView P, con
         uint32_t const d = lane + 64u * k;
         if (d < D) output[(static_cast<uint64_t>(layer) * P.heads + h) * D + d] = o[k] * inv;
     }
+}
+
+// Decode launch (+ split-K merge) shared by both entry points.  `partials`
+// replaces the lanes' workspaces when non-null; `timed` lets the benchmark's
+// event timing see the launch (its events are created on demand).
+kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item* device_items,
+                           const uint32_t* device_chunk_prefix, uint32_t lane_count, uint32_t total_chunks,
+                           uint32_t chunk_flags, uint32_t query_heads, kimkv_stream_t stream, float* partials,
+                           bool timed)
+{
+    bool const head_split = (chunk_flags & KIMKV_DECODE_HEAD_SPLIT) != 0;
+    uint32_t const chunk_tokens = chunk_flags & ~KIMKV_DECODE_HEAD_SPLIT;
+    if (storage == nullptr || device_items == nullptr || device_chunk_prefix == nullptr || lane_count == 0
+        || query_heads == 0 || query_heads % storage->layout.kv_heads != 0 || chunk_tokens == 0
+        || chunk_tokens % 64 != 0 || chunk_tokens > kMaxChunk || storage->layout.head_dim > 256) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    if (total_chunks == 0) return KIMKV_OK;
+    hipStream_t const s = native(stream);
+    uint32_t const H = storage->layout.kv_heads;
+    dim3 const grid(total_chunks, head_split ? H : (H + kHeadsPerBlock - 1) / kHeadsPerBlock);
+    void* start = nullptr;
+    if (timed) kernel_timing_begin(TimedKernel::Decode, s, &start);
+    if (head_split) {
+        decode_kernel<true><<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
+                                                    lane_count, chunk_tokens, query_heads, partials);
+    } else {
+        decode_kernel<false><<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
+                                                     lane_count, chunk_tokens, query_heads, partials);
+    }
+    if (timed) kernel_timing_end(TimedKernel::Decode, s, start);
+    kimkv_status const status = launch_status();
+    if (status != KIMKV_OK) return status;
+    if (total_chunks > lane_count) {
+        dim3 const cgrid(lane_count, (query_heads + kCombineHeads - 1) / kCombineHeads);
+        uint32_t const D = storage->layout.head_dim;
+        if (D <= 64) {
+            combine_kernel<1><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
+                                                                     device_chunk_prefix, query_heads, D,
+                                                                     partials);
+        } else if (D <= 128) {
+            combine_kernel<2><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
+                                                                     device_chunk_prefix, query_heads, D,
+                                                                     partials);
+        } else {
+            combine_kernel<4><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
+                                                                     device_chunk_prefix, query_heads, D,
+                                                                     partials);
+        }
+        return launch_status();
+    }
+    return KIMKV_OK;
+}
+
+// ---- allocation-free decode: split-K partials in a file-scope array ----------
+// One copy per device, held until the process ends.  Host code never passes
+// the array's name to a kernel (on the host it is a stand-in, not a device
+// address): decode_scratch resolves the device address once per device with
+// hipGetSymbolAddress and every launch uses that.
+__device__ __align__(256) float scratch[KIMKV_DECODE_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the storage's device, which must be the
+// current device (the launch runs there).
+kimkv_status decode_scratch(const kimkv_storage* storage, float** out)
+{
+    *out = nullptr;
+    int device = -1;
+    kimkv_status const got = record_error(hipGetDevice(&device), KIMKV_RUNTIME_UNAVAILABLE);
+    if (got != KIMKV_OK) return got;
+    if (device != storage->device || device < 0 || device >= kMaxScratchDevices) return KIMKV_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* ptr = nullptr;
+        kimkv_status const resolved =
+            record_error(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), KIMKV_RUNTIME_UNAVAILABLE);
+        if (resolved != KIMKV_OK) return resolved;
+        if (ptr == nullptr) return KIMKV_RUNTIME_UNAVAILABLE;
+        g_scratch_ptr[device] = static_cast<float*>(ptr);
+    }
+    *out = g_scratch_ptr[device];
+    return KIMKV_OK;
 }
 
 }  // namespace
@@ -808,45 +901,25 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage, const kimkv_
                                       uint32_t total_chunks, uint32_t chunk_flags, uint32_t query_heads,
                                       kimkv_stream_t stream)
 {
-    bool const head_split = (chunk_flags & KIMKV_DECODE_HEAD_SPLIT) != 0;
-    uint32_t const chunk_tokens = chunk_flags & ~KIMKV_DECODE_HEAD_SPLIT;
-    if (storage == nullptr || device_items == nullptr || device_chunk_prefix == nullptr || lane_count == 0
-        || query_heads == 0 || query_heads % storage->layout.kv_heads != 0 || chunk_tokens == 0
-        || chunk_tokens % 64 != 0 || chunk_tokens > kMaxChunk || storage->layout.head_dim > 256) {
-        return KIMKV_INVALID_ARGUMENT;
-    }
-    if (total_chunks == 0) return KIMKV_OK;
-    hipStream_t const s = native(stream);
-    uint32_t const H = storage->layout.kv_heads;
-    dim3 const grid(total_chunks, head_split ? H : (H + kHeadsPerBlock - 1) / kHeadsPerBlock);
-    void* start = nullptr;
-    kernel_timing_begin(TimedKernel::Decode, s, &start);
-    if (head_split) {
-        decode_kernel<true><<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
-                                                    lane_count, chunk_tokens, query_heads);
-    } else {
-        decode_kernel<false><<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
-                                                     lane_count, chunk_tokens, query_heads);
-    }
-    kernel_timing_end(TimedKernel::Decode, s, start);
-    kimkv_status const status = launch_status();
-    if (status != KIMKV_OK) return status;
-    if (total_chunks > lane_count) {
-        dim3 const cgrid(lane_count, (query_heads + kCombineHeads - 1) / kCombineHeads);
-        uint32_t const D = storage->layout.head_dim;
-        if (D <= 64) {
-            combine_kernel<1><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
-                                                                     device_chunk_prefix, query_heads, D);
-        } else if (D <= 128) {
-            combine_kernel<2><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
-                                                                     device_chunk_prefix, query_heads, D);
-        } else {
-            combine_kernel<4><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
-                                                                     device_chunk_prefix, query_heads, D);
-        }
-        return launch_status();
-    }
-    return KIMKV_OK;
+    return kimkv::launch_decode(storage, device_items, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
+                                query_heads, stream, nullptr, true);
+}
+
+kimkv_status kimkv_paged_decode_batch_noalloc(const kimkv_storage* storage, const kimkv_decode_item* device_items,
+                                              const uint32_t* device_chunk_prefix, uint32_t lane_count,
+                                              uint32_t total_chunks, uint32_t chunk_flags, uint32_t query_heads,
+                                              kimkv_stream_t stream)
+{
+    if (storage == nullptr || query_heads == 0) return KIMKV_INVALID_ARGUMENT;
+    // Partials are needed only when some lane has several chunks.
+    uint64_t const need = static_cast<uint64_t>(total_chunks) * query_heads * (storage->layout.head_dim + 2)
+        * sizeof(float);
+    if (total_chunks > lane_count && need > KIMKV_DECODE_SCRATCH_BYTES) return KIMKV_INVALID_ARGUMENT;
+    float* partials = nullptr;
+    kimkv_status const resolved = kimkv::decode_scratch(storage, &partials);
+    if (resolved != KIMKV_OK) return resolved;
+    return kimkv::launch_decode(storage, device_items, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
+                                query_heads, stream, partials, false);
 }
 
 kimkv_status kimkv_reference_attention(const kimkv_storage* storage, const kimkv_block_desc* device_descriptors,

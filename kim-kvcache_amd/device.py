@@ -125,6 +125,9 @@ _SIGNATURES = {
     "kimkv_paged_decode_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                 ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                 ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_paged_decode_batch_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                        ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                                        ctypes.c_uint32, ctypes.c_void_p]),
     "kimkv_prefill_tokens_per_block": (ctypes.c_uint32, [ctypes.c_void_p, ctypes.c_uint32]),
     "kimkv_paged_prefill_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
                                                  ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]),
