@@ -81,33 +81,55 @@ def apply_rope(v: np.ndarray, heads: int, dim: int, position: int, theta: float)
 
 
 class ReferenceModel:
-    """Token-at-a-time forward with its own KV history (positions in order)."""
+    """Token-at-a-time forward with its own KV history (positions in order).
+    `threads` > 1 generates the weight tensors concurrently (the generator and
+    codec are C calls that release the GIL; every tensor is a pure function of
+    the seed and its rows, so the weights are the same)."""
 
-    def __init__(self, cfg: ModelConfig, seed: int):
+    def __init__(self, cfg: ModelConfig, seed: int, threads: int = 1):
         self.cfg = cfg
         H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocabulary_size
         QD = cfg.attention_head_count * cfg.head_dimension
         KD = cfg.kv_head_count * cfg.head_dimension
-        self.layers = []
-        for l in range(cfg.layer_count):
-            self.layers.append({
-                "q": seeded_weight(seed, QD, H, weight_row(l, "q")),
-                "k": seeded_weight(seed, KD, H, weight_row(l, "k")),
-                "v": seeded_weight(seed, KD, H, weight_row(l, "v")),
-                "o": seeded_weight(seed, H, H, weight_row(l, "o")),
-                "gate": seeded_weight(seed, I, H, weight_row(l, "gate")),
-                "up": seeded_weight(seed, I, H, weight_row(l, "up")),
-                "down": seeded_weight(seed, H, I, weight_row(l, "down")),
-                "ln1": np.ones(H, dtype=np.float32),
-                "ln2": np.ones(H, dtype=np.float32),
-            })
         L = cfg.layer_count
-        self.embed = seeded_weight(seed, V, H, weight_row(L, "embed"))
-        self.head = seeded_weight(seed, V, H, weight_row(L, "head"))
+        shapes = {"q": (QD, H), "k": (KD, H), "v": (KD, H), "o": (H, H), "gate": (I, H), "up": (I, H),
+                  "down": (H, I)}
+        jobs = [(l, kind, rows, cols) for l in range(L) for kind, (rows, cols) in shapes.items()]
+        jobs += [(L, "embed", V, H), (L, "head", V, H)]
+
+        def make(job):
+            l, kind, rows, cols = job
+            return seeded_weight(seed, rows, cols, weight_row(l, kind))
+
+        if threads > 1:
+            from concurrent.futures import ThreadPoolExecutor
+            with ThreadPoolExecutor(max_workers=threads) as pool:
+                made = list(pool.map(make, jobs))
+        else:
+            made = [make(j) for j in jobs]
+        tensors = {(j[0], j[1]): w for j, w in zip(jobs, made)}
+        self.layers = []
+        for l in range(L):
+            layer = {kind: tensors[(l, kind)] for kind in shapes}
+            layer["ln1"] = np.ones(H, dtype=np.float32)
+            layer["ln2"] = np.ones(H, dtype=np.float32)
+            self.layers.append(layer)
+        self.embed = tensors[(L, "embed")]
+        self.head = tensors[(L, "head")]
         self.final_norm = np.ones(H, dtype=np.float32)
         self.keys = [[] for _ in range(L)]
         self.values = [[] for _ in range(L)]
         self.final_hidden = None
+
+    def fresh(self) -> "ReferenceModel":
+        """Another request on the same weights: shares them, empty KV history."""
+        other = object.__new__(ReferenceModel)
+        other.__dict__.update(self.__dict__)
+        L = self.cfg.layer_count
+        other.keys = [[] for _ in range(L)]
+        other.values = [[] for _ in range(L)]
+        other.final_hidden = None
+        return other
 
     def forward(self, token: int, position: int) -> np.ndarray:
         cfg = self.cfg

@@ -95,3 +95,15 @@ def test_wrong_structure_is_detected():
     got = [ref.forward(tk, p) for p, tk in enumerate(tokens)]
     err = max(float(np.max(np.abs(g - w))) for g, w in zip(got, want))
     assert err > 0.05 * float(np.abs(want).max())
+
+
+def test_threaded_weight_generation_is_identical():
+    cfg = om.ModelConfig(hidden_size=64, intermediate_size=96, layer_count=3, attention_head_count=4,
+                         kv_head_count=2, head_dimension=16, vocabulary_size=100, max_position_embeddings=64)
+    a, b = om.ReferenceModel(cfg, 11), om.ReferenceModel(cfg, 11, threads=4)
+    for la, lb in zip(a.layers, b.layers):
+        for k in la:
+            assert np.array_equal(la[k], lb[k]), k
+    assert np.array_equal(a.embed, b.embed) and np.array_equal(a.head, b.head)
+    c = b.fresh()
+    assert np.array_equal(b.forward(5, 0), c.forward(5, 0)) and len(b.keys[0]) == 1 and len(c.keys[0]) == 1
