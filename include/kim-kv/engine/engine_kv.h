@@ -266,10 +266,18 @@ public:
     [[nodiscard]] EngineKvStatus rollback() noexcept;
 
 private:
+    // The two per-layer steps of a token.
+    enum class Step : std::uint8_t { Write, Attend };
+
     [[nodiscard]] bool active() const noexcept;
+    // Whether `step` for `layer` may be submitted now, as the status the call
+    // returns (InvalidState, LayerOutOfOrder, InvalidArgument in that order).
+    [[nodiscard]] EngineKvStatus admit(Step step, std::uint32_t layer, bool arguments_ok) const noexcept;
+    // Applies a submitted step's outcome: Failed, or the next phase.
+    void settle(Step step, EngineKvStatus const& outcome) noexcept;
+    void end(TokenTransactionPhase final_phase) noexcept;
     void rollbackNoexcept() noexcept;
-    void resetMovedFrom() noexcept;
-    void advanceAfterAttend() noexcept;
+    void adopt(TokenTransaction& other) noexcept;
 
     std::unique_ptr<TokenTransactionBackend> backend_{};
     TokenTransactionId transaction_id_{kInvalidTokenTransactionId};
@@ -281,8 +289,7 @@ private:
     EngineStream stream_{nullptr};
 
     friend class TokenTransactionBackend;
-    friend void attendLayerBatch(PagedDecodeBatch& batch);
-    friend void writeLayerBatch(LayerKvWriteBatch& batch);
+    friend struct TokenBatchRunner;
 };
 
 // Validates every lane against its transaction's state machine, dispatches

@@ -1,7 +1,23 @@
-// TokenTransaction state machine and the ragged batch entry points
-// (semantics of src/engine/engine_kv.cpp:9-318 in the reference: argument
-// errors never submit, a failed call moves the token to Failed, commit is the
-// only completion point, and batch lanes succeed or fail independently).
+// TokenTransaction: the per-token state machine of the engine SPI, and the
+// ragged batch entry points over it.
+//
+// Contract (include/kim-kv/engine/engine_kv.h; reference semantics in
+// src/engine/engine_kv.cpp:9-318): a token advances layer by layer, write
+// then attend; a call that is not admitted returns its error and submits
+// nothing; a submitted step that fails leaves the token Failed (only
+// rollback remains); commit is the single completion point; an abandoned
+// token rolls back.  Batch lanes are admitted one by one, the first admitted
+// lane's backend submits the whole batch once, and each lane settles on its
+// own status.
+//
+// The phase table this file implements:
+//
+//   phase                   admitted step      success ->                        failure ->
+//   AwaitingLayerWrite      Write(next_layer)  AwaitingLayerAttention            Failed
+//   AwaitingLayerAttention  Attend(next_layer) AwaitingLayerWrite of next layer, Failed
+//                                              or ReadyToCommit after the last
+//   ReadyToCommit           commit             Committed                         RolledBack
+//   any live phase          rollback           RolledBack
 #include "kim-kv/engine/engine_kv.h"
 
 #include <utility>
@@ -9,184 +25,214 @@
 namespace kimkvcache {
 namespace {
 
-constexpr EngineKvStatus status(EngineKvError e) noexcept { return EngineKvStatus{e}; }
+constexpr EngineKvStatus fail(EngineKvError e) noexcept { return EngineKvStatus{e}; }
 
-bool decodeArgumentsValid(PagedDecodeRequest const& r) noexcept
+constexpr bool live(TokenTransactionPhase p) noexcept
+{
+    return p == TokenTransactionPhase::AwaitingLayerWrite || p == TokenTransactionPhase::AwaitingLayerAttention
+        || p == TokenTransactionPhase::ReadyToCommit || p == TokenTransactionPhase::Failed;
+}
+
+bool writeArgumentsOk(LayerKvWrite const& w) noexcept { return w.device_key != nullptr && w.device_value != nullptr; }
+
+bool attendArgumentsOk(PagedDecodeRequest const& r) noexcept
 {
     return r.device_query != nullptr && r.device_output != nullptr && r.device_workspace != nullptr
         && r.workspace_bytes != 0 && r.attention_scale > 0.0F;
 }
 
+// Per-item access for the two batch kinds.
+std::uint32_t layerOf(PagedDecodeBatchItem const& item) noexcept { return item.request.layer; }
+std::uint32_t layerOf(LayerKvWriteBatchItem const& item) noexcept { return item.write.layer; }
+bool argumentsOk(PagedDecodeBatchItem const& item) noexcept { return attendArgumentsOk(item.request); }
+bool argumentsOk(LayerKvWriteBatchItem const& item) noexcept { return writeArgumentsOk(item.write); }
+
 }  // namespace
 
-TokenTransactionBackend* TokenTransactionBackend::batchBackend(PagedDecodeBatchItem const& item) noexcept
+// ---- TokenTransactionBackend defaults ---------------------------------------------------------------------
+
+namespace {
+
+// Runs `one(backend, item, stream)` for every item that is still ok.
+template <typename Item, typename One>
+void eachLane(Item* items, std::size_t count, One one)
 {
-    return item.transaction != nullptr ? item.transaction->backend_.get() : nullptr;
+    for (std::size_t i = 0; i < count; ++i) {
+        Item& item = items[i];
+        if (!item.status.ok()) continue;
+        TokenTransactionBackend* b = item.transaction != nullptr ? one.backendOf(item) : nullptr;
+        item.status = b == nullptr ? fail(EngineKvError::InvalidState) : one(*b, item);
+    }
 }
 
-EngineStream TokenTransactionBackend::batchStream(PagedDecodeBatchItem const& item) noexcept
-{
-    return item.transaction != nullptr ? item.transaction->stream_ : nullptr;
-}
-
-TokenTransactionBackend* TokenTransactionBackend::batchBackend(LayerKvWriteBatchItem const& item) noexcept
-{
-    return item.transaction != nullptr ? item.transaction->backend_.get() : nullptr;
-}
-
-EngineStream TokenTransactionBackend::batchStream(LayerKvWriteBatchItem const& item) noexcept
-{
-    return item.transaction != nullptr ? item.transaction->stream_ : nullptr;
-}
+}  // namespace
 
 void TokenTransactionBackend::attendLayerBatch(PagedDecodeBatch& batch)
 {
-    for (std::size_t i = 0; i < batch.item_count; ++i) {
-        PagedDecodeBatchItem& item = batch.items[i];
-        if (!item.status.ok()) continue;
-        TokenTransactionBackend* b = batchBackend(item);
-        item.status = b == nullptr ? status(EngineKvError::InvalidState) : b->attendLayer(item.request, batchStream(item));
-    }
+    struct One {
+        TokenTransactionBackend* backendOf(PagedDecodeBatchItem const& i) const noexcept { return batchBackend(i); }
+        EngineKvStatus operator()(TokenTransactionBackend& b, PagedDecodeBatchItem const& i) const
+        {
+            return b.attendLayer(i.request, batchStream(i));
+        }
+    };
+    eachLane(batch.items, batch.item_count, One{});
 }
 
 void TokenTransactionBackend::writeLayerBatch(LayerKvWriteBatch& batch)
 {
-    for (std::size_t i = 0; i < batch.item_count; ++i) {
-        LayerKvWriteBatchItem& item = batch.items[i];
-        if (!item.status.ok()) continue;
-        TokenTransactionBackend* b = batchBackend(item);
-        item.status = b == nullptr ? status(EngineKvError::InvalidState) : b->writeLayer(item.write, batchStream(item));
-    }
+    struct One {
+        TokenTransactionBackend* backendOf(LayerKvWriteBatchItem const& i) const noexcept { return batchBackend(i); }
+        EngineKvStatus operator()(TokenTransactionBackend& b, LayerKvWriteBatchItem const& i) const
+        {
+            return b.writeLayer(i.write, batchStream(i));
+        }
+    };
+    eachLane(batch.items, batch.item_count, One{});
 }
+
+TokenTransactionBackend* TokenTransactionBackend::batchBackend(PagedDecodeBatchItem const& item) noexcept
+{
+    return item.transaction == nullptr ? nullptr : item.transaction->backend_.get();
+}
+
+EngineStream TokenTransactionBackend::batchStream(PagedDecodeBatchItem const& item) noexcept
+{
+    return item.transaction == nullptr ? nullptr : item.transaction->stream_;
+}
+
+TokenTransactionBackend* TokenTransactionBackend::batchBackend(LayerKvWriteBatchItem const& item) noexcept
+{
+    return item.transaction == nullptr ? nullptr : item.transaction->backend_.get();
+}
+
+EngineStream TokenTransactionBackend::batchStream(LayerKvWriteBatchItem const& item) noexcept
+{
+    return item.transaction == nullptr ? nullptr : item.transaction->stream_;
+}
+
+// ---- TokenTransaction -------------------------------------------------------------------------------------
 
 TokenTransaction::TokenTransaction(std::unique_ptr<TokenTransactionBackend> backend, TokenTransactionId transaction_id,
                                    RequestId request_id, std::uint32_t logical_token_position,
                                    std::uint32_t layer_count, EngineStream stream) noexcept
-    : backend_(std::move(backend)),
-      transaction_id_(transaction_id),
-      request_id_(request_id),
-      logical_token_position_(logical_token_position),
-      layer_count_(layer_count),
-      phase_(TokenTransactionPhase::AwaitingLayerWrite),
-      stream_(stream)
 {
-    if (backend_ == nullptr || transaction_id_ == kInvalidTokenTransactionId || request_id_ == kInvalidRequestId
-        || layer_count_ == 0) {
-        if (backend_ != nullptr) backend_->rollback(stream_);
-        backend_.reset();
-        resetMovedFrom();
+    bool const usable = backend != nullptr && transaction_id != kInvalidTokenTransactionId
+        && request_id != kInvalidRequestId && layer_count != 0;
+    if (!usable) {
+        // A backend handed over with unusable identifiers is released at once.
+        if (backend != nullptr) backend->rollback(stream);
+        return;
     }
+    backend_ = std::move(backend);
+    transaction_id_ = transaction_id;
+    request_id_ = request_id;
+    logical_token_position_ = logical_token_position;
+    layer_count_ = layer_count;
+    stream_ = stream;
+    phase_ = TokenTransactionPhase::AwaitingLayerWrite;
 }
 
 TokenTransaction::~TokenTransaction() { rollbackNoexcept(); }
 
-TokenTransaction::TokenTransaction(TokenTransaction&& other) noexcept
-    : backend_(std::move(other.backend_)),
-      transaction_id_(other.transaction_id_),
-      request_id_(other.request_id_),
-      logical_token_position_(other.logical_token_position_),
-      layer_count_(other.layer_count_),
-      next_layer_(other.next_layer_),
-      phase_(other.phase_),
-      stream_(other.stream_)
-{
-    other.resetMovedFrom();
-}
+TokenTransaction::TokenTransaction(TokenTransaction&& other) noexcept { adopt(other); }
 
 TokenTransaction& TokenTransaction::operator=(TokenTransaction&& other) noexcept
 {
-    if (this == &other) return *this;
-    rollbackNoexcept();
-    backend_ = std::move(other.backend_);
-    transaction_id_ = other.transaction_id_;
-    request_id_ = other.request_id_;
-    logical_token_position_ = other.logical_token_position_;
-    layer_count_ = other.layer_count_;
-    next_layer_ = other.next_layer_;
-    phase_ = other.phase_;
-    stream_ = other.stream_;
-    other.resetMovedFrom();
+    if (this != &other) {
+        rollbackNoexcept();   // an uncommitted token being replaced rolls back
+        adopt(other);
+    }
     return *this;
 }
 
-bool TokenTransaction::active() const noexcept
+void TokenTransaction::adopt(TokenTransaction& other) noexcept
 {
-    switch (phase_) {
-    case TokenTransactionPhase::AwaitingLayerWrite:
-    case TokenTransactionPhase::AwaitingLayerAttention:
-    case TokenTransactionPhase::ReadyToCommit:
-    case TokenTransactionPhase::Failed:
-        return backend_ != nullptr;
-    default:
-        return false;
-    }
+    backend_ = std::move(other.backend_);
+    transaction_id_ = std::exchange(other.transaction_id_, kInvalidTokenTransactionId);
+    request_id_ = std::exchange(other.request_id_, kInvalidRequestId);
+    logical_token_position_ = std::exchange(other.logical_token_position_, 0u);
+    layer_count_ = std::exchange(other.layer_count_, 0u);
+    next_layer_ = std::exchange(other.next_layer_, 0u);
+    phase_ = std::exchange(other.phase_, TokenTransactionPhase::Empty);
+    stream_ = std::exchange(other.stream_, nullptr);
 }
+
+bool TokenTransaction::active() const noexcept { return backend_ != nullptr && live(phase_); }
 
 bool TokenTransaction::valid() const noexcept { return active(); }
 
 TokenTransactionSnapshot TokenTransaction::snapshot() const noexcept
 {
-    return TokenTransactionSnapshot{transaction_id_, request_id_, logical_token_position_, layer_count_, next_layer_,
-                                    phase_};
+    TokenTransactionSnapshot s;
+    s.transaction_id = transaction_id_;
+    s.request_id = request_id_;
+    s.logical_token_position = logical_token_position_;
+    s.layer_count = layer_count_;
+    s.next_layer = next_layer_;
+    s.phase = phase_;
+    return s;
+}
+
+EngineKvStatus TokenTransaction::admit(Step step, std::uint32_t layer, bool arguments_ok) const noexcept
+{
+    if (!active()) return fail(EngineKvError::InvalidState);
+    TokenTransactionPhase const expected =
+        step == Step::Write ? TokenTransactionPhase::AwaitingLayerWrite : TokenTransactionPhase::AwaitingLayerAttention;
+    if (phase_ != expected || layer != next_layer_) return fail(EngineKvError::LayerOutOfOrder);
+    if (!arguments_ok) return fail(EngineKvError::InvalidArgument);
+    return {};
+}
+
+void TokenTransaction::settle(Step step, EngineKvStatus const& outcome) noexcept
+{
+    if (!outcome.ok()) {
+        phase_ = TokenTransactionPhase::Failed;
+    } else if (step == Step::Write) {
+        phase_ = TokenTransactionPhase::AwaitingLayerAttention;
+    } else {
+        ++next_layer_;
+        phase_ = next_layer_ < layer_count_ ? TokenTransactionPhase::AwaitingLayerWrite
+                                            : TokenTransactionPhase::ReadyToCommit;
+    }
+}
+
+void TokenTransaction::end(TokenTransactionPhase final_phase) noexcept
+{
+    backend_.reset();
+    phase_ = final_phase;
 }
 
 EngineKvStatus TokenTransaction::writeLayer(LayerKvWrite const& write)
 {
-    if (!active()) return status(EngineKvError::InvalidState);
-    if (phase_ != TokenTransactionPhase::AwaitingLayerWrite || write.layer != next_layer_) {
-        return status(EngineKvError::LayerOutOfOrder);
-    }
-    if (write.device_key == nullptr || write.device_value == nullptr) return status(EngineKvError::InvalidArgument);
-    EngineKvStatus const r = backend_->writeLayer(write, stream_);
-    if (!r.ok()) {
-        phase_ = TokenTransactionPhase::Failed;
-        return r;
-    }
-    phase_ = TokenTransactionPhase::AwaitingLayerAttention;
-    return {};
-}
-
-void TokenTransaction::advanceAfterAttend() noexcept
-{
-    ++next_layer_;
-    phase_ = next_layer_ == layer_count_ ? TokenTransactionPhase::ReadyToCommit
-                                         : TokenTransactionPhase::AwaitingLayerWrite;
+    EngineKvStatus const admitted = admit(Step::Write, write.layer, writeArgumentsOk(write));
+    if (!admitted.ok()) return admitted;
+    EngineKvStatus const outcome = backend_->writeLayer(write, stream_);
+    settle(Step::Write, outcome);
+    return outcome;
 }
 
 EngineKvStatus TokenTransaction::attendLayer(PagedDecodeRequest const& request)
 {
-    if (!active()) return status(EngineKvError::InvalidState);
-    if (phase_ != TokenTransactionPhase::AwaitingLayerAttention || request.layer != next_layer_) {
-        return status(EngineKvError::LayerOutOfOrder);
-    }
-    if (!decodeArgumentsValid(request)) return status(EngineKvError::InvalidArgument);
-    EngineKvStatus const r = backend_->attendLayer(request, stream_);
-    if (!r.ok()) {
-        phase_ = TokenTransactionPhase::Failed;
-        return r;
-    }
-    advanceAfterAttend();
-    return {};
+    EngineKvStatus const admitted = admit(Step::Attend, request.layer, attendArgumentsOk(request));
+    if (!admitted.ok()) return admitted;
+    EngineKvStatus const outcome = backend_->attendLayer(request, stream_);
+    settle(Step::Attend, outcome);
+    return outcome;
 }
 
 EngineKvStatus TokenTransaction::commit()
 {
-    if (!active() || phase_ != TokenTransactionPhase::ReadyToCommit) return status(EngineKvError::InvalidState);
-    EngineKvStatus const r = backend_->commit(stream_);
-    if (!r.ok()) {
-        backend_->rollback(stream_);
-        backend_.reset();
-        phase_ = TokenTransactionPhase::RolledBack;
-        return r;
-    }
-    backend_.reset();
-    phase_ = TokenTransactionPhase::Committed;
-    return {};
+    if (!active() || phase_ != TokenTransactionPhase::ReadyToCommit) return fail(EngineKvError::InvalidState);
+    EngineKvStatus const outcome = backend_->commit(stream_);
+    if (!outcome.ok()) backend_->rollback(stream_);   // a token that cannot complete is undone
+    end(outcome.ok() ? TokenTransactionPhase::Committed : TokenTransactionPhase::RolledBack);
+    return outcome;
 }
 
 EngineKvStatus TokenTransaction::rollback() noexcept
 {
-    if (!active()) return status(EngineKvError::InvalidState);
+    if (!active()) return fail(EngineKvError::InvalidState);
     rollbackNoexcept();
     return {};
 }
@@ -195,93 +241,63 @@ void TokenTransaction::rollbackNoexcept() noexcept
 {
     if (!active()) return;
     backend_->rollback(stream_);
-    backend_.reset();
-    phase_ = TokenTransactionPhase::RolledBack;
+    end(TokenTransactionPhase::RolledBack);
 }
 
-void TokenTransaction::resetMovedFrom() noexcept
-{
-    transaction_id_ = kInvalidTokenTransactionId;
-    request_id_ = kInvalidRequestId;
-    logical_token_position_ = 0;
-    layer_count_ = 0;
-    next_layer_ = 0;
-    phase_ = TokenTransactionPhase::Empty;
-    stream_ = nullptr;
-}
+// ---- batches ----------------------------------------------------------------------------------------------
 
-void attendLayerBatch(PagedDecodeBatch& batch)
-{
-    if (batch.items == nullptr || batch.item_count == 0) return;
-    bool const scratch = batch.host_items != nullptr && batch.device_items != nullptr
-        && batch.item_capacity >= batch.item_count;
-    TokenTransactionBackend* dispatcher = nullptr;
-    for (std::size_t i = 0; i < batch.item_count; ++i) {
-        PagedDecodeBatchItem& item = batch.items[i];
-        item.status = {};
-        item.dispatched = false;
-        TokenTransaction* t = item.transaction;
-        if (!scratch) {
-            item.status = status(EngineKvError::InvalidArgument);
-        } else if (t == nullptr || !t->active()) {
-            item.status = status(EngineKvError::InvalidState);
-        } else if (t->phase_ != TokenTransactionPhase::AwaitingLayerAttention || item.request.layer != t->next_layer_) {
-            item.status = status(EngineKvError::LayerOutOfOrder);
-        } else if (!decodeArgumentsValid(item.request)) {
-            item.status = status(EngineKvError::InvalidArgument);
-        } else {
+// Admission, one submission and per-lane settling, shared by both batch kinds.
+struct TokenBatchRunner {
+    template <typename Item, typename Submit>
+    static void run(Item* items, std::size_t count, TokenTransaction::Step step, bool batch_ok, Submit submit)
+    {
+        if (items == nullptr || count == 0) return;
+        TokenTransactionBackend* submitter = nullptr;
+        for (std::size_t i = 0; i < count; ++i) {
+            Item& item = items[i];
+            TokenTransaction const* t = item.transaction;
+            item.dispatched = false;
+            if (!batch_ok) {
+                item.status = fail(EngineKvError::InvalidArgument);
+            } else if (t == nullptr) {
+                item.status = fail(EngineKvError::InvalidState);
+            } else {
+                item.status = t->admit(step, layerOf(item), argumentsOk(item));
+            }
+            if (!item.status.ok()) continue;
             item.dispatched = true;
-            if (dispatcher == nullptr) dispatcher = t->backend_.get();
+            if (submitter == nullptr) submitter = t->backend_.get();
+        }
+        if (submitter == nullptr) return;
+        submit(*submitter);
+        for (std::size_t i = 0; i < count; ++i) {
+            Item& item = items[i];
+            TokenTransaction* t = item.transaction;
+            // A transaction listed twice settles once: the second entry no longer admits.
+            if (item.dispatched && t != nullptr && t->admit(step, layerOf(item), true).ok()) {
+                t->settle(step, item.status);
+            }
         }
     }
-    if (dispatcher == nullptr) return;
-    dispatcher->attendLayerBatch(batch);
-    for (std::size_t i = 0; i < batch.item_count; ++i) {
-        PagedDecodeBatchItem& item = batch.items[i];
-        TokenTransaction* t = item.transaction;
-        if (!item.dispatched || t == nullptr || t->phase_ != TokenTransactionPhase::AwaitingLayerAttention
-            || item.request.layer != t->next_layer_) {
-            continue;
-        }
-        if (!item.status.ok()) {
-            t->phase_ = TokenTransactionPhase::Failed;
-            continue;
-        }
-        t->advanceAfterAttend();
-    }
-}
 
-void writeLayerBatch(LayerKvWriteBatch& batch)
-{
-    if (batch.items == nullptr || batch.item_count == 0) return;
-    TokenTransactionBackend* dispatcher = nullptr;
-    for (std::size_t i = 0; i < batch.item_count; ++i) {
-        LayerKvWriteBatchItem& item = batch.items[i];
-        item.status = {};
-        item.dispatched = false;
-        TokenTransaction* t = item.transaction;
-        if (t == nullptr || !t->active()) {
-            item.status = status(EngineKvError::InvalidState);
-        } else if (t->phase_ != TokenTransactionPhase::AwaitingLayerWrite || item.write.layer != t->next_layer_) {
-            item.status = status(EngineKvError::LayerOutOfOrder);
-        } else if (item.write.device_key == nullptr || item.write.device_value == nullptr) {
-            item.status = status(EngineKvError::InvalidArgument);
-        } else {
-            item.dispatched = true;
-            if (dispatcher == nullptr) dispatcher = t->backend_.get();
-        }
+    static void attend(PagedDecodeBatch& batch)
+    {
+        // The caller's item scratch must hold every lane (reference contract).
+        bool const scratch_ok = batch.host_items != nullptr && batch.device_items != nullptr
+            && batch.item_capacity >= batch.item_count;
+        run(batch.items, batch.item_count, TokenTransaction::Step::Attend, scratch_ok,
+            [&batch](TokenTransactionBackend& b) { b.attendLayerBatch(batch); });
     }
-    if (dispatcher == nullptr) return;
-    dispatcher->writeLayerBatch(batch);
-    for (std::size_t i = 0; i < batch.item_count; ++i) {
-        LayerKvWriteBatchItem& item = batch.items[i];
-        TokenTransaction* t = item.transaction;
-        if (!item.dispatched || t == nullptr || t->phase_ != TokenTransactionPhase::AwaitingLayerWrite
-            || item.write.layer != t->next_layer_) {
-            continue;
-        }
-        t->phase_ = item.status.ok() ? TokenTransactionPhase::AwaitingLayerAttention : TokenTransactionPhase::Failed;
+
+    static void write(LayerKvWriteBatch& batch)
+    {
+        run(batch.items, batch.item_count, TokenTransaction::Step::Write, true,
+            [&batch](TokenTransactionBackend& b) { b.writeLayerBatch(batch); });
     }
-}
+};
+
+void attendLayerBatch(PagedDecodeBatch& batch) { TokenBatchRunner::attend(batch); }
+
+void writeLayerBatch(LayerKvWriteBatch& batch) { TokenBatchRunner::write(batch); }
 
 }  // namespace kimkvcache

@@ -5,7 +5,14 @@
                                (src/core, src/runtime, src/reference, read in
                                place under the reference tree) plus
                                oracle/ref_driver.cpp; only when that tree exists.
-Both outputs are git-ignored; oracle/_ref travels with the tree.
+  oracle/_ref/contracts/*      the reference's own CPU contract tests (its
+                               tests/core, tests/runtime, tests/engine and
+                               tests/reference sources, read in place) compiled
+                               against THIS build's include/ and linked with its
+                               libkimkv.so: the reference's checks run against
+                               the drop-in (build_reference_contracts, after the
+                               package is built).
+All outputs are git-ignored and stay off GPU runs (nothing there uses them).
 """
 from __future__ import annotations
 
@@ -52,6 +59,38 @@ def build_reference() -> str | None:
           *srcs, os.path.join(ORACLE_DIR, "ref_driver.cpp"), "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
     return out
+
+
+# Reference tests whose includes this build provides (the fixed-size page
+# strategy and the weight manifest are not part of it).
+REFERENCE_CONTRACTS = (
+    "core/page_pool_test",
+    "runtime/block_table_test",
+    "runtime/page_lease_test",
+    "runtime/promotion_test",
+    "engine/engine_kv_contract_test",
+    "engine/generation_runtime_test",
+    "engine/iteration_scheduler_test",
+    "reference/kv_reference_test",
+)
+
+
+def build_reference_contracts() -> list[str]:
+    """Compiles the reference's contract tests against include/ and libkimkv.so."""
+    lib_dir = os.path.join(REPO, "kim-kvcache_amd", "_lib")
+    srcs = [os.path.join(REFERENCE, "tests", t + ".cpp") for t in REFERENCE_CONTRACTS]
+    if not all(os.path.exists(s) for s in srcs) or not os.path.exists(os.path.join(lib_dir, "libkimkv.so")):
+        return []
+    out_dir = os.path.join(ORACLE_DIR, "_ref", "contracts")
+    os.makedirs(out_dir, exist_ok=True)
+    outs = []
+    for src in srcs:
+        out = os.path.join(out_dir, os.path.splitext(os.path.basename(src))[0])
+        _run(["g++", "-std=c++17", "-O1", f"-I{os.path.join(REPO, 'include')}", src, f"-L{lib_dir}", "-lkimkv",
+              "-lkimkv_hip", f"-Wl,-rpath,{lib_dir}", "-pthread", "-o", out + ".tmp"])
+        os.replace(out + ".tmp", out)
+        outs.append(out)
+    return outs
 
 
 def build_all() -> list[str]:
