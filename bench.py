@@ -64,6 +64,7 @@ class Workload:
         self.H, self.D, self.QH = kv_heads, head_dim, query_heads
         self.total_steps = total_steps
         self.seed = seed
+        self.decode_mode = "plan"
         self.ext_per_lane = context // 64
         assert context % 64 == 0
         self.micro_per_lane = (total_steps + 7) // 8
@@ -143,6 +144,13 @@ class Workload:
         count = m + 1
         T = self.lane_tokens(step)
         chunk, prefix, total = self.storage.decode_plan([T] * self.lanes, self.QH)
+        if self.decode_mode == "head_split":      # one chunk per lane, split over the four waves
+            chunk = (T + 63) // 64 * 64 | dev.DECODE_HEAD_SPLIT
+        elif self.decode_mode == "guided":
+            chunk = dev.DECODE_GUIDED | 64
+        if self.decode_mode != "plan":
+            prefix = dev.chunk_prefix([T] * self.lanes, chunk, self.D)
+            total = int(prefix[-1])
         ws_lane = dev.workspace_bytes(T, chunk, self.QH, self.D)
         if self.ws is None or ws_lane > self.ws_stride:
             self.ws_stride = max(ws_lane, 256)
@@ -1064,6 +1072,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=22)
     ap.add_argument("--cpu-lanes", type=int, default=32, help="lanes in the CPU baseline sample (0 = skip)")
     ap.add_argument("--seed", type=int, default=20260829)
+    ap.add_argument("--decode-mode", choices=["plan", "head_split", "guided"], default="plan",
+                    help="kernel path: decode mode (default: the planner's choice)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -1097,6 +1107,7 @@ def main() -> int:
     else:
         w = Workload(dev, args.lanes, args.context, args.layers, H, D, QH, total_steps, args.seed,
                      permute=args.slots == "permuted")
+        w.decode_mode = args.decode_mode
         stream = dev.Stream()
 
     for s in range(args.warmup):
@@ -1197,8 +1208,9 @@ def main() -> int:
                                   else "kernels driven directly"),
                    "path": args.path,
                    "lanes": args.lanes, "context": args.context, "layers": args.layers,
-                   "decode_chunk_tokens": w.plan[0] & ~dev.DECODE_HEAD_SPLIT,
-                   "decode_head_split": bool(w.plan[0] & dev.DECODE_HEAD_SPLIT), "decode_chunks_per_launch": w.plan[1],
+                   "decode_mode": dev.decode_mode(w.plan[0]),
+                   "decode_chunk_tokens": w.plan[0] & 0x3FFFFFFF if not w.plan[0] & dev.DECODE_GUIDED else None,
+                   "decode_chunks_per_launch": w.plan[1],
                    "lane_groups": args.groups if args.path == "engine" else 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4),

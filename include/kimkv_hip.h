@@ -242,6 +242,23 @@ kimkv_status kimkv_promote_batch(const kimkv_storage* storage,
  * kimkv_decode_workspace_bytes unchanged. */
 #define KIMKV_DECODE_HEAD_SPLIT 0x80000000u
 
+/* Opt-in (kimkv_decode_plan does not choose it) guided persistent mode, set in
+ * chunk_tokens by the caller:
+ * a lane of T tokens is cut into n = min(KIMKV_DECODE_GUIDED_SLICES,
+ * max(1, T / (head_dim + 2))) slices of halving length (T/2, T/4, ...,
+ * the last two equal; starts 64-aligned), about two workgroups per CU take
+ * (slice, lane, KV head) units from a device counter, longest slices first,
+ * and the merge launch combines each lane's slices (a one-slice lane is
+ * written directly).  The other bits are ignored in this mode; a lane's
+ * chunk count is kimkv_decode_lane_chunks. */
+#define KIMKV_DECODE_GUIDED 0x40000000u
+#define KIMKV_DECODE_GUIDED_SLICES 6u
+
+/* Chunks (split-K partial slots) of a lane of token_count tokens under a
+ * planned chunk_tokens value (flags included): the chunk prefix of a launch
+ * is the running sum of this over its lanes. */
+uint32_t kimkv_decode_lane_chunks(uint32_t token_count, uint32_t chunk_tokens, uint32_t head_dim);
+
 /* Split-K planning for a ragged decode batch.  Given the lanes' token counts
  * (host array), picks the chunk length (a multiple of 64 tokens, 256..65536,
  * possibly with KIMKV_DECODE_HEAD_SPLIT set) and fills

@@ -398,84 +398,28 @@ __device__ inline bool decode_item_valid(const PoolView& P, const kimkv_decode_i
         && QH % P.heads == 0 && P.dim <= 256 && (nchunks <= 1 || item.workspace != nullptr);
 }
 
-// Two waves per SIMD: each wave holds two 64-token steps of K/V operands in
-// registers, so a CU keeps as many bytes in flight as four single-buffered
-// waves while the compute of one step hides under the loads of the next.
-//
-// kSplit = false: workgroup = (lane, chunk, four kv heads), wave w takes kv
-//   head 4 blockIdx.y + w over the whole chunk.
-// kSplit = true: workgroup = (lane, chunk, kv head blockIdx.y); the chunk is
-//   cut into four 64-token-aligned quarters, one per wave, and the four
-//   online-softmax states are merged through LDS, so a lane that fits one
-//   chunk writes its output directly and needs no combine launch.
-//
-// partials: when non-null, split-K partials of global chunk c go to
-// partials + c * QH * (D + 2) instead of the lanes' own workspaces.
-template <bool kSplit>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
-    PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t chunk_tokens,
-    uint32_t QH, float* partials)
+// LDS of a decode workgroup: the chunk's group table (also the buffer the
+// head-split merge uses) and the per-wave token records of the generic path.
+struct DecodeLds {
+    __attribute__((aligned(16))) GroupEntry groups[kMaxGroups];
+    WaveTokens wave_tokens[kHeadsPerBlock];
+    uint32_t idx0;
+    uint32_t dok;
+    uint32_t generic;
+};
+
+// Builds the group table of tokens [c0, c1) of `item` (c0 a multiple of 8)
+// and returns whether the fast path applies (head_dim 64, group <= 16, every
+// 8-token group mapped and aligned).  Called by every thread of the block.
+__device__ bool build_chunk_table(const PoolView& P, const kimkv_decode_item& item, uint32_t QH, uint32_t c0,
+                                  uint32_t c1, DecodeLds& lds)
 {
-    __shared__ __attribute__((aligned(16))) GroupEntry groups[kMaxGroups];   // also the merge buffer
-    __shared__ WaveTokens wave_tokens[kHeadsPerBlock];
-    __shared__ uint32_t s_lane;
-    __shared__ uint32_t s_hit;
-    __shared__ uint32_t s_idx0;
-    __shared__ uint32_t s_dok;
-    __shared__ uint32_t s_generic;
-
     uint32_t const tid = threadIdx.x;
-    uint32_t const chunk_id = blockIdx.x;
-    if (lane_count == 0) return;
-    // The prologue is a chain of dependent global reads, and under full HBM
-    // load each costs microseconds while this workgroup streams nothing, so
-    // both lookups are guessed and verified in the same round trip.
-    // Lane: guess from the average chunk count per lane (exact when lanes
-    // have equal chunk counts), with that lane's item loaded alongside.
-    uint32_t const guess = static_cast<uint32_t>(
-        min(static_cast<uint64_t>(chunk_id) * lane_count / gridDim.x, static_cast<uint64_t>(lane_count - 1)));
-    kimkv_decode_item item = items[guess];
-    uint32_t const pg0 = prefix[guess];
-    uint32_t const pg1 = prefix[guess + 1];
-    if (tid == 0) {
-        s_hit = pg0 <= chunk_id && chunk_id < pg1 ? 1u : 0u;
-        s_lane = 0xFFFFFFFFu;
-        s_generic = 0;
-    }
-    __syncthreads();
-    uint32_t lane = guess;
-    if (s_hit == 0) {
-        for (uint32_t i = tid; i < lane_count; i += kBlock) {
-            if (prefix[i] <= chunk_id && chunk_id < prefix[i + 1]) s_lane = i;
-        }
-        __syncthreads();
-        lane = s_lane;
-        if (lane == 0xFFFFFFFFu) {   // the chunk prefix does not cover this workgroup
-            report_fault(P, KIMKV_FAULT_DECODE_ITEM);
-            return;
-        }
-        item = items[lane];
-    }
-
-    uint32_t const H = P.heads;
-    uint32_t const D = P.dim;
-    uint32_t const lane_first = prefix[lane];
-    uint32_t const chunk_index = chunk_id - lane_first;
-    uint32_t const nchunks = prefix[lane + 1] - lane_first;
-    if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(lane_first) * QH * (D + 2);
     uint32_t const T = item.token_count;
-    uint32_t const c0 = chunk_index * chunk_tokens;
-    if (!decode_item_valid(P, item, QH, nchunks) || c0 >= T || chunk_tokens > kMaxChunk) {
-        report_fault(P, KIMKV_FAULT_DECODE_ITEM);
-        return;
-    }
-    uint32_t const c1 = min(c0 + chunk_tokens, T);
-    uint32_t const G = QH / H;
-    bool const single = nchunks == 1;
-    bool const fast_shape = D == 64 && G <= 16;
     uint32_t const ngroups = (c1 - c0 + 7) / 8;
+    if (tid == 0) lds.generic = 0;
     for (uint32_t g = tid; g < ngroups; g += kBlock) {
-        groups[g] = GroupEntry{kUnmappedGroup, 0, 0};
+        lds.groups[g] = GroupEntry{kUnmappedGroup, 0, 0};
     }
     __syncthreads();
 
@@ -486,22 +430,22 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t const dguess = min(c0 / 64u, item.descriptor_count - 1);
     for (uint32_t j = tid; j <= ngroups && dguess + j < item.descriptor_count; j += kBlock) {
         kimkv_block_desc const e = item.descriptors[dguess + j];
-        if (j == 0) s_dok = e.logical_token_begin <= c0 && c0 - e.logical_token_begin < e.valid_tokens ? 1u : 0u;
-        add_groups(P, e, c0, c1, T, groups, &s_generic);
+        if (j == 0) lds.dok = e.logical_token_begin <= c0 && c0 - e.logical_token_begin < e.valid_tokens ? 1u : 0u;
+        add_groups(P, e, c0, c1, T, lds.groups, &lds.generic);
     }
     __syncthreads();
-    if (s_dok == 0) {
+    if (lds.dok == 0) {
         for (uint32_t g = tid; g < ngroups; g += kBlock) {
-            groups[g] = GroupEntry{kUnmappedGroup, 0, 0};
+            lds.groups[g] = GroupEntry{kUnmappedGroup, 0, 0};
         }
         if (tid < 64) {
             uint32_t const idx0 = find_descriptor_wave(item.descriptors, item.descriptor_count, c0);
-            if (tid == 0) s_idx0 = idx0;
+            if (tid == 0) lds.idx0 = idx0;
         }
         __syncthreads();
-        uint32_t const idx0 = s_idx0;
+        uint32_t const idx0 = lds.idx0;
         for (uint32_t j = tid; j <= ngroups && idx0 + j < item.descriptor_count; j += kBlock) {
-            add_groups(P, item.descriptors[idx0 + j], c0, c1, T, groups, &s_generic);
+            add_groups(P, item.descriptors[idx0 + j], c0, c1, T, lds.groups, &lds.generic);
         }
         __syncthreads();
     }
@@ -510,35 +454,28 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // an unmapped 8-token group goes to the generic path, which skips
     // unmapped tokens.
     bool hole = false;
-    for (uint32_t g = tid; g < ngroups; g += kBlock) hole |= groups[g].page == kUnmappedGroup;
-    if (hole) s_generic = 1;
+    for (uint32_t g = tid; g < ngroups; g += kBlock) hole |= lds.groups[g].page == kUnmappedGroup;
+    if (hole) lds.generic = 1;
     __syncthreads();
+    uint32_t const G = QH / P.heads;
+    return P.dim == 64 && G <= 16 && lds.generic == 0;
+}
 
+// One (lane, kv head, chunk) by the whole workgroup: tokens [c0, c1) cut
+// into four 64-token-aligned quarters, one per wave, the four online-softmax
+// states merged through LDS, then the output (single chunk) or the chunk's
+// partial written.  Called by every thread of the block after
+// build_chunk_table; ends with the merge buffer still in use (callers that
+// reuse the LDS synchronize first).
+__device__ void decode_head_split_chunk(const PoolView& P, const kimkv_decode_item& item, uint32_t h, uint32_t QH,
+                                        uint32_t c0, uint32_t c1, uint32_t chunk_index, bool single, bool fast,
+                                        DecodeLds& lds)
+{
+    uint32_t const tid = threadIdx.x;
     uint32_t const wave = tid >> 6;
-    bool const fast = fast_shape && s_generic == 0;
-    if (!kSplit) {
-        uint32_t const h = blockIdx.y * kHeadsPerBlock + wave;
-        if (h >= H) return;
-        if (!fast) {
-            decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &wave_tokens[wave]);
-            return;
-        }
-        WavePartial const w = decode_wave_d64(groups, GroupResolver(P, item.layer, h), item, h, G, c0, c0, c1);
-        uint32_t const l = tid & 63u;
-        uint32_t const r = l & 15u;
-        if (r >= G) return;
-#pragma unroll
-        for (uint32_t db = 0; db < 4; ++db) {
-            store_partial(item, QH, h * G + r, chunk_index, single, w.acc[db], db * 16 + 4 * (l >> 4), w.m, w.l,
-                          db == 0 && l < 16);
-        }
-        return;
-    }
-
-    uint32_t const h = blockIdx.y;
-    if (h >= H) return;
+    uint32_t const G = QH / P.heads;
     if (!fast) {
-        if (wave == 0) decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &wave_tokens[0]);
+        if (wave == 0) decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &lds.wave_tokens[0]);
         return;
     }
     uint32_t const quarter = ((c1 - c0 + 3) / 4 + 63) / 64 * 64;
@@ -546,7 +483,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t const s1 = min(s0 + quarter, c1);
     WavePartial w;
     if (s0 < s1) {
-        w = decode_wave_d64(groups, GroupResolver(P, item.layer, h), item, h, G, c0, s0, s1);
+        w = decode_wave_d64(lds.groups, GroupResolver(P, item.layer, h), item, h, G, c0, s0, s1);
     } else {
 #pragma unroll
         for (uint32_t db = 0; db < 4; ++db) w.acc[db] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -557,7 +494,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // [wave][query column][68 floats: o(64), m, l, pad].
     constexpr uint32_t kRow = 68;
     __syncthreads();
-    float* part = reinterpret_cast<float*>(groups);
+    float* part = reinterpret_cast<float*>(lds.groups);
     {
         uint32_t const l = tid & 63u;
         float* row = part + (wave * 16 + (l & 15u)) * kRow;
@@ -589,6 +526,186 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         o += c * *reinterpret_cast<const float4_t*>(row + d0);
     }
     store_partial(item, QH, h * G + r, chunk_index, single, o, d0, M, den, d0 == 0);
+}
+
+// Two waves per SIMD: each wave holds two 64-token steps of K/V operands in
+// registers, so a CU keeps as many bytes in flight as four single-buffered
+// waves while the compute of one step hides under the loads of the next.
+//
+// kSplit = false: workgroup = (lane, chunk, four kv heads), wave w takes kv
+//   head 4 blockIdx.y + w over the whole chunk.
+// kSplit = true: workgroup = (lane, chunk, kv head blockIdx.y); the chunk is
+//   cut into four 64-token-aligned quarters, one per wave, and the four
+//   online-softmax states are merged through LDS, so a lane that fits one
+//   chunk writes its output directly and needs no combine launch.
+//
+// partials: when non-null, split-K partials of global chunk c go to
+// partials + c * QH * (D + 2) instead of the lanes' own workspaces.
+template <bool kSplit>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
+    PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t chunk_tokens,
+    uint32_t QH, float* partials)
+{
+    __shared__ DecodeLds lds;
+    __shared__ uint32_t s_lane;
+    __shared__ uint32_t s_hit;
+
+    uint32_t const tid = threadIdx.x;
+    uint32_t const chunk_id = blockIdx.x;
+    if (lane_count == 0) return;
+    // The prologue is a chain of dependent global reads, and under full HBM
+    // load each costs microseconds while this workgroup streams nothing, so
+    // both lookups are guessed and verified in the same round trip.
+    // Lane: guess from the average chunk count per lane (exact when lanes
+    // have equal chunk counts), with that lane's item loaded alongside.
+    uint32_t const guess = static_cast<uint32_t>(
+        min(static_cast<uint64_t>(chunk_id) * lane_count / gridDim.x, static_cast<uint64_t>(lane_count - 1)));
+    kimkv_decode_item item = items[guess];
+    uint32_t const pg0 = prefix[guess];
+    uint32_t const pg1 = prefix[guess + 1];
+    if (tid == 0) {
+        s_hit = pg0 <= chunk_id && chunk_id < pg1 ? 1u : 0u;
+        s_lane = 0xFFFFFFFFu;
+    }
+    __syncthreads();
+    uint32_t lane = guess;
+    if (s_hit == 0) {
+        for (uint32_t i = tid; i < lane_count; i += kBlock) {
+            if (prefix[i] <= chunk_id && chunk_id < prefix[i + 1]) s_lane = i;
+        }
+        __syncthreads();
+        lane = s_lane;
+        if (lane == 0xFFFFFFFFu) {   // the chunk prefix does not cover this workgroup
+            report_fault(P, KIMKV_FAULT_DECODE_ITEM);
+            return;
+        }
+        item = items[lane];
+    }
+
+    uint32_t const H = P.heads;
+    uint32_t const D = P.dim;
+    uint32_t const lane_first = prefix[lane];
+    uint32_t const chunk_index = chunk_id - lane_first;
+    uint32_t const nchunks = prefix[lane + 1] - lane_first;
+    if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(lane_first) * QH * (D + 2);
+    uint32_t const T = item.token_count;
+    uint32_t const c0 = chunk_index * chunk_tokens;
+    if (!decode_item_valid(P, item, QH, nchunks) || c0 >= T || chunk_tokens > kMaxChunk) {
+        report_fault(P, KIMKV_FAULT_DECODE_ITEM);
+        return;
+    }
+    uint32_t const c1 = min(c0 + chunk_tokens, T);
+    uint32_t const G = QH / H;
+    bool const single = nchunks == 1;
+    bool const fast = build_chunk_table(P, item, QH, c0, c1, lds);
+
+    uint32_t const wave = tid >> 6;
+    if (!kSplit) {
+        uint32_t const h = blockIdx.y * kHeadsPerBlock + wave;
+        if (h >= H) return;
+        if (!fast) {
+            decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &lds.wave_tokens[wave]);
+            return;
+        }
+        WavePartial const w = decode_wave_d64(lds.groups, GroupResolver(P, item.layer, h), item, h, G, c0, c0, c1);
+        uint32_t const l = tid & 63u;
+        uint32_t const r = l & 15u;
+        if (r >= G) return;
+#pragma unroll
+        for (uint32_t db = 0; db < 4; ++db) {
+            store_partial(item, QH, h * G + r, chunk_index, single, w.acc[db], db * 16 + 4 * (l >> 4), w.m, w.l,
+                          db == 0 && l < 16);
+        }
+        return;
+    }
+    uint32_t const h = blockIdx.y;
+    if (h >= H) return;
+    decode_head_split_chunk(P, item, h, QH, c0, c1, chunk_index, single, fast, lds);
+}
+
+// Slices of a lane of T tokens in the guided mode: at most six, and no more
+// than T / (D + 2), so the lane's partials (slices * QH * (D + 2) floats)
+// never exceed the reference's QH * T float workspace.
+__host__ __device__ inline uint32_t guided_slices(uint32_t T, uint32_t D)
+{
+    uint32_t const cap = T / (D + 2u);
+    return cap < 1u ? 1u : (cap < KIMKV_DECODE_GUIDED_SLICES ? cap : KIMKV_DECODE_GUIDED_SLICES);
+}
+
+// First token of guided slice k of n: slices of halving length (T/2, T/4,
+// ..., the last two equal), starts 64-aligned.
+__host__ __device__ inline uint32_t guided_edge(uint32_t T, uint32_t n, uint32_t k)
+{
+    if (k == 0) return 0;
+    if (k >= n) return T;
+    return (T - (T >> k)) / 64u * 64u;
+}
+
+// Guided persistent decode: gridDim.x workgroups (about two per CU) take
+// units from counter[0] until none is left.  Unit u is slice u / pairs of
+// (lane, kv head) pair u % pairs, so every pair's longest slice comes first
+// and the shortest last: workgroups on CUs that get more bandwidth take more
+// units, and the launch ends about one short slice after the work runs out
+// instead of when the slowest of a fixed set of workgroups finishes.  Each
+// unit is a head-split chunk whose partial goes to the lane's slot k; the
+// merge launch combines the slices.  The last workgroup to leave resets the
+// counter slot for the next launch that uses it.
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_guided_kernel(
+    PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t QH,
+    float* partials, uint32_t* counter)
+{
+    __shared__ DecodeLds lds;
+    __shared__ uint32_t s_unit;
+    constexpr uint32_t K = KIMKV_DECODE_GUIDED_SLICES;
+    uint32_t const tid = threadIdx.x;
+    uint32_t const H = P.heads;
+    uint32_t const D = P.dim;
+    uint32_t const G = QH / H;
+    uint32_t const pairs = lane_count * H;
+    uint32_t const total = pairs * K;
+    for (;;) {
+        if (tid == 0) s_unit = atomicAdd(&counter[0], 1u);
+        __syncthreads();
+        uint32_t const u = s_unit;
+        __syncthreads();   // every thread has the unit before thread 0 fetches the next
+        if (u >= total) break;
+        uint32_t const k = u / pairs;
+        uint32_t const pair = u - k * pairs;
+        uint32_t const lane = pair / H;
+        uint32_t const h = pair - lane * H;
+        kimkv_decode_item item = items[lane];
+        uint32_t const T = item.token_count;
+        uint32_t const n = guided_slices(T, D);
+        if (k >= n) continue;   // a short lane has fewer slices
+        uint32_t const first = prefix[lane];
+        if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(first) * QH * (D + 2);
+        uint32_t const c0 = guided_edge(T, n, k);
+        uint32_t const c1 = guided_edge(T, n, k + 1);
+        if (!decode_item_valid(P, item, QH, n) || prefix[lane + 1] - first != n || c1 - c0 > kMaxChunk) {
+            report_fault(P, KIMKV_FAULT_DECODE_ITEM);
+            continue;
+        }
+        if (c0 >= c1) {
+            // An empty slice still leaves its partial: weight zero in the merge.
+            uint32_t const r = tid >> 4;
+            uint32_t const d0 = (tid & 15u) * 4;
+            if (r < G) {
+                store_partial(item, QH, h * G + r, k, false, float4_t{0.0f, 0.0f, 0.0f, 0.0f}, d0, -INFINITY, 0.0f,
+                              d0 == 0);
+            }
+            continue;
+        }
+        bool const fast = build_chunk_table(P, item, QH, c0, c1, lds);
+        decode_head_split_chunk(P, item, h, QH, c0, c1, k, n == 1, fast, lds);
+        __syncthreads();   // the next unit rebuilds the table in the same LDS
+    }
+    if (tid == 0) {
+        uint32_t const left = atomicAdd(&counter[1], 1u);
+        if (left + 1 == gridDim.x) {
+            atomicExch(&counter[0], 0u);
+            atomicExch(&counter[1], 0u);
+        }
+    }
 }
 
 // Merges the per-chunk partials of every multi-chunk lane.  Block = (lane,
@@ -750,19 +867,30 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
                            bool timed)
 {
     bool const head_split = (chunk_flags & KIMKV_DECODE_HEAD_SPLIT) != 0;
-    uint32_t const chunk_tokens = chunk_flags & ~KIMKV_DECODE_HEAD_SPLIT;
+    bool const guided = (chunk_flags & KIMKV_DECODE_GUIDED) != 0;
+    uint32_t const chunk_tokens = chunk_flags & ~(KIMKV_DECODE_HEAD_SPLIT | KIMKV_DECODE_GUIDED);
     if (storage == nullptr || device_items == nullptr || device_chunk_prefix == nullptr || lane_count == 0
-        || query_heads == 0 || query_heads % storage->layout.kv_heads != 0 || chunk_tokens == 0
-        || chunk_tokens % 64 != 0 || chunk_tokens > kMaxChunk || storage->layout.head_dim > 256) {
+        || query_heads == 0 || query_heads % storage->layout.kv_heads != 0 || storage->layout.head_dim > 256
+        || (head_split && guided)
+        || (!guided && (chunk_tokens == 0 || chunk_tokens % 64 != 0 || chunk_tokens > kMaxChunk))) {
         return KIMKV_INVALID_ARGUMENT;
     }
     if (total_chunks == 0) return KIMKV_OK;
     hipStream_t const s = native(stream);
     uint32_t const H = storage->layout.kv_heads;
+    uint64_t const units = static_cast<uint64_t>(lane_count) * H * KIMKV_DECODE_GUIDED_SLICES;
+    if (guided && (units > 0x7FFFFFFFu || storage->work_counters == nullptr)) return KIMKV_INVALID_ARGUMENT;
     dim3 const grid(total_chunks, head_split ? H : (H + kHeadsPerBlock - 1) / kHeadsPerBlock);
     void* start = nullptr;
     if (timed) kernel_timing_begin(TimedKernel::Decode, s, &start);
-    if (head_split) {
+    if (guided) {
+        uint32_t const slot = storage->next_work_counter.fetch_add(1, std::memory_order_relaxed) % kWorkCounterSlots;
+        uint32_t* counter = storage->work_counters + static_cast<size_t>(slot) * kWorkCounterStride;
+        uint64_t const resident = 2ull * (storage->compute_units > 0 ? storage->compute_units : 256);
+        auto const workers = static_cast<uint32_t>(units < resident ? units : resident);
+        decode_guided_kernel<<<workers, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
+                                                         lane_count, query_heads, partials, counter);
+    } else if (head_split) {
         decode_kernel<true><<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
                                                     lane_count, chunk_tokens, query_heads, partials);
     } else {
@@ -862,8 +990,12 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
     // When four kv heads per workgroup would need split-K but one kv head per
     // workgroup would not, take one head per workgroup with its chunk split
     // over the four waves: same workgroup count, no partials, no merge launch.
-    bool const head_split = per_block < longest && per_head >= longest && storage->layout.head_dim == 64
-        && query_heads % H == 0 && query_heads / H <= 16;
+    bool const fast_shape = storage->layout.head_dim == 64 && query_heads % H == 0 && query_heads / H <= 16;
+    // The guided persistent mode (KIMKV_DECODE_GUIDED) is not chosen here: at
+    // 128 lanes x 32k tokens it measured 0.638 ms per launch (six slices) and
+    // 0.652 ms (three) against 0.628 ms for one head-split chunk per lane on
+    // the same MI355X; callers may still request it explicitly.
+    bool const head_split = per_block < longest && per_head >= longest && fast_shape;
     uint64_t target = head_split ? longest : per_block;
     if (target < kMinChunk) target = kMinChunk;
     if (target > kMaxChunk) target = kMaxChunk;
@@ -886,12 +1018,18 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
     return KIMKV_OK;
 }
 
+uint32_t kimkv_decode_lane_chunks(uint32_t token_count, uint32_t chunk_tokens, uint32_t head_dim)
+{
+    if ((chunk_tokens & KIMKV_DECODE_GUIDED) != 0) return guided_slices(token_count, head_dim);
+    chunk_tokens &= ~(KIMKV_DECODE_HEAD_SPLIT | KIMKV_DECODE_GUIDED);
+    if (chunk_tokens == 0) return 0;
+    return static_cast<uint32_t>((static_cast<uint64_t>(token_count) + chunk_tokens - 1) / chunk_tokens);
+}
+
 size_t kimkv_decode_workspace_bytes(uint32_t token_count, uint32_t chunk_tokens, uint32_t query_heads,
                                     uint32_t head_dim)
 {
-    chunk_tokens &= ~KIMKV_DECODE_HEAD_SPLIT;
-    if (chunk_tokens == 0) return 0;
-    uint64_t const chunks = (static_cast<uint64_t>(token_count) + chunk_tokens - 1) / chunk_tokens;
+    uint64_t const chunks = kimkv_decode_lane_chunks(token_count, chunk_tokens, head_dim);
     if (chunks <= 1) return 0;
     return static_cast<size_t>(chunks * query_heads * (head_dim + 2ull) * sizeof(float));
 }

@@ -8,9 +8,16 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
+#include <atomic>
 #include <cstdint>
 
 #include "kimkv_hip.h"
+
+// Work-counter slots of persistent launches: a launch takes the next slot
+// round-robin and its last workgroup resets it, so a slot is reused only
+// after that many later launches (in-order streams never overlap on one).
+constexpr uint32_t kWorkCounterSlots = 64;
+constexpr uint32_t kWorkCounterStride = 64;   // words: one slot per 256-byte line
 
 struct kimkv_storage {
     kimkv_layout layout{};
@@ -23,6 +30,8 @@ struct kimkv_storage {
     uint16_t* micro{nullptr};
     uint16_t* extent{nullptr};
     uint32_t* faults{nullptr};        // device word, KIMKV_FAULT_* bits
+    uint32_t* work_counters{nullptr}; // kWorkCounterSlots slots of kWorkCounterStride words
+    mutable std::atomic<uint32_t> next_work_counter{0};
     uint32_t* fault_host{nullptr};    // mapped pinned word kimkv_storage_faults reads
     uint32_t* fault_view{nullptr};    // its device address
     int device{0};

@@ -310,6 +310,11 @@ kimkv_status kimkv_storage_create(kimkv_storage** out, kimkv_layout layout, uint
         e = hipMalloc(reinterpret_cast<void**>(&s->faults), 256);
         if (e == hipSuccess) e = hipMemset(s->faults, 0, 256);
     }
+    size_t const counter_bytes = sizeof(uint32_t) * kWorkCounterSlots * kWorkCounterStride;
+    if (e == hipSuccess) {
+        e = hipMalloc(reinterpret_cast<void**>(&s->work_counters), counter_bytes);
+        if (e == hipSuccess) e = hipMemset(s->work_counters, 0, counter_bytes);
+    }
     if (e == hipSuccess) {
         e = hipHostMalloc(reinterpret_cast<void**>(&s->fault_host), 256, hipHostMallocMapped | hipHostMallocCoherent);
         if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void**>(&s->fault_view), s->fault_host, 0);
@@ -320,6 +325,7 @@ kimkv_status kimkv_storage_create(kimkv_storage** out, kimkv_layout layout, uint
         if (s->micro) static_cast<void>(hipFree(s->micro));
         if (s->extent) static_cast<void>(hipFree(s->extent));
         if (s->faults) static_cast<void>(hipFree(s->faults));
+        if (s->work_counters) static_cast<void>(hipFree(s->work_counters));
         if (s->fault_host) static_cast<void>(hipHostFree(s->fault_host));
         delete s;
         return KIMKV_ALLOCATION_FAILED;
@@ -336,6 +342,7 @@ kimkv_status kimkv_storage_destroy(kimkv_storage* storage)
     if (storage->micro) static_cast<void>(hipFree(storage->micro));
     if (storage->extent) static_cast<void>(hipFree(storage->extent));
     if (storage->faults) static_cast<void>(hipFree(storage->faults));
+    if (storage->work_counters) static_cast<void>(hipFree(storage->work_counters));
     if (storage->fault_host) static_cast<void>(hipHostFree(storage->fault_host));
     delete storage;
     return KIMKV_OK;

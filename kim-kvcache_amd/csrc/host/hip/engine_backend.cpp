@@ -292,8 +292,7 @@ public:
         // Prefix over the surviving lanes with the chunk length their workspaces
         // were checked against (re-planning could shrink it and overflow them).
         std::vector<std::uint32_t> pre(n + 1, 0);
-        std::uint32_t const length = chunk & ~KIMKV_DECODE_HEAD_SPLIT;
-        for (std::size_t i = 0; i < n; ++i) pre[i + 1] = pre[i] + (launch_tokens[i] + length - 1) / length;
+        for (std::size_t i = 0; i < n; ++i) pre[i + 1] = pre[i] + kimkv_decode_lane_chunks(launch_tokens[i], chunk, D);
         total = pre[n];
         // Items and chunk prefix are staged together in pinned host memory
         // that the kernels read directly (a copy command on the stream would

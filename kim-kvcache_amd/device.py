@@ -122,6 +122,7 @@ _SIGNATURES = {
                                          ctypes.POINTER(ctypes.c_uint32)]),
     "kimkv_decode_workspace_bytes": (ctypes.c_size_t, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                        ctypes.c_uint32]),
+    "kimkv_decode_lane_chunks": (ctypes.c_uint32, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
     "kimkv_paged_decode_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                 ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                 ctypes.c_uint32, ctypes.c_void_p]),
@@ -423,6 +424,8 @@ def prefill_order(kv_heads: int, head_dim: int, query_heads: int, compute_units:
 
 
 DECODE_HEAD_SPLIT = 0x80000000
+DECODE_GUIDED = 0x40000000
+DECODE_GUIDED_SLICES = 6
 
 # Fault bits of kimkv_storage_faults (include/kimkv_hip.h).
 FAULT_APPEND_JOB = 0x1
@@ -433,7 +436,8 @@ FAULT_PROMOTION_JOB = 0x8
 
 def decode_plan(storage_handle: int, token_counts, query_heads: int):
     """kimkv_decode_plan: (chunk_tokens, chunk prefix over lanes, total chunks).  chunk_tokens may carry
-    DECODE_HEAD_SPLIT (one kv head per workgroup); pass it to the launch and workspace_bytes unchanged."""
+    DECODE_HEAD_SPLIT (one kv head per workgroup) or DECODE_GUIDED (persistent slices); pass it to the
+    launch, workspace_bytes and lane_chunks unchanged."""
     counts = np.ascontiguousarray(np.asarray(token_counts, dtype=np.uint32))
     prefix = np.zeros(len(counts) + 1, dtype=np.uint32)
     chunk = ctypes.c_uint32()
@@ -446,6 +450,25 @@ def decode_plan(storage_handle: int, token_counts, query_heads: int):
 
 def workspace_bytes(token_count: int, chunk_tokens: int, query_heads: int, head_dim: int) -> int:
     return int(lib().kimkv_decode_workspace_bytes(token_count, chunk_tokens, query_heads, head_dim))
+
+
+def lane_chunks(token_count: int, chunk_tokens: int, head_dim: int) -> int:
+    """kimkv_decode_lane_chunks: a lane's chunk (partial slot) count under a planned chunk_tokens."""
+    return int(lib().kimkv_decode_lane_chunks(token_count, chunk_tokens, head_dim))
+
+
+def chunk_prefix(token_counts, chunk_tokens: int, head_dim: int) -> np.ndarray:
+    """Running chunk counts over lanes for a chunk_tokens value chosen by the caller."""
+    prefix = np.zeros(len(token_counts) + 1, dtype=np.uint32)
+    prefix[1:] = np.cumsum([lane_chunks(int(t), chunk_tokens, head_dim) for t in token_counts])
+    return prefix
+
+
+def decode_mode(chunk_tokens: int) -> str:
+    """'guided', 'head_split' or 'chunked' for a planned chunk_tokens value."""
+    if chunk_tokens & DECODE_GUIDED:
+        return "guided"
+    return "head_split" if chunk_tokens & DECODE_HEAD_SPLIT else "chunked"
 
 
 def linear(x_ptr: int, rows: int, in_features: int, w_ptr: int, out_features: int, y_ptr: int, y_f32: bool,

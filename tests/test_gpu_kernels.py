@@ -145,8 +145,7 @@ def _run_decode(dev, storage, lanes, query_heads, stream=None, chunk=None):
     if chunk is None:
         chunk, prefix, total = storage.decode_plan(counts, query_heads)
     else:
-        length = chunk & ~dev.DECODE_HEAD_SPLIT
-        prefix = np.concatenate([[0], np.cumsum([(t + length - 1) // length for t in counts])]).astype(np.uint32)
+        prefix = dev.chunk_prefix(counts, chunk, storage.head_dim)
         total = int(prefix[-1])
     keep = []
     items = np.zeros(len(lanes), dtype=dev.DECODE_ITEM)
@@ -168,7 +167,7 @@ def _run_decode(dev, storage, lanes, query_heads, stream=None, chunk=None):
 
 
 def _decode_case(dev, shape, token_counts, G, micro_tokens=8, extent_tokens=64, layer=None, seed=1,
-                 uniform_pages=None, chunk=None):
+                 uniform_pages=None, chunk=None, repeat=1):
     L, H, D = shape
     QH = H * G
     micro_cap = sum(t // micro_tokens + 2 for t in token_counts) + 8
@@ -189,14 +188,20 @@ def _decode_case(dev, shape, token_counts, G, micro_tokens=8, extent_tokens=64, 
         q = oracle.synth_rows(QH * D, seed * 1000 + i, 0, D)
         lay = (i * 7) % L if layer is None else layer
         lanes.append((table, T, lay, q, 1.0 / math.sqrt(D)))
-    outs, chunk, total = _run_decode(dev, storage, lanes, QH, chunk=chunk)
+    wants = [pools.paged_decode(table, T, lay, QH, q, scale, f32=True) for (table, T, lay, q, scale) in lanes]
     worst = 0.0
-    for (table, T, lay, q, scale), got in zip(lanes, outs):
-        want = pools.paged_decode(table, T, lay, QH, q, scale, f32=True)
-        worst = max(worst, helpers.assert_attention_close(got, want))
-    split = "+split" if chunk & dev.DECODE_HEAD_SPLIT else ""
-    print(f"decode shape={shape} G={G} T={token_counts} chunk={chunk & ~dev.DECODE_HEAD_SPLIT}{split} chunks={total} "
-          f"max_err={worst:.2e}", flush=True)
+    first = None
+    for _ in range(repeat):
+        outs, planned, total = _run_decode(dev, storage, lanes, QH, chunk=chunk)
+        for got, want in zip(outs, wants):
+            worst = max(worst, helpers.assert_attention_close(got, want))
+        if first is None:
+            first = outs
+        else:   # every launch of the same batch gives the same bits
+            assert all(np.array_equal(a, b) for a, b in zip(first, outs))
+    chunk = planned
+    print(f"decode shape={shape} G={G} T={token_counts} chunk={chunk & 0x3FFFFFFF} mode={dev.decode_mode(chunk)} "
+          f"chunks={total} max_err={worst:.2e}", flush=True)
     return chunk, total
 
 
@@ -236,8 +241,9 @@ def test_decode_plan_balances_long_lanes(dev):
     cus = storage.info().compute_units
     H = 4
     for lanes, T in [(256, 32769), (128, 32769), (64, 32769), (256, 32768), (60, 1600), (3, 12345), (1, 1),
-                     (4, 200000)]:
+                     (4, 200000), (64, 8192), (60, 20000)]:
         flags, prefix, total = storage.decode_plan([T] * lanes, 32)
+        assert not flags & dev.DECODE_GUIDED, (lanes, T, flags)   # the guided mode is opt-in
         split = bool(flags & dev.DECODE_HEAD_SPLIT)
         chunk = flags & ~dev.DECODE_HEAD_SPLIT
         n = (T + chunk - 1) // chunk
@@ -256,6 +262,31 @@ def test_decode_plan_balances_long_lanes(dev):
     flags, prefix, total = storage.decode_plan(ragged, 32)
     chunk = flags & ~dev.DECODE_HEAD_SPLIT
     assert total == sum((t + chunk - 1) // chunk for t in ragged)
+    # Guided lanes: min(6, max(1, T / (D + 2))) slices, so a lane's partials
+    # never exceed the reference's QH * T float workspace.
+    for T in [1, 65, 66, 131, 132, 395, 396, 1000, 32769]:
+        n = dev.lane_chunks(T, dev.DECODE_GUIDED | 64, 64)
+        assert n == min(6, max(1, T // 66)), (T, n)
+        assert dev.workspace_bytes(T, dev.DECODE_GUIDED | 64, 32, 64) <= 32 * T * 4
+
+
+def test_decode_guided_slices(dev):
+    # Persistent workgroups taking (slice, lane, kv head) units from the
+    # device counter: ragged lanes with one to six slices (one-slice lanes
+    # written directly, empty slices from 64-alignment), the longest slices
+    # the table holds (T/2 <= 65536), group sizes 16 and 1, generic head dims
+    # and unaligned pages (generic wave path), and many launches in a row
+    # (counter slots reused after their reset).
+    GU = dev.DECODE_GUIDED | 64
+    _decode_case(dev, (2, 4, 64), [1, 5, 66, 100, 131, 396, 397, 4000, 12345, 33000], G=8, seed=60, chunk=GU)
+    _decode_case(dev, (1, 4, 64), [130000, 70000, 64, 8193], G=8, seed=61, chunk=GU)
+    _decode_case(dev, (2, 2, 64), [700, 9000], G=16, seed=62, chunk=GU)
+    _decode_case(dev, (2, 8, 64), [333, 5000], G=1, seed=63, chunk=GU)
+    _decode_case(dev, (1, 2, 128), [90, 1500, 3000], G=4, seed=64, chunk=GU)
+    _decode_case(dev, (2, 4, 64), [17, 200, 3000], G=8, micro_tokens=6, extent_tokens=48, seed=65,
+                 uniform_pages=True, chunk=GU)
+    # 70 launches on one storage: its 64 counter slots are reused after their reset.
+    _decode_case(dev, (1, 4, 64), [300, 1000, 2500], G=8, seed=66, chunk=GU, repeat=70)
 
 
 def test_decode_long_chunks(dev):
