@@ -4,7 +4,7 @@
 // (counterpart of createCudaTinyLlamaModelRunner, src/cuda/model/
 // runner_factory.cpp:56-196, and the batched forward of src/cuda/model/
 // runner.cpp:410-848).  Weights are seeded N(0, 0.02) fp16 (RMSNorm weights
-// one) instead of a loaded checkpoint.  One forward call takes spans: a
+// one), or loaded from a checkpoint archive described by a weight manifest.  One forward call takes spans: a
 // decode step (one position) goes through a token transaction and the fused
 // split-K decode kernel, a prompt chunk (several positions) through a
 // PrefillChunk and the MFMA chunked-prefill kernel; the dense layers run on
@@ -13,6 +13,7 @@
 
 #include "kim-kv/engine/generation.h"
 #include "kim-kv/hip/hip_status.h"
+#include "kim-kv/model/weight_manifest.h"
 
 #include <cstdint>
 #include <memory>
@@ -35,6 +36,16 @@ public:
     // and sets *error on a shape mismatch or an allocation failure.
     static std::unique_ptr<HipTinyLlamaRunner> create(EngineKvBackend& kv, HipModelRunnerConfig const& config,
                                                       HipStream stream, std::string* error);
+    // Weights from a checkpoint archive instead of the seed (the reference's
+    // createCudaTinyLlamaModelRunner(kv, manifest_path, data_path, ...),
+    // src/cuda/model/runner_factory.cpp:11-196): the manifest is loaded and
+    // validated, every tensor range of the data file is checked against its
+    // SHA-256, the model dimensions come from the manifest, and the tensors
+    // are copied into the runner's fused q|k|v and gate|up matrices.
+    static std::unique_ptr<HipTinyLlamaRunner> createFromArchive(EngineKvBackend& kv, std::string const& manifest_path,
+                                                                 std::string const& data_path,
+                                                                 std::uint32_t max_positions, std::uint32_t max_spans,
+                                                                 HipStream stream, std::string* error);
     ~HipTinyLlamaRunner() override;
 
     TinyLlamaConfig generationConfig() const noexcept override;

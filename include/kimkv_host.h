@@ -280,6 +280,16 @@ typedef struct kimkv_model_config {
 /* NULL on a shape mismatch with the engine or an allocation failure. */
 kimkv_runner* kimkv_runner_create(kimkv_engine* e, const kimkv_model_config* model, uint64_t weight_seed,
                                   uint32_t max_positions, uint32_t max_spans, kimkv_stream_t stream);
+/* A runner whose weights come from a checkpoint archive: manifest_path is the
+ * weight manifest (include/kim-kv/model/weight_manifest.h), data_path its
+ * fp16 data file; the model dimensions are the manifest's.  On failure
+ * returns NULL and writes a NUL-terminated reason into error (when
+ * error_capacity > 0).  Counterpart of the reference's
+ * createCudaTinyLlamaModelRunner(kv, manifest_path, data_path, ...)
+ * (src/cuda/model/runner_factory.cpp:11-196). */
+kimkv_runner* kimkv_runner_create_from_archive(kimkv_engine* e, const char* manifest_path, const char* data_path,
+                                               uint32_t max_positions, uint32_t max_spans, kimkv_stream_t stream,
+                                               char* error, size_t error_capacity);
 void kimkv_runner_destroy(kimkv_runner* r);
 uint64_t kimkv_runner_weight_bytes(const kimkv_runner* r);
 /* One forward over span_count spans (span i: request_ids[i], positions

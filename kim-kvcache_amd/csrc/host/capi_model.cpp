@@ -7,7 +7,9 @@
 #include "kim-kv/hip/hip_model_runner.h"
 
 #include <algorithm>
+#include <cstring>
 #include <memory>
+#include <string>
 #include <new>
 #include <vector>
 
@@ -45,6 +47,28 @@ kimkv_runner* kimkv_runner_create(kimkv_engine* e, const kimkv_model_config* mod
     } catch (...) {
         return nullptr;
     }
+}
+
+kimkv_runner* kimkv_runner_create_from_archive(kimkv_engine* e, const char* manifest_path, const char* data_path,
+                                               uint32_t max_positions, uint32_t max_spans, kimkv_stream_t stream,
+                                               char* error, size_t error_capacity)
+{
+    if (error != nullptr && error_capacity != 0) error[0] = '\0';
+    if (e == nullptr || manifest_path == nullptr || data_path == nullptr) return nullptr;
+    std::string message;
+    try {
+        std::unique_ptr<HipTinyLlamaRunner> r = HipTinyLlamaRunner::createFromArchive(
+            *e->backend, manifest_path, data_path, max_positions, max_spans, stream, &message);
+        if (r != nullptr) return new kimkv_runner{std::move(r)};
+    } catch (...) {
+        message = "unexpected exception";
+    }
+    if (error != nullptr && error_capacity != 0) {
+        std::size_t const n = std::min(message.size(), error_capacity - 1);
+        std::memcpy(error, message.data(), n);
+        error[n] = '\0';
+    }
+    return nullptr;
 }
 
 void kimkv_runner_destroy(kimkv_runner* r) { delete r; }

@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <fstream>
 #include <new>
 #include <utility>
 
@@ -209,6 +210,83 @@ struct HipTinyLlamaRunner::Impl {
         ones(final_norm, H);
         fill(head, V, H, weightRow(m.layer_count, kHead));
         return ok && kimkv_stream_synchronize(stream) == KIMKV_OK;
+    }
+
+    // Copies every tensor of a validated archive to its place in the weight
+    // block (fused q|k|v and gate|up rows), through a pinned staging buffer
+    // in pieces of at most kStagePiece bytes.
+    bool loadArchive(WeightManifest const& manifest, std::string const& data_path, std::string* error)
+    {
+        TinyLlamaConfig const& m = cfg.model;
+        std::uint64_t const H = m.hidden_size, I = m.intermediate_size;
+        auto target = [&](std::string const& name) -> std::uint16_t* {
+            if (name == "model.embed_tokens.weight") return embed;
+            if (name == "model.norm.weight") return final_norm;
+            if (name == "lm_head.weight") return head;
+            std::string const prefix = "model.layers.";
+            if (name.compare(0, prefix.size(), prefix) != 0) return nullptr;
+            std::size_t dot = name.find('.', prefix.size());
+            if (dot == std::string::npos) return nullptr;
+            std::uint32_t l = 0;
+            for (std::size_t i = prefix.size(); i < dot; ++i) {
+                if (name[i] < '0' || name[i] > '9') return nullptr;
+                l = l * 10 + static_cast<std::uint32_t>(name[i] - '0');
+                if (l >= layers.size()) return nullptr;
+            }
+            Layer const& L = layers[l];
+            std::string const part = name.substr(dot + 1);
+            if (part == "input_layernorm.weight") return L.ln1;
+            if (part == "post_attention_layernorm.weight") return L.ln2;
+            if (part == "self_attn.q_proj.weight") return L.wqkv;
+            if (part == "self_attn.k_proj.weight") return L.wqkv + std::uint64_t{QD} * H;
+            if (part == "self_attn.v_proj.weight") return L.wqkv + std::uint64_t{QD + KD} * H;
+            if (part == "self_attn.o_proj.weight") return L.wo;
+            if (part == "mlp.gate_proj.weight") return L.wgu;
+            if (part == "mlp.up_proj.weight") return L.wgu + I * H;
+            if (part == "mlp.down_proj.weight") return L.wdown;
+            return nullptr;
+        };
+        constexpr std::size_t kStagePiece = std::size_t{32} << 20;
+        void* stage = nullptr;
+        if (kimkv_host_malloc_pinned(&stage, 2 * kStagePiece) != KIMKV_OK) {
+            if (error) *error = "pinned staging allocation failed";
+            return false;
+        }
+        std::ifstream in(data_path, std::ios::binary);
+        bool ok = static_cast<bool>(in);
+        int half = 0;
+        void* pending[2] = {nullptr, nullptr};   // an event per staging half while its copy is in flight
+        for (WeightTensorDescriptor const& t : manifest.tensors) {
+            std::uint16_t* dst = target(t.name);
+            if (!ok || dst == nullptr) {
+                ok = false;
+                break;
+            }
+            in.seekg(static_cast<std::streamoff>(t.offset));
+            for (std::uint64_t done = 0; ok && done < t.byte_size;) {
+                auto const n = static_cast<std::size_t>(std::min<std::uint64_t>(kStagePiece, t.byte_size - done));
+                auto* buf = static_cast<char*>(stage) + half * kStagePiece;
+                if (pending[half] != nullptr) {   // the copy out of this half must finish before it is refilled
+                    ok = kimkv_event_synchronize(pending[half]) == KIMKV_OK;
+                    kimkv_event_destroy(pending[half]);
+                    pending[half] = nullptr;
+                }
+                in.read(buf, static_cast<std::streamsize>(n));
+                ok = ok && in.gcount() == static_cast<std::streamsize>(n)
+                    && kimkv_memcpy_h2d_async(reinterpret_cast<char*>(dst) + done, buf, n, stream) == KIMKV_OK
+                    && kimkv_event_create(&pending[half], 0) == KIMKV_OK
+                    && kimkv_event_record(pending[half], stream) == KIMKV_OK;
+                done += n;
+                half ^= 1;
+            }
+        }
+        ok = kimkv_stream_synchronize(stream) == KIMKV_OK && ok;
+        for (void* e : pending) {
+            if (e != nullptr) kimkv_event_destroy(e);
+        }
+        kimkv_host_free_pinned(stage);
+        if (!ok && error) *error = "reading the weight archive into device memory failed";
+        return ok;
     }
 
     GenerationBatchResult forward(std::vector<GenerationSpan> const& spans, float* host_logits);
@@ -477,6 +555,50 @@ std::unique_ptr<HipTinyLlamaRunner> HipTinyLlamaRunner::create(EngineKvBackend& 
         if (error) *error = "weight initialisation failed";
         return nullptr;
     }
+    if (!impl->tuneGemms()) {
+        if (error) *error = "GEMM algorithm selection failed";
+        return nullptr;
+    }
+    return std::unique_ptr<HipTinyLlamaRunner>(new HipTinyLlamaRunner(std::move(impl)));
+}
+
+std::unique_ptr<HipTinyLlamaRunner> HipTinyLlamaRunner::createFromArchive(EngineKvBackend& kv,
+                                                                          std::string const& manifest_path,
+                                                                          std::string const& data_path,
+                                                                          std::uint32_t max_positions,
+                                                                          std::uint32_t max_spans, HipStream stream,
+                                                                          std::string* error)
+{
+    WeightManifestLoadResult loaded = loadWeightManifest(manifest_path);
+    if (!loaded.ok()) {
+        if (error) *error = "weight manifest: " + std::string(toString(loaded.status.error)) + ": " + loaded.status.detail;
+        return nullptr;
+    }
+    WeightManifestStatus const data = validateWeightDataFile(loaded.manifest, data_path);
+    if (!data.ok()) {
+        if (error) *error = "weight archive: " + std::string(toString(data.error)) + ": " + data.detail;
+        return nullptr;
+    }
+    TinyLlamaConfig const& m = loaded.manifest.config;
+    EngineKvConfig const e = kv.config();
+    if (max_positions == 0 || max_spans == 0) {
+        if (error) *error = "invalid runner configuration";
+        return nullptr;
+    }
+    if (e.kv_layout.layer_count != m.layer_count || e.kv_layout.kv_head_count != m.kv_head_count
+        || e.kv_layout.head_dimension != m.head_dimension || e.query_head_count != m.attention_head_count) {
+        if (error) *error = "KV backend layout does not match the model manifest";
+        return nullptr;
+    }
+    auto impl = std::make_unique<Impl>();
+    impl->kv = &kv;
+    impl->cfg = HipModelRunnerConfig{m, 0, max_positions, max_spans};
+    impl->stream = stream;
+    impl->QD = m.attention_head_count * m.head_dimension;
+    impl->KD = m.kv_head_count * m.head_dimension;
+    impl->W_qkv = impl->QD + 2 * impl->KD;
+    impl->ws_lane = (e.attention_workspace_bytes + 255) & ~std::size_t{255};
+    if (!impl->allocate(error) || !impl->loadArchive(loaded.manifest, data_path, error)) return nullptr;
     if (!impl->tuneGemms()) {
         if (error) *error = "GEMM algorithm selection failed";
         return nullptr;

@@ -143,6 +143,8 @@ _SIG = {
     "kimkv_prefill_attend_batch": (None, [ctypes.POINTER(P), U32, U32, ctypes.POINTER(P), ctypes.POINTER(P),
                                           ctypes.c_float, ctypes.POINTER(I)]),
     "kimkv_runner_create": (P, [P, ctypes.POINTER(ModelConfig), U64, U32, U32, P]),
+    "kimkv_runner_create_from_archive": (P, [P, ctypes.c_char_p, ctypes.c_char_p, U32, U32, P, ctypes.c_char_p,
+                                             ctypes.c_size_t]),
     "kimkv_runner_destroy": (None, [P]),
     "kimkv_runner_weight_bytes": (U64, [P]),
     "kimkv_runner_forward": (I, [P, U32, P, P, P, P, P, P, P]),
@@ -574,7 +576,8 @@ class LaneBatch:
 
 
 class Runner:
-    """HipTinyLlamaRunner (seeded N(0, 0.02) fp16 weights) on an Engine."""
+    """HipTinyLlamaRunner on an Engine: seeded N(0, 0.02) fp16 weights, or a
+    checkpoint archive (Runner.from_archive)."""
 
     def __init__(self, engine: "Engine", model: ModelConfig, seed: int, max_positions: int, max_spans: int,
                  stream: Optional[device.Stream] = None):
@@ -583,6 +586,21 @@ class Runner:
                                            stream.handle if stream else None)
         if not self.h:
             raise RuntimeError("model runner creation failed")
+
+    @classmethod
+    def from_archive(cls, engine: "Engine", model: ModelConfig, manifest_path: str, data_path: str,
+                     max_positions: int, max_spans: int, stream: Optional[device.Stream] = None) -> "Runner":
+        """Weights from a weight manifest + fp16 data file (model: the manifest's dimensions, for the caller's
+        bookkeeping; the library takes them from the manifest).  Raises with the library's reason."""
+        self = cls.__new__(cls)
+        self.engine, self.model = engine, model
+        reason = ctypes.create_string_buffer(512)
+        self.h = lib().kimkv_runner_create_from_archive(engine.h, manifest_path.encode(), data_path.encode(),
+                                                        max_positions, max_spans, stream.handle if stream else None,
+                                                        reason, len(reason))
+        if not self.h:
+            raise RuntimeError("model runner creation failed: " + reason.value.decode())
+        return self
 
     def weight_bytes(self) -> int:
         return lib().kimkv_runner_weight_bytes(self.h)

@@ -62,7 +62,7 @@ def build_reference() -> str | None:
 
 
 # Reference tests whose includes this build provides (the fixed-size page
-# strategy and the weight manifest are not part of it).
+# strategy is not part of it).
 REFERENCE_CONTRACTS = (
     "core/page_pool_test",
     "runtime/block_table_test",
@@ -72,6 +72,7 @@ REFERENCE_CONTRACTS = (
     "engine/generation_runtime_test",
     "engine/iteration_scheduler_test",
     "reference/kv_reference_test",
+    "model/weight_manifest_test",
 )
 
 

@@ -11,7 +11,7 @@ import pytest
 BIN = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "kim-kvcache_amd", "_lib", "tests")
 
 
-@pytest.mark.parametrize("name", ["generation_contract_test", "staging_ring_test", "kv_reference_test"])
+@pytest.mark.parametrize("name", ["generation_contract_test", "staging_ring_test", "kv_reference_test", "sha256_test"])
 def test_cpp_contract(name):
     path = os.path.join(BIN, name)
     if not os.path.exists(path):

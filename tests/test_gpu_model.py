@@ -177,3 +177,87 @@ def test_linear_matches_fp32_reference(dev):
             err = np.abs(got - want)
             assert np.all(err <= 1e-4 + rel * np.abs(want)), (tune, y_f32, beta, float(err.max()))
     print(f"linear {rows}x{fin}x{fout}: within fp32-accumulate + fp16 rounding", flush=True)
+
+
+def _write_archive(directory, cfg, seed, corrupt=False):
+    """The seeded runner's weights as a checkpoint archive: fp16 data file plus
+    weight manifest (Hugging Face Llama tensor names, per-tensor SHA-256)."""
+    import hashlib
+    import os
+    from oracle import f32_to_f16
+    H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocabulary_size
+    QD = cfg.attention_head_count * cfg.head_dimension
+    KD = cfg.kv_head_count * cfg.head_dimension
+    ones = np.full(H, 0x3C00, dtype=np.uint16)
+    tensors = [("model.embed_tokens.weight", f32_to_f16(om.seeded_weight(seed, V, H, om.weight_row(cfg.layer_count, "embed")))),
+               ("model.norm.weight", ones),
+               ("lm_head.weight", f32_to_f16(om.seeded_weight(seed, V, H, om.weight_row(cfg.layer_count, "head"))))]
+    shapes = {"q": (QD, H), "k": (KD, H), "v": (KD, H), "o": (H, H), "gate": (I, H), "up": (I, H), "down": (H, I)}
+    names = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self_attn.v_proj", "o": "self_attn.o_proj",
+             "gate": "mlp.gate_proj", "up": "mlp.up_proj", "down": "mlp.down_proj"}
+    for l in range(cfg.layer_count):
+        p = f"model.layers.{l}."
+        tensors.append((p + "input_layernorm.weight", ones))
+        tensors.append((p + "post_attention_layernorm.weight", ones))
+        for kind, (rows, cols) in shapes.items():
+            tensors.append((p + names[kind] + ".weight",
+                            f32_to_f16(om.seeded_weight(seed, rows, cols, om.weight_row(l, kind)))))
+    data_path = os.path.join(directory, "weights.bin")
+    lines, offset = [], 0
+    with open(data_path, "wb") as f:
+        for name, t in tensors:
+            raw = np.ascontiguousarray(t, dtype=np.uint16).tobytes()
+            shape = ",".join(str(d) for d in (t.shape if t.ndim == 2 else (t.size,)))
+            lines.append(f"tensor={name}|{offset}|{len(raw)}|{shape}|{hashlib.sha256(raw).hexdigest()}")
+            f.write(raw)
+            offset += len(raw)
+    if corrupt:
+        with open(data_path, "r+b") as f:
+            f.seek(offset // 2)
+            b = f.read(1)
+            f.seek(offset // 2)
+            f.write(bytes([b[0] ^ 1]))
+    manifest = [f"version=1", "checkpoint=synthetic/tinyllama-shaped", "checkpoint_revision=seeded",
+                "tokenizer_revision=none", "config_sha256=" + "0" * 64, "dtype=fp16", "data_file=weights.bin",
+                f"data_bytes={offset}", f"hidden_size={H}", f"intermediate_size={I}",
+                f"layer_count={cfg.layer_count}", f"attention_head_count={cfg.attention_head_count}",
+                f"kv_head_count={cfg.kv_head_count}", f"head_dimension={cfg.head_dimension}",
+                f"vocabulary_size={V}", f"max_position_embeddings={cfg.max_position_embeddings}",
+                f"bos_token_id={cfg.bos_token_id}", f"eos_token_id={cfg.eos_token_id}",
+                f"rms_norm_epsilon={cfg.rms_norm_epsilon}", f"rope_theta={cfg.rope_theta}",
+                "tied_word_embeddings=0", f"tensor_count={len(tensors)}"] + lines
+    manifest_path = os.path.join(directory, "weights.manifest")
+    with open(manifest_path, "w") as f:
+        f.write("\n".join(manifest) + "\n")
+    return manifest_path, data_path
+
+
+def test_runner_from_archive_matches_seeded_runner(host, dev, tmp_path):
+    """A runner loaded from a checkpoint archive (weight manifest + fp16 data,
+    every tensor hashed) holding the seeded weights gives the seeded runner's
+    logits bit for bit, and the oracle's within 0.035; a corrupted archive is
+    refused with a checksum mismatch."""
+    manifest_path, data_path = _write_archive(str(tmp_path), CFG, SEED)
+    engine, seeded, stream = make(host, dev)
+    loaded = host.Runner.from_archive(engine, model_config(host), manifest_path, data_path, 256, 8, stream)
+    assert engine.create_request(1) == 0 and engine.create_request(2) == 0
+    rng = np.random.default_rng(17)
+    prompt = [int(t) for t in rng.integers(3, CFG.vocabulary_size, 21)]
+    ref = om.ReferenceModel(CFG, SEED)
+    na, _, la = seeded.forward([(1, 0, prompt)], want_logits=True)
+    nb, _, lb = loaded.forward([(2, 0, prompt)], want_logits=True)
+    assert np.array_equal(la, lb)
+    for p, t in enumerate(prompt):
+        want = ref.forward(t, p)
+    check_logits(lb[0], want, "archive chunk")
+    na, _, la = seeded.forward([(1, len(prompt), [int(na[0])])], want_logits=True)
+    nb, _, lb = loaded.forward([(2, len(prompt), [int(nb[0])])], want_logits=True)
+    assert np.array_equal(la, lb) and int(na[0]) == int(nb[0])
+    bad_dir = tmp_path / "corrupt"
+    bad_dir.mkdir()
+    bad_manifest, bad_data = _write_archive(str(bad_dir), CFG, SEED, corrupt=True)
+    with pytest.raises(RuntimeError, match="checksum_mismatch"):
+        host.Runner.from_archive(engine, model_config(host), bad_manifest, bad_data, 256, 8, stream)
+    for r in (seeded, loaded):
+        r.close()
+    stream.destroy()

@@ -2,8 +2,8 @@
 this build's headers and linked with its libkimkv.so (oracle/build.py,
 build_reference_contracts): page pool, block table / COW / fork, page
 leases, promotion, the engine SPI transaction contract, the generation
-runtime, the iteration scheduler and the binary16 codec + reference
-attention.  Each binary must exit 0.  Skipped where the reference tree (and
+runtime, the iteration scheduler, the binary16 codec + reference attention
+and the weight manifest.  Each binary must exit 0.  Skipped where the reference tree (and
 so the binaries) is absent."""
 import os
 import subprocess
@@ -13,7 +13,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(ROOT, "oracle", "_ref", "contracts")
 NAMES = ["page_pool_test", "block_table_test", "page_lease_test", "promotion_test", "engine_kv_contract_test",
-         "generation_runtime_test", "iteration_scheduler_test", "kv_reference_test"]
+         "generation_runtime_test", "iteration_scheduler_test", "kv_reference_test", "weight_manifest_test"]
 
 
 @pytest.mark.parametrize("name", NAMES)
