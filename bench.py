@@ -454,14 +454,66 @@ def run_gather(dev, args) -> int:
         l, c, t = int(rng.integers(L)), int(rng.integers(2)), int(rng.integers(T))
         want = oracle.synth_rows(H * D, args.seed, oracle.kv_row(0, l, c, t), H * D)
         bad += int(not np.array_equal(got[l, c, t], want))
+    cpu = cpu_gather_baseline(args, entries, T, L, H, D, moved) if args.cpu_lanes > 0 else None
     print(json.dumps({
         "metric": "long-sequence gather (paged -> contiguous) GB/s", "value": round(moved / (ms * 1e-3) / 1e9, 1),
         "unit": "GB/s", "us_per_launch": round(ms * 1000, 2), "bytes_per_launch": moved,
         "read_bytes": n * 2, "write_bytes": n * 2, "pct_of_peak_hbm": round(100 * moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
         "config": {"workload": f"gather of one {T}-token sequence x {L} layers (4 kv heads x 64, fp16), "
                                f"{n_ext} extents in permuted slots + {k} micro pages"},
-        "steps": args.steps, "check": {"sampled_rows": 256, "mismatches": bad}}), flush=True)
+        "steps": args.steps, "check": {"sampled_rows": 256, "mismatches": bad}, "cpu_baseline": cpu}), flush=True)
     return 0 if bad == 0 else 1
+
+
+def synth_history(seed, stream_of, layers, T, H, D, threads):
+    """[len(layers)][2][T][H][D] generator rows: token t is row kv_row(stream_of(t), layer, comp, t); the
+    (layer, comp) blocks are generated on `threads` threads (the oracle's C calls release the GIL)."""
+    import oracle
+    from concurrent.futures import ThreadPoolExecutor
+    out = np.empty((len(layers), 2, T, H, D), dtype=np.uint16)
+    runs, a = [], 0
+    while a < T:
+        sid, b = stream_of(a), a + 1
+        while b < T and stream_of(b) == sid:
+            b += 1
+        runs.append((sid, a, b))
+        a = b
+
+    def fill(job):
+        li, l, c = job
+        for sid, a, b in runs:
+            out[li, c, a:b] = oracle.synth_rows((b - a) * H * D, seed, oracle.kv_row(sid, l, c, a), H * D) \
+                .reshape(b - a, H, D)
+
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        list(pool.map(fill, [(li, l, c) for li, l in enumerate(layers) for c in range(2)]))
+    return out
+
+
+def cpu_gather_baseline(args, entries, T, L, H, D, moved):
+    """The oracle's gather of the same table (same slots, same generator rows), on one host core: the
+    reference's CPU data path is single-threaded and the oracle gathers a table in one call."""
+    import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    kv = synth_history(args.seed, lambda t: 0, list(range(L)), T, H, D, threads)
+    n_ext = sum(1 for e in entries if e[5] == 1)
+    n_micro = max([e[0] for e in entries if e[5] == 0] + [0]) + 1
+    pools = oracle.HostPools(L, H, D, n_micro, n_ext)
+    table = np.array(entries, dtype=oracle.DESC)
+    for slot, _, b, n, _, kind in entries:
+        pools.append_tokens(kv, T, b, kind, slot, 0, n)
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        out = pools.gather(table, T)
+    sec = (time.perf_counter() - t0) / reps
+    if not np.array_equal(out, kv.reshape(-1)):
+        raise RuntimeError("oracle gather differs from the generator")
+    return {"value": round(moved / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "us_per_launch": round(sec * 1e6, 1),
+            "sample": f"the whole workload: oracle kvo_gather of the same {T}-token x {L}-layer table, mean of "
+                      f"{reps} calls on {platform.processor() or platform.machine()}",
+            "seconds": round(sec * reps, 2)}
 
 
 def run_append(kimkv, dev, args) -> int:
@@ -548,6 +600,26 @@ def run_append(kimkv, dev, args) -> int:
                 want = oracle.synth_rows(T * HD, args.seed, oracle.kv_row(int(i), l, c, 0), HD).reshape(T, HD)
                 bad += int(not np.array_equal(got[l, c], want))
         checked += 1
+    # CPU baseline: the same step's page writes by the oracle (one
+    # kvo_append_tokens call per lane writes its token in all layers).
+    pools = oracle.HostPools(L, H, D, lanes, 1)
+    steps_cpu = 200
+    newrows = np.empty((lanes, L, 2, 1, H, D), dtype=np.uint16)
+    for i in range(lanes):
+        for l in range(L):
+            for c in range(2):
+                newrows[i, l, c, 0] = oracle.synth_rows(HD, args.seed, oracle.kv_row(i, l, c, int(lengths[i])),
+                                                        HD).reshape(H, D)
+    t0 = time.perf_counter()
+    for s_ in range(steps_cpu):
+        for i in range(lanes):
+            pools.append_tokens(newrows[i], 1, 0, 0, i, s_ % 8, 1)
+    cpu_us = (time.perf_counter() - t0) * 1e6 / steps_cpu
+    cpu = {"value": round(cpu_us, 2), "unit": "us/step", "cores": 1, "kind": "port",
+           "gb_per_s": round(step_bytes / (cpu_us * 1e-6) / 1e9, 3),
+           "sample": f"{steps_cpu} steps of {lanes} oracle kvo_append_tokens calls (1 token x {L} layers each) through "
+                     f"ctypes on {platform.processor() or platform.machine()}; page writes only, the page-table "
+                     f"metadata is this library's host code in both runs"}
     print(json.dumps({
         "metric": "ragged KV append (1 token x 22 layers per lane, tail allocation included) us/step",
         "value": round(wall_us, 2), "unit": "us/step", "higher_is_better": False,
@@ -557,8 +629,115 @@ def run_append(kimkv, dev, args) -> int:
                                f"fp16, micro/extent pages in permuted pool order",
                    "tokens": int(lengths.sum())},
         "steps": args.steps, "warmup": args.warmup,
-        "check": {"lanes": checked, "mismatched_rows_blocks": bad, "bit_exact": bad == 0}}), flush=True)
+        "check": {"lanes": checked, "mismatched_rows_blocks": bad, "bit_exact": bad == 0},
+        "cpu_baseline": cpu}), flush=True)
     return 0 if bad == 0 else 1
+
+
+def run_parity(kimkv, dev, args) -> int:
+    """Config 1: one TinyLlama layer (32 q / 4 kv heads x 64, fp16), 4 lanes with
+    contexts {17, 100, 513, 1000} built by bulk prefill + promotion in
+    512-slot micro and extent pools with seeded permuted slots.  One step =
+    reserve one token per lane, write its K/V, decode all 32 query heads
+    (scale 1/8), commit, through the engine's batch API.  Latency-bound: the
+    value is microseconds per step; the oracle's decode of the same 4 lanes
+    is the CPU baseline."""
+    import importlib
+    import oracle
+    host = importlib.import_module(kimkv.__name__ + ".host")
+    L, H, D, QH = 1, 4, 64, 32
+    HD, QD = H * D, QH * D
+    contexts = [17, 100, 513, 1000]
+    lanes = len(contexts)
+    total_steps = args.warmup + args.steps
+    ws_lane = max(dev.workspace_bytes(max(contexts) + total_steps, 64, QH, D), 256)
+    engine = host.Engine(L, H, D, QH, ws_lane, 512, 512)
+    for kind, sd in ((1, args.seed), (0, args.seed + 1)):
+        assert engine.permute_free_slots(kind, sd) == 0
+    stream = dev.Stream()
+    stage = dev.DeviceBuffer(L * 2 * max(contexts) * HD * 2)
+    for i, T in enumerate(contexts):
+        assert engine.create_request(i + 1) == 0
+        dev.fill_kv(stage.ptr, L, T, HD, args.seed, i, 0, stream)
+        rc, _ = engine.append_prefill(i + 1, T, stage.ptr, stream, promote=True)
+        assert rc == 0, host.ENGINE_ERRORS[rc]
+    S = total_steps
+    newkv = dev.DeviceBuffer(lanes * 2 * S * HD * 2)
+    query = dev.DeviceBuffer(lanes * S * QD * 2)
+    out = dev.DeviceBuffer(lanes * QD * 2)
+    qseed = args.seed ^ 0x51
+    for i, T in enumerate(contexts):
+        for c in range(2):
+            dev.fill_rows(newkv.ptr + 2 * ((i * 2 + c) * S * HD), S * HD, args.seed, dev.synth_kv_row(i, 0, c, T), HD)
+        dev.fill_rows(query.ptr + 2 * (i * S * QD), S * QD, qseed, dev.synth_kv_row(i, 0, 0, T), QD)
+    lane = np.arange(lanes, dtype=np.uint64)
+    ws = dev.DeviceBuffer(lanes * ws_lane)
+    b = host.LaneBatch(engine, lane + np.uint64(1), ws.ptr + lane * np.uint64(ws_lane), ws_lane, 0.125, stream)
+    b.outputs[0, :] = out.ptr + np.uint64(2 * QD) * lane
+    stream.synchronize()
+
+    def step(s_):
+        b.keys[0, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * S) + np.uint64(s_))
+        b.values[0, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * S) + np.uint64(S + s_))
+        b.queries[0, :] = query.ptr + np.uint64(2 * QD) * (lane * np.uint64(S) + np.uint64(s_))
+        b.reserve(np.array(contexts, dtype=np.uint32) + s_)
+        b.write(0)
+        b.attend(0)
+        b.commit()
+        assert not b.failed(), b.status
+
+    for s_ in range(args.warmup):
+        step(s_)
+    t0 = time.perf_counter()
+    for s_ in range(args.warmup, total_steps):
+        step(s_)
+    us = (time.perf_counter() - t0) * 1e6 / args.steps
+    got = dev.download(out.ptr, (lanes, QD), np.uint16)
+    # Oracle: the last step of every lane (history regenerated), timed on one core.
+    last = total_steps - 1
+    cases = []
+    for i, T0 in enumerate(contexts):
+        T = T0 + last + 1
+        kv = synth_history(args.seed, lambda t, i=i: i, [0], T, H, D, 1)
+        q = oracle.synth_rows(QD, qseed, oracle.kv_row(i, 0, 0, T0) + last, QD)
+        cases.append((oracle_pages_layer(kv[0], T), T, q))
+    reps = 20
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        refs = [pools.paged_decode(table, T, 0, QH, q, 0.125, f32=True) for (pools, table), T, q in cases]
+    cpu_us = (time.perf_counter() - t0) * 1e6 / reps
+    worst, ok = 0.0, True
+    for i, ref in enumerate(refs):
+        err = np.abs(got[i].view(np.float16).astype(np.float32) - ref)
+        worst = max(worst, float(err.max()))
+        ok = ok and bool(np.all(err <= 2e-3 + 1e-3 * np.abs(ref)))
+    assert engine.check_invariants()
+    print(json.dumps({
+        "metric": "config-1 decode step (reserve + write + GQA decode + commit, 4 lanes, 1 layer) us/step",
+        "value": round(us, 2), "unit": "us/step", "higher_is_better": False,
+        "config": {"workload": "one TinyLlama layer, 4 lanes, contexts 17/100/513/1000 (+1 appended per step), "
+                               "512-slot permuted micro/extent pools, through the engine"},
+        "steps": args.steps, "warmup": args.warmup,
+        "check": {"lanes": lanes, "max_abs_err": worst, "within_tolerance": ok, "tolerance": "2e-3 + 1e-3*|ref|"},
+        "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
+                         "sample": f"the decode of the whole step: oracle kvo_paged_decode of the 4 lanes, mean of "
+                                   f"{reps} on {platform.processor() or platform.machine()}"}}), flush=True)
+    return 0 if ok else 1
+
+
+def oracle_pages_layer(kv_layer, T):
+    """Host pages (8-token micro pages, one layer) holding kv_layer [2][T][H][D] and their table."""
+    import oracle
+    H, D = kv_layer.shape[2], kv_layer.shape[3]
+    pages = (T + 7) // 8
+    pools = oracle.HostPools(1, H, D, pages, 1)
+    table = np.zeros(pages, dtype=oracle.DESC)
+    kv = np.ascontiguousarray(kv_layer[None])
+    for k in range(pages):
+        n = min(8, T - 8 * k)
+        table[k] = (k, 1, 8 * k, n, 8, 0)
+        pools.append_tokens(kv, T, 8 * k, 0, k, 0, n)
+    return pools, table
 
 
 def oracle_decode_layer(kv_layer, T, q, QH, D):
@@ -693,27 +872,49 @@ def run_shared(kimkv, dev, args) -> int:
     appended = args.warmup + (args.steps + 1) / 2.0          # mean tokens appended by the timed steps
     logical_bytes = (lengths.sum() + lanes * appended) * 2 * HD * 2
     physical_bytes = (physical + lanes * appended) * 2 * HD * 2
-    # Check: last step, layer 0, sampled lanes against the oracle.
+    # Check and CPU baseline: the last step's layer 0 of every lane by the
+    # oracle (one host core, then the lanes over all cores), the GPU's
+    # outputs against it.
     last = total_steps - 1
     got = dev.download(out.ptr, (lanes, QD), np.uint16)
     worst, ok = 0.0, True
     import oracle
-    for i in rng.choice(lanes, size=min(args.shared_check, lanes), replace=False):
-        i = int(i)
+    from concurrent.futures import ThreadPoolExecutor
+    threads = max(1, min(16, os.cpu_count() or 1))
+    cases = []
+    for i in range(lanes):
         g = i // per_group
         P = int(prefix[g])
         T = int(lengths[i]) + last + 1
-        kv = np.empty((2, T, H, D), dtype=np.uint16)
-        for c in range(2):
-            kv[c, :P] = oracle.synth_rows(P * HD, args.seed, oracle.kv_row(root_sid + g, 0, c, 0), HD).reshape(P, H, D)
-            n = T - P
-            kv[c, P:] = oracle.synth_rows(n * HD, args.seed, oracle.kv_row(i, 0, c, P), HD).reshape(n, H, D)
+        kv = synth_history(args.seed, lambda t, g=g, i=i, P=P: root_sid + g if t < P else i, [0], T, H, D, threads)
         q = oracle.synth_rows(QD, qseed, oracle.kv_row(i, 0, 0, int(lengths[i])) + last, QD)
-        ref = oracle_decode_layer(kv, T, q, QH, D)
+        cases.append((oracle_pages_layer(kv[0], T), T, q))
+
+    def decode(case):
+        (pools, table), T, q = case
+        return pools.paged_decode(table, T, 0, QH, q, 1.0 / math.sqrt(D), f32=True)
+
+    t0 = time.perf_counter()
+    refs = [decode(c) for c in cases]
+    cpu_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        par = list(pool.map(decode, cases))
+    cpu_par_s = time.perf_counter() - t0
+    for i, ref in enumerate(refs):
+        assert np.array_equal(ref, par[i])
         a = got[i].view(np.float16).astype(np.float32)
         err = np.abs(a - ref)
         worst = max(worst, float(err.max()))
         ok = ok and bool(np.all(err <= 2e-3 + 1e-3 * np.abs(ref)))
+    layer_bytes = sum(T for (_, T, _) in cases) * 2 * HD * 2
+    cpu = {"value": round(cpu_s * 1e6, 1), "unit": "us/layer", "cores": 1, "kind": "port",
+           "gb_per_s": round(layer_bytes / cpu_s / 1e9, 4),
+           "sample": f"the whole layer: oracle kvo_paged_decode of all {lanes} lanes (layer 0, last step) on "
+                     f"{platform.processor() or platform.machine()}",
+           "seconds": round(cpu_s, 2),
+           "all_cores": {"value": round(cpu_par_s * 1e6, 1), "unit": "us/layer", "cores": threads,
+                         "gb_per_s": round(layer_bytes / cpu_par_s / 1e9, 4), "seconds": round(cpu_par_s, 2)}}
     print(json.dumps({
         "metric": "shared-prefix paged decode attn+append us/layer (logical GB/s)",
         "value": round(us_per_layer, 2), "unit": "us/layer", "higher_is_better": False,
@@ -726,8 +927,9 @@ def run_shared(kimkv, dev, args) -> int:
                                f"32q/4kv/64d fp16, through the engine",
                    "logical_tokens": logical, "unique_physical_tokens": physical},
         "steps": args.steps, "warmup": args.warmup,
-        "check": {"lanes": min(args.shared_check, lanes), "layer": 0, "max_abs_err": worst, "within_tolerance": ok,
-                  "tolerance": "2e-3 + 1e-3*|ref|"}}), flush=True)
+        "check": {"lanes": lanes, "layer": 0, "max_abs_err": worst, "within_tolerance": ok,
+                  "tolerance": "2e-3 + 1e-3*|ref|"},
+        "cpu_baseline": cpu}), flush=True)
     return 0 if ok else 1
 
 
@@ -1040,13 +1242,12 @@ def profiled_traffic(lanes_per_launch: int, context: int, layers: int):
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", choices=["decode", "gather", "append", "shared", "prefill", "e2e", "copy"],
+    ap.add_argument("--config", choices=["decode", "parity", "gather", "append", "shared", "prefill", "e2e", "copy"],
                     default="decode",
                     help="decode: HBM-scale decode+append (the headline line); gather: long-sequence gather; "
                          "append: ragged one-token append with tail allocation; shared: fork/COW shared-prefix "
                          "decode; prefill: chunked-prefill attention through the engine; e2e: TinyLlama under the iteration "
                          "scheduler; copy: plain device copy (bandwidth and counter calibration)")
-    ap.add_argument("--shared-check", type=int, default=4, help="lanes of the shared config checked")
     ap.add_argument("--append-lanes", type=int, default=64)
     ap.add_argument("--append-check", type=int, default=4, help="lanes gathered and compared bit-exactly")
     ap.add_argument("--path", choices=["engine", "kernel"], default="engine",
@@ -1086,6 +1287,8 @@ def main() -> int:
     if dev.device_count() == 0:
         print(json.dumps({"error": "no HIP device visible"}), flush=True)
         return 1
+    if args.config == "parity":
+        return run_parity(kimkv, dev, args)
     if args.config == "gather":
         return run_gather(dev, args)
     if args.config == "copy":
