@@ -43,6 +43,32 @@ struct KvCacheManagerSnapshot final {
     PagePoolSnapshot extent_pool{};
 };
 
+// A reservation of KvCacheManager::reserveTokenDelta, described by what it
+// changes instead of by two full tables: the candidate table is the committed
+// one (version `committed_version`, last entry `previous_tail` when
+// `has_previous_tail`) with `tail` appended when `appended`, else with its last
+// entry replaced by `tail`; it holds `entry_count` entries.  No counterpart in
+// the reference, whose reserveToken returns both tables: this form lets a
+// caller keep a device-resident copy of the table and patch one entry per
+// token.
+struct TokenReservationDelta final {
+    KvCacheError error{KvCacheError::None};
+    KvTokenReservationId reservation_id{kInvalidKvTokenReservationId};
+    RequestId request_id{kInvalidRequestId};
+    std::uint32_t logical_token_position{0};
+    std::uint64_t committed_version{0};
+    std::uint32_t entry_count{0};
+    bool appended{false};
+    bool has_previous_tail{false};
+    MappingEntry tail{};
+    MappingEntry previous_tail{};
+
+    [[nodiscard]] constexpr bool ok() const noexcept
+    {
+        return error == KvCacheError::None && reservation_id != kInvalidKvTokenReservationId;
+    }
+};
+
 class KvCacheManager final {
 public:
     KvCacheManager(std::uint32_t micro_capacity, std::uint32_t extent_capacity);
@@ -57,6 +83,10 @@ public:
 
     [[nodiscard]] TokenReservationResult reserveToken(RequestId request_id,
                                                       std::uint32_t expected_committed_tokens);
+    // The same reservation as reserveToken (same checks, errors, ids and page
+    // staging) in O(1): no table is copied.
+    [[nodiscard]] TokenReservationDelta reserveTokenDelta(RequestId request_id,
+                                                          std::uint32_t expected_committed_tokens);
     [[nodiscard]] KvCacheError commitTokenReservation(KvTokenReservationId reservation_id);
     [[nodiscard]] KvCacheError rollbackTokenReservation(KvTokenReservationId reservation_id);
 
@@ -110,7 +140,8 @@ private:
         KvTokenReservationId id{kInvalidKvTokenReservationId};
         RequestId request_id{kInvalidRequestId};
         std::uint64_t prepared_version{0};
-        BlockTable candidate{};
+        MappingEntry tail{};                               // the candidate's last entry
+        bool appended{false};                              // new entry, else replaces the last
         PageHandle staged{PageHandle::invalid()};          // freshly allocated tail page
         PageHandle existing_mutable{PageHandle::invalid()};
         PageHandle replaced_tail{PageHandle::invalid()};   // sealed partial tail being COW-replaced
@@ -138,6 +169,11 @@ private:
     [[nodiscard]] static std::uint64_t nextId(std::uint64_t& counter, Map const& live);
 
     [[nodiscard]] bool hasReservationLocked(RequestId request_id) const noexcept;
+    // reserveToken's body; with `candidate` the full candidate table is built
+    // there and checked whole, else only its changed tail is checked.
+    [[nodiscard]] TokenReservationDelta reserveLocked(RequestId request_id, std::uint32_t expected_committed_tokens,
+                                                      BlockTable* candidate);
+    [[nodiscard]] static BlockTable candidateOf(Reservation const& r, BlockTable const& committed);
     [[nodiscard]] PageLeaseAcquireResult leaseLocked(std::vector<PageHandle> handles, BlockTable table);
     [[nodiscard]] KvCacheError rollbackPromotionLocked(PromotionId promotion_id);
     [[nodiscard]] KvCacheError rollbackRequestPromotionsLocked(RequestId request_id);

@@ -235,6 +235,25 @@ kimkv_status kimkv_promote_batch(const kimkv_storage* storage,
                                  const kimkv_promotion_job* device_jobs, uint32_t job_count,
                                  kimkv_stream_t stream);
 
+/* One range of a device block table rewritten from a source array:
+ * table[first, first + count) = descriptors[source, source + count). */
+typedef struct kimkv_descriptor_patch {
+    kimkv_block_desc* table;
+    uint32_t first;
+    uint32_t count;
+    uint32_t source;
+    uint32_t reserved;
+} kimkv_descriptor_patch;
+
+/* Applies `patch_count` patches in one launch.  `patches` and `descriptors`
+ * may be device memory or mapped pinned host memory; no two patches may
+ * write the same entry.  No counterpart in the reference, which uploads
+ * every reserved table whole (HipKvStorage / token_reservation.cpp:74): with
+ * per-request tables resident on the device, a token's reservation rewrites
+ * only the table's tail entry. */
+kimkv_status kimkv_patch_descriptors(const kimkv_descriptor_patch* patches, uint32_t patch_count,
+                                     const kimkv_block_desc* descriptors, kimkv_stream_t stream);
+
 /* Set by kimkv_decode_plan in *chunk_tokens when each workgroup should take
  * one KV head and split its chunk over its four waves (merged in the
  * workgroup) instead of taking four KV heads; the other bits are the chunk

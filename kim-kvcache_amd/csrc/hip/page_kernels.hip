@@ -399,6 +399,19 @@ __global__ __launch_bounds__(kBlock) void gather_kernel(PoolView P, const kimkv_
 // ---------------------------------------------------------------------------
 // Batched promotion: block = (job, layer).  Extent token t <- micro page t/8.
 // ---------------------------------------------------------------------------
+// One workgroup per patch: the range is copied as 32-bit words (a
+// descriptor is 5 words), so a one-entry patch is a single wave's loads.
+__global__ __launch_bounds__(kBlock) void patch_descriptors_kernel(const kimkv_descriptor_patch* patches,
+                                                                   const kimkv_block_desc* descriptors)
+{
+    static_assert(sizeof(kimkv_block_desc) == 5 * sizeof(uint32_t), "descriptor is five words");
+    kimkv_descriptor_patch const p = patches[blockIdx.x];
+    uint32_t const words = p.count * 5u;
+    auto const* src = reinterpret_cast<const uint32_t*>(descriptors + p.source);
+    auto* dst = reinterpret_cast<uint32_t*>(p.table + p.first);
+    for (uint32_t w = threadIdx.x; w < words; w += kBlock) dst[w] = src[w];
+}
+
 __global__ __launch_bounds__(kBlock) void promote_kernel(PoolView P, const kimkv_promotion_job* jobs,
                                                          uint32_t job_count)
 {
@@ -603,6 +616,15 @@ kimkv_status kimkv_promote_batch(const kimkv_storage* storage, const kimkv_promo
     if (static_cast<uint32_t>(storage->micro_tokens) * 8 != storage->extent_tokens) return KIMKV_INVALID_ARGUMENT;
     dim3 const grid(job_count, storage->layout.layers);
     promote_kernel<<<grid, kBlock, 0, native(stream)>>>(pool_view(*storage), device_jobs, job_count);
+    return launch_status();
+}
+
+kimkv_status kimkv_patch_descriptors(const kimkv_descriptor_patch* patches, uint32_t patch_count,
+                                     const kimkv_block_desc* descriptors, kimkv_stream_t stream)
+{
+    if (patch_count == 0) return KIMKV_OK;
+    if (patches == nullptr || descriptors == nullptr) return KIMKV_INVALID_ARGUMENT;
+    patch_descriptors_kernel<<<patch_count, kBlock, 0, native(stream)>>>(patches, descriptors);
     return launch_status();
 }
 

@@ -1,14 +1,17 @@
 // Heterogeneous engine backend on MI355X.
 //
 // Behaviour follows the reference's CUDA backend (src/cuda/engine/backend.cpp:
-// 19-610 and transaction.cpp:24-423): reserve = metadata reservation + page
-// lease + descriptor upload; writeLayer / attendLayer only enqueue; commit
-// waits on one completion event, releases the lease and publishes the table;
-// any failure rolls back after in-flight work has drained; error codes map as
-// in backend.cpp:19-65.  Differences: batched attention has no lane cap and
-// one decode launch covers every lane; writeLayerBatch appends all lanes in
-// one launch; descriptors come from a buffer cache and small per-launch
-// uploads go through a pinned staging ring instead of cudaMalloc per token.
+// 19-610 and transaction.cpp:24-423): reserve = metadata reservation +
+// device descriptors; writeLayer / attendLayer only enqueue; commit waits on
+// one completion event and publishes the table; any failure rolls back after
+// in-flight work has drained; error codes map as in backend.cpp:19-65.
+// Differences: a reservation costs O(1) in the context length -- the manager
+// reserves by tail delta, each request's table stays resident on the device
+// and only its tail entry is patched (the reference copies both tables,
+// leases every page and uploads the whole table per token); batched
+// attention has no lane cap and one decode launch covers every lane;
+// writeLayerBatch appends all lanes in one launch; small per-launch uploads go
+// through a pinned staging ring instead of cudaMalloc per token.
 #include "kim-kv/hip/hip_engine_kv_backend.h"
 
 #include "kim-kv/runtime/kv_cache_manager.h"
@@ -59,11 +62,79 @@ EngineKvStatus mapDevice(HipStatus s) noexcept
 HipStatus invalidArgument() noexcept { return HipStatus{HipError::InvalidArgument, 0}; }
 HipStatus injectedSubmission() noexcept { return HipStatus{HipError::SubmissionFailed, 0}; }
 
+constexpr std::uint64_t kStaleTable = ~std::uint64_t{0};
+
+// A request's committed block table kept in device memory across tokens: a
+// token reservation patches its tail entry instead of uploading the table.
+// `version` is the manager table version the copy holds, kStaleTable while a
+// reservation's candidate is patched in or after a failure; a reservation
+// that finds it stale (or too small) rewrites it whole.  Only the request's
+// own token transactions read it, and each of them waits for its device work
+// before it resolves, which the manager requires before the request's next
+// reservation, append, promotion or release: the copy is rewritten or freed
+// without a fence.
+struct DeviceTable final {
+    DeviceBufferCache* cache{nullptr};
+    kimkv_block_desc* ptr{nullptr};
+    std::size_t granted{0};
+    std::uint64_t version{kStaleTable};
+
+    DeviceTable() = default;
+    DeviceTable(DeviceTable const&) = delete;
+    DeviceTable& operator=(DeviceTable const&) = delete;
+    DeviceTable(DeviceTable&& o) noexcept : cache(o.cache), ptr(o.ptr), granted(o.granted), version(o.version)
+    {
+        o.ptr = nullptr;
+        o.granted = 0;
+    }
+    DeviceTable& operator=(DeviceTable&&) = delete;
+    ~DeviceTable() { reset(); }
+
+    [[nodiscard]] std::uint32_t capacity() const noexcept
+    {
+        return static_cast<std::uint32_t>(std::min<std::size_t>(granted / sizeof(kimkv_block_desc), 0xFFFFFFFFu));
+    }
+    void reset() noexcept
+    {
+        if (ptr != nullptr) cache->release(ptr, granted);
+        ptr = nullptr;
+        granted = 0;
+        version = kStaleTable;
+    }
+    // Room for `entries` (plus headroom for the next tokens); false when out
+    // of device memory (the copy is then released and stale).
+    bool fit(DeviceBufferCache& buffers, std::uint32_t entries) noexcept
+    {
+        if (ptr != nullptr && capacity() >= entries) return true;
+        reset();
+        std::size_t const want = (static_cast<std::size_t>(entries) + std::max<std::size_t>(entries / 4, 32))
+            * sizeof(kimkv_block_desc);
+        void* mem = nullptr;
+        try {
+            mem = buffers.acquire(want, granted);
+        } catch (...) {
+            mem = nullptr;
+        }
+        if (mem == nullptr) {
+            granted = 0;
+            return false;
+        }
+        cache = &buffers;
+        ptr = static_cast<kimkv_block_desc*>(mem);
+        return true;
+    }
+};
+
+struct RequestState final {
+    std::uint32_t length{0};   // committed tokens
+    DeviceTable table;
+};
+
 struct BackendState final {
     EngineKvConfig config;
     KvCacheManager manager;
     HipKvStorage storage;
-    std::unordered_map<RequestId, std::uint32_t> committed_lengths;
+    std::unordered_map<RequestId, RequestState> requests;
     // Requests with an unfinished PrefillChunk: their table already holds the
     // chunk, so every other mutation of them is refused until finish().
     std::unordered_set<RequestId> prefilling;
@@ -162,24 +233,19 @@ struct DescriptorArena final {
 
 class HipTokenTransaction final : public TokenTransactionBackend {
 public:
-    HipTokenTransaction(std::shared_ptr<BackendState> owner, TokenReservationResult const& r, PageLeaseId lease,
-                        HipStream stream)
+    HipTokenTransaction(std::shared_ptr<BackendState> owner, TokenReservationDelta const& r, HipStream stream)
         : owner_(std::move(owner)),
           reservation_(r.reservation_id),
           request_(r.request_id),
-          lease_(lease),
+          committed_version_(r.committed_version),
           stream_(stream),
-          token_count_(r.reserved.tokenCount())
+          token_count_(r.logical_token_position + 1)
     {
-        MappingEntry const& tail = r.reserved.entries().back();
-        tail_ = tail.handle;
-        tail_token_ = static_cast<std::uint16_t>(token_count_ - 1 - tail.logical_token_begin);
-        if (!r.before.entries().empty()) {
-            MappingEntry const& old = r.before.entries().back();
-            if (old.logical_token_begin == tail.logical_token_begin && old.handle != tail.handle) {
-                cow_src_ = old.handle;           // partial tail replaced: copy per layer
-                cow_tokens_ = old.valid_tokens;
-            }
+        tail_ = r.tail.handle;
+        tail_token_ = static_cast<std::uint16_t>(token_count_ - 1 - r.tail.logical_token_begin);
+        if (!r.appended && r.has_previous_tail && r.previous_tail.handle != r.tail.handle) {
+            cow_src_ = r.previous_tail.handle;   // partial tail replaced: copy per layer
+            cow_tokens_ = r.previous_tail.valid_tokens;
         }
     }
 
@@ -189,15 +255,14 @@ public:
         releaseDescriptors();
     }
 
-    // Binds the transaction to its slice of a reserve call's descriptor arena
-    // (the descriptor upload of beginEngineTransaction, issued by the caller
-    // on this transaction's stream before any of its launches).
-    void attach(std::shared_ptr<DescriptorArena> arena, std::size_t first, std::uint32_t count) noexcept
+    // Binds the transaction to its request's device table, whose candidate
+    // patch the reserve call has enqueued on this transaction's stream.
+    void attach(kimkv_block_desc const* table, std::uint32_t count) noexcept
     {
-        descriptors_ = static_cast<kimkv_block_desc const*>(arena->ptr) + first;
+        table_ = table;
+        descriptors_ = table;
         desc_count_ = count;
-        arena_ = std::move(arena);
-        dirty_ = true;   // the descriptor copy is in flight
+        dirty_ = true;   // the patch is in flight
         submission_ = {};
     }
 
@@ -384,13 +449,13 @@ public:
         HipStatus const done = finish();
         if (!done.ok()) return mapDevice(done);
         std::lock_guard<std::mutex> lock(owner_->mutex);
-        EngineKvStatus const lease = releaseLeaseLocked();
-        if (!lease.ok()) return lease;
         KvCacheError const c = owner_->manager.commitTokenReservation(reservation_);
         if (c != KvCacheError::None) return mapMetadata(c);
-        auto it = owner_->committed_lengths.find(request_);
-        if (it == owner_->committed_lengths.end()) return {EngineKvError::InternalError};
-        ++it->second;
+        auto it = owner_->requests.find(request_);
+        if (it == owner_->requests.end()) return {EngineKvError::InternalError};
+        ++it->second.length;
+        // The device copy holds the candidate, which is now the committed table.
+        if (it->second.table.ptr == table_) it->second.table.version = committed_version_ + 1;
         --owner_->active_transactions;
         resolved_ = true;
         return {};
@@ -401,7 +466,6 @@ public:
         if (resolved_) return;
         static_cast<void>(finish());
         std::lock_guard<std::mutex> lock(owner_->mutex);
-        static_cast<void>(releaseLeaseLocked());
         static_cast<void>(owner_->manager.rollbackTokenReservation(reservation_));
         if (owner_->active_transactions != 0) --owner_->active_transactions;
         resolved_ = true;
@@ -549,32 +613,20 @@ private:
         dirty_ = false;
     }
 
-    void releaseDescriptors() noexcept
-    {
-        arena_.reset();
-        descriptors_ = nullptr;
-    }
-
-    EngineKvStatus releaseLeaseLocked() noexcept
-    {
-        if (lease_ == kInvalidPageLeaseId) return {};
-        KvCacheError const e = owner_->manager.releasePageLease(lease_);
-        if (e == KvCacheError::None) lease_ = kInvalidPageLeaseId;
-        return mapMetadata(e);
-    }
+    void releaseDescriptors() noexcept { descriptors_ = nullptr; }
 
     std::shared_ptr<BackendState> owner_;
     KvTokenReservationId reservation_;
     RequestId request_;
-    PageLeaseId lease_;
+    std::uint64_t committed_version_;
     HipStream stream_;
     std::uint32_t token_count_;
     PageHandle tail_{};
     std::uint16_t tail_token_{0};
     PageHandle cow_src_{};
     std::uint16_t cow_tokens_{0};
-    std::shared_ptr<DescriptorArena> arena_;
-    kimkv_block_desc const* descriptors_{nullptr};
+    kimkv_block_desc const* table_{nullptr};         // the request's device table
+    kimkv_block_desc const* descriptors_{nullptr};   // table_ until the transaction finishes
     std::uint32_t desc_count_{0};
     std::shared_ptr<CompletionMark> mark_;
     bool dirty_{false};   // work enqueued after mark_ (or no mark yet)
@@ -682,12 +734,12 @@ struct PrefillChunk::Impl {
             if (lease_after != kInvalidPageLeaseId) static_cast<void>(m.releasePageLease(lease_after));
             if (lease_before != kInvalidPageLeaseId) static_cast<void>(m.releasePageLease(lease_before));
             if (final_status.ok()) {
-                auto len = owner->committed_lengths.find(request);
-                if (len != owner->committed_lengths.end()) len->second += count;
+                auto len = owner->requests.find(request);
+                if (len != owner->requests.end()) len->second.length += count;
             } else {
                 // The table already names the chunk's pages: cancel rather than expose them.
                 static_cast<void>(m.releaseRequest(request));
-                owner->committed_lengths.erase(request);
+                owner->requests.erase(request);
             }
         }
         arena.reset();
@@ -899,6 +951,83 @@ void attendPrefillBatch(PrefillChunk* const* chunks, std::size_t count, std::uin
 
 namespace {
 
+// The descriptor patches of one reserve call.  Patches and their source
+// descriptors are staged together in the pinned ring and applied by one
+// kimkv_patch_descriptors launch per ring request (the kernel reads the
+// staged bytes directly).  Once a launch fails the whole batch has failed.
+class PatchBatch final {
+public:
+    PatchBatch(HipKvStorage& storage, HipStream stream) : storage_(storage), stream_(stream)
+    {
+        patches_.clear();
+        sources_.clear();
+    }
+
+    // Queues table[first, first + n) = src[0, n); false once the batch failed.
+    bool add(kimkv_block_desc* table, std::uint32_t first, kimkv_block_desc const* src, std::uint32_t n)
+    {
+        std::size_t const limit = storage_.ring().maxStage();
+        while (n != 0 && !failed_) {
+            std::size_t const used = bytes(patches_.size() + 1, sources_.size());
+            if (used + sizeof(kimkv_block_desc) > limit) {
+                if (patches_.empty()) failed_ = true;   // a ring too small for one entry
+                else static_cast<void>(flush());
+                continue;
+            }
+            auto const k = static_cast<std::uint32_t>(
+                std::min<std::size_t>(n, (limit - used) / sizeof(kimkv_block_desc)));
+            patches_.push_back(
+                kimkv_descriptor_patch{table, first, k, static_cast<std::uint32_t>(sources_.size()), 0});
+            sources_.insert(sources_.end(), src, src + k);
+            first += k;
+            src += k;
+            n -= k;
+        }
+        return !failed_;
+    }
+
+    // Issues what is queued; true when every launch of the batch was issued.
+    bool flush()
+    {
+        if (failed_ || patches_.empty()) return !failed_;
+        std::size_t const head = bytes(patches_.size(), 0);
+        staging_.resize(bytes(patches_.size(), sources_.size()));
+        std::memcpy(staging_.data(), patches_.data(), patches_.size() * sizeof(kimkv_descriptor_patch));
+        std::memcpy(staging_.data() + head, sources_.data(), sources_.size() * sizeof(kimkv_block_desc));
+        {
+            std::lock_guard<std::mutex> launch(storage_.launchMutex());
+            auto* staged = static_cast<unsigned char*>(storage_.ring().stage(staging_.data(), staging_.size(), stream_));
+            kimkv_status const k = staged == nullptr
+                ? KIMKV_SUBMISSION_FAILED
+                : kimkv_patch_descriptors(reinterpret_cast<kimkv_descriptor_patch const*>(staged),
+                                          static_cast<std::uint32_t>(patches_.size()),
+                                          reinterpret_cast<kimkv_block_desc const*>(staged + head), stream_);
+            storage_.ring().fence(stream_);
+            if (k != KIMKV_OK) failed_ = true;
+        }
+        patches_.clear();
+        sources_.clear();
+        return !failed_;
+    }
+
+private:
+    static std::size_t bytes(std::size_t patches, std::size_t sources) noexcept
+    {
+        return (patches * sizeof(kimkv_descriptor_patch) + 7) / 8 * 8 + sources * sizeof(kimkv_block_desc);
+    }
+
+    HipKvStorage& storage_;
+    HipStream stream_;
+    bool failed_{false};
+    static thread_local std::vector<kimkv_descriptor_patch> patches_;
+    static thread_local std::vector<kimkv_block_desc> sources_;
+    static thread_local std::vector<unsigned char> staging_;
+};
+
+thread_local std::vector<kimkv_descriptor_patch> PatchBatch::patches_;
+thread_local std::vector<kimkv_block_desc> PatchBatch::sources_;
+thread_local std::vector<unsigned char> PatchBatch::staging_;
+
 class HipEngineKvBackend final : public EngineKvBackend {
 public:
     explicit HipEngineKvBackend(std::shared_ptr<BackendState> s) : state_(std::move(s)) {}
@@ -911,18 +1040,22 @@ public:
         std::lock_guard<std::mutex> lock(state_->mutex);
         if (!state_->config.valid() || !state_->storage.status().ok()) return {EngineKvError::InvalidState};
         KvCacheError const e = state_->manager.createRequest(request_id);
-        if (e == KvCacheError::None) state_->committed_lengths.emplace(request_id, 0);
+        if (e == KvCacheError::None) state_->requests.emplace(request_id, RequestState{});
         return mapMetadata(e);
     }
 
     EngineKvStatus forkRequest(RequestId source, RequestId child) override
     {
         std::lock_guard<std::mutex> lock(state_->mutex);
-        auto it = state_->committed_lengths.find(source);
-        if (it == state_->committed_lengths.end()) return {EngineKvError::RequestNotFound};
+        auto it = state_->requests.find(source);
+        if (it == state_->requests.end()) return {EngineKvError::RequestNotFound};
         if (state_->prefilling.count(source) != 0) return {EngineKvError::InvalidState};
         KvCacheError const e = state_->manager.forkRequest(source, child);
-        if (e == KvCacheError::None) state_->committed_lengths.emplace(child, it->second);
+        if (e == KvCacheError::None) {
+            RequestState forked;
+            forked.length = it->second.length;
+            state_->requests.emplace(child, std::move(forked));
+        }
         return mapMetadata(e);
     }
 
@@ -931,7 +1064,7 @@ public:
         std::lock_guard<std::mutex> lock(state_->mutex);
         if (state_->prefilling.count(request_id) != 0) return {EngineKvError::InvalidState};
         KvCacheError const e = state_->manager.releaseRequest(request_id);
-        if (e == KvCacheError::None) state_->committed_lengths.erase(request_id);
+        if (e == KvCacheError::None) state_->requests.erase(request_id);
         return mapMetadata(e);
     }
 
@@ -942,10 +1075,12 @@ public:
         return result;
     }
 
-    // reserveToken for several requests sharing one stream: per-request
-    // metadata (reservation, lease, table checks) exactly as one by one, then
-    // every descriptor table in one arena with a single upload.  A request
-    // that fails keeps its own status and does not affect the others.
+    // reserveToken for several requests sharing one stream.  Per request:
+    // the manager's delta reservation, the new tail entry checked, and the
+    // request's device table brought to the candidate -- its tail entry
+    // patched, or the whole table written when the device copy is stale or
+    // too small.  The patches of the call go to the device in one launch.  A
+    // request that fails keeps its own status and does not affect the others.
     void reserveBatch(ReserveTokenRequest const* requests, std::size_t count, TokenReserveResult* results)
     {
         std::lock_guard<std::mutex> lock(state_->mutex);
@@ -953,17 +1088,15 @@ public:
         HipKvStorage& st = state_->storage;
         struct Pending {
             std::size_t index;
-            TokenReservationResult r;
-            PageLeaseId lease;
+            TokenReservationDelta r;
             std::unique_ptr<HipTokenTransaction> tx;
-            std::size_t first;
-            std::uint32_t descriptors;
+            DeviceTable* table;
         };
         std::vector<Pending> pending;
         pending.reserve(count);
-        thread_local std::vector<kimkv_block_desc> all;
-        all.clear();
         HipStream const stream = count != 0 ? requests[0].stream : nullptr;
+        PatchBatch patches(st, stream);
+        thread_local std::vector<kimkv_block_desc> whole;
         for (std::size_t i = 0; i < count; ++i) {
             ReserveTokenRequest const& request = requests[i];
             TokenReserveResult& result = results[i];
@@ -972,7 +1105,8 @@ public:
                 result.status = {EngineKvError::InvalidArgument};
                 continue;
             }
-            if (state_->committed_lengths.find(request.request_id) == state_->committed_lengths.end()) {
+            auto rs = state_->requests.find(request.request_id);
+            if (rs == state_->requests.end()) {
                 result.status = {EngineKvError::RequestNotFound};
                 continue;
             }
@@ -980,86 +1114,74 @@ public:
                 result.status = {EngineKvError::InvalidState};
                 continue;
             }
-            TokenReservationResult r = m.reserveToken(request.request_id, request.expected_committed_tokens);
+            TokenReservationDelta const r = m.reserveTokenDelta(request.request_id, request.expected_committed_tokens);
             if (!r.ok()) {
                 result.status = mapMetadata(r.error);
                 continue;
             }
-            PageLeaseAcquireResult lease = m.acquireTokenReservationLease(r.reservation_id);
-            if (!lease.ok()) {
-                static_cast<void>(m.rollbackTokenReservation(r.reservation_id));
-                result.status = mapMetadata(lease.error);
-                continue;
-            }
+            DeviceTable& table = rs->second.table;
+            bool const rewrite = table.version != r.committed_version || table.capacity() < r.entry_count;
+            kimkv_block_desc tail{};
             EngineKvStatus refuse{};
             if (!st.status().ok()) {
                 refuse = mapDevice(st.status());
-            } else if (!st.validTable(r.before) || !st.validTable(r.reserved) || r.reserved.entries().empty()) {
+            } else if (!st.descriptor(r.tail, tail)) {
                 refuse = {EngineKvError::InvalidArgument};
-            } else if (st.consumeFailure(HipFailurePoint::Submission)) {
+            } else if (rewrite) {
+                // The committed table is checked whole once, when written whole.
+                table.version = kStaleTable;
+                std::optional<BlockTable> committed = m.blockTable(request.request_id);
+                if (!committed || committed->version() != r.committed_version || !st.validTable(*committed)
+                    || committed->entries().size() + (r.appended ? 1 : 0) != r.entry_count) {
+                    refuse = {EngineKvError::InvalidArgument};
+                } else {
+                    st.descriptors(*committed, whole);
+                    if (r.appended) {
+                        whole.push_back(tail);
+                    } else {
+                        whole.back() = tail;
+                    }
+                }
+            }
+            if (refuse.ok() && st.consumeFailure(HipFailurePoint::Submission)) {
                 refuse = {EngineKvError::SubmissionFailed};
+            }
+            if (refuse.ok() && rewrite && !table.fit(st.buffers(), r.entry_count)) {
+                refuse = {EngineKvError::ResourceExhausted};
             }
             std::unique_ptr<HipTokenTransaction> tx;
             if (refuse.ok()) {
                 try {
-                    tx = std::make_unique<HipTokenTransaction>(state_, r, lease.lease_id, stream);
+                    tx = std::make_unique<HipTokenTransaction>(state_, r, stream);
                 } catch (...) {
                     refuse = {EngineKvError::ResourceExhausted};
                 }
             }
+            if (refuse.ok()) {
+                table.version = kStaleTable;   // holds the candidate from here on
+                bool const queued = rewrite ? patches.add(table.ptr, 0, whole.data(), r.entry_count)
+                                            : patches.add(table.ptr, r.entry_count - 1, &tail, 1);
+                if (!queued) refuse = {EngineKvError::SubmissionFailed};
+            }
             if (!refuse.ok()) {
-                static_cast<void>(m.releasePageLease(lease.lease_id));
+                tx.reset();   // drains the stream (patches of this call may be in flight)
                 static_cast<void>(m.rollbackTokenReservation(r.reservation_id));
                 result.status = refuse;
                 continue;
             }
-            std::size_t const first = all.size();
-            for (MappingEntry const& e : r.reserved.entries()) {
-                kimkv_block_desc d{};
-                d.slot = e.handle.slot;
-                d.generation = e.handle.generation;
-                d.logical_token_begin = e.logical_token_begin;
-                d.valid_tokens = e.valid_tokens;
-                d.page_token_capacity = st.pageTokenCapacity(e.kind);
-                d.kind = static_cast<std::uint8_t>(e.kind);
-                all.push_back(d);
-            }
-            auto const n = static_cast<std::uint32_t>(all.size() - first);
-            pending.push_back(Pending{i, std::move(r), lease.lease_id, std::move(tx), first, n});
+            pending.push_back(Pending{i, r, std::move(tx), &table});
         }
         if (pending.empty()) return;
-        // One arena and one upload for every table of the call.
-        std::size_t const bytes = all.size() * sizeof(kimkv_block_desc);
-        std::size_t granted = 0;
-        void* mem = st.buffers().acquire(bytes, granted);
-        std::shared_ptr<DescriptorArena> arena;
-        EngineKvStatus failure{};
-        if (mem == nullptr) {
-            failure = {EngineKvError::ResourceExhausted};
-        } else {
-            try {
-                arena = std::make_shared<DescriptorArena>(state_, mem, granted);
-            } catch (...) {
-                st.buffers().release(mem, granted);
-                failure = {EngineKvError::ResourceExhausted};
-            }
-        }
-        if (failure.ok()) {
-            std::lock_guard<std::mutex> launch(state_->storage.launchMutex());
-            // Fenced by the first attention launch on this stream.
-            bool const staged = st.ring().uploadTo(arena->ptr, all.data(), bytes, stream);
-            if (!staged) failure = {EngineKvError::SubmissionFailed};
-        }
+        bool const issued = patches.flush();
         for (Pending& p : pending) {
             TokenReserveResult& result = results[p.index];
-            if (failure.ok()) p.tx->attach(arena, p.first, p.descriptors);
-            if (!failure.ok()) {
+            if (!issued) {
                 p.tx.reset();   // drains its stream before the metadata is undone
-                static_cast<void>(m.releasePageLease(p.lease));
                 static_cast<void>(m.rollbackTokenReservation(p.r.reservation_id));
-                result.status = failure;
+                result.status = {EngineKvError::SubmissionFailed};
                 continue;
             }
+            p.tx->attach(p.table->ptr, p.r.entry_count);
             std::uint64_t const id = state_->next_transaction_id.fetch_add(1, std::memory_order_relaxed);
             result.transaction = TokenTransaction(std::move(p.tx), id, p.r.request_id, p.r.logical_token_position,
                                                   state_->config.kv_layout.layer_count, stream);
@@ -1076,9 +1198,9 @@ public:
     {
         std::lock_guard<std::mutex> lock(state_->mutex);
         EngineKvBackendSnapshot s;
-        s.request_count = state_->committed_lengths.size();
+        s.request_count = state_->requests.size();
         s.active_transaction_count = state_->active_transactions;
-        for (auto const& kv : state_->committed_lengths) s.committed_token_count += kv.second;
+        for (auto const& kv : state_->requests) s.committed_token_count += kv.second.length;
         s.batched_attention_submissions = state_->batched_attention_submissions.load(std::memory_order_relaxed);
         s.batched_attention_lanes = state_->batched_attention_lanes.load(std::memory_order_relaxed);
         s.batched_write_submissions = state_->batched_write_submissions.load(std::memory_order_relaxed);
@@ -1161,7 +1283,7 @@ public:
         HipStatus const copied = state_->storage.promoteBatch(committed, stream);
         if (!copied.ok()) {
             static_cast<void>(m.releaseRequest(request_id));
-            state_->committed_lengths.erase(request_id);
+            state_->requests.erase(request_id);
             return mapDevice(copied);
         }
         if (promoted) *promoted = static_cast<std::uint32_t>(committed.size());
@@ -1186,8 +1308,8 @@ public:
         {
             std::lock_guard<std::mutex> lock(state_->mutex);
             if (!state_->storage.status().ok()) return mapDevice(state_->storage.status());
-            auto len = state_->committed_lengths.find(request_id);
-            if (len == state_->committed_lengths.end()) return {EngineKvError::RequestNotFound};
+            auto len = state_->requests.find(request_id);
+            if (len == state_->requests.end()) return {EngineKvError::RequestNotFound};
             if (state_->prefilling.count(request_id) != 0) return {EngineKvError::InvalidState};
             KvCacheManager& m = state_->manager;
             before = m.acquireRequestReadLease(request_id);
@@ -1202,7 +1324,7 @@ public:
             if (!after.ok()) {
                 static_cast<void>(m.releasePageLease(before.lease_id));
                 static_cast<void>(m.releaseRequest(request_id));
-                state_->committed_lengths.erase(request_id);
+                state_->requests.erase(request_id);
                 return mapMetadata(after.error);
             }
         }
@@ -1215,12 +1337,12 @@ public:
             static_cast<void>(m.releasePageLease(before.lease_id));
             if (!device.ok()) {
                 static_cast<void>(m.releaseRequest(request_id));
-                state_->committed_lengths.erase(request_id);
+                state_->requests.erase(request_id);
                 return mapDevice(device);
             }
-            auto len = state_->committed_lengths.find(request_id);
-            if (len == state_->committed_lengths.end()) return {EngineKvError::RequestNotFound};
-            len->second += token_count;
+            auto len = state_->requests.find(request_id);
+            if (len == state_->requests.end()) return {EngineKvError::RequestNotFound};
+            len->second.length += token_count;
             MappingEntry const& tail = after.table.entries().back();
             if (tail.valid_tokens == kMicroPageTokenCapacity && tail.kind == PageKind::Micro) {
                 KvCacheError const sealed = m.sealTail(request_id);
@@ -1245,12 +1367,12 @@ public:
             result.status = mapDevice(st.status());
             return result;
         }
-        auto len = state_->committed_lengths.find(request_id);
-        if (len == state_->committed_lengths.end()) {
+        auto len = state_->requests.find(request_id);
+        if (len == state_->requests.end()) {
             result.status = {EngineKvError::RequestNotFound};
             return result;
         }
-        if (len->second != expected || state_->prefilling.count(request_id) != 0) {
+        if (len->second.length != expected || state_->prefilling.count(request_id) != 0) {
             result.status = {EngineKvError::InvalidState};
             return result;
         }
@@ -1275,7 +1397,7 @@ public:
             if (after.ok()) static_cast<void>(m.releasePageLease(after.lease_id));
             static_cast<void>(m.releasePageLease(before.lease_id));
             static_cast<void>(m.releaseRequest(request_id));
-            state_->committed_lengths.erase(request_id);
+            state_->requests.erase(request_id);
             result.status = why;
             return std::move(result);
         };
@@ -1323,7 +1445,7 @@ public:
     EngineKvStatus permuteFreeSlots(PageKind kind, std::uint64_t seed)
     {
         std::lock_guard<std::mutex> lock(state_->mutex);
-        if (!state_->committed_lengths.empty()) return {EngineKvError::InvalidState};
+        if (!state_->requests.empty()) return {EngineKvError::InvalidState};
         return mapMetadata(permuteFreeSlotsOf(state_->manager, kind, seed));
     }
 

@@ -319,20 +319,36 @@ bool HipKvStorage::validTable(BlockTable const& table) const
     return true;
 }
 
+namespace {
+
+kimkv_block_desc toDescriptor(MappingEntry const& e, std::uint16_t capacity) noexcept
+{
+    kimkv_block_desc d{};
+    d.slot = e.handle.slot;
+    d.generation = e.handle.generation;
+    d.logical_token_begin = e.logical_token_begin;
+    d.valid_tokens = e.valid_tokens;
+    d.page_token_capacity = capacity;
+    d.kind = static_cast<std::uint8_t>(e.kind);
+    return d;
+}
+
+}  // namespace
+
 void HipKvStorage::descriptors(BlockTable const& table, std::vector<kimkv_block_desc>& out) const
 {
     out.clear();
     out.reserve(table.entries().size());
-    for (MappingEntry const& e : table.entries()) {
-        kimkv_block_desc d{};
-        d.slot = e.handle.slot;
-        d.generation = e.handle.generation;
-        d.logical_token_begin = e.logical_token_begin;
-        d.valid_tokens = e.valid_tokens;
-        d.page_token_capacity = pageTokenCapacity(e.kind);
-        d.kind = static_cast<std::uint8_t>(e.kind);
-        out.push_back(d);
-    }
+    for (MappingEntry const& e : table.entries()) out.push_back(toDescriptor(e, pageTokenCapacity(e.kind)));
+}
+
+bool HipKvStorage::descriptor(MappingEntry const& entry, kimkv_block_desc& out) const noexcept
+{
+    if (!pageExists(entry.handle) || entry.kind != entry.handle.kind) return false;
+    std::uint16_t const cap = pageTokenCapacity(entry.kind);
+    if (entry.valid_tokens == 0 || entry.valid_tokens > cap) return false;
+    out = toDescriptor(entry, cap);
+    return true;
 }
 
 bool HipKvStorage::consumeFailure(HipFailurePoint point) noexcept

@@ -58,6 +58,8 @@ public:
 
     [[nodiscard]] bool ok() const noexcept { return host_ != nullptr && device_.get() != nullptr; }
     [[nodiscard]] std::size_t capacity() const noexcept { return size_; }
+    // Largest single stage() / upload().
+    [[nodiscard]] std::size_t maxStage() const noexcept { return regions_.maxRequest(); }
     // Copies `bytes` into the pinned ring and returns that host address, which
     // kernels read directly (mapped, coherent host memory: no copy command on
     // the stream).  For small per-launch argument arrays read once per
@@ -126,6 +128,9 @@ public:
     // entries twice per lane per token).
     [[nodiscard]] bool validTable(BlockTable const& table) const;
     void descriptors(BlockTable const& table, std::vector<kimkv_block_desc>& out) const;
+    // One entry's descriptor; false when its page is out of range, its kind
+    // disagrees with its handle or its token count with the page capacity.
+    [[nodiscard]] bool descriptor(MappingEntry const& entry, kimkv_block_desc& out) const noexcept;
 
     [[nodiscard]] bool consumeFailure(HipFailurePoint point) noexcept;
     void injectFailureOnce(HipFailurePoint point) noexcept;

@@ -45,16 +45,15 @@ bool KvCacheManager::reservationInvariantsLocked(Expected& expected) const
 {
     if (reservation_of_.size() != reservations_.size()) return false;
     for (auto const& [id, r] : reservations_) {
-        if (id == kInvalidKvTokenReservationId || r.id != id || r.request_id == kInvalidRequestId
-            || !r.candidate.checkInvariants()) {
-            return false;
-        }
+        if (id == kInvalidKvTokenReservationId || r.id != id || r.request_id == kInvalidRequestId) return false;
         auto const table = tables_.find(r.request_id);
         auto const owner = reservation_of_.find(r.request_id);
         if (table == tables_.end() || owner == reservation_of_.end() || owner->second != id) return false;
         BlockTable const& before = table->second;
-        if (before.version() != r.prepared_version || r.candidate.version() != before.version() + 1
-            || r.candidate.tokenCount() != before.tokenCount() + 1) {
+        if (!r.appended && before.entries().empty()) return false;
+        BlockTable const candidate = candidateOf(r, before);
+        if (!candidate.checkInvariants() || before.version() != r.prepared_version
+            || candidate.version() != before.version() + 1 || candidate.tokenCount() != before.tokenCount() + 1) {
             return false;
         }
         if (static_cast<int>(r.staged.isStructurallyValid()) + static_cast<int>(r.existing_mutable.isStructurallyValid())
@@ -70,7 +69,7 @@ bool KvCacheManager::reservationInvariantsLocked(Expected& expected) const
                 return false;
             }
             std::uint16_t const want = r.replaced_tail.isStructurallyValid()
-                ? static_cast<std::uint16_t>(r.candidate.entries().back().valid_tokens - 1)
+                ? static_cast<std::uint16_t>(r.tail.valid_tokens - 1)
                 : 0;
             if (t->valid_tokens != want) return false;
             targets[r.staged.slot] = 1;

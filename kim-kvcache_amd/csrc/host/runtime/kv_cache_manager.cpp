@@ -305,6 +305,128 @@ KvCacheError KvCacheManager::append(RequestId request_id, std::uint32_t token_co
 
 // ---- single-token reservations --------------------------------------------------
 
+TokenReservationDelta KvCacheManager::reserveLocked(RequestId request_id, std::uint32_t expected_committed_tokens,
+                                                    BlockTable* candidate)
+{
+    TokenReservationDelta out;
+    out.request_id = request_id;
+    out.logical_token_position = expected_committed_tokens;
+    auto it = tables_.find(request_id);
+    if (it == tables_.end()) {
+        out.error = KvCacheError::RequestNotFound;
+        return out;
+    }
+    bool const promoting = std::any_of(promotions_.begin(), promotions_.end(),
+                                       [request_id](auto const& p) { return p.second.request_id == request_id; });
+    if (hasReservationLocked(request_id) || promoting) {
+        out.error = KvCacheError::RequestConflict;
+        return out;
+    }
+    BlockTable& before = it->second;
+    if (before.tokenCount() != expected_committed_tokens || before.version_ == kU64Max
+        || expected_committed_tokens == kU32Max) {
+        out.error = KvCacheError::InvalidState;
+        return out;
+    }
+    // A new entry is appended when there is no partial micro tail; the
+    // committed table gets the room now so that commit cannot fail on memory.
+    bool const appended = before.entries_.empty() || before.entries_.back().kind == PageKind::Extent
+        || before.entries_.back().valid_tokens == kMicroPageTokenCapacity;
+    if (appended) before.entries_.reserve(before.entries_.size() + 1);
+
+    PageHandle staged = PageHandle::invalid();
+    PageHandle existing_mutable = PageHandle::invalid();
+    PageHandle replaced_tail = PageHandle::invalid();
+    MappingEntry tail{};
+    if (appended) {
+        KvCacheError const e = stageMicroLocked(0, staged);
+        if (e != KvCacheError::None) {
+            out.error = e;
+            return out;
+        }
+        tail = MappingEntry{expected_committed_tokens, 1, PageKind::Micro, staged};
+    } else {
+        tail = before.entries_.back();
+        Page* p = page(tail.handle);
+        if (p == nullptr || tail.kind != PageKind::Micro || p->valid_tokens != tail.valid_tokens) {
+            out.error = KvCacheError::InternalInvariantViolation;
+            return out;
+        }
+        if (p->state == PageState::Mutable) {
+            if (p->ref_count != 1 || p->mutable_owner != request_id) {
+                out.error = KvCacheError::InternalInvariantViolation;
+                return out;
+            }
+            existing_mutable = tail.handle;
+        } else if (p->state == PageState::Sealed) {
+            // Copy-on-write: the shared partial tail is replaced by a fresh page.
+            KvCacheError const e = stageMicroLocked(tail.valid_tokens, staged);
+            if (e != KvCacheError::None) {
+                out.error = e;
+                return out;
+            }
+            replaced_tail = tail.handle;
+            tail.handle = staged;
+        } else {
+            out.error = KvCacheError::InvalidState;
+            return out;
+        }
+        ++tail.valid_tokens;
+    }
+
+    auto abandon = [&](KvCacheError e) {
+        if (staged.isStructurallyValid()) static_cast<void>(freeLocked(staged));
+        out.error = e;
+        return out;
+    };
+    bool sound = false;
+    if (candidate != nullptr) {
+        Reservation const probe{0, request_id, before.version_, tail, appended, staged, existing_mutable,
+                                replaced_tail};
+        *candidate = candidateOf(probe, before);
+        sound = candidate->checkInvariants();
+    } else {
+        // The committed table satisfies the table invariants; only its tail
+        // changed, and a staged page is in no table, so checking the tail
+        // entry checks the candidate.
+        std::uint32_t const begin = appended ? before.tokenCount() : before.entries_.back().logical_token_begin;
+        sound = tail.handle.isStructurallyValid() && tail.handle.kind == PageKind::Micro
+            && tail.logical_token_begin == begin && tail.valid_tokens >= 1
+            && tail.valid_tokens <= kMicroPageTokenCapacity;
+    }
+    if (!sound) return abandon(KvCacheError::InternalInvariantViolation);
+    KvTokenReservationId const id = nextId(next_reservation_id_, reservations_);
+    if (id == kInvalidKvTokenReservationId) return abandon(KvCacheError::InternalInvariantViolation);
+    auto inserted = reservations_.emplace(
+        id, Reservation{id, request_id, before.version_, tail, appended, staged, existing_mutable, replaced_tail});
+    if (!inserted.second) return abandon(KvCacheError::InternalInvariantViolation);
+    if (!reservation_of_.emplace(request_id, id).second) {
+        reservations_.erase(inserted.first);
+        return abandon(KvCacheError::InternalInvariantViolation);
+    }
+    out.error = KvCacheError::None;
+    out.reservation_id = id;
+    out.committed_version = before.version_;
+    out.entry_count = static_cast<std::uint32_t>(before.entries_.size() + (appended ? 1 : 0));
+    out.appended = appended;
+    out.has_previous_tail = !before.entries_.empty();
+    if (out.has_previous_tail) out.previous_tail = before.entries_.back();
+    out.tail = tail;
+    return out;
+}
+
+BlockTable KvCacheManager::candidateOf(Reservation const& r, BlockTable const& committed)
+{
+    BlockTable cand = committed;
+    if (r.appended) {
+        cand.entries_.push_back(r.tail);
+    } else if (!cand.entries_.empty()) {
+        cand.entries_.back() = r.tail;
+    }
+    cand.version_ = r.prepared_version + 1;
+    return cand;
+}
+
 TokenReservationResult KvCacheManager::reserveToken(RequestId request_id, std::uint32_t expected_committed_tokens)
 {
     TokenReservationResult result;
@@ -315,87 +437,28 @@ TokenReservationResult KvCacheManager::reserveToken(RequestId request_id, std::u
         return result;
     }
     std::lock_guard<std::mutex> lock(mutex_);
-    auto it = tables_.find(request_id);
-    if (it == tables_.end()) {
-        result.error = KvCacheError::RequestNotFound;
-        return result;
-    }
-    bool const promoting = std::any_of(promotions_.begin(), promotions_.end(),
-                                       [request_id](auto const& p) { return p.second.request_id == request_id; });
-    if (hasReservationLocked(request_id) || promoting) {
-        result.error = KvCacheError::RequestConflict;
-        return result;
-    }
-    BlockTable const& before = it->second;
-    if (before.tokenCount() != expected_committed_tokens || before.version_ == kU64Max
-        || expected_committed_tokens == kU32Max) {
-        result.error = KvCacheError::InvalidState;
-        return result;
-    }
-
-    BlockTable cand = before;
-    cand.entries_.reserve(cand.entries_.size() + 1);
-    PageHandle staged = PageHandle::invalid();
-    PageHandle existing_mutable = PageHandle::invalid();
-    PageHandle replaced_tail = PageHandle::invalid();
-
-    if (cand.entries_.empty() || cand.entries_.back().kind == PageKind::Extent
-        || cand.entries_.back().valid_tokens == kMicroPageTokenCapacity) {
-        KvCacheError const e = stageMicroLocked(0, staged);
-        if (e != KvCacheError::None) {
-            result.error = e;
-            return result;
-        }
-        cand.entries_.push_back(MappingEntry{expected_committed_tokens, 1, PageKind::Micro, staged});
-    } else {
-        MappingEntry& tail = cand.entries_.back();
-        Page* p = page(tail.handle);
-        if (p == nullptr || tail.kind != PageKind::Micro || p->valid_tokens != tail.valid_tokens) {
-            result.error = KvCacheError::InternalInvariantViolation;
-            return result;
-        }
-        if (p->state == PageState::Mutable) {
-            if (p->ref_count != 1 || p->mutable_owner != request_id) {
-                result.error = KvCacheError::InternalInvariantViolation;
-                return result;
-            }
-            existing_mutable = tail.handle;
-        } else if (p->state == PageState::Sealed) {
-            KvCacheError const e = stageMicroLocked(tail.valid_tokens, staged);
-            if (e != KvCacheError::None) {
-                result.error = e;
-                return result;
-            }
-            replaced_tail = tail.handle;
-            tail.handle = staged;
-        } else {
-            result.error = KvCacheError::InvalidState;
-            return result;
-        }
-        ++tail.valid_tokens;
-    }
-    cand.version_ = before.version_ + 1;
-
-    auto abandon = [&](KvCacheError e) {
-        if (staged.isStructurallyValid()) static_cast<void>(freeLocked(staged));
-        result.error = e;
-        return result;
-    };
-    if (!cand.checkInvariants()) return abandon(KvCacheError::InternalInvariantViolation);
-    KvTokenReservationId const id = nextId(next_reservation_id_, reservations_);
-    if (id == kInvalidKvTokenReservationId) return abandon(KvCacheError::InternalInvariantViolation);
-    auto inserted = reservations_.emplace(
-        id, Reservation{id, request_id, before.version_, cand, staged, existing_mutable, replaced_tail});
-    if (!inserted.second) return abandon(KvCacheError::InternalInvariantViolation);
-    if (!reservation_of_.emplace(request_id, id).second) {
-        reservations_.erase(inserted.first);
-        return abandon(KvCacheError::InternalInvariantViolation);
-    }
-    result.error = KvCacheError::None;
-    result.reservation_id = id;
-    result.before = before;
+    BlockTable cand;
+    TokenReservationDelta const d = reserveLocked(request_id, expected_committed_tokens, &cand);
+    result.error = d.error;
+    if (!d.ok()) return result;
+    result.reservation_id = d.reservation_id;
+    result.before = tables_.find(request_id)->second;
     result.reserved = std::move(cand);
     return result;
+}
+
+TokenReservationDelta KvCacheManager::reserveTokenDelta(RequestId request_id,
+                                                        std::uint32_t expected_committed_tokens)
+{
+    if (request_id == kInvalidRequestId) {
+        TokenReservationDelta out;
+        out.request_id = request_id;
+        out.logical_token_position = expected_committed_tokens;
+        out.error = KvCacheError::InvalidArgument;
+        return out;
+    }
+    std::lock_guard<std::mutex> lock(mutex_);
+    return reserveLocked(request_id, expected_committed_tokens, nullptr);
 }
 
 KvCacheError KvCacheManager::commitTokenReservation(KvTokenReservationId reservation_id)
@@ -408,7 +471,9 @@ KvCacheError KvCacheManager::commitTokenReservation(KvTokenReservationId reserva
     auto tit = tables_.find(r.request_id);
     if (tit == tables_.end() || tit->second.version_ != r.prepared_version) return KvCacheError::RequestConflict;
 
-    MappingEntry const& tail = r.candidate.entries_.back();
+    MappingEntry const& tail = r.tail;
+    BlockTable& table = tit->second;
+    if (!r.appended && table.entries_.empty()) return KvCacheError::InternalInvariantViolation;
     Page* staged = r.staged.isStructurallyValid() ? page(r.staged) : nullptr;
     Page* existing = r.existing_mutable.isStructurallyValid() ? page(r.existing_mutable) : nullptr;
     Page* replaced = r.replaced_tail.isStructurallyValid() ? page(r.replaced_tail) : nullptr;
@@ -437,7 +502,14 @@ KvCacheError KvCacheManager::commitTokenReservation(KvTokenReservationId reserva
         staged->state = full ? PageState::Sealed : PageState::Mutable;
         staged->mutable_owner = full ? kInvalidRequestId : r.request_id;
     }
-    tit->second = std::move(r.candidate);
+    // The candidate: the committed table with the new tail (room for an
+    // appended entry was reserved with the reservation).
+    if (r.appended) {
+        table.entries_.push_back(tail);
+    } else {
+        table.entries_.back() = tail;
+    }
+    table.version_ = r.prepared_version + 1;
     reservation_of_.erase(r.request_id);
     reservations_.erase(rit);
     return KvCacheError::None;
@@ -477,11 +549,17 @@ PageLeaseAcquireResult KvCacheManager::acquireTokenReservationLease(KvTokenReser
         return result;
     }
     Reservation const& r = it->second;
+    auto const committed = tables_.find(r.request_id);
+    if (committed == tables_.end()) {
+        result.error = KvCacheError::InternalInvariantViolation;
+        return result;
+    }
+    BlockTable cand = candidateOf(r, committed->second);
     std::vector<PageHandle> handles;
-    handles.reserve(r.candidate.entries_.size() + 1);
-    for (MappingEntry const& e : r.candidate.entries_) handles.push_back(e.handle);
+    handles.reserve(cand.entries_.size() + 1);
+    for (MappingEntry const& e : cand.entries_) handles.push_back(e.handle);
     if (r.replaced_tail.isStructurallyValid()) handles.push_back(r.replaced_tail);
-    return leaseLocked(std::move(handles), r.candidate);
+    return leaseLocked(std::move(handles), std::move(cand));
 }
 
 // ---- fork / seal / release ---------------------------------------------------------

@@ -46,6 +46,12 @@ APPEND_JOB = np.dtype({
     "itemsize": 56,
 })
 PREFILL_BLOCK = np.dtype([("item", "<u4"), ("head", "<u2"), ("block", "<u2")])
+DESCRIPTOR_PATCH = np.dtype({
+    "names": ["table", "first", "count", "source"],
+    "formats": ["<u8", "<u4", "<u4", "<u4"],
+    "offsets": [0, 8, 12, 16],
+    "itemsize": 24,
+})
 
 PREFILL_ITEM = np.dtype({
     "names": ["descriptors", "descriptor_count", "token_count", "new_tokens", "layer", "query", "output",
@@ -117,6 +123,7 @@ _SIGNATURES = {
     "kimkv_gather": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                     ctypes.c_void_p, ctypes.c_void_p]),
     "kimkv_promote_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_patch_descriptors": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]),
     "kimkv_decode_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                          ctypes.POINTER(ctypes.c_uint32), ctypes.c_void_p,
                                          ctypes.POINTER(ctypes.c_uint32)]),
@@ -266,6 +273,16 @@ def copy_to_device(dst_ptr: int, array: np.ndarray, stream: Optional[Stream] = N
     array = np.ascontiguousarray(array)
     check(lib().kimkv_memcpy_h2d_async(ctypes.c_void_p(dst_ptr), array.ctypes.data_as(ctypes.c_void_p),
                                        array.nbytes, _sh(stream)), "h2d")
+    sync(stream)
+
+
+def patch_descriptors(patches: np.ndarray, descriptors: np.ndarray, stream: Optional[Stream] = None) -> None:
+    """kimkv_patch_descriptors with both arrays uploaded to device memory (waited for)."""
+    patches = np.ascontiguousarray(patches, dtype=DESCRIPTOR_PATCH)
+    descriptors = np.ascontiguousarray(descriptors, dtype=BLOCK_DESC)
+    p, d = upload(patches, stream), upload(descriptors, stream)
+    check(lib().kimkv_patch_descriptors(ctypes.c_void_p(p.ptr), len(patches), ctypes.c_void_p(d.ptr), _sh(stream)),
+          "patch_descriptors")
     sync(stream)
 
 

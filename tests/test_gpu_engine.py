@@ -138,6 +138,68 @@ def test_engine_backend_tokens_fork_and_faults(host, dev):
     stream.destroy()
 
 
+def _closed_form_prefill(dev, tokens):
+    """[layer][K/V][token][1 head][2 dims] fp16 rows of run_token's closed form for `tokens`."""
+    kv = np.zeros((2, 2, len(tokens), 1, 2), dtype=np.float32)
+    for layer in range(2):
+        off = 0.02 if layer == 1 else 0.0
+        for j, t in enumerate(tokens):
+            kv[layer, 0, j, 0] = (0.1 * (t + 1) + off, -0.05 * t + off * 0.5)
+            kv[layer, 1, j, 0] = (t + 1 + off * 10.0, (t + 1) * 0.5 - off * 5.0)
+    return kv.astype(np.float16).view(np.uint16)
+
+
+def test_engine_device_table_after_rollback_and_append(host, dev):
+    """Each request's device block table is patched in place per token; a
+    reservation that is rolled back leaves the candidate in the device copy.
+    The next reservation must rewrite it, also when a prefill append has
+    meanwhile moved the table to the version the abandoned candidate had,
+    and when a fork's first token replaces the shared partial tail."""
+    engine = host.Engine(2, 1, 2, 2, 4096, 64, 4)
+    assert engine.create_request(1) == 0
+    stream = dev.Stream()
+    buf = Buffers(dev)
+    history = []
+    for token in range(10):
+        assert run_token(host, dev, engine, 1, history, token, buf, stream)
+    staged = dev.DeviceBuffer(2 * 2 * 16 * 2 * 2)
+    for round_ in range(2):
+        # Reserve, write and attend a token, then roll it back.
+        rc, txn = engine.reserve_token(1, len(history), stream)
+        assert rc == 0, host.ENGINE_ERRORS[rc]
+        for layer in range(2):
+            assert txn.write_layer(layer, buf.keys[layer].ptr, buf.values[layer].ptr) == 0
+            assert txn.attend_layer(layer, buf.query.ptr, buf.output.ptr, buf.workspace.ptr, buf.workspace_bytes,
+                                    1.0 / math.sqrt(2.0)) == 0
+        assert txn.rollback() == 0
+        txn.close()
+        assert engine.check_invariants()
+        if round_ == 0:
+            # Same version as before the reservation: rewritten on the next reserve.
+            assert run_token(host, dev, engine, 1, history, 40, buf, stream)
+        else:
+            # A prefill append takes the table to the abandoned candidate's version.
+            tokens = list(range(50, 55))
+            dev.copy_to_device(staged.ptr, _closed_form_prefill(dev, tokens).reshape(-1), stream)
+            rc, _ = engine.append_prefill(1, len(tokens), staged.ptr, stream, promote=False)
+            assert rc == 0, host.ENGINE_ERRORS[rc]
+            history.extend(tokens)
+            assert run_token(host, dev, engine, 1, history, 41, buf, stream)
+    for token in range(42, 48):
+        assert run_token(host, dev, engine, 1, history, token, buf, stream)
+    # A fork shares the partial tail; its first token replaces it (COW) in
+    # the child's own device table while the parent's stays valid.
+    assert engine.fork_request(1, 2) == 0
+    child = list(history)
+    assert run_token(host, dev, engine, 2, child, 60, buf, stream)
+    assert run_token(host, dev, engine, 1, history, 61, buf, stream)
+    assert run_token(host, dev, engine, 2, child, 62, buf, stream)
+    assert engine.release_request(2) == 0
+    assert engine.release_request(1) == 0
+    assert engine.check_invariants()
+    stream.destroy()
+
+
 def test_extent_plus_micro_attention_known_answer(host, dev):
     """testExtentPagedAttention, cuda_engine_kv_backend_test.cpp:347-500: 64
     tokens K=(1,1), V=(t/64, -t/128) promoted into one extent, then a token
@@ -723,8 +785,10 @@ def test_engine_head_split_batch_matches_oracle(host, dev):
 
 
 def test_engine_small_staging_ring(host, dev, monkeypatch):
-    """The same lanes with a 64 KiB staging ring: each reserve's ~50 KB
-    descriptor upload goes in pieces and the ring wraps several times per step
-    (items, jobs and descriptor pieces interleaved), over three steps."""
+    """The same lanes with a 64 KiB staging ring (32 KiB per request): the
+    first reserve writes every lane's whole device table (~60 KB of patches
+    and descriptors, so several patch launches), the later ones patch one
+    entry per lane, and the ring wraps with items, jobs and patches
+    interleaved, over three steps."""
     monkeypatch.setenv("KIMKV_STAGING_RING_BYTES", str(64 << 10))
     _engine_lane_batch_case(host, dev, steps=3, seed=78)

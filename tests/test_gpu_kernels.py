@@ -65,6 +65,30 @@ def test_append_gather_bit_exact(dev, shape, T):
     assert np.array_equal(got, pools.gather(table, T))
 
 
+def test_patch_descriptors(dev):
+    """kimkv_patch_descriptors: whole-table writes (one longer than a
+    workgroup's 256 words) and one-entry tail patches land exactly on their
+    ranges, all 20 bytes of each entry; entries no patch names keep theirs."""
+    rng = np.random.default_rng(11)
+    n_tables, cap = 5, 700
+    tables = [dev.DeviceBuffer(cap * 20) for _ in range(n_tables)]
+    want = []
+    for t in tables:
+        init = rng.integers(0, 256, (cap, 20), dtype=np.uint8)
+        dev.copy_to_device(t.ptr, init)
+        want.append(init)
+    src = rng.integers(0, 256, (2000, 20), dtype=np.uint8)
+    spans = [(0, 0, 600, 0), (1, 3, 1, 600), (2, 699, 1, 601), (3, 10, 52, 602), (4, 0, 1, 654), (4, 1, 645, 655)]
+    patches = np.zeros(len(spans), dtype=dev.DESCRIPTOR_PATCH)
+    for k, (ti, first, count, source) in enumerate(spans):
+        patches[k] = (tables[ti].ptr, first, count, source)
+        want[ti][first:first + count] = src[source:source + count]
+    dev.patch_descriptors(patches, src.view(dev.BLOCK_DESC).reshape(-1))
+    for t, w in zip(tables, want):
+        assert np.array_equal(dev.download(t.ptr, (cap, 20), np.uint8), w)
+    dev.patch_descriptors(np.zeros(0, dtype=dev.DESCRIPTOR_PATCH), src.view(dev.BLOCK_DESC).reshape(-1))
+
+
 def test_fill_rows_matches_oracle(dev):
     n = 100003
     buf = dev.DeviceBuffer(n * 2)
