@@ -69,6 +69,26 @@ struct TokenReservationDelta final {
     }
 };
 
+// What KvCacheManager::appendWithLease changed: the table's entries from
+// `first_entry` on (the extended or copy-on-write-replaced partial tail, then
+// the fresh pages), the copy-on-write source when a shared partial tail was
+// replaced, and a read lease on exactly the pages a device copy of the new
+// tokens touches (those entries' pages and the replaced tail).  No
+// counterpart in the reference, whose callers lease and copy the whole table
+// before and after append().
+struct AppendChange final {
+    KvCacheError error{KvCacheError::None};
+    std::uint32_t logical_token_begin{0};              // committed tokens before the append
+    std::uint64_t version{0};                          // the table's new version
+    std::size_t first_entry{0};
+    std::vector<MappingEntry> entries;
+    PageHandle replaced_tail{PageHandle::invalid()};
+    std::uint16_t replaced_tokens{0};
+    PageLeaseId lease_id{kInvalidPageLeaseId};
+
+    [[nodiscard]] bool ok() const noexcept { return error == KvCacheError::None && lease_id != kInvalidPageLeaseId; }
+};
+
 class KvCacheManager final {
 public:
     KvCacheManager(std::uint32_t micro_capacity, std::uint32_t extent_capacity);
@@ -80,6 +100,10 @@ public:
 
     [[nodiscard]] KvCacheError createRequest(RequestId request_id);
     [[nodiscard]] KvCacheError append(RequestId request_id, std::uint32_t token_count);
+    // append() in time proportional to the appended tokens (no table copy),
+    // plus the lease described at AppendChange; release it with
+    // releasePageLease once the device copy is done.
+    [[nodiscard]] AppendChange appendWithLease(RequestId request_id, std::uint32_t token_count);
 
     [[nodiscard]] TokenReservationResult reserveToken(RequestId request_id,
                                                       std::uint32_t expected_committed_tokens);
@@ -169,6 +193,9 @@ private:
     [[nodiscard]] static std::uint64_t nextId(std::uint64_t& counter, Map const& live);
 
     [[nodiscard]] bool hasReservationLocked(RequestId request_id) const noexcept;
+    // append()'s body: with `change` only the changed entries are checked and
+    // the lease is taken, else the whole candidate table is checked.
+    [[nodiscard]] KvCacheError appendLocked(RequestId request_id, std::uint32_t token_count, AppendChange* change);
     // reserveToken's body; with `candidate` the full candidate table is built
     // there and checked whole, else only its changed tail is checked.
     [[nodiscard]] TokenReservationDelta reserveLocked(RequestId request_id, std::uint32_t expected_committed_tokens,

@@ -1,7 +1,10 @@
 // HipKvCache: metadata + device pools for the micro-benchmark path
 // (semantics of src/cuda/kv/cache.cpp:76-293 in the reference: read leases
 // around every device access, a failed device append cancels the request,
-// a failed promotion copy rolls the promotion back).
+// a failed promotion copy rolls the promotion back).  An append leases only
+// the pages its copy touches and builds its jobs from the manager's change
+// record, so its cost does not grow with the context (the reference leases
+// and copies the whole table before and after).
 #include "kim-kv/hip/hip_kv_cache.h"
 
 #include "storage.h"
@@ -38,53 +41,42 @@ KvCacheError HipKvCache::releaseRequest(RequestId id) { return manager_.releaseR
 HipKvOperationResult HipKvCache::append(RequestId request_id, std::uint32_t token_count, KvScalar const* device_input,
                                         HipStream stream)
 {
-    if (request_id == kInvalidRequestId || token_count == 0 || device_input == nullptr) {
-        return metadataFailure(KvCacheError::InvalidArgument);
+    HipKvOperationResult result;
+    appendBatch(&request_id, 1, token_count, &device_input, stream, &result);
+    if (result.ok() && !manager_.blockTable(request_id).has_value()) {
+        return metadataFailure(KvCacheError::RequestNotFound);
     }
-    HipStatus const st = status();
-    if (!st.ok()) return HipKvOperationResult{KvCacheError::None, st};
-    PageLeaseAcquireResult before = manager_.acquireRequestReadLease(request_id);
-    if (!before.ok()) return metadataFailure(before.error);
-    std::uint32_t const begin = before.table.tokenCount();
-    KvCacheError const appended = manager_.append(request_id, token_count);
-    if (appended != KvCacheError::None) {
-        KvCacheError const l = manager_.releasePageLease(before.lease_id);
-        return metadataFailure(l == KvCacheError::None ? appended : l);
-    }
-    PageLeaseAcquireResult after = manager_.acquireRequestReadLease(request_id);
-    if (!after.ok()) {
-        KvCacheError const l = manager_.releasePageLease(before.lease_id);
-        if (after.error != KvCacheError::RequestNotFound) static_cast<void>(manager_.releaseRequest(request_id));
-        return metadataFailure(l == KvCacheError::None ? after.error : l);
-    }
-    HipStatus const device = storage_->append(before.table, after.table, begin, token_count, device_input, stream);
-    KvCacheError const ra = manager_.releasePageLease(after.lease_id);
-    KvCacheError const rb = manager_.releasePageLease(before.lease_id);
-    if (ra != KvCacheError::None) return metadataFailure(ra);
-    if (rb != KvCacheError::None) return metadataFailure(rb);
-    if (!device.ok()) {
-        // The metadata append is committed but the pages are not: cancel the
-        // request rather than expose uninitialised KV.
-        KvCacheError const c = manager_.releaseRequest(request_id);
-        if (c != KvCacheError::None && c != KvCacheError::RequestNotFound) return HipKvOperationResult{c, device};
-        return HipKvOperationResult{KvCacheError::None, device};
-    }
-    if (!manager_.blockTable(request_id).has_value()) return metadataFailure(KvCacheError::RequestNotFound);
-    return {};
+    return result;
 }
 
+// Per request: the manager's in-place append, which also leases exactly the
+// pages the copy touches (the new tokens' pages and a copy-on-write source),
+// and that change's jobs; then one append launch for every request, waited
+// for, and the leases released.  A request whose pages do not check out, or
+// every request of a failed launch, is cancelled: its metadata append is
+// committed but its pages are not written.
 void HipKvCache::appendBatch(RequestId const* request_ids, std::size_t count, std::uint32_t token_count,
                              KvScalar const* const* device_inputs, HipStream stream, HipKvOperationResult* results)
 {
     struct Pending {
         std::size_t index;
-        PageLeaseAcquireResult before;
-        PageLeaseAcquireResult after;
-        std::uint32_t begin;
+        PageLeaseId lease;
     };
-    std::vector<Pending> pending;
-    pending.reserve(count);
+    thread_local std::vector<Pending> pending;
+    thread_local std::vector<kimkv_append_job> jobs;
+    pending.clear();
+    jobs.clear();
     HipStatus const st = status();
+    auto settle = [&](std::size_t i, PageLeaseId lease, HipStatus device) {
+        KvCacheError const l = manager_.releasePageLease(lease);
+        if (!device.ok()) {
+            KvCacheError const c = manager_.releaseRequest(request_ids[i]);
+            results[i] = HipKvOperationResult{
+                c != KvCacheError::None && c != KvCacheError::RequestNotFound ? c : KvCacheError::None, device};
+        } else {
+            results[i] = l == KvCacheError::None ? HipKvOperationResult{} : metadataFailure(l);
+        }
+    };
     for (std::size_t i = 0; i < count; ++i) {
         RequestId const id = request_ids[i];
         if (id == kInvalidRequestId || token_count == 0 || device_inputs[i] == nullptr) {
@@ -95,53 +87,20 @@ void HipKvCache::appendBatch(RequestId const* request_ids, std::size_t count, st
             results[i] = HipKvOperationResult{KvCacheError::None, st};
             continue;
         }
-        PageLeaseAcquireResult before = manager_.acquireRequestReadLease(id);
-        if (!before.ok()) {
-            results[i] = metadataFailure(before.error);
+        AppendChange const change = manager_.appendWithLease(id, token_count);
+        if (!change.ok()) {
+            results[i] = metadataFailure(change.error);
             continue;
         }
-        std::uint32_t const begin = before.table.tokenCount();
-        KvCacheError const appended = manager_.append(id, token_count);
-        if (appended != KvCacheError::None) {
-            KvCacheError const l = manager_.releasePageLease(before.lease_id);
-            results[i] = metadataFailure(l == KvCacheError::None ? appended : l);
+        if (!storage_->changeJobs(change, token_count, device_inputs[i], jobs)) {
+            settle(i, change.lease_id, HipStatus{HipError::InvalidArgument, 0});
             continue;
         }
-        PageLeaseAcquireResult after = manager_.acquireRequestReadLease(id);
-        if (!after.ok()) {
-            KvCacheError const l = manager_.releasePageLease(before.lease_id);
-            if (after.error != KvCacheError::RequestNotFound) static_cast<void>(manager_.releaseRequest(id));
-            results[i] = metadataFailure(l == KvCacheError::None ? after.error : l);
-            continue;
-        }
-        pending.push_back(Pending{i, std::move(before), std::move(after), begin});
+        pending.push_back(Pending{i, change.lease_id});
     }
     if (pending.empty()) return;
-    std::vector<HipKvStorage::AppendPlan> plans;
-    plans.reserve(pending.size());
-    for (Pending const& p : pending) {
-        plans.push_back(HipKvStorage::AppendPlan{&p.before.table, &p.after.table, p.begin, token_count,
-                                                 device_inputs[p.index]});
-    }
-    HipStatus const device = storage_->appendMany(plans, stream);
-    for (Pending& p : pending) {
-        KvCacheError const ra = manager_.releasePageLease(p.after.lease_id);
-        KvCacheError const rb = manager_.releasePageLease(p.before.lease_id);
-        RequestId const id = request_ids[p.index];
-        if (!device.ok()) {
-            KvCacheError const c = manager_.releaseRequest(id);
-            results[p.index] = HipKvOperationResult{
-                c != KvCacheError::None && c != KvCacheError::RequestNotFound ? c : KvCacheError::None, device};
-            continue;
-        }
-        if (ra != KvCacheError::None) {
-            results[p.index] = metadataFailure(ra);
-        } else if (rb != KvCacheError::None) {
-            results[p.index] = metadataFailure(rb);
-        } else {
-            results[p.index] = {};
-        }
-    }
+    HipStatus const device = storage_->appendJobsNow(jobs, stream);
+    for (Pending const& p : pending) settle(p.index, p.lease, device);
 }
 
 HipKvOperationResult HipKvCache::promote(RequestId request_id, std::uint32_t logical_token_begin, HipStream stream)

@@ -397,15 +397,17 @@ bool HipKvStorage::appendSegments(BlockTable const& before, BlockTable const& af
         || before.tokenCount() != begin || after.tokenCount() != end) {
         return false;
     }
-    // Copy-on-write source of the replaced partial tail, if any.
+    // Copy-on-write source of the replaced partial tail, if any.  Both
+    // tables are contiguous from token 0 and `after` extends `before`, so an
+    // entry of `before` can only reappear at its own index.
     PageHandle cow_src = PageHandle::invalid();
     std::uint16_t cow_tokens = 0;
     PageHandle cow_dst = PageHandle::invalid();
-    for (MappingEntry const& old : before.entries()) {
-        auto rep = std::find_if(after.entries().begin(), after.entries().end(), [&old](MappingEntry const& e) {
-            return e.logical_token_begin == old.logical_token_begin;
-        });
-        if (rep == after.entries().end()) return false;
+    if (after.entries().size() < before.entries().size()) return false;
+    for (std::size_t k = 0; k < before.entries().size(); ++k) {
+        MappingEntry const& old = before.entries()[k];
+        auto const rep = after.entries().begin() + static_cast<std::ptrdiff_t>(k);
+        if (rep->logical_token_begin != old.logical_token_begin) return false;
         if (rep->handle == old.handle) continue;
         bool const tail = old.logicalTokenEnd() == begin;
         if (!tail || old.kind != PageKind::Micro || rep->kind != PageKind::Micro || old.valid_tokens >= micro_tokens_
@@ -498,16 +500,70 @@ HipStatus HipKvStorage::append(BlockTable const& before, BlockTable const& after
     return launchAppendJobs(jobs, stream);
 }
 
-HipStatus HipKvStorage::appendMany(std::vector<AppendPlan> const& plans, HipStream stream)
+bool HipKvStorage::changeJobs(AppendChange const& change, std::uint32_t count, KvScalar const* input,
+                              std::vector<kimkv_append_job>& jobs) const
+{
+    std::uint32_t const begin = change.logical_token_begin;
+    std::uint64_t const end = static_cast<std::uint64_t>(begin) + count;
+    if (input == nullptr || count == 0 || end > 0xFFFFFFFFull || change.entries.empty()
+        || change.entries.front().logical_token_begin > begin) {
+        return false;
+    }
+    bool const cow = change.replaced_tail.isStructurallyValid();
+    if (cow) {
+        // The private copy continues the replaced partial tail: its first
+        // replaced_tokens tokens come from the source page, then the new ones.
+        MappingEntry const& dst = change.entries.front();
+        if (!pageExists(change.replaced_tail) || change.replaced_tail.kind != PageKind::Micro
+            || dst.kind != PageKind::Micro || change.replaced_tokens == 0 || change.replaced_tokens >= micro_tokens_
+            || static_cast<std::uint64_t>(dst.logical_token_begin) + change.replaced_tokens != begin) {
+            return false;
+        }
+    }
+    std::size_t const first = jobs.size();
+    std::size_t const hd = static_cast<std::size_t>(layout_.kv_head_count) * layout_.head_dimension;
+    std::uint64_t next = change.entries.front().logical_token_begin;
+    for (std::size_t k = 0; k < change.entries.size(); ++k) {
+        MappingEntry const& e = change.entries[k];
+        kimkv_block_desc d{};
+        if (!descriptor(e, d) || e.logical_token_begin != next) {
+            jobs.resize(first);
+            return false;
+        }
+        next += e.valid_tokens;
+        std::uint32_t const sb = std::max(begin, e.logical_token_begin);
+        std::uint32_t const se = static_cast<std::uint32_t>(std::min<std::uint64_t>(end, e.logicalTokenEnd()));
+        if (sb >= se) continue;
+        kimkv_append_job j{};
+        std::size_t const off = static_cast<std::size_t>(sb - begin) * hd;
+        j.src_key = input + off;
+        j.src_value = input + static_cast<std::size_t>(count) * hd + off;
+        j.src_layer_stride = 2ull * count * hd;
+        j.src_token_stride = static_cast<std::uint32_t>(hd);
+        j.layer_begin = 0;
+        j.layer_count = layout_.layer_count;
+        j.token_count = se - sb;
+        j.dst_slot = e.handle.slot;
+        j.dst_kind = static_cast<std::uint8_t>(e.kind);
+        j.dst_token = static_cast<std::uint16_t>(sb - e.logical_token_begin);
+        if (cow && k == 0) {
+            j.cow_slot = change.replaced_tail.slot;
+            j.cow_kind = static_cast<std::uint8_t>(change.replaced_tail.kind);
+            j.cow_tokens = change.replaced_tokens;
+        }
+        jobs.push_back(j);
+    }
+    if (next != end || jobs.size() == first) {
+        jobs.resize(first);
+        return false;
+    }
+    return true;
+}
+
+HipStatus HipKvStorage::appendJobsNow(std::vector<kimkv_append_job> const& jobs, HipStream stream)
 {
     if (!status_.ok()) return status_;
     if (consumeFailure(HipFailurePoint::Submission)) return HipStatus{HipError::SubmissionFailed, 0};
-    std::vector<kimkv_append_job> jobs;
-    for (AppendPlan const& p : plans) {
-        if (!appendJobs(*p.before, *p.after, p.begin, p.count, p.input, jobs)) {
-            return HipStatus{HipError::InvalidArgument, 0};
-        }
-    }
     if (jobs.empty()) return HipStatus{HipError::InvalidArgument, 0};
     return launchAppendJobs(jobs, stream);
 }

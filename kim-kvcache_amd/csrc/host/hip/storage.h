@@ -9,6 +9,7 @@
 #include "kim-kv/core/block_table.h"
 #include "kim-kv/core/kv_layout.h"
 #include "kim-kv/hip/hip_status.h"
+#include "kim-kv/runtime/kv_cache_manager.h"
 #include "kim-kv/runtime/promotion.h"
 #include "ring_regions.h"
 
@@ -146,15 +147,15 @@ public:
     [[nodiscard]] HipStatus append(BlockTable const& before, BlockTable const& after,
                                    std::uint32_t append_token_begin, std::uint32_t token_count,
                                    KvScalar const* device_input, HipStream stream);
-    // Several requests' appends in one launch.
-    struct AppendPlan {
-        BlockTable const* before;
-        BlockTable const* after;
-        std::uint32_t begin;
-        std::uint32_t count;
-        KvScalar const* input;
-    };
-    [[nodiscard]] HipStatus appendMany(std::vector<AppendPlan> const& plans, HipStream stream);
+    // Jobs of one metadata append from its AppendChange (the new tokens land
+    // in change.entries; the first of them continues the copy-on-write
+    // source, if any) for a [layer][K/V][count][head][dim] input.  Checks
+    // every named page and the copy-on-write rule; false leaves `jobs` as it
+    // was.  Proportional to the appended tokens, not to the table.
+    [[nodiscard]] bool changeJobs(AppendChange const& change, std::uint32_t count, KvScalar const* input,
+                                  std::vector<kimkv_append_job>& jobs) const;
+    // One launch of jobs from changeJobs (several requests), waited for.
+    [[nodiscard]] HipStatus appendJobsNow(std::vector<kimkv_append_job> const& jobs, HipStream stream);
     [[nodiscard]] HipStatus gather(BlockTable const& table, KvScalar* device_output, HipStream stream);
     [[nodiscard]] HipStatus promote(PromotionPrepareResult const& promotion, HipStream stream);
     [[nodiscard]] HipStatus promoteBatch(std::vector<PromotionPrepareResult> const& promotions, HipStream stream);

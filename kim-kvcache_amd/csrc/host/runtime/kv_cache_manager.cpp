@@ -176,6 +176,23 @@ KvCacheError KvCacheManager::append(RequestId request_id, std::uint32_t token_co
 {
     if (request_id == kInvalidRequestId || token_count == 0) return KvCacheError::InvalidArgument;
     std::lock_guard<std::mutex> lock(mutex_);
+    return appendLocked(request_id, token_count, nullptr);
+}
+
+AppendChange KvCacheManager::appendWithLease(RequestId request_id, std::uint32_t token_count)
+{
+    AppendChange change;
+    if (request_id == kInvalidRequestId || token_count == 0) {
+        change.error = KvCacheError::InvalidArgument;
+        return change;
+    }
+    std::lock_guard<std::mutex> lock(mutex_);
+    change.error = appendLocked(request_id, token_count, &change);
+    return change;
+}
+
+KvCacheError KvCacheManager::appendLocked(RequestId request_id, std::uint32_t token_count, AppendChange* change)
+{
     auto it = tables_.find(request_id);
     if (it == tables_.end()) return KvCacheError::RequestNotFound;
     if (hasReservationLocked(request_id)) return KvCacheError::RequestConflict;
@@ -183,42 +200,48 @@ KvCacheError KvCacheManager::append(RequestId request_id, std::uint32_t token_co
     std::uint32_t const old_tokens = table.tokenCount();
     if (token_count > kU32Max - old_tokens) return KvCacheError::InvalidArgument;
 
-    BlockTable cand = table;
+    // Only the table's end changes: `part` replaces its entries from `first`
+    // on -- the partial micro tail, when there is one (extended in place, or
+    // continued in a private copy when it is sealed), then fresh pages.
     std::size_t const max_new = (static_cast<std::size_t>(token_count) + kMicroPageTokenCapacity - 1)
             / kMicroPageTokenCapacity + 1;
-    cand.entries_.reserve(cand.entries_.size() + max_new);
-    std::vector<Staged> staged;
+    table.entries_.reserve(table.entries_.size() + max_new);   // so that the commit cannot fail on memory
+    std::size_t first = table.entries_.size();
+    std::vector<MappingEntry> part;
+    part.reserve(max_new);
+    std::vector<Staged> staged;   // entry: index in the new table
     staged.reserve(max_new);
 
-    std::size_t active = kNoEntry;
+    std::size_t active = kNoEntry;   // index in `part` of the page taking tokens
     PageHandle existing_mutable = PageHandle::invalid();
     PageHandle replaced_tail = PageHandle::invalid();
+    std::uint16_t replaced_tokens = 0;
 
-    if (!cand.entries_.empty()) {
-        std::size_t const tail_index = cand.entries_.size() - 1;
-        MappingEntry& tail = cand.entries_[tail_index];
+    if (!table.entries_.empty()) {
+        MappingEntry tail = table.entries_.back();
         Page* tp = page(tail.handle);
         if (tp == nullptr || tp->valid_tokens != tail.valid_tokens) return KvCacheError::InternalInvariantViolation;
         if (tail.kind == PageKind::Micro && tail.valid_tokens < kMicroPageTokenCapacity) {
+            first = table.entries_.size() - 1;
             if (tp->state == PageState::Mutable) {
                 if (tp->ref_count != 1 || tp->mutable_owner != request_id) {
                     return KvCacheError::InternalInvariantViolation;
                 }
                 existing_mutable = tail.handle;
-                active = tail_index;
             } else if (tp->state == PageState::Sealed) {
                 // Shared or sealed partial tail: continue in a private copy.
                 PageHandle copy = PageHandle::invalid();
                 KvCacheError const e = stageMicroLocked(tail.valid_tokens, copy);
                 if (e != KvCacheError::None) return e;
-                staged.push_back(Staged{copy, tail_index});
+                staged.push_back(Staged{copy, first});
                 replaced_tail = tail.handle;
-                tail.kind = PageKind::Micro;
+                replaced_tokens = tail.valid_tokens;
                 tail.handle = copy;
-                active = tail_index;
             } else {
                 return KvCacheError::InvalidState;
             }
+            part.push_back(tail);
+            active = 0;
         } else if (tp->state != PageState::Sealed) {
             return KvCacheError::InternalInvariantViolation;
         }
@@ -234,25 +257,42 @@ KvCacheError KvCacheManager::append(RequestId request_id, std::uint32_t token_co
                 unstageLocked(staged);
                 return e;
             }
-            std::size_t const idx = cand.entries_.size();
-            cand.entries_.push_back(MappingEntry{logical_end, 0, PageKind::Micro, fresh});
-            staged.push_back(Staged{fresh, idx});
-            active = idx;
+            part.push_back(MappingEntry{logical_end, 0, PageKind::Micro, fresh});
+            active = part.size() - 1;
+            staged.push_back(Staged{fresh, first + active});
         }
-        MappingEntry& a = cand.entries_[active];
+        MappingEntry& a = part[active];
         std::uint32_t const take = std::min<std::uint32_t>(remaining, kMicroPageTokenCapacity - a.valid_tokens);
         a.valid_tokens = static_cast<std::uint16_t>(a.valid_tokens + take);
         logical_end += take;
         remaining -= take;
         if (a.valid_tokens == kMicroPageTokenCapacity) active = kNoEntry;
     }
-    cand.version_ = table.version_ + 1;
 
     auto fail = [&](KvCacheError e) {
         unstageLocked(staged);
         return e;
     };
-    if (!cand.checkInvariants()) return fail(KvCacheError::InternalInvariantViolation);
+    if (change == nullptr) {
+        BlockTable cand = table;
+        cand.entries_.resize(first);
+        cand.entries_.insert(cand.entries_.end(), part.begin(), part.end());
+        cand.version_ = table.version_ + 1;
+        if (!cand.checkInvariants()) return fail(KvCacheError::InternalInvariantViolation);
+    } else {
+        // The committed table satisfies the table invariants and a staged
+        // page is in no table, so checking the replaced end (contiguous with
+        // the kept entries, micro pages of 1..8 tokens) checks the candidate.
+        std::uint32_t next = first < table.entries_.size() ? table.entries_[first].logical_token_begin : old_tokens;
+        for (MappingEntry const& e : part) {
+            if (!e.handle.isStructurallyValid() || e.handle.kind != PageKind::Micro || e.kind != PageKind::Micro
+                || e.logical_token_begin != next || e.valid_tokens == 0 || e.valid_tokens > kMicroPageTokenCapacity) {
+                return fail(KvCacheError::InternalInvariantViolation);
+            }
+            next += e.valid_tokens;
+        }
+        if (next != logical_end) return fail(KvCacheError::InternalInvariantViolation);
+    }
     if (existing_mutable.isStructurallyValid()) {
         Page* p = page(existing_mutable);
         if (p == nullptr || p->state != PageState::Mutable || p->ref_count != 1 || p->mutable_owner != request_id) {
@@ -267,39 +307,73 @@ KvCacheError KvCacheManager::append(RequestId request_id, std::uint32_t token_co
     }
     for (Staged const& s : staged) {
         Page* p = page(s.handle);
-        if (p == nullptr || p->state != PageState::CopyTarget || p->ref_count != 0
-            || s.entry >= cand.entries_.size() || cand.entries_[s.entry].handle != s.handle) {
+        if (p == nullptr || p->state != PageState::CopyTarget || p->ref_count != 0 || s.entry < first
+            || s.entry - first >= part.size() || part[s.entry - first].handle != s.handle) {
             return fail(KvCacheError::InternalInvariantViolation);
         }
+    }
+
+    // The device copy's lease, taken before the replaced tail loses this
+    // table's reference so that a copy-on-write source outlives the copy.
+    PageLeaseId lease = kInvalidPageLeaseId;
+    std::vector<PageHandle> const* leased = nullptr;
+    if (change != nullptr) {
+        std::vector<PageHandle> handles;
+        handles.reserve(part.size() + 1);
+        for (MappingEntry const& e : part) handles.push_back(e.handle);
+        if (replaced_tail.isStructurallyValid()) handles.push_back(replaced_tail);
+        for (PageHandle const h : handles) {
+            if (page(h)->inflight_readers == kU32Max) return fail(KvCacheError::InvalidState);
+        }
+        lease = nextId(next_lease_id_, leases_);
+        if (lease == kInvalidPageLeaseId) return fail(KvCacheError::InternalInvariantViolation);
+        auto inserted = leases_.emplace(lease, std::move(handles));
+        if (!inserted.second) return fail(KvCacheError::InternalInvariantViolation);
+        leased = &inserted.first->second;
+        for (PageHandle const h : *leased) ++page(h)->inflight_readers;
     }
 
     // Commit: nothing below can fail except an inconsistent replaced tail.
     if (replaced_tail.isStructurallyValid()) {
         KvCacheError const e = dropReferenceLocked(replaced_tail);
-        if (e != KvCacheError::None) return fail(e);
+        if (e != KvCacheError::None) {
+            if (leased != nullptr) {
+                for (PageHandle const h : *leased) --page(h)->inflight_readers;
+                leases_.erase(lease);
+            }
+            return fail(e);
+        }
     }
     if (existing_mutable.isStructurallyValid()) {
         Page* p = page(existing_mutable);
-        for (MappingEntry const& e : cand.entries_) {
-            if (e.handle != existing_mutable) continue;
-            p->valid_tokens = e.valid_tokens;
-            if (e.valid_tokens == kMicroPageTokenCapacity) {
-                p->state = PageState::Sealed;
-                p->mutable_owner = kInvalidRequestId;
-            }
-            break;
+        MappingEntry const& e = part.front();   // the extended tail
+        p->valid_tokens = e.valid_tokens;
+        if (e.valid_tokens == kMicroPageTokenCapacity) {
+            p->state = PageState::Sealed;
+            p->mutable_owner = kInvalidRequestId;
         }
     }
     for (Staged const& s : staged) {
         Page* p = page(s.handle);
-        MappingEntry const& e = cand.entries_[s.entry];
+        MappingEntry const& e = part[s.entry - first];
         p->valid_tokens = e.valid_tokens;
         p->ref_count = 1;
         bool const full = e.valid_tokens == kMicroPageTokenCapacity;
         p->state = full ? PageState::Sealed : PageState::Mutable;
         p->mutable_owner = full ? kInvalidRequestId : request_id;
     }
-    table = std::move(cand);
+    table.entries_.resize(first);
+    table.entries_.insert(table.entries_.end(), part.begin(), part.end());
+    ++table.version_;
+    if (change != nullptr) {
+        change->logical_token_begin = old_tokens;
+        change->version = table.version_;
+        change->first_entry = first;
+        change->entries = std::move(part);
+        change->replaced_tail = replaced_tail;
+        change->replaced_tokens = replaced_tokens;
+        change->lease_id = lease;
+    }
     return KvCacheError::None;
 }
 

@@ -2,7 +2,9 @@
 uses a fake KV backend and a fake model and mirrors the reference's
 tests/engine scenarios for the single-request generation runtime and the
 iteration scheduler; staging_ring_test replays allocation sequences through
-the staging ring's region bookkeeping."""
+the staging ring's region bookkeeping; manager_delta_test runs the
+manager's delta append and reservation paths against its reference-form calls
+on twin managers."""
 import os
 import subprocess
 
@@ -11,7 +13,8 @@ import pytest
 BIN = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "kim-kvcache_amd", "_lib", "tests")
 
 
-@pytest.mark.parametrize("name", ["generation_contract_test", "staging_ring_test", "kv_reference_test", "sha256_test"])
+@pytest.mark.parametrize("name", ["generation_contract_test", "staging_ring_test", "kv_reference_test", "sha256_test",
+                                  "manager_delta_test"])
 def test_cpp_contract(name):
     path = os.path.join(BIN, name)
     if not os.path.exists(path):
