@@ -174,7 +174,13 @@ kimkv_status kimkv_device_synchronize(void);
 
 /* Completion events (the reference's cudaEventRecord/Synchronize at the token
  * boundary, src/cuda/engine/transaction.cpp:84-120). */
-kimkv_status kimkv_event_create(void** event, int timing);
+/* kind: 0 = a synchronization event, 1 = one that also records timing,
+ * KIMKV_EVENT_ORDER_ONLY = a synchronization event whose completion
+ * publishes no device memory to the host (no system-scope cache writeback
+ * when it is reached): for fences that only tell the host that earlier work
+ * has finished reading memory the host wrote. */
+#define KIMKV_EVENT_ORDER_ONLY 2
+kimkv_status kimkv_event_create(void** event, int kind);
 kimkv_status kimkv_event_destroy(void* event);
 kimkv_status kimkv_event_record(void* event, kimkv_stream_t stream);
 kimkv_status kimkv_event_query(void* event);       /* KIMKV_OK or KIMKV_NOT_READY */

@@ -24,9 +24,33 @@ struct DecodeTiming {
     uint32_t every{1};        // time every n-th launch
     uint64_t seen{0};
     std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+    std::vector<hipEvent_t> spare;   // read events, reused
     double total_ms{0.0};
     uint64_t launches{0};
 };
+
+// A timing event: reused when one is spare.  No system-scope fence when it
+// is reached (nothing is published to the host; the fence's cache
+// writeback would only add to the timed span).
+hipEvent_t timing_event_locked(DecodeTiming& t)
+{
+    if (!t.spare.empty()) {
+        hipEvent_t const e = t.spare.back();
+        t.spare.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    return hipEventCreateWithFlags(&e, hipEventDisableSystemFence) == hipSuccess ? e : nullptr;
+}
+
+void spare_event_locked(DecodeTiming& t, hipEvent_t e)
+{
+    try {
+        t.spare.push_back(e);
+    } catch (...) {
+        static_cast<void>(hipEventDestroy(e));
+    }
+}
 
 DecodeTiming& timing(TimedKernel kind = TimedKernel::Decode)
 {
@@ -44,8 +68,8 @@ void drain_locked(DecodeTiming& t)
                 t.launches += 1;
             }
         }
-        static_cast<void>(hipEventDestroy(pair.first));
-        static_cast<void>(hipEventDestroy(pair.second));
+        spare_event_locked(t, pair.first);
+        spare_event_locked(t, pair.second);
     }
     t.pending.clear();
 }
@@ -75,11 +99,11 @@ void kernel_timing_begin(TimedKernel kind, hipStream_t stream, void** start)
     if (!t.enabled || t.seen++ % t.every != 0) {
         return;
     }
-    hipEvent_t event = nullptr;
-    if (hipEventCreate(&event) == hipSuccess && hipEventRecord(event, stream) == hipSuccess) {
+    hipEvent_t const event = timing_event_locked(t);
+    if (event != nullptr && hipEventRecord(event, stream) == hipSuccess) {
         *start = event;
     } else if (event != nullptr) {
-        static_cast<void>(hipEventDestroy(event));
+        spare_event_locked(t, event);
     }
 }
 
@@ -90,14 +114,20 @@ void kernel_timing_end(TimedKernel kind, hipStream_t stream, void* start)
     }
     DecodeTiming& t = timing(kind);
     std::lock_guard<std::mutex> lock(t.mutex);
-    hipEvent_t stop = nullptr;
-    if (hipEventCreate(&stop) == hipSuccess && hipEventRecord(stop, stream) == hipSuccess) {
-        t.pending.emplace_back(static_cast<hipEvent_t>(start), stop);
-    } else {
-        static_cast<void>(hipEventDestroy(static_cast<hipEvent_t>(start)));
-        if (stop != nullptr) {
-            static_cast<void>(hipEventDestroy(stop));
+    hipEvent_t const stop = timing_event_locked(t);
+    bool recorded = false;
+    if (stop != nullptr && hipEventRecord(stop, stream) == hipSuccess) {
+        try {
+            t.pending.emplace_back(static_cast<hipEvent_t>(start), stop);
+            recorded = true;
+        } catch (...) {
         }
+    }
+    if (!recorded) {
+        // The start event may still be pending on the stream: destroying a
+        // recorded event is allowed (HIP releases it once it completes).
+        static_cast<void>(hipEventDestroy(static_cast<hipEvent_t>(start)));
+        if (stop != nullptr) static_cast<void>(hipEventDestroy(stop));
     }
 }
 
@@ -216,13 +246,14 @@ kimkv_status kimkv_device_synchronize(void)
     return record_error(hipDeviceSynchronize(), KIMKV_EXECUTION_FAILED);
 }
 
-kimkv_status kimkv_event_create(void** event, int timing)
+kimkv_status kimkv_event_create(void** event, int kind)
 {
-    if (event == nullptr) return KIMKV_INVALID_ARGUMENT;
+    if (event == nullptr || kind < 0 || kind > KIMKV_EVENT_ORDER_ONLY) return KIMKV_INVALID_ARGUMENT;
+    unsigned const flags = kind == 1 ? hipEventDefault
+        : kind == KIMKV_EVENT_ORDER_ONLY ? (hipEventDisableTiming | hipEventDisableSystemFence)
+                                         : hipEventDisableTiming;
     hipEvent_t e = nullptr;
-    kimkv_status const status = record_error(
-        hipEventCreateWithFlags(&e, timing ? hipEventDefault : hipEventDisableTiming),
-        KIMKV_RUNTIME_UNAVAILABLE);
+    kimkv_status const status = record_error(hipEventCreateWithFlags(&e, flags), KIMKV_RUNTIME_UNAVAILABLE);
     *event = e;
     return status;
 }

@@ -159,7 +159,7 @@ void StagingRing::fence(HipStream stream)
     if (!spare_events_.empty()) {
         event = spare_events_.back();
         spare_events_.pop_back();
-    } else if (kimkv_event_create(&event, 0) != KIMKV_OK) {
+    } else if (kimkv_event_create(&event, KIMKV_EVENT_ORDER_ONLY) != KIMKV_OK) {
         event = nullptr;
     }
     if (event != nullptr && kimkv_event_record(event, stream) != KIMKV_OK) {
