@@ -1365,7 +1365,11 @@ def main() -> int:
     # One decode launch per layer per lane group: bytes per launch (mean over
     # all timed launches) and time per launch (mean over the timed sample).
     launches = args.steps * args.layers * (len(w.groups) if args.path == "engine" else 1)
-    per_launch_decode_bytes = decode_bytes / launches
+    # On the engine path a layer's decode launch also writes the lanes' new
+    # tokens (kimkv_paged_decode_write_batch); the kernel path appends in a
+    # launch of its own.
+    fused_bytes = append_bytes if args.path == "engine" else 0
+    per_launch_decode_bytes = (decode_bytes + fused_bytes) / launches
     decode_avg_ms = decode_ms_total / max(decode_launches, 1)
     achieved = per_launch_decode_bytes / (decode_avg_ms * 1e-3) / 1e9
 

@@ -315,6 +315,26 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage,
                                       uint32_t chunk_tokens, uint32_t query_heads,
                                       kimkv_stream_t stream);
 
+/* kimkv_paged_decode_batch with each lane's new token written in the same
+ * launch: device_writes[i] (memory the device reads) is lane i's
+ * single-token append job for this layer (token_count 1, layer_count 1,
+ * layer_begin = the item's layer, source rows [kv_heads][head_dim], its
+ * destination the lane's last table entry, optionally a copy-on-write
+ * source), or token_count 0 for none; the workgroups whose chunk holds the
+ * lane's last token write it (and the copy-on-write tokens) for their KV
+ * heads before reading the page.  Equals kimkv_append_batch of the jobs
+ * followed by kimkv_paged_decode_batch, in one launch.  No counterpart in
+ * the reference, which launches writeLayer and attendLayer separately
+ * (src/cuda/engine/transaction.cpp); the engine's batched token path uses it
+ * for writeLayerBatch + attendLayerBatch of a layer.  A job that names no
+ * page of the storage sets KIMKV_FAULT_APPEND_JOB and is skipped. */
+kimkv_status kimkv_paged_decode_write_batch(const kimkv_storage* storage,
+                                            const kimkv_decode_item* device_items,
+                                            const uint32_t* device_chunk_prefix, uint32_t lane_count,
+                                            uint32_t total_chunks, uint32_t chunk_flags,
+                                            uint32_t query_heads, const kimkv_append_job* device_writes,
+                                            kimkv_stream_t stream);
+
 /* Size of the device scratch array of kimkv_paged_decode_batch_noalloc. */
 #define KIMKV_DECODE_SCRATCH_BYTES (16u << 20)
 

@@ -528,6 +528,61 @@ __device__ void decode_head_split_chunk(const PoolView& P, const kimkv_decode_it
     store_partial(item, QH, h * G + r, chunk_index, single, o, d0, M, den, d0 == 0);
 }
 
+// The lane's new token for kv heads [h0, h1) of `layer`, written by the
+// workgroup whose chunk holds it (a write job of
+// kimkv_paged_decode_write_batch: one token, one layer, source rows [H][D]),
+// the copy-on-write of a replaced partial tail included.  Every thread of
+// the workgroup calls it; it issues the stores and returns without waiting:
+// the caller makes every thread wait for its stores (s_waitcnt) and then
+// synchronizes the workgroup before the first load of the page.  Only this
+// workgroup reads these heads of the page in this launch (the other chunks
+// end before the tail page, other heads are other blocks).  False when the
+// job does not name a page of this storage.
+__device__ bool write_token_heads(const PoolView& P, const kimkv_append_job& job, uint32_t layer, uint32_t h0,
+                                  uint32_t h1)
+{
+    uint32_t const D = P.dim;
+    uint32_t const dcap = pool_tokens(P, job.dst_kind);
+    uint16_t* dst = page_base(P, job.dst_kind, job.dst_slot, dcap);
+    if (dst == nullptr || job.token_count != 1 || job.layer_count != 1 || job.layer_begin != layer
+        || layer >= P.layers || job.dst_token >= dcap || job.src_key == nullptr || job.src_value == nullptr) {
+        return false;
+    }
+    uint32_t const tid = threadIdx.x;
+    uint32_t const n = job.cow_tokens;
+    if (n != 0) {
+        uint32_t const scap = pool_tokens(P, job.cow_kind);
+        uint16_t const* src = page_base(P, job.cow_kind, job.cow_slot, scap);
+        if (src == nullptr || n > scap || n > job.dst_token) return false;
+        uint32_t const per_head = n * D;
+        for (uint32_t i = tid; i < (h1 - h0) * per_head; i += kBlock) {
+            uint32_t const h = h0 + i / per_head;
+            uint32_t const rem = i % per_head;
+            uint32_t const t = rem / D;
+            uint32_t const d = rem - t * D;
+            uint64_t const sh = head_block(P, scap, layer, h);
+            uint64_t const dh = head_block(P, dcap, layer, h);
+            dst[dh + k_offset(dcap, D, t, d)] = src[sh + k_offset(scap, D, t, d)];
+            dst[dh + v_offset(dcap, D, t, d)] = src[sh + v_offset(scap, D, t, d)];
+        }
+    }
+    for (uint32_t i = tid; i < (h1 - h0) * D; i += kBlock) {
+        uint32_t const h = h0 + i / D;
+        uint32_t const d = i % D;
+        uint64_t const dh = head_block(P, dcap, layer, h);
+        dst[dh + k_offset(dcap, D, job.dst_token, d)] = job.src_key[h * D + d];
+        dst[dh + v_offset(dcap, D, job.dst_token, d)] = job.src_value[h * D + d];
+    }
+    return true;
+}
+
+// Completes write_token_heads: every thread's stores done, then a barrier.
+__device__ inline void written_token_visible()
+{
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+}
+
 // Two waves per SIMD: each wave holds two 64-token steps of K/V operands in
 // registers, so a CU keeps as many bytes in flight as four single-buffered
 // waves while the compute of one step hides under the loads of the next.
@@ -541,10 +596,12 @@ __device__ void decode_head_split_chunk(const PoolView& P, const kimkv_decode_it
 //
 // partials: when non-null, split-K partials of global chunk c go to
 // partials + c * QH * (D + 2) instead of the lanes' own workspaces.
+// writes: when non-null, lane i's new token (writes[i], token_count 0 for
+// none) is written first by the workgroups of the chunk that holds it.
 template <bool kSplit>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
     PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t chunk_tokens,
-    uint32_t QH, float* partials)
+    uint32_t QH, float* partials, const kimkv_append_job* writes)
 {
     __shared__ DecodeLds lds;
     __shared__ uint32_t s_lane;
@@ -561,6 +618,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t const guess = static_cast<uint32_t>(
         min(static_cast<uint64_t>(chunk_id) * lane_count / gridDim.x, static_cast<uint64_t>(lane_count - 1)));
     kimkv_decode_item item = items[guess];
+    // The lane's write job comes in the same round trip (kimkv_append_job{}
+    // when there is none).
+    kimkv_append_job job = writes != nullptr ? writes[guess] : kimkv_append_job{};
     uint32_t const pg0 = prefix[guess];
     uint32_t const pg1 = prefix[guess + 1];
     if (tid == 0) {
@@ -580,6 +640,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             return;
         }
         item = items[lane];
+        if (writes != nullptr) job = writes[lane];
     }
 
     uint32_t const H = P.heads;
@@ -597,7 +658,15 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t const c1 = min(c0 + chunk_tokens, T);
     uint32_t const G = QH / H;
     bool const single = nchunks == 1;
+    // The chunk holding the lane's new token writes it first; its stores
+    // drain while the group table is built.
+    uint32_t const wh0 = kSplit ? blockIdx.y : blockIdx.y * kHeadsPerBlock;
+    bool const writer = job.token_count != 0 && c1 == T && wh0 < H;
+    if (writer && !write_token_heads(P, job, item.layer, wh0, kSplit ? wh0 + 1 : min(H, wh0 + kHeadsPerBlock))) {
+        report_fault(P, KIMKV_FAULT_APPEND_JOB);
+    }
     bool const fast = build_chunk_table(P, item, QH, c0, c1, lds);
+    if (writer) written_token_visible();
 
     uint32_t const wave = tid >> 6;
     if (!kSplit) {
@@ -652,7 +721,7 @@ __host__ __device__ inline uint32_t guided_edge(uint32_t T, uint32_t n, uint32_t
 // counter slot for the next launch that uses it.
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_guided_kernel(
     PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t QH,
-    float* partials, uint32_t* counter)
+    float* partials, uint32_t* counter, const kimkv_append_job* writes)
 {
     __shared__ DecodeLds lds;
     __shared__ uint32_t s_unit;
@@ -684,6 +753,13 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         if (!decode_item_valid(P, item, QH, n) || prefix[lane + 1] - first != n || c1 - c0 > kMaxChunk) {
             report_fault(P, KIMKV_FAULT_DECODE_ITEM);
             continue;
+        }
+        if (writes != nullptr && c1 == T) {
+            kimkv_append_job const job = writes[lane];
+            if (job.token_count != 0) {
+                if (!write_token_heads(P, job, item.layer, h, h + 1)) report_fault(P, KIMKV_FAULT_APPEND_JOB);
+                written_token_visible();
+            }
         }
         if (c0 >= c1) {
             // An empty slice still leaves its partial: weight zero in the merge.
@@ -864,7 +940,7 @@ __global__ __launch_bounds__(64) void reference_attention_kernel(PoolView P, con
 kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item* device_items,
                            const uint32_t* device_chunk_prefix, uint32_t lane_count, uint32_t total_chunks,
                            uint32_t chunk_flags, uint32_t query_heads, kimkv_stream_t stream, float* partials,
-                           bool timed)
+                           const kimkv_append_job* writes, bool timed)
 {
     bool const head_split = (chunk_flags & KIMKV_DECODE_HEAD_SPLIT) != 0;
     bool const guided = (chunk_flags & KIMKV_DECODE_GUIDED) != 0;
@@ -889,13 +965,13 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
         uint64_t const resident = 2ull * (storage->compute_units > 0 ? storage->compute_units : 256);
         auto const workers = static_cast<uint32_t>(units < resident ? units : resident);
         decode_guided_kernel<<<workers, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
-                                                         lane_count, query_heads, partials, counter);
+                                                         lane_count, query_heads, partials, counter, writes);
     } else if (head_split) {
         decode_kernel<true><<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
-                                                    lane_count, chunk_tokens, query_heads, partials);
+                                                    lane_count, chunk_tokens, query_heads, partials, writes);
     } else {
         decode_kernel<false><<<grid, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
-                                                     lane_count, chunk_tokens, query_heads, partials);
+                                                     lane_count, chunk_tokens, query_heads, partials, writes);
     }
     if (timed) kernel_timing_end(TimedKernel::Decode, s, start);
     kimkv_status const status = launch_status();
@@ -1040,7 +1116,17 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage, const kimkv_
                                       kimkv_stream_t stream)
 {
     return kimkv::launch_decode(storage, device_items, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
-                                query_heads, stream, nullptr, true);
+                                query_heads, stream, nullptr, nullptr, true);
+}
+
+kimkv_status kimkv_paged_decode_write_batch(const kimkv_storage* storage, const kimkv_decode_item* device_items,
+                                            const uint32_t* device_chunk_prefix, uint32_t lane_count,
+                                            uint32_t total_chunks, uint32_t chunk_flags, uint32_t query_heads,
+                                            const kimkv_append_job* device_writes, kimkv_stream_t stream)
+{
+    if (device_writes == nullptr) return KIMKV_INVALID_ARGUMENT;
+    return kimkv::launch_decode(storage, device_items, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
+                                query_heads, stream, nullptr, device_writes, true);
 }
 
 kimkv_status kimkv_paged_decode_batch_noalloc(const kimkv_storage* storage, const kimkv_decode_item* device_items,
@@ -1057,7 +1143,7 @@ kimkv_status kimkv_paged_decode_batch_noalloc(const kimkv_storage* storage, cons
     kimkv_status const resolved = kimkv::decode_scratch(storage, &partials);
     if (resolved != KIMKV_OK) return resolved;
     return kimkv::launch_decode(storage, device_items, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
-                                query_heads, stream, partials, false);
+                                query_heads, stream, partials, nullptr, false);
 }
 
 kimkv_status kimkv_reference_attention(const kimkv_storage* storage, const kimkv_block_desc* device_descriptors,

@@ -271,8 +271,8 @@ public:
         kimkv_append_job job{};
         HipStatus s = prepareWrite(write, job);
         if (!s.ok()) return mapDevice(s);
-        std::lock_guard<std::mutex> lock(owner_->storage.launchMutex());
-        return mapDevice(launchWrites(&job, 1, stream_, {this}));
+        holdWrite(job);
+        return {};
     }
 
     EngineKvStatus attendLayer(PagedDecodeRequest const& request, EngineStream) override
@@ -287,14 +287,16 @@ public:
         HipKvStorage& st = owner_->storage;
         struct {
             kimkv_decode_item item;
+            kimkv_append_job write;
             std::uint32_t prefix[2];
-        } packed{item, {prefix[0], prefix[1]}};
+        } packed{item, takeWrite(), {prefix[0], prefix[1]}};
         auto* staged = static_cast<unsigned char*>(st.ring().stage(&packed, sizeof(packed), stream_));
         if (staged == nullptr) return mapDevice(failSubmission(kimkv_last_native_error()));
-        kimkv_status const k = kimkv_paged_decode_batch(
+        kimkv_status const k = kimkv_paged_decode_write_batch(
             st.handle(), reinterpret_cast<kimkv_decode_item const*>(staged),
             reinterpret_cast<std::uint32_t const*>(staged + offsetof(decltype(packed), prefix)), 1, total, chunk,
-            owner_->config.query_head_count, stream_);
+            owner_->config.query_head_count,
+            reinterpret_cast<kimkv_append_job const*>(staged + offsetof(decltype(packed), write)), stream_);
         st.ring().fence(stream_);
         if (k != KIMKV_OK) return mapDevice(failSubmission(kimkv_last_native_error()));
         dirty_ = true;
@@ -340,6 +342,8 @@ public:
         std::vector<std::size_t> launched;
         std::vector<std::uint32_t> launch_prefix(1, 0);
         std::vector<std::uint32_t> launch_tokens;
+        thread_local std::vector<kimkv_append_job> writes;
+        writes.clear();
         for (std::size_t k : ready) {
             PagedDecodeBatchItem& item = batch.items[index[k]];
             HipTokenTransaction* t = lanes[k];
@@ -349,6 +353,7 @@ public:
                 continue;
             }
             batch.host_items[n] = t->deviceItem(item.request, need != 0);
+            writes.push_back(t->takeWrite());   // this layer's token, written by the launch
             launched.push_back(index[k]);
             launch_tokens.push_back(t->token_count_);
             ++n;
@@ -364,18 +369,22 @@ public:
         // cost a dispatch and a gap between kernels); the caller's
         // device_items scratch is validated by the API but not needed here.
         std::size_t const items_bytes = (n * sizeof(DevicePagedDecodeBatchItem) + 15) & ~std::size_t{15};
+        std::size_t const writes_bytes = n * sizeof(kimkv_append_job);
+        std::size_t const prefix_at = items_bytes + ((writes_bytes + 15) & ~std::size_t{15});
         thread_local std::vector<unsigned char> staging;
-        staging.resize(items_bytes + pre.size() * 4);
+        staging.resize(prefix_at + pre.size() * 4);
         std::memcpy(staging.data(), batch.host_items, n * sizeof(DevicePagedDecodeBatchItem));
-        std::memcpy(staging.data() + items_bytes, pre.data(), pre.size() * 4);
+        std::memcpy(staging.data() + items_bytes, writes.data(), writes_bytes);
+        std::memcpy(staging.data() + prefix_at, pre.data(), pre.size() * 4);
         std::lock_guard<std::mutex> lock(o.storage.launchMutex());
         HipStream const stream = stream_;
         auto* staged = static_cast<unsigned char*>(st.ring().stage(staging.data(), staging.size(), stream));
         kimkv_status k = KIMKV_SUBMISSION_FAILED;
         if (staged != nullptr) {
-            k = kimkv_paged_decode_batch(st.handle(), reinterpret_cast<kimkv_decode_item const*>(staged),
-                                         reinterpret_cast<std::uint32_t const*>(staged + items_bytes),
-                                         static_cast<std::uint32_t>(n), total, chunk, QH, stream);
+            k = kimkv_paged_decode_write_batch(
+                st.handle(), reinterpret_cast<kimkv_decode_item const*>(staged),
+                reinterpret_cast<std::uint32_t const*>(staged + prefix_at), static_cast<std::uint32_t>(n), total,
+                chunk, QH, reinterpret_cast<kimkv_append_job const*>(staged + items_bytes), stream);
         }
         st.ring().fence(stream);
         // Only the last layer's launch needs a completion mark (commit waits
@@ -417,9 +426,9 @@ public:
             lanes.push_back(t);
             index.push_back(i);
         }
-        std::vector<kimkv_append_job> jobs;
-        std::vector<HipTokenTransaction*> launched;
-        std::vector<std::size_t> launched_index;
+        // Each lane's job is held for the layer's attention launch, which
+        // writes the token before reading the page (one launch per layer).
+        bool any = false;
         for (std::size_t k = 0; k < lanes.size(); ++k) {
             LayerKvWriteBatchItem& item = batch.items[index[k]];
             kimkv_append_job job{};
@@ -428,20 +437,11 @@ public:
                 item.status = mapDevice(s);
                 continue;
             }
-            jobs.push_back(job);
-            launched.push_back(lanes[k]);
-            launched_index.push_back(index[k]);
+            lanes[k]->holdWrite(job);
+            item.status = {};
+            any = true;
         }
-        if (jobs.empty()) return;
-        HipStatus s;
-        {
-            std::lock_guard<std::mutex> lock(owner_->storage.launchMutex());
-            s = launchWrites(jobs.data(), jobs.size(), stream_, launched);
-        }
-        for (std::size_t k = 0; k < launched.size(); ++k) {
-            batch.items[launched_index[k]].status = mapDevice(s.ok() ? HipStatus{} : launched[k]->submission_);
-        }
-        if (s.ok()) owner_->batched_write_submissions.fetch_add(1, std::memory_order_relaxed);
+        if (any) owner_->batched_write_submissions.fetch_add(1, std::memory_order_relaxed);
     }
 
     EngineKvStatus commit(EngineStream) override
@@ -519,24 +519,24 @@ private:
         return {};
     }
 
-    HipStatus launchWrites(kimkv_append_job const* jobs, std::size_t n, HipStream stream,
-                           std::vector<HipTokenTransaction*> const& owners)
+    // A layer's token write is not launched on its own: writeLayer checks it
+    // and holds the job, and the layer's attention launch
+    // (kimkv_paged_decode_write_batch) writes the token before reading the
+    // page.  The state machine admits attendLayer(l) only after writeLayer(l)
+    // and commit only after every layer's attention, so a held job is either
+    // written by its attention launch or dropped with a rollback.
+    void holdWrite(kimkv_append_job const& job) noexcept
     {
-        HipKvStorage& st = owner_->storage;
-        void* d = st.ring().stage(jobs, n * sizeof(kimkv_append_job), stream);
-        kimkv_status k = KIMKV_SUBMISSION_FAILED;
-        if (d != nullptr) {
-            k = kimkv_append_batch(st.handle(), static_cast<kimkv_append_job const*>(d),
-                                   static_cast<std::uint32_t>(n), 1, stream);
-        }
-        // No fence here: the layer's attention launch fences this stream's
-        // staged regions (an unfenced region is reclaimed by draining its
-        // stream).
-        for (HipTokenTransaction* t : owners) t->dirty_ = true;
-        if (k == KIMKV_OK) return {};
-        int const native = kimkv_last_native_error();
-        for (HipTokenTransaction* t : owners) static_cast<void>(t->failSubmission(native));
-        return HipStatus{HipError::SubmissionFailed, native};
+        held_write_ = job;
+        holding_ = true;
+    }
+
+    kimkv_append_job takeWrite() noexcept
+    {
+        kimkv_append_job job{};   // token_count 0: nothing to write
+        if (holding_) job = held_write_;
+        holding_ = false;
+        return job;
     }
 
     HipStatus checkAttention(PagedDecodeRequest const& r)
@@ -625,6 +625,8 @@ private:
     std::uint16_t tail_token_{0};
     PageHandle cow_src_{};
     std::uint16_t cow_tokens_{0};
+    kimkv_append_job held_write_{};
+    bool holding_{false};
     kimkv_block_desc const* table_{nullptr};         // the request's device table
     kimkv_block_desc const* descriptors_{nullptr};   // table_ until the transaction finishes
     std::uint32_t desc_count_{0};
