@@ -133,6 +133,9 @@ _SIGNATURES = {
     "kimkv_paged_decode_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                 ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                 ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_paged_decode_write_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                      ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                                      ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]),
     "kimkv_paged_decode_batch_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                         ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                         ctypes.c_uint32, ctypes.c_void_p]),
@@ -391,6 +394,15 @@ class Storage:
         check(lib().kimkv_paged_decode_batch(self.h, ctypes.c_void_p(items_ptr), ctypes.c_void_p(prefix_ptr),
                                              lanes, total_chunks, chunk_tokens, query_heads, _sh(stream)),
               "paged_decode_batch")
+
+    def decode_write_launch(self, items_ptr: int, prefix_ptr: int, lanes: int, total_chunks: int,
+                            chunk_tokens: int, query_heads: int, writes_ptr: int,
+                            stream: Optional[Stream] = None) -> None:
+        """kimkv_paged_decode_write_batch: the decode with each lane's new token (writes[i]) written first."""
+        check(lib().kimkv_paged_decode_write_batch(self.h, ctypes.c_void_p(items_ptr), ctypes.c_void_p(prefix_ptr),
+                                                   lanes, total_chunks, chunk_tokens, query_heads,
+                                                   ctypes.c_void_p(writes_ptr), _sh(stream)),
+              "paged_decode_write_batch")
 
     def prefill_plan(self, new_token_counts, query_heads: int):
         """(tokens per workgroup, workgroup prefix over items, total workgroups)."""

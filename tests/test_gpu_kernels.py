@@ -229,6 +229,104 @@ def _decode_case(dev, shape, token_counts, G, micro_tokens=8, extent_tokens=64, 
     return chunk, total
 
 
+def _write_then_decode(dev, fused, tables, T, news, lanes_meta, QH, chunk, shape, seed, cows):
+    """One storage populated from `tables`, each lane's new token at position T[i] (into its tail page, a
+    fresh page, or a copy-on-write copy of a shared tail), then the decode of T[i] + 1 tokens: by
+    kimkv_paged_decode_write_batch (fused) or kimkv_append_batch + kimkv_paged_decode_batch.  Returns the
+    outputs and every lane's gathered pages."""
+    L, H, D = shape
+    micro_cap = sum(t // 8 + 4 for t in T) + 16
+    ext_cap = sum(t // 64 + 1 for t in T) + 2
+    storage = dev.Storage(L, H, D, micro_cap, ext_cap)
+    pools = oracle.HostPools(L, H, D, micro_cap, ext_cap)
+    keep = []
+    for i, table in enumerate(tables):
+        keep.append(_populate(dev, storage, pools, table, _input(L, H, D, T[i], seed=seed * 100 + i)))
+    jobs = np.zeros(len(T), dtype=dev.APPEND_JOB)
+    ext_tables = []
+    src = dev.upload(news)            # [lane][2][H][D]
+    for i, table in enumerate(tables):
+        layer = lanes_meta[i]
+        t = table.copy()
+        tail = t[-1]
+        j = jobs[i]
+        j["src_key"] = src.ptr + 2 * (i * 2) * H * D
+        j["src_value"] = src.ptr + 2 * (i * 2 + 1) * H * D
+        j["layer_begin"], j["layer_count"], j["token_count"] = layer, 1, 1
+        j["dst_kind"] = 0
+        if tail["kind"] == 0 and tail["valid_tokens"] < 8 and i in cows:
+            # Shared partial tail: continue in a copy (the last free micro slots, distinct per lane).
+            new_slot = micro_cap - 1 - i
+            j["cow_slot"], j["cow_kind"], j["cow_tokens"] = tail["slot"], 0, tail["valid_tokens"]
+            j["dst_slot"], j["dst_token"] = new_slot, tail["valid_tokens"]
+            t[-1]["slot"] = new_slot
+            t[-1]["valid_tokens"] += 1
+        elif tail["kind"] == 0 and tail["valid_tokens"] < 8:
+            j["dst_slot"], j["dst_token"] = tail["slot"], tail["valid_tokens"]
+            t[-1]["valid_tokens"] += 1
+        else:
+            new_slot = micro_cap - 1 - i
+            j["dst_slot"], j["dst_token"] = new_slot, 0
+            t = np.concatenate([t, np.array([(new_slot, 1, T[i], 1, 8, 0)], dtype=t.dtype)])
+        ext_tables.append(t)
+    lanes = []
+    for i, t in enumerate(ext_tables):
+        q = oracle.synth_rows(QH * D, seed * 1000 + i, 0, D)
+        lanes.append((t, T[i] + 1, lanes_meta[i], q, 1.0 / math.sqrt(D)))
+    counts = [T[i] + 1 for i in range(len(T))]
+    prefix = dev.chunk_prefix(counts, chunk, D)
+    total = int(prefix[-1])
+    items = np.zeros(len(lanes), dtype=dev.DECODE_ITEM)
+    outs = []
+    for i, (table, n, layer, q, scale) in enumerate(lanes):
+        dbuf, qbuf = dev.upload(table), dev.upload(q)
+        obuf = dev.DeviceBuffer(QH * D * 2)
+        wsz = dev.workspace_bytes(n, chunk, QH, D)
+        wbuf = dev.DeviceBuffer(max(wsz, 4))
+        items[i] = (dbuf.ptr, len(table), n, layer, qbuf.ptr, wbuf.ptr if wsz else 0, obuf.ptr, scale)
+        keep += [dbuf, qbuf, wbuf]
+        outs.append(obuf)
+    ibuf, pbuf, jbuf = dev.upload(items), dev.upload(prefix), dev.upload(jobs)
+    if fused:
+        storage.decode_write_launch(ibuf.ptr, pbuf.ptr, len(lanes), total, chunk, QH, jbuf.ptr)
+    else:
+        storage.append_batch(jobs)
+        storage.decode_launch(ibuf.ptr, pbuf.ptr, len(lanes), total, chunk, QH)
+    dev.sync()
+    assert storage.faults() == (0, 0)
+    got = [dev.download(o.ptr, (QH * D,), np.uint16) for o in outs]
+    pages = [storage.gather(t, n) for (t, n, _, _, _) in lanes]
+    return got, pages, total
+
+
+@pytest.mark.parametrize("mode", ["four_heads", "head_split", "guided"])
+def test_decode_write_batch_matches_append_then_decode(dev, mode):
+    """kimkv_paged_decode_write_batch equals kimkv_append_batch of the same jobs followed by
+    kimkv_paged_decode_batch, bit for bit in the outputs and the pages: tokens into a partial tail,
+    into a fresh page after a full one, and copy-on-write of a shared partial tail; lanes of one chunk and
+    of several (the chunk holding the new token writes it)."""
+    shape = (3, 4, 64)
+    L, H, D = shape
+    G = 8
+    QH = H * G
+    T = [5, 8, 63, 64, 100, 700, 1303, 2049]
+    alloc = helpers.SlotAllocator(sum(t // 8 + 4 for t in T) + 16 - len(T) - 4, sum(t // 64 + 1 for t in T) + 2,
+                                  seed=21)
+    tables = [helpers.hetero_table(t, alloc) for t in T]
+    rng = np.random.default_rng(22)
+    news = oracle.synth_rows(len(T) * 2 * H * D, 23, 0, D).reshape(len(T), 2, H, D)
+    layers = [int(x) for x in rng.integers(0, L, len(T))]
+    cows = {0, 4, 6}
+    chunk = {"four_heads": 256, "head_split": 256 | dev.DECODE_HEAD_SPLIT, "guided": dev.DECODE_GUIDED | 64}[mode]
+    a, pa, total = _write_then_decode(dev, False, tables, T, news, layers, QH, chunk, shape, 24, cows)
+    b, pb, _ = _write_then_decode(dev, True, tables, T, news, layers, QH, chunk, shape, 24, cows)
+    assert total > len(T)
+    for i in range(len(T)):
+        assert np.array_equal(pa[i], pb[i]), (mode, i)
+        assert np.array_equal(a[i], b[i]), (mode, i)
+    print(f"decode+write mode={mode} lanes={len(T)} chunks={total}", flush=True)
+
+
 def test_decode_config1_tinyllama(dev):
     """One TinyLlama layer, 4 lanes at {17,100,513,1000} + 1 appended token."""
     _decode_case(dev, (1, 4, 64), [18, 101, 514, 1001], G=8, layer=0)
