@@ -312,7 +312,9 @@ __device__ inline void prefill_wave_step(PrefillWave& w, const KvTile& tile, uin
         // A column whose keys so far are all masked keeps m = -inf.
         float const m_cand = fmaxf(w.m_run[cb], mx * w.scale2);
         bool const grow = m_cand > w.m_run[cb] + kLazyRescaleLog2;
-        if (__any(grow)) {
+        if (__builtin_expect(__any(grow), 0)) {
+            // Not speculated: the multiplies run only on tiles that move the reference point.
+            __asm__ volatile("" ::: "memory");
             float const alpha = grow ? __builtin_amdgcn_exp2f(w.m_run[cb] - m_cand) : 1.0f;
             if (grow) w.m_run[cb] = m_cand;
 #pragma unroll
