@@ -304,17 +304,21 @@ __device__ inline void prefill_wave_step(PrefillWave& w, const KvTile& tile, uin
                 }
             }
         }
-        mx = fmaxf(mx, xor16(mx));
-        mx = fmaxf(mx, xor32(mx));
         // Lazy running max: the reference point moves (and the accumulators
         // are rescaled) only when a score exceeds it by more than 2^8, so
         // p <= 256 stays well inside fp16 and most tiles skip the rescale.
-        // A column whose keys so far are all masked keeps m = -inf.
-        float const m_cand = fmaxf(w.m_run[cb], mx * w.scale2);
-        bool const grow = m_cand > w.m_run[cb] + kLazyRescaleLog2;
-        if (__builtin_expect(__any(grow), 0)) {
-            // Not speculated: the multiplies run only on tiles that move the reference point.
+        // The test runs on this lane's 16 keys; only a tile where some lane
+        // passes it takes the column max across the four row groups (a
+        // column's m stays the same on all of its lanes).  A column whose
+        // keys so far are all masked keeps m = -inf.
+        bool const over = mx * w.scale2 > w.m_run[cb] + kLazyRescaleLog2;
+        if (__builtin_expect(__any(over), 0)) {
+            // Not speculated: the reduction and the multiplies run only on tiles that move the reference point.
             __asm__ volatile("" ::: "memory");
+            mx = fmaxf(mx, xor16(mx));
+            mx = fmaxf(mx, xor32(mx));
+            float const m_cand = fmaxf(w.m_run[cb], mx * w.scale2);
+            bool const grow = m_cand > w.m_run[cb] + kLazyRescaleLog2;
             float const alpha = grow ? __builtin_amdgcn_exp2f(w.m_run[cb] - m_cand) : 1.0f;
             if (grow) w.m_run[cb] = m_cand;
 #pragma unroll
