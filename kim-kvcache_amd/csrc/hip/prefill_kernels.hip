@@ -128,26 +128,40 @@ struct TileLoad {
     half8_t v[2];
 };
 
+// A wave-uniform 64-bit value in SGPRs.  readfirstlane returns int: each
+// half goes through uint32_t so that the low half is not sign-extended.
+__device__ __attribute__((always_inline)) inline uint64_t uniform_u64(uint64_t x)
+{
+    uint32_t const lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x)));
+    uint32_t const hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x >> 32)));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 // kFull: all 64 keys of the tile are below nvalid and every group of the
-// segment names a page, so no lane needs a check.
+// segment names a page, so no lane needs a check.  A K unit's group (c / 64)
+// is the same for the whole wave: its base goes to SGPRs and each lane adds a
+// 32-bit offset (panel (tid / 32) % 2, key (tid / 4) % 8, octet tid % 4, the
+// same for both units).
 template <bool kFull>
 __device__ inline void tile_fetch(TileLoad& r, const HeadGroup* groups, uint32_t tg, uint32_t nvalid, uint32_t tid)
 {
     half8_t const zero8 = {};
+    uint32_t const tk = (tid >> 2) & 7u;
+    uint32_t const k_off = tk * 64u + (tid & 3u) * 16u;
+    uint32_t const k_panel = (tid >> 5) & 1u;
 #pragma unroll
     for (uint32_t j = 0; j < 2; ++j) {
-        uint32_t const c = tid + kBlock * j;
-        uint32_t const g = c >> 6;
-        uint32_t const tk = (c >> 2) & 7u;
-        if (kFull) {
+        uint32_t const g = (tid >> 6) + kWaves * j;
+        if (kFull || 8 * g + tk < nvalid) {
             HeadGroup const e = groups[tg + g];
-            r.k[j] = load_half8_stream(e.k + ((c >> 5) & 1u) * e.kpanel + tk * 32 + (c & 3u) * 8);
+            uint64_t const kb = uniform_u64(reinterpret_cast<uintptr_t>(e.k));
+            uint32_t const off = k_off + k_panel * static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(e.kpanel)) * 2u;
+            r.k[j] = zero8;
+            if (kFull || kb != 0) {
+                r.k[j] = __builtin_nontemporal_load(reinterpret_cast<const global_half8_t*>(kb + off));
+            }
         } else {
             r.k[j] = zero8;
-            if (8 * g + tk < nvalid) {
-                HeadGroup const e = groups[tg + g];
-                if (e.k != nullptr) r.k[j] = load_half8_stream(e.k + ((c >> 5) & 1u) * e.kpanel + tk * 32 + (c & 3u) * 8);
-            }
         }
         uint32_t const ko = 4 * j + (tid & 3u);
         if (kFull) {
