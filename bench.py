@@ -220,7 +220,7 @@ class EngineWorkload:
     page id comes from the manager's (permuted) pools."""
 
     def __init__(self, kimkv, dev, lanes, context, layers, kv_heads, head_dim, query_heads, total_steps, seed,
-                 groups=2):
+                 groups=2, group_streams=True):
         import importlib
         host = importlib.import_module(kimkv.__name__ + ".host")
         self.dev, self.host = dev, host
@@ -288,12 +288,20 @@ class EngineWorkload:
         obase = self.out.ptr + np.uint64(2 * QD) * (lay * np.uint64(lanes) + lane[None, :])
         # Lane groups: each group is one batch of token transactions; with two
         # groups the host reserves/launches one while the GPU runs the other.
+        # With group_streams each group has its own stream, so one group's
+        # decode launch fills the compute units that the other's last
+        # workgroups leave idle at the end of a launch.
         self.groups = []
+        self.streams = [stream]
         bounds = np.linspace(0, lanes, groups + 1).astype(int)
         for g in range(groups):
             sl = slice(bounds[g], bounds[g + 1])
+            gs = stream
+            if group_streams and g > 0:
+                gs = dev.Stream()
+                self.streams.append(gs)
             b = host.LaneBatch(self.engine, lane[sl] + np.uint64(1), self.ws.ptr + lane[sl] * np.uint64(self.ws_lane),
-                               self.ws_lane, 1.0 / math.sqrt(head_dim), stream)
+                               self.ws_lane, 1.0 / math.sqrt(head_dim), gs)
             b.outputs[:] = obase[:, sl]
             self.groups.append((b, kbase[:, sl], kbase[:, sl] + np.uint64(2 * HD * S), qbase[:, sl]))
         self.stream = stream
@@ -1259,6 +1267,8 @@ def main() -> int:
     ap.add_argument("--path", choices=["engine", "kernel"], default="engine",
                     help="engine: EngineKvBackend token transactions (reserve / writeLayerBatch / attendLayerBatch / "
                          "commit); kernel: the C-ABI kernels driven directly with bench-built page tables")
+    ap.add_argument("--group-streams", choices=["own", "shared"], default="own",
+                    help="engine path: each lane group on its own stream (own) or all on one (shared)")
     ap.add_argument("--groups", type=int, default=2,
                     help="engine path: lane groups pipelined against each other (1 = one batch per step)")
     ap.add_argument("--slots", choices=["permuted", "sequential"], default="permuted",
@@ -1311,7 +1321,7 @@ def main() -> int:
     total_steps = args.warmup + args.steps
     if args.path == "engine":
         w = EngineWorkload(kimkv, dev, args.lanes, args.context, args.layers, H, D, QH, total_steps, args.seed,
-                           args.groups)
+                           args.groups, group_streams=args.group_streams == "own")
         stream = w.stream
     else:
         w = Workload(dev, args.lanes, args.context, args.layers, H, D, QH, total_steps, args.seed,
@@ -1335,7 +1345,11 @@ def main() -> int:
     # Events bracket every 5th decode launch of the timed steps (5 is prime
     # to the 44 launches of a step, so the sample walks every layer and lane
     # group); events around every launch cost the stream ~1 % of a step.
-    dev.decode_timing(True, every=5)
+    # With the lane groups on their own streams two launches overlap, and
+    # every launch is timed so that the union of their intervals (the time
+    # the decode kernel occupies the GPU) is known.
+    multi = args.path == "engine" and len(w.streams) > 1
+    dev.decode_timing(True, every=1 if multi else 5)
     dev.sync()
     t_wall = time.perf_counter()
     start.record(stream)
@@ -1343,10 +1357,12 @@ def main() -> int:
         w.step(s, stream)
     if args.path == "engine":
         w.drain()
+    dev.sync()
     stop.record(stream)
     stop.synchronize()
     wall_ms = (time.perf_counter() - t_wall) * 1000.0
     decode_ms_total, decode_launches = dev.decode_timing(False)
+    decode_busy_ms = dev.decode_timing_busy()
     gpu_ms = start.elapsed_ms(stop)
     ms_per_step = max(gpu_ms, wall_ms) / args.steps
 
@@ -1371,7 +1387,11 @@ def main() -> int:
     fused_bytes = append_bytes if args.path == "engine" else 0
     per_launch_decode_bytes = (decode_bytes + fused_bytes) / launches
     decode_avg_ms = decode_ms_total / max(decode_launches, 1)
-    achieved = per_launch_decode_bytes / (decode_avg_ms * 1e-3) / 1e9
+    # Per launch: its share of the time the decode kernel occupied the GPU.
+    # One stream: the launches do not overlap and this is their mean
+    # duration; several streams: the busy union over the launches.
+    decode_eff_ms = decode_busy_ms / max(decode_launches, 1) if multi else decode_avg_ms
+    achieved = per_launch_decode_bytes / (decode_eff_ms * 1e-3) / 1e9
 
     # Correctness sample + CPU baseline: lanes 0..k-1, layer 0, last step.
     last = total_steps - 1
@@ -1424,11 +1444,15 @@ def main() -> int:
                    "decode_mode": dev.decode_mode(w.plan[0]),
                    "decode_chunk_tokens": w.plan[0] & 0x3FFFFFFF if not w.plan[0] & dev.DECODE_GUIDED else None,
                    "decode_chunks_per_launch": w.plan[1],
-                   "lane_groups": args.groups if args.path == "engine" else 1},
+                   "lane_groups": args.groups if args.path == "engine" else 1,
+                   "group_streams": len(w.streams) if args.path == "engine" else 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": profiled_traffic(lanes_per_launch, args.context, args.layers),
-                     "kernel": "decode_kernel", "avg_launch_ms": round(decode_avg_ms, 4),
+                     "kernel": "decode_kernel", "launch_ms": round(decode_eff_ms, 4),
+                     "avg_launch_ms": round(decode_avg_ms, 4),
+                     "launches_in_flight": round(decode_ms_total / decode_busy_ms, 3) if multi and decode_busy_ms
+                     else 1.0,
                      "timed_launches": decode_launches, "launches": launches,
                      "lanes_per_launch": lanes_per_launch,
                      "bytes_per_launch": int(per_launch_decode_bytes)},

@@ -421,6 +421,13 @@ kimkv_status kimkv_reference_attention(const kimkv_storage* storage,
 kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launches);
 /* The same for the chunked-prefill attention kernel (same `enable`). */
 kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launches);
+/* Time (ms) during which at least one timed decode launch was running, over
+ * the window the last kimkv_decode_timing call closed: the union of the
+ * launches' intervals.  Launches on several streams overlap, so this is less
+ * than their summed duration; with every launch timed it is the time the
+ * decode kernel occupied the GPU.  No counterpart in the reference (benchmark
+ * instrumentation). */
+kimkv_status kimkv_decode_timing_busy(double* busy_ms);
 
 /* ---- dense TinyLlama layers (the model runner's device side) --------------
  * Counterparts of src/cuda/model/kernels.cuh:11-119 and the cuBLAS calls of

@@ -4,6 +4,7 @@
 // allocation per pool, zero-filled, page pointer = base + slot * page_elements.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <limits>
 #include <mutex>
@@ -27,6 +28,10 @@ struct DecodeTiming {
     std::vector<hipEvent_t> spare;   // read events, reused
     double total_ms{0.0};
     uint64_t launches{0};
+    // The union of the drained launches' intervals (launches on several
+    // streams overlap), measured from the window's first start event.
+    std::vector<std::pair<double, double>> intervals;
+    double busy_ms{0.0};   // of the last closed window
 };
 
 // A timing event: reused when one is spare.  No system-scope fence when it
@@ -60,18 +65,53 @@ DecodeTiming& timing(TimedKernel kind = TimedKernel::Decode)
 
 void drain_locked(DecodeTiming& t)
 {
+    if (t.pending.empty()) return;
+    hipEvent_t const ref = t.pending.front().first;
     for (auto& pair : t.pending) {
         if (hipEventSynchronize(pair.second) == hipSuccess) {
             float ms = 0.0f;
+            float from = 0.0f;
+            float to = 0.0f;
             if (hipEventElapsedTime(&ms, pair.first, pair.second) == hipSuccess) {
                 t.total_ms += ms;
                 t.launches += 1;
+                if (hipEventElapsedTime(&from, ref, pair.first) == hipSuccess
+                    && hipEventElapsedTime(&to, ref, pair.second) == hipSuccess) {
+                    try {
+                        t.intervals.emplace_back(from, to);
+                    } catch (...) {
+                    }
+                }
             }
         }
+    }
+    for (auto& pair : t.pending) {
         spare_event_locked(t, pair.first);
         spare_event_locked(t, pair.second);
     }
     t.pending.clear();
+}
+
+// Length of the union of the window's intervals.
+double busy_locked(DecodeTiming& t)
+{
+    std::sort(t.intervals.begin(), t.intervals.end());
+    double busy = 0.0;
+    double lo = 0.0;
+    double hi = 0.0;
+    bool open = false;
+    for (auto const& iv : t.intervals) {
+        if (!open || iv.first > hi) {
+            if (open) busy += hi - lo;
+            lo = iv.first;
+            hi = iv.second;
+            open = true;
+        } else if (iv.second > hi) {
+            hi = iv.second;
+        }
+    }
+    if (open) busy += hi - lo;
+    return busy;
 }
 }  // namespace
 
@@ -447,6 +487,8 @@ kimkv_status kernel_timing(kimkv::TimedKernel kind, int enable, double* total_ms
     kimkv::drain_locked(t);
     if (total_ms != nullptr) *total_ms = t.total_ms;
     if (launches != nullptr) *launches = t.launches;
+    t.busy_ms = kimkv::busy_locked(t);
+    t.intervals.clear();
     t.total_ms = 0.0;
     t.launches = 0;
     t.enabled = enable > 0;
@@ -464,6 +506,15 @@ kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launche
 kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launches)
 {
     return kernel_timing(kimkv::TimedKernel::Prefill, enable, total_ms, launches);
+}
+
+kimkv_status kimkv_decode_timing_busy(double* busy_ms)
+{
+    if (busy_ms == nullptr) return KIMKV_INVALID_ARGUMENT;
+    kimkv::DecodeTiming& t = kimkv::timing(kimkv::TimedKernel::Decode);
+    std::lock_guard<std::mutex> lock(t.mutex);
+    *busy_ms = t.busy_ms;
+    return KIMKV_OK;
 }
 
 }  // extern "C"

@@ -154,6 +154,7 @@ _SIGNATURES = {
                                            ctypes.POINTER(ctypes.c_uint64)]),
     "kimkv_prefill_timing": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_uint64)]),
+    "kimkv_decode_timing_busy": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double)]),
     "kimkv_linear": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
                                     ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_void_p]),
     "kimkv_linear_tune": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
@@ -523,6 +524,13 @@ def decode_timing(enable, every: int = 1):
     check(lib().kimkv_decode_timing(max(1, int(every)) if enable else 0, ctypes.byref(total),
                                     ctypes.byref(launches)), "decode_timing")
     return float(total.value), int(launches.value)
+
+
+def decode_timing_busy() -> float:
+    """Union (ms) of the decode launches timed in the window the last decode_timing call closed."""
+    busy = ctypes.c_double()
+    check(lib().kimkv_decode_timing_busy(ctypes.byref(busy)), "decode_timing_busy")
+    return float(busy.value)
 
 
 def prefill_timing(enable, every: int = 1):

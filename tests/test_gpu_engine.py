@@ -707,12 +707,14 @@ def test_engine_prefill_chunk_errors(host, dev):
     stream.destroy()
 
 
-def _engine_lane_batch_case(host, dev, steps=1, seed=77):
+def _engine_lane_batch_case(host, dev, steps=1, seed=77, groups=1):
     """256 ragged lanes through reserveBatch + writeLayerBatch + attendLayerBatch + commitBatch for
     `steps` tokens: enough (lane, kv head) pairs for the decode planner to take one kv head per workgroup
     with each lane in one chunk (no split-K merge).  Contexts are built by bulk prefill with promotion of
     every full 64-token run; every lane's output at every step is checked against the oracle's fp32 GQA
-    decode of its history."""
+    decode of its history.  groups > 1 splits the lanes into that many batches, each on its own stream,
+    launched one after the other and committed after the next batch's layers are queued (as the
+    benchmark pipelines them), so their launches overlap on the GPU."""
     L, H, D, QH, lanes = 2, 4, 64, 32, 256
     HD = H * D
     rng = np.random.default_rng(seed)
@@ -732,14 +734,22 @@ def _engine_lane_batch_case(host, dev, steps=1, seed=77):
     qseed = seed ^ 0x5155
     flags, _, _ = dev.decode_plan(engine.storage_handle(), [t + 1 for t in T], QH)
     assert flags & dev.DECODE_HEAD_SPLIT and (flags & ~dev.DECODE_HEAD_SPLIT) >= max(T) + 1
-    lane = np.arange(lanes, dtype=np.uint64)
-    ws = dev.DeviceBuffer(lanes * 256)
-    b = host.LaneBatch(engine, lane + np.uint64(1), ws.ptr + lane * np.uint64(256), 256, 1.0 / math.sqrt(D), stream)
-    for l in range(L):
-        b.keys[l, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * L) + np.uint64(2 * l))
-        b.values[l, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * L) + np.uint64(2 * l + 1))
-        b.queries[l, :] = query.ptr + np.uint64(2 * QH * D) * (lane * np.uint64(L) + np.uint64(l))
-        b.outputs[l, :] = out.ptr + np.uint64(2 * QH * D) * (lane * np.uint64(L) + np.uint64(l))
+    # A smaller batch may be planned with split-K chunks: room for their partials.
+    ws_lane = max(dev.workspace_bytes(max(T) + steps, 64, QH, D), 256)
+    ws = dev.DeviceBuffer(lanes * ws_lane)
+    bounds = np.linspace(0, lanes, groups + 1).astype(int)
+    streams = [stream] + [dev.Stream() for _ in range(groups - 1)]
+    batches = []
+    for g in range(groups):
+        lane = np.arange(bounds[g], bounds[g + 1], dtype=np.uint64)
+        b = host.LaneBatch(engine, lane + np.uint64(1), ws.ptr + lane * np.uint64(ws_lane), ws_lane,
+                           1.0 / math.sqrt(D), streams[g])
+        for l in range(L):
+            b.keys[l, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * L) + np.uint64(2 * l))
+            b.values[l, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * L) + np.uint64(2 * l + 1))
+            b.queries[l, :] = query.ptr + np.uint64(2 * QH * D) * (lane * np.uint64(L) + np.uint64(l))
+            b.outputs[l, :] = out.ptr + np.uint64(2 * QH * D) * (lane * np.uint64(L) + np.uint64(l))
+        batches.append((b, [T[int(i)] for i in lane]))
     worst = 0.0
     for step in range(steps):
         for i in range(lanes):
@@ -749,13 +759,22 @@ def _engine_lane_batch_case(host, dev, steps=1, seed=77):
                 dev.fill_rows(query.ptr + (i * L + l) * QH * D * 2, QH * D, qseed, dev.synth_kv_row(i, l, 0, t),
                               QH * D, stream)
         stream.synchronize()
-        b.reserve(np.array([t + step for t in T], dtype=np.uint32))
-        assert not b.failed()
-        for l in range(L):
-            b.write(l)
-            b.attend(l)
-        b.commit()
-        assert not b.failed(), sorted(set(b.status.tolist()))
+        pending = None
+        for b, Tg in batches:
+            b.reserve(np.array([t + step for t in Tg], dtype=np.uint32))
+            assert not b.failed()
+            for l in range(L):
+                b.write(l)
+                assert not b.failed(), (l, sorted(set(b.status.tolist())))
+                b.attend(l)
+                assert not b.failed(), (l, sorted(set(b.status.tolist())))
+            if pending is not None:
+                pending.commit()
+                assert not pending.failed(), sorted(set(pending.status.tolist()))
+            pending = b
+        pending.commit()
+        assert not pending.failed(), sorted(set(pending.status.tolist()))
+        dev.sync()
         got = dev.download(out.ptr, (lanes, L, QH * D), np.uint16)
         for i in range(lanes):
             n = T[i] + step + 1
@@ -776,12 +795,20 @@ def _engine_lane_batch_case(host, dev, steps=1, seed=77):
                 assert np.all(err <= 2e-3 + 1e-3 * np.abs(want)), (step, i, l, float(err.max()))
                 worst = max(worst, float(err.max()))
     assert engine.check_invariants()
-    print(f"engine lane batch: lanes={lanes} steps={steps} T=[{min(T)},{max(T)}] "
+    for extra in streams[1:]:
+        extra.destroy()
+    print(f"engine lane batch: lanes={lanes} steps={steps} groups={groups} T=[{min(T)},{max(T)}] "
           f"chunk={flags & ~dev.DECODE_HEAD_SPLIT} max_err={worst:.2e}", flush=True)
 
 
 def test_engine_head_split_batch_matches_oracle(host, dev):
     _engine_lane_batch_case(host, dev)
+
+
+def test_engine_lane_groups_on_own_streams(host, dev):
+    """Two lane batches on two streams whose decode launches overlap (the
+    benchmark's default), three tokens each, against the oracle."""
+    _engine_lane_batch_case(host, dev, steps=3, seed=78, groups=2)
 
 
 def test_engine_small_staging_ring(host, dev, monkeypatch):
