@@ -183,6 +183,10 @@ kimkv_status kimkv_device_synchronize(void);
 kimkv_status kimkv_event_create(void** event, int kind);
 kimkv_status kimkv_event_destroy(void* event);
 kimkv_status kimkv_event_record(void* event, kimkv_stream_t stream);
+/* Work enqueued on `stream` after this call waits for the event's most
+ * recent record (cross-stream ordering without a host wait; the model
+ * runner's decode stream joins and leaves its main stream this way). */
+kimkv_status kimkv_stream_wait_event(kimkv_stream_t stream, void* event);
 kimkv_status kimkv_event_query(void* event);       /* KIMKV_OK or KIMKV_NOT_READY */
 kimkv_status kimkv_event_synchronize(void* event);
 kimkv_status kimkv_event_elapsed_ms(float* ms, void* start, void* stop);

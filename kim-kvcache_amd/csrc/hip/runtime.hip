@@ -311,6 +311,13 @@ kimkv_status kimkv_event_record(void* event, kimkv_stream_t stream)
                         KIMKV_SUBMISSION_FAILED);
 }
 
+kimkv_status kimkv_stream_wait_event(kimkv_stream_t stream, void* event)
+{
+    if (event == nullptr) return KIMKV_INVALID_ARGUMENT;
+    return record_error(hipStreamWaitEvent(kimkv::native(stream), static_cast<hipEvent_t>(event), 0),
+                        KIMKV_SUBMISSION_FAILED);
+}
+
 kimkv_status kimkv_event_query(void* event)
 {
     if (event == nullptr) return KIMKV_INVALID_ARGUMENT;

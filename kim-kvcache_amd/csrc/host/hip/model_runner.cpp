@@ -77,8 +77,25 @@ struct HipTinyLlamaRunner::Impl {
     std::uint8_t* decode_ws{nullptr};
     DevicePagedDecodeBatchItem* d_items{nullptr};
 
+    // The decode lanes' token transactions run on their own stream, so a
+    // layer's decode attention runs beside its chunked-prefill attention
+    // (they read different requests' pages) and fills the compute units the
+    // prefill launch's last workgroups leave idle.  Per layer the decode
+    // stream waits for the main stream's q/k/v (qkv_ready) and the main
+    // stream waits for the decode outputs (decode_done) before the output
+    // projection.
+    HipStream decode_stream{nullptr};
+    void* qkv_ready{nullptr};
+    void* decode_done{nullptr};
+
     ~Impl()
     {
+        if (decode_stream) {
+            static_cast<void>(kimkv_stream_synchronize(decode_stream));
+            kimkv_stream_destroy(decode_stream);
+        }
+        if (qkv_ready) kimkv_event_destroy(qkv_ready);
+        if (decode_done) kimkv_event_destroy(decode_done);
         if (weights) kimkv_device_free(weights);
         if (work) kimkv_device_free(work);
         if (pinned) kimkv_host_free_pinned(pinned);
@@ -86,6 +103,12 @@ struct HipTinyLlamaRunner::Impl {
 
     bool allocate(std::string* error)
     {
+        if (kimkv_stream_create(&decode_stream) != KIMKV_OK
+            || kimkv_event_create(&qkv_ready, KIMKV_EVENT_ORDER_ONLY) != KIMKV_OK
+            || kimkv_event_create(&decode_done, KIMKV_EVENT_ORDER_ONLY) != KIMKV_OK) {
+            if (error) *error = "decode stream creation failed";
+            return false;
+        }
         TinyLlamaConfig const& m = cfg.model;
         std::uint64_t const H = m.hidden_size, I = m.intermediate_size, V = m.vocabulary_size;
         std::uint64_t per_layer = 0;
@@ -367,7 +390,7 @@ GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSp
     std::vector<ReserveTokenRequest> reqs(dec.size());
     std::vector<TokenReserveResult> reserved(dec.size());
     for (std::size_t j = 0; j < dec.size(); ++j) {
-        reqs[j] = ReserveTokenRequest{spans[dec[j]].request_id, spans[dec[j]].first_position, stream};
+        reqs[j] = ReserveTokenRequest{spans[dec[j]].request_id, spans[dec[j]].first_position, decode_stream};
     }
     if (!dec.empty() && !reserveTokenBatch(*kv, reqs.data(), reqs.size(), reserved.data())) {
         for (std::size_t j = 0; j < dec.size(); ++j) reserved[j].status = {EngineKvError::InvalidArgument};
@@ -403,6 +426,9 @@ GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSp
     for (std::uint32_t l = 0; l < m.layer_count && ok; ++l) {
         Layer const& L = layers[l];
         if (l > 0) ok = pre_attention(L);
+        // The decode stream starts the layer once its q/k/v rows exist.
+        ok = ok && kimkv_event_record(qkv_ready, stream) == KIMKV_OK
+            && kimkv_stream_wait_event(decode_stream, qkv_ready) == KIMKV_OK;
         if (!ok) break;
         // Writes.
         wr.clear();
@@ -481,8 +507,11 @@ GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSp
                 if (!pst[c].ok()) fail(live_pre[c], "chunk attention failed: " + std::string(toString(pst[c].error)));
             }
         }
+        // The decode lanes' attention rows are in attn before the output projection reads them.
+        ok = kimkv_event_record(decode_done, decode_stream) == KIMKV_OK
+            && kimkv_stream_wait_event(stream, decode_done) == KIMKV_OK;
         // Output projection + residual, MLP + residual.
-        ok = kimkv_linear(attn, G, m.hidden_size, L.wo, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK
+        ok = ok && kimkv_linear(attn, G, m.hidden_size, L.wo, m.hidden_size, x, 0, 1.0f, stream) == KIMKV_OK
             && kimkv_model_rmsnorm(x, nullptr, P, L.ln2, m.hidden_size, m.rms_norm_epsilon, h, stream) == KIMKV_OK
             && kimkv_linear(h, G, m.hidden_size, L.wgu, 2 * m.intermediate_size, gu, 0, 0.0f, stream) == KIMKV_OK
             && kimkv_model_swiglu(gu, P, m.intermediate_size, act, stream) == KIMKV_OK
@@ -514,6 +543,7 @@ GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSp
         if (!f.ok()) fail(pre[j], "prefill chunk finish failed: " + std::string(toString(f.error)));
     }
     if (kimkv_stream_synchronize(stream) != KIMKV_OK) ok = false;
+    if (kimkv_stream_synchronize(decode_stream) != KIMKV_OK) ok = false;
     if (!ok) {
         result.detail = "device submission failed in the model forward";
         return result;

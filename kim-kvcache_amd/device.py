@@ -109,6 +109,7 @@ _SIGNATURES = {
     "kimkv_event_create": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int]),
     "kimkv_event_destroy": (ctypes.c_int, [ctypes.c_void_p]),
     "kimkv_event_record": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "kimkv_stream_wait_event": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "kimkv_event_query": (ctypes.c_int, [ctypes.c_void_p]),
     "kimkv_event_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
     "kimkv_event_elapsed_ms": (ctypes.c_int, [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]),
