@@ -467,6 +467,10 @@ def run_gather(dev, args) -> int:
         "metric": "long-sequence gather (paged -> contiguous) GB/s", "value": round(moved / (ms * 1e-3) / 1e9, 1),
         "unit": "GB/s", "us_per_launch": round(ms * 1000, 2), "bytes_per_launch": moved,
         "read_bytes": n * 2, "write_bytes": n * 2, "pct_of_peak_hbm": round(100 * moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+        "roofline": {"bound": "hbm", "achieved": round(moved / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic("gather_kernel_long_sequence.md", tokens=T, layers=L),
+                     "kernel": "gather_kernel", "launch_ms": round(ms, 4), "bytes_per_launch": moved},
         "config": {"workload": f"gather of one {T}-token sequence x {L} layers (4 kv heads x 64, fp16), "
                                f"{n_ext} extents in permuted slots + {k} micro pages"},
         "steps": args.steps, "check": {"sampled_rows": 256, "mismatches": bad}, "cpu_baseline": cpu}), flush=True)
@@ -540,7 +544,8 @@ def run_append(kimkv, dev, args) -> int:
     lanes = args.append_lanes
     rng = np.random.default_rng(args.seed)
     lengths = rng.integers(1, 4097, lanes)
-    total_steps = args.warmup + args.steps
+    timing_steps = 8                       # after the timed loop: append kernel duration by events
+    total_steps = args.warmup + args.steps + timing_steps
     n_ext = int(sum(lengths // 64)) + 16
     n_micro = 512 + lanes * (8 + total_steps // 8 + 2)
     cache = host.Cache(L, H, D, n_micro, n_ext)
@@ -585,13 +590,18 @@ def run_append(kimkv, dev, args) -> int:
     start, stop = dev.Event(), dev.Event()
     walls = []
     start.record(stream)
-    for s_ in range(args.warmup, total_steps):
+    for s_ in range(args.warmup, args.warmup + args.steps):
         t = time.perf_counter()
         step(s_)
         walls.append(time.perf_counter() - t)
     stop.record(stream)
     stop.synchronize()
     gpu_ms = start.elapsed_ms(stop)
+    dev.append_timing(True)
+    for s_ in range(args.warmup + args.steps, total_steps):
+        step(s_)
+    stream.synchronize()
+    ap_ms, ap_n = dev.append_timing(False)
     wall_us = 1e6 * sum(walls) / len(walls)
     step_bytes = lanes * L * 2 * (2 * HD * 2)          # read new K/V + write into the page
     # Bit-exact check: gather sampled lanes and compare with the generator.
@@ -633,6 +643,13 @@ def run_append(kimkv, dev, args) -> int:
         "value": round(wall_us, 2), "unit": "us/step", "higher_is_better": False,
         "gb_per_s": round(step_bytes / (wall_us * 1e-6) / 1e9, 2), "bytes_per_step": step_bytes,
         "gpu_span_us_per_step": round(1000 * gpu_ms / args.steps, 2),
+        "append_kernel_avg_us": round(1000 * ap_ms / max(ap_n, 1), 2),
+        "roofline": {"bound": "hbm", "achieved": round(step_bytes / (ap_ms / max(ap_n, 1) * 1e-3) / 1e9, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(step_bytes / (ap_ms / max(ap_n, 1) * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": None, "kernel": "append_kernel", "launch_ms": round(ap_ms / max(ap_n, 1), 4),
+                     "timed_launches": ap_n, "bytes_per_launch": step_bytes,
+                     "note": f"latency-bound: one launch of {lanes * L} (lane, layer) jobs of 1 KiB K + 1 KiB V each"},
         "config": {"workload": f"{lanes} lanes, contexts uniform in [1, 4096] tokens, {L} layers x 4 kv heads x 64 "
                                f"fp16, micro/extent pages in permuted pool order",
                    "tokens": int(lengths.sum())},
@@ -657,7 +674,8 @@ def run_parity(kimkv, dev, args) -> int:
     HD, QD = H * D, QH * D
     contexts = [17, 100, 513, 1000]
     lanes = len(contexts)
-    total_steps = args.warmup + args.steps
+    timing_steps = 20                      # after the timed loop: decode kernel duration by events
+    total_steps = args.warmup + args.steps + timing_steps
     ws_lane = max(dev.workspace_bytes(max(contexts) + total_steps, 64, QH, D), 256)
     engine = host.Engine(L, H, D, QH, ws_lane, 512, 512)
     for kind, sd in ((1, args.seed), (0, args.seed + 1)):
@@ -697,9 +715,19 @@ def run_parity(kimkv, dev, args) -> int:
     for s_ in range(args.warmup):
         step(s_)
     t0 = time.perf_counter()
-    for s_ in range(args.warmup, total_steps):
+    for s_ in range(args.warmup, args.warmup + args.steps):
         step(s_)
     us = (time.perf_counter() - t0) * 1e6 / args.steps
+    dev.decode_timing(True)
+    for s_ in range(args.warmup + args.steps, total_steps):
+        step(s_)
+    stream.synchronize()
+    dec_ms, dec_n = dev.decode_timing(False)
+    dec_ms /= max(dec_n, 1)
+    # Algorithmic bytes of one decode launch: every lane's K/V (mean over the
+    # timed launches) plus the queries, the outputs and the tokens written.
+    mean_ctx = sum(contexts) + lanes * (args.warmup + args.steps + (timing_steps + 1) / 2.0)
+    dec_bytes = mean_ctx * 2 * HD * 2 + lanes * (2 * QD * 2 + 2 * HD * 2)
     got = dev.download(out.ptr, (lanes, QD), np.uint16)
     # Oracle: the last step of every lane (history regenerated), timed on one core.
     last = total_steps - 1
@@ -727,6 +755,12 @@ def run_parity(kimkv, dev, args) -> int:
                                "512-slot permuted micro/extent pools, through the engine"},
         "steps": args.steps, "warmup": args.warmup,
         "check": {"lanes": lanes, "max_abs_err": worst, "within_tolerance": ok, "tolerance": "2e-3 + 1e-3*|ref|"},
+        "decode_kernel_avg_us": round(dec_ms * 1000, 2),
+        "roofline": {"bound": "hbm", "achieved": round(dec_bytes / (dec_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(dec_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": None, "kernel": "decode_kernel", "launch_ms": round(dec_ms, 4),
+                     "timed_launches": dec_n, "bytes_per_launch": int(dec_bytes),
+                     "note": "latency-bound: 4 lanes, 1.6 k tokens of K/V in one launch"},
         "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
                          "sample": f"the decode of the whole step: oracle kvo_paged_decode of the 4 lanes, mean of "
                                    f"{reps} on {platform.processor() or platform.machine()}"}}), flush=True)
@@ -882,6 +916,11 @@ def run_shared(kimkv, dev, args) -> int:
         step(s_)
     stream.synchronize()
     dec_ms, dec_n = dev.decode_timing(False)
+    dec_ms /= max(dec_n, 1)
+    # Algorithmic bytes of one decode launch: every lane's logical K/V (mean
+    # over the timed launches), the queries, the outputs and the tokens written.
+    dec_appended = args.warmup + args.steps + (total_steps - args.warmup - args.steps + 1) / 2.0
+    dec_bytes = (lengths.sum() + lanes * dec_appended) * 2 * HD * 2 + lanes * (2 * QD * 2 + 2 * HD * 2)
     us_per_layer = ms_per_step * 1000.0 / L
     appended = args.warmup + (args.steps + 1) / 2.0          # mean tokens appended by the timed steps
     logical_bytes = (lengths.sum() + lanes * appended) * 2 * HD * 2
@@ -934,8 +973,16 @@ def run_shared(kimkv, dev, args) -> int:
         "value": round(us_per_layer, 2), "unit": "us/layer", "higher_is_better": False,
         "logical_gb_per_s": round(logical_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "physical_gb_per_s": round(physical_bytes / (us_per_layer * 1e-6) / 1e9, 1),
-        "decode_kernel_avg_us": round(1000 * dec_ms / max(dec_n, 1), 2),
+        "decode_kernel_avg_us": round(1000 * dec_ms, 2),
         "ms_per_step": round(ms_per_step, 3),
+        "roofline": {"bound": "hbm", "achieved": round(dec_bytes / (dec_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(dec_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic("decode_kernel_shared_prefix.md", lanes=lanes, layers=L,
+                                                 logical_tokens=int(logical)),
+                     "kernel": "decode_kernel", "launch_ms": round(dec_ms, 4), "timed_launches": dec_n,
+                     "bytes_per_launch": int(dec_bytes),
+                     "note": "bytes are the lanes' logical K/V; the fork groups share prefix pages, so the unique "
+                             "pages are about half of them; latency-bound (one round of 256-token chunks)"},
         "config": {"workload": f"{lanes} lanes ({groups} groups of {per_group} forking a 2048+r-token prefix, "
                                f"partial-tail COW), contexts log-uniform in [128, 8192], {L} layers TinyLlama GQA "
                                f"32q/4kv/64d fp16, through the engine",
@@ -1036,9 +1083,12 @@ def run_prefill(kimkv, dev, args) -> int:
     flops = 4.0 * QH * D * pairs
     kv_bytes = float(sum(int(t) + n for t in T0)) * 2 * HD * 2 + 2 * lanes * n * QD * 2
     tflops = flops / (kernel_ms * 1e-3) / 1e12
-    # Check sampled rows of layers 0 and L-1 against the oracle's decode of the first T0 + r + 1 tokens.
+    # Check sampled rows of layers 0 and L-1 against the oracle's decode of
+    # the first T0 + r + 1 tokens; the oracle's decode of those rows is also
+    # the CPU baseline (one core), as FLOP/s over the same per-pair count.
     import oracle
     worst, ok, rows = 0.0, True, 0
+    cpu_s, cpu_pairs = 0.0, 0
     for i in range(lanes):
         t0 = int(T0[i])
         for l in (0, L - 1):
@@ -1050,11 +1100,21 @@ def run_prefill(kimkv, dev, args) -> int:
             got = dev.download(out.ptr + ((i * L + l) * n * QD) * 2, (n, QD), np.uint16)
             for r in (0, n // 2, n - 1):
                 T = t0 + r + 1
+                t_cpu = time.perf_counter()
                 ref = oracle_decode_layer(kvl[:, :T], T, ql[r], QH, D)
+                cpu_s += time.perf_counter() - t_cpu
+                cpu_pairs += T
                 err = np.abs(got[r].view(np.float16).astype(np.float32) - ref)
                 worst = max(worst, float(err.max()))
                 ok = ok and bool(np.all(err <= 2e-3 + 1e-3 * np.abs(ref)))
                 rows += 1
+    cpu_tflops = 4.0 * QH * D * cpu_pairs / cpu_s / 1e12
+    cpu = {"value": round(cpu_tflops, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+           "us_per_launch_equivalent": round(flops / (cpu_tflops * 1e12) * 1e6, 1),
+           "sample": f"the check's {rows} query rows (one token's GQA decode over its {cpu_pairs // rows}-token mean "
+                     f"causal context each, page setup included) by the oracle's kvo_paged_decode on "
+                     f"{platform.processor() or platform.machine()}, {round(cpu_s, 2)} s",
+           "seconds": round(cpu_s, 2)}
     print(json.dumps({
         "metric": "chunked-prefill causal paged GQA attention (MFMA) TFLOP/s",
         "value": round(tflops, 2), "unit": "TFLOP/s", "higher_is_better": True,
@@ -1063,7 +1123,10 @@ def run_prefill(kimkv, dev, args) -> int:
         "prefill_kernel_avg_us": round(kernel_ms * 1000, 2), "prefill_launches": pf_n,
         "dtype": "f16 in, f32 accumulate",
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None,
+                     "frac": round(tflops / PEAK_MFMA_F16_TFLOPS, 4),
+                     "traffic": profiled_traffic("prefill_kernel_chunked.md", chunks=lanes, chunk_tokens=n,
+                                                 context_tokens=int(sum(int(t) for t in T0)), layers=L),
+                     "kernel": "prefill_kernel", "launch_ms": round(kernel_ms, 4), "timed_launches": pf_n,
                      "flops_per_launch": flops,
                      "kv_q_o_bytes_per_launch": kv_bytes,
                      "hbm_gb_per_s_if_read_once": round(kv_bytes / (kernel_ms * 1e-3) / 1e9, 1)},
@@ -1073,7 +1136,8 @@ def run_prefill(kimkv, dev, args) -> int:
                                f"forked per step (partial-tail COW), through the engine"},
         "steps": args.steps, "warmup": args.warmup,
         "check": {"rows": rows, "layers": [0, L - 1], "max_abs_err": worst, "within_tolerance": ok,
-                  "tolerance": "2e-3 + 1e-3*|ref|"}}), flush=True)
+                  "tolerance": "2e-3 + 1e-3*|ref|"},
+        "cpu_baseline": cpu}), flush=True)
     return 0 if ok else 1
 
 
@@ -1169,18 +1233,42 @@ def run_e2e(kimkv, dev, args) -> int:
             break
     t0 = time.time()
     ref = om.ReferenceModel(om.ModelConfig(HID, INTER, L, QH, KVH, D, VOC, MAXPOS), args.seed)
+    # The oracle's token-by-token forwards are also the CPU baseline.
+    fwd_s, fwd_n = 0.0, 0
+
+    def forward(tok, pos):
+        nonlocal fwd_s, fwd_n
+        t = time.perf_counter()
+        r = ref.forward(tok, pos)
+        fwd_s += time.perf_counter() - t
+        fwd_n += 1
+        return r
+
     for p, t in enumerate(prompt):
-        logits = ref.forward(t, p)
+        logits = forward(t, p)
     ok, margin = len(out) == 3, 0.0
     for g, tok in enumerate(out):
         margin = max(margin, float(logits.max() - logits[tok]))
         ok = ok and bool(logits[tok] >= logits.max() - 0.035)
         if g + 1 < len(out):
-            logits = ref.forward(tok, len(prompt) + g)
+            logits = forward(tok, len(prompt) + g)
     log(f"oracle check in {time.time() - t0:.1f}s")
+    try:
+        from threadpoolctl import threadpool_info
+        blas_threads = max((int(i.get("num_threads", 1)) for i in threadpool_info()), default=1)
+    except ImportError:
+        blas_threads = 1
+    cpu = {"value": round(fwd_n / fwd_s, 2) if fwd_s > 0 else None, "unit": "tokens/s", "cores": blas_threads,
+           "kind": "port",
+           "sample": f"the check's {fwd_n} single-token forwards (positions 0-{fwd_n - 1}) through the oracle's "
+                     f"fp32/fp16-rounded numpy model of the same weights on "
+                     f"{platform.processor() or platform.machine()}, {round(fwd_s, 2)} s; no batching",
+           "seconds": round(fwd_s, 2)}
     sched.close()
     runner.close()
     total = tok_pre + tok_dec
+    per_layer_weights = HID * (QH * D + 2 * KVH * D) + QH * D * HID + HID * 2 * INTER + INTER * HID
+    lin_flops = 2.0 * L * per_layer_weights * total
     print(json.dumps({
         "metric": "e2e TinyLlama chunked prefill + decode tokens/s (iteration scheduler)",
         "value": round(total / wall, 1), "unit": "tokens/s", "higher_is_better": True,
@@ -1196,7 +1284,14 @@ def run_e2e(kimkv, dev, args) -> int:
                    "max_batched_tokens": budget},
         "steps": args.steps, "warmup": args.warmup, "data": "synthetic (random token ids, seeded weights)",
         "check": {"request_prompt": 6, "tokens": len(out), "all_near_argmax": ok,
-                  "max_logit_gap_to_oracle_max": margin, "tolerance": 0.035}}), flush=True)
+                  "max_logit_gap_to_oracle_max": margin, "tolerance": 0.035},
+        "roofline": {"bound": "mfma", "achieved": round(lin_flops / wall / 1e12, 2), "peak": PEAK_MFMA_F16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(lin_flops / wall / 1e12 / PEAK_MFMA_F16_TFLOPS, 4),
+                     "traffic": None, "kernel": "whole iteration",
+                     "flops_per_step": round(lin_flops / args.steps),
+                     "note": "FLOPs of the 22 layers' four linear projections (2 x 968.9 M weights per token) "
+                             "over the step's wall time; attention and the LM head are not counted"},
+        "cpu_baseline": cpu}), flush=True)
     return 0 if ok else 1
 
 
@@ -1229,24 +1324,26 @@ def run_copy(dev, args) -> int:
     return 0
 
 
-def profiled_traffic(lanes_per_launch: int, context: int, layers: int):
-    """HBM bytes per decode launch from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE per dispatch, each times its copy-calibrated
-    factor), when the summary was measured on this launch shape."""
-    path = os.path.join(ROOT, "profiles", "decode_kernel_hbm_scale.md")
+def profiled_traffic(profile: str, **shape):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary under
+    profiles/ (FETCH_SIZE and WRITE_SIZE per dispatch, each times its
+    copy-calibrated factor), when the summary's machine-readable lines name
+    the same workload shape as `shape`; None otherwise."""
+    path = os.path.join(ROOT, "profiles", profile)
     if not os.path.exists(path):
         return None
     vals = {}
+    block = False
     for line in open(path):
-        if ":" in line:
+        block = block or line.startswith("Machine-readable")
+        if block and ":" in line:
             k, _, v = line.strip().partition(":")
             try:
                 vals[k.strip()] = float(v)
             except ValueError:
                 pass
     try:
-        if (int(vals["lanes_per_launch"]), int(vals["context"]), int(vals["layers"])) != (
-                lanes_per_launch, context, layers):
+        if any(vals[k] != float(v) for k, v in shape.items()):
             return None
         return int(vals["fetch_size_kib_per_dispatch"] * 1024 * vals["fetch_factor"]
                    + vals["write_size_kib_per_dispatch"] * 1024 * vals["write_factor"])
@@ -1448,7 +1545,8 @@ def main() -> int:
                    "group_streams": len(w.streams) if args.path == "engine" else 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": profiled_traffic(lanes_per_launch, args.context, args.layers),
+                     "traffic": profiled_traffic("decode_kernel_hbm_scale.md", lanes_per_launch=lanes_per_launch,
+                                                 context=args.context, layers=args.layers),
                      "kernel": "decode_kernel", "launch_ms": round(decode_eff_ms, 4),
                      "avg_launch_ms": round(decode_avg_ms, 4),
                      "launches_in_flight": round(decode_ms_total / decode_busy_ms, 3) if multi and decode_busy_ms

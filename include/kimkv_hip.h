@@ -425,6 +425,8 @@ kimkv_status kimkv_reference_attention(const kimkv_storage* storage,
 kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launches);
 /* The same for the chunked-prefill attention kernel (same `enable`). */
 kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launches);
+/* The same for the page-append kernel (kimkv_append_batch launches). */
+kimkv_status kimkv_append_timing(int enable, double* total_ms, uint64_t* launches);
 /* Time (ms) during which at least one timed decode launch was running, over
  * the window the last kimkv_decode_timing call closed: the union of the
  * launches' intervals.  Launches on several streams overlap, so this is less

@@ -584,8 +584,12 @@ kimkv_status kimkv_append_batch(const kimkv_storage* storage, const kimkv_append
     if (job_count == 0 || max_layer_count == 0) return KIMKV_OK;
     if (max_layer_count > storage->layout.layers || job_count > 0x7FFFFFFFu) return KIMKV_INVALID_ARGUMENT;
     dim3 const grid(job_count, max_layer_count);
+    void* start = nullptr;
+    kernel_timing_begin(TimedKernel::Append, native(stream), &start);
     append_kernel<<<grid, kBlock, 0, native(stream)>>>(pool_view(*storage), device_jobs, job_count);
-    return launch_status();
+    kimkv_status const status = launch_status();
+    kernel_timing_end(TimedKernel::Append, native(stream), start);
+    return status;
 }
 
 kimkv_status kimkv_gather(const kimkv_storage* storage, const kimkv_block_desc* device_descriptors,

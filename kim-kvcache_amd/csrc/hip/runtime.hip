@@ -59,7 +59,7 @@ void spare_event_locked(DecodeTiming& t, hipEvent_t e)
 
 DecodeTiming& timing(TimedKernel kind = TimedKernel::Decode)
 {
-    static DecodeTiming instances[2];
+    static DecodeTiming instances[3];
     return instances[static_cast<int>(kind)];
 }
 
@@ -513,6 +513,11 @@ kimkv_status kimkv_decode_timing(int enable, double* total_ms, uint64_t* launche
 kimkv_status kimkv_prefill_timing(int enable, double* total_ms, uint64_t* launches)
 {
     return kernel_timing(kimkv::TimedKernel::Prefill, enable, total_ms, launches);
+}
+
+kimkv_status kimkv_append_timing(int enable, double* total_ms, uint64_t* launches)
+{
+    return kernel_timing(kimkv::TimedKernel::Append, enable, total_ms, launches);
 }
 
 kimkv_status kimkv_decode_timing_busy(double* busy_ms)

@@ -21,7 +21,7 @@ inline hipStream_t native(kimkv_stream_t stream) { return static_cast<hipStream_
 // Kernel event timing used by the benchmark (kimkv_decode_timing,
 // kimkv_prefill_timing): events recorded on the launch stream around each
 // launch while enabled.
-enum class TimedKernel : int { Decode = 0, Prefill = 1 };
+enum class TimedKernel : int { Decode = 0, Prefill = 1, Append = 2 };
 void kernel_timing_begin(TimedKernel kind, hipStream_t stream, void** start);
 void kernel_timing_end(TimedKernel kind, hipStream_t stream, void* start);
 

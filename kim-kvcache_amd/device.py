@@ -155,6 +155,8 @@ _SIGNATURES = {
                                            ctypes.POINTER(ctypes.c_uint64)]),
     "kimkv_prefill_timing": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_uint64)]),
+    "kimkv_append_timing": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                           ctypes.POINTER(ctypes.c_uint64)]),
     "kimkv_decode_timing_busy": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double)]),
     "kimkv_linear": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
                                     ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_void_p]),
@@ -540,4 +542,14 @@ def prefill_timing(enable, every: int = 1):
     launches = ctypes.c_uint64()
     check(lib().kimkv_prefill_timing(max(1, int(every)) if enable else 0, ctypes.byref(total),
                                      ctypes.byref(launches)), "prefill_timing")
+    return float(total.value), int(launches.value)
+
+
+def append_timing(enable, every: int = 1):
+    """Returns (ms, launches) of the page-append kernel timed since the last call; then
+    times every `every`-th launch if enable."""
+    total = ctypes.c_double()
+    launches = ctypes.c_uint64()
+    check(lib().kimkv_append_timing(max(1, int(every)) if enable else 0, ctypes.byref(total),
+                                    ctypes.byref(launches)), "append_timing")
     return float(total.value), int(launches.value)
