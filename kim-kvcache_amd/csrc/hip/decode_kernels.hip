@@ -623,7 +623,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     __shared__ uint32_t s_hit;
 
     uint32_t const tid = threadIdx.x;
-    uint32_t const chunk_id = blockIdx.x;
+    // One workgroup per chunk with every head (grid.y == 1): each XCD takes a
+    // contiguous run of chunks (workgroups are dealt to the XCDs round-robin),
+    // so the lanes next to each other in the batch -- forks of one prefix,
+    // whose leading chunks read the same pages -- meet in one XCD's L2.
+    uint32_t const chunk_id = !kSplit && gridDim.y == 1 ? xcd_logical_index(blockIdx.x, gridDim.x) : blockIdx.x;
     if (lane_count == 0) return;
     // The prologue is a chain of dependent global reads, and under full HBM
     // load each costs microseconds while this workgroup streams nothing, so
