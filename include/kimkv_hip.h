@@ -339,6 +339,25 @@ kimkv_status kimkv_paged_decode_write_batch(const kimkv_storage* storage,
                                             uint32_t query_heads, const kimkv_append_job* device_writes,
                                             kimkv_stream_t stream);
 
+/* Bytes per lane of kimkv_paged_decode_write_batch_slots's merge records. */
+#define KIMKV_DECODE_LANE_SLOT_BYTES 32u
+
+/* kimkv_paged_decode_write_batch whose split-K merge reads no launch item:
+ * device_lane_slots (lane_count x KIMKV_DECODE_LANE_SLOT_BYTES bytes of
+ * device memory, 16-byte aligned, contents ignored) receives from the decode
+ * launch what each lane's merge needs (output, partials, chunk count, tagged
+ * with the launch), and the merge launch reads that instead of the items and
+ * the chunk prefix.  For callers whose items live in host memory the device
+ * reads directly (the engine's staged batches): the merge then starts
+ * without a round trip to the host.  Same results as
+ * kimkv_paged_decode_write_batch.  No counterpart in the reference. */
+kimkv_status kimkv_paged_decode_write_batch_slots(const kimkv_storage* storage,
+                                                  const kimkv_decode_item* device_items,
+                                                  const uint32_t* device_chunk_prefix, uint32_t lane_count,
+                                                  uint32_t total_chunks, uint32_t chunk_flags,
+                                                  uint32_t query_heads, const kimkv_append_job* device_writes,
+                                                  void* device_lane_slots, kimkv_stream_t stream);
+
 /* Size of the device scratch array of kimkv_paged_decode_batch_noalloc. */
 #define KIMKV_DECODE_SCRATCH_BYTES (16u << 20)
 

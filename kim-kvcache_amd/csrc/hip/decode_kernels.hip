@@ -597,6 +597,20 @@ __device__ inline void written_token_visible()
     __syncthreads();
 }
 
+// What a lane's split-K merge needs, written by the decode launch's first
+// workgroup of the lane (chunk 0, first head block) so that the merge launch
+// reads device memory instead of the launch's items (host memory when the
+// engine stages them).  `tag` names the launch: a slot another launch wrote,
+// or that no workgroup wrote, does not match and is skipped.
+struct DecodeLaneSlot {
+    uint16_t* output;
+    float* workspace;   // where the lane's partials went
+    uint32_t chunks;
+    uint32_t lane;
+    uint64_t tag;
+};
+static_assert(sizeof(DecodeLaneSlot) == KIMKV_DECODE_LANE_SLOT_BYTES, "slot size");
+
 // Two waves per SIMD: each wave holds two 64-token steps of K/V operands in
 // registers, so a CU keeps as many bytes in flight as four single-buffered
 // waves while the compute of one step hides under the loads of the next.
@@ -613,10 +627,12 @@ __device__ inline void written_token_visible()
 // writes: when non-null, lane i's new token (writes[i], token_count 0 for
 // none) is written first by the workgroups of the chunk that holds it.
 // kStream: non-temporal K/V loads (load_kv).
+// slots: when non-null, each lane's merge record (DecodeLaneSlot, tagged
+// `tag`) for the merge launch.
 template <bool kSplit, bool kStream>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
     PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t chunk_tokens,
-    uint32_t QH, float* partials, const kimkv_append_job* writes)
+    uint32_t QH, float* partials, const kimkv_append_job* writes, DecodeLaneSlot* slots, uint64_t tag)
 {
     __shared__ DecodeLds lds;
     __shared__ uint32_t s_lane;
@@ -673,6 +689,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     if (!decode_item_valid(P, item, QH, nchunks) || c0 >= T || chunk_tokens > kMaxChunk) {
         report_fault(P, KIMKV_FAULT_DECODE_ITEM);
         return;
+    }
+    if (slots != nullptr && chunk_index == 0 && blockIdx.y == 0 && tid == 0) {
+        slots[lane] = DecodeLaneSlot{item.output, item.workspace, nchunks, lane, tag};
     }
     uint32_t const c1 = min(c0 + chunk_tokens, T);
     uint32_t const G = QH / H;
@@ -811,23 +830,40 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 // chunks fold into the running (M, den, acc) like an online softmax.
 constexpr unsigned kCombineHeads = 4;
 
+// slots: when non-null, the lanes' merge records the decode launch tagged
+// `tag` replace the items and the chunk prefix.
 template <uint32_t kDims>
 __global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(PoolView P, const kimkv_decode_item* items,
                                                                     const uint32_t* prefix, uint32_t QH, uint32_t D,
-                                                                    float* partials)
+                                                                    float* partials, const DecodeLaneSlot* slots,
+                                                                    uint64_t tag)
 {
     constexpr uint32_t kBatch = 64 / kDims;   // partial rows held in registers at once
     uint32_t const lane = blockIdx.x;
     uint32_t const q = blockIdx.y * kCombineHeads + (threadIdx.x >> 6);
     uint32_t const l = threadIdx.x & 63u;
     if (q >= QH) return;
-    uint32_t const n = prefix[lane + 1] - prefix[lane];
-    if (n <= 1) return;
-    kimkv_decode_item item = items[lane];
-    if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(prefix[lane]) * QH * (D + 2);
-    if (!decode_item_valid(P, item, QH, n)) return;   // decode_kernel reported it
+    uint32_t n = 0;
+    uint16_t* output = nullptr;
+    const float* workspace = nullptr;
+    if (slots != nullptr) {
+        DecodeLaneSlot const slot = slots[lane];
+        if (slot.tag != tag || slot.lane != lane) return;   // no decode workgroup of this launch wrote it
+        n = slot.chunks;
+        output = slot.output;
+        workspace = slot.workspace;
+        if (n <= 1) return;
+    } else {
+        n = prefix[lane + 1] - prefix[lane];
+        if (n <= 1) return;
+        kimkv_decode_item item = items[lane];
+        if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(prefix[lane]) * QH * (D + 2);
+        if (!decode_item_valid(P, item, QH, n)) return;   // decode_kernel reported it
+        output = item.output;
+        workspace = item.workspace;
+    }
     uint64_t const stride = static_cast<uint64_t>(QH) * (D + 2);
-    const float* ws = item.workspace + static_cast<uint64_t>(q) * (D + 2);
+    const float* ws = workspace + static_cast<uint64_t>(q) * (D + 2);
     float M = -INFINITY;
     float den = 0.0f;
     float acc[kDims];
@@ -875,7 +911,7 @@ __global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(PoolView P,
 #pragma unroll
     for (uint32_t j = 0; j < kDims; ++j) {
         uint32_t const d = l + 64u * j;
-        if (d < D) item.output[static_cast<uint64_t>(q) * D + d] = __half_as_ushort(__float2half_rn(acc[j] * inv));
+        if (d < D) output[static_cast<uint64_t>(q) * D + d] = __half_as_ushort(__float2half_rn(acc[j] * inv));
     }
 }
 
@@ -959,7 +995,7 @@ __global__ __launch_bounds__(64) void reference_attention_kernel(PoolView P, con
 kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item* device_items,
                            const uint32_t* device_chunk_prefix, uint32_t lane_count, uint32_t total_chunks,
                            uint32_t chunk_flags, uint32_t query_heads, kimkv_stream_t stream, float* partials,
-                           const kimkv_append_job* writes, bool timed)
+                           const kimkv_append_job* writes, bool timed, DecodeLaneSlot* slots = nullptr)
 {
     bool const head_split = (chunk_flags & KIMKV_DECODE_HEAD_SPLIT) != 0;
     bool const guided = (chunk_flags & KIMKV_DECODE_GUIDED) != 0;
@@ -976,6 +1012,9 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
     uint64_t const units = static_cast<uint64_t>(lane_count) * H * KIMKV_DECODE_GUIDED_SLICES;
     if (guided && (units > 0x7FFFFFFFu || storage->work_counters == nullptr)) return KIMKV_INVALID_ARGUMENT;
     dim3 const grid(total_chunks, head_split ? H : (H + kHeadsPerBlock - 1) / kHeadsPerBlock);
+    // The guided kernel writes no merge records.
+    if (guided) slots = nullptr;
+    uint64_t const tag = slots != nullptr ? storage->next_decode_tag.fetch_add(1, std::memory_order_relaxed) : 0;
     void* start = nullptr;
     if (timed) kernel_timing_begin(TimedKernel::Decode, s, &start);
     if (guided) {
@@ -994,16 +1033,16 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
         PoolView const pv = pool_view(*storage);
         if (head_split && stream_loads) {
             decode_kernel<true, true><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
-                                                              chunk_tokens, query_heads, partials, writes);
+                                                              chunk_tokens, query_heads, partials, writes, slots, tag);
         } else if (head_split) {
             decode_kernel<true, false><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
-                                                               chunk_tokens, query_heads, partials, writes);
+                                                               chunk_tokens, query_heads, partials, writes, slots, tag);
         } else if (stream_loads) {
             decode_kernel<false, true><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
-                                                               chunk_tokens, query_heads, partials, writes);
+                                                               chunk_tokens, query_heads, partials, writes, slots, tag);
         } else {
             decode_kernel<false, false><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
-                                                                chunk_tokens, query_heads, partials, writes);
+                                                                chunk_tokens, query_heads, partials, writes, slots, tag);
         }
     }
     if (timed) kernel_timing_end(TimedKernel::Decode, s, start);
@@ -1015,15 +1054,15 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
         if (D <= 64) {
             combine_kernel<1><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
                                                                      device_chunk_prefix, query_heads, D,
-                                                                     partials);
+                                                                     partials, slots, tag);
         } else if (D <= 128) {
             combine_kernel<2><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
                                                                      device_chunk_prefix, query_heads, D,
-                                                                     partials);
+                                                                     partials, slots, tag);
         } else {
             combine_kernel<4><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
                                                                      device_chunk_prefix, query_heads, D,
-                                                                     partials);
+                                                                     partials, slots, tag);
         }
         return launch_status();
     }
@@ -1160,6 +1199,22 @@ kimkv_status kimkv_paged_decode_write_batch(const kimkv_storage* storage, const 
     if (device_writes == nullptr) return KIMKV_INVALID_ARGUMENT;
     return kimkv::launch_decode(storage, device_items, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
                                 query_heads, stream, nullptr, device_writes, true);
+}
+
+kimkv_status kimkv_paged_decode_write_batch_slots(const kimkv_storage* storage,
+                                                  const kimkv_decode_item* device_items,
+                                                  const uint32_t* device_chunk_prefix, uint32_t lane_count,
+                                                  uint32_t total_chunks, uint32_t chunk_flags, uint32_t query_heads,
+                                                  const kimkv_append_job* device_writes, void* device_lane_slots,
+                                                  kimkv_stream_t stream)
+{
+    if (device_writes == nullptr || device_lane_slots == nullptr
+        || (reinterpret_cast<uintptr_t>(device_lane_slots) & 15u) != 0) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    return kimkv::launch_decode(storage, device_items, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
+                                query_heads, stream, nullptr, device_writes, true,
+                                static_cast<kimkv::DecodeLaneSlot*>(device_lane_slots));
 }
 
 kimkv_status kimkv_paged_decode_batch_noalloc(const kimkv_storage* storage, const kimkv_decode_item* device_items,

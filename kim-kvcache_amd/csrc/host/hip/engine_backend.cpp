@@ -381,10 +381,18 @@ public:
         auto* staged = static_cast<unsigned char*>(st.ring().stage(staging.data(), staging.size(), stream));
         kimkv_status k = KIMKV_SUBMISSION_FAILED;
         if (staged != nullptr) {
-            k = kimkv_paged_decode_write_batch(
-                st.handle(), reinterpret_cast<kimkv_decode_item const*>(staged),
-                reinterpret_cast<std::uint32_t const*>(staged + prefix_at), static_cast<std::uint32_t>(n), total,
-                chunk, QH, reinterpret_cast<kimkv_append_job const*>(staged + items_bytes), stream);
+            // With split-K lanes, the merge launch reads its per-lane records
+            // from device scratch the decode launch fills, not the staged
+            // items (a round trip to host memory at its start).
+            void* slots = total > n ? st.ring().deviceScratch(n * KIMKV_DECODE_LANE_SLOT_BYTES, stream) : nullptr;
+            auto const* items_d = reinterpret_cast<kimkv_decode_item const*>(staged);
+            auto const* prefix_d = reinterpret_cast<std::uint32_t const*>(staged + prefix_at);
+            auto const* writes_d = reinterpret_cast<kimkv_append_job const*>(staged + items_bytes);
+            k = slots != nullptr
+                ? kimkv_paged_decode_write_batch_slots(st.handle(), items_d, prefix_d, static_cast<std::uint32_t>(n),
+                                                       total, chunk, QH, writes_d, slots, stream)
+                : kimkv_paged_decode_write_batch(st.handle(), items_d, prefix_d, static_cast<std::uint32_t>(n),
+                                                 total, chunk, QH, writes_d, stream);
         }
         st.ring().fence(stream);
         // Only the last layer's launch needs a completion mark (commit waits

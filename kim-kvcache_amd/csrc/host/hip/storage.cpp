@@ -128,6 +128,16 @@ void* StagingRing::upload(void const* data, std::size_t bytes, HipStream stream)
     return dev;
 }
 
+void* StagingRing::deviceScratch(std::size_t bytes, HipStream stream)
+{
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (host_ == nullptr || bytes > regions_.maxRequest()) return nullptr;
+    if (device_.get() == nullptr) device_ = DeviceMemory(size_);
+    if (device_.get() == nullptr) return nullptr;
+    std::size_t const off = reserve(bytes, stream);
+    return static_cast<unsigned char*>(device_.get()) + off;
+}
+
 bool StagingRing::uploadTo(void* device_dst, void const* data, std::size_t bytes, HipStream stream)
 {
     std::lock_guard<std::mutex> lock(mutex_);

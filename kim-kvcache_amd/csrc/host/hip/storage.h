@@ -68,6 +68,10 @@ public:
     [[nodiscard]] void* stage(void const* data, std::size_t bytes, HipStream stream);
     // Returns the device address of the staged copy, or nullptr on failure.
     [[nodiscard]] void* upload(void const* data, std::size_t bytes, HipStream stream);
+    // Device scratch of `bytes` (16-byte aligned, contents undefined) that
+    // work on `stream` may use until the next fence's work completes; nullptr
+    // on failure.  No copy command.
+    [[nodiscard]] void* deviceScratch(std::size_t bytes, HipStream stream);
     // Host staging only (the caller names the device destination).  Any
     // size: uploads beyond half the ring are split into pieces.
     [[nodiscard]] bool uploadTo(void* device_dst, void const* data, std::size_t bytes, HipStream stream);

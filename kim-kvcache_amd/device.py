@@ -137,6 +137,10 @@ _SIGNATURES = {
     "kimkv_paged_decode_write_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                       ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                       ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]),
+    "kimkv_paged_decode_write_batch_slots": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                            ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                                            ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
+                                                            ctypes.c_void_p]),
     "kimkv_paged_decode_batch_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                         ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                         ctypes.c_uint32, ctypes.c_void_p]),
@@ -408,6 +412,17 @@ class Storage:
                                                    ctypes.c_void_p(writes_ptr), _sh(stream)),
               "paged_decode_write_batch")
 
+    def decode_write_slots_launch(self, items_ptr: int, prefix_ptr: int, lanes: int, total_chunks: int,
+                                  chunk_tokens: int, query_heads: int, writes_ptr: int, slots_ptr: int,
+                                  stream: Optional[Stream] = None) -> None:
+        """kimkv_paged_decode_write_batch_slots: as decode_write_launch, the merge reading per-lane records
+        the decode launch leaves in slots_ptr (lanes x DECODE_LANE_SLOT_BYTES of device memory)."""
+        check(lib().kimkv_paged_decode_write_batch_slots(self.h, ctypes.c_void_p(items_ptr),
+                                                         ctypes.c_void_p(prefix_ptr), lanes, total_chunks,
+                                                         chunk_tokens, query_heads, ctypes.c_void_p(writes_ptr),
+                                                         ctypes.c_void_p(slots_ptr), _sh(stream)),
+              "paged_decode_write_batch_slots")
+
     def prefill_plan(self, new_token_counts, query_heads: int):
         """(tokens per workgroup, workgroup prefix over items, total workgroups)."""
         per = int(lib().kimkv_prefill_tokens_per_block(self.h, query_heads))
@@ -459,6 +474,7 @@ def prefill_order(kv_heads: int, head_dim: int, query_heads: int, compute_units:
 DECODE_HEAD_SPLIT = 0x80000000
 DECODE_GUIDED = 0x40000000
 DECODE_GUIDED_SLICES = 6
+DECODE_LANE_SLOT_BYTES = 32
 
 # Fault bits of kimkv_storage_faults (include/kimkv_hip.h).
 FAULT_APPEND_JOB = 0x1

@@ -287,7 +287,24 @@ def _write_then_decode(dev, fused, tables, T, news, lanes_meta, QH, chunk, shape
         keep += [dbuf, qbuf, wbuf]
         outs.append(obuf)
     ibuf, pbuf, jbuf = dev.upload(items), dev.upload(prefix), dev.upload(jobs)
-    if fused:
+    if fused == "slots":
+        # Merge records in device scratch holding leftovers: random bytes, then a first launch's records
+        # (the second launch's tag differs, so none of them may be taken for its own).
+        junk = np.random.default_rng(seed).integers(0, 256, len(lanes) * dev.DECODE_LANE_SLOT_BYTES, dtype=np.uint8)
+        slots = dev.upload(junk)
+        keep.append(slots)
+        storage.decode_write_slots_launch(ibuf.ptr, pbuf.ptr, len(lanes), total, chunk, QH, jbuf.ptr, slots.ptr)
+        dev.sync()
+        for o in outs:
+            dev.copy_to_device(o.ptr, np.zeros(QH * D, dtype=np.uint16))
+        # The first launch wrote the tokens; the second must not write them again over a copy-on-write
+        # source: its jobs write nothing.
+        none = jobs.copy()
+        none["token_count"] = 0
+        jbuf2 = dev.upload(none)
+        keep.append(jbuf2)
+        storage.decode_write_slots_launch(ibuf.ptr, pbuf.ptr, len(lanes), total, chunk, QH, jbuf2.ptr, slots.ptr)
+    elif fused:
         storage.decode_write_launch(ibuf.ptr, pbuf.ptr, len(lanes), total, chunk, QH, jbuf.ptr)
     else:
         storage.append_batch(jobs)
@@ -320,10 +337,14 @@ def test_decode_write_batch_matches_append_then_decode(dev, mode):
     chunk = {"four_heads": 256, "head_split": 256 | dev.DECODE_HEAD_SPLIT, "guided": dev.DECODE_GUIDED | 64}[mode]
     a, pa, total = _write_then_decode(dev, False, tables, T, news, layers, QH, chunk, shape, 24, cows)
     b, pb, _ = _write_then_decode(dev, True, tables, T, news, layers, QH, chunk, shape, 24, cows)
+    c, pc, _ = _write_then_decode(dev, "slots", tables, T, news, layers, QH, chunk, shape, 24, cows)
     assert total > len(T)
     for i in range(len(T)):
         assert np.array_equal(pa[i], pb[i]), (mode, i)
         assert np.array_equal(a[i], b[i]), (mode, i)
+        # kimkv_paged_decode_write_batch_slots: the same pages and outputs.
+        assert np.array_equal(pa[i], pc[i]), (mode, i)
+        assert np.array_equal(a[i], c[i]), (mode, i)
     print(f"decode+write mode={mode} lanes={len(T)} chunks={total}", flush=True)
 
 
