@@ -1014,7 +1014,10 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
     dim3 const grid(total_chunks, head_split ? H : (H + kHeadsPerBlock - 1) / kHeadsPerBlock);
     // The guided kernel writes no merge records.
     if (guided) slots = nullptr;
-    uint64_t const tag = slots != nullptr ? storage->next_decode_tag.fetch_add(1, std::memory_order_relaxed) : 0;
+    // Launch tags are unique in the process, so a slot array shared by
+    // several storages still never matches another launch's records.
+    static std::atomic<uint64_t> next_tag{1};
+    uint64_t const tag = slots != nullptr ? next_tag.fetch_add(1, std::memory_order_relaxed) : 0;
     void* start = nullptr;
     if (timed) kernel_timing_begin(TimedKernel::Decode, s, &start);
     if (guided) {

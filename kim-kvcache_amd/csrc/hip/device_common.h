@@ -32,7 +32,6 @@ struct kimkv_storage {
     uint32_t* faults{nullptr};        // device word, KIMKV_FAULT_* bits
     uint32_t* work_counters{nullptr}; // kWorkCounterSlots slots of kWorkCounterStride words
     mutable std::atomic<uint32_t> next_work_counter{0};
-    mutable std::atomic<uint64_t> next_decode_tag{1};   // names a launch's merge records
     uint32_t* fault_host{nullptr};    // mapped pinned word kimkv_storage_faults reads
     uint32_t* fault_view{nullptr};    // its device address
     int device{0};
