@@ -647,7 +647,8 @@ def run_append(kimkv, dev, args) -> int:
         "roofline": {"bound": "hbm", "achieved": round(step_bytes / (ap_ms / max(ap_n, 1) * 1e-3) / 1e9, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(step_bytes / (ap_ms / max(ap_n, 1) * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": None, "kernel": "append_kernel", "launch_ms": round(ap_ms / max(ap_n, 1), 4),
+                     "traffic": profiled_traffic("append_kernel_ragged_append.md", lanes=lanes, layers=L),
+                     "kernel": "append_kernel", "launch_ms": round(ap_ms / max(ap_n, 1), 4),
                      "timed_launches": ap_n, "bytes_per_launch": step_bytes,
                      "note": f"latency-bound: one launch of {lanes * L} (lane, layer) jobs of 1 KiB K + 1 KiB V each"},
         "config": {"workload": f"{lanes} lanes, contexts uniform in [1, 4096] tokens, {L} layers x 4 kv heads x 64 "
@@ -758,7 +759,8 @@ def run_parity(kimkv, dev, args) -> int:
         "decode_kernel_avg_us": round(dec_ms * 1000, 2),
         "roofline": {"bound": "hbm", "achieved": round(dec_bytes / (dec_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(dec_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": None, "kernel": "decode_kernel", "launch_ms": round(dec_ms, 4),
+                     "traffic": profiled_traffic("decode_kernel_config1_step.md", lanes=lanes, layers=L),
+                     "kernel": "decode_kernel", "launch_ms": round(dec_ms, 4),
                      "timed_launches": dec_n, "bytes_per_launch": int(dec_bytes),
                      "note": "latency-bound: 4 lanes, 1.6 k tokens of K/V in one launch"},
         "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
