@@ -62,12 +62,34 @@ __device__ __attribute__((always_inline)) inline half8_t load_kv(const uint16_t*
     return kStream ? load_half8_stream(p) : load_half8(p);
 }
 
+// A score times the folded scale (attention scale * log2 e), rounded on its
+// own: kept out of FMA contraction with the exponent's subtraction so that
+// full steps and tail steps (a chunk's last step, or the step that reads a
+// write job's new token) give the same bits for the same token.
+__device__ inline float scaled_score(float s, float scale2)
+{
+#pragma clang fp contract(off)
+    return s * scale2;
+}
+
+// The lane's new token as one kv head reads it in a launch that also writes
+// it: its K and V rows ([D] each) come from the write job's source, not from
+// the page (whose store is issued at the end of the launch).  t = absolute
+// token index, kNoToken when the chunk reads no new token.
+constexpr uint32_t kNoToken = 0xFFFFFFFFu;
+struct NewTokenRows {
+    const uint16_t* key;
+    const uint16_t* value;
+    uint32_t t;
+};
+
 // Tokens [c0, c1) of kv head h; the group table starts at token g0 (c0 - g0
-// is a multiple of 64).
+// is a multiple of 64).  When nt.t == c1 - 1 the last token's K and V come
+// from nt's rows (its page group may hold anything at that position).
 template <bool kStream>
 __device__ WavePartial decode_wave_d64(const GroupEntry* groups, const GroupResolver& res,
                                        const kimkv_decode_item& item, uint32_t h, uint32_t G, uint32_t g0,
-                                       uint32_t c0, uint32_t c1)
+                                       uint32_t c0, uint32_t c1, NewTokenRows const& nt)
 {
     constexpr uint32_t D = 64;
     uint32_t const l = threadIdx.x & 63u;
@@ -76,6 +98,9 @@ __device__ WavePartial decode_wave_d64(const GroupEntry* groups, const GroupReso
     uint32_t const x = (l >> 2) & 3u;     // K-operand row group
     uint32_t const q = h * G + r;
     bool const qvalid = r < G;
+    // The new token is always read in the tail variant of the last step.
+    bool const has_new = nt.t != kNoToken && nt.t + 1 == c1;
+    uint32_t const new_t = has_new ? nt.t : kNoToken;
 
     half8_t qb0 = {};
     half8_t qb1 = {};
@@ -111,7 +136,11 @@ __device__ WavePartial decode_wave_d64(const GroupEntry* groups, const GroupReso
 #pragma unroll
             for (uint32_t e = 0; e < 2; ++e) {
                 uint32_t const tt = 32 * kb + 8 * x + 4 * e + (l & 3u);
-                if (!kTail || (tt < nvalid && gk.page != kUnmappedGroup)) {
+                if (kTail && t0 + tt == new_t) {
+                    // The new token's K row: dims [8a, 8a+8) and [32+8a, 40+8a) of the source.
+                    o.k[kb][e][0] = load_half8(nt.key + a * 8);
+                    o.k[kb][e][1] = load_half8(nt.key + 32 + a * 8);
+                } else if (!kTail || (tt < nvalid && gk.page != kUnmappedGroup)) {
                     // K column blocks of 32 dims: dims [8a, 8a+8) and [32+8a, 40+8a).
                     const uint16_t* row = res.block(gk) + static_cast<uint64_t>(gk.pt0 + 4 * e + (l & 3u)) * 32
                         + a * 8;
@@ -178,7 +207,7 @@ __device__ WavePartial decode_wave_d64(const GroupEntry* groups, const GroupReso
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i) {
                     uint32_t const tt = 32 * kb + 8 * a + 4 * e + i;
-                    float const v = !kTail || tt < nvalid ? s[kb][e][i] * scale2 : -INFINITY;
+                    float const v = !kTail || tt < nvalid ? scaled_score(s[kb][e][i], scale2) : -INFINITY;
                     s[kb][e][i] = v;
                     mx = fmaxf(mx, v);
                 }
@@ -230,7 +259,7 @@ __device__ WavePartial decode_wave_d64(const GroupEntry* groups, const GroupReso
     Ops buf_a;
     Ops buf_b;
     std::false_type const full{};
-    uint32_t const nfull = (c1 - c0) >> 6;
+    uint32_t const nfull = (has_new ? c1 - c0 - 1 : c1 - c0) >> 6;
     if (nfull > 0) {
         // At the top of each round buf_a holds step s - 1 in flight; the body
         // has no bounds test, so no load in it is conditional.
@@ -251,8 +280,24 @@ __device__ WavePartial decode_wave_d64(const GroupEntry* groups, const GroupReso
         }
     }
     if (c0 + 64 * nfull < c1) {
-        load(buf_a, c0 + 64 * nfull, std::true_type{});
-        compute(buf_a, c0 + 64 * nfull, std::true_type{});
+        uint32_t const t0 = c0 + 64 * nfull;
+        load(buf_a, t0, std::true_type{});
+        if (has_new) {
+            // V^T rows d = 16 db + r of the new token's 8-token group: element
+            // j of lane group a (tokens [32 kb + 8 a, +8) of the step) is the
+            // new token for one (kb, a).
+#pragma unroll
+            for (uint32_t kb = 0; kb < 2; ++kb) {
+                uint32_t const j = new_t - t0 - (32 * kb + 8 * a);
+                if (j < 8) {
+#pragma unroll
+                    for (uint32_t db = 0; db < 4; ++db) {
+                        buf_a.v[kb][db][j] = __builtin_bit_cast(_Float16, nt.value[16 * db + r]);
+                    }
+                }
+            }
+        }
+        compute(buf_a, t0, std::true_type{});
     }
 
     float l_tot = l_part + __shfl_xor(l_part, 16);
@@ -294,14 +339,81 @@ __device__ inline void store_partial(const kimkv_decode_item& item, uint32_t QH,
 // ---------------------------------------------------------------------------
 struct WaveTokens {
     float p[64];
-    const uint16_t* head[64];   // (layer, head) block of the token's page
+    const uint16_t* head[64];   // (layer, head) block of the token's page; the V row when cap == 0
     uint32_t cap[64];
     uint32_t pt[64];
 };
 
+// A lane's single-token write job (kimkv_paged_decode_write_batch) as the
+// decode reads the pages: positions of the destination page that the job
+// writes are read from where the job takes them -- [0, cow_tokens) from the
+// copy-on-write source page, dst_token from the job's rows -- never from the
+// destination page.  So no read of the launch depends on the job's stores,
+// and the workgroups that make them issue them last.  `active` is false when
+// the lane has no job or the job is invalid.
+struct JobView {
+    bool active;
+    uint32_t dst_tag;        // GroupEntry::page form of the destination page
+    uint32_t cow_tag;        // and of the copy-on-write source
+    uint32_t dst_kind;
+    uint32_t dst_slot;
+    uint32_t dst_token;
+    uint32_t cow_kind;
+    uint32_t cow_slot;
+    uint32_t cow_tokens;
+    uint32_t cow_cap;
+    const uint16_t* key;     // the new token's rows [H][D]
+    const uint16_t* value;
+};
+
+// A job kimkv_paged_decode_write_batch can apply to `layer`: one token of one
+// layer into a page of this storage, an optional copy-on-write source that
+// holds the copied positions.
+__device__ inline bool write_job_valid(const PoolView& P, const kimkv_append_job& job, uint32_t layer)
+{
+    uint32_t const dcap = pool_tokens(P, job.dst_kind);
+    if (page_base(P, job.dst_kind, job.dst_slot, dcap) == nullptr || job.token_count != 1 || job.layer_count != 1
+        || job.layer_begin != layer || layer >= P.layers || job.dst_token >= dcap || job.src_key == nullptr
+        || job.src_value == nullptr) {
+        return false;
+    }
+    if (job.cow_tokens != 0) {
+        uint32_t const scap = pool_tokens(P, job.cow_kind);
+        if (page_base(P, job.cow_kind, job.cow_slot, scap) == nullptr || job.cow_tokens > scap
+            || job.cow_tokens > job.dst_token) {
+            return false;
+        }
+    }
+    return true;
+}
+
+__device__ inline uint32_t group_tag(uint32_t kind, uint32_t slot)
+{
+    return kind == KIMKV_PAGE_EXTENT ? slot | kExtentPage : slot;
+}
+
+__device__ inline JobView job_view(const PoolView& P, const kimkv_append_job& job, bool valid)
+{
+    JobView v{};
+    v.active = valid;
+    if (!valid) return v;
+    v.dst_kind = job.dst_kind;
+    v.dst_slot = job.dst_slot;
+    v.dst_token = job.dst_token;
+    v.dst_tag = group_tag(job.dst_kind, job.dst_slot);
+    v.cow_tokens = job.cow_tokens;
+    v.cow_kind = job.cow_kind;
+    v.cow_slot = job.cow_slot;
+    v.cow_tag = group_tag(job.cow_kind, job.cow_slot);
+    v.cow_cap = job.cow_tokens != 0 ? pool_tokens(P, job.cow_kind) : 0;
+    v.key = job.src_key;
+    v.value = job.src_value;
+    return v;
+}
+
 __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& item, uint32_t h,
                                     uint32_t G, uint32_t QH, uint32_t c0, uint32_t c1,
-                                    uint32_t chunk_index, bool single_chunk, WaveTokens* tokens)
+                                    uint32_t chunk_index, bool single_chunk, WaveTokens* tokens, JobView const& jv)
 {
     uint32_t const lane = threadIdx.x & 63u;
     uint32_t const D = P.dim;
@@ -337,10 +449,21 @@ __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& 
             const uint16_t* hb = nullptr;
             if (page != nullptr) {
                 hb = page + head_block(P, cap, layer, h);
+                const uint16_t* krow = nullptr;   // contiguous K row when the job supplies the token
+                if (jv.active && page == page_base(P, jv.dst_kind, jv.dst_slot, pool_tokens(P, jv.dst_kind))) {
+                    if (pt == jv.dst_token) {
+                        krow = jv.key + static_cast<uint64_t>(h) * D;
+                        hb = jv.value + static_cast<uint64_t>(h) * D;
+                        cap = 0;
+                    } else if (pt < jv.cow_tokens) {
+                        hb = page_base(P, jv.cow_kind, jv.cow_slot, jv.cow_cap) + head_block(P, jv.cow_cap, layer, h);
+                        cap = jv.cow_cap;
+                    }
+                }
                 float dot = 0.0f;
                 for (uint32_t d = 0; d < D; ++d) {
-                    dot += __half2float(__ushort_as_half(qv[d]))
-                        * __half2float(__ushort_as_half(hb[k_offset(cap, D, pt, d)]));
+                    uint16_t const kc = krow != nullptr ? krow[d] : hb[k_offset(cap, D, pt, d)];
+                    dot += __half2float(__ushort_as_half(qv[d])) * __half2float(__ushort_as_half(kc));
                 }
                 s = dot * scale2;
             }
@@ -370,7 +493,10 @@ __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& 
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     uint32_t const d = lane + 64u * k;
-                    if (d < D) o[k] += pp * __half2float(__ushort_as_half(vb[v_offset(vc, D, vp, d)]));
+                    if (d < D) {
+                        uint16_t const vv = vc == 0 ? vb[d] : vb[v_offset(vc, D, vp, d)];
+                        o[k] += pp * __half2float(__ushort_as_half(vv));
+                    }
                 }
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -401,14 +527,17 @@ __device__ void decode_wave_generic(const PoolView& P, const kimkv_decode_item& 
     }
 }
 
-// The per-lane conditions decode_kernel checks before touching a lane (the
-// merge skips the same lanes, so a rejected lane's output stays unwritten).
+// The per-lane conditions decode_kernel checks before touching a lane with
+// tokens (the merge skips the same lanes, so a rejected lane's output stays
+// unwritten).  `merged`: the launch runs the split-K merge (its chunk count
+// exceeds its lane count); without it a lane of several chunks would never
+// get its output.
 __device__ inline bool decode_item_valid(const PoolView& P, const kimkv_decode_item& item, uint32_t QH,
-                                         uint32_t nchunks)
+                                         uint32_t nchunks, bool merged)
 {
     return item.token_count != 0 && item.descriptors != nullptr && item.descriptor_count != 0
         && item.query != nullptr && item.output != nullptr && item.layer < P.layers && QH != 0
-        && QH % P.heads == 0 && P.dim <= 256 && (nchunks <= 1 || item.workspace != nullptr);
+        && QH % P.heads == 0 && P.dim <= 256 && (nchunks <= 1 || (item.workspace != nullptr && merged));
 }
 
 // LDS of a decode workgroup: the chunk's group table (also the buffer the
@@ -419,18 +548,29 @@ struct DecodeLds {
     uint32_t idx0;
     uint32_t dok;
     uint32_t generic;
+    uint32_t new_ok;   // the chunk reads the write job's new token as its last token
 };
 
 // Builds the group table of tokens [c0, c1) of `item` (c0 a multiple of 8)
 // and returns whether the fast path applies (head_dim 64, group <= 16, every
-// 8-token group mapped and aligned).  Called by every thread of the block.
+// 8-token group mapped and aligned).  With an active write job, groups of
+// its destination page below the copied count are read from the
+// copy-on-write source page instead, and lds.new_ok says whether the chunk's
+// last token is the job's new token (read from the job's rows by the fast
+// path); a table the fast path cannot read that way (the destination
+// position of the new token read as another token, a group mixing copied
+// and kept positions) goes to the generic path, which applies the same rule
+// per token.  Called by every thread of the block.
 __device__ bool build_chunk_table(const PoolView& P, const kimkv_decode_item& item, uint32_t QH, uint32_t c0,
-                                  uint32_t c1, DecodeLds& lds)
+                                  uint32_t c1, DecodeLds& lds, JobView const& jv)
 {
     uint32_t const tid = threadIdx.x;
     uint32_t const T = item.token_count;
     uint32_t const ngroups = (c1 - c0 + 7) / 8;
-    if (tid == 0) lds.generic = 0;
+    if (tid == 0) {
+        lds.generic = 0;
+        lds.new_ok = 0;
+    }
     for (uint32_t g = tid; g < ngroups; g += kBlock) {
         lds.groups[g] = GroupEntry{kUnmappedGroup, 0, 0};
     }
@@ -466,9 +606,30 @@ __device__ bool build_chunk_table(const PoolView& P, const kimkv_decode_item& it
     // The fast path loads full steps without per-group checks: a chunk with
     // an unmapped 8-token group goes to the generic path, which skips
     // unmapped tokens.
-    bool hole = false;
-    for (uint32_t g = tid; g < ngroups; g += kBlock) hole |= lds.groups[g].page == kUnmappedGroup;
-    if (hole) lds.generic = 1;
+    bool generic = false;
+    for (uint32_t g = tid; g < ngroups; g += kBlock) {
+        GroupEntry const e = lds.groups[g];
+        generic |= e.page == kUnmappedGroup;
+        if (!jv.active || e.page != jv.dst_tag) continue;
+        uint32_t const rel = jv.dst_token - e.pt0;   // the new token's place in the group, if < 8
+        if (rel < 8u) {
+            if (c0 + 8 * g + rel == T - 1) {
+                lds.new_ok = 1;
+            } else {
+                generic = true;
+            }
+        }
+        if (jv.cow_tokens != 0 && e.pt0 < jv.cow_tokens) {
+            // Positions past the copied ones are the new token or past it
+            // (tokens >= T, masked) when cow_tokens == dst_token.
+            if ((e.pt0 + 8u <= jv.cow_tokens || jv.cow_tokens == jv.dst_token) && (jv.cow_cap & 7u) == 0) {
+                lds.groups[g] = GroupEntry{jv.cow_tag, e.pt0, static_cast<uint16_t>(jv.cow_cap)};
+            } else {
+                generic = true;
+            }
+        }
+    }
+    if (generic) lds.generic = 1;
     __syncthreads();
     uint32_t const G = QH / P.heads;
     return P.dim == 64 && G <= 16 && lds.generic == 0;
@@ -480,16 +641,27 @@ __device__ bool build_chunk_table(const PoolView& P, const kimkv_decode_item& it
 // partial written.  Called by every thread of the block after
 // build_chunk_table; ends with the merge buffer still in use (callers that
 // reuse the LDS synchronize first).
+// The new-token rows kv head h of a fast-path chunk reads (kNoToken when the
+// chunk's last token is not the write job's new token).
+__device__ inline NewTokenRows new_token_rows(const DecodeLds& lds, JobView const& jv, uint32_t T, uint32_t h,
+                                              uint32_t D)
+{
+    if (lds.new_ok == 0) return NewTokenRows{nullptr, nullptr, kNoToken};
+    return NewTokenRows{jv.key + static_cast<uint64_t>(h) * D, jv.value + static_cast<uint64_t>(h) * D, T - 1};
+}
+
 template <bool kStream>
 __device__ void decode_head_split_chunk(const PoolView& P, const kimkv_decode_item& item, uint32_t h, uint32_t QH,
                                         uint32_t c0, uint32_t c1, uint32_t chunk_index, bool single, bool fast,
-                                        DecodeLds& lds)
+                                        DecodeLds& lds, JobView const& jv)
 {
     uint32_t const tid = threadIdx.x;
     uint32_t const wave = tid >> 6;
     uint32_t const G = QH / P.heads;
     if (!fast) {
-        if (wave == 0) decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &lds.wave_tokens[0]);
+        if (wave == 0) {
+            decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &lds.wave_tokens[0], jv);
+        }
         return;
     }
     uint32_t const quarter = ((c1 - c0 + 3) / 4 + 63) / 64 * 64;
@@ -497,7 +669,8 @@ __device__ void decode_head_split_chunk(const PoolView& P, const kimkv_decode_it
     uint32_t const s1 = min(s0 + quarter, c1);
     WavePartial w;
     if (s0 < s1) {
-        w = decode_wave_d64<kStream>(lds.groups, GroupResolver(P, item.layer, h), item, h, G, c0, s0, s1);
+        w = decode_wave_d64<kStream>(lds.groups, GroupResolver(P, item.layer, h), item, h, G, c0, s0, s1,
+                                     new_token_rows(lds, jv, item.token_count, h, 64));
     } else {
 #pragma unroll
         for (uint32_t db = 0; db < 4; ++db) w.acc[db] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -542,32 +715,23 @@ __device__ void decode_head_split_chunk(const PoolView& P, const kimkv_decode_it
     store_partial(item, QH, h * G + r, chunk_index, single, o, d0, M, den, d0 == 0);
 }
 
-// The lane's new token for kv heads [h0, h1) of `layer`, written by the
-// workgroup whose chunk holds it (a write job of
-// kimkv_paged_decode_write_batch: one token, one layer, source rows [H][D]),
-// the copy-on-write of a replaced partial tail included.  Every thread of
-// the workgroup calls it; it issues the stores and returns without waiting:
-// the caller makes every thread wait for its stores (s_waitcnt) and then
-// synchronizes the workgroup before the first load of the page.  Only this
-// workgroup reads these heads of the page in this launch (the other chunks
-// end before the tail page, other heads are other blocks).  False when the
-// job does not name a page of this storage.
-__device__ bool write_token_heads(const PoolView& P, const kimkv_append_job& job, uint32_t layer, uint32_t h0,
+// Stores the lane's new token for kv heads [h0, h1) of `layer` (a job that
+// write_job_valid accepted: one token, one layer, source rows [H][D]), the
+// copy-on-write of a replaced partial tail included.  Made by the workgroup
+// whose chunk holds the lane's last token, after its own reads: no read of
+// the launch takes these positions from the destination page (JobView), so
+// nothing waits for the stores.  Every thread of the workgroup calls it.
+__device__ void write_token_heads(const PoolView& P, const kimkv_append_job& job, uint32_t layer, uint32_t h0,
                                   uint32_t h1)
 {
     uint32_t const D = P.dim;
     uint32_t const dcap = pool_tokens(P, job.dst_kind);
     uint16_t* dst = page_base(P, job.dst_kind, job.dst_slot, dcap);
-    if (dst == nullptr || job.token_count != 1 || job.layer_count != 1 || job.layer_begin != layer
-        || layer >= P.layers || job.dst_token >= dcap || job.src_key == nullptr || job.src_value == nullptr) {
-        return false;
-    }
     uint32_t const tid = threadIdx.x;
     uint32_t const n = job.cow_tokens;
     if (n != 0) {
         uint32_t const scap = pool_tokens(P, job.cow_kind);
         uint16_t const* src = page_base(P, job.cow_kind, job.cow_slot, scap);
-        if (src == nullptr || n > scap || n > job.dst_token) return false;
         uint32_t const per_head = n * D;
         for (uint32_t i = tid; i < (h1 - h0) * per_head; i += kBlock) {
             uint32_t const h = h0 + i / per_head;
@@ -587,14 +751,6 @@ __device__ bool write_token_heads(const PoolView& P, const kimkv_append_job& job
         dst[dh + k_offset(dcap, D, job.dst_token, d)] = job.src_key[h * D + d];
         dst[dh + v_offset(dcap, D, job.dst_token, d)] = job.src_value[h * D + d];
     }
-    return true;
-}
-
-// Completes write_token_heads: every thread's stores done, then a barrier.
-__device__ inline void written_token_visible()
-{
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
 }
 
 // What a lane's split-K merge needs, written by the decode launch's first
@@ -625,10 +781,16 @@ static_assert(sizeof(DecodeLaneSlot) == KIMKV_DECODE_LANE_SLOT_BYTES, "slot size
 // partials: when non-null, split-K partials of global chunk c go to
 // partials + c * QH * (D + 2) instead of the lanes' own workspaces.
 // writes: when non-null, lane i's new token (writes[i], token_count 0 for
-// none) is written first by the workgroups of the chunk that holds it.
+// none): every chunk reads the positions the job writes from the job's
+// sources, and the workgroups of the chunk that holds the lane's last token
+// store them after their reads.
 // kStream: non-temporal K/V loads (load_kv).
 // slots: when non-null, each lane's merge record (DecodeLaneSlot, tagged
 // `tag`) for the merge launch.
+// The grid has one workgroup per chunk (x) and head block (y); the merge
+// launch follows when gridDim.x > lane_count, and a lane of several chunks
+// in a launch without it is reported and skipped.  A lane of no tokens is
+// skipped (its output is not written), as the reference's batch kernel does.
 template <bool kSplit, bool kStream>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
     PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t chunk_tokens,
@@ -685,8 +847,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t const nchunks = prefix[lane + 1] - lane_first;
     if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(lane_first) * QH * (D + 2);
     uint32_t const T = item.token_count;
+    if (T == 0) return;
     uint32_t const c0 = chunk_index * chunk_tokens;
-    if (!decode_item_valid(P, item, QH, nchunks) || c0 >= T || chunk_tokens > kMaxChunk) {
+    // A lane's chunks must lie inside the launch (the merge reads them all).
+    if (!decode_item_valid(P, item, QH, nchunks, gridDim.x > lane_count) || c0 >= T || chunk_tokens > kMaxChunk
+        || prefix[lane + 1] > gridDim.x) {
         report_fault(P, KIMKV_FAULT_DECODE_ITEM);
         return;
     }
@@ -696,38 +861,40 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t const c1 = min(c0 + chunk_tokens, T);
     uint32_t const G = QH / H;
     bool const single = nchunks == 1;
-    // The chunk holding the lane's new token writes it first; its stores
-    // drain while the group table is built.
     uint32_t const wh0 = kSplit ? blockIdx.y : blockIdx.y * kHeadsPerBlock;
+    uint32_t const wh1 = kSplit ? wh0 + 1 : min(H, wh0 + kHeadsPerBlock);
+    bool const job_ok = job.token_count != 0 && write_job_valid(P, job, item.layer);
+    // The chunk holding the lane's last token stores the job's positions of
+    // its kv heads, after its reads.
     bool const writer = job.token_count != 0 && c1 == T && wh0 < H;
-    if (writer && !write_token_heads(P, job, item.layer, wh0, kSplit ? wh0 + 1 : min(H, wh0 + kHeadsPerBlock))) {
-        report_fault(P, KIMKV_FAULT_APPEND_JOB);
-    }
-    bool const fast = build_chunk_table(P, item, QH, c0, c1, lds);
-    if (writer) written_token_visible();
+    if (writer && !job_ok) report_fault(P, KIMKV_FAULT_APPEND_JOB);
+    JobView const jv = job_view(P, job, job_ok);
+    bool const fast = build_chunk_table(P, item, QH, c0, c1, lds, jv);
 
     uint32_t const wave = tid >> 6;
     if (!kSplit) {
         uint32_t const h = blockIdx.y * kHeadsPerBlock + wave;
-        if (h >= H) return;
-        if (!fast) {
-            decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &lds.wave_tokens[wave]);
-            return;
-        }
-        WavePartial const w = decode_wave_d64<kStream>(lds.groups, GroupResolver(P, item.layer, h), item, h, G, c0, c0, c1);
-        uint32_t const l = tid & 63u;
-        uint32_t const r = l & 15u;
-        if (r >= G) return;
+        if (h < H && !fast) {
+            decode_wave_generic(P, item, h, G, QH, c0, c1, chunk_index, single, &lds.wave_tokens[wave], jv);
+        } else if (h < H) {
+            WavePartial const w = decode_wave_d64<kStream>(lds.groups, GroupResolver(P, item.layer, h), item, h, G,
+                                                           c0, c0, c1, new_token_rows(lds, jv, T, h, 64));
+            uint32_t const l = tid & 63u;
+            uint32_t const r = l & 15u;
+            if (r < G) {
 #pragma unroll
-        for (uint32_t db = 0; db < 4; ++db) {
-            store_partial(item, QH, h * G + r, chunk_index, single, w.acc[db], db * 16 + 4 * (l >> 4), w.m, w.l,
-                          db == 0 && l < 16);
+                for (uint32_t db = 0; db < 4; ++db) {
+                    store_partial(item, QH, h * G + r, chunk_index, single, w.acc[db], db * 16 + 4 * (l >> 4), w.m,
+                                  w.l, db == 0 && l < 16);
+                }
+            }
         }
-        return;
+    } else if (blockIdx.y < H) {
+        decode_head_split_chunk<kStream>(P, item, blockIdx.y, QH, c0, c1, chunk_index, single, fast, lds, jv);
     }
-    uint32_t const h = blockIdx.y;
-    if (h >= H) return;
-    decode_head_split_chunk<kStream>(P, item, h, QH, c0, c1, chunk_index, single, fast, lds);
+    // The job is read again here rather than kept in registers across the
+    // streaming loop.
+    if (writer && job_ok) write_token_heads(P, writes[lane], item.layer, wh0, wh1);
 }
 
 // Slices of a lane of T tokens in the guided mode: at most six, and no more
@@ -758,8 +925,8 @@ __host__ __device__ inline uint32_t guided_edge(uint32_t T, uint32_t n, uint32_t
 // merge launch combines the slices.  The last workgroup to leave resets the
 // counter slot for the next launch that uses it.
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_guided_kernel(
-    PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t QH,
-    float* partials, uint32_t* counter, const kimkv_append_job* writes)
+    PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t total_chunks,
+    uint32_t QH, float* partials, uint32_t* counter, const kimkv_append_job* writes)
 {
     __shared__ DecodeLds lds;
     __shared__ uint32_t s_unit;
@@ -782,23 +949,23 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         uint32_t const h = pair - lane * H;
         kimkv_decode_item item = items[lane];
         uint32_t const T = item.token_count;
+        if (T == 0) continue;   // skipped, as in decode_kernel
         uint32_t const n = guided_slices(T, D);
         if (k >= n) continue;   // a short lane has fewer slices
         uint32_t const first = prefix[lane];
         if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(first) * QH * (D + 2);
         uint32_t const c0 = guided_edge(T, n, k);
         uint32_t const c1 = guided_edge(T, n, k + 1);
-        if (!decode_item_valid(P, item, QH, n) || prefix[lane + 1] - first != n || c1 - c0 > kMaxChunk) {
+        if (!decode_item_valid(P, item, QH, n, total_chunks > lane_count) || prefix[lane + 1] - first != n
+            || prefix[lane + 1] > total_chunks || c1 - c0 > kMaxChunk) {
             report_fault(P, KIMKV_FAULT_DECODE_ITEM);
             continue;
         }
-        if (writes != nullptr && c1 == T) {
-            kimkv_append_job const job = writes[lane];
-            if (job.token_count != 0) {
-                if (!write_token_heads(P, job, item.layer, h, h + 1)) report_fault(P, KIMKV_FAULT_APPEND_JOB);
-                written_token_visible();
-            }
-        }
+        kimkv_append_job const job = writes != nullptr ? writes[lane] : kimkv_append_job{};
+        bool const job_ok = job.token_count != 0 && write_job_valid(P, job, item.layer);
+        bool const writer = job.token_count != 0 && c1 == T;
+        if (writer && !job_ok) report_fault(P, KIMKV_FAULT_APPEND_JOB);
+        JobView const jv = job_view(P, job, job_ok);
         if (c0 >= c1) {
             // An empty slice still leaves its partial: weight zero in the merge.
             uint32_t const r = tid >> 4;
@@ -809,8 +976,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             }
             continue;
         }
-        bool const fast = build_chunk_table(P, item, QH, c0, c1, lds);
-        decode_head_split_chunk<true>(P, item, h, QH, c0, c1, k, n == 1, fast, lds);
+        bool const fast = build_chunk_table(P, item, QH, c0, c1, lds, jv);
+        decode_head_split_chunk<true>(P, item, h, QH, c0, c1, k, n == 1, fast, lds, jv);
+        // The last slice (never empty) stores the job's positions of head h.
+        if (writer && job_ok) write_token_heads(P, writes[lane], item.layer, h, h + 1);
         __syncthreads();   // the next unit rebuilds the table in the same LDS
     }
     if (tid == 0) {
@@ -834,9 +1003,9 @@ constexpr unsigned kCombineHeads = 4;
 // `tag` replace the items and the chunk prefix.
 template <uint32_t kDims>
 __global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(PoolView P, const kimkv_decode_item* items,
-                                                                    const uint32_t* prefix, uint32_t QH, uint32_t D,
-                                                                    float* partials, const DecodeLaneSlot* slots,
-                                                                    uint64_t tag)
+                                                                    const uint32_t* prefix, uint32_t total_chunks,
+                                                                    uint32_t QH, uint32_t D, float* partials,
+                                                                    const DecodeLaneSlot* slots, uint64_t tag)
 {
     constexpr uint32_t kBatch = 64 / kDims;   // partial rows held in registers at once
     uint32_t const lane = blockIdx.x;
@@ -855,10 +1024,10 @@ __global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(PoolView P,
         if (n <= 1) return;
     } else {
         n = prefix[lane + 1] - prefix[lane];
-        if (n <= 1) return;
+        if (n <= 1 || prefix[lane + 1] > total_chunks) return;   // decode_kernel reported the latter
         kimkv_decode_item item = items[lane];
         if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(prefix[lane]) * QH * (D + 2);
-        if (!decode_item_valid(P, item, QH, n)) return;   // decode_kernel reported it
+        if (!decode_item_valid(P, item, QH, n, true)) return;   // decode_kernel reported it
         output = item.output;
         workspace = item.workspace;
     }
@@ -989,6 +1158,24 @@ __global__ __launch_bounds__(64) void reference_attention_kernel(PoolView P, con
     }
 }
 
+// The work-counter slot of `stream` on this storage: the stream's own slot,
+// taken on its first guided launch.  False when every slot already belongs
+// to another stream.
+bool work_counter_slot(const kimkv_storage* storage, kimkv_stream_t stream, uint32_t* slot)
+{
+    std::lock_guard<std::mutex> lock(storage->work_counter_mutex);
+    for (uint32_t i = 0; i < storage->work_counter_owners; ++i) {
+        if (storage->work_counter_stream[i] == stream) {
+            *slot = i;
+            return true;
+        }
+    }
+    if (storage->work_counter_owners == kWorkCounterSlots) return false;
+    *slot = storage->work_counter_owners++;
+    storage->work_counter_stream[*slot] = stream;
+    return true;
+}
+
 // Decode launch (+ split-K merge) shared by both entry points.  `partials`
 // replaces the lanes' workspaces when non-null; `timed` lets the benchmark's
 // event timing see the launch (its events are created on demand).
@@ -1018,15 +1205,17 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
     // several storages still never matches another launch's records.
     static std::atomic<uint64_t> next_tag{1};
     uint64_t const tag = slots != nullptr ? next_tag.fetch_add(1, std::memory_order_relaxed) : 0;
+    uint32_t slot = 0;
+    if (guided && !work_counter_slot(storage, stream, &slot)) return KIMKV_INVALID_ARGUMENT;
     void* start = nullptr;
     if (timed) kernel_timing_begin(TimedKernel::Decode, s, &start);
     if (guided) {
-        uint32_t const slot = storage->next_work_counter.fetch_add(1, std::memory_order_relaxed) % kWorkCounterSlots;
         uint32_t* counter = storage->work_counters + static_cast<size_t>(slot) * kWorkCounterStride;
         uint64_t const resident = 2ull * (storage->compute_units > 0 ? storage->compute_units : 256);
         auto const workers = static_cast<uint32_t>(units < resident ? units : resident);
         decode_guided_kernel<<<workers, kBlock, 0, s>>>(pool_view(*storage), device_items, device_chunk_prefix,
-                                                         lane_count, query_heads, partials, counter, writes);
+                                                         lane_count, total_chunks, query_heads, partials, counter,
+                                                         writes);
     } else {
         // Streamed K/V loads for long chunks (a workgroup streams at least
         // 2048 tokens) or more than one round of resident workgroups (two
@@ -1056,16 +1245,16 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
         uint32_t const D = storage->layout.head_dim;
         if (D <= 64) {
             combine_kernel<1><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
-                                                                     device_chunk_prefix, query_heads, D,
-                                                                     partials, slots, tag);
+                                                                     device_chunk_prefix, total_chunks,
+                                                                     query_heads, D, partials, slots, tag);
         } else if (D <= 128) {
             combine_kernel<2><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
-                                                                     device_chunk_prefix, query_heads, D,
-                                                                     partials, slots, tag);
+                                                                     device_chunk_prefix, total_chunks,
+                                                                     query_heads, D, partials, slots, tag);
         } else {
             combine_kernel<4><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
-                                                                     device_chunk_prefix, query_heads, D,
-                                                                     partials, slots, tag);
+                                                                     device_chunk_prefix, total_chunks,
+                                                                     query_heads, D, partials, slots, tag);
         }
         return launch_status();
     }
@@ -1157,10 +1346,13 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
     }
     target = (target + 63) / 64 * 64;
     if (target < kMinChunk) target = kMinChunk;
+    // Every lane gets at least one chunk (a lane of no tokens is one skipped
+    // workgroup), so a launch has more chunks than lanes exactly when some
+    // lane is split and needs the merge launch.
     uint64_t acc = 0;
     chunk_prefix[0] = 0;
     for (uint32_t i = 0; i < lane_count; ++i) {
-        acc += (token_counts[i] + target - 1) / target;
+        acc += token_counts[i] == 0 ? 1u : (token_counts[i] + target - 1) / target;
         if (acc > 0x7FFFFFFFu) return KIMKV_INVALID_ARGUMENT;
         chunk_prefix[i + 1] = static_cast<uint32_t>(acc);
     }
@@ -1174,6 +1366,7 @@ uint32_t kimkv_decode_lane_chunks(uint32_t token_count, uint32_t chunk_tokens, u
     if ((chunk_tokens & KIMKV_DECODE_GUIDED) != 0) return guided_slices(token_count, head_dim);
     chunk_tokens &= ~(KIMKV_DECODE_HEAD_SPLIT | KIMKV_DECODE_GUIDED);
     if (chunk_tokens == 0) return 0;
+    if (token_count == 0) return 1;
     return static_cast<uint32_t>((static_cast<uint64_t>(token_count) + chunk_tokens - 1) / chunk_tokens);
 }
 
@@ -1226,7 +1419,9 @@ kimkv_status kimkv_paged_decode_batch_noalloc(const kimkv_storage* storage, cons
                                               kimkv_stream_t stream)
 {
     if (storage == nullptr || query_heads == 0) return KIMKV_INVALID_ARGUMENT;
-    // Partials are needed only when some lane has several chunks.
+    // Partials are written only when the launch has more chunks than lanes
+    // (the kernel refuses a split lane in any other launch), and then within
+    // the first total_chunks partial rows.
     uint64_t const need = static_cast<uint64_t>(total_chunks) * query_heads * (storage->layout.head_dim + 2)
         * sizeof(float);
     if (total_chunks > lane_count && need > KIMKV_DECODE_SCRATCH_BYTES) return KIMKV_INVALID_ARGUMENT;

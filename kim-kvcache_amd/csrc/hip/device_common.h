@@ -10,12 +10,15 @@
 
 #include <atomic>
 #include <cstdint>
+#include <mutex>
 
 #include "kimkv_hip.h"
 
-// Work-counter slots of persistent launches: a launch takes the next slot
-// round-robin and its last workgroup resets it, so a slot is reused only
-// after that many later launches (in-order streams never overlap on one).
+// Work-counter slots of persistent launches: each stream that makes such a
+// launch on a storage owns one slot for the storage's lifetime, and a
+// launch's last workgroup resets its slot.  Launches on one stream run in
+// order, so the next launch on that stream finds the slot cleared, and
+// launches on different streams never share a slot.
 constexpr uint32_t kWorkCounterSlots = 64;
 constexpr uint32_t kWorkCounterStride = 64;   // words: one slot per 256-byte line
 
@@ -31,7 +34,9 @@ struct kimkv_storage {
     uint16_t* extent{nullptr};
     uint32_t* faults{nullptr};        // device word, KIMKV_FAULT_* bits
     uint32_t* work_counters{nullptr}; // kWorkCounterSlots slots of kWorkCounterStride words
-    mutable std::atomic<uint32_t> next_work_counter{0};
+    mutable std::mutex work_counter_mutex;
+    mutable void* work_counter_stream[kWorkCounterSlots]{};   // slot owners
+    mutable uint32_t work_counter_owners{0};
     uint32_t* fault_host{nullptr};    // mapped pinned word kimkv_storage_faults reads
     uint32_t* fault_view{nullptr};    // its device address
     int device{0};

@@ -267,7 +267,8 @@ def _write_then_decode(dev, fused, tables, T, news, lanes_meta, QH, chunk, shape
         else:
             new_slot = micro_cap - 1 - i
             j["dst_slot"], j["dst_token"] = new_slot, 0
-            t = np.concatenate([t, np.array([(new_slot, 1, T[i], 1, 8, 0)], dtype=t.dtype)])
+            # (np.concatenate drops the descriptor's padding: convert back to the 20-byte layout)
+            t = np.concatenate([t, np.array([(new_slot, 1, T[i], 1, 8, 0)], dtype=t.dtype)]).astype(helpers.DESC)
         ext_tables.append(t)
     lanes = []
     for i, t in enumerate(ext_tables):
@@ -346,6 +347,248 @@ def test_decode_write_batch_matches_append_then_decode(dev, mode):
         assert np.array_equal(pa[i], pc[i]), (mode, i)
         assert np.array_equal(a[i], c[i]), (mode, i)
     print(f"decode+write mode={mode} lanes={len(T)} chunks={total}", flush=True)
+
+
+def _fused_case(dev, shape, lanes, chunk, micro_tokens=8, extent_tokens=64, seed=70, QH=None):
+    """Write-and-decode launches against the oracle and against append-then-decode, with explicit jobs.
+
+    lanes: (table before, mode, layer) with mode "tail" (the new token goes into the tail page),
+    "cow" (the tail's valid tokens are copied into a fresh page of the tail's kind, the new token
+    after them), ("cow_short", n) (only the first n tokens copied, the new token still after the
+    tail's valid count) or "fresh" (a new micro page).  Pages must match the oracle's bit for bit and
+    outputs the oracle within tolerance; outputs must also equal append-then-decode bit for bit,
+    except for "cow_short" lanes, whose fused chunk holding the destination page takes the generic
+    path (kept and copied positions share an 8-token group) while append-then-decode reads the
+    written page on the fast path.  Returns the worst error against the oracle."""
+    L, H, D = shape
+    QH = QH or 8 * H
+    cap = {helpers.MICRO: micro_tokens, helpers.EXTENT: extent_tokens}
+    used = {helpers.MICRO: set(), helpers.EXTENT: set()}
+    for table, _, _ in lanes:
+        for e in table:
+            used[int(e["kind"])].add(int(e["slot"]))
+    micro_cap = max(used[helpers.MICRO] | {0}) + len(lanes) + 4
+    ext_cap = max(used[helpers.EXTENT] | {0}) + len(lanes) + 4
+    spare = {helpers.MICRO: [s for s in range(micro_cap) if s not in used[helpers.MICRO]],
+             helpers.EXTENT: [s for s in range(ext_cap) if s not in used[helpers.EXTENT]]}
+    news = oracle.synth_rows(len(lanes) * 2 * H * D, seed + 1, 0, D).reshape(len(lanes), 2, H, D)
+    plans = []
+    for i, (table, mode, layer) in enumerate(lanes):
+        T = int(table[-1]["logical_token_begin"]) + int(table[-1]["valid_tokens"])
+        tail = table[-1]
+        kind, valid = int(tail["kind"]), int(tail["valid_tokens"])
+        after = table.copy()
+        job = dict(dst_kind=helpers.MICRO, dst_slot=0, dst_token=0, cow_kind=0, cow_slot=0, cow_tokens=0)
+        if mode == "tail":
+            assert valid < cap[kind]
+            job.update(dst_kind=kind, dst_slot=int(tail["slot"]), dst_token=valid)
+            after[-1]["valid_tokens"] += 1
+        elif mode == "fresh":
+            slot = spare[helpers.MICRO].pop()
+            job.update(dst_kind=helpers.MICRO, dst_slot=slot)
+            after = np.concatenate([after, np.array([(slot, 1, T, 1, micro_tokens, helpers.MICRO)],
+                                                    dtype=after.dtype)]).astype(helpers.DESC)
+        else:
+            assert valid < cap[kind]
+            n = valid if mode == "cow" else mode[1]
+            slot = spare[kind].pop()
+            job.update(dst_kind=kind, dst_slot=slot, dst_token=valid, cow_kind=kind, cow_slot=int(tail["slot"]),
+                       cow_tokens=n)
+            after[-1]["slot"] = slot
+            after[-1]["valid_tokens"] += 1
+        plans.append((table, after, T, layer, job))
+
+    def run(fused):
+        storage = dev.Storage(L, H, D, micro_cap, ext_cap, micro_tokens, extent_tokens)
+        pools = oracle.HostPools(L, H, D, micro_cap, ext_cap, micro_tokens, extent_tokens)
+        keep = []
+        for i, (table, _, T, _, _) in enumerate(plans):
+            keep.append(_populate(dev, storage, pools, table, _input(L, H, D, T, seed=seed * 100 + i)))
+        src = dev.upload(news)
+        jobs = np.zeros(len(plans), dtype=dev.APPEND_JOB)
+        for i, (_, _, _, layer, job) in enumerate(plans):
+            j = jobs[i]
+            j["src_key"] = src.ptr + 2 * (i * 2) * H * D
+            j["src_value"] = src.ptr + 2 * (i * 2 + 1) * H * D
+            j["layer_begin"], j["layer_count"], j["token_count"] = layer, 1, 1
+            for k, v in job.items():
+                j[k] = v
+            if job["cow_tokens"]:
+                pools.copy_layer_tokens(job["cow_kind"], job["cow_slot"], job["dst_kind"], job["dst_slot"],
+                                        job["cow_tokens"], layer)
+            pools.write_layer_token(job["dst_kind"], job["dst_slot"], job["dst_token"], layer, news[i, 0], news[i, 1])
+        counts = [T + 1 for (_, _, T, _, _) in plans]
+        prefix = dev.chunk_prefix(counts, chunk, D)
+        total = int(prefix[-1])
+        items = np.zeros(len(plans), dtype=dev.DECODE_ITEM)
+        outs, wants = [], []
+        for i, (_, after, T, layer, _) in enumerate(plans):
+            q = oracle.synth_rows(QH * D, seed * 1000 + i, 0, D)
+            dbuf, qbuf = dev.upload(after), dev.upload(q)
+            obuf = dev.DeviceBuffer(QH * D * 2)
+            wsz = dev.workspace_bytes(T + 1, chunk, QH, D)
+            wbuf = dev.DeviceBuffer(max(wsz, 4))
+            items[i] = (dbuf.ptr, len(after), T + 1, layer, qbuf.ptr, wbuf.ptr if wsz else 0, obuf.ptr, 0.125)
+            keep += [dbuf, qbuf, wbuf]
+            outs.append(obuf)
+            wants.append(pools.paged_decode(after, T + 1, layer, QH, q, 0.125, f32=True))
+        ibuf, pbuf, jbuf = dev.upload(items), dev.upload(prefix), dev.upload(jobs)
+        if fused:
+            storage.decode_write_launch(ibuf.ptr, pbuf.ptr, len(plans), total, chunk, QH, jbuf.ptr)
+        else:
+            storage.append_batch(jobs)
+            storage.decode_launch(ibuf.ptr, pbuf.ptr, len(plans), total, chunk, QH)
+        dev.sync()
+        assert storage.faults() == (0, 0)
+        got = [dev.download(o.ptr, (QH * D,), np.uint16) for o in outs]
+        pages = [storage.gather(after, T + 1) for (_, after, T, _, _) in plans]
+        want_pages = [pools.gather(after, T + 1) for (_, after, T, _, _) in plans]
+        return got, pages, wants, want_pages, total
+
+    a, pa, wants, want_pages, total = run(False)
+    b, pb, _, _, _ = run(True)
+    worst = 0.0
+    for i, (_, mode, _) in enumerate(lanes):
+        assert np.array_equal(pb[i], want_pages[i]), i
+        assert np.array_equal(pa[i], pb[i]), i
+        helpers.assert_attention_close(a[i], wants[i])
+        if not isinstance(mode, tuple):
+            assert np.array_equal(a[i], b[i]), i
+        worst = max(worst, helpers.assert_attention_close(b[i], wants[i]))
+    print(f"fused write+decode chunk={chunk & 0x3FFFFFFF} mode={dev.decode_mode(chunk)} chunks={total} "
+          f"pages={micro_tokens}/{extent_tokens} max_err={worst:.2e}", flush=True)
+    return worst
+
+
+@pytest.mark.parametrize("mode", ["four_heads", "head_split", "guided"])
+def test_decode_write_batch_unaligned_pages_cow_across_chunks(dev, mode):
+    """6-token micro / 48-token extent pages (not 8-aligned: the generic path): copy-on-write tails
+    that start in one chunk and end in the next (tokens [252, 258) with 256-token chunks), so the
+    earlier chunk's workgroup reads copied positions while the later one stores them.  Every chunk
+    takes copied positions from the source page and the new token from the job's rows, so the
+    fused launch equals append-then-decode bit for bit and the oracle within tolerance."""
+    shape = (2, 4, 64)
+    alloc = helpers.SlotAllocator(400, 8, seed=71, micro_tokens=6, extent_tokens=48)
+    lanes = [(helpers.uniform_table(257, 6, alloc), "cow", 1),      # tail [252, 257): crosses 256
+             (helpers.uniform_table(250, 6, alloc), "cow", 0),
+             (helpers.uniform_table(253, 6, alloc), "tail", 1),
+             (helpers.uniform_table(511, 6, alloc), "tail", 0),     # tail [510, 511)
+             (helpers.uniform_table(300, 6, alloc), "fresh", 1),
+             (helpers.uniform_table(515, 6, alloc), ("cow_short", 2), 0)]
+    chunk = {"four_heads": 256, "head_split": 256 | dev.DECODE_HEAD_SPLIT, "guided": dev.DECODE_GUIDED | 64}[mode]
+    _fused_case(dev, shape, lanes, chunk, micro_tokens=6, extent_tokens=48)
+
+
+@pytest.mark.parametrize("mode", ["four_heads", "head_split"])
+def test_decode_write_batch_fast_path_redirects(dev, mode):
+    """8/64-token pages (fast path): an extent tail at token 8 (not 64-aligned) copied on write across
+    a chunk boundary (chunk 0 reads copied positions of the destination from the source page), a
+    micro copy-on-write tail, copies shorter than the tail (generic path), a new token that lands on
+    a full 64-token step, and plain tail writes; fused equals append-then-decode bit for bit."""
+    shape = (3, 4, 64)
+    alloc = helpers.SlotAllocator(200, 64, seed=72)
+
+    def ext_at_8(valid):
+        return np.array([(alloc.take(helpers.MICRO), 1, 0, 8, 8, helpers.MICRO),
+                         (alloc.take(helpers.EXTENT), 1, 8, valid, 64, helpers.EXTENT)], dtype=helpers.DESC)
+
+    lanes = [(ext_at_8(60), "cow", 2),                          # extent [8, 68) -> copy; new token 68
+             (ext_at_8(30), "cow", 1),
+             (ext_at_8(55), "tail", 0),
+             (helpers.hetero_table(127, alloc), "tail", 1),     # new token 127: last of a full step
+             (helpers.hetero_table(1003, alloc), "cow", 2),         # micro tail [1000, 1003)
+             (helpers.hetero_table(1005, alloc), ("cow_short", 1), 0),
+             (helpers.hetero_table(512, alloc), "fresh", 1),
+             (helpers.hetero_table(64 * 5 + 6, alloc), "cow", 0)]
+    chunk = {"four_heads": 64, "head_split": 64 | dev.DECODE_HEAD_SPLIT}[mode]
+    _fused_case(dev, shape, lanes, chunk)
+    _fused_case(dev, shape, lanes, chunk + 192)
+
+
+def test_decode_zero_token_lane_beside_split_lane(dev):
+    """A lane of no tokens gets one (skipped) chunk from the planner, so a batch of lanes [0, 300]
+    still runs the split-K merge for the 300-token lane, through kimkv_paged_decode_batch and the
+    no-alloc entry point; the empty lane's output is left untouched.  A prefix that gives the empty
+    lane no chunk ([0, 0, 2]: as many chunks as lanes) would skip the merge: the split lane is then
+    reported and skipped instead of left unmerged, and nothing is written past the chunks."""
+    import ctypes
+    L, H, D, G = 1, 4, 64, 8
+    QH = H * G
+    storage = dev.Storage(L, H, D, 64, 16)
+    pools = oracle.HostPools(L, H, D, 64, 16)
+    alloc = helpers.SlotAllocator(64, 16, seed=73)
+    table = helpers.hetero_table(300, alloc)
+    keep = [_populate(dev, storage, pools, table, _input(L, H, D, 300, seed=74))]
+    q = oracle.synth_rows(QH * D, 75, 0, D)
+    want = pools.paged_decode(table, 300, 0, QH, q, 0.125, f32=True)
+    chunk = 256
+    prefix = dev.chunk_prefix([0, 300], chunk, D)
+    assert list(prefix) == [0, 1, 3]
+    flags, planned, total = storage.decode_plan([0, 300], QH)
+    assert planned[1] == 1 and total == planned[2] and total > 2
+    dbuf, qbuf = dev.upload(table), dev.upload(q)
+    sentinel = np.full(QH * D, 0x7E00, dtype=np.uint16)
+    lib = dev.lib()
+    for noalloc in (False, True):
+        outs = [dev.upload(sentinel), dev.upload(sentinel)]
+        ws = dev.DeviceBuffer(dev.workspace_bytes(300, chunk, QH, D))
+        items = np.zeros(2, dtype=dev.DECODE_ITEM)
+        items[0] = (dbuf.ptr, len(table), 0, 0, qbuf.ptr, 0, outs[0].ptr, 0.125)
+        items[1] = (dbuf.ptr, len(table), 300, 0, qbuf.ptr, 0 if noalloc else ws.ptr, outs[1].ptr, 0.125)
+        ibuf, pbuf = dev.upload(items), dev.upload(prefix)
+        fn = lib.kimkv_paged_decode_batch_noalloc if noalloc else lib.kimkv_paged_decode_batch
+        print(f"zero-token lane: noalloc={noalloc} prefix={list(prefix)}", flush=True)
+        assert fn(storage.h, ctypes.c_void_p(ibuf.ptr), ctypes.c_void_p(pbuf.ptr), 2, 3, chunk, QH, None) == 0
+        dev.sync()
+        assert storage.faults() == (0, 0)
+        assert np.array_equal(dev.download(outs[0].ptr, (QH * D,), np.uint16), sentinel)
+        helpers.assert_attention_close(dev.download(outs[1].ptr, (QH * D,), np.uint16), want)
+        # The inconsistent plan: no chunk for the empty lane, two for the other.
+        bad = np.array([0, 0, 2], dtype=np.uint32)
+        out2 = dev.upload(sentinel)
+        items[1]["output"] = out2.ptr
+        ibuf2, pbuf2 = dev.upload(items), dev.upload(bad)
+        assert fn(storage.h, ctypes.c_void_p(ibuf2.ptr), ctypes.c_void_p(pbuf2.ptr), 2, 2, chunk, QH, None) == 0
+        dev.sync()
+        assert storage.faults() == (1, dev.FAULT_DECODE_ITEM)
+        assert np.array_equal(dev.download(out2.ptr, (QH * D,), np.uint16), sentinel)
+        keep += [ws, ibuf, pbuf, ibuf2, pbuf2, out2] + outs
+    del keep
+
+
+def test_decode_guided_streams_own_counter_slots(dev):
+    """Guided launches take the work-counter slot of their stream: interleaved launches on several
+    streams stay correct, and a storage refuses a guided launch from a 65th distinct stream (no slot
+    left) without launching, while streams that own a slot keep working."""
+    L, H, D, G = 1, 4, 64, 8
+    QH = H * G
+    storage = dev.Storage(L, H, D, 256, 64)
+    pools = oracle.HostPools(L, H, D, 256, 64)
+    alloc = helpers.SlotAllocator(256, 64, seed=76)
+    lanes, keep = [], []
+    for i, T in enumerate([700, 2000, 90]):
+        table = helpers.hetero_table(T, alloc)
+        keep.append(_populate(dev, storage, pools, table, _input(L, H, D, T, seed=77 + i)))
+        lanes.append((table, T, 0, oracle.synth_rows(QH * D, 80 + i, 0, D), 0.125))
+    wants = [pools.paged_decode(t, T, 0, QH, q, s, f32=True) for (t, T, _, q, s) in lanes]
+    GU = dev.DECODE_GUIDED | 64
+    streams = [dev.Stream() for _ in range(64)]
+    for rnd in range(2):
+        for k, st in enumerate(streams):
+            if rnd == 1 and k % 8 != 0:
+                continue
+            outs, _, _ = _run_decode(dev, storage, lanes, QH, stream=st, chunk=GU)
+            for got, want in zip(outs, wants):
+                helpers.assert_attention_close(got, want)
+    extra = dev.Stream()
+    with pytest.raises(dev.KimkvError):
+        _run_decode(dev, storage, lanes, QH, stream=extra, chunk=GU)
+    outs, _, _ = _run_decode(dev, storage, lanes, QH, stream=streams[5], chunk=GU)
+    for got, want in zip(outs, wants):
+        helpers.assert_attention_close(got, want)
+    for st in streams + [extra]:
+        st.destroy()
+    del keep
 
 
 def test_decode_config1_tinyllama(dev):
