@@ -279,20 +279,30 @@ kimkv_status kimkv_patch_descriptors(const kimkv_descriptor_patch* patches, uint
  * (slice, lane, KV head) units from a device counter, longest slices first,
  * and the merge launch combines each lane's slices (a one-slice lane is
  * written directly).  The other bits are ignored in this mode; a lane's
- * chunk count is kimkv_decode_lane_chunks. */
+ * chunk count is kimkv_decode_lane_chunks.  The counter belongs to the
+ * launch's stream (one of 64 per storage, taken on the stream's first guided
+ * launch and kept for the storage's lifetime): guided launches on one stream
+ * run in order and never share a counter with another stream's; a guided
+ * launch from a 65th stream returns KIMKV_INVALID_ARGUMENT. */
 #define KIMKV_DECODE_GUIDED 0x40000000u
 #define KIMKV_DECODE_GUIDED_SLICES 6u
 
 /* Chunks (split-K partial slots) of a lane of token_count tokens under a
  * planned chunk_tokens value (flags included): the chunk prefix of a launch
- * is the running sum of this over its lanes. */
+ * is the running sum of this over its lanes.  A lane of no tokens has one
+ * chunk (a workgroup that skips it), so a launch has more chunks than lanes
+ * exactly when some lane is split; the decode launches the split-K merge on
+ * that condition and reports (KIMKV_FAULT_DECODE_ITEM) a split lane in a
+ * launch with no more chunks than lanes. */
 uint32_t kimkv_decode_lane_chunks(uint32_t token_count, uint32_t chunk_tokens, uint32_t head_dim);
 
 /* Split-K planning for a ragged decode batch.  Given the lanes' token counts
  * (host array), picks the chunk length (a multiple of 64 tokens, 256..65536,
  * possibly with KIMKV_DECODE_HEAD_SPLIT set) and fills
- * chunk_prefix[0..lane_count] (host array) with the running chunk count.
- * Returns the total chunk count in *total_chunks. */
+ * chunk_prefix[0..lane_count] (host array) with the running chunk count
+ * (kimkv_decode_lane_chunks per lane).  Returns the total chunk count in
+ * *total_chunks.  A lane of no tokens is skipped by the decode (its output
+ * is not written), as the reference's batch kernel skips it. */
 kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* token_counts,
                                uint32_t lane_count, uint32_t query_heads,
                                uint32_t* chunk_tokens, uint32_t* chunk_prefix,
@@ -323,12 +333,19 @@ kimkv_status kimkv_paged_decode_batch(const kimkv_storage* storage,
  * launch: device_writes[i] (memory the device reads) is lane i's
  * single-token append job for this layer (token_count 1, layer_count 1,
  * layer_begin = the item's layer, source rows [kv_heads][head_dim], its
- * destination the lane's last table entry, optionally a copy-on-write
- * source), or token_count 0 for none; the workgroups whose chunk holds the
- * lane's last token write it (and the copy-on-write tokens) for their KV
- * heads before reading the page.  Equals kimkv_append_batch of the jobs
- * followed by kimkv_paged_decode_batch, in one launch.  No counterpart in
- * the reference, which launches writeLayer and attendLayer separately
+ * destination normally the lane's last table entry, optionally a
+ * copy-on-write source of cow_tokens <= dst_token tokens), or token_count 0
+ * for none.  Equals kimkv_append_batch of the jobs followed by
+ * kimkv_paged_decode_batch, in one launch: every read of a position the job
+ * writes takes it from the job's source (copied positions from the
+ * copy-on-write page, dst_token from the source rows), and the workgroups
+ * whose chunk holds the lane's last token store the job's positions for
+ * their KV heads after their reads, so no read waits for a store and a
+ * copied tail may span chunks (any page size).  Outputs are bit-identical to
+ * the two-launch form, except for a job copying fewer than dst_token tokens
+ * (then within the decode tolerance).  A page a job writes may be read, in
+ * the same launch, only by that job's own lane.  No counterpart in the
+ * reference, which launches writeLayer and attendLayer separately
  * (src/cuda/engine/transaction.cpp); the engine's batched token path uses it
  * for writeLayerBatch + attendLayerBatch of a layer.  A job that names no
  * page of the storage sets KIMKV_FAULT_APPEND_JOB and is skipped. */
@@ -366,8 +383,9 @@ kimkv_status kimkv_paged_decode_write_batch_slots(const kimkv_storage* storage,
  * hipMalloc).  No counterpart in the reference.  Same arguments, kernels and
  * results; the items' `workspace` pointers are ignored: split-K partials go
  * to a file-scope device array of KIMKV_DECODE_SCRATCH_BYTES bytes (one per
- * device, held until the process ends), which a batch needs only when some
- * lane has several chunks, then total_chunks * query_heads * (head_dim + 2)
+ * device, held until the process ends), which a batch needs only when it
+ * has more chunks than lanes (some lane is split; see
+ * kimkv_decode_lane_chunks), then total_chunks * query_heads * (head_dim + 2)
  * * 4 bytes of it (16 MiB = 1985 chunks at 32 query heads x 64 dims).
  * KIMKV_INVALID_ARGUMENT for a larger batch or when the storage's device is
  * not the current device; nothing is launched then.  Calls no allocating
