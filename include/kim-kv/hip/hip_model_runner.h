@@ -60,6 +60,16 @@ public:
     // position to host_logits ([spans.size()][vocabulary]) when non-null.
     GenerationBatchResult forwardSpans(std::vector<GenerationSpan> const& spans, float* host_logits);
 
+    // Observation hook with no counterpart in the reference (its runner tests
+    // compare generated tokens): after each forward -- the scheduler's
+    // included -- that holds a span of request ids[k], the fp32 logits after
+    // that span's last position are copied to rows + k * vocabulary,
+    // positions[k] is set to that position and counts[k] is incremented.
+    // The buffers are the caller's host memory and must stay valid while the
+    // watch lasts; an empty id list (or a null buffer) ends it.  Not thread
+    // safe, like the forward calls it observes.
+    void watchLogits(std::vector<RequestId> ids, float* rows, std::uint32_t* positions, std::uint32_t* counts);
+
     std::uint64_t deviceWeightBytes() const noexcept;
     std::uint64_t deviceWorkspaceBytes() const noexcept;
 

@@ -301,6 +301,15 @@ int kimkv_runner_forward(kimkv_runner* r, uint32_t span_count, const uint64_t* r
                          const uint32_t* first_positions, const uint32_t* token_counts, const uint32_t* tokens,
                          uint32_t* next_tokens, int* step_ok, float* logits);
 
+/* HipTinyLlamaRunner::watchLogits: after each forward (the scheduler's
+ * included) holding a span of request_ids[k], the fp32 logits after that
+ * span's last position go to rows + k * vocabulary, positions[k] gets that
+ * position and counts[k] is incremented.  Host buffers owned by the caller,
+ * valid while watched; count 0 ends the watch.  No counterpart in the
+ * reference.  Returns 0, or -1 for a null argument. */
+int kimkv_runner_watch_logits(kimkv_runner* r, uint32_t count, const uint64_t* request_ids, float* rows,
+                              uint32_t* positions, uint32_t* counts);
+
 /* IterationSchedulerConfig. */
 typedef struct kimkv_scheduler_config {
     uint32_t max_active_requests;

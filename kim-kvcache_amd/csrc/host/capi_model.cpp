@@ -99,6 +99,21 @@ int kimkv_runner_forward(kimkv_runner* r, uint32_t span_count, const uint64_t* r
     }
 }
 
+int kimkv_runner_watch_logits(kimkv_runner* r, uint32_t count, const uint64_t* request_ids, float* rows,
+                              uint32_t* positions, uint32_t* counts)
+{
+    if (r == nullptr || (count != 0 && (request_ids == nullptr || rows == nullptr || positions == nullptr
+                                        || counts == nullptr))) {
+        return -1;
+    }
+    try {
+        r->runner->watchLogits(std::vector<RequestId>(request_ids, request_ids + count), rows, positions, counts);
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
 kimkv_scheduler* kimkv_scheduler_create(kimkv_engine* e, kimkv_runner* r, const kimkv_scheduler_config* config)
 {
     if (e == nullptr || r == nullptr || config == nullptr) return nullptr;

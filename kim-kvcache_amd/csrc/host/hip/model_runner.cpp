@@ -88,6 +88,13 @@ struct HipTinyLlamaRunner::Impl {
     void* qkv_ready{nullptr};
     void* decode_done{nullptr};
 
+    // Watched requests (watchLogits): their spans' logits rows go to the
+    // caller's host buffers after each forward.
+    std::vector<RequestId> watch_ids;
+    float* watch_rows{nullptr};
+    std::uint32_t* watch_positions{nullptr};
+    std::uint32_t* watch_counts{nullptr};
+
     ~Impl()
     {
         if (decode_stream) {
@@ -526,6 +533,18 @@ GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSp
     if (ok && host_logits != nullptr) {
         ok = kimkv_memcpy_d2h_async(host_logits, logits, S * std::uint64_t{m.vocabulary_size} * 4, stream) == KIMKV_OK;
     }
+    // (watch slot, span) pairs of watched requests; rows copied here, the
+    // positions and counts set once the forward has succeeded.
+    std::vector<std::pair<std::size_t, std::size_t>> watched;
+    for (std::size_t i = 0; ok && i < S && !watch_ids.empty(); ++i) {
+        for (std::size_t k = 0; k < watch_ids.size(); ++k) {
+            if (watch_ids[k] != spans[i].request_id) continue;
+            watched.emplace_back(k, i);
+            ok = kimkv_memcpy_d2h_async(watch_rows + k * std::uint64_t{m.vocabulary_size},
+                                        logits + i * std::uint64_t{m.vocabulary_size},
+                                        std::uint64_t{m.vocabulary_size} * 4, stream) == KIMKV_OK;
+        }
+    }
 
     // Completion: commit / finish (each waits for its work), then the stream.
     for (std::size_t j = 0; j < dec.size(); ++j) {
@@ -550,6 +569,11 @@ GenerationBatchResult HipTinyLlamaRunner::Impl::forward(std::vector<GenerationSp
     }
     for (std::size_t i = 0; i < S; ++i) {
         if (steps[i].success) steps[i].greedy_token_id = tokens_out[i];
+    }
+    for (auto const& [k, i] : watched) {
+        if (!steps[i].success) continue;
+        watch_positions[k] = spans[i].first_position + static_cast<std::uint32_t>(spans[i].token_ids.size()) - 1;
+        ++watch_counts[k];
     }
     result.steps = std::move(steps);
     result.success = true;
@@ -668,6 +692,16 @@ GenerationBatchResult HipTinyLlamaRunner::generationForwardSpans(std::vector<Gen
 GenerationBatchResult HipTinyLlamaRunner::forwardSpans(std::vector<GenerationSpan> const& spans, float* host_logits)
 {
     return impl_->forward(spans, host_logits);
+}
+
+void HipTinyLlamaRunner::watchLogits(std::vector<RequestId> ids, float* rows, std::uint32_t* positions,
+                                     std::uint32_t* counts)
+{
+    bool const off = ids.empty() || rows == nullptr || positions == nullptr || counts == nullptr;
+    impl_->watch_ids = off ? std::vector<RequestId>{} : std::move(ids);
+    impl_->watch_rows = off ? nullptr : rows;
+    impl_->watch_positions = off ? nullptr : positions;
+    impl_->watch_counts = off ? nullptr : counts;
 }
 
 }  // namespace kimkvcache

@@ -148,6 +148,7 @@ _SIG = {
     "kimkv_runner_destroy": (None, [P]),
     "kimkv_runner_weight_bytes": (U64, [P]),
     "kimkv_runner_forward": (I, [P, U32, P, P, P, P, P, P, P]),
+    "kimkv_runner_watch_logits": (I, [P, U32, P, P, P, P]),
     "kimkv_scheduler_create": (P, [P, P, ctypes.POINTER(SchedulerConfig)]),
     "kimkv_scheduler_destroy": (None, [P]),
     "kimkv_scheduler_submit": (I, [P, U64, P, U32, U32, ctypes.c_int64]),
@@ -604,6 +605,22 @@ class Runner:
 
     def weight_bytes(self) -> int:
         return lib().kimkv_runner_weight_bytes(self.h)
+
+    def watch_logits(self, request_ids):
+        """kimkv_runner_watch_logits: returns (rows [n][vocabulary] fp32, positions [n], counts [n]), filled
+        after every forward that holds a span of request_ids[k]; watch_logits([]) ends the watch."""
+        import numpy as np
+        ids = np.ascontiguousarray(np.asarray(request_ids, dtype=np.uint64))
+        n = ids.size
+        rows = np.zeros((max(n, 1), self.model.vocabulary_size), dtype=np.float32)
+        positions = np.zeros(max(n, 1), dtype=np.uint32)
+        counts = np.zeros(max(n, 1), dtype=np.uint32)
+        self._watch = (ids, rows, positions, counts)     # kept alive while the library writes them
+        rc = lib().kimkv_runner_watch_logits(self.h, n, ids.ctypes.data if n else None, rows.ctypes.data,
+                                             positions.ctypes.data, counts.ctypes.data)
+        if rc != 0:
+            raise RuntimeError("watch_logits failed")
+        return rows[:n], positions[:n], counts[:n]
 
     def forward(self, spans, want_logits: bool = False):
         """spans: list of (request_id, first_position, [token ids]).  Returns

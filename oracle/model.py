@@ -67,6 +67,37 @@ def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
     return rounded(x * scale * weight)
 
 
+def matmul_rows(x: np.ndarray, w: np.ndarray, round_output: bool = True) -> np.ndarray:
+    """Row-wise matvec of every row of x ([n][in]) by w ([out][in]) as one fp32
+    product (fp32 accumulation; the summation order may differ from
+    matvec's, a difference below fp16 resolution in almost every output)."""
+    y = np.dot(x.astype(np.float32), w.T).astype(np.float32)
+    return rounded(y) if round_output else y
+
+
+def rms_norm_rows(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    """rms_norm of every row of x ([n][hidden])."""
+    sq = np.sum(x.astype(np.float64) ** 2, axis=1).astype(np.float32)
+    scale = np.float32(1.0) / np.sqrt(sq / np.float32(x.shape[1]) + np.float32(eps), dtype=np.float32)
+    return rounded(x * scale[:, None] * weight)
+
+
+def apply_rope_rows(v: np.ndarray, heads: int, dim: int, positions: np.ndarray, theta: float) -> np.ndarray:
+    """apply_rope of row i of v ([n][heads * dim]) at positions[i]."""
+    half = dim // 2
+    n = v.shape[0]
+    out = v.copy().reshape(n, heads, dim)
+    d = np.arange(half, dtype=np.float32)
+    inv = np.power(np.float32(theta), np.float32(-2.0) * d / np.float32(dim), dtype=np.float32)
+    angle = positions.astype(np.float32)[:, None] * inv[None, :]
+    c = np.cos(angle).astype(np.float32)[:, None, :]
+    s = np.sin(angle).astype(np.float32)[:, None, :]
+    left, right = out[:, :, :half].copy(), out[:, :, half:].copy()
+    out[:, :, :half] = rounded(left * c - right * s)
+    out[:, :, half:] = rounded(right * c + left * s)
+    return out.reshape(n, heads * dim)
+
+
 def apply_rope(v: np.ndarray, heads: int, dim: int, position: int, theta: float) -> np.ndarray:
     half = dim // 2
     out = v.copy().reshape(heads, dim)
@@ -157,6 +188,55 @@ class ReferenceModel:
             act = rounded(gate / (np.float32(1.0) + np.exp(-gate)) * up)
             hidden = rounded(hidden + matvec(W["down"], act))
         self.final_hidden = rms_norm(hidden, self.final_norm, cfg.rms_norm_epsilon)
+        return matvec(self.head, self.final_hidden, round_output=False)
+
+    @staticmethod
+    def _span_mask(positions: np.ndarray, total: int) -> np.ndarray:
+        """Causal mask of the span's rows (at `positions`) over the history +
+        span keys [0, total)."""
+        return np.arange(total)[None, :] <= positions[:, None]
+
+    def forward_span(self, tokens, first_position: int) -> np.ndarray:
+        """The token-at-a-time forward of tokens at positions first_position,
+        first_position + 1, ... (the next positions of this request), with the
+        span's rows batched into matrix products and its causal attention
+        computed for all rows at once; same fp16 rounding points and the same
+        KV history afterwards.  Returns the logits after the span's last
+        token.  Agrees with forward() token by token within fp16 noise (only
+        the fp32 summation order of the products differs)."""
+        cfg = self.cfg
+        D, QH, KVH = cfg.head_dimension, cfg.attention_head_count, cfg.kv_head_count
+        G = QH // KVH
+        n = len(tokens)
+        assert n > 0 and len(self.keys[0]) == first_position
+        positions = np.arange(first_position, first_position + n)
+        scale = np.float32(1.0) / np.sqrt(np.float32(D))
+        hidden = self.embed[np.asarray(tokens, dtype=np.int64)].copy()
+        total = first_position + n
+        allowed = self._span_mask(positions, total)
+        for l, W in enumerate(self.layers):
+            x = rms_norm_rows(hidden, W["ln1"], cfg.rms_norm_epsilon)
+            q = apply_rope_rows(matmul_rows(x, W["q"]), QH, D, positions, cfg.rope_theta)
+            k = apply_rope_rows(matmul_rows(x, W["k"]), KVH, D, positions, cfg.rope_theta)
+            v = matmul_rows(x, W["v"])
+            self.keys[l].extend(list(k))
+            self.values[l].extend(list(v))
+            K = np.stack(self.keys[l]).reshape(total, KVH, D).astype(np.float64)
+            Vv = np.stack(self.values[l]).reshape(total, KVH, D).astype(np.float64)
+            attn = np.zeros((n, QH * D), dtype=np.float32)
+            q64 = q.reshape(n, QH, D).astype(np.float64)
+            for h in range(QH):
+                s = (q64[:, h, :] @ K[:, h // G, :].T).astype(np.float32) * scale        # [n][total]
+                s = np.where(allowed, s, np.float32(-np.inf))
+                p = np.exp((s - s.max(axis=1, keepdims=True)).astype(np.float64))
+                attn[:, h * D:(h + 1) * D] = rounded(((p / p.sum(axis=1, keepdims=True)) @ Vv[:, h // G, :])
+                                                     .astype(np.float32))
+            hidden = rounded(hidden + matmul_rows(attn, W["o"]))
+            x = rms_norm_rows(hidden, W["ln2"], cfg.rms_norm_epsilon)
+            gate, up = matmul_rows(x, W["gate"]), matmul_rows(x, W["up"])
+            act = rounded(gate / (np.float32(1.0) + np.exp(-gate)) * up)
+            hidden = rounded(hidden + matmul_rows(act, W["down"]))
+        self.final_hidden = rms_norm(hidden[-1], self.final_norm, cfg.rms_norm_epsilon)
         return matvec(self.head, self.final_hidden, round_output=False)
 
     def generate(self, prompt, max_new_tokens: int, eos: int | None = None):

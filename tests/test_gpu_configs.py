@@ -1,5 +1,4 @@
-"""GPU parity at the benchmark workloads' own sizes (2, 3
-and 5; config 4's 189 GB is checked by sampled lanes inside bench.py).
+"""GPU parity at the benchmark workloads' own sizes.
 
 * config 1: one TinyLlama layer, 4 lanes {17, 100, 513, 1000} in 512-slot
   permuted pools, reserve -> write -> attend through the engine (lane 4
@@ -13,9 +12,15 @@ and 5; config 4's 189 GB is checked by sampled lanes inside bench.py).
   2048 + r prefix (partial micro tail, copy-on-write), one decode step of 22
   layers through LaneBatch, every lane at layers 0 and 21 vs the oracle, and
   the committed tables (shared prefix pages, distinct COW targets);
+* config 4: 256 lanes x 32 768 tokens x 22 layers (189 GB of extent pages)
+  through two lane groups on two streams, two decode steps, sampled lanes at
+  layers 0 and 21 vs the oracle, tail pages bit-exact;
 * config 5: the TinyLlama-1.1B-shaped runner (22 layers, hidden 2048,
   vocab 32 000) on a 16-token chunk plus decode steps beside a second
-  request's chunk, logits within 0.035 of the oracle's CPU forward.
+  request's chunk, logits within 0.035 of the oracle's CPU forward; and the
+  config's own workload, the iteration scheduler mixing 4 requests in
+  512-token chunked prefill with 60 decode lanes, with per-iteration
+  properties and logits at sampled positions against the oracle.
 
 Scenarios after tests/cuda/cuda_kv_test.cpp:287-391,
 tests/cuda/cuda_engine_kv_backend_test.cpp:258-345 and
@@ -321,6 +326,118 @@ def test_config3_shared_prefix_fork_cow_decode(host, dev):
     stream.destroy()
 
 
+# ---- config 4 ------------------------------------------------------------------------------------------------
+
+def test_config4_hbm_scale_two_lane_groups(host, dev):
+    """Config 4 at its full size: 256 lanes x 32 768-token contexts x 22 layers (131 072 extent pages,
+    189 GB, slots permuted) built by the engine's bulk prefill + promotion, then two decode steps
+    through two lane groups of 128 token transactions on two streams, the first group committed after
+    the second group's layers are queued (src/cuda/engine/backend.cpp:198-259 at 256 lanes).  Eight
+    lanes from both groups at layers 0 and 21 against the oracle's decode of the generator's history
+    (32 770 tokens), committed tables (512 extents + one micro tail of two tokens), and two lanes' tail
+    pages gathered bit-exact."""
+    lanes, context, L, steps, seed = 256, 32768, 22, 2, 4040
+    ws_lane = max(dev.workspace_bytes(context + steps, 64, QH, D), 256)
+    n_micro = lanes * 2 + 64
+    engine = host.Engine(L, H, D, QH, ws_lane, n_micro, lanes * context // 64)
+    streams = [dev.Stream(), dev.Stream()]
+    try:
+        assert engine.permute_free_slots(1, seed) == 0 and engine.permute_free_slots(0, seed + 1) == 0
+        stage = dev.DeviceBuffer(L * 2 * 512 * HD * 2)
+        for i in range(lanes):
+            assert engine.create_request(i + 1) == 0
+            for t in range(0, context, 512):
+                dev.fill_kv(stage.ptr, L, 512, HD, seed, i, t, streams[0])
+                rc, promoted = engine.append_prefill(i + 1, 512, stage.ptr, streams[0], promote=True)
+                assert rc == 0 and promoted == 8, (i, t, rc, promoted)
+        streams[0].synchronize()
+        del stage
+        print(f"config 4: {lanes} x {context} tokens prefilled, "
+              f"{engine.snapshot().storage_reserved_bytes / 1e9:.1f} GB of pools", flush=True)
+        lane = np.arange(lanes, dtype=np.uint64)
+        newkv = dev.DeviceBuffer(lanes * L * 2 * steps * HD * 2)       # [lane][layer][comp][step][HD]
+        query = dev.DeviceBuffer(lanes * L * steps * QD * 2)           # [lane][layer][step][QD]
+        out = dev.DeviceBuffer(lanes * L * QD * 2)                      # [lane][layer][QD]
+        qseed = seed ^ 0x5155
+        for i in range(lanes):
+            for l in range(L):
+                for c in range(2):
+                    dev.fill_rows(newkv.ptr + (((i * L + l) * 2 + c) * steps) * HD * 2, steps * HD, seed,
+                                  dev.synth_kv_row(i, l, c, context), HD)
+                dev.fill_rows(query.ptr + ((i * L + l) * steps) * QD * 2, steps * QD, qseed,
+                              dev.synth_kv_row(i, l, 0, context), QD)
+        dev.sync()
+        ws = dev.DeviceBuffer(ws_lane * lanes)
+        groups = []
+        layer = np.arange(L, dtype=np.uint64)[:, None]
+        for g, sl in enumerate([slice(0, lanes // 2), slice(lanes // 2, lanes)]):
+            b = host.LaneBatch(engine, lane[sl] + np.uint64(1), ws.ptr + lane[sl] * np.uint64(ws_lane), ws_lane,
+                               1.0 / math.sqrt(D), streams[g])
+            row = lane[sl][None, :] * np.uint64(L) + layer                    # [layer][lane] (lane, layer) index
+            kbase = newkv.ptr + np.uint64(2 * HD) * row * np.uint64(2 * steps)
+            qbase = query.ptr + np.uint64(2 * QD) * row * np.uint64(steps)
+            b.outputs[:] = out.ptr + np.uint64(2 * QD) * row
+            groups.append((b, kbase, qbase))
+        pending = None
+        for step in range(steps):
+            for b, kbase, qbase in groups:
+                b.keys[:] = kbase + np.uint64(2 * HD * step)
+                b.values[:] = kbase + np.uint64(2 * HD * (steps + step))
+                b.queries[:] = qbase + np.uint64(2 * QD * step)
+                b.reserve(context + step)
+                assert not b.failed(), ("reserve", step, sorted(set(b.status.tolist())))
+                for l in range(L):
+                    b.write(l)
+                    b.attend(l)
+                assert not b.failed(), ("launch", step, sorted(set(b.status.tolist())))
+                if pending is not None:          # the other group's commit waits behind this group's launches
+                    pending.commit()
+                    assert not pending.failed()
+                pending = b
+        pending.commit()
+        assert not pending.failed()
+        assert engine.check_invariants()
+        T = context + steps
+        got = dev.download(out.ptr, (lanes, L, QD), np.uint16)
+        sample = [0, 37, 90, 127, 128, 171, 200, 255]
+        cases = []
+        for i in sample:
+            hist = _history(seed, lambda t, i=i: i, [0, L - 1], T)
+            for li, l in enumerate([0, L - 1]):
+                q = oracle.synth_rows(QD, qseed, oracle.kv_row(i, l, 0, context) + steps - 1, QD)
+                cases.append((i, l, hist[li], q))
+        with ThreadPoolExecutor(THREADS) as pool:
+            wants = list(pool.map(lambda c: _oracle_decode(c[2], T, c[3]), cases))
+        worst = 0.0
+        for (i, l, _, _), want in zip(cases, wants):
+            worst = max(worst, assert_attention_close(got[i, l], want))
+        # Tables and tail pages.
+        for i in (5, 250):
+            _, entries = engine.block_table(i + 1)
+            assert [e[2] for e in entries] == [1] * 512 + [0] and entries[-1][:2] == (context, steps)
+            tail = entries[-3:]                                  # two extents + the micro tail
+            base = tail[0][0]
+            desc = host.descriptors_from_entries([(e[0] - base,) + tuple(e[1:]) for e in tail])
+            d = dev.upload(desc)
+            buf = dev.DeviceBuffer(L * 2 * (T - base) * HD * 2)
+            import ctypes
+            dev.check(dev.lib().kimkv_gather(ctypes.c_void_p(engine.storage_handle()), ctypes.c_void_p(d.ptr),
+                                             len(desc), T - base, ctypes.c_void_p(buf.ptr), None), "gather")
+            pages = dev.download(buf.ptr, (L, 2, T - base, H, D), np.uint16)
+            want = np.empty_like(pages)
+            for l in range(L):
+                for c in range(2):
+                    want[l, c] = oracle.synth_rows((T - base) * HD, seed, oracle.kv_row(i, l, c, base),
+                                                   HD).reshape(T - base, H, D)
+            assert np.array_equal(pages, want), i
+        print(f"config 4: {lanes} lanes x {T} tokens x {L} layers, 2 groups on 2 streams, "
+              f"{len(cases)} lane-layers max decode err {worst:.2e}", flush=True)
+    finally:
+        engine.close()
+        for st in streams:
+            st.destroy()
+
+
 # ---- config 5 ------------------------------------------------------------------------------------------------
 
 def test_config5_tinyllama_1b_runner_logits(host, dev):
@@ -370,5 +487,152 @@ def test_config5_tinyllama_1b_runner_logits(host, dev):
         check(logits[1], ref_b.forward(gb, len(pb) + step), f"B decode {step + 1}")
     assert engine.check_invariants()
     print(f"config 5: TinyLlama-1.1B shape, max logit err {worst:.2e}", flush=True)
+    runner.close()
+    stream.destroy()
+
+
+def test_config5_scheduler_chunked_prefill_beside_60_decode_lanes(host, dev):
+    """Config 5's own workload: the iteration scheduler over the TinyLlama-1.1B-shaped runner with 60
+    decode lanes beside 4 requests in 512-token chunked prefill (prompts U[256, 2048], a finished one
+    replaced at once), max_batched_tokens 4 x 512 + 60 (tests/cuda/cuda_model_runner_test.cpp:703-825
+    at this shape).  Every iteration of the mix: one model call, every active request one span (decode
+    lanes one position further, prefilling requests min(512, remaining) positions), the scheduler's
+    token counts matching, each request's committed KV length = its last processed position + 1, engine
+    invariants.  Logits (runner watch) against the oracle's CPU forward within 0.035 at: two decode
+    lanes (256-token prompts) from their prompt's last row through every decode step, teacher-forced
+    with the lanes' own greedy tokens; a 700-token prompt's chunk ends (positions 511 and 699).  The
+    drained terminals hold every lane's tokens, all inside the vocabulary."""
+    from oracle import model as om
+    cfg = om.ModelConfig(hidden_size=2048, intermediate_size=5632, layer_count=22, attention_head_count=32,
+                         kv_head_count=4, head_dimension=64, vocabulary_size=32000, max_position_embeddings=2048)
+    L, V = cfg.layer_count, cfg.vocabulary_size
+    n_dec, n_pre, chunk, max_new, tol = 60, 4, 512, 48, 0.035
+    budget = n_pre * chunk + n_dec
+    seed = 9090
+    rng = np.random.default_rng(seed)
+    engine = host.Engine(L, H, D, QH, 1 << 20, (n_dec * 1100 + (2 * n_pre + 4) * 2048) // 8 + 512, 16)
+    assert engine.permute_free_slots(0, seed) == 0
+    stream = dev.Stream()
+    mc = host.ModelConfig(cfg.hidden_size, cfg.intermediate_size, L, cfg.attention_head_count, cfg.kv_head_count,
+                          cfg.head_dimension, V, cfg.max_position_embeddings, cfg.bos_token_id, cfg.eos_token_id,
+                          cfg.rms_norm_epsilon, cfg.rope_theta)
+    runner = host.Runner(engine, mc, seed, budget + 64, n_dec + n_pre + 8, stream)
+    sched = host.Scheduler(engine, runner, max_active=n_dec + n_pre + 8, max_batched_tokens=budget,
+                           max_kv_tokens=1 << 40, prefill_chunk=chunk)
+    prompts = {}
+
+    def submit(rid, n, new):
+        prompts[rid] = [int(t) for t in rng.integers(3, V, n)]
+        assert sched.submit(rid, prompts[rid], new) == "none"
+
+    sampled = [1, 2]
+    for rid in range(1, n_dec + 1):
+        submit(rid, 256 if rid in sampled else int(rng.integers(256, 1025)), max_new)
+    seen = {rid: {} for rid in sampled}            # rid -> {position: GPU logits}
+
+    def record(rows, pos, cnt, ids):
+        for k, rid in enumerate(ids):
+            if rid in seen and cnt[k]:
+                seen[rid][int(pos[k])] = rows[k].copy()
+
+    # Setup: until every decode lane is decoding.
+    setup = 0
+    while True:
+        rows, pos, cnt = runner.watch_logits(sampled)
+        r = sched.run_iteration()
+        record(rows, pos, cnt, sampled)
+        setup += 1
+        assert r.model_forward_batches == 1 and setup < 200
+        if r.prefill_tokens == 0:
+            break
+    assert not sched.take_terminals()
+    assert r.decode_tokens == n_dec
+
+    # The mix: 4 prefilling requests (one of them the sampled 700-token prompt) beside the 60 lanes.
+    last = {}
+    for rid in range(1, n_dec + 1):
+        _, entries = engine.block_table(rid)
+        last[rid] = entries[-1][0] + entries[-1][1] - 1        # last committed position
+    prefilling, next_rid, pre_sample = {}, 101, 101
+    mix_iters = 6
+    for it in range(mix_iters):
+        while len(prefilling) < n_pre:
+            n = 700 if next_rid == pre_sample else int(rng.integers(256, 2049))
+            submit(next_rid, n, 1)
+            prefilling[next_rid] = 0                             # prompt tokens processed
+            next_rid += 1
+        ids = list(range(1, n_dec + 1)) + sorted(prefilling)
+        rows, pos, cnt = runner.watch_logits(ids)
+        want_pre = {rid: min(chunk, len(prompts[rid]) - done) for rid, done in prefilling.items()}
+        finishing = {rid for rid, n in want_pre.items() if prefilling[rid] + n == len(prompts[rid])}
+        r = sched.run_iteration()
+        print(f"config 5 mix iteration {it}: prefill {r.prefill_tokens} decode {r.decode_tokens} "
+              f"forward {r.model_forward_tokens} terminals {r.terminals_produced}", flush=True)
+        assert r.model_forward_batches == 1
+        assert r.decode_tokens == n_dec and r.prefill_tokens == sum(want_pre.values())
+        assert r.model_forward_tokens == r.prefill_tokens + r.decode_tokens
+        assert r.terminals_produced == len(finishing)
+        assert list(cnt) == [1] * len(ids), "every active request gets one span per iteration"
+        for k, rid in enumerate(ids):
+            if rid <= n_dec:
+                assert pos[k] == last[rid] + 1, (rid, int(pos[k]), last[rid])
+                last[rid] = int(pos[k])
+            else:
+                assert pos[k] == prefilling[rid] + want_pre[rid] - 1, (rid, int(pos[k]))
+                if rid == pre_sample:
+                    seen.setdefault(rid, {})[int(pos[k])] = rows[k].copy()
+        record(rows, pos, cnt, ids)
+        for rid in ids:
+            if rid in finishing:
+                continue
+            _, entries = engine.block_table(rid)
+            committed = entries[-1][0] + entries[-1][1]
+            want = last[rid] + 1 if rid <= n_dec else prefilling[rid] + want_pre[rid]
+            assert committed == want, (rid, committed, want)
+        for rid, n in want_pre.items():
+            prefilling[rid] += n
+        for t in sched.take_terminals():
+            assert t["error"] == "none" and t["request_id"] in finishing, t
+            assert t["completion_tokens"] == 1 and all(0 <= x < V for x in t["tokens"])
+            prefilling.pop(t["request_id"])
+        assert engine.check_invariants()
+    runner.watch_logits([])
+    terminals = {t["request_id"]: t for t in sched.drain()}
+    for rid in range(1, n_dec + 1):
+        t = terminals[rid]
+        assert t["error"] == "none" and t["prompt_tokens"] == len(prompts[rid]), t
+        if t["reason"] == "eos_token":      # random weights do produce the model's EOS now and then
+            assert t["tokens"][-1] == cfg.eos_token_id and len(t["tokens"]) <= max_new, t
+        else:
+            assert t["reason"] == "max_new_tokens" and len(t["tokens"]) == max_new, t
+        assert all(0 <= x < V for x in t["tokens"])
+    sched.close()
+    assert engine.snapshot().request_count == 0
+
+    # Oracle: logits at the recorded positions.
+    ref = om.ReferenceModel(cfg, seed, threads=THREADS)
+    worst = 0.0
+
+    def check(got, want, tag):
+        nonlocal worst
+        err = float(np.max(np.abs(got - want)))
+        assert err < tol, (tag, err)
+        worst = max(worst, err)
+
+    for rid in sampled:
+        m = ref.fresh()
+        P = len(prompts[rid])
+        check(seen[rid][P - 1], m.forward_span(prompts[rid], 0), f"lane {rid} prompt")
+        toks = terminals[rid]["tokens"]
+        positions = sorted(p for p in seen[rid] if p >= P)
+        assert positions == list(range(P, P + len(positions))) and len(positions) >= mix_iters
+        for p in positions:
+            check(seen[rid][p], m.forward(toks[p - P], p), f"lane {rid} position {p}")
+    m = ref.fresh()
+    pp = prompts[pre_sample]
+    assert sorted(seen[pre_sample]) == [511, 699]
+    check(seen[pre_sample][511], m.forward_span(pp[:512], 0), "700-token prompt, first chunk")
+    check(seen[pre_sample][699], m.forward_span(pp[512:], 512), "700-token prompt, second chunk")
+    print(f"config 5 workload: {setup} setup + {mix_iters} mixed iterations, max logit err {worst:.2e}", flush=True)
     runner.close()
     stream.destroy()

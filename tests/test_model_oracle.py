@@ -107,3 +107,45 @@ def test_threaded_weight_generation_is_identical():
     assert np.array_equal(a.embed, b.embed) and np.array_equal(a.head, b.head)
     c = b.fresh()
     assert np.array_equal(b.forward(5, 0), c.forward(5, 0)) and len(b.keys[0]) == 1 and len(c.keys[0]) == 1
+
+
+def test_span_forward_matches_token_forward():
+    """forward_span (a span's rows batched into matrix products, causal
+    attention over the span at once) against the token-at-a-time forward on
+    the same weights: the logits after every span end agree within fp16
+    noise, so do the KV histories (the same values in almost every element,
+    the rest one fp16 rounding step apart), and both agree with the
+    independent float64 Llama."""
+    tokens = [5, 17, 3, 88, 41, 0, 63, 12, 9, 50, 33, 71, 2]
+    one = om.ReferenceModel(CFG, SEED)
+    per_token = [one.forward(t, p) for p, t in enumerate(tokens)]
+    span = one.fresh()
+    want64 = _torch_logits(one, tokens)
+    scale = float(np.abs(want64).max())
+    for a, b in [(0, 4), (4, 9), (9, 10), (10, 13)]:
+        got = span.forward_span(tokens[a:b], a)
+        assert np.max(np.abs(got - per_token[b - 1])) < 2e-3 * scale, (a, b)
+        assert np.max(np.abs(got - want64[b - 1])) < 0.004 * scale + 1e-3, (a, b)
+    for l in range(CFG.layer_count):
+        for hist_a, hist_b in ((one.keys[l], span.keys[l]), (one.values[l], span.values[l])):
+            a, b = np.stack(hist_a), np.stack(hist_b)
+            assert a.shape == b.shape
+            ulp = np.spacing(np.abs(a).astype(np.float16)).astype(np.float32)
+            assert np.all(np.abs(a - b) <= ulp * 1.01)
+            assert np.mean(a == b) > 0.97
+    # Planted mistakes fail the check: attention that ignores the causal mask
+    # (earlier rows attend to later keys, which changes the next layer's keys
+    # and so the last row), and RoPE at the span's first position for every row.
+    leaky = one.fresh()
+    leaky._span_mask = lambda positions, total: np.ones((len(positions), total), dtype=bool)
+    assert np.max(np.abs(leaky.forward_span(tokens[:6], 0) - per_token[5])) > 0.02 * scale
+    real = om.apply_rope_rows
+    try:
+        om.apply_rope_rows = lambda v, heads, dim, positions, theta: real(v, heads, dim, positions * 0 + positions[0],
+                                                                          theta)
+        stuck = one.fresh().forward_span(tokens[:6], 0)
+    finally:
+        om.apply_rope_rows = real
+    # (attention over random small weights is nearly uniform, so RoPE moves the
+    # logits little: still twice the agreement bound above)
+    assert np.max(np.abs(stuck - per_token[5])) > 4e-3 * scale
