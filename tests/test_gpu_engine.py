@@ -819,3 +819,126 @@ def test_engine_small_staging_ring(host, dev, monkeypatch):
     interleaved, over three steps."""
     monkeypatch.setenv("KIMKV_STAGING_RING_BYTES", str(64 << 10))
     _engine_lane_batch_case(host, dev, steps=3, seed=78)
+
+
+def test_inflight_transaction_pages_survive_sibling_release_and_promotion(host, dev):
+    """The engine's token transactions take no page lease (the reference leases every page of the
+    candidate table per token, src/cuda/engine/backend.cpp:411-424): a request's committed table holds a
+    reference to every page its launches read and the reservation owns the copy-on-write target until
+    commit, while the manager refuses release, fork, append and promotion of a request with a live
+    reservation.  Checked on the device: a lane batch of two fork children is reserved (each copies the
+    shared partial prefix tail) and every layer's write and attention is queued behind a long fill
+    kernel on its stream; meanwhile, on another stream, the two sibling forks are released, a third
+    request is promoted (its micro pages return to the LIFO free list) and a fourth request allocates
+    and writes 4096 tokens of fresh pages.  Had any page of the in-flight lanes been freed, the fourth
+    request would have been given it and overwritten it before the decode read it.  The outputs match
+    the oracle, the lanes' pages gather bit for bit after commit, and so do the other requests'."""
+    L, H, D, QH, seed = 4, 4, 64, 32, 515
+    HD, QD = H * D, QH * D
+    engine = host.Engine(L, H, D, QH, 1 << 16, 2048, 256)
+    assert engine.permute_free_slots(1, seed) == 0 and engine.permute_free_slots(0, seed + 1) == 0
+    sa, sb = dev.Stream(), dev.Stream()
+    P = 2048 + 3
+    stage = dev.DeviceBuffer(L * 2 * 4096 * HD * 2)
+    root, kids, promo, fresh = 100, [1, 2, 3, 4], 200, 300
+    assert engine.create_request(root) == 0
+    dev.fill_kv(stage.ptr, L, P, HD, seed, 7, 0, sa)
+    rc, _ = engine.append_prefill(root, P, stage.ptr, sa, promote=True)
+    assert rc == 0
+    for k in kids:
+        assert engine.fork_request(root, k) == 0
+    assert engine.release_request(root) == 0
+    assert engine.create_request(promo) == 0
+    dev.fill_kv(stage.ptr, L, 512, HD, seed, 8, 0, sa)
+    rc, promoted = engine.append_prefill(promo, 512, stage.ptr, sa, promote=False)
+    assert rc == 0 and promoted == 0
+    sa.synchronize()
+    tables_before = {k: engine.block_table(k)[1] for k in kids[:2]}
+
+    lanes = np.arange(2, dtype=np.uint64)
+    newkv = dev.DeviceBuffer(2 * L * 2 * HD * 2)
+    query = dev.DeviceBuffer(2 * L * QD * 2)
+    out = dev.DeviceBuffer(2 * L * QD * 2)
+    qseed = seed ^ 0x77
+    for i in range(2):
+        dev.fill_kv(newkv.ptr + i * L * 2 * HD * 2, L, 1, HD, seed, 50 + i, P, sa)
+        for l in range(L):
+            dev.fill_rows(query.ptr + (i * L + l) * QD * 2, QD, qseed, dev.synth_kv_row(i, l, 0, P), QD, sa)
+    ws_lane = max(dev.workspace_bytes(P + 1, 64, QH, D), 256)          # room for any split-K plan
+    ws = dev.DeviceBuffer(2 * ws_lane)
+    b = host.LaneBatch(engine, lanes + np.uint64(1), ws.ptr + lanes * np.uint64(ws_lane), ws_lane, 0.125, sa)
+    for l in range(L):
+        b.keys[l, :] = newkv.ptr + np.uint64(2 * HD) * (lanes * np.uint64(2 * L) + np.uint64(2 * l))
+        b.values[l, :] = newkv.ptr + np.uint64(2 * HD) * (lanes * np.uint64(2 * L) + np.uint64(2 * l + 1))
+        b.queries[l, :] = query.ptr + np.uint64(2 * QD) * (lanes * np.uint64(L) + np.uint64(l))
+        b.outputs[l, :] = out.ptr + np.uint64(2 * QD) * (lanes * np.uint64(L) + np.uint64(l))
+    delay = dev.DeviceBuffer(1 << 31)
+    sa.synchronize()
+    for rep in range(2):                                               # ~4 GB of stores ahead of the lanes
+        dev.fill_rows(delay.ptr, 1 << 30, rep, 0, 1 << 16, sa)
+    b.reserve(np.array([P, P], dtype=np.uint32))
+    assert not b.failed()
+    for l in range(L):
+        b.write(l)
+        b.attend(l)
+    assert not b.failed(), sorted(set(b.status.tolist()))
+    # While the lanes' launches wait behind the fill: the in-flight requests are pinned ...
+    conflict = host.ENGINE_ERRORS.index("request_conflict")
+    assert engine.release_request(1) == conflict
+    assert engine.fork_request(1, 999) == conflict
+    # ... and their siblings, a promotion and fresh allocations go ahead on another stream.
+    assert engine.release_request(3) == 0 and engine.release_request(4) == 0
+    rc, promoted = engine.promote_request(promo, sb)
+    assert rc == 0 and promoted == 8
+    assert engine.create_request(fresh) == 0
+    fresh_stage = dev.DeviceBuffer(L * 2 * 4096 * HD * 2)
+    dev.fill_kv(fresh_stage.ptr, L, 4096, HD, seed, 9, 0, sb)
+    rc, _ = engine.append_prefill(fresh, 4096, fresh_stage.ptr, sb, promote=True)
+    assert rc == 0
+    sb.synchronize()
+    b.commit()
+    assert not b.failed(), sorted(set(b.status.tolist()))
+    assert engine.check_invariants()
+    got = dev.download(out.ptr, (2, L, QD), np.uint16)
+    T = P + 1
+    for i, k in enumerate(kids[:2]):
+        hist = np.empty((L, 2, T, H, D), dtype=np.uint16)
+        for l in range(L):
+            for c in range(2):
+                hist[l, c, :P] = oracle.synth_rows(P * HD, seed, oracle.kv_row(7, l, c, 0), HD).reshape(P, H, D)
+                hist[l, c, P] = oracle.synth_rows(HD, seed, oracle.kv_row(50 + i, l, c, P), HD).reshape(H, D)
+        for l in range(L):
+            q = oracle.synth_rows(QD, qseed, oracle.kv_row(i, l, 0, P), QD)
+            pools = oracle.HostPools(1, H, D, (T + 7) // 8, 1)
+            table = np.zeros((T + 7) // 8, dtype=oracle.DESC)
+            for g in range(len(table)):
+                n = min(8, T - 8 * g)
+                table[g] = (g, 1, 8 * g, n, 8, 0)
+                pools.append_tokens(hist[l:l + 1], T, 8 * g, 0, g, 0, n)
+            want = pools.paged_decode(table, T, 0, QH, q, 0.125, f32=True)
+            a = to_f32(got[i, l])
+            assert np.all(np.abs(a - want) <= 2e-3 + 1e-3 * np.abs(want)), (k, l)
+        _, entries = engine.block_table(k)
+        assert entries[:-1] == tables_before[k][:-1] and entries[-1][1] == 4      # COW tail: 3 copied + 1
+        assert entries[-1][3] != tables_before[k][-1][3]
+        descs = host.descriptors_from_entries(entries)
+        d = dev.upload(descs)
+        buf = dev.DeviceBuffer(hist.nbytes)
+        dev.check(dev.lib().kimkv_gather(ctypes.c_void_p(engine.storage_handle()), ctypes.c_void_p(d.ptr),
+                                         len(descs), T, ctypes.c_void_p(buf.ptr), None), "gather")
+        assert np.array_equal(dev.download(buf.ptr, hist.shape, np.uint16), hist), k
+    for rid, sid, n in ((promo, 8, 512), (fresh, 9, 4096)):
+        _, entries = engine.block_table(rid)
+        descs = host.descriptors_from_entries(entries)
+        d = dev.upload(descs)
+        buf = dev.DeviceBuffer(L * 2 * n * HD * 2)
+        dev.check(dev.lib().kimkv_gather(ctypes.c_void_p(engine.storage_handle()), ctypes.c_void_p(d.ptr),
+                                         len(descs), n, ctypes.c_void_p(buf.ptr), None), "gather")
+        want = np.empty((L, 2, n, H, D), dtype=np.uint16)
+        for l in range(L):
+            for c in range(2):
+                want[l, c] = oracle.synth_rows(n * HD, seed, oracle.kv_row(sid, l, c, 0), HD).reshape(n, H, D)
+        assert np.array_equal(dev.download(buf.ptr, want.shape, np.uint16), want), rid
+    del delay
+    sa.destroy()
+    sb.destroy()
