@@ -375,6 +375,29 @@ kimkv_status kimkv_paged_decode_write_batch_slots(const kimkv_storage* storage,
                                                   uint32_t query_heads, const kimkv_append_job* device_writes,
                                                   void* device_lane_slots, kimkv_stream_t stream);
 
+/* Largest lane count whose chunk prefix kimkv_paged_decode_write_batch_slots_prefix
+ * carries in the launch's arguments. */
+#define KIMKV_DECODE_ARG_PREFIX_LANES 64u
+
+/* kimkv_paged_decode_write_batch_slots with host_chunk_prefix, the same
+ * chunk prefix (lane_count + 1 entries) in host memory: for launches of up
+ * to KIMKV_DECODE_ARG_PREFIX_LANES lanes the library copies it into the
+ * launch's arguments, and each workgroup finds its lane from them with no
+ * read of device_chunk_prefix, so when the caller stages the launch data in
+ * mapped host memory (the engine) a workgroup's lane lookup costs no round
+ * trip to the host and no scan of the prefix; larger launches behave as
+ * kimkv_paged_decode_write_batch_slots.  host_chunk_prefix must start at 0
+ * and end at total_chunks (else KIMKV_INVALID_ARGUMENT, nothing launched) and
+ * equal device_chunk_prefix.  Same results.  No counterpart in the
+ * reference. */
+kimkv_status kimkv_paged_decode_write_batch_slots_prefix(const kimkv_storage* storage,
+                                                         const kimkv_decode_item* device_items,
+                                                         const uint32_t* device_chunk_prefix,
+                                                         const uint32_t* host_chunk_prefix, uint32_t lane_count,
+                                                         uint32_t total_chunks, uint32_t chunk_flags,
+                                                         uint32_t query_heads, const kimkv_append_job* device_writes,
+                                                         void* device_lane_slots, kimkv_stream_t stream);
+
 /* Size of the device scratch array of kimkv_paged_decode_batch_noalloc. */
 #define KIMKV_DECODE_SCRATCH_BYTES (16u << 20)
 

@@ -791,10 +791,21 @@ static_assert(sizeof(DecodeLaneSlot) == KIMKV_DECODE_LANE_SLOT_BYTES, "slot size
 // launch follows when gridDim.x > lane_count, and a lane of several chunks
 // in a launch without it is reported and skipped.  A lane of no tokens is
 // skipped (its output is not written), as the reference's batch kernel does.
-template <bool kSplit, bool kStream>
+// The chunk prefix of a small launch carried in its arguments (kimkv
+// launches copy the arguments to device memory with the dispatch), so a
+// workgroup finds its lane exactly without reading the prefix from wherever
+// the caller staged it; used for launches of up to
+// KIMKV_DECODE_ARG_PREFIX_LANES lanes when the caller passes a host copy.
+struct ArgPrefix {
+    uint32_t v[KIMKV_DECODE_ARG_PREFIX_LANES + 1];
+};
+struct NoArgPrefix {};
+
+template <bool kSplit, bool kStream, bool kArgPrefix>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
     PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t chunk_tokens,
-    uint32_t QH, float* partials, const kimkv_append_job* writes, DecodeLaneSlot* slots, uint64_t tag)
+    uint32_t QH, float* partials, const kimkv_append_job* writes, DecodeLaneSlot* slots, uint64_t tag,
+    std::conditional_t<kArgPrefix, ArgPrefix, NoArgPrefix> ap)
 {
     __shared__ DecodeLds lds;
     __shared__ uint32_t s_lane;
@@ -807,51 +818,82 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // whose leading chunks read the same pages -- meet in one XCD's L2.
     uint32_t const chunk_id = !kSplit && gridDim.y == 1 ? xcd_logical_index(blockIdx.x, gridDim.x) : blockIdx.x;
     if (lane_count == 0) return;
-    // The prologue is a chain of dependent global reads, and under full HBM
-    // load each costs microseconds while this workgroup streams nothing, so
-    // both lookups are guessed and verified in the same round trip.
-    // Lane: guess from the average chunk count per lane (exact when lanes
-    // have equal chunk counts), with that lane's item loaded alongside.
-    uint32_t const guess = static_cast<uint32_t>(
-        min(static_cast<uint64_t>(chunk_id) * lane_count / gridDim.x, static_cast<uint64_t>(lane_count - 1)));
-    kimkv_decode_item item = items[guess];
-    // The lane's write job comes in the same round trip (kimkv_append_job{}
-    // when there is none).
-    kimkv_append_job job = writes != nullptr ? writes[guess] : kimkv_append_job{};
-    uint32_t const pg0 = prefix[guess];
-    uint32_t const pg1 = prefix[guess + 1];
-    if (tid == 0) {
-        s_hit = pg0 <= chunk_id && chunk_id < pg1 ? 1u : 0u;
-        s_lane = 0xFFFFFFFFu;
-    }
-    __syncthreads();
-    uint32_t lane = guess;
-    if (s_hit == 0) {
-        for (uint32_t i = tid; i < lane_count; i += kBlock) {
-            if (prefix[i] <= chunk_id && chunk_id < prefix[i + 1]) s_lane = i;
+    uint32_t lane = 0;
+    uint32_t lane_first = 0;
+    uint32_t lane_end = 0;
+    kimkv_decode_item item;
+    kimkv_append_job job;
+    if constexpr (kArgPrefix) {
+        // The last lane whose first chunk is <= chunk_id (scalar loads of the
+        // launch arguments), then one round trip for its item and job.
+        uint32_t lo = 0;
+        uint32_t hi = lane_count;
+        while (hi - lo > 1) {
+            uint32_t const mid = (lo + hi) >> 1;
+            if (ap.v[mid] <= chunk_id) {
+                lo = mid;
+            } else {
+                hi = mid;
+            }
         }
-        __syncthreads();
-        lane = s_lane;
-        if (lane == 0xFFFFFFFFu) {   // the chunk prefix does not cover this workgroup
+        lane = lo;
+        lane_first = ap.v[lane];
+        lane_end = ap.v[lane + 1];
+        if (!(lane_first <= chunk_id && chunk_id < lane_end)) {   // the prefix does not cover this workgroup
             report_fault(P, KIMKV_FAULT_DECODE_ITEM);
             return;
         }
         item = items[lane];
-        if (writes != nullptr) job = writes[lane];
+        job = writes != nullptr ? writes[lane] : kimkv_append_job{};
+    } else {
+        // The prologue is a chain of dependent global reads, and under full
+        // HBM load each costs microseconds while this workgroup streams
+        // nothing, so both lookups are guessed and verified in the same round
+        // trip.  Lane: guess from the average chunk count per lane (exact
+        // when lanes have equal chunk counts), with that lane's item loaded
+        // alongside.
+        uint32_t const guess = static_cast<uint32_t>(
+            min(static_cast<uint64_t>(chunk_id) * lane_count / gridDim.x, static_cast<uint64_t>(lane_count - 1)));
+        item = items[guess];
+        // The lane's write job comes in the same round trip (kimkv_append_job{}
+        // when there is none).
+        job = writes != nullptr ? writes[guess] : kimkv_append_job{};
+        uint32_t const pg0 = prefix[guess];
+        uint32_t const pg1 = prefix[guess + 1];
+        if (tid == 0) {
+            s_hit = pg0 <= chunk_id && chunk_id < pg1 ? 1u : 0u;
+            s_lane = 0xFFFFFFFFu;
+        }
+        __syncthreads();
+        lane = guess;
+        if (s_hit == 0) {
+            for (uint32_t i = tid; i < lane_count; i += kBlock) {
+                if (prefix[i] <= chunk_id && chunk_id < prefix[i + 1]) s_lane = i;
+            }
+            __syncthreads();
+            lane = s_lane;
+            if (lane == 0xFFFFFFFFu) {   // the chunk prefix does not cover this workgroup
+                report_fault(P, KIMKV_FAULT_DECODE_ITEM);
+                return;
+            }
+            item = items[lane];
+            if (writes != nullptr) job = writes[lane];
+        }
+        lane_first = prefix[lane];
+        lane_end = prefix[lane + 1];
     }
 
     uint32_t const H = P.heads;
     uint32_t const D = P.dim;
-    uint32_t const lane_first = prefix[lane];
     uint32_t const chunk_index = chunk_id - lane_first;
-    uint32_t const nchunks = prefix[lane + 1] - lane_first;
+    uint32_t const nchunks = lane_end - lane_first;
     if (partials != nullptr) item.workspace = partials + static_cast<uint64_t>(lane_first) * QH * (D + 2);
     uint32_t const T = item.token_count;
     if (T == 0) return;
     uint32_t const c0 = chunk_index * chunk_tokens;
     // A lane's chunks must lie inside the launch (the merge reads them all).
     if (!decode_item_valid(P, item, QH, nchunks, gridDim.x > lane_count) || c0 >= T || chunk_tokens > kMaxChunk
-        || prefix[lane + 1] > gridDim.x) {
+        || lane_end > gridDim.x) {
         report_fault(P, KIMKV_FAULT_DECODE_ITEM);
         return;
     }
@@ -1182,7 +1224,8 @@ bool work_counter_slot(const kimkv_storage* storage, kimkv_stream_t stream, uint
 kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item* device_items,
                            const uint32_t* device_chunk_prefix, uint32_t lane_count, uint32_t total_chunks,
                            uint32_t chunk_flags, uint32_t query_heads, kimkv_stream_t stream, float* partials,
-                           const kimkv_append_job* writes, bool timed, DecodeLaneSlot* slots = nullptr)
+                           const kimkv_append_job* writes, bool timed, DecodeLaneSlot* slots = nullptr,
+                           const uint32_t* host_prefix = nullptr)
 {
     bool const head_split = (chunk_flags & KIMKV_DECODE_HEAD_SPLIT) != 0;
     bool const guided = (chunk_flags & KIMKV_DECODE_GUIDED) != 0;
@@ -1223,18 +1266,31 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
         uint64_t const resident = 2ull * (storage->compute_units > 0 ? storage->compute_units : 256);
         bool const stream_loads = chunk_tokens >= 2048 || static_cast<uint64_t>(grid.x) * grid.y > resident;
         PoolView const pv = pool_view(*storage);
-        if (head_split && stream_loads) {
-            decode_kernel<true, true><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
-                                                              chunk_tokens, query_heads, partials, writes, slots, tag);
-        } else if (head_split) {
-            decode_kernel<true, false><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
-                                                               chunk_tokens, query_heads, partials, writes, slots, tag);
-        } else if (stream_loads) {
-            decode_kernel<false, true><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
-                                                               chunk_tokens, query_heads, partials, writes, slots, tag);
+        auto go = [&](auto split, auto stream_kv, auto arg) {
+            constexpr bool kS = decltype(split)::value;
+            constexpr bool kT = decltype(stream_kv)::value;
+            constexpr bool kA = decltype(arg)::value;
+            std::conditional_t<kA, ArgPrefix, NoArgPrefix> ap{};
+            if constexpr (kA) {
+                for (uint32_t i = 0; i <= lane_count; ++i) ap.v[i] = host_prefix[i];
+            }
+            decode_kernel<kS, kT, kA><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
+                                                              chunk_tokens, query_heads, partials, writes, slots, tag,
+                                                              ap);
+        };
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        bool const arg_prefix = host_prefix != nullptr && lane_count <= KIMKV_DECODE_ARG_PREFIX_LANES;
+        if (arg_prefix) {
+            if (head_split && stream_loads) go(T_{}, T_{}, T_{});
+            else if (head_split) go(T_{}, F_{}, T_{});
+            else if (stream_loads) go(F_{}, T_{}, T_{});
+            else go(F_{}, F_{}, T_{});
         } else {
-            decode_kernel<false, false><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
-                                                                chunk_tokens, query_heads, partials, writes, slots, tag);
+            if (head_split && stream_loads) go(T_{}, T_{}, F_{});
+            else if (head_split) go(T_{}, F_{}, F_{});
+            else if (stream_loads) go(F_{}, T_{}, F_{});
+            else go(F_{}, F_{}, F_{});
         }
     }
     if (timed) kernel_timing_end(TimedKernel::Decode, s, start);
@@ -1411,6 +1467,27 @@ kimkv_status kimkv_paged_decode_write_batch_slots(const kimkv_storage* storage,
     return kimkv::launch_decode(storage, device_items, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
                                 query_heads, stream, nullptr, device_writes, true,
                                 static_cast<kimkv::DecodeLaneSlot*>(device_lane_slots));
+}
+
+kimkv_status kimkv_paged_decode_write_batch_slots_prefix(const kimkv_storage* storage,
+                                                         const kimkv_decode_item* device_items,
+                                                         const uint32_t* device_chunk_prefix,
+                                                         const uint32_t* host_chunk_prefix, uint32_t lane_count,
+                                                         uint32_t total_chunks, uint32_t chunk_flags,
+                                                         uint32_t query_heads, const kimkv_append_job* device_writes,
+                                                         void* device_lane_slots, kimkv_stream_t stream)
+{
+    if (device_writes == nullptr || device_lane_slots == nullptr || host_chunk_prefix == nullptr
+        || (reinterpret_cast<uintptr_t>(device_lane_slots) & 15u) != 0) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    // The copy in the arguments must describe the same launch.
+    if (lane_count != 0 && (host_chunk_prefix[0] != 0 || host_chunk_prefix[lane_count] != total_chunks)) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    return kimkv::launch_decode(storage, device_items, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
+                                query_heads, stream, nullptr, device_writes, true,
+                                static_cast<kimkv::DecodeLaneSlot*>(device_lane_slots), host_chunk_prefix);
 }
 
 kimkv_status kimkv_paged_decode_batch_noalloc(const kimkv_storage* storage, const kimkv_decode_item* device_items,

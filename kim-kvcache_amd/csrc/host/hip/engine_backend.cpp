@@ -388,9 +388,13 @@ public:
             auto const* items_d = reinterpret_cast<kimkv_decode_item const*>(staged);
             auto const* prefix_d = reinterpret_cast<std::uint32_t const*>(staged + prefix_at);
             auto const* writes_d = reinterpret_cast<kimkv_append_job const*>(staged + items_bytes);
+            // Small batches also carry the chunk prefix in the launch's
+            // arguments: every workgroup finds its lane without a round trip
+            // to the staged prefix (ragged lanes miss the kernel's guess).
             k = slots != nullptr
-                ? kimkv_paged_decode_write_batch_slots(st.handle(), items_d, prefix_d, static_cast<std::uint32_t>(n),
-                                                       total, chunk, QH, writes_d, slots, stream)
+                ? kimkv_paged_decode_write_batch_slots_prefix(st.handle(), items_d, prefix_d, pre.data(),
+                                                              static_cast<std::uint32_t>(n), total, chunk, QH,
+                                                              writes_d, slots, stream)
                 : kimkv_paged_decode_write_batch(st.handle(), items_d, prefix_d, static_cast<std::uint32_t>(n),
                                                  total, chunk, QH, writes_d, stream);
         }

@@ -17,6 +17,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "_lib", "libkimkv_hip.so")
 
 OK = 0
+INVALID_ARGUMENT = 1
 STATUS_NAMES = {
     0: "ok", 1: "invalid_argument", 2: "runtime_unavailable", 3: "allocation_failed",
     4: "submission_failed", 5: "not_ready", 6: "execution_failed", 7: "internal_error",
@@ -137,6 +138,11 @@ _SIGNATURES = {
     "kimkv_paged_decode_write_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                       ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                       ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]),
+    "kimkv_paged_decode_write_batch_slots_prefix": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p,
+                                                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
+                                                                    ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                                                    ctypes.c_void_p, ctypes.c_void_p,
+                                                                    ctypes.c_void_p]),
     "kimkv_paged_decode_write_batch_slots": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                             ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                             ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
@@ -423,6 +429,17 @@ class Storage:
                                                          ctypes.c_void_p(slots_ptr), _sh(stream)),
               "paged_decode_write_batch_slots")
 
+    def decode_write_slots_prefix_launch(self, items_ptr: int, prefix_ptr: int, host_prefix: np.ndarray,
+                                         lanes: int, total_chunks: int, chunk_tokens: int, query_heads: int,
+                                         writes_ptr: int, slots_ptr: int, stream: Optional[Stream] = None) -> int:
+        """kimkv_paged_decode_write_batch_slots_prefix (host_prefix: the chunk prefix as a host uint32 array,
+        carried in the launch's arguments for small launches); returns the status."""
+        hp = np.ascontiguousarray(host_prefix, dtype=np.uint32)
+        return lib().kimkv_paged_decode_write_batch_slots_prefix(
+            self.h, ctypes.c_void_p(items_ptr), ctypes.c_void_p(prefix_ptr), hp.ctypes.data_as(ctypes.c_void_p),
+            lanes, total_chunks, chunk_tokens, query_heads, ctypes.c_void_p(writes_ptr), ctypes.c_void_p(slots_ptr),
+            _sh(stream))
+
     def prefill_plan(self, new_token_counts, query_heads: int):
         """(tokens per workgroup, workgroup prefix over items, total workgroups)."""
         per = int(lib().kimkv_prefill_tokens_per_block(self.h, query_heads))
@@ -475,6 +492,7 @@ DECODE_HEAD_SPLIT = 0x80000000
 DECODE_GUIDED = 0x40000000
 DECODE_GUIDED_SLICES = 6
 DECODE_LANE_SLOT_BYTES = 32
+DECODE_ARG_PREFIX_LANES = 64
 
 # Fault bits of kimkv_storage_faults (include/kimkv_hip.h).
 FAULT_APPEND_JOB = 0x1

@@ -288,7 +288,18 @@ def _write_then_decode(dev, fused, tables, T, news, lanes_meta, QH, chunk, shape
         keep += [dbuf, qbuf, wbuf]
         outs.append(obuf)
     ibuf, pbuf, jbuf = dev.upload(items), dev.upload(prefix), dev.upload(jobs)
-    if fused == "slots":
+    if fused == "slots_prefix":
+        # The chunk prefix also in the launch's arguments: a wrong copy is refused without a launch,
+        # the right one gives the same pages and outputs.
+        slots = dev.DeviceBuffer(len(lanes) * dev.DECODE_LANE_SLOT_BYTES)
+        keep.append(slots)
+        bad = prefix.copy()
+        bad[-1] += 1
+        assert storage.decode_write_slots_prefix_launch(ibuf.ptr, pbuf.ptr, bad, len(lanes), total, chunk, QH,
+                                                        jbuf.ptr, slots.ptr) == dev.INVALID_ARGUMENT
+        assert storage.decode_write_slots_prefix_launch(ibuf.ptr, pbuf.ptr, prefix, len(lanes), total, chunk, QH,
+                                                        jbuf.ptr, slots.ptr) == 0
+    elif fused == "slots":
         # Merge records in device scratch holding leftovers: random bytes, then a first launch's records
         # (the second launch's tag differs, so none of them may be taken for its own).
         junk = np.random.default_rng(seed).integers(0, 256, len(lanes) * dev.DECODE_LANE_SLOT_BYTES, dtype=np.uint8)
@@ -339,13 +350,16 @@ def test_decode_write_batch_matches_append_then_decode(dev, mode):
     a, pa, total = _write_then_decode(dev, False, tables, T, news, layers, QH, chunk, shape, 24, cows)
     b, pb, _ = _write_then_decode(dev, True, tables, T, news, layers, QH, chunk, shape, 24, cows)
     c, pc, _ = _write_then_decode(dev, "slots", tables, T, news, layers, QH, chunk, shape, 24, cows)
+    d, pd, _ = _write_then_decode(dev, "slots_prefix", tables, T, news, layers, QH, chunk, shape, 24, cows)
     assert total > len(T)
     for i in range(len(T)):
         assert np.array_equal(pa[i], pb[i]), (mode, i)
         assert np.array_equal(a[i], b[i]), (mode, i)
-        # kimkv_paged_decode_write_batch_slots: the same pages and outputs.
+        # kimkv_paged_decode_write_batch_slots (and _prefix): the same pages and outputs.
         assert np.array_equal(pa[i], pc[i]), (mode, i)
         assert np.array_equal(a[i], c[i]), (mode, i)
+        assert np.array_equal(pa[i], pd[i]), (mode, i)
+        assert np.array_equal(a[i], d[i]), (mode, i)
     print(f"decode+write mode={mode} lanes={len(T)} chunks={total}", flush=True)
 
 
