@@ -38,6 +38,43 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+_HOST_CPU = None
+
+
+def host_cpu() -> dict:
+    """The host CPU the baselines run on, as lscpu reports it (model, sockets, cores per socket,
+    threads per core, logical CPUs), plus the CPUs this process may use (its affinity) and
+    os.cpu_count()."""
+    global _HOST_CPU
+    if _HOST_CPU is None:
+        info = {"model": platform.processor() or platform.machine()}
+        try:
+            import subprocess
+            out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+            fields = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+            fields = {k.strip(): v.strip() for k, v in fields.items()}
+            for key, name in (("Model name", "model"), ("Socket(s)", "sockets"),
+                              ("Core(s) per socket", "cores_per_socket"), ("Thread(s) per core", "threads_per_core"),
+                              ("CPU(s)", "logical_cpus")):
+                if key in fields:
+                    info[name] = int(fields[key]) if fields[key].isdigit() else fields[key]
+        except (OSError, ValueError, subprocess.SubprocessError):
+            pass
+        try:
+            info["usable_cpus"] = len(os.sched_getaffinity(0))
+        except (AttributeError, OSError):
+            pass
+        info["os_cpu_count"] = os.cpu_count()
+        _HOST_CPU = info
+    return _HOST_CPU
+
+
+def cpu_on_host(cpu: dict) -> dict:
+    """A cpu_baseline object with the host CPU it was measured on."""
+    cpu["host"] = host_cpu()
+    return cpu
+
+
 def permutation(seed: int, n: int) -> np.ndarray:
     """splitmix64 Fisher-Yates (kimkv_seeded_permutation), vectorised over the draws."""
     mask = np.uint64(0xFFFFFFFFFFFFFFFF)
@@ -473,7 +510,7 @@ def run_gather(dev, args) -> int:
                      "kernel": "gather_kernel", "launch_ms": round(ms, 4), "bytes_per_launch": moved},
         "config": {"workload": f"gather of one {T}-token sequence x {L} layers (4 kv heads x 64, fp16), "
                                f"{n_ext} extents in permuted slots + {k} micro pages"},
-        "steps": args.steps, "check": {"sampled_rows": 256, "mismatches": bad}, "cpu_baseline": cpu}), flush=True)
+        "steps": args.steps, "check": {"sampled_rows": 256, "mismatches": bad}, "cpu_baseline": cpu_on_host(cpu)}), flush=True)
     return 0 if bad == 0 else 1
 
 
@@ -524,7 +561,7 @@ def cpu_gather_baseline(args, entries, T, L, H, D, moved):
     return {"value": round(moved / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "us_per_launch": round(sec * 1e6, 1),
             "sample": f"the whole workload: oracle kvo_gather of the same {T}-token x {L}-layer table, mean of "
-                      f"{reps} calls on {platform.processor() or platform.machine()}",
+                      f"{reps} calls on {host_cpu()['model']}",
             "seconds": round(sec * reps, 2)}
 
 
@@ -636,7 +673,7 @@ def run_append(kimkv, dev, args) -> int:
     cpu = {"value": round(cpu_us, 2), "unit": "us/step", "cores": 1, "kind": "port",
            "gb_per_s": round(step_bytes / (cpu_us * 1e-6) / 1e9, 3),
            "sample": f"{steps_cpu} steps of {lanes} oracle kvo_append_tokens calls (1 token x {L} layers each) through "
-                     f"ctypes on {platform.processor() or platform.machine()}; page writes only, the page-table "
+                     f"ctypes on {host_cpu()['model']}; page writes only, the page-table "
                      f"metadata is this library's host code in both runs"}
     print(json.dumps({
         "metric": "ragged KV append (1 token x 22 layers per lane, tail allocation included) us/step",
@@ -656,7 +693,7 @@ def run_append(kimkv, dev, args) -> int:
                    "tokens": int(lengths.sum())},
         "steps": args.steps, "warmup": args.warmup,
         "check": {"lanes": checked, "mismatched_rows_blocks": bad, "bit_exact": bad == 0},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": cpu_on_host(cpu)}), flush=True)
     return 0 if bad == 0 else 1
 
 
@@ -763,9 +800,9 @@ def run_parity(kimkv, dev, args) -> int:
                      "kernel": "decode_kernel", "launch_ms": round(dec_ms, 4),
                      "timed_launches": dec_n, "bytes_per_launch": int(dec_bytes),
                      "note": "latency-bound: 4 lanes, 1.6 k tokens of K/V in one launch"},
-        "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
+        "cpu_baseline": cpu_on_host({"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
                          "sample": f"the decode of the whole step: oracle kvo_paged_decode of the 4 lanes, mean of "
-                                   f"{reps} on {platform.processor() or platform.machine()}"}}), flush=True)
+                                   f"{reps} on {host_cpu()['model']}"})}), flush=True)
     return 0 if ok else 1
 
 
@@ -966,7 +1003,7 @@ def run_shared(kimkv, dev, args) -> int:
     cpu = {"value": round(cpu_s * 1e6, 1), "unit": "us/layer", "cores": 1, "kind": "port",
            "gb_per_s": round(layer_bytes / cpu_s / 1e9, 4),
            "sample": f"the whole layer: oracle kvo_paged_decode of all {lanes} lanes (layer 0, last step) on "
-                     f"{platform.processor() or platform.machine()}",
+                     f"{host_cpu()['model']}",
            "seconds": round(cpu_s, 2),
            "all_cores": {"value": round(cpu_par_s * 1e6, 1), "unit": "us/layer", "cores": threads,
                          "gb_per_s": round(layer_bytes / cpu_par_s / 1e9, 4), "seconds": round(cpu_par_s, 2)}}
@@ -992,7 +1029,7 @@ def run_shared(kimkv, dev, args) -> int:
         "steps": args.steps, "warmup": args.warmup,
         "check": {"lanes": lanes, "layer": 0, "max_abs_err": worst, "within_tolerance": ok,
                   "tolerance": "2e-3 + 1e-3*|ref|"},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": cpu_on_host(cpu)}), flush=True)
     return 0 if ok else 1
 
 
@@ -1115,7 +1152,7 @@ def run_prefill(kimkv, dev, args) -> int:
            "us_per_launch_equivalent": round(flops / (cpu_tflops * 1e12) * 1e6, 1),
            "sample": f"the check's {rows} query rows (one token's GQA decode over its {cpu_pairs // rows}-token mean "
                      f"causal context each, page setup included) by the oracle's kvo_paged_decode on "
-                     f"{platform.processor() or platform.machine()}, {round(cpu_s, 2)} s",
+                     f"{host_cpu()['model']}, {round(cpu_s, 2)} s",
            "seconds": round(cpu_s, 2)}
     print(json.dumps({
         "metric": "chunked-prefill causal paged GQA attention (MFMA) TFLOP/s",
@@ -1139,7 +1176,7 @@ def run_prefill(kimkv, dev, args) -> int:
         "steps": args.steps, "warmup": args.warmup,
         "check": {"rows": rows, "layers": [0, L - 1], "max_abs_err": worst, "within_tolerance": ok,
                   "tolerance": "2e-3 + 1e-3*|ref|"},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": cpu_on_host(cpu)}), flush=True)
     return 0 if ok else 1
 
 
@@ -1264,7 +1301,7 @@ def run_e2e(kimkv, dev, args) -> int:
            "kind": "port",
            "sample": f"the check's {fwd_n} single-token forwards (positions 0-{fwd_n - 1}) through the oracle's "
                      f"fp32/fp16-rounded numpy model of the same weights on "
-                     f"{platform.processor() or platform.machine()}, {round(fwd_s, 2)} s; no batching",
+                     f"{host_cpu()['model']}, {round(fwd_s, 2)} s; no batching",
            "seconds": round(fwd_s, 2)}
     sched.close()
     runner.close()
@@ -1293,7 +1330,7 @@ def run_e2e(kimkv, dev, args) -> int:
                      "flops_per_step": round(lin_flops / args.steps),
                      "note": "FLOPs of the 22 layers' four linear projections (2 x 968.9 M weights per token) "
                              "over the step's wall time; attention and the LM head are not counted"},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": cpu_on_host(cpu)}), flush=True)
     return 0 if ok else 1
 
 
@@ -1510,7 +1547,7 @@ def main() -> int:
                  "within_tolerance": all(ok for _, ok in errs), "tolerance": "2e-3 + 1e-3*|ref|"}
         cpu = {"value": round(cpu_bytes / cpu_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": f"oracle kvo_paged_decode, {args.cpu_lanes} lanes x 1 layer x {w.lane_tokens(last)} tokens "
-                         f"(QH=32, H=4, D=64), {cpu_s:.1f}s on {platform.processor() or platform.machine()}",
+                         f"(QH=32, H=4, D=64), {cpu_s:.1f}s on {host_cpu()['model']}",
                "seconds": round(cpu_s, 2),
                "all_cores": {"value": round(cpu_bytes / cpu_par_s / 1e9, 4), "unit": "GB/s", "cores": threads,
                              "seconds": round(cpu_par_s, 2),
@@ -1556,7 +1593,7 @@ def main() -> int:
                      "timed_launches": decode_launches, "launches": launches,
                      "lanes_per_launch": lanes_per_launch,
                      "bytes_per_launch": int(per_launch_decode_bytes)},
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu_on_host(cpu),
         "check": check,
         "timing": {"gpu_event_ms": round(gpu_ms, 3), "wall_ms": round(wall_ms, 3)},
         "host": ({"path": "engine", "reserve_ms_per_step": round(w.reserve_s * 1000 / args.steps, 3),
