@@ -69,8 +69,11 @@ def host_cpu() -> dict:
     return _HOST_CPU
 
 
-def cpu_on_host(cpu: dict) -> dict:
-    """A cpu_baseline object with the host CPU it was measured on."""
+def cpu_on_host(cpu: dict | None) -> dict | None:
+    """A cpu_baseline object with the host CPU it was measured on (None when the baseline was
+    skipped)."""
+    if cpu is None:
+        return None
     cpu["host"] = host_cpu()
     return cpu
 

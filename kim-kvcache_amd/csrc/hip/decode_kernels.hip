@@ -541,10 +541,13 @@ __device__ inline bool decode_item_valid(const PoolView& P, const kimkv_decode_i
 }
 
 // LDS of a decode workgroup: the chunk's group table (also the buffer the
-// head-split merge uses) and the per-wave token records of the generic path.
+// head-split merge uses), the per-wave token records of the generic path and
+// the lane's write job, kept for the stores at the workgroup's end (the
+// caller's job array may live in host memory, a round trip away).
 struct DecodeLds {
     __attribute__((aligned(16))) GroupEntry groups[kMaxGroups];
     WaveTokens wave_tokens[kHeadsPerBlock];
+    kimkv_append_job job;
     uint32_t idx0;
     uint32_t dok;
     uint32_t generic;
@@ -911,6 +914,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     bool const writer = job.token_count != 0 && c1 == T && wh0 < H;
     if (writer && !job_ok) report_fault(P, KIMKV_FAULT_APPEND_JOB);
     JobView const jv = job_view(P, job, job_ok);
+    if (tid == 0) lds.job = job;   // visible after build_chunk_table's barriers
     bool const fast = build_chunk_table(P, item, QH, c0, c1, lds, jv);
 
     uint32_t const wave = tid >> 6;
@@ -934,9 +938,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     } else if (blockIdx.y < H) {
         decode_head_split_chunk<kStream>(P, item, blockIdx.y, QH, c0, c1, chunk_index, single, fast, lds, jv);
     }
-    // The job is read again here rather than kept in registers across the
-    // streaming loop.
-    if (writer && job_ok) write_token_heads(P, writes[lane], item.layer, wh0, wh1);
+    // The job comes back from LDS rather than staying in registers across
+    // the streaming loop.
+    if (writer && job_ok) write_token_heads(P, lds.job, item.layer, wh0, wh1);
 }
 
 // Slices of a lane of T tokens in the guided mode: at most six, and no more
@@ -1008,6 +1012,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         bool const writer = job.token_count != 0 && c1 == T;
         if (writer && !job_ok) report_fault(P, KIMKV_FAULT_APPEND_JOB);
         JobView const jv = job_view(P, job, job_ok);
+        if (tid == 0) lds.job = job;   // the previous unit ended with a barrier
         if (c0 >= c1) {
             // An empty slice still leaves its partial: weight zero in the merge.
             uint32_t const r = tid >> 4;
@@ -1021,7 +1026,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         bool const fast = build_chunk_table(P, item, QH, c0, c1, lds, jv);
         decode_head_split_chunk<true>(P, item, h, QH, c0, c1, k, n == 1, fast, lds, jv);
         // The last slice (never empty) stores the job's positions of head h.
-        if (writer && job_ok) write_token_heads(P, writes[lane], item.layer, h, h + 1);
+        if (writer && job_ok) write_token_heads(P, lds.job, item.layer, h, h + 1);
         __syncthreads();   // the next unit rebuilds the table in the same LDS
     }
     if (tid == 0) {
