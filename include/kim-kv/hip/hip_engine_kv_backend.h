@@ -112,4 +112,10 @@ void attendPrefillBatch(PrefillChunk* const* chunks, std::size_t count, std::uin
 // The backend's device storage handle (kimkv_storage*), for data-path helpers.
 [[nodiscard]] void const* engineStorage(EngineKvBackend const& backend) noexcept;
 
+// Batched attention launches that read their lanes from device lane records
+// (kimkv_paged_decode_lanes: at most 64 lanes whose per-layer addresses are
+// evenly spaced) rather than from items staged in host memory; 0 when
+// `backend` is not a HIP backend.  No reference counterpart.
+[[nodiscard]] std::uint64_t laneRecordLaunches(EngineKvBackend const& backend) noexcept;
+
 }  // namespace kimkvcache

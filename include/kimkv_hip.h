@@ -398,6 +398,65 @@ kimkv_status kimkv_paged_decode_write_batch_slots_prefix(const kimkv_storage* st
                                                          uint32_t query_heads, const kimkv_append_job* device_writes,
                                                          void* device_lane_slots, kimkv_stream_t stream);
 
+/* The part of one lane of a batched decode that stays the same for every
+ * layer of a token step: the lane's block table and token count, and the
+ * destination of its single-token write (the write job of
+ * kimkv_paged_decode_write_batch without its per-layer source rows).  32
+ * bytes; kept by the caller in device memory across the step's layers. */
+typedef struct kimkv_decode_lane {
+    const kimkv_block_desc* descriptors;
+    uint32_t descriptor_count;
+    uint32_t token_count;
+    uint32_t dst_slot;       /* the write, when has_write != 0 */
+    uint32_t cow_slot;
+    uint16_t dst_token;
+    uint16_t cow_tokens;
+    uint8_t dst_kind;
+    uint8_t cow_kind;
+    uint8_t has_write;
+    uint8_t reserved;
+} kimkv_decode_lane;
+
+/* The per-layer part of such a launch: lane i reads its query at
+ * query + i * query_stride, writes output + i * output_stride, uses workspace
+ * + i * workspace_stride when it has more than one chunk, and its write job
+ * takes its new K and V rows ([kv_heads][head_dim] fp16) from key + i *
+ * key_stride and value + i * value_stride (strides in bytes; arithmetic
+ * modulo 2^64, so a negative stride works). */
+typedef struct kimkv_decode_layer_args {
+    uint32_t layer;
+    float attention_scale;
+    const uint16_t* query;
+    uint64_t query_stride;
+    uint16_t* output;
+    uint64_t output_stride;
+    float* workspace;
+    uint64_t workspace_stride;
+    const uint16_t* key;
+    uint64_t key_stride;
+    const uint16_t* value;
+    uint64_t value_stride;
+} kimkv_decode_layer_args;
+
+/* kimkv_paged_decode_write_batch_slots_prefix with each lane's item and write
+ * job assembled in the kernel from device_lanes[lane] (device memory) and
+ * *args (copied into the launch's arguments): a workgroup's only read before
+ * its block table is one device-memory record, where the item form reads the
+ * caller's items and jobs (in mapped host memory when the engine stages
+ * them, a round trip to the host).  For a caller whose lanes' queries,
+ * outputs, workspaces and new rows are evenly spaced (base + lane * stride),
+ * which keeps the lane records across a step's layers.  lane_count at most
+ * KIMKV_DECODE_ARG_PREFIX_LANES; host_chunk_prefix as for the _prefix form;
+ * device_lane_slots required when total_chunks > lane_count; not with
+ * KIMKV_DECODE_GUIDED.  Anything else returns KIMKV_INVALID_ARGUMENT and
+ * launches nothing.  Same results as the item form with the same items and
+ * jobs.  No counterpart in the reference. */
+kimkv_status kimkv_paged_decode_lanes(const kimkv_storage* storage, const kimkv_decode_lane* device_lanes,
+                                      const uint32_t* device_chunk_prefix, const uint32_t* host_chunk_prefix,
+                                      uint32_t lane_count, uint32_t total_chunks, uint32_t chunk_flags,
+                                      uint32_t query_heads, const kimkv_decode_layer_args* args,
+                                      void* device_lane_slots, kimkv_stream_t stream);
+
 /* Size of the device scratch array of kimkv_paged_decode_batch_noalloc. */
 #define KIMKV_DECODE_SCRATCH_BYTES (16u << 20)
 

@@ -186,6 +186,11 @@ int kimkv_engine_block_table(const kimkv_engine* e, uint64_t request_id, uint64_
                              kimkv_mapping_entry* entries, uint32_t capacity, uint32_t* count);
 /* The engine's device storage (for data-path helpers such as kimkv_gather). */
 const kimkv_storage* kimkv_engine_storage(const kimkv_engine* e);
+/* Batched attention launches that read their lanes from device lane records
+ * (kimkv_paged_decode_lanes) instead of items staged in host memory: batches
+ * of at most 64 lanes whose queries, outputs, workspaces and new K/V rows are
+ * evenly spaced.  No reference counterpart (a test hook for which path ran). */
+uint64_t kimkv_engine_lane_record_launches(const kimkv_engine* e);
 /* Bulk prompt append (no reference counterpart: the reference engine appends
  * one token per transaction).  device_kv is [layer][K/V][token_count][head][dim]
  * fp16; waits for the copy, seals a full tail and, when promote != 0,

@@ -790,6 +790,9 @@ static_assert(sizeof(DecodeLaneSlot) == KIMKV_DECODE_LANE_SLOT_BYTES, "slot size
 // kStream: non-temporal K/V loads (load_kv).
 // slots: when non-null, each lane's merge record (DecodeLaneSlot, tagged
 // `tag`) for the merge launch.
+// kSrc / lanes / sa: where a workgroup gets its lane, item and job (LaneSource
+// below); lanes is read only by kRecords launches, items and writes only by
+// the others.
 // The grid has one workgroup per chunk (x) and head block (y); the merge
 // launch follows when gridDim.x > lane_count, and a lane of several chunks
 // in a launch without it is reported and skipped.  A lane of no tokens is
@@ -804,11 +807,64 @@ struct ArgPrefix {
 };
 struct NoArgPrefix {};
 
-template <bool kSplit, bool kStream, bool kArgPrefix>
+// Where a workgroup finds its lane and reads the lane's item and write job.
+enum class LaneSource {
+    kGuess,       // items[] and writes[]; lane guessed from the chunk, checked against prefix[]
+    kArgPrefix,   // items[] and writes[]; lane from the prefix in the launch arguments
+    kRecords,     // lane from the prefix in the arguments; item and job built from a
+                  // step-constant kimkv_decode_lane in device memory and the layer arguments
+};
+
+// Arguments of a kRecords launch: the prefix and the per-layer addresses.
+struct RecordArgs {
+    ArgPrefix ap;
+    kimkv_decode_layer_args layer;
+};
+
+template <LaneSource kSrc>
+using SourceArgs = std::conditional_t<kSrc == LaneSource::kGuess, NoArgPrefix,
+                                      std::conditional_t<kSrc == LaneSource::kArgPrefix, ArgPrefix, RecordArgs>>;
+
+template <typename T>
+__device__ inline T* at_stride(T* base, uint64_t stride, uint32_t i)
+{
+    return reinterpret_cast<T*>(reinterpret_cast<uintptr_t>(base) + stride * i);
+}
+
+// The item and write job of lane i of a kRecords launch: what the engine
+// would stage for it, from its step record and the layer's arguments.
+__device__ inline void record_lane(const kimkv_decode_lane& r, const kimkv_decode_layer_args& a, uint32_t i,
+                                   kimkv_decode_item& item, kimkv_append_job& job)
+{
+    item.descriptors = r.descriptors;
+    item.descriptor_count = r.descriptor_count;
+    item.token_count = r.token_count;
+    item.layer = a.layer;
+    item.query = at_stride(a.query, a.query_stride, i);
+    item.workspace = a.workspace != nullptr ? at_stride(a.workspace, a.workspace_stride, i) : nullptr;
+    item.output = at_stride(a.output, a.output_stride, i);
+    item.attention_scale = a.attention_scale;
+    job = kimkv_append_job{};
+    if (r.has_write != 0) {
+        job.src_key = at_stride(a.key, a.key_stride, i);
+        job.src_value = at_stride(a.value, a.value_stride, i);
+        job.layer_begin = a.layer;
+        job.layer_count = 1;
+        job.token_count = 1;
+        job.dst_slot = r.dst_slot;
+        job.cow_slot = r.cow_slot;
+        job.dst_token = r.dst_token;
+        job.cow_tokens = r.cow_tokens;
+        job.dst_kind = r.dst_kind;
+        job.cow_kind = r.cow_kind;
+    }
+}
+
+template <bool kSplit, bool kStream, LaneSource kSrc>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
     PoolView P, const kimkv_decode_item* items, const uint32_t* prefix, uint32_t lane_count, uint32_t chunk_tokens,
     uint32_t QH, float* partials, const kimkv_append_job* writes, DecodeLaneSlot* slots, uint64_t tag,
-    std::conditional_t<kArgPrefix, ArgPrefix, NoArgPrefix> ap)
+    const kimkv_decode_lane* lanes, SourceArgs<kSrc> sa)
 {
     __shared__ DecodeLds lds;
     __shared__ uint32_t s_lane;
@@ -826,9 +882,16 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t lane_end = 0;
     kimkv_decode_item item;
     kimkv_append_job job;
-    if constexpr (kArgPrefix) {
+    if constexpr (kSrc != LaneSource::kGuess) {
         // The last lane whose first chunk is <= chunk_id (scalar loads of the
         // launch arguments), then one round trip for its item and job.
+        ArgPrefix const& ap = [&]() -> ArgPrefix const& {
+            if constexpr (kSrc == LaneSource::kArgPrefix) {
+                return sa;
+            } else {
+                return sa.ap;
+            }
+        }();
         uint32_t lo = 0;
         uint32_t hi = lane_count;
         while (hi - lo > 1) {
@@ -846,8 +909,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             report_fault(P, KIMKV_FAULT_DECODE_ITEM);
             return;
         }
-        item = items[lane];
-        job = writes != nullptr ? writes[lane] : kimkv_append_job{};
+        if constexpr (kSrc == LaneSource::kArgPrefix) {
+            item = items[lane];
+            job = writes != nullptr ? writes[lane] : kimkv_append_job{};
+        } else {
+            record_lane(lanes[lane], sa.layer, lane, item, job);
+        }
     } else {
         // The prologue is a chain of dependent global reads, and under full
         // HBM load each costs microseconds while this workgroup streams
@@ -1230,12 +1297,20 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
                            const uint32_t* device_chunk_prefix, uint32_t lane_count, uint32_t total_chunks,
                            uint32_t chunk_flags, uint32_t query_heads, kimkv_stream_t stream, float* partials,
                            const kimkv_append_job* writes, bool timed, DecodeLaneSlot* slots = nullptr,
-                           const uint32_t* host_prefix = nullptr)
+                           const uint32_t* host_prefix = nullptr, const kimkv_decode_lane* lanes = nullptr,
+                           const kimkv_decode_layer_args* layer_args = nullptr)
 {
     bool const head_split = (chunk_flags & KIMKV_DECODE_HEAD_SPLIT) != 0;
     bool const guided = (chunk_flags & KIMKV_DECODE_GUIDED) != 0;
     uint32_t const chunk_tokens = chunk_flags & ~(KIMKV_DECODE_HEAD_SPLIT | KIMKV_DECODE_GUIDED);
-    if (storage == nullptr || device_items == nullptr || device_chunk_prefix == nullptr || lane_count == 0
+    // Lane records: the prefix travels in the arguments, and the merge reads
+    // the decode launch's lane slots (there are no items to read).
+    bool const records = lanes != nullptr;
+    if (records && (layer_args == nullptr || host_prefix == nullptr || lane_count > KIMKV_DECODE_ARG_PREFIX_LANES
+                    || guided || (total_chunks > lane_count && slots == nullptr))) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    if (storage == nullptr || (device_items == nullptr && !records) || device_chunk_prefix == nullptr || lane_count == 0
         || query_heads == 0 || query_heads % storage->layout.kv_heads != 0 || storage->layout.head_dim > 256
         || (head_split && guided)
         || (!guided && (chunk_tokens == 0 || chunk_tokens % 64 != 0 || chunk_tokens > kMaxChunk))) {
@@ -1271,31 +1346,35 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
         uint64_t const resident = 2ull * (storage->compute_units > 0 ? storage->compute_units : 256);
         bool const stream_loads = chunk_tokens >= 2048 || static_cast<uint64_t>(grid.x) * grid.y > resident;
         PoolView const pv = pool_view(*storage);
-        auto go = [&](auto split, auto stream_kv, auto arg) {
+        auto go = [&](auto split, auto stream_kv, auto src) {
             constexpr bool kS = decltype(split)::value;
             constexpr bool kT = decltype(stream_kv)::value;
-            constexpr bool kA = decltype(arg)::value;
-            std::conditional_t<kA, ArgPrefix, NoArgPrefix> ap{};
-            if constexpr (kA) {
-                for (uint32_t i = 0; i <= lane_count; ++i) ap.v[i] = host_prefix[i];
+            constexpr LaneSource kL = decltype(src)::value;
+            SourceArgs<kL> sa{};
+            if constexpr (kL == LaneSource::kArgPrefix) {
+                for (uint32_t i = 0; i <= lane_count; ++i) sa.v[i] = host_prefix[i];
+            } else if constexpr (kL == LaneSource::kRecords) {
+                for (uint32_t i = 0; i <= lane_count; ++i) sa.ap.v[i] = host_prefix[i];
+                sa.layer = *layer_args;
             }
-            decode_kernel<kS, kT, kA><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
+            decode_kernel<kS, kT, kL><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
                                                               chunk_tokens, query_heads, partials, writes, slots, tag,
-                                                              ap);
+                                                              lanes, sa);
         };
-        using T_ = std::true_type;
-        using F_ = std::false_type;
-        bool const arg_prefix = host_prefix != nullptr && lane_count <= KIMKV_DECODE_ARG_PREFIX_LANES;
-        if (arg_prefix) {
-            if (head_split && stream_loads) go(T_{}, T_{}, T_{});
-            else if (head_split) go(T_{}, F_{}, T_{});
-            else if (stream_loads) go(F_{}, T_{}, T_{});
-            else go(F_{}, F_{}, T_{});
+        auto pick = [&](auto src) {
+            using T_ = std::true_type;
+            using F_ = std::false_type;
+            if (head_split && stream_loads) go(T_{}, T_{}, src);
+            else if (head_split) go(T_{}, F_{}, src);
+            else if (stream_loads) go(F_{}, T_{}, src);
+            else go(F_{}, F_{}, src);
+        };
+        if (records) {
+            pick(std::integral_constant<LaneSource, LaneSource::kRecords>{});
+        } else if (host_prefix != nullptr && lane_count <= KIMKV_DECODE_ARG_PREFIX_LANES) {
+            pick(std::integral_constant<LaneSource, LaneSource::kArgPrefix>{});
         } else {
-            if (head_split && stream_loads) go(T_{}, T_{}, F_{});
-            else if (head_split) go(T_{}, F_{}, F_{});
-            else if (stream_loads) go(F_{}, T_{}, F_{});
-            else go(F_{}, F_{}, F_{});
+            pick(std::integral_constant<LaneSource, LaneSource::kGuess>{});
         }
     }
     if (timed) kernel_timing_end(TimedKernel::Decode, s, start);
@@ -1493,6 +1572,26 @@ kimkv_status kimkv_paged_decode_write_batch_slots_prefix(const kimkv_storage* st
     return kimkv::launch_decode(storage, device_items, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
                                 query_heads, stream, nullptr, device_writes, true,
                                 static_cast<kimkv::DecodeLaneSlot*>(device_lane_slots), host_chunk_prefix);
+}
+
+kimkv_status kimkv_paged_decode_lanes(const kimkv_storage* storage, const kimkv_decode_lane* device_lanes,
+                                      const uint32_t* device_chunk_prefix, const uint32_t* host_chunk_prefix,
+                                      uint32_t lane_count, uint32_t total_chunks, uint32_t chunk_flags,
+                                      uint32_t query_heads, const kimkv_decode_layer_args* args,
+                                      void* device_lane_slots, kimkv_stream_t stream)
+{
+    static_assert(sizeof(kimkv_decode_lane) == 32, "lane record is 32 bytes");
+    if (device_lanes == nullptr || args == nullptr || host_chunk_prefix == nullptr
+        || (reinterpret_cast<uintptr_t>(device_lane_slots) & 15u) != 0) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    if (lane_count != 0 && (host_chunk_prefix[0] != 0 || host_chunk_prefix[lane_count] != total_chunks)) {
+        return KIMKV_INVALID_ARGUMENT;
+    }
+    return kimkv::launch_decode(storage, nullptr, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
+                                query_heads, stream, nullptr, nullptr, true,
+                                static_cast<kimkv::DecodeLaneSlot*>(device_lane_slots), host_chunk_prefix,
+                                device_lanes, args);
 }
 
 kimkv_status kimkv_paged_decode_batch_noalloc(const kimkv_storage* storage, const kimkv_decode_item* device_items,

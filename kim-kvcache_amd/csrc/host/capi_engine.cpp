@@ -156,6 +156,11 @@ const kimkv_storage* kimkv_engine_storage(const kimkv_engine* e)
     return static_cast<const kimkv_storage*>(engineStorage(*e->backend));
 }
 
+uint64_t kimkv_engine_lane_record_launches(const kimkv_engine* e)
+{
+    return laneRecordLaunches(*e->backend);
+}
+
 int kimkv_engine_append_prefill(kimkv_engine* e, uint64_t id, uint32_t n, const uint16_t* device_kv,
                                 kimkv_stream_t stream, int promote, uint32_t* promoted)
 {

@@ -142,10 +142,86 @@ struct BackendState final {
     std::atomic<std::uint64_t> batched_attention_submissions{0};
     std::atomic<std::uint64_t> batched_attention_lanes{0};
     std::atomic<std::uint64_t> batched_write_submissions{0};
+    std::atomic<std::uint64_t> lane_record_launches{0};   // of batched_attention_submissions
     std::atomic<std::uint64_t> next_transaction_id{1};
     mutable std::mutex mutex;
     std::mutex event_mutex;
     std::vector<void*> free_events;   // completion events of finished transactions
+
+    // Device copies of the lane records (kimkv_decode_lane + chunk prefix)
+    // of recent batched attention launches, a few per stream.  The layers of
+    // a token step launch the same lanes with the same records, so the copy
+    // is made when a stream asks for the same records a second time (the
+    // step's second layer: a one-layer step never pays for a copy) and reused
+    // by the later layers.  An entry is written only by copies on its own
+    // stream, which run after that stream's earlier launches that read it,
+    // and is never freed before the backend.  Guarded by the storage's launch
+    // mutex.
+    struct LaneRecords {
+        HipStream stream{nullptr};
+        std::vector<unsigned char> bytes;   // what `device` holds
+        DeviceMemory device;
+        std::uint64_t used{0};
+    };
+    struct LaneRecordsSeen {
+        HipStream stream{nullptr};
+        std::vector<unsigned char> bytes;   // the stream's last request without a copy
+    };
+    std::vector<LaneRecordsSeen> lane_records_seen;
+    static constexpr std::size_t kLaneRecordsPerStream = 4;
+    static constexpr std::size_t kLaneRecordEntries = 64;
+    static constexpr std::size_t kLaneRecordBytes =
+        KIMKV_DECODE_ARG_PREFIX_LANES * sizeof(kimkv_decode_lane) + (KIMKV_DECODE_ARG_PREFIX_LANES + 1) * 4;
+    std::vector<LaneRecords> lane_records;
+    std::uint64_t lane_record_clock{0};
+
+    // Device address of `bytes` for launches on `stream`: an entry already
+    // holding them, or, when the stream asked for the same bytes last time,
+    // one of the stream's entries refilled by a copy on the stream.  nullptr
+    // otherwise (the caller stages the launch another way).
+    void const* laneRecords(std::vector<unsigned char> const& bytes, HipStream stream)
+    {
+        if (bytes.size() > kLaneRecordBytes) return nullptr;
+        LaneRecords* victim = nullptr;
+        std::size_t mine = 0;
+        for (LaneRecords& e : lane_records) {
+            if (e.stream != stream) continue;
+            if (e.bytes == bytes) {
+                e.used = ++lane_record_clock;
+                return e.device.get();
+            }
+            ++mine;
+            if (victim == nullptr || e.used < victim->used) victim = &e;
+        }
+        LaneRecordsSeen* seen = nullptr;
+        for (LaneRecordsSeen& e : lane_records_seen) {
+            if (e.stream == stream) seen = &e;
+        }
+        if (seen == nullptr) {
+            if (lane_records_seen.size() >= kLaneRecordEntries) return nullptr;
+            lane_records_seen.push_back(LaneRecordsSeen{stream, {}});
+            seen = &lane_records_seen.back();
+        }
+        if (seen->bytes != bytes) {   // first request: remember it, copy nothing yet
+            seen->bytes = bytes;
+            return nullptr;
+        }
+        seen->bytes.clear();
+        if (mine < kLaneRecordsPerStream && lane_records.size() < kLaneRecordEntries) {
+            LaneRecords e;
+            e.stream = stream;
+            e.device = DeviceMemory(kLaneRecordBytes);
+            if (e.device.get() == nullptr) return nullptr;
+            lane_records.push_back(std::move(e));
+            victim = &lane_records.back();
+        }
+        if (victim == nullptr) return nullptr;
+        victim->bytes.clear();   // unknown contents until the copy is queued
+        if (!storage.ring().uploadTo(victim->device.get(), bytes.data(), bytes.size(), stream)) return nullptr;
+        victim->bytes = bytes;
+        victim->used = ++lane_record_clock;
+        return victim->device.get();
+    }
 
     BackendState(EngineKvConfig c, std::uint32_t micro, std::uint32_t extent)
         : config(c), manager(micro, extent), storage(c.kv_layout, micro, extent)
@@ -304,6 +380,82 @@ public:
         return {};
     }
 
+    // The per-layer arguments of kimkv_paged_decode_lanes for the first n
+    // launched lanes: true when they attend one layer with one scale, every
+    // lane or none writes a token (a one-token, one-layer job), and each of
+    // their queries, outputs, workspaces and new K / V rows sits at base +
+    // lane * stride.  Lanes whose chunk needs no workspace get the evenly
+    // spaced address too; the kernel uses it only for multi-chunk lanes,
+    // whose workspaces were checked.
+    static bool evenLayerArgs(PagedDecodeBatch const& batch, std::vector<std::size_t> const& launched,
+                              std::vector<kimkv_append_job> const& writes, std::size_t n,
+                              kimkv_decode_layer_args& a)
+    {
+        DevicePagedDecodeBatchItem const* h = batch.host_items;
+        bool const writing = writes[0].token_count != 0;
+        for (std::size_t i = 0; i < n; ++i) {
+            kimkv_append_job const& w = writes[i];
+            if (h[i].layer != h[0].layer || h[i].attention_scale != h[0].attention_scale
+                || (w.token_count != 0) != writing) {
+                return false;
+            }
+            if (writing && (w.token_count != 1 || w.layer_count != 1 || w.layer_begin != h[i].layer
+                            || w.src_layer_stride != 0 || w.src_token_stride != 0)) {
+                return false;
+            }
+        }
+        auto even = [n](auto at, auto& base, std::uint64_t& stride) {
+            auto const b = reinterpret_cast<std::uintptr_t>(at(0));
+            stride = n > 1 ? static_cast<std::uint64_t>(reinterpret_cast<std::uintptr_t>(at(1)) - b) : 0;
+            for (std::size_t i = 2; i < n; ++i) {
+                if (reinterpret_cast<std::uintptr_t>(at(i)) != b + stride * i) return false;
+            }
+            base = at(0);
+            return true;
+        };
+        a = kimkv_decode_layer_args{};
+        a.layer = h[0].layer;
+        a.attention_scale = h[0].attention_scale;
+        bool ok = even([h](std::size_t i) { return reinterpret_cast<std::uint16_t const*>(h[i].device_query); },
+                       a.query, a.query_stride)
+            && even([h](std::size_t i) { return reinterpret_cast<std::uint16_t*>(h[i].device_output); }, a.output,
+                    a.output_stride)
+            && even([&](std::size_t i) { return static_cast<float*>(batch.items[launched[i]].request.device_workspace); },
+                    a.workspace, a.workspace_stride);
+        if (ok && writing) {
+            ok = even([&](std::size_t i) { return writes[i].src_key; }, a.key, a.key_stride)
+                && even([&](std::size_t i) { return writes[i].src_value; }, a.value, a.value_stride);
+        }
+        return ok;
+    }
+
+    // kimkv_decode_lane records of the first n launched lanes followed by
+    // their chunk prefix: the bytes kimkv_paged_decode_lanes reads.
+    static void laneRecordBytes(DevicePagedDecodeBatchItem const* h, std::vector<kimkv_append_job> const& writes,
+                                std::vector<std::uint32_t> const& pre, std::size_t n,
+                                std::vector<unsigned char>& out)
+    {
+        out.assign(n * sizeof(kimkv_decode_lane) + (n + 1) * sizeof(std::uint32_t), 0);
+        for (std::size_t i = 0; i < n; ++i) {
+            kimkv_decode_lane r{};
+            r.descriptors = reinterpret_cast<kimkv_block_desc const*>(h[i].device_descriptors);
+            r.descriptor_count = h[i].descriptor_count;
+            r.token_count = h[i].token_count;
+            kimkv_append_job const& w = writes[i];
+            if (w.token_count != 0) {
+                r.dst_slot = w.dst_slot;
+                r.cow_slot = w.cow_slot;
+                r.dst_token = w.dst_token;
+                r.cow_tokens = w.cow_tokens;
+                r.dst_kind = w.dst_kind;
+                r.cow_kind = w.cow_kind;
+                r.has_write = 1;
+            }
+            std::memcpy(out.data() + i * sizeof(r), &r, sizeof(r));
+        }
+        std::memcpy(out.data() + n * sizeof(kimkv_decode_lane), pre.data(), (n + 1) * sizeof(std::uint32_t));
+    }
+
     void attendLayerBatch(PagedDecodeBatch& batch) override
     {
         std::vector<HipTokenTransaction*> lanes;
@@ -364,22 +516,45 @@ public:
         std::vector<std::uint32_t> pre(n + 1, 0);
         for (std::size_t i = 0; i < n; ++i) pre[i + 1] = pre[i] + kimkv_decode_lane_chunks(launch_tokens[i], chunk, D);
         total = pre[n];
-        // Items and chunk prefix are staged together in pinned host memory
-        // that the kernels read directly (a copy command on the stream would
-        // cost a dispatch and a gap between kernels); the caller's
-        // device_items scratch is validated by the API but not needed here.
+        std::lock_guard<std::mutex> lock(o.storage.launchMutex());
+        HipStream const stream = stream_;
+        kimkv_status k = KIMKV_SUBMISSION_FAILED;
+        bool launched_from_records = false;
+        kimkv_decode_layer_args args{};
+        if (n <= KIMKV_DECODE_ARG_PREFIX_LANES && evenLayerArgs(batch, launched, writes, n, args)) {
+            // Every lane's step-constant record from a device copy the step's
+            // first layer made: no workgroup reads host memory before its
+            // block table.
+            thread_local std::vector<unsigned char> records;
+            laneRecordBytes(batch.host_items, writes, pre, n, records);
+            void const* dev = o.laneRecords(records, stream);
+            void* slots = total > n ? st.ring().deviceScratch(n * KIMKV_DECODE_LANE_SLOT_BYTES, stream) : nullptr;
+            if (dev != nullptr && (total == n || slots != nullptr)) {
+                auto const* lanes_d = static_cast<kimkv_decode_lane const*>(dev);
+                auto const* prefix_d = reinterpret_cast<std::uint32_t const*>(lanes_d + n);
+                k = kimkv_paged_decode_lanes(st.handle(), lanes_d, prefix_d, pre.data(), static_cast<std::uint32_t>(n),
+                                             total, chunk, QH, &args, slots, stream);
+                launched_from_records = true;
+                if (k == KIMKV_OK) o.lane_record_launches.fetch_add(1, std::memory_order_relaxed);
+            }
+        }
+        // Otherwise items, write jobs and chunk prefix are staged together in
+        // pinned host memory that the kernels read directly (a copy command
+        // on the stream would cost a dispatch and a gap between kernels); the
+        // caller's device_items scratch is validated by the API but not
+        // needed here.
         std::size_t const items_bytes = (n * sizeof(DevicePagedDecodeBatchItem) + 15) & ~std::size_t{15};
         std::size_t const writes_bytes = n * sizeof(kimkv_append_job);
         std::size_t const prefix_at = items_bytes + ((writes_bytes + 15) & ~std::size_t{15});
         thread_local std::vector<unsigned char> staging;
-        staging.resize(prefix_at + pre.size() * 4);
-        std::memcpy(staging.data(), batch.host_items, n * sizeof(DevicePagedDecodeBatchItem));
-        std::memcpy(staging.data() + items_bytes, writes.data(), writes_bytes);
-        std::memcpy(staging.data() + prefix_at, pre.data(), pre.size() * 4);
-        std::lock_guard<std::mutex> lock(o.storage.launchMutex());
-        HipStream const stream = stream_;
-        auto* staged = static_cast<unsigned char*>(st.ring().stage(staging.data(), staging.size(), stream));
-        kimkv_status k = KIMKV_SUBMISSION_FAILED;
+        unsigned char* staged = nullptr;
+        if (!launched_from_records) {
+            staging.resize(prefix_at + pre.size() * 4);
+            std::memcpy(staging.data(), batch.host_items, n * sizeof(DevicePagedDecodeBatchItem));
+            std::memcpy(staging.data() + items_bytes, writes.data(), writes_bytes);
+            std::memcpy(staging.data() + prefix_at, pre.data(), pre.size() * 4);
+            staged = static_cast<unsigned char*>(st.ring().stage(staging.data(), staging.size(), stream));
+        }
         if (staged != nullptr) {
             // With split-K lanes, the merge launch reads its per-lane records
             // from device scratch the decode launch fills, not the staged
@@ -1552,6 +1727,12 @@ void const* engineStorage(EngineKvBackend const& backend) noexcept
 {
     auto const* b = dynamic_cast<HipEngineKvBackend const*>(&backend);
     return b != nullptr ? b->state()->storage.handle() : nullptr;
+}
+
+std::uint64_t laneRecordLaunches(EngineKvBackend const& backend) noexcept
+{
+    auto const* b = dynamic_cast<HipEngineKvBackend const*>(&backend);
+    return b != nullptr ? b->state()->lane_record_launches.load(std::memory_order_relaxed) : 0;
 }
 
 }  // namespace kimkvcache

@@ -79,6 +79,24 @@ class Layout(ctypes.Structure):
     _fields_ = [("layers", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32)]
 
 
+class DecodeLayerArgs(ctypes.Structure):
+    """kimkv_decode_layer_args: the layer and each lane's addresses as base + lane * stride (bytes)."""
+    _fields_ = [("layer", ctypes.c_uint32), ("attention_scale", ctypes.c_float),
+                ("query", ctypes.c_uint64), ("query_stride", ctypes.c_uint64),
+                ("output", ctypes.c_uint64), ("output_stride", ctypes.c_uint64),
+                ("workspace", ctypes.c_uint64), ("workspace_stride", ctypes.c_uint64),
+                ("key", ctypes.c_uint64), ("key_stride", ctypes.c_uint64),
+                ("value", ctypes.c_uint64), ("value_stride", ctypes.c_uint64)]
+
+
+# kimkv_decode_lane (32 bytes): the step-constant part of a lane of a batched decode.
+DECODE_LANE = np.dtype([("descriptors", np.uint64), ("descriptor_count", np.uint32), ("token_count", np.uint32),
+                        ("dst_slot", np.uint32), ("cow_slot", np.uint32), ("dst_token", np.uint16),
+                        ("cow_tokens", np.uint16), ("dst_kind", np.uint8), ("cow_kind", np.uint8),
+                        ("has_write", np.uint8), ("reserved", np.uint8)])
+assert DECODE_LANE.itemsize == 32
+
+
 class StorageInfo(ctypes.Structure):
     _fields_ = [
         ("layout", Layout), ("micro_capacity", ctypes.c_uint32), ("extent_capacity", ctypes.c_uint32),
@@ -138,6 +156,9 @@ _SIGNATURES = {
     "kimkv_paged_decode_write_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                       ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                       ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]),
+    "kimkv_paged_decode_lanes": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                 ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "kimkv_paged_decode_write_batch_slots_prefix": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p,
                                                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
                                                                     ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
@@ -428,6 +449,17 @@ class Storage:
                                                          chunk_tokens, query_heads, ctypes.c_void_p(writes_ptr),
                                                          ctypes.c_void_p(slots_ptr), _sh(stream)),
               "paged_decode_write_batch_slots")
+
+    def decode_lanes_launch(self, lanes_ptr: int, prefix_ptr: int, host_prefix: np.ndarray, lanes: int,
+                            total_chunks: int, chunk_tokens: int, query_heads: int, args: DecodeLayerArgs,
+                            slots_ptr: int, stream: Optional[Stream] = None) -> int:
+        """kimkv_paged_decode_lanes (lanes_ptr: DECODE_LANE records in device memory; args: the layer's
+        evenly spaced addresses); returns the status."""
+        hp = np.ascontiguousarray(host_prefix, dtype=np.uint32)
+        return lib().kimkv_paged_decode_lanes(
+            self.h, ctypes.c_void_p(lanes_ptr), ctypes.c_void_p(prefix_ptr), hp.ctypes.data_as(ctypes.c_void_p),
+            lanes, total_chunks, chunk_tokens, query_heads, ctypes.byref(args), ctypes.c_void_p(slots_ptr),
+            _sh(stream))
 
     def decode_write_slots_prefix_launch(self, items_ptr: int, prefix_ptr: int, host_prefix: np.ndarray,
                                          lanes: int, total_chunks: int, chunk_tokens: int, query_heads: int,

@@ -119,6 +119,7 @@ _SIG = {
     "kimkv_engine_promote_request": (I, [P, U64, P, ctypes.POINTER(U32)]),
     "kimkv_engine_block_table": (I, [P, U64, ctypes.POINTER(U64), P, U32, ctypes.POINTER(U32)]),
     "kimkv_engine_storage": (P, [P]),
+    "kimkv_engine_lane_record_launches": (U64, [P]),
     "kimkv_engine_append_prefill": (I, [P, U64, U32, P, P, I, ctypes.POINTER(U32)]),
     "kimkv_engine_permute_free_slots": (I, [P, U32, U64]),
     "kimkv_engine_reserve_batch": (None, [P, P, P, U32, P, P, P]),
@@ -391,6 +392,10 @@ class Engine:
 
     def storage_handle(self) -> int:
         return lib().kimkv_engine_storage(self.h)
+
+    def lane_record_launches(self) -> int:
+        """Batched attention launches made from device lane records (evenly spaced lanes, at most 64)."""
+        return int(lib().kimkv_engine_lane_record_launches(self.h))
 
     def close(self):
         if self.h:

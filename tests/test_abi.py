@@ -35,6 +35,8 @@ def test_struct_layouts_match_reference_sizes(kimkv):
     assert d.PROMOTION_JOB.itemsize == 36   # PromotionSlots + target slot
     assert d.PREFILL_ITEM.itemsize == 48
     assert d.PREFILL_BLOCK.itemsize == 8
+    assert d.DECODE_LANE.itemsize == 32      # kimkv_decode_lane (no reference counterpart)
+    assert ctypes.sizeof(d.DecodeLayerArgs) == 88
 
 
 def _block_cost(T, n, b, per=16):

@@ -821,6 +821,117 @@ def test_engine_small_staging_ring(host, dev, monkeypatch):
     _engine_lane_batch_case(host, dev, steps=3, seed=78)
 
 
+def _lane_records_run(host, dev, shuffle, steps=3, seed=81):
+    """24 lanes (two of them forks of one prefix with a partial tail, so their first token copies it on
+    write; ragged contexts up to ~3000 tokens, so some lanes split into several chunks) through
+    LaneBatch for `steps` tokens.  shuffle: lanes' query and output buffers in a random order (not
+    evenly spaced).  Returns per-step outputs in lane order, the engine's lane_record_launches, and the
+    inputs for an oracle check."""
+    L, H, D, QH, lanes = 3, 4, 64, 32, 24
+    HD, QD = H * D, QH * D
+    rng = np.random.default_rng(seed)
+    T = [int(t) for t in rng.integers(20, 3000, lanes)]
+    P = 1003                                   # the forks' prefix: a partial 8-token tail (1003 % 8 = 3)
+    T[-2], T[-1] = P, P
+    ws_lane = max(dev.workspace_bytes(max(T) + steps, 64, QH, D), 256)
+    engine = host.Engine(L, H, D, QH, ws_lane, sum(t // 8 + 3 + steps for t in T) + 64,
+                         sum(t // 64 for t in T) + 16)
+    stream = dev.Stream()
+    stage = dev.DeviceBuffer(L * 2 * max(T) * HD * 2)
+    for i in range(lanes - 2):
+        assert engine.create_request(i + 1) == 0
+        dev.fill_kv(stage.ptr, L, T[i], HD, seed, i, 0, stream)
+        rc, _ = engine.append_prefill(i + 1, T[i], stage.ptr, stream, promote=True)
+        assert rc == 0
+    root = 1000
+    assert engine.create_request(root) == 0
+    dev.fill_kv(stage.ptr, L, P, HD, seed, 500, 0, stream)
+    assert engine.append_prefill(root, P, stage.ptr, stream, promote=True)[0] == 0
+    for i in (lanes - 2, lanes - 1):
+        assert engine.fork_request(root, i + 1) == 0
+    assert engine.release_request(root) == 0
+    stream.synchronize()
+    newkv = dev.DeviceBuffer(lanes * L * 2 * HD * 2)
+    query = dev.DeviceBuffer(lanes * L * QD * 2)
+    out = dev.DeviceBuffer(lanes * L * QD * 2)
+    ws = dev.DeviceBuffer(lanes * ws_lane)
+    slot = np.random.default_rng(seed + 1).permutation(lanes) if shuffle else np.arange(lanes)
+    lane = np.arange(lanes, dtype=np.uint64)
+    b = host.LaneBatch(engine, lane + np.uint64(1), ws.ptr + lane * np.uint64(ws_lane), ws_lane, 0.125, stream)
+    pos = slot.astype(np.uint64)
+    for l in range(L):
+        b.keys[l, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * L) + np.uint64(2 * l))
+        b.values[l, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * L) + np.uint64(2 * l + 1))
+        b.queries[l, :] = query.ptr + np.uint64(2 * QD) * (np.uint64(l * lanes) + pos)
+        b.outputs[l, :] = out.ptr + np.uint64(2 * QD) * (np.uint64(l * lanes) + pos)
+    qseed = seed ^ 0x5155
+    outs = []
+    for step in range(steps):
+        for i in range(lanes):
+            t = T[i] + step
+            dev.fill_kv(newkv.ptr + i * L * 2 * HD * 2, L, 1, HD, seed, i, t, stream)
+            for l in range(L):
+                dev.fill_rows(query.ptr + (l * lanes + int(slot[i])) * QD * 2, QD, qseed, dev.synth_kv_row(i, l, 0, t),
+                              QD, stream)
+        stream.synchronize()
+        b.reserve(np.array([t + step for t in T], dtype=np.uint32))
+        assert not b.failed()
+        for l in range(L):
+            b.write(l)
+            assert not b.failed(), sorted(set(b.status.tolist()))
+            b.attend(l)
+            assert not b.failed(), sorted(set(b.status.tolist()))
+        b.commit()
+        assert not b.failed(), sorted(set(b.status.tolist()))
+        dev.sync()
+        got = dev.download(out.ptr, (L, lanes, QD), np.uint16)
+        outs.append(np.stack([got[:, int(slot[i])] for i in range(lanes)]))   # [lane][layer][QD]
+    assert engine.check_invariants()
+    launches = engine.lane_record_launches()
+    engine.close()
+    stream.destroy()
+    return outs, launches, T, qseed
+
+
+def test_engine_lane_records_and_staged_items_agree(host, dev):
+    """Batched attention of at most 64 lanes whose queries, outputs, workspaces and new rows are evenly
+    spaced launches from device lane records (kimkv_paged_decode_lanes) from a step's second layer on:
+    the first layer stages items and the second copies the records to the device for the rest of the
+    step.  The same lanes with shuffled query and output buffers take the staged-item launch at every
+    layer.  The two give the same outputs bit for bit over three token steps of three layers (split-K
+    lanes, fresh pages, a fork's copy-on-write tail), and plain lanes match the oracle."""
+    even, n_even, T, qseed = _lane_records_run(host, dev, shuffle=False)
+    mixed, n_mixed, _, _ = _lane_records_run(host, dev, shuffle=True)
+    steps, L = len(even), even[0].shape[1]
+    assert n_even == steps * (L - 1), n_even
+    assert n_mixed == 0, n_mixed
+    for s_ in range(steps):
+        assert np.array_equal(even[s_], mixed[s_]), s_
+    H, D, QH, seed = 4, 64, 32, 81
+    HD = H * D
+    worst = 0.0
+    for i in range(3):                          # plain lanes: the oracle's decode of their history
+        n = T[i] + steps
+        for l in range(L):
+            kv = np.empty((1, 2, n, H, D), dtype=np.uint16)
+            for c in range(2):
+                kv[0, c] = oracle.synth_rows(n * HD, seed, oracle.kv_row(i, l, c, 0), HD).reshape(n, H, D)
+            pages = (n + 7) // 8
+            pools = oracle.HostPools(1, H, D, pages, 1)
+            table = np.zeros(pages, dtype=oracle.DESC)
+            for k in range(pages):
+                table[k] = (k, 1, 8 * k, min(8, n - 8 * k), 8, 0)
+                pools.append_tokens(kv, n, 8 * k, 0, k, 0, min(8, n - 8 * k))
+            q = oracle.synth_rows(QH * D, qseed, oracle.kv_row(i, l, 0, n - 1), QH * D)
+            want = pools.paged_decode(table, n, 0, QH, q, 0.125, f32=True)
+            a = even[-1][i, l].view(np.float16).astype(np.float32)
+            err = np.abs(a - want)
+            assert np.all(err <= 2e-3 + 1e-3 * np.abs(want)), (i, l, float(err.max()))
+            worst = max(worst, float(err.max()))
+    print(f"lane records vs staged items: {steps} steps x {L} layers, record launches {n_even}, "
+          f"oracle max err {worst:.2e}", flush=True)
+
+
 def test_inflight_transaction_pages_survive_sibling_release_and_promotion(host, dev):
     """The engine's token transactions take no page lease (the reference leases every page of the
     candidate table per token, src/cuda/engine/backend.cpp:411-424): a request's committed table holds a

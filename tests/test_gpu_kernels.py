@@ -363,6 +363,124 @@ def test_decode_write_batch_matches_append_then_decode(dev, mode):
     print(f"decode+write mode={mode} lanes={len(T)} chunks={total}", flush=True)
 
 
+@pytest.mark.parametrize("mode,order", [("four_heads", 1), ("head_split", 1), ("four_heads", -1),
+                                        ("head_split", -1)])
+def test_decode_lane_records_match_item_launch(dev, mode, order):
+    """kimkv_paged_decode_lanes (each lane's item and job built in the kernel from a device lane record
+    and the layer's evenly spaced addresses) equals kimkv_paged_decode_write_batch_slots_prefix with the
+    same items and jobs, bit for bit in the outputs and the pages: tail writes, fresh pages, copy-on-write
+    tails, single- and multi-chunk lanes, lanes in address order (order 1) and reversed (order -1: negative
+    strides).  Malformed launches are refused without running."""
+    shape = (3, 4, 64)
+    L, H, D = shape
+    QH, layer = 32, 1
+    T = [5, 8, 63, 64, 100, 700, 1303, 2049, 17]
+    n = len(T)
+    cows = {0, 4, 8}
+    alloc = helpers.SlotAllocator(sum(t // 8 + 4 for t in T) + 16 - n - 4, sum(t // 64 + 1 for t in T) + 2, seed=31)
+    tables = [helpers.hetero_table(t, alloc) for t in T]
+    news = oracle.synth_rows(n * 2 * H * D, 33, 0, D).reshape(n, 2, H, D)
+    chunk = {"four_heads": 256, "head_split": 256 | dev.DECODE_HEAD_SPLIT}[mode]
+    counts = [t + 1 for t in T]
+    prefix = dev.chunk_prefix(counts, chunk, D)
+    total = int(prefix[-1])
+    assert total > n
+    slot_of = list(range(n)) if order == 1 else list(range(n - 1, -1, -1))
+    ws_stride = max(max(dev.workspace_bytes(c, chunk, QH, D) for c in counts), 256)
+
+    def run(records):
+        micro_cap = sum(t // 8 + 4 for t in T) + 16
+        ext_cap = sum(t // 64 + 1 for t in T) + 2
+        storage = dev.Storage(L, H, D, micro_cap, ext_cap)
+        pools = oracle.HostPools(L, H, D, micro_cap, ext_cap)
+        keep = [_populate(dev, storage, pools, table, _input(L, H, D, T[i], seed=3400 + i))
+                for i, table in enumerate(tables)]
+        # Lane i's rows and buffers sit in slot slot_of[i] of contiguous arrays.
+        src = dev.upload(np.stack([news[slot_of.index(k)] for k in range(n)]))
+        qs = dev.upload(np.stack([oracle.synth_rows(QH * D, 3500 + slot_of.index(k), 0, D) for k in range(n)]))
+        out = dev.upload(np.zeros((n, QH * D), dtype=np.uint16))
+        ws = dev.DeviceBuffer(n * ws_stride)
+        keep += [src, qs, out, ws]
+        jobs = np.zeros(n, dtype=dev.APPEND_JOB)
+        items = np.zeros(n, dtype=dev.DECODE_ITEM)
+        lanes = np.zeros(n, dtype=dev.DECODE_LANE)
+        after = []
+        for i, table in enumerate(tables):
+            k = slot_of[i]
+            t = table.copy()
+            tail = t[-1]
+            j = jobs[i]
+            j["src_key"] = src.ptr + 2 * (k * 2) * H * D
+            j["src_value"] = src.ptr + 2 * (k * 2 + 1) * H * D
+            j["layer_begin"], j["layer_count"], j["token_count"] = layer, 1, 1
+            if tail["kind"] == 0 and tail["valid_tokens"] < 8 and i in cows:
+                new_slot = micro_cap - 1 - i
+                j["cow_slot"], j["cow_kind"], j["cow_tokens"] = tail["slot"], 0, tail["valid_tokens"]
+                j["dst_slot"], j["dst_token"] = new_slot, tail["valid_tokens"]
+                t[-1]["slot"] = new_slot
+                t[-1]["valid_tokens"] += 1
+            elif tail["kind"] == 0 and tail["valid_tokens"] < 8:
+                j["dst_slot"], j["dst_token"] = tail["slot"], tail["valid_tokens"]
+                t[-1]["valid_tokens"] += 1
+            else:
+                new_slot = micro_cap - 1 - i
+                j["dst_slot"], j["dst_token"] = new_slot, 0
+                t = np.concatenate([t, np.array([(new_slot, 1, T[i], 1, 8, 0)], dtype=t.dtype)]).astype(helpers.DESC)
+            dbuf = dev.upload(t)
+            keep.append(dbuf)
+            after.append(t)
+            wsz = dev.workspace_bytes(counts[i], chunk, QH, D)
+            items[i] = (dbuf.ptr, len(t), counts[i], layer, qs.ptr + k * QH * D * 2,
+                        ws.ptr + k * ws_stride if wsz else 0, out.ptr + k * QH * D * 2, 0.125)
+            lanes[i] = (dbuf.ptr, len(t), counts[i], j["dst_slot"], j["cow_slot"], j["dst_token"], j["cow_tokens"],
+                        j["dst_kind"], j["cow_kind"], 1, 0)
+        slots = dev.DeviceBuffer(n * dev.DECODE_LANE_SLOT_BYTES)
+        pbuf = dev.upload(prefix)
+        keep += [slots, pbuf]
+        if records:
+            lbuf = dev.upload(lanes)
+            keep.append(lbuf)
+            step = -1 if order == -1 else 1
+            a = dev.DecodeLayerArgs()
+            a.layer, a.attention_scale = layer, 0.125
+            m = 1 << 64
+            a.query, a.query_stride = qs.ptr + slot_of[0] * QH * D * 2, (step * QH * D * 2) % m
+            a.output, a.output_stride = out.ptr + slot_of[0] * QH * D * 2, (step * QH * D * 2) % m
+            a.workspace, a.workspace_stride = ws.ptr + slot_of[0] * ws_stride, (step * ws_stride) % m
+            a.key, a.key_stride = src.ptr + slot_of[0] * 4 * H * D, (step * 4 * H * D) % m
+            a.value, a.value_stride = src.ptr + slot_of[0] * 4 * H * D + 2 * H * D, (step * 4 * H * D) % m
+            bad = prefix.copy()
+            bad[-1] += 1
+            assert storage.decode_lanes_launch(lbuf.ptr, pbuf.ptr, bad, n, total, chunk, QH, a,
+                                               slots.ptr) == dev.INVALID_ARGUMENT
+            assert storage.decode_lanes_launch(lbuf.ptr, pbuf.ptr, prefix, n, total, chunk, QH, a,
+                                               0) == dev.INVALID_ARGUMENT     # split lanes need merge records
+            assert storage.decode_lanes_launch(lbuf.ptr, pbuf.ptr, prefix, n, total, dev.DECODE_GUIDED | 64, QH, a,
+                                               slots.ptr) == dev.INVALID_ARGUMENT
+            big = np.concatenate([prefix, np.full(70 - n, total, dtype=np.uint32)])
+            assert storage.decode_lanes_launch(lbuf.ptr, pbuf.ptr, big, 69, total, chunk, QH, a,
+                                               slots.ptr) == dev.INVALID_ARGUMENT     # more than 64 lanes
+            assert storage.decode_lanes_launch(lbuf.ptr, pbuf.ptr, prefix, n, total, chunk, QH, a, slots.ptr) == 0
+        else:
+            ibuf, jbuf = dev.upload(items), dev.upload(jobs)
+            keep += [ibuf, jbuf]
+            assert storage.decode_write_slots_prefix_launch(ibuf.ptr, pbuf.ptr, prefix, n, total, chunk, QH,
+                                                            jbuf.ptr, slots.ptr) == 0
+        dev.sync()
+        assert storage.faults() == (0, 0)
+        got = dev.download(out.ptr, (n, QH * D), np.uint16)
+        outs = [got[slot_of[i]] for i in range(n)]
+        pages = [storage.gather(t, counts[i]) for i, t in enumerate(after)]
+        return outs, pages
+
+    a_out, a_pages = run(False)
+    b_out, b_pages = run(True)
+    for i in range(n):
+        assert np.array_equal(a_pages[i], b_pages[i]), (mode, order, i)
+        assert np.array_equal(a_out[i], b_out[i]), (mode, order, i)
+    print(f"lane records mode={mode} order={order} lanes={n} chunks={total}", flush=True)
+
+
 def _fused_case(dev, shape, lanes, chunk, micro_tokens=8, extent_tokens=64, seed=70, QH=None):
     """Write-and-decode launches against the oracle and against append-then-decode, with explicit jobs.
 
