@@ -614,7 +614,8 @@ public:
             index.push_back(i);
         }
         // Each lane's job is held for the layer's attention launch, which
-        // writes the token before reading the page (one launch per layer).
+        // stores the token (its reads take the token from the job's rows:
+        // one launch per layer).
         bool any = false;
         for (std::size_t k = 0; k < lanes.size(); ++k) {
             LayerKvWriteBatchItem& item = batch.items[index[k]];
@@ -708,8 +709,9 @@ private:
 
     // A layer's token write is not launched on its own: writeLayer checks it
     // and holds the job, and the layer's attention launch
-    // (kimkv_paged_decode_write_batch) writes the token before reading the
-    // page.  The state machine admits attendLayer(l) only after writeLayer(l)
+    // (kimkv_paged_decode_write_batch or _lanes) stores the token, reading
+    // the positions it writes from the job's rows and copy-on-write source
+    // rather than from the page.  The state machine admits attendLayer(l) only after writeLayer(l)
     // and commit only after every layer's attention, so a held job is either
     // written by its attention launch or dropped with a rollback.
     void holdWrite(kimkv_append_job const& job) noexcept
