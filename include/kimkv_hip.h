@@ -9,14 +9,15 @@
  * asynchronous on the given stream (NULL = the device's default stream), like
  * the reference's `CudaStream` (include/kim-kv/cuda/cuda_status.h:13).
  *
- * Device page layout (private to the storage, identical total size to the
- * reference's page): for a page of `cap` tokens,
- *     K(l,t,h,d) = l*2*cap*H*D + h*2*cap*D + t*D + d
- *     V(l,t,h,d) = l*2*cap*H*D + h*2*cap*D + cap*D + d*cap + t
- * i.e. per (layer, head) one contiguous block holding K rows [cap][D]
- * followed by V transposed [D][cap].  The contiguous tensors that cross the
- * API (append input, gather output) keep the reference order
- * [layer][K/V][token][head][dim] (include/kim-kv/core/kv_layout.h:73-90).
+ * Device page layout (private to the storage; a page holds as many bytes
+ * as the reference's): both pools are one allocation of `layers` regions,
+ * region l holding every micro page's layer-l block and then every extent
+ * page's, so a launch that works on one layer reads one region.  A page's
+ * block of one layer holds, per head, 2*cap*D fp16 values: K for `cap`
+ * tokens in 32-dim column blocks, then V transposed ([D][cap], in 32-token
+ * column blocks).  The contiguous tensors that cross the API (append input,
+ * gather output) keep the reference order [layer][K/V][token][head][dim]
+ * (include/kim-kv/core/kv_layout.h:73-90).
  */
 #ifndef KIMKV_HIP_H
 #define KIMKV_HIP_H
@@ -201,7 +202,11 @@ kimkv_status kimkv_storage_create(kimkv_storage** out, kimkv_layout layout,
 kimkv_status kimkv_storage_destroy(kimkv_storage* storage);
 kimkv_status kimkv_storage_query(const kimkv_storage* storage, kimkv_storage_info* info);
 /* Device address of a page: CudaKvStorage::Impl::pagePointer (storage.cpp:46-68).
- * Returns NULL for an out-of-range slot. */
+ * Returns NULL for an out-of-range slot.  The page layout is private to the
+ * kernels and layer-major: the address is the page's layer-0 block (K and V^T
+ * of every head); its layer-l block lies l layer regions further on (a region
+ * holds every page's block of one layer), so a page is not one contiguous
+ * range. */
 uint16_t* kimkv_storage_page(const kimkv_storage* storage, uint32_t kind, uint32_t slot);
 
 /* Fault bits.  A kernel that finds one of its jobs or items invalid (layer

@@ -31,28 +31,29 @@ struct GroupEntry {
 };
 
 // Resolves group entries to the (layer, head) block of their page for one
-// (layer, KV head): block = pool + slot * page_elements + cap * unit with
-// unit = (layer * H + head) * 2 * D.
+// (layer, KV head): block = page_base(slot) + head_block(layer, head), i.e.
+// a per-kind base for this (layer, head) plus slot * slot_elements.
 struct GroupResolver {
     const uint16_t* micro;
     const uint16_t* extent;
-    uint64_t micro_page_elements;
-    uint64_t extent_page_elements;
+    uint64_t micro_slot_elements;
+    uint64_t extent_slot_elements;
 
     __device__ GroupResolver(const PoolView& P, uint32_t layer, uint32_t head)
     {
-        uint64_t const unit = (static_cast<uint64_t>(layer) * P.heads + head) * 2ull * P.dim;
-        micro = P.micro + unit * P.micro_tokens;
-        extent = P.extent + unit * P.extent_tokens;
-        micro_page_elements = P.micro_page_elements;
-        extent_page_elements = P.extent_page_elements;
+        uint64_t const region = static_cast<uint64_t>(layer) * P.layer_elements;
+        uint64_t const unit = static_cast<uint64_t>(head) * 2ull * P.dim;
+        micro = P.micro + region + unit * P.micro_tokens;
+        extent = P.extent + region + unit * P.extent_tokens;
+        micro_slot_elements = P.micro_slot_elements;
+        extent_slot_elements = P.extent_slot_elements;
     }
 
     __device__ const uint16_t* block(GroupEntry g) const
     {
         uint64_t const slot = g.page & ~kExtentPage;
-        return (g.page & kExtentPage) != 0 ? extent + slot * extent_page_elements
-                                           : micro + slot * micro_page_elements;
+        return (g.page & kExtentPage) != 0 ? extent + slot * extent_slot_elements
+                                           : micro + slot * micro_slot_elements;
     }
 };
 

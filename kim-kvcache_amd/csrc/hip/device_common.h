@@ -28,10 +28,11 @@ struct kimkv_storage {
     uint32_t extent_capacity{0};
     uint16_t micro_tokens{0};
     uint16_t extent_tokens{0};
-    uint64_t micro_page_elements{0};
+    uint64_t micro_page_elements{0};   // one page, every layer
     uint64_t extent_page_elements{0};
-    uint16_t* micro{nullptr};
-    uint16_t* extent{nullptr};
+    uint16_t* pool{nullptr};           // the one allocation (layer-major, see page_base)
+    uint16_t* micro{nullptr};          // layer 0's micro blocks
+    uint16_t* extent{nullptr};         // layer 0's extent blocks
     uint32_t* faults{nullptr};        // device word, KIMKV_FAULT_* bits
     uint32_t* work_counters{nullptr}; // kWorkCounterSlots slots of kWorkCounterStride words
     mutable std::mutex work_counter_mutex;
@@ -51,8 +52,9 @@ constexpr unsigned kWave = 64;
 struct PoolView {
     uint16_t* micro;
     uint16_t* extent;
-    uint64_t micro_page_elements;
-    uint64_t extent_page_elements;
+    uint64_t micro_slot_elements;    // one micro page's block of one layer (every head)
+    uint64_t extent_slot_elements;
+    uint64_t layer_elements;         // one layer's region: every micro, then every extent page
     uint32_t micro_capacity;
     uint32_t extent_capacity;
     uint32_t micro_tokens;
@@ -63,9 +65,18 @@ struct PoolView {
     uint32_t* faults;
 };
 
+// Elements of one page's block of one layer (K and V^T of every head).
+inline uint64_t slot_elements(const kimkv_layout& l, uint32_t page_tokens)
+{
+    return 2ull * l.kv_heads * l.head_dim * page_tokens;
+}
+
 inline PoolView pool_view(const kimkv_storage& s)
 {
-    return PoolView{s.micro, s.extent, s.micro_page_elements, s.extent_page_elements,
+    uint64_t const micro_slot = slot_elements(s.layout, s.micro_tokens);
+    uint64_t const extent_slot = slot_elements(s.layout, s.extent_tokens);
+    return PoolView{s.micro, s.extent, micro_slot, extent_slot,
+                    micro_slot * s.micro_capacity + extent_slot * s.extent_capacity,
                     s.micro_capacity, s.extent_capacity, s.micro_tokens, s.extent_tokens,
                     s.layout.layers, s.layout.kv_heads, s.layout.head_dim, s.faults};
 }
@@ -79,8 +90,21 @@ __device__ inline void report_fault(const PoolView& p, uint32_t bit)
     if (threadIdx.x == 0 && p.faults != nullptr) atomicOr(p.faults, bit);
 }
 
-// Page base for a (kind, slot), or nullptr when the handle does not name a page
-// of this storage or its declared capacity disagrees with the pool's.
+// The pools are one allocation, layer-major: `layers` regions of
+// layer_elements each; region l holds every micro page's layer-l block, then
+// every extent page's, and a page's block holds its heads one after the
+// other.  So the (layer, head) block of a page is
+//   pool + l * layer_elements + [micro part] + slot * slot_elements(kind)
+//        + head * 2 * cap * D,
+// page_base() being the layer-0 block and head_block() the rest.  A decode
+// or prefill launch works on one layer, and one layer's blocks of all pages
+// lie in one region (8.6 GB for 131 072 extent pages of 4 heads x 64 dims)
+// instead of being spread over the whole pool: random 16 KiB pieces stream
+// at 7.0 TB/s from one region against 6.7 TB/s from a 189 GB span
+// (measured on MI355X; the difference is address-translation reach).
+//
+// Layer-0 block of a (kind, slot), or nullptr when the handle does not name
+// a page of this storage or its declared capacity disagrees with the pool's.
 __device__ inline uint16_t* page_base(const PoolView& p, uint32_t kind, uint32_t slot,
                                       uint32_t capacity)
 {
@@ -88,13 +112,13 @@ __device__ inline uint16_t* page_base(const PoolView& p, uint32_t kind, uint32_t
         if (slot >= p.micro_capacity || capacity != p.micro_tokens || p.micro == nullptr) {
             return nullptr;
         }
-        return p.micro + static_cast<uint64_t>(slot) * p.micro_page_elements;
+        return p.micro + static_cast<uint64_t>(slot) * p.micro_slot_elements;
     }
     if (kind == KIMKV_PAGE_EXTENT) {
         if (slot >= p.extent_capacity || capacity != p.extent_tokens || p.extent == nullptr) {
             return nullptr;
         }
-        return p.extent + static_cast<uint64_t>(slot) * p.extent_page_elements;
+        return p.extent + static_cast<uint64_t>(slot) * p.extent_slot_elements;
     }
     return nullptr;
 }
@@ -104,10 +128,11 @@ __device__ inline uint32_t pool_tokens(const PoolView& p, uint32_t kind)
     return kind == KIMKV_PAGE_MICRO ? p.micro_tokens : p.extent_tokens;
 }
 
-// Element offset of the (layer, head) block inside a page of `cap` tokens.
+// Element offset of a page's (layer, head) block from its page_base(), for
+// a page of `cap` tokens.
 __device__ inline uint64_t head_block(const PoolView& p, uint32_t cap, uint32_t layer, uint32_t head)
 {
-    return (static_cast<uint64_t>(layer) * p.heads + head) * 2ull * cap * p.dim;
+    return static_cast<uint64_t>(layer) * p.layer_elements + static_cast<uint64_t>(head) * 2ull * cap * p.dim;
 }
 
 // Inside a (layer, head) block of a page with `cap` tokens and head dim D:

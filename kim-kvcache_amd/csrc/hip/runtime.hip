@@ -1,7 +1,8 @@
 // runtime.hip -- C-ABI runtime wrappers and device pool storage.
 //
-// Storage follows CudaKvStorage (src/cuda/kv/storage.cpp:99-190): one device
-// allocation per pool, zero-filled, page pointer = base + slot * page_elements.
+// Storage keeps the interface of CudaKvStorage (src/cuda/kv/storage.cpp:99-190)
+// with a layout of its own: one device allocation for both pools,
+// zero-filled, layer-major (page_base in device_common.h).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -374,15 +375,17 @@ kimkv_status kimkv_storage_create(kimkv_storage** out, kimkv_layout layout, uint
     if (e == hipSuccess) {
         e = hipDeviceGetAttribute(&s->compute_units, hipDeviceAttributeMultiprocessorCount, s->device);
     }
+    // One allocation, layer-major (page_base in device_common.h): layer 0's
+    // micro blocks, its extent blocks, then layer 1's, ...
     uint64_t const micro_bytes = micro_elems * micro_capacity * 2ull;
     uint64_t const extent_bytes = extent_elems * extent_capacity * 2ull;
-    if (e == hipSuccess && micro_bytes != 0) {
-        e = hipMalloc(reinterpret_cast<void**>(&s->micro), micro_bytes);
-        if (e == hipSuccess) e = hipMemset(s->micro, 0, micro_bytes);
-    }
-    if (e == hipSuccess && extent_bytes != 0) {
-        e = hipMalloc(reinterpret_cast<void**>(&s->extent), extent_bytes);
-        if (e == hipSuccess) e = hipMemset(s->extent, 0, extent_bytes);
+    if (e == hipSuccess && micro_bytes + extent_bytes != 0) {
+        e = hipMalloc(reinterpret_cast<void**>(&s->pool), micro_bytes + extent_bytes);
+        if (e == hipSuccess) e = hipMemset(s->pool, 0, micro_bytes + extent_bytes);
+        if (e == hipSuccess) {
+            s->micro = s->pool;
+            s->extent = s->pool + kimkv::slot_elements(layout, micro_page_tokens) * micro_capacity;
+        }
     }
     if (e == hipSuccess) {
         e = hipMalloc(reinterpret_cast<void**>(&s->faults), 256);
@@ -400,8 +403,7 @@ kimkv_status kimkv_storage_create(kimkv_storage** out, kimkv_layout layout, uint
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         record_error(e, KIMKV_ALLOCATION_FAILED);
-        if (s->micro) static_cast<void>(hipFree(s->micro));
-        if (s->extent) static_cast<void>(hipFree(s->extent));
+        if (s->pool) static_cast<void>(hipFree(s->pool));
         if (s->faults) static_cast<void>(hipFree(s->faults));
         if (s->work_counters) static_cast<void>(hipFree(s->work_counters));
         if (s->fault_host) static_cast<void>(hipHostFree(s->fault_host));
@@ -417,8 +419,7 @@ kimkv_status kimkv_storage_destroy(kimkv_storage* storage)
     if (storage == nullptr) return KIMKV_OK;
     // In-flight work may still read the pools (storage.cpp:22-32 waits too).
     static_cast<void>(hipDeviceSynchronize());
-    if (storage->micro) static_cast<void>(hipFree(storage->micro));
-    if (storage->extent) static_cast<void>(hipFree(storage->extent));
+    if (storage->pool) static_cast<void>(hipFree(storage->pool));
     if (storage->faults) static_cast<void>(hipFree(storage->faults));
     if (storage->work_counters) static_cast<void>(hipFree(storage->work_counters));
     if (storage->fault_host) static_cast<void>(hipHostFree(storage->fault_host));
@@ -467,10 +468,10 @@ uint16_t* kimkv_storage_page(const kimkv_storage* s, uint32_t kind, uint32_t slo
 {
     if (s == nullptr) return nullptr;
     if (kind == KIMKV_PAGE_MICRO && slot < s->micro_capacity && s->micro != nullptr) {
-        return s->micro + static_cast<uint64_t>(slot) * s->micro_page_elements;
+        return s->micro + static_cast<uint64_t>(slot) * kimkv::slot_elements(s->layout, s->micro_tokens);
     }
     if (kind == KIMKV_PAGE_EXTENT && slot < s->extent_capacity && s->extent != nullptr) {
-        return s->extent + static_cast<uint64_t>(slot) * s->extent_page_elements;
+        return s->extent + static_cast<uint64_t>(slot) * kimkv::slot_elements(s->layout, s->extent_tokens);
     }
     return nullptr;
 }
