@@ -219,13 +219,10 @@ __device__ inline float xor32(float v)
 struct PrefillWave {
     uint32_t l, a, r, x;
     uint32_t i0;                       // first new token of the wave
-    half8_t qb[kColBlocks][2];         // queries times scale * log2(e), rounded to fp16
+    half8_t qb[kColBlocks][2];
     uint32_t limit[kColBlocks];        // last key this lane's column may see
-    float m_run[kColBlocks];           // reference point (log2 units); -inf until a key is seen
-    // The score MFMAs start from -m_base (4 equal values: one MFMA C operand),
-    // so they return score - m_base with no VALU work per score; m_base is
-    // m_run once that is finite, 0 before.
-    float4_t neg_base[kColBlocks];
+    float scale2;
+    float m_run[kColBlocks];
     // acc[0..3]: O^T dims 16 db .. 16 db + 15; acc[4] row 0: the softmax
     // denominator, accumulated by the MFMA from a ones row of V^T.
     float4_t acc[5][kColBlocks];
@@ -256,21 +253,11 @@ __device__ void prefill_wave_init(PrefillWave& w, const kimkv_prefill_item& item
             w.qb[cb][0] = *reinterpret_cast<const half8_t*>(qrow + w.a * 8);
             w.qb[cb][1] = *reinterpret_cast<const half8_t*>(qrow + 32 + w.a * 8);
         }
-        // Scores come out of the MFMA in log2 units: the queries carry the
-        // scale (one more fp16 rounding of each query element).
-        float const scale2 = item.attention_scale * kLog2e;
-#pragma unroll
-        for (uint32_t j = 0; j < 2; ++j) {
-#pragma unroll
-            for (uint32_t e = 0; e < 8; ++e) {
-                w.qb[cb][j][e] = static_cast<_Float16>(static_cast<float>(w.qb[cb][j][e]) * scale2);
-            }
-        }
         w.m_run[cb] = -INFINITY;
-        w.neg_base[cb] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (uint32_t db = 0; db < 5; ++db) w.acc[db][cb] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    w.scale2 = item.attention_scale * kLog2e;
     _Float16 const one = static_cast<_Float16>(w.r == 0 ? 1.0f : 0.0f);
     w.ones = half8_t{one, one, one, one, one, one, one, one};
 }
@@ -300,8 +287,8 @@ __device__ inline void prefill_wave_step(PrefillWave& w, const KvTile& tile, uin
         for (uint32_t kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (uint32_t e = 0; e < 2; ++e) {
-                float4_t z = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][0], w.qb[cb][0], w.neg_base[cb], 0,
-                                                                     0, 0);
+                float4_t z = {};
+                z = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][0], w.qb[cb][0], z, 0, 0, 0);
                 s[cb][kb][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kb][e][1], w.qb[cb][1], z, 0, 0, 0);
             }
         }
@@ -314,8 +301,8 @@ __device__ inline void prefill_wave_step(PrefillWave& w, const KvTile& tile, uin
     }
 #pragma unroll
     for (uint32_t cb = 0; cb < kColBlocks; ++cb) {
-        // Element i of s[cb][kb][e] is key t0 + 32 kb + 8 a + 4 e + i of this lane's column, as its score
-        // in log2 units minus m_base.
+        // Element i of s[cb][kb][e] is key t0 + 32 kb + 8 a + 4 e + i of this lane's column.  The max is
+        // taken on the unscaled dots (scale2 > 0 keeps the order and rounding is monotonic).
         float mx = -INFINITY;
 #pragma unroll
         for (uint32_t kb = 0; kb < 2; ++kb) {
@@ -338,33 +325,21 @@ __device__ inline void prefill_wave_step(PrefillWave& w, const KvTile& tile, uin
         // passes it takes the column max across the four row groups (a
         // column's m stays the same on all of its lanes).  A column whose
         // keys so far are all masked keeps m = -inf.
-        // With m_run finite (= m_base) the test is score - m_base > 2^8; before any key, every finite
-        // score passes.
-        float const base = -w.neg_base[cb][0];
-        bool const over = mx > (w.m_run[cb] == -INFINITY ? -INFINITY : kLazyRescaleLog2);
+        bool const over = mx * w.scale2 > w.m_run[cb] + kLazyRescaleLog2;
         if (__builtin_expect(__any(over), 0)) {
-            // Not speculated: the reduction and the rescale run only on tiles that move the reference point.
+            // Not speculated: the reduction and the multiplies run only on tiles that move the reference point.
             __asm__ volatile("" ::: "memory");
             mx = fmaxf(mx, xor16(mx));
             mx = fmaxf(mx, xor32(mx));
-            float const m_cand = fmaxf(w.m_run[cb], mx + base);
+            float const m_cand = fmaxf(w.m_run[cb], mx * w.scale2);
             bool const grow = m_cand > w.m_run[cb] + kLazyRescaleLog2;
-            if (grow) {
-                float const alpha = __builtin_amdgcn_exp2f(w.m_run[cb] - m_cand);
-                w.m_run[cb] = m_cand;
+            float const alpha = grow ? __builtin_amdgcn_exp2f(w.m_run[cb] - m_cand) : 1.0f;
+            if (grow) w.m_run[cb] = m_cand;
 #pragma unroll
-                for (uint32_t db = 0; db < 5; ++db) w.acc[db][cb] *= alpha;
-                // This tile's scores were taken from the old base.
-                float const shift = m_cand - base;
-#pragma unroll
-                for (uint32_t kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (uint32_t e = 0; e < 2; ++e) s[cb][kb][e] -= shift;
-                }
-                w.neg_base[cb] = float4_t{-m_cand, -m_cand, -m_cand, -m_cand};
-            }
+            for (uint32_t db = 0; db < 5; ++db) w.acc[db][cb] *= alpha;
         }
-        bool const empty = kMasked && w.m_run[cb] == -INFINITY;
+        float const mref = w.m_run[cb];
+        bool const empty = kMasked && mref == -INFINITY;
         half8_t pb[2];
 #pragma unroll
         for (uint32_t kb = 0; kb < 2; ++kb) {
@@ -372,7 +347,7 @@ __device__ inline void prefill_wave_step(PrefillWave& w, const KvTile& tile, uin
             for (uint32_t e = 0; e < 2; ++e) {
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i) {
-                    float p = __builtin_amdgcn_exp2f(s[cb][kb][e][i]);
+                    float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[cb][kb][e][i], w.scale2, -mref));
                     if (kMasked && empty) p = 0.0f;
                     pb[kb][4 * e + i] = static_cast<_Float16>(p);
                 }
