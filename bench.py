@@ -951,7 +951,8 @@ def run_shared(kimkv, dev, args) -> int:
     stop.record(stream)
     stop.synchronize()
     wall_ms = (time.perf_counter() - t_wall) * 1000.0
-    ms_per_step = max(start.elapsed_ms(stop), wall_ms) / args.steps
+    gpu_ms = start.elapsed_ms(stop)
+    ms_per_step = max(gpu_ms, wall_ms) / args.steps
     # Decode kernel duration from a separate short loop with event timing.
     dev.decode_timing(True)
     for s_ in range(args.warmup + args.steps, total_steps):
@@ -1017,6 +1018,7 @@ def run_shared(kimkv, dev, args) -> int:
         "physical_gb_per_s": round(physical_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "decode_kernel_avg_us": round(1000 * dec_ms, 2),
         "ms_per_step": round(ms_per_step, 3),
+        "gpu_ms_per_step": round(gpu_ms / args.steps, 3), "host_ms_per_step": round(wall_ms / args.steps, 3),
         "roofline": {"bound": "hbm", "achieved": round(dec_bytes / (dec_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(dec_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                      "traffic": profiled_traffic("decode_kernel_shared_prefix.md", lanes=lanes, layers=L,

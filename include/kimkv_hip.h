@@ -403,11 +403,13 @@ kimkv_status kimkv_paged_decode_write_batch_slots_prefix(const kimkv_storage* st
                                                          uint32_t query_heads, const kimkv_append_job* device_writes,
                                                          void* device_lane_slots, kimkv_stream_t stream);
 
-/* The part of one lane of a batched decode that stays the same for every
- * layer of a token step: the lane's block table and token count, and the
- * destination of its single-token write (the write job of
- * kimkv_paged_decode_write_batch without its per-layer source rows).  32
- * bytes; kept by the caller in device memory across the step's layers. */
+/* One chunk of a batched decode launch, with what stays the same for every
+ * layer of a token step: its lane's block table and token count, the
+ * destination of the lane's single-token write (the write job of
+ * kimkv_paged_decode_write_batch without its per-layer source rows), and
+ * where the chunk sits (its lane, the lane's first chunk in the launch and
+ * the lane's chunk count: the planned chunk prefix, per chunk).  48 bytes;
+ * kept by the caller in device memory across the step's layers. */
 typedef struct kimkv_decode_lane {
     const kimkv_block_desc* descriptors;
     uint32_t descriptor_count;
@@ -420,6 +422,10 @@ typedef struct kimkv_decode_lane {
     uint8_t cow_kind;
     uint8_t has_write;
     uint8_t reserved;
+    uint32_t lane;
+    uint32_t first_chunk;
+    uint32_t chunk_count;
+    uint32_t reserved2;
 } kimkv_decode_lane;
 
 /* The per-layer part of such a launch: lane i reads its query at
@@ -443,24 +449,44 @@ typedef struct kimkv_decode_layer_args {
     uint64_t value_stride;
 } kimkv_decode_layer_args;
 
-/* kimkv_paged_decode_write_batch_slots_prefix with each lane's item and write
- * job assembled in the kernel from device_lanes[lane] (device memory) and
- * *args (copied into the launch's arguments): a workgroup's only read before
- * its block table is one device-memory record, where the item form reads the
- * caller's items and jobs (in mapped host memory when the engine stages
- * them, a round trip to the host).  For a caller whose lanes' queries,
- * outputs, workspaces and new rows are evenly spaced (base + lane * stride),
- * which keeps the lane records across a step's layers.  lane_count at most
- * KIMKV_DECODE_ARG_PREFIX_LANES; host_chunk_prefix as for the _prefix form;
+/* kimkv_paged_decode_write_batch_slots with each chunk's item and write job
+ * assembled in the kernel from device_chunks[chunk] (device memory, 16-byte
+ * aligned, one kimkv_decode_lane per chunk of the launch: total_chunks
+ * records, the chunks of a lane consecutive) and *args (copied into the
+ * launch's arguments): a workgroup's only read before its block table is its
+ * chunk's record, whose address follows from the workgroup alone, where the
+ * item form finds its lane in the chunk prefix and reads the caller's items
+ * and jobs (in mapped host memory when the engine stages them, a round trip
+ * to the host).  For a caller whose lanes' queries, outputs, workspaces and
+ * new rows are evenly spaced (base + lane * stride), which keeps the records
+ * across a step's layers.  lane_count at most KIMKV_DECODE_ARG_PREFIX_LANES;
  * device_lane_slots required when total_chunks > lane_count; not with
- * KIMKV_DECODE_GUIDED.  Anything else returns KIMKV_INVALID_ARGUMENT and
- * launches nothing.  Same results as the item form with the same items and
- * jobs.  No counterpart in the reference. */
-kimkv_status kimkv_paged_decode_lanes(const kimkv_storage* storage, const kimkv_decode_lane* device_lanes,
-                                      const uint32_t* device_chunk_prefix, const uint32_t* host_chunk_prefix,
+ * KIMKV_DECODE_GUIDED.  A record that names a lane past lane_count or a chunk
+ * range that does not hold its own chunk, or lies outside the launch, is
+ * reported (KIMKV_FAULT_DECODE_ITEM) and skipped.
+ * device_table_cache (optional, NULL for none; 16-byte aligned, at least
+ * kimkv_decode_table_cache_bytes(total_chunks, chunk_flags) bytes of device
+ * memory; chunks of at most 4096 tokens): a cache of each chunk's group
+ * table, the page lookups a workgroup derives from its lane's descriptors.
+ * They are the same for every layer of a token step, so the step's first
+ * launch with a given nonzero table_tag stores them and later launches with
+ * that tag read them in the same round trip as the chunk record instead of
+ * reading the descriptors.  A tag must not have been stored in this cache by
+ * a launch whose records, block-table contents or chunk_flags differ (a
+ * fresh tag per token step, and a cache zeroed before first use, keep that),
+ * and launches sharing a cache must not overlap (one stream).
+ * Anything else returns KIMKV_INVALID_ARGUMENT and launches nothing.  Same
+ * results as the item form with the same items, jobs and plan.  No
+ * counterpart in the reference. */
+kimkv_status kimkv_paged_decode_lanes(const kimkv_storage* storage, const kimkv_decode_lane* device_chunks,
                                       uint32_t lane_count, uint32_t total_chunks, uint32_t chunk_flags,
                                       uint32_t query_heads, const kimkv_decode_layer_args* args,
-                                      void* device_lane_slots, kimkv_stream_t stream);
+                                      void* device_lane_slots, void* device_table_cache,
+                                      uint64_t table_cache_bytes, uint32_t table_tag, kimkv_stream_t stream);
+/* Bytes of the table cache of kimkv_paged_decode_lanes for a launch of
+ * total_chunks chunks planned with chunk_flags.  No counterpart in the
+ * reference. */
+uint64_t kimkv_decode_table_cache_bytes(uint32_t total_chunks, uint32_t chunk_flags);
 
 /* Size of the device scratch array of kimkv_paged_decode_batch_noalloc. */
 #define KIMKV_DECODE_SCRATCH_BYTES (16u << 20)

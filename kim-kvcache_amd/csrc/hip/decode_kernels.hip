@@ -638,6 +638,71 @@ __device__ bool build_chunk_table(const PoolView& P, const kimkv_decode_item& it
     return P.dim == 64 && G <= 16 && lds.generic == 0;
 }
 
+// A kRecords launch's cache of chunk group tables (optional): the table a
+// chunk's workgroup builds from its lane's descriptors is the same for every
+// layer of a token step, so the first launch of the step stores it and later
+// launches copy it into LDS instead of reading the descriptors -- in the
+// same round trip as the lane record, where building it waits for that
+// record.  Per chunk: a 16-byte header, then `stride` 8-byte group entries.
+// A header whose tag is not the launch's (another step, or never written)
+// makes the workgroup build the table and store it with the launch's tag.
+struct TableCacheHeader {
+    uint32_t tag;
+    uint32_t ngroups;
+    uint32_t generic;
+    uint32_t new_ok;
+};
+static_assert(sizeof(TableCacheHeader) == 16 && sizeof(GroupEntry) == 8, "cache layout");
+
+struct TableCache {
+    unsigned char* base;   // nullptr: no cache
+    uint32_t stride;       // group entries per chunk (chunk_tokens / 8)
+    uint32_t tag;          // nonzero
+};
+// Entries one thread prefetches: chunks of up to 4096 tokens.
+constexpr uint32_t kTableCachePerThread = 2;
+constexpr uint32_t kTableCacheMaxChunk = kTableCachePerThread * kBlock * 8;
+
+__host__ __device__ inline uint64_t table_cache_chunk_bytes(uint32_t stride)
+{
+    return sizeof(TableCacheHeader) + static_cast<uint64_t>(stride) * sizeof(GroupEntry);
+}
+
+// build_chunk_table for a kRecords launch with a table cache (see
+// TableCache): when the header this workgroup loaded with its lane record
+// carries the launch's tag and the chunk's group count, the entries it
+// copied into lds.groups are the table; otherwise the table is built from
+// the descriptors and stored with the launch's tag (every workgroup of a
+// chunk -- one per kv head in the head-split mode -- stores the same bytes).
+// Called by every thread of the block.
+__device__ inline bool chunk_table_cached(const PoolView& P, const kimkv_decode_item& item, uint32_t QH, uint32_t c0,
+                                          uint32_t c1, DecodeLds& lds, JobView const& jv, TableCache const& cache,
+                                          uint32_t chunk_id, TableCacheHeader const& s_hdr)
+{
+    uint32_t const ngroups = (c1 - c0 + 7) / 8;
+    if (cache.base == nullptr || ngroups > cache.stride) return build_chunk_table(P, item, QH, c0, c1, lds, jv);
+    __syncthreads();   // the header and entries copied into LDS
+    uint32_t const G = QH / P.heads;
+    if (s_hdr.tag == cache.tag && s_hdr.ngroups == ngroups) {
+        if (threadIdx.x == 0) {
+            lds.generic = s_hdr.generic;
+            lds.new_ok = s_hdr.new_ok;
+        }
+        __syncthreads();
+        return P.dim == 64 && G <= 16 && lds.generic == 0;
+    }
+    __syncthreads();   // every thread has read the header before the table is rebuilt
+    bool const fast = build_chunk_table(P, item, QH, c0, c1, lds, jv);
+    unsigned char* c = cache.base + table_cache_chunk_bytes(cache.stride) * chunk_id;
+    for (uint32_t g = threadIdx.x; g < ngroups; g += kBlock) {
+        reinterpret_cast<GroupEntry*>(c + sizeof(TableCacheHeader))[g] = lds.groups[g];
+    }
+    if (threadIdx.x == 0) {
+        *reinterpret_cast<TableCacheHeader*>(c) = TableCacheHeader{cache.tag, ngroups, lds.generic, lds.new_ok};
+    }
+    return fast;
+}
+
 // One (lane, kv head, chunk) by the whole workgroup: tokens [c0, c1) cut
 // into four 64-token-aligned quarters, one per wave, the four online-softmax
 // states merged through LDS, then the output (single chunk) or the chunk's
@@ -811,15 +876,16 @@ struct NoArgPrefix {};
 enum class LaneSource {
     kGuess,       // items[] and writes[]; lane guessed from the chunk, checked against prefix[]
     kArgPrefix,   // items[] and writes[]; lane from the prefix in the launch arguments
-    kRecords,     // lane from the prefix in the arguments; item and job built from a
-                  // step-constant kimkv_decode_lane in device memory and the layer arguments
+    kRecords,     // item, job and lane built from the chunk's step-constant
+                  // kimkv_decode_lane in device memory and the layer arguments
 };
 
 // Arguments of a kRecords launch: the prefix and the per-layer addresses.
 struct RecordArgs {
-    ArgPrefix ap;
     kimkv_decode_layer_args layer;
+    TableCache cache;
 };
+
 
 template <LaneSource kSrc>
 using SourceArgs = std::conditional_t<kSrc == LaneSource::kGuess, NoArgPrefix,
@@ -869,6 +935,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     __shared__ DecodeLds lds;
     __shared__ uint32_t s_lane;
     __shared__ uint32_t s_hit;
+    __shared__ TableCacheHeader s_cache_hdr;
 
     uint32_t const tid = threadIdx.x;
     // One workgroup per chunk with every head (grid.y == 1): each XCD takes a
@@ -882,16 +949,49 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t lane_end = 0;
     kimkv_decode_item item;
     kimkv_append_job job;
-    if constexpr (kSrc != LaneSource::kGuess) {
+    if constexpr (kSrc == LaneSource::kRecords) {
+        // One round trip: the chunk's record and its cached group table (if
+        // any), both at addresses that follow from the chunk alone.  (Plain
+        // vector values, not arrays or structs, so that they stay in
+        // registers: a local aggregate may be placed in LDS by the compiler,
+        // which then waits for its load at once to store it there.)
+        static_assert(sizeof(kimkv_decode_lane) == 48, "chunk record is 48 bytes");
+        static_assert(kTableCachePerThread == 2, "two prefetched entries per thread");
+        const uint4* rp = reinterpret_cast<const uint4*>(lanes + chunk_id);
+        uint4 const r0 = rp[0];
+        uint4 const r1 = rp[1];
+        uint4 const r2 = rp[2];
+        uint4 hdr = {0u, 0u, 0u, 0u};
+        uint2 ent0 = {0u, 0u};
+        uint2 ent1 = {0u, 0u};
+        if (sa.cache.base != nullptr) {
+            const unsigned char* c = sa.cache.base + table_cache_chunk_bytes(sa.cache.stride) * chunk_id;
+            const uint2* e = reinterpret_cast<const uint2*>(c + sizeof(TableCacheHeader));
+            hdr = *reinterpret_cast<const uint4*>(c);
+            if (tid < sa.cache.stride) ent0 = e[tid];
+            if (tid + kBlock < sa.cache.stride) ent1 = e[tid + kBlock];
+        }
+        struct Thirds {
+            uint4 a, b, c;
+        };
+        kimkv_decode_lane const rec = __builtin_bit_cast(kimkv_decode_lane, Thirds{r0, r1, r2});
+        lane = rec.lane;
+        lane_first = rec.first_chunk;
+        lane_end = rec.first_chunk + rec.chunk_count;
+        if (!(lane < lane_count && lane_first <= chunk_id && chunk_id < lane_end && lane_end >= lane_first)) {
+            report_fault(P, KIMKV_FAULT_DECODE_ITEM);   // the record does not cover this workgroup
+            return;
+        }
+        record_lane(rec, sa.layer, lane, item, job);
+        if (sa.cache.base != nullptr) {
+            if (tid == 0) s_cache_hdr = __builtin_bit_cast(TableCacheHeader, hdr);
+            if (tid < sa.cache.stride) lds.groups[tid] = __builtin_bit_cast(GroupEntry, ent0);
+            if (tid + kBlock < sa.cache.stride) lds.groups[tid + kBlock] = __builtin_bit_cast(GroupEntry, ent1);
+        }
+    } else if constexpr (kSrc == LaneSource::kArgPrefix) {
         // The last lane whose first chunk is <= chunk_id (scalar loads of the
         // launch arguments), then one round trip for its item and job.
-        ArgPrefix const& ap = [&]() -> ArgPrefix const& {
-            if constexpr (kSrc == LaneSource::kArgPrefix) {
-                return sa;
-            } else {
-                return sa.ap;
-            }
-        }();
+        ArgPrefix const& ap = sa;
         uint32_t lo = 0;
         uint32_t hi = lane_count;
         while (hi - lo > 1) {
@@ -909,12 +1009,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             report_fault(P, KIMKV_FAULT_DECODE_ITEM);
             return;
         }
-        if constexpr (kSrc == LaneSource::kArgPrefix) {
-            item = items[lane];
-            job = writes != nullptr ? writes[lane] : kimkv_append_job{};
-        } else {
-            record_lane(lanes[lane], sa.layer, lane, item, job);
-        }
+        item = items[lane];
+        job = writes != nullptr ? writes[lane] : kimkv_append_job{};
     } else {
         // The prologue is a chain of dependent global reads, and under full
         // HBM load each costs microseconds while this workgroup streams
@@ -982,7 +1078,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     if (writer && !job_ok) report_fault(P, KIMKV_FAULT_APPEND_JOB);
     JobView const jv = job_view(P, job, job_ok);
     if (tid == 0) lds.job = job;   // visible after build_chunk_table's barriers
-    bool const fast = build_chunk_table(P, item, QH, c0, c1, lds, jv);
+    bool fast;
+    if constexpr (kSrc == LaneSource::kRecords) {
+        fast = chunk_table_cached(P, item, QH, c0, c1, lds, jv, sa.cache, chunk_id, s_cache_hdr);
+    } else {
+        fast = build_chunk_table(P, item, QH, c0, c1, lds, jv);
+    }
 
     uint32_t const wave = tid >> 6;
     if (!kSplit) {
@@ -1298,7 +1399,7 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
                            uint32_t chunk_flags, uint32_t query_heads, kimkv_stream_t stream, float* partials,
                            const kimkv_append_job* writes, bool timed, DecodeLaneSlot* slots = nullptr,
                            const uint32_t* host_prefix = nullptr, const kimkv_decode_lane* lanes = nullptr,
-                           const kimkv_decode_layer_args* layer_args = nullptr)
+                           const kimkv_decode_layer_args* layer_args = nullptr, TableCache cache = {})
 {
     bool const head_split = (chunk_flags & KIMKV_DECODE_HEAD_SPLIT) != 0;
     bool const guided = (chunk_flags & KIMKV_DECODE_GUIDED) != 0;
@@ -1306,11 +1407,12 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
     // Lane records: the prefix travels in the arguments, and the merge reads
     // the decode launch's lane slots (there are no items to read).
     bool const records = lanes != nullptr;
-    if (records && (layer_args == nullptr || host_prefix == nullptr || lane_count > KIMKV_DECODE_ARG_PREFIX_LANES
-                    || guided || (total_chunks > lane_count && slots == nullptr))) {
+    if (records && (layer_args == nullptr || lane_count > KIMKV_DECODE_ARG_PREFIX_LANES || guided
+                    || (total_chunks > lane_count && slots == nullptr))) {
         return KIMKV_INVALID_ARGUMENT;
     }
-    if (storage == nullptr || (device_items == nullptr && !records) || device_chunk_prefix == nullptr || lane_count == 0
+    if (storage == nullptr || (!records && (device_items == nullptr || device_chunk_prefix == nullptr))
+        || lane_count == 0
         || query_heads == 0 || query_heads % storage->layout.kv_heads != 0 || storage->layout.head_dim > 256
         || (head_split && guided)
         || (!guided && (chunk_tokens == 0 || chunk_tokens % 64 != 0 || chunk_tokens > kMaxChunk))) {
@@ -1354,8 +1456,8 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
             if constexpr (kL == LaneSource::kArgPrefix) {
                 for (uint32_t i = 0; i <= lane_count; ++i) sa.v[i] = host_prefix[i];
             } else if constexpr (kL == LaneSource::kRecords) {
-                for (uint32_t i = 0; i <= lane_count; ++i) sa.ap.v[i] = host_prefix[i];
                 sa.layer = *layer_args;
+                sa.cache = cache;
             }
             decode_kernel<kS, kT, kL><<<grid, kBlock, 0, s>>>(pv, device_items, device_chunk_prefix, lane_count,
                                                               chunk_tokens, query_heads, partials, writes, slots, tag,
@@ -1574,24 +1676,36 @@ kimkv_status kimkv_paged_decode_write_batch_slots_prefix(const kimkv_storage* st
                                 static_cast<kimkv::DecodeLaneSlot*>(device_lane_slots), host_chunk_prefix);
 }
 
-kimkv_status kimkv_paged_decode_lanes(const kimkv_storage* storage, const kimkv_decode_lane* device_lanes,
-                                      const uint32_t* device_chunk_prefix, const uint32_t* host_chunk_prefix,
+kimkv_status kimkv_paged_decode_lanes(const kimkv_storage* storage, const kimkv_decode_lane* device_chunks,
                                       uint32_t lane_count, uint32_t total_chunks, uint32_t chunk_flags,
                                       uint32_t query_heads, const kimkv_decode_layer_args* args,
-                                      void* device_lane_slots, kimkv_stream_t stream)
+                                      void* device_lane_slots, void* device_table_cache,
+                                      uint64_t table_cache_bytes, uint32_t table_tag, kimkv_stream_t stream)
 {
-    static_assert(sizeof(kimkv_decode_lane) == 32, "lane record is 32 bytes");
-    if (device_lanes == nullptr || args == nullptr || host_chunk_prefix == nullptr
-        || (reinterpret_cast<uintptr_t>(device_lane_slots) & 15u) != 0) {
+    if (device_chunks == nullptr || args == nullptr || (reinterpret_cast<uintptr_t>(device_chunks) & 15u) != 0
+        || (reinterpret_cast<uintptr_t>(device_lane_slots) & 15u) != 0
+        || (reinterpret_cast<uintptr_t>(device_table_cache) & 15u) != 0) {
         return KIMKV_INVALID_ARGUMENT;
     }
-    if (lane_count != 0 && (host_chunk_prefix[0] != 0 || host_chunk_prefix[lane_count] != total_chunks)) {
-        return KIMKV_INVALID_ARGUMENT;
+    kimkv::TableCache cache{};
+    if (device_table_cache != nullptr) {
+        uint32_t const chunk = chunk_flags & ~(KIMKV_DECODE_HEAD_SPLIT | KIMKV_DECODE_GUIDED);
+        uint32_t const stride = (chunk + 7) / 8;
+        if (table_tag == 0 || chunk > kimkv::kTableCacheMaxChunk
+            || table_cache_bytes / kimkv::table_cache_chunk_bytes(stride) < total_chunks) {
+            return KIMKV_INVALID_ARGUMENT;
+        }
+        cache = kimkv::TableCache{static_cast<unsigned char*>(device_table_cache), stride, table_tag};
     }
-    return kimkv::launch_decode(storage, nullptr, device_chunk_prefix, lane_count, total_chunks, chunk_flags,
-                                query_heads, stream, nullptr, nullptr, true,
-                                static_cast<kimkv::DecodeLaneSlot*>(device_lane_slots), host_chunk_prefix,
-                                device_lanes, args);
+    return kimkv::launch_decode(storage, nullptr, nullptr, lane_count, total_chunks, chunk_flags, query_heads,
+                                stream, nullptr, nullptr, true, static_cast<kimkv::DecodeLaneSlot*>(device_lane_slots),
+                                nullptr, device_chunks, args, cache);
+}
+
+uint64_t kimkv_decode_table_cache_bytes(uint32_t total_chunks, uint32_t chunk_flags)
+{
+    uint32_t const chunk = chunk_flags & ~(KIMKV_DECODE_HEAD_SPLIT | KIMKV_DECODE_GUIDED);
+    return static_cast<uint64_t>(total_chunks) * kimkv::table_cache_chunk_bytes((chunk + 7) / 8);
 }
 
 kimkv_status kimkv_paged_decode_batch_noalloc(const kimkv_storage* storage, const kimkv_decode_item* device_items,

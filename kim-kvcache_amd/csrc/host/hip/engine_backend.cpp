@@ -148,47 +148,69 @@ struct BackendState final {
     std::mutex event_mutex;
     std::vector<void*> free_events;   // completion events of finished transactions
 
-    // Device copies of the lane records (kimkv_decode_lane + chunk prefix)
-    // of recent batched attention launches, a few per stream.  The layers of
-    // a token step launch the same lanes with the same records, so the copy
-    // is made when a stream asks for the same records a second time (the
-    // step's second layer: a one-layer step never pays for a copy) and reused
-    // by the later layers.  An entry is written only by copies on its own
-    // stream, which run after that stream's earlier launches that read it,
-    // and is never freed before the backend.  Guarded by the storage's launch
-    // mutex.
+    // Device copies of the chunk records (kimkv_decode_lane, one per chunk)
+    // of recent batched attention launches, a few per stream, each keyed by
+    // its lanes' records and plan (one record per lane, then the chunk
+    // flags).  The layers of a token step launch the same lanes with the same
+    // records, so the copy is made when a stream asks for the same key a
+    // second time (the step's second layer: a one-layer step never pays for
+    // a copy) and reused by the later layers.  An entry is written only by
+    // copies on its own stream, which run after that stream's earlier
+    // launches that read it; a buffer is replaced only after its stream has
+    // drained.  Guarded by the storage's launch mutex.
     struct LaneRecords {
         HipStream stream{nullptr};
-        std::vector<unsigned char> bytes;   // what `device` holds
+        std::vector<unsigned char> key;   // what `device` was expanded from
         DeviceMemory device;
+        std::uint64_t device_bytes{0};
         std::uint64_t used{0};
+        // The chunk group tables of launches from these records
+        // (kimkv_paged_decode_lanes' table cache), tagged per copy of them
+        // and again after any block-table write on the storage.
+        std::uint32_t tag{0};
+        std::uint64_t tag_writes{0};   // the storage's descriptorWrites() when tagged
+        DeviceMemory tables;
+        std::uint64_t tables_bytes{0};
     };
+    static constexpr std::uint32_t kTableCacheMaxChunk = 4096;   // tokens
+    std::uint32_t last_table_tag{0};
     struct LaneRecordsSeen {
         HipStream stream{nullptr};
-        std::vector<unsigned char> bytes;   // the stream's last request without a copy
+        std::vector<unsigned char> key;   // the stream's last request without a copy
     };
     std::vector<LaneRecordsSeen> lane_records_seen;
     static constexpr std::size_t kLaneRecordsPerStream = 4;
     static constexpr std::size_t kLaneRecordEntries = 64;
-    static constexpr std::size_t kLaneRecordBytes =
-        KIMKV_DECODE_ARG_PREFIX_LANES * sizeof(kimkv_decode_lane) + (KIMKV_DECODE_ARG_PREFIX_LANES + 1) * 4;
     std::vector<LaneRecords> lane_records;
     std::uint64_t lane_record_clock{0};
 
-    // Device address of `bytes` for launches on `stream`: an entry already
-    // holding them, or, when the stream asked for the same bytes last time,
-    // one of the stream's entries refilled by a copy on the stream.  nullptr
-    // otherwise (the caller stages the launch another way).
-    void const* laneRecords(std::vector<unsigned char> const& bytes, HipStream stream)
+    // Grows `mem` (capacity `bytes`) to at least `need` bytes for work on
+    // `stream`, draining the stream first when a buffer is replaced.
+    static bool growDevice(DeviceMemory& mem, std::uint64_t& bytes, std::uint64_t need, HipStream stream)
     {
-        if (bytes.size() > kLaneRecordBytes) return nullptr;
+        if (bytes >= need) return true;
+        if (mem.get() != nullptr && kimkv_stream_synchronize(stream) != KIMKV_OK) return false;
+        std::uint64_t const grown = std::max<std::uint64_t>(need, 2 * bytes);
+        mem = DeviceMemory(grown);
+        bytes = mem.get() != nullptr ? grown : 0;
+        return mem.get() != nullptr;
+    }
+
+    // The entry holding the chunk records of `key` (lane records, then the
+    // chunk flags) for launches on `stream`: one already holding them, or,
+    // when the stream asked for the same key last time, one of the stream's
+    // entries refilled by a copy on the stream.  nullptr otherwise (the
+    // caller stages the launch another way).
+    LaneRecords* laneRecords(std::vector<unsigned char> const& key, std::uint32_t total_chunks, HipStream stream)
+    {
         LaneRecords* victim = nullptr;
         std::size_t mine = 0;
         for (LaneRecords& e : lane_records) {
             if (e.stream != stream) continue;
-            if (e.bytes == bytes) {
+            if (e.key == key) {
                 e.used = ++lane_record_clock;
-                return e.device.get();
+                retag(e, false);
+                return &e;
             }
             ++mine;
             if (victim == nullptr || e.used < victim->used) victim = &e;
@@ -202,25 +224,72 @@ struct BackendState final {
             lane_records_seen.push_back(LaneRecordsSeen{stream, {}});
             seen = &lane_records_seen.back();
         }
-        if (seen->bytes != bytes) {   // first request: remember it, copy nothing yet
-            seen->bytes = bytes;
+        if (seen->key != key) {   // first request: remember it, copy nothing yet
+            seen->key = key;
             return nullptr;
         }
-        seen->bytes.clear();
+        seen->key.clear();
         if (mine < kLaneRecordsPerStream && lane_records.size() < kLaneRecordEntries) {
             LaneRecords e;
             e.stream = stream;
-            e.device = DeviceMemory(kLaneRecordBytes);
-            if (e.device.get() == nullptr) return nullptr;
             lane_records.push_back(std::move(e));
             victim = &lane_records.back();
         }
         if (victim == nullptr) return nullptr;
-        victim->bytes.clear();   // unknown contents until the copy is queued
-        if (!storage.ring().uploadTo(victim->device.get(), bytes.data(), bytes.size(), stream)) return nullptr;
-        victim->bytes = bytes;
+        victim->key.clear();   // unknown contents until the copy is queued
+        // One record per chunk: each lane's record repeated over its chunks.
+        std::size_t const rec = sizeof(kimkv_decode_lane);
+        std::size_t const lanes = (key.size() - sizeof(std::uint32_t)) / rec;
+        thread_local std::vector<unsigned char> chunks;
+        chunks.assign(static_cast<std::size_t>(total_chunks) * rec, 0);
+        for (std::size_t i = 0; i < lanes; ++i) {
+            kimkv_decode_lane r;
+            std::memcpy(&r, key.data() + i * rec, rec);
+            if (static_cast<std::uint64_t>(r.first_chunk) + r.chunk_count > total_chunks) return nullptr;
+            for (std::uint32_t k = 0; k < r.chunk_count; ++k) {
+                std::memcpy(chunks.data() + (static_cast<std::size_t>(r.first_chunk) + k) * rec, &r, rec);
+            }
+        }
+        if (!growDevice(victim->device, victim->device_bytes, chunks.size(), stream)
+            || !storage.ring().uploadTo(victim->device.get(), chunks.data(), chunks.size(), stream)) {
+            return nullptr;
+        }
+        victim->key = key;
         victim->used = ++lane_record_clock;
-        return victim->device.get();
+        retag(*victim, true);
+        return victim;
+    }
+
+    // A fresh table tag (never 0) for new records, or when a block table may
+    // have changed since the entry was tagged: a tag names one set of
+    // records over unchanged tables.  Under the storage's launch mutex.
+    void retag(LaneRecords& e, bool fresh_records)
+    {
+        std::uint64_t const writes = storage.descriptorWrites();
+        if (!fresh_records && e.tag != 0 && e.tag_writes == writes) return;
+        e.tag = ++last_table_tag == 0 ? ++last_table_tag : last_table_tag;
+        e.tag_writes = writes;
+    }
+
+    // The entry's table cache for a launch of total_chunks chunks planned
+    // with chunk_flags (grown, and zeroed, on the entry's stream when too
+    // small), or nullptr when chunks are too long to cache or memory is short.
+    void* laneTables(LaneRecords& e, std::uint32_t total_chunks, std::uint32_t chunk_flags, std::uint64_t& bytes)
+    {
+        std::uint32_t const chunk = chunk_flags & ~(KIMKV_DECODE_HEAD_SPLIT | KIMKV_DECODE_GUIDED);
+        if (chunk > kTableCacheMaxChunk) return nullptr;
+        std::uint64_t const need = kimkv_decode_table_cache_bytes(total_chunks, chunk_flags);
+        if (e.tables_bytes < need) {
+            // A new buffer starts zeroed: tag 0 is never a launch's.
+            if (!growDevice(e.tables, e.tables_bytes, need, e.stream)
+                || kimkv_fill_f16(static_cast<std::uint16_t*>(e.tables.get()), e.tables_bytes / 2, 0, e.stream)
+                       != KIMKV_OK) {
+                e.tables_bytes = 0;
+                return nullptr;
+            }
+        }
+        bytes = e.tables_bytes;
+        return e.tables.get();
     }
 
     BackendState(EngineKvConfig c, std::uint32_t micro, std::uint32_t extent)
@@ -429,13 +498,14 @@ public:
         return ok;
     }
 
-    // kimkv_decode_lane records of the first n launched lanes followed by
-    // their chunk prefix: the bytes kimkv_paged_decode_lanes reads.
+    // The key of the first n launched lanes' chunk records: one
+    // kimkv_decode_lane per lane (its chunks given by the prefix), then the
+    // planned chunk flags (so that a copy stands for one plan).
     static void laneRecordBytes(DevicePagedDecodeBatchItem const* h, std::vector<kimkv_append_job> const& writes,
-                                std::vector<std::uint32_t> const& pre, std::size_t n,
+                                std::vector<std::uint32_t> const& pre, std::uint32_t chunk, std::size_t n,
                                 std::vector<unsigned char>& out)
     {
-        out.assign(n * sizeof(kimkv_decode_lane) + (n + 1) * sizeof(std::uint32_t), 0);
+        out.assign(n * sizeof(kimkv_decode_lane) + sizeof(std::uint32_t), 0);
         for (std::size_t i = 0; i < n; ++i) {
             kimkv_decode_lane r{};
             r.descriptors = reinterpret_cast<kimkv_block_desc const*>(h[i].device_descriptors);
@@ -451,9 +521,12 @@ public:
                 r.cow_kind = w.cow_kind;
                 r.has_write = 1;
             }
+            r.lane = static_cast<std::uint32_t>(i);
+            r.first_chunk = pre[i];
+            r.chunk_count = pre[i + 1] - pre[i];
             std::memcpy(out.data() + i * sizeof(r), &r, sizeof(r));
         }
-        std::memcpy(out.data() + n * sizeof(kimkv_decode_lane), pre.data(), (n + 1) * sizeof(std::uint32_t));
+        std::memcpy(out.data() + n * sizeof(kimkv_decode_lane), &chunk, sizeof(chunk));
     }
 
     void attendLayerBatch(PagedDecodeBatch& batch) override
@@ -526,14 +599,17 @@ public:
             // first layer made: no workgroup reads host memory before its
             // block table.
             thread_local std::vector<unsigned char> records;
-            laneRecordBytes(batch.host_items, writes, pre, n, records);
-            void const* dev = o.laneRecords(records, stream);
+            laneRecordBytes(batch.host_items, writes, pre, chunk, n, records);
+            BackendState::LaneRecords* rec = o.laneRecords(records, total, stream);
             void* slots = total > n ? st.ring().deviceScratch(n * KIMKV_DECODE_LANE_SLOT_BYTES, stream) : nullptr;
-            if (dev != nullptr && (total == n || slots != nullptr)) {
-                auto const* lanes_d = static_cast<kimkv_decode_lane const*>(dev);
-                auto const* prefix_d = reinterpret_cast<std::uint32_t const*>(lanes_d + n);
-                k = kimkv_paged_decode_lanes(st.handle(), lanes_d, prefix_d, pre.data(), static_cast<std::uint32_t>(n),
-                                             total, chunk, QH, &args, slots, stream);
+            if (rec != nullptr && (total == n || slots != nullptr)) {
+                // Chunk group tables cached per copy of the records: built
+                // by the first launch from them, read by the later layers.
+                std::uint64_t table_bytes = 0;
+                void* tables = o.laneTables(*rec, total, chunk, table_bytes);
+                k = kimkv_paged_decode_lanes(st.handle(), static_cast<kimkv_decode_lane const*>(rec->device.get()),
+                                             static_cast<std::uint32_t>(n), total, chunk, QH, &args, slots, tables,
+                                             table_bytes, tables != nullptr ? rec->tag : 0, stream);
                 launched_from_records = true;
                 if (k == KIMKV_OK) o.lane_record_launches.fetch_add(1, std::memory_order_relaxed);
             }
@@ -1187,6 +1263,7 @@ public:
         std::memcpy(staging_.data() + head, sources_.data(), sources_.size() * sizeof(kimkv_block_desc));
         {
             std::lock_guard<std::mutex> launch(storage_.launchMutex());
+            storage_.noteDescriptorWrite();
             auto* staged = static_cast<unsigned char*>(storage_.ring().stage(staging_.data(), staging_.size(), stream_));
             kimkv_status const k = staged == nullptr
                 ? KIMKV_SUBMISSION_FAILED
@@ -1612,6 +1689,7 @@ public:
         {
             // Fenced by the chunk's first attention launch on this stream.
             std::lock_guard<std::mutex> launch(st.launchMutex());
+            st.noteDescriptorWrite();
             if (!st.ring().uploadTo(impl->arena->ptr, d.data(), bytes, stream)) {
                 return cancel({EngineKvError::SubmissionFailed});
             }

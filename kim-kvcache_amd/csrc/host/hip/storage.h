@@ -145,6 +145,11 @@ public:
     // fence always covers the regions staged just before it.
     std::mutex& launchMutex() noexcept { return launch_mutex_; }
     DeviceBufferCache& buffers() noexcept { return buffers_; }
+    // Device block-table writes enqueued on this storage so far (reserve
+    // patches, prefill table uploads), counted under launchMutex(): data
+    // derived from the tables' device contents is reusable while it holds.
+    void noteDescriptorWrite() noexcept { ++descriptor_writes_; }
+    [[nodiscard]] std::uint64_t descriptorWrites() const noexcept { return descriptor_writes_; }
 
     // Synchronous data-path operations used by HipKvCache: enqueue on
     // `stream`, then wait for completion.
@@ -194,6 +199,7 @@ private:
     HipStatus status_{};
     StagingRing ring_;
     std::mutex launch_mutex_;
+    std::uint64_t descriptor_writes_{0};
     DeviceBufferCache buffers_;
     // Per-slot visit stamps for the O(entries) duplicate-page check.
     mutable std::mutex stamp_mutex_;

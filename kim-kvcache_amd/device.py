@@ -89,12 +89,13 @@ class DecodeLayerArgs(ctypes.Structure):
                 ("value", ctypes.c_uint64), ("value_stride", ctypes.c_uint64)]
 
 
-# kimkv_decode_lane (32 bytes): the step-constant part of a lane of a batched decode.
+# kimkv_decode_lane (48 bytes): one chunk of a batched decode with its lane's step-constant part.
 DECODE_LANE = np.dtype([("descriptors", np.uint64), ("descriptor_count", np.uint32), ("token_count", np.uint32),
                         ("dst_slot", np.uint32), ("cow_slot", np.uint32), ("dst_token", np.uint16),
                         ("cow_tokens", np.uint16), ("dst_kind", np.uint8), ("cow_kind", np.uint8),
-                        ("has_write", np.uint8), ("reserved", np.uint8)])
-assert DECODE_LANE.itemsize == 32
+                        ("has_write", np.uint8), ("reserved", np.uint8), ("lane", np.uint32),
+                        ("first_chunk", np.uint32), ("chunk_count", np.uint32), ("reserved2", np.uint32)])
+assert DECODE_LANE.itemsize == 48
 
 
 class StorageInfo(ctypes.Structure):
@@ -156,9 +157,10 @@ _SIGNATURES = {
     "kimkv_paged_decode_write_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                       ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                                       ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]),
-    "kimkv_paged_decode_lanes": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                                                 ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
-                                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    "kimkv_paged_decode_lanes": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                                 ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
+                                                 ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_void_p]),
+    "kimkv_decode_table_cache_bytes": (ctypes.c_uint64, [ctypes.c_uint32, ctypes.c_uint32]),
     "kimkv_paged_decode_write_batch_slots_prefix": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p,
                                                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
                                                                     ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
@@ -450,16 +452,15 @@ class Storage:
                                                          ctypes.c_void_p(slots_ptr), _sh(stream)),
               "paged_decode_write_batch_slots")
 
-    def decode_lanes_launch(self, lanes_ptr: int, prefix_ptr: int, host_prefix: np.ndarray, lanes: int,
-                            total_chunks: int, chunk_tokens: int, query_heads: int, args: DecodeLayerArgs,
-                            slots_ptr: int, stream: Optional[Stream] = None) -> int:
-        """kimkv_paged_decode_lanes (lanes_ptr: DECODE_LANE records in device memory; args: the layer's
-        evenly spaced addresses); returns the status."""
-        hp = np.ascontiguousarray(host_prefix, dtype=np.uint32)
+    def decode_lanes_launch(self, chunks_ptr: int, lanes: int, total_chunks: int, chunk_tokens: int,
+                            query_heads: int, args: DecodeLayerArgs, slots_ptr: int, stream: Optional[Stream] = None,
+                            cache_ptr: int = 0, cache_bytes: int = 0, tag: int = 0) -> int:
+        """kimkv_paged_decode_lanes (chunks_ptr: one DECODE_LANE record per chunk in device memory; args: the
+        layer's evenly spaced addresses; cache_ptr/cache_bytes/tag: the optional chunk table cache); returns
+        the status."""
         return lib().kimkv_paged_decode_lanes(
-            self.h, ctypes.c_void_p(lanes_ptr), ctypes.c_void_p(prefix_ptr), hp.ctypes.data_as(ctypes.c_void_p),
-            lanes, total_chunks, chunk_tokens, query_heads, ctypes.byref(args), ctypes.c_void_p(slots_ptr),
-            _sh(stream))
+            self.h, ctypes.c_void_p(chunks_ptr), lanes, total_chunks, chunk_tokens, query_heads, ctypes.byref(args),
+            ctypes.c_void_p(slots_ptr), ctypes.c_void_p(cache_ptr), cache_bytes, tag, _sh(stream))
 
     def decode_write_slots_prefix_launch(self, items_ptr: int, prefix_ptr: int, host_prefix: np.ndarray,
                                          lanes: int, total_chunks: int, chunk_tokens: int, query_heads: int,
@@ -545,6 +546,11 @@ def decode_plan(storage_handle: int, token_counts, query_heads: int):
                                   len(counts), query_heads, ctypes.byref(chunk),
                                   prefix.ctypes.data_as(ctypes.c_void_p), ctypes.byref(total)), "decode_plan")
     return int(chunk.value), prefix, int(total.value)
+
+
+def table_cache_bytes(total_chunks: int, chunk_tokens: int) -> int:
+    """kimkv_decode_table_cache_bytes: the chunk table cache of a lane-record decode launch."""
+    return int(lib().kimkv_decode_table_cache_bytes(total_chunks, chunk_tokens))
 
 
 def workspace_bytes(token_count: int, chunk_tokens: int, query_heads: int, head_dim: int) -> int:

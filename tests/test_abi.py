@@ -35,7 +35,7 @@ def test_struct_layouts_match_reference_sizes(kimkv):
     assert d.PROMOTION_JOB.itemsize == 36   # PromotionSlots + target slot
     assert d.PREFILL_ITEM.itemsize == 48
     assert d.PREFILL_BLOCK.itemsize == 8
-    assert d.DECODE_LANE.itemsize == 32      # kimkv_decode_lane (no reference counterpart)
+    assert d.DECODE_LANE.itemsize == 48      # kimkv_decode_lane (no reference counterpart)
     assert ctypes.sizeof(d.DecodeLayerArgs) == 88
 
 

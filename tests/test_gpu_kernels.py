@@ -370,7 +370,9 @@ def test_decode_lane_records_match_item_launch(dev, mode, order):
     and the layer's evenly spaced addresses) equals kimkv_paged_decode_write_batch_slots_prefix with the
     same items and jobs, bit for bit in the outputs and the pages: tail writes, fresh pages, copy-on-write
     tails, single- and multi-chunk lanes, lanes in address order (order 1) and reversed (order -1: negative
-    strides).  Malformed launches are refused without running."""
+    strides).  With a chunk table cache: the first launch of a tag builds and stores the tables, the next
+    two read them, and a new tag over the same cache rebuilds them; every launch gives the same outputs.
+    Malformed launches are refused without running."""
     shape = (3, 4, 64)
     L, H, D = shape
     QH, layer = 32, 1
@@ -433,12 +435,14 @@ def test_decode_lane_records_match_item_launch(dev, mode, order):
             items[i] = (dbuf.ptr, len(t), counts[i], layer, qs.ptr + k * QH * D * 2,
                         ws.ptr + k * ws_stride if wsz else 0, out.ptr + k * QH * D * 2, 0.125)
             lanes[i] = (dbuf.ptr, len(t), counts[i], j["dst_slot"], j["cow_slot"], j["dst_token"], j["cow_tokens"],
-                        j["dst_kind"], j["cow_kind"], 1, 0)
+                        j["dst_kind"], j["cow_kind"], 1, 0, i, prefix[i], prefix[i + 1] - prefix[i], 0)
         slots = dev.DeviceBuffer(n * dev.DECODE_LANE_SLOT_BYTES)
         pbuf = dev.upload(prefix)
         keep += [slots, pbuf]
         if records:
-            lbuf = dev.upload(lanes)
+            chunks = np.concatenate([np.repeat(lanes[i:i + 1], prefix[i + 1] - prefix[i]) for i in range(n)])
+            assert len(chunks) == total
+            lbuf = dev.upload(chunks)
             keep.append(lbuf)
             step = -1 if order == -1 else 1
             a = dev.DecodeLayerArgs()
@@ -449,18 +453,40 @@ def test_decode_lane_records_match_item_launch(dev, mode, order):
             a.workspace, a.workspace_stride = ws.ptr + slot_of[0] * ws_stride, (step * ws_stride) % m
             a.key, a.key_stride = src.ptr + slot_of[0] * 4 * H * D, (step * 4 * H * D) % m
             a.value, a.value_stride = src.ptr + slot_of[0] * 4 * H * D + 2 * H * D, (step * 4 * H * D) % m
-            bad = prefix.copy()
-            bad[-1] += 1
-            assert storage.decode_lanes_launch(lbuf.ptr, pbuf.ptr, bad, n, total, chunk, QH, a,
-                                               slots.ptr) == dev.INVALID_ARGUMENT
-            assert storage.decode_lanes_launch(lbuf.ptr, pbuf.ptr, prefix, n, total, chunk, QH, a,
+            assert storage.decode_lanes_launch(lbuf.ptr, n, total, chunk, QH, a,
                                                0) == dev.INVALID_ARGUMENT     # split lanes need merge records
-            assert storage.decode_lanes_launch(lbuf.ptr, pbuf.ptr, prefix, n, total, dev.DECODE_GUIDED | 64, QH, a,
+            assert storage.decode_lanes_launch(lbuf.ptr, n, total, dev.DECODE_GUIDED | 64, QH, a,
                                                slots.ptr) == dev.INVALID_ARGUMENT
-            big = np.concatenate([prefix, np.full(70 - n, total, dtype=np.uint32)])
-            assert storage.decode_lanes_launch(lbuf.ptr, pbuf.ptr, big, 69, total, chunk, QH, a,
+            assert storage.decode_lanes_launch(lbuf.ptr, 69, total, chunk, QH, a,
                                                slots.ptr) == dev.INVALID_ARGUMENT     # more than 64 lanes
-            assert storage.decode_lanes_launch(lbuf.ptr, pbuf.ptr, prefix, n, total, chunk, QH, a, slots.ptr) == 0
+            need = dev.table_cache_bytes(total, chunk)
+            cache = dev.upload(np.full(need // 2, 0x7777, dtype=np.uint16))    # leftovers, no valid tag
+            keep.append(cache)
+            assert storage.decode_lanes_launch(lbuf.ptr, n, total, chunk, QH, a, slots.ptr,
+                                               cache_ptr=cache.ptr, cache_bytes=need - 16,
+                                               tag=5) == dev.INVALID_ARGUMENT       # cache too small
+            assert storage.decode_lanes_launch(lbuf.ptr, n, total, chunk, QH, a, slots.ptr,
+                                               cache_ptr=cache.ptr, cache_bytes=need,
+                                               tag=0) == dev.INVALID_ARGUMENT       # tag 0 is reserved
+            # Records that do not describe their chunk (a lane past lane_count, a chunk range that
+            # misses the chunk) are reported by the workgroup and skipped.
+            wrong = chunks.copy()
+            wrong[0]["lane"] = n
+            wrong[total - 1]["first_chunk"] = total
+            wbuf = dev.upload(wrong)
+            keep.append(wbuf)
+            assert storage.decode_lanes_launch(wbuf.ptr, n, total, chunk, QH, a, slots.ptr) == 0
+            status, bits = storage.faults()
+            assert status == dev.INVALID_ARGUMENT and bits & dev.FAULT_DECODE_ITEM, (status, bits)
+            runs = [dict()] + [dict(cache_ptr=cache.ptr, cache_bytes=need, tag=t) for t in (5, 5, 5, 6)]
+            for kw in runs:
+                assert storage.decode_lanes_launch(lbuf.ptr, n, total, chunk, QH, a, slots.ptr, **kw) == 0
+                dev.sync()
+                snap = dev.download(out.ptr, (n, QH * D), np.uint16)
+                if kw:
+                    assert np.array_equal(snap, first), kw
+                else:
+                    first = snap
         else:
             ibuf, jbuf = dev.upload(items), dev.upload(jobs)
             keep += [ibuf, jbuf]
