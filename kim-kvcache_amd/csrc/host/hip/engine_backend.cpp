@@ -185,12 +185,15 @@ struct BackendState final {
     std::uint64_t lane_record_clock{0};
 
     // Grows `mem` (capacity `bytes`) to at least `need` bytes for work on
-    // `stream`, draining the stream first when a buffer is replaced.
+    // `stream`, draining the stream first when a buffer is replaced.  Sizes
+    // leave headroom (at least 64 KiB, 1.5x the need, twice the old size):
+    // a batch's chunk count creeps up as its lanes grow, and each
+    // replacement waits for the stream.
     static bool growDevice(DeviceMemory& mem, std::uint64_t& bytes, std::uint64_t need, HipStream stream)
     {
         if (bytes >= need) return true;
         if (mem.get() != nullptr && kimkv_stream_synchronize(stream) != KIMKV_OK) return false;
-        std::uint64_t const grown = std::max<std::uint64_t>(need, 2 * bytes);
+        std::uint64_t const grown = std::max<std::uint64_t>({need + need / 2, 2 * bytes, std::uint64_t{64} << 10});
         mem = DeviceMemory(grown);
         bytes = mem.get() != nullptr ? grown : 0;
         return mem.get() != nullptr;
