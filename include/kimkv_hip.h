@@ -460,8 +460,13 @@ typedef struct kimkv_decode_layer_args {
  * to the host).  For a caller whose lanes' queries, outputs, workspaces and
  * new rows are evenly spaced (base + lane * stride), which keeps the records
  * across a step's layers.  lane_count at most KIMKV_DECODE_ARG_PREFIX_LANES;
- * device_lane_slots required when total_chunks > lane_count; not with
- * KIMKV_DECODE_GUIDED.  A record that names a lane past lane_count or a chunk
+ * not with KIMKV_DECODE_GUIDED.  When total_chunks > lane_count the split-K
+ * merge needs each lane's chunk count: from host_chunk_prefix (optional,
+ * NULL for none; lane_count + 1 entries in host memory, 0 first,
+ * total_chunks last, strictly increasing, the plan the records were made
+ * from), which travels in the merge launch's arguments with the layer's
+ * output and workspace bases, so its first reads are the partials; else
+ * from device_lane_slots, which is then required.  A record that names a lane past lane_count or a chunk
  * range that does not hold its own chunk, or lies outside the launch, is
  * reported (KIMKV_FAULT_DECODE_ITEM) and skipped.
  * device_table_cache (optional, NULL for none; 16-byte aligned, at least
@@ -481,8 +486,9 @@ typedef struct kimkv_decode_layer_args {
 kimkv_status kimkv_paged_decode_lanes(const kimkv_storage* storage, const kimkv_decode_lane* device_chunks,
                                       uint32_t lane_count, uint32_t total_chunks, uint32_t chunk_flags,
                                       uint32_t query_heads, const kimkv_decode_layer_args* args,
-                                      void* device_lane_slots, void* device_table_cache,
-                                      uint64_t table_cache_bytes, uint32_t table_tag, kimkv_stream_t stream);
+                                      const uint32_t* host_chunk_prefix, void* device_lane_slots,
+                                      void* device_table_cache, uint64_t table_cache_bytes, uint32_t table_tag,
+                                      kimkv_stream_t stream);
 /* Bytes of the table cache of kimkv_paged_decode_lanes for a launch of
  * total_chunks chunks planned with chunk_flags.  No counterpart in the
  * reference. */

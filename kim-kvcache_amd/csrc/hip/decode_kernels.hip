@@ -1214,23 +1214,47 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 // chunks fold into the running (M, den, acc) like an online softmax.
 constexpr unsigned kCombineHeads = 4;
 
+// Where the merge of a record launch finds its lanes: each lane's output
+// and partials at base + lane * stride, its chunk count from the chunk
+// prefix, all in the launch arguments, so a block's first loads are its
+// partials.
+struct CombineLaneArgs {
+    uint16_t* output;
+    uint64_t output_stride;   // bytes
+    float* workspace;
+    uint64_t workspace_stride;   // bytes
+    uint32_t prefix[KIMKV_DECODE_ARG_PREFIX_LANES + 1];
+};
+struct NoCombineLaneArgs {};
+
 // slots: when non-null, the lanes' merge records the decode launch tagged
-// `tag` replace the items and the chunk prefix.
-template <uint32_t kDims>
+// `tag` replace the items and the chunk prefix.  With CombineLaneArgs the
+// launch arguments replace all three.
+template <uint32_t kDims, typename LaneArgs>
 __global__ __launch_bounds__(64 * kCombineHeads) void combine_kernel(PoolView P, const kimkv_decode_item* items,
                                                                     const uint32_t* prefix, uint32_t total_chunks,
                                                                     uint32_t QH, uint32_t D, float* partials,
-                                                                    const DecodeLaneSlot* slots, uint64_t tag)
+                                                                    const DecodeLaneSlot* slots, uint64_t tag,
+                                                                    LaneArgs la)
 {
     constexpr uint32_t kBatch = 64 / kDims;   // partial rows held in registers at once
     uint32_t const lane = blockIdx.x;
     uint32_t const q = blockIdx.y * kCombineHeads + (threadIdx.x >> 6);
     uint32_t const l = threadIdx.x & 63u;
-    if (q >= QH) return;
     uint32_t n = 0;
     uint16_t* output = nullptr;
     const float* workspace = nullptr;
-    if (slots != nullptr) {
+    if constexpr (std::is_same_v<LaneArgs, CombineLaneArgs>) {
+        // Every argument the block needs is read in one round, before the
+        // first test (which names the workspace so the load is not sunk
+        // below it).
+        n = la.prefix[lane + 1] - la.prefix[lane];
+        output = at_stride(la.output, la.output_stride, lane);
+        workspace = at_stride(la.workspace, la.workspace_stride, lane);
+        if (q >= QH || n <= 1 || workspace == nullptr) return;
+    } else if (q >= QH) {
+        return;
+    } else if (slots != nullptr) {
         DecodeLaneSlot const slot = slots[lane];
         if (slot.tag != tag || slot.lane != lane) return;   // no decode workgroup of this launch wrote it
         n = slot.chunks;
@@ -1404,11 +1428,13 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
     bool const head_split = (chunk_flags & KIMKV_DECODE_HEAD_SPLIT) != 0;
     bool const guided = (chunk_flags & KIMKV_DECODE_GUIDED) != 0;
     uint32_t const chunk_tokens = chunk_flags & ~(KIMKV_DECODE_HEAD_SPLIT | KIMKV_DECODE_GUIDED);
-    // Lane records: the prefix travels in the arguments, and the merge reads
-    // the decode launch's lane slots (there are no items to read).
+    // Lane records: the merge takes its lanes from the chunk prefix and the
+    // layer's addresses in its arguments when the caller gives the prefix,
+    // else from the decode launch's lane slots (there are no items to read).
     bool const records = lanes != nullptr;
     if (records && (layer_args == nullptr || lane_count > KIMKV_DECODE_ARG_PREFIX_LANES || guided
-                    || (total_chunks > lane_count && slots == nullptr))) {
+                    || (total_chunks > lane_count && slots == nullptr && host_prefix == nullptr)
+                    || (total_chunks > lane_count && layer_args->workspace == nullptr))) {
         return KIMKV_INVALID_ARGUMENT;
     }
     if (storage == nullptr || (!records && (device_items == nullptr || device_chunk_prefix == nullptr))
@@ -1485,18 +1511,31 @@ kimkv_status launch_decode(const kimkv_storage* storage, const kimkv_decode_item
     if (total_chunks > lane_count) {
         dim3 const cgrid(lane_count, (query_heads + kCombineHeads - 1) / kCombineHeads);
         uint32_t const D = storage->layout.head_dim;
-        if (D <= 64) {
-            combine_kernel<1><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
-                                                                     device_chunk_prefix, total_chunks,
-                                                                     query_heads, D, partials, slots, tag);
-        } else if (D <= 128) {
-            combine_kernel<2><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
-                                                                     device_chunk_prefix, total_chunks,
-                                                                     query_heads, D, partials, slots, tag);
+        auto merge = [&](auto la) {
+            if (D <= 64) {
+                combine_kernel<1><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
+                                                                         device_chunk_prefix, total_chunks,
+                                                                         query_heads, D, partials, slots, tag, la);
+            } else if (D <= 128) {
+                combine_kernel<2><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
+                                                                         device_chunk_prefix, total_chunks,
+                                                                         query_heads, D, partials, slots, tag, la);
+            } else {
+                combine_kernel<4><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
+                                                                         device_chunk_prefix, total_chunks,
+                                                                         query_heads, D, partials, slots, tag, la);
+            }
+        };
+        if (records && host_prefix != nullptr) {
+            CombineLaneArgs la{};
+            la.output = layer_args->output;
+            la.output_stride = layer_args->output_stride;
+            la.workspace = layer_args->workspace;
+            la.workspace_stride = layer_args->workspace_stride;
+            for (uint32_t i = 0; i <= lane_count; ++i) la.prefix[i] = host_prefix[i];
+            merge(la);
         } else {
-            combine_kernel<4><<<cgrid, 64 * kCombineHeads, 0, s>>>(pool_view(*storage), device_items,
-                                                                     device_chunk_prefix, total_chunks,
-                                                                     query_heads, D, partials, slots, tag);
+            merge(NoCombineLaneArgs{});
         }
         return launch_status();
     }
@@ -1679,13 +1718,25 @@ kimkv_status kimkv_paged_decode_write_batch_slots_prefix(const kimkv_storage* st
 kimkv_status kimkv_paged_decode_lanes(const kimkv_storage* storage, const kimkv_decode_lane* device_chunks,
                                       uint32_t lane_count, uint32_t total_chunks, uint32_t chunk_flags,
                                       uint32_t query_heads, const kimkv_decode_layer_args* args,
-                                      void* device_lane_slots, void* device_table_cache,
-                                      uint64_t table_cache_bytes, uint32_t table_tag, kimkv_stream_t stream)
+                                      const uint32_t* host_chunk_prefix, void* device_lane_slots,
+                                      void* device_table_cache, uint64_t table_cache_bytes, uint32_t table_tag,
+                                      kimkv_stream_t stream)
 {
     if (device_chunks == nullptr || args == nullptr || (reinterpret_cast<uintptr_t>(device_chunks) & 15u) != 0
         || (reinterpret_cast<uintptr_t>(device_lane_slots) & 15u) != 0
         || (reinterpret_cast<uintptr_t>(device_table_cache) & 15u) != 0) {
         return KIMKV_INVALID_ARGUMENT;
+    }
+    if (host_chunk_prefix != nullptr) {
+        // A plan of this launch: starts at 0, ends at total_chunks, every
+        // lane at least one chunk.
+        if (lane_count > KIMKV_DECODE_ARG_PREFIX_LANES || host_chunk_prefix[0] != 0
+            || host_chunk_prefix[lane_count] != total_chunks) {
+            return KIMKV_INVALID_ARGUMENT;
+        }
+        for (uint32_t i = 0; i < lane_count; ++i) {
+            if (host_chunk_prefix[i + 1] <= host_chunk_prefix[i]) return KIMKV_INVALID_ARGUMENT;
+        }
     }
     kimkv::TableCache cache{};
     if (device_table_cache != nullptr) {
@@ -1699,7 +1750,7 @@ kimkv_status kimkv_paged_decode_lanes(const kimkv_storage* storage, const kimkv_
     }
     return kimkv::launch_decode(storage, nullptr, nullptr, lane_count, total_chunks, chunk_flags, query_heads,
                                 stream, nullptr, nullptr, true, static_cast<kimkv::DecodeLaneSlot*>(device_lane_slots),
-                                nullptr, device_chunks, args, cache);
+                                host_chunk_prefix, device_chunks, args, cache);
 }
 
 uint64_t kimkv_decode_table_cache_bytes(uint32_t total_chunks, uint32_t chunk_flags)

@@ -597,22 +597,24 @@ public:
         kimkv_status k = KIMKV_SUBMISSION_FAILED;
         bool launched_from_records = false;
         kimkv_decode_layer_args args{};
-        if (n <= KIMKV_DECODE_ARG_PREFIX_LANES && evenLayerArgs(batch, launched, writes, n, args)) {
+        if (n <= KIMKV_DECODE_ARG_PREFIX_LANES && evenLayerArgs(batch, launched, writes, n, args)
+            && (total == n || args.workspace != nullptr)) {
             // Every lane's step-constant record from a device copy the step's
             // first layer made: no workgroup reads host memory before its
             // block table.
             thread_local std::vector<unsigned char> records;
             laneRecordBytes(batch.host_items, writes, pre, chunk, n, records);
             BackendState::LaneRecords* rec = o.laneRecords(records, total, stream);
-            void* slots = total > n ? st.ring().deviceScratch(n * KIMKV_DECODE_LANE_SLOT_BYTES, stream) : nullptr;
-            if (rec != nullptr && (total == n || slots != nullptr)) {
+            if (rec != nullptr) {
                 // Chunk group tables cached per copy of the records: built
                 // by the first launch from them, read by the later layers.
+                // The merge takes the lanes' chunk counts from the prefix in
+                // its arguments (no merge records).
                 std::uint64_t table_bytes = 0;
                 void* tables = o.laneTables(*rec, total, chunk, table_bytes);
                 k = kimkv_paged_decode_lanes(st.handle(), static_cast<kimkv_decode_lane const*>(rec->device.get()),
-                                             static_cast<std::uint32_t>(n), total, chunk, QH, &args, slots, tables,
-                                             table_bytes, tables != nullptr ? rec->tag : 0, stream);
+                                             static_cast<std::uint32_t>(n), total, chunk, QH, &args, pre.data(),
+                                             nullptr, tables, table_bytes, tables != nullptr ? rec->tag : 0, stream);
                 launched_from_records = true;
                 if (k == KIMKV_OK) o.lane_record_launches.fetch_add(1, std::memory_order_relaxed);
             }

@@ -159,7 +159,8 @@ _SIGNATURES = {
                                                       ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]),
     "kimkv_paged_decode_lanes": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                                  ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
-                                                 ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_void_p]),
+                                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32,
+                                                 ctypes.c_void_p]),
     "kimkv_decode_table_cache_bytes": (ctypes.c_uint64, [ctypes.c_uint32, ctypes.c_uint32]),
     "kimkv_paged_decode_write_batch_slots_prefix": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p,
                                                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
@@ -454,13 +455,17 @@ class Storage:
 
     def decode_lanes_launch(self, chunks_ptr: int, lanes: int, total_chunks: int, chunk_tokens: int,
                             query_heads: int, args: DecodeLayerArgs, slots_ptr: int, stream: Optional[Stream] = None,
-                            cache_ptr: int = 0, cache_bytes: int = 0, tag: int = 0) -> int:
+                            cache_ptr: int = 0, cache_bytes: int = 0, tag: int = 0,
+                            host_prefix: Optional[np.ndarray] = None) -> int:
         """kimkv_paged_decode_lanes (chunks_ptr: one DECODE_LANE record per chunk in device memory; args: the
-        layer's evenly spaced addresses; cache_ptr/cache_bytes/tag: the optional chunk table cache); returns
+        layer's evenly spaced addresses; cache_ptr/cache_bytes/tag: the optional chunk table cache;
+        host_prefix: the optional chunk prefix the merge takes from its arguments instead of slots); returns
         the status."""
+        hp = None if host_prefix is None else np.ascontiguousarray(host_prefix, dtype=np.uint32)
         return lib().kimkv_paged_decode_lanes(
             self.h, ctypes.c_void_p(chunks_ptr), lanes, total_chunks, chunk_tokens, query_heads, ctypes.byref(args),
-            ctypes.c_void_p(slots_ptr), ctypes.c_void_p(cache_ptr), cache_bytes, tag, _sh(stream))
+            None if hp is None else hp.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(slots_ptr),
+            ctypes.c_void_p(cache_ptr), cache_bytes, tag, _sh(stream))
 
     def decode_write_slots_prefix_launch(self, items_ptr: int, prefix_ptr: int, host_prefix: np.ndarray,
                                          lanes: int, total_chunks: int, chunk_tokens: int, query_heads: int,

@@ -478,9 +478,24 @@ def test_decode_lane_records_match_item_launch(dev, mode, order):
             assert storage.decode_lanes_launch(wbuf.ptr, n, total, chunk, QH, a, slots.ptr) == 0
             status, bits = storage.faults()
             assert status == dev.INVALID_ARGUMENT and bits & dev.FAULT_DECODE_ITEM, (status, bits)
+            bad = prefix.copy()
+            bad[-1] += 1
+            assert storage.decode_lanes_launch(lbuf.ptr, n, total, chunk, QH, a, 0,
+                                               host_prefix=bad) == dev.INVALID_ARGUMENT   # ends past total
+            bad = prefix.copy()
+            bad[1] = bad[0]
+            assert storage.decode_lanes_launch(lbuf.ptr, n, total, chunk, QH, a, 0,
+                                               host_prefix=bad) == dev.INVALID_ARGUMENT   # a lane without chunks
+            # Merge from slots, then from the prefix in its arguments (no slots), each with and
+            # without the table cache: every output the same.
             runs = [dict()] + [dict(cache_ptr=cache.ptr, cache_bytes=need, tag=t) for t in (5, 5, 5, 6)]
+            runs += [dict(host_prefix=prefix, slots=0), dict(host_prefix=prefix, slots=0, cache_ptr=cache.ptr,
+                                                               cache_bytes=need, tag=7),
+                     dict(host_prefix=prefix, slots=0, cache_ptr=cache.ptr, cache_bytes=need, tag=7)]
             for kw in runs:
-                assert storage.decode_lanes_launch(lbuf.ptr, n, total, chunk, QH, a, slots.ptr, **kw) == 0
+                kw = dict(kw)
+                sp = kw.pop("slots", slots.ptr)
+                assert storage.decode_lanes_launch(lbuf.ptr, n, total, chunk, QH, a, sp, **kw) == 0
                 dev.sync()
                 snap = dev.download(out.ptr, (n, QH * D), np.uint16)
                 if kw:
