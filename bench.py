@@ -617,11 +617,18 @@ def run_append(kimkv, dev, args) -> int:
     results = (host.CacheResult * lanes)()
     lane = np.arange(lanes, dtype=np.uint64)
 
+    # Every step's input addresses, computed before the timed loop.
+    steps_in = [newkv.ptr + np.uint64(2 * per) * (lane * np.uint64(total_steps) + np.uint64(t))
+                for t in range(total_steps)]
+
+    # The results as one int32 pair per lane (metadata error, device
+    # status): every lane is checked in one vector test.
+    res_words = np.frombuffer(results, dtype=np.int32)
+
     def step(s_):
-        inputs = newkv.ptr + np.uint64(2 * per) * (lane * np.uint64(total_steps) + np.uint64(s_))
-        cache.append_batch(ids, 1, inputs, results, stream)
-        bad = [k for k in range(lanes) if not results[k].ok()]
-        if bad:
+        cache.append_batch(ids, 1, steps_in[s_], results, stream)
+        if res_words.any():
+            bad = [k for k in range(lanes) if not results[k].ok()]
             raise RuntimeError(f"append failed for lanes {bad[:4]}: {results[bad[0]].metadata_error}, "
                                f"{results[bad[0]].device_status}")
 

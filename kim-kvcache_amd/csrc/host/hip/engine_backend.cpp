@@ -152,9 +152,10 @@ struct BackendState final {
     // of recent batched attention launches, a few per stream, each keyed by
     // its lanes' records and plan (one record per lane, then the chunk
     // flags).  The layers of a token step launch the same lanes with the same
-    // records, so the copy is made when a stream asks for the same key a
-    // second time (the step's second layer: a one-layer step never pays for
-    // a copy) and reused by the later layers.  An entry is written only by
+    // records, so the copy is made at layer 0 of a model with more layers,
+    // or else when a stream asks for the same key a second time (a one-layer
+    // step never pays for a copy), and reused by the later layers.  An entry
+    // is written only by
     // copies on its own stream, which run after that stream's earlier
     // launches that read it; a buffer is replaced only after its stream has
     // drained.  Guarded by the storage's launch mutex.
@@ -201,10 +202,12 @@ struct BackendState final {
 
     // The entry holding the chunk records of `key` (lane records, then the
     // chunk flags) for launches on `stream`: one already holding them, or,
-    // when the stream asked for the same key last time, one of the stream's
-    // entries refilled by a copy on the stream.  nullptr otherwise (the
-    // caller stages the launch another way).
-    LaneRecords* laneRecords(std::vector<unsigned char> const& key, std::uint32_t total_chunks, HipStream stream)
+    // when the stream asked for the same key last time or the caller expects
+    // it again (`reused`: later layers of the step follow), one of the
+    // stream's entries refilled by a copy on the stream.  nullptr otherwise
+    // (the caller stages the launch another way).
+    LaneRecords* laneRecords(std::vector<unsigned char> const& key, std::uint32_t total_chunks, HipStream stream,
+                             bool reused)
     {
         LaneRecords* victim = nullptr;
         std::size_t mine = 0;
@@ -227,7 +230,7 @@ struct BackendState final {
             lane_records_seen.push_back(LaneRecordsSeen{stream, {}});
             seen = &lane_records_seen.back();
         }
-        if (seen->key != key) {   // first request: remember it, copy nothing yet
+        if (seen->key != key && !reused) {   // first request: remember it, copy nothing yet
             seen->key = key;
             return nullptr;
         }
@@ -604,7 +607,12 @@ public:
             // block table.
             thread_local std::vector<unsigned char> records;
             laneRecordBytes(batch.host_items, writes, pre, chunk, n, records);
-            BackendState::LaneRecords* rec = o.laneRecords(records, total, stream);
+            // Layer 0 of a model with more layers copies the records at once
+            // (the step's other layers reuse them); otherwise only a batch
+            // the stream asks for twice is copied, so a one-layer step
+            // never pays for a copy.
+            bool const first_of_many = args.layer == 0 && o.config.kv_layout.layer_count > 1;
+            BackendState::LaneRecords* rec = o.laneRecords(records, total, stream, first_of_many);
             if (rec != nullptr) {
                 // Chunk group tables cached per copy of the records: built
                 // by the first launch from them, read by the later layers.

@@ -895,15 +895,14 @@ def _lane_records_run(host, dev, shuffle, steps=3, seed=81):
 
 def test_engine_lane_records_and_staged_items_agree(host, dev):
     """Batched attention of at most 64 lanes whose queries, outputs, workspaces and new rows are evenly
-    spaced launches from device lane records (kimkv_paged_decode_lanes) from a step's second layer on:
-    the first layer stages items and the second copies the records to the device for the rest of the
-    step.  The same lanes with shuffled query and output buffers take the staged-item launch at every
-    layer.  The two give the same outputs bit for bit over three token steps of three layers (split-K
+    spaced launches from device lane records (kimkv_paged_decode_lanes) at every layer: layer 0 copies
+    the step's records to the device and the later layers reuse them.  The same lanes with shuffled
+    query and output buffers take the staged-item launch at every layer.  The two give the same outputs bit for bit over three token steps of three layers (split-K
     lanes, fresh pages, a fork's copy-on-write tail), and plain lanes match the oracle."""
     even, n_even, T, qseed = _lane_records_run(host, dev, shuffle=False)
     mixed, n_mixed, _, _ = _lane_records_run(host, dev, shuffle=True)
     steps, L = len(even), even[0].shape[1]
-    assert n_even == steps * (L - 1), n_even
+    assert n_even == steps * L, n_even
     assert n_mixed == 0, n_mixed
     for s_ in range(steps):
         assert np.array_equal(even[s_], mixed[s_]), s_
