@@ -19,6 +19,7 @@
 #include "storage.h"
 
 #include <algorithm>
+#include <deque>
 #include <atomic>
 #include <cstddef>
 #include <cstring>
@@ -130,6 +131,70 @@ struct RequestState final {
     DeviceTable table;
 };
 
+// One lane of a batched attention launch from device lane records
+// (kimkv_paged_decode_lanes), without its chunk range: its request's table,
+// its token count and the single-token write the launch stores (none when
+// w.token_count is 0).
+kimkv_decode_lane laneRecordOf(kimkv_block_desc const* table, std::uint32_t count, std::uint32_t tokens,
+                               kimkv_append_job const& w) noexcept
+{
+    kimkv_decode_lane r{};
+    r.descriptors = table;
+    r.descriptor_count = count;
+    r.token_count = tokens;
+    if (w.token_count != 0) {
+        r.dst_slot = w.dst_slot;
+        r.cow_slot = w.cow_slot;
+        r.dst_token = w.dst_token;
+        r.cow_tokens = w.cow_tokens;
+        r.dst_kind = w.dst_kind;
+        r.cow_kind = w.cow_kind;
+        r.has_write = 1;
+    }
+    return r;
+}
+
+// The key of a launch's chunk records: each lane's record with its chunk
+// range from the plan's prefix, then the planned chunk flags (so that a copy
+// stands for one plan).
+void laneRecordKey(std::vector<kimkv_decode_lane> const& lanes, std::vector<std::uint32_t> const& pre,
+                   std::uint32_t chunk, std::vector<unsigned char>& out)
+{
+    std::size_t const n = lanes.size();
+    out.assign(n * sizeof(kimkv_decode_lane) + sizeof(std::uint32_t), 0);
+    for (std::size_t i = 0; i < n; ++i) {
+        kimkv_decode_lane r = lanes[i];
+        r.lane = static_cast<std::uint32_t>(i);
+        r.first_chunk = pre[i];
+        r.chunk_count = pre[i + 1] - pre[i];
+        std::memcpy(out.data() + i * sizeof(r), &r, sizeof(r));
+    }
+    std::memcpy(out.data() + n * sizeof(kimkv_decode_lane), &chunk, sizeof(chunk));
+}
+
+// The chunk records of a key: each lane's record repeated over its chunks
+// (total_chunks records), padded with zeros to a whole number of
+// descriptors (the unit the reserve call's patch launch copies).  False when
+// a lane's range lies outside the launch.
+bool expandLaneRecords(std::vector<unsigned char> const& key, std::uint32_t total_chunks,
+                       std::vector<kimkv_block_desc>& out)
+{
+    std::size_t const rec = sizeof(kimkv_decode_lane);
+    std::size_t const lanes = (key.size() - sizeof(std::uint32_t)) / rec;
+    std::size_t const bytes = static_cast<std::size_t>(total_chunks) * rec;
+    out.assign((bytes + sizeof(kimkv_block_desc) - 1) / sizeof(kimkv_block_desc), kimkv_block_desc{});
+    auto* dst = reinterpret_cast<unsigned char*>(out.data());
+    for (std::size_t i = 0; i < lanes; ++i) {
+        kimkv_decode_lane r;
+        std::memcpy(&r, key.data() + i * rec, rec);
+        if (static_cast<std::uint64_t>(r.first_chunk) + r.chunk_count > total_chunks) return false;
+        for (std::uint32_t k = 0; k < r.chunk_count; ++k) {
+            std::memcpy(dst + (static_cast<std::size_t>(r.first_chunk) + k) * rec, &r, rec);
+        }
+    }
+    return true;
+}
+
 struct BackendState final {
     EngineKvConfig config;
     KvCacheManager manager;
@@ -182,7 +247,7 @@ struct BackendState final {
     std::vector<LaneRecordsSeen> lane_records_seen;
     static constexpr std::size_t kLaneRecordsPerStream = 4;
     static constexpr std::size_t kLaneRecordEntries = 64;
-    std::vector<LaneRecords> lane_records;
+    std::deque<LaneRecords> lane_records;   // grows only; entries keep their addresses
     std::uint64_t lane_record_clock{0};
 
     // Grows `mem` (capacity `bytes`) to at least `need` bytes for work on
@@ -200,26 +265,44 @@ struct BackendState final {
         return mem.get() != nullptr;
     }
 
-    // The entry holding the chunk records of `key` (lane records, then the
-    // chunk flags) for launches on `stream`: one already holding them, or,
-    // when the stream asked for the same key last time or the caller expects
-    // it again (`reused`: later layers of the step follow), one of the
-    // stream's entries refilled by a copy on the stream.  nullptr otherwise
-    // (the caller stages the launch another way).
-    LaneRecords* laneRecords(std::vector<unsigned char> const& key, std::uint32_t total_chunks, HipStream stream,
-                             bool reused)
+    // The least recently used entry of `stream`, or a new one while the
+    // stream has fewer than kLaneRecordsPerStream; nullptr when none can be
+    // had.  Its contents are unknown from here on (key cleared).
+    LaneRecords* laneRecordsVictim(HipStream stream)
     {
         LaneRecords* victim = nullptr;
         std::size_t mine = 0;
         for (LaneRecords& e : lane_records) {
             if (e.stream != stream) continue;
-            if (e.key == key) {
+            ++mine;
+            if (victim == nullptr || e.used < victim->used) victim = &e;
+        }
+        if (mine < kLaneRecordsPerStream && lane_records.size() < kLaneRecordEntries) {
+            LaneRecords e;
+            e.stream = stream;
+            lane_records.push_back(std::move(e));
+            victim = &lane_records.back();
+        }
+        if (victim != nullptr) victim->key.clear();
+        return victim;
+    }
+
+    // The entry holding the chunk records of `key` (lane records, then the
+    // chunk flags) for launches on `stream`: one already holding them (a
+    // reserve call may have copied them), or, when the stream asked for the
+    // same key last time or the caller expects it again (`reused`: later
+    // layers of the step follow), one of the stream's entries refilled by a
+    // copy on the stream.  nullptr otherwise (the caller stages the launch
+    // another way).
+    LaneRecords* laneRecords(std::vector<unsigned char> const& key, std::uint32_t total_chunks, HipStream stream,
+                             bool reused)
+    {
+        for (LaneRecords& e : lane_records) {
+            if (e.stream == stream && e.key == key) {
                 e.used = ++lane_record_clock;
                 retag(e, false);
                 return &e;
             }
-            ++mine;
-            if (victim == nullptr || e.used < victim->used) victim = &e;
         }
         LaneRecordsSeen* seen = nullptr;
         for (LaneRecordsSeen& e : lane_records_seen) {
@@ -235,31 +318,31 @@ struct BackendState final {
             return nullptr;
         }
         seen->key.clear();
-        if (mine < kLaneRecordsPerStream && lane_records.size() < kLaneRecordEntries) {
-            LaneRecords e;
-            e.stream = stream;
-            lane_records.push_back(std::move(e));
-            victim = &lane_records.back();
-        }
-        if (victim == nullptr) return nullptr;
-        victim->key.clear();   // unknown contents until the copy is queued
-        // One record per chunk: each lane's record repeated over its chunks.
-        std::size_t const rec = sizeof(kimkv_decode_lane);
-        std::size_t const lanes = (key.size() - sizeof(std::uint32_t)) / rec;
-        thread_local std::vector<unsigned char> chunks;
-        chunks.assign(static_cast<std::size_t>(total_chunks) * rec, 0);
-        for (std::size_t i = 0; i < lanes; ++i) {
-            kimkv_decode_lane r;
-            std::memcpy(&r, key.data() + i * rec, rec);
-            if (static_cast<std::uint64_t>(r.first_chunk) + r.chunk_count > total_chunks) return nullptr;
-            for (std::uint32_t k = 0; k < r.chunk_count; ++k) {
-                std::memcpy(chunks.data() + (static_cast<std::size_t>(r.first_chunk) + k) * rec, &r, rec);
-            }
-        }
-        if (!growDevice(victim->device, victim->device_bytes, chunks.size(), stream)
-            || !storage.ring().uploadTo(victim->device.get(), chunks.data(), chunks.size(), stream)) {
+        thread_local std::vector<kimkv_block_desc> chunks;
+        if (!expandLaneRecords(key, total_chunks, chunks)) return nullptr;
+        std::size_t const bytes = chunks.size() * sizeof(kimkv_block_desc);
+        LaneRecords* victim = laneRecordsVictim(stream);
+        if (victim == nullptr || !growDevice(victim->device, victim->device_bytes, bytes, stream)
+            || !storage.ring().uploadTo(victim->device.get(), chunks.data(), bytes, stream)) {
             return nullptr;
         }
+        victim->key = key;
+        victim->used = ++lane_record_clock;
+        retag(*victim, true);
+        return victim;
+    }
+
+    // An entry of `stream` for the chunk records of `key` that the caller
+    // copies into it before anything else runs on the stream (a reserve
+    // call's patch launch): grown to `bytes`, keyed and freshly tagged.
+    // nullptr when no entry or memory can be had.  Under the launch mutex.
+    LaneRecords* seedLaneRecords(std::vector<unsigned char> const& key, std::uint64_t bytes, HipStream stream)
+    {
+        for (LaneRecords& e : lane_records) {
+            if (e.stream == stream && e.key == key) e.key.clear();   // one entry per key
+        }
+        LaneRecords* victim = laneRecordsVictim(stream);
+        if (victim == nullptr || !growDevice(victim->device, victim->device_bytes, bytes, stream)) return nullptr;
         victim->key = key;
         victim->used = ++lane_record_clock;
         retag(*victim, true);
@@ -504,36 +587,40 @@ public:
         return ok;
     }
 
-    // The key of the first n launched lanes' chunk records: one
-    // kimkv_decode_lane per lane (its chunks given by the prefix), then the
-    // planned chunk flags (so that a copy stands for one plan).
+    // The key of the first n launched lanes' chunk records (laneRecordKey).
     static void laneRecordBytes(DevicePagedDecodeBatchItem const* h, std::vector<kimkv_append_job> const& writes,
                                 std::vector<std::uint32_t> const& pre, std::uint32_t chunk, std::size_t n,
                                 std::vector<unsigned char>& out)
     {
-        out.assign(n * sizeof(kimkv_decode_lane) + sizeof(std::uint32_t), 0);
+        thread_local std::vector<kimkv_decode_lane> lanes;
+        lanes.resize(n);
         for (std::size_t i = 0; i < n; ++i) {
-            kimkv_decode_lane r{};
-            r.descriptors = reinterpret_cast<kimkv_block_desc const*>(h[i].device_descriptors);
-            r.descriptor_count = h[i].descriptor_count;
-            r.token_count = h[i].token_count;
-            kimkv_append_job const& w = writes[i];
-            if (w.token_count != 0) {
-                r.dst_slot = w.dst_slot;
-                r.cow_slot = w.cow_slot;
-                r.dst_token = w.dst_token;
-                r.cow_tokens = w.cow_tokens;
-                r.dst_kind = w.dst_kind;
-                r.cow_kind = w.cow_kind;
-                r.has_write = 1;
-            }
-            r.lane = static_cast<std::uint32_t>(i);
-            r.first_chunk = pre[i];
-            r.chunk_count = pre[i + 1] - pre[i];
-            std::memcpy(out.data() + i * sizeof(r), &r, sizeof(r));
+            lanes[i] = laneRecordOf(reinterpret_cast<kimkv_block_desc const*>(h[i].device_descriptors),
+                                    h[i].descriptor_count, h[i].token_count, writes[i]);
         }
-        std::memcpy(out.data() + n * sizeof(kimkv_decode_lane), &chunk, sizeof(chunk));
+        laneRecordKey(lanes, pre, chunk, out);
     }
+
+    // This transaction's lane record as its attention launches from device
+    // lane records will read it, once attached to `table` (`count` entries):
+    // every layer's attention stores the layer's token (writeLayer must
+    // precede it), at the destination the reservation fixed.
+    kimkv_decode_lane plannedLaneRecord(kimkv_block_desc const* table, std::uint32_t count) const noexcept
+    {
+        kimkv_append_job job{};
+        job.token_count = 1;
+        job.dst_slot = tail_.slot;
+        job.dst_kind = static_cast<std::uint8_t>(tail_.kind);
+        job.dst_token = tail_token_;
+        if (cow_tokens_ != 0) {
+            job.cow_slot = cow_src_.slot;
+            job.cow_kind = static_cast<std::uint8_t>(cow_src_.kind);
+            job.cow_tokens = cow_tokens_;
+        }
+        return laneRecordOf(table, count, token_count_, job);
+    }
+
+    std::uint32_t tokenCount() const noexcept { return token_count_; }
 
     void attendLayerBatch(PagedDecodeBatch& batch) override
     {
@@ -1356,6 +1443,59 @@ public:
         return result;
     }
 
+    // Chunk records for a batched attention of the reserved transactions in
+    // reservation order (the usual next call), queued into the reserve
+    // call's patch launch: that attention then launches from device lane
+    // records without a copy of its own.  An attention of other lanes or in
+    // another order misses them and copies its own.  At most
+    // KIMKV_DECODE_ARG_PREFIX_LANES lanes; nullptr when nothing was queued.
+    template <typename Pending>
+    BackendState::LaneRecords* seedLaneRecords(std::vector<Pending> const& pending, HipStream stream,
+                                               PatchBatch& patches)
+    {
+        std::size_t const n = pending.size();
+        if (n == 0 || n > KIMKV_DECODE_ARG_PREFIX_LANES) return nullptr;
+        HipKvStorage& st = state_->storage;
+        std::uint32_t const QH = state_->config.query_head_count;
+        thread_local std::vector<std::uint32_t> tokens;
+        thread_local std::vector<std::uint32_t> pre;
+        thread_local std::vector<kimkv_decode_lane> lanes;
+        tokens.resize(n);
+        pre.assign(n + 1, 0);
+        lanes.resize(n);
+        for (std::size_t i = 0; i < n; ++i) {
+            tokens[i] = pending[i].tx->tokenCount();
+            lanes[i] = pending[i].tx->plannedLaneRecord(pending[i].table->ptr, pending[i].r.entry_count);
+        }
+        std::uint32_t chunk = 0;
+        std::uint32_t total = 0;
+        if (kimkv_decode_plan(st.handle(), tokens.data(), static_cast<std::uint32_t>(n), QH, &chunk, pre.data(),
+                              &total) != KIMKV_OK
+            || (chunk & KIMKV_DECODE_GUIDED) != 0) {
+            return nullptr;
+        }
+        thread_local std::vector<unsigned char> key;
+        thread_local std::vector<kimkv_block_desc> blob;
+        laneRecordKey(lanes, pre, chunk, key);
+        if (!expandLaneRecords(key, total, blob)) return nullptr;
+        BackendState::LaneRecords* e = nullptr;
+        kimkv_block_desc* dst = nullptr;
+        {
+            std::lock_guard<std::mutex> launch(st.launchMutex());
+            e = state_->seedLaneRecords(key, blob.size() * sizeof(kimkv_block_desc), stream);
+            if (e != nullptr) dst = static_cast<kimkv_block_desc*>(e->device.get());
+        }
+        if (e == nullptr) return nullptr;
+        // No launch can name these records before this call returns its
+        // transactions; the patch batch takes the launch mutex itself.
+        if (!patches.add(dst, 0, blob.data(), static_cast<std::uint32_t>(blob.size()))) {
+            std::lock_guard<std::mutex> launch(st.launchMutex());
+            e->key.clear();
+            return nullptr;
+        }
+        return e;
+    }
+
     // reserveToken for several requests sharing one stream.  Per request:
     // the manager's delta reservation, the new tail entry checked, and the
     // request's device table brought to the candidate -- its tail entry
@@ -1453,7 +1593,12 @@ public:
             pending.push_back(Pending{i, r, std::move(tx), &table});
         }
         if (pending.empty()) return;
+        BackendState::LaneRecords* seeded = seedLaneRecords(pending, stream, patches);
         bool const issued = patches.flush();
+        if (!issued && seeded != nullptr) {
+            std::lock_guard<std::mutex> launch(st.launchMutex());
+            seeded->key.clear();   // the copy was not issued
+        }
         for (Pending& p : pending) {
             TokenReserveResult& result = results[p.index];
             if (!issued) {
