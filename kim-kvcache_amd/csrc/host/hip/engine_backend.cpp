@@ -217,10 +217,12 @@ struct BackendState final {
     // of recent batched attention launches, a few per stream, each keyed by
     // its lanes' records and plan (one record per lane, then the chunk
     // flags).  The layers of a token step launch the same lanes with the same
-    // records, so the copy is made at layer 0 of a model with more layers,
-    // or else when a stream asks for the same key a second time (a one-layer
-    // step never pays for a copy), and reused by the later layers.  An entry
-    // is written only by
+    // records: a reserve call copies the records of its transactions in
+    // reservation order with its descriptor patches; an attention that
+    // misses them copies its own at layer 0 of a model with more layers, or
+    // else when a stream asks for the same key a second time (a one-layer
+    // step never pays for a separate copy); later layers reuse the copy.  An
+    // entry is written only by
     // copies on its own stream, which run after that stream's earlier
     // launches that read it; a buffer is replaced only after its stream has
     // drained.  Guarded by the storage's launch mutex.
