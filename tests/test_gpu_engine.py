@@ -6,6 +6,7 @@ tests/cuda/cuda_kv_test.cpp; every data check is against closed forms or the
 oracle."""
 import ctypes
 import math
+import types
 
 import numpy as np
 import pytest
@@ -821,12 +822,13 @@ def test_engine_small_staging_ring(host, dev, monkeypatch):
     _engine_lane_batch_case(host, dev, steps=3, seed=78)
 
 
-def _lane_records_run(host, dev, shuffle, steps=3, seed=81):
+def _lane_records_run(host, dev, shuffle, steps=3, seed=81, reverse_attend=False):
     """24 lanes (two of them forks of one prefix with a partial tail, so their first token copies it on
     write; ragged contexts up to ~3000 tokens, so some lanes split into several chunks) through
     LaneBatch for `steps` tokens.  shuffle: lanes' query and output buffers in a random order (not
-    evenly spaced).  Returns per-step outputs in lane order, the engine's lane_record_launches, and the
-    inputs for an oracle check."""
+    evenly spaced).  reverse_attend: every layer's write and attention take the reserved transactions
+    in reverse order (still evenly spaced, with negative strides).  Returns per-step outputs in lane
+    order, the engine's lane_record_launches, and the inputs for an oracle check."""
     L, H, D, QH, lanes = 3, 4, 64, 32, 24
     HD, QD = H * D, QH * D
     rng = np.random.default_rng(seed)
@@ -865,6 +867,7 @@ def _lane_records_run(host, dev, shuffle, steps=3, seed=81):
         b.queries[l, :] = query.ptr + np.uint64(2 * QD) * (np.uint64(l * lanes) + pos)
         b.outputs[l, :] = out.ptr + np.uint64(2 * QD) * (np.uint64(l * lanes) + pos)
     qseed = seed ^ 0x5155
+    items = dev.DeviceBuffer(lanes * host.DECODE_ITEM_BYTES)
     outs = []
     for step in range(steps):
         for i in range(lanes):
@@ -877,6 +880,16 @@ def _lane_records_run(host, dev, shuffle, steps=3, seed=81):
         b.reserve(np.array([t + step for t in T], dtype=np.uint32))
         assert not b.failed()
         for l in range(L):
+            if reverse_attend:
+                rt = [types.SimpleNamespace(h=int(x)) for x in b.txns[::-1]]
+                st = host.write_layer_batch(rt, [l] * lanes, [int(k) for k in b.keys[l, ::-1]],
+                                            [int(v) for v in b.values[l, ::-1]])
+                assert not any(st), st
+                reqs = [(l, int(b.queries[l, i]), int(b.outputs[l, i]), ws.ptr + i * ws_lane, ws_lane, 0.125)
+                        for i in reversed(range(lanes))]
+                st = host.attend_layer_batch(rt, reqs, items)
+                assert not any(st), st
+                continue
             b.write(l)
             assert not b.failed(), sorted(set(b.status.tolist()))
             b.attend(l)
@@ -929,6 +942,19 @@ def test_engine_lane_records_and_staged_items_agree(host, dev):
             worst = max(worst, float(err.max()))
     print(f"lane records vs staged items: {steps} steps x {L} layers, record launches {n_even}, "
           f"oracle max err {worst:.2e}", flush=True)
+
+
+def test_engine_lane_records_in_another_order(host, dev):
+    """The reserve call copies the lane records for an attention of its transactions in reservation
+    order.  Attending them in reverse order instead (evenly spaced with negative strides) misses that
+    copy: layer 0 copies its own records and every layer still launches from records, with the same
+    outputs bit for bit as the attention in reservation order."""
+    fwd, n_fwd, _, _ = _lane_records_run(host, dev, shuffle=False)
+    rev, n_rev, _, _ = _lane_records_run(host, dev, shuffle=False, reverse_attend=True)
+    steps, L = len(fwd), fwd[0].shape[1]
+    assert n_fwd == steps * L and n_rev == steps * L, (n_fwd, n_rev)
+    for s_ in range(steps):
+        assert np.array_equal(fwd[s_], rev[s_]), s_
 
 
 def test_inflight_transaction_pages_survive_sibling_release_and_promotion(host, dev):
