@@ -1489,8 +1489,17 @@ public:
         }
         if (e == nullptr) return nullptr;
         // No launch can name these records before this call returns its
-        // transactions; the patch batch takes the launch mutex itself.
-        if (!patches.add(dst, 0, blob.data(), static_cast<std::uint32_t>(blob.size()))) {
+        // transactions; the patch batch takes the launch mutex itself.  The
+        // patch kernel copies each patch with one workgroup, a word per
+        // thread per round trip to the staged (host) bytes, so the records
+        // go in pieces of one round each, copied side by side.
+        constexpr std::uint32_t kPiece = 256 / 5;   // descriptors: 5 words each
+        bool queued = true;
+        for (std::uint32_t k = 0; queued && k < blob.size(); k += kPiece) {
+            std::uint32_t const m = std::min<std::uint32_t>(kPiece, static_cast<std::uint32_t>(blob.size()) - k);
+            queued = patches.add(dst, k, blob.data() + k, m);
+        }
+        if (!queued) {
             std::lock_guard<std::mutex> launch(st.launchMutex());
             e->key.clear();
             return nullptr;
