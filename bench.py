@@ -928,39 +928,66 @@ def run_shared(kimkv, dev, args) -> int:
     out = dev.DeviceBuffer(L * lanes * QD * 2)
     ws = dev.DeviceBuffer(ws_lane * lanes)
     lane_ix = np.arange(lanes, dtype=np.uint64)
-    batch = host.LaneBatch(engine, lane_ix + np.uint64(1), ws.ptr + lane_ix * np.uint64(ws_lane), ws_lane,
-                           1.0 / math.sqrt(D), stream)
     lay = np.arange(L, dtype=np.uint64)[:, None]
     kbase = newkv.ptr + np.uint64(2 * HD) * ((lane_ix[None, :] * np.uint64(L) + lay) * np.uint64(2 * S))
     vbase = kbase + np.uint64(2 * HD * S)
     qbase = query.ptr + np.uint64(2 * QD) * ((lane_ix[None, :] * np.uint64(L) + lay) * np.uint64(S))
-    batch.outputs[:] = out.ptr + np.uint64(2 * QD) * (lay * np.uint64(lanes) + lane_ix[None, :])
+    obase = out.ptr + np.uint64(2 * QD) * (lay * np.uint64(lanes) + lane_ix[None, :])
+    # Lane groups (whole fork groups): one batch of token transactions each,
+    # on its own stream, pipelined like the HBM-scale workload's groups (a
+    # group commits after the next group's layers are queued).  One group
+    # (the default) is the whole step as a single batch.
+    n_groups = max(1, min(args.shared_groups, groups))
+    bounds = [per_group * (groups * g // n_groups) for g in range(n_groups + 1)]
+    streams = [stream] + [dev.Stream() for _ in range(n_groups - 1)]
+    # Per group: its batch and every step's input addresses and expected
+    # lengths, computed before the timed loop (a step copies them into the
+    # batch's argument arrays).
+    batches = []
+    for g in range(n_groups):
+        sl = slice(bounds[g], bounds[g + 1])
+        b = host.LaneBatch(engine, lane_ix[sl] + np.uint64(1), ws.ptr + lane_ix[sl] * np.uint64(ws_lane), ws_lane,
+                           1.0 / math.sqrt(D), streams[g])
+        b.outputs[:] = obase[:, sl]
+        batches.append((b, [np.ascontiguousarray(kbase[:, sl] + np.uint64(2 * HD * t)) for t in range(S)],
+                        [np.ascontiguousarray(vbase[:, sl] + np.uint64(2 * HD * t)) for t in range(S)],
+                        [np.ascontiguousarray(qbase[:, sl] + np.uint64(2 * QD * t)) for t in range(S)],
+                        [(lengths[sl] + t).astype(np.uint32) for t in range(S)]))
     stream.synchronize()
+    pending = []
 
-    # Every step's input addresses and expected lengths, computed before the
-    # timed loop (the step copies them into the batch's argument arrays).
-    steps_k = [kbase + np.uint64(2 * HD * t) for t in range(S)]
-    steps_v = [vbase + np.uint64(2 * HD * t) for t in range(S)]
-    steps_q = [qbase + np.uint64(2 * QD * t) for t in range(S)]
-    steps_e = [(lengths + t).astype(np.uint32) for t in range(S)]
+    def commit(b):
+        b.commit()
+        assert not b.failed(), b.status
 
     def step(s_):
-        batch.keys[:] = steps_k[s_]
-        batch.values[:] = steps_v[s_]
-        batch.queries[:] = steps_q[s_]
-        batch.reserve(steps_e[s_])
-        assert not batch.failed(), batch.status
-        for l in range(L):
-            batch.write(l)
-            assert not batch.failed(), batch.status
-            batch.attend(l)
-            assert not batch.failed(), batch.status
-        batch.commit()
-        assert not batch.failed(), batch.status
+        for g in batches:
+            b, ks, vs, qs, es = g
+            if pending and pending[0] is g:   # a single group commits before its next token
+                commit(pending.pop()[0])
+            b.keys[:] = ks[s_]
+            b.values[:] = vs[s_]
+            b.queries[:] = qs[s_]
+            b.reserve(es[s_])
+            assert not b.failed(), b.status
+            for l in range(L):
+                b.write(l)
+                assert not b.failed(), b.status
+                b.attend(l)
+                assert not b.failed(), b.status
+            if pending:
+                commit(pending.pop()[0])
+            pending.append(g)
+
+    def drain():
+        while pending:
+            commit(pending.pop()[0])
+        for st in streams:
+            st.synchronize()
 
     for s_ in range(args.warmup):
         step(s_)
-    stream.synchronize()
+    drain()
     # Timed loop without per-launch kernel timing (its events sit between the
     # kernels and lengthen a step of short launches).
     start, stop = dev.Event(), dev.Event()
@@ -968,6 +995,7 @@ def run_shared(kimkv, dev, args) -> int:
     start.record(stream)
     for s_ in range(args.warmup, args.warmup + args.steps):
         step(s_)
+    drain()
     stop.record(stream)
     stop.synchronize()
     wall_ms = (time.perf_counter() - t_wall) * 1000.0
@@ -977,13 +1005,19 @@ def run_shared(kimkv, dev, args) -> int:
     dev.decode_timing(True)
     for s_ in range(args.warmup + args.steps, total_steps):
         step(s_)
-    stream.synchronize()
-    dec_ms, dec_n = dev.decode_timing(False)
-    dec_ms /= max(dec_n, 1)
-    # Algorithmic bytes of one decode launch: every lane's logical K/V (mean
-    # over the timed launches), the queries, the outputs and the tokens written.
+    drain()
+    dec_total_ms, dec_n = dev.decode_timing(False)
+    dec_busy_ms = dev.decode_timing_busy()
+    dec_avg_ms = dec_total_ms / max(dec_n, 1)
+    # Per launch: its share of the time the decode kernel occupied the GPU
+    # (with several lane groups two launches overlap: the busy union over
+    # the launches; one group: their mean duration).
+    dec_ms = dec_busy_ms / max(dec_n, 1) if n_groups > 1 else dec_avg_ms
+    # Algorithmic bytes of one decode launch (mean over the timed launches,
+    # one per layer per group): the lanes' logical K/V, the queries, the
+    # outputs and the tokens written.
     dec_appended = args.warmup + args.steps + (total_steps - args.warmup - args.steps + 1) / 2.0
-    dec_bytes = (lengths.sum() + lanes * dec_appended) * 2 * HD * 2 + lanes * (2 * QD * 2 + 2 * HD * 2)
+    dec_bytes = ((lengths.sum() + lanes * dec_appended) * 2 * HD * 2 + lanes * (2 * QD * 2 + 2 * HD * 2)) / n_groups
     us_per_layer = ms_per_step * 1000.0 / L
     appended = args.warmup + (args.steps + 1) / 2.0          # mean tokens appended by the timed steps
     logical_bytes = (lengths.sum() + lanes * appended) * 2 * HD * 2
@@ -1036,21 +1070,27 @@ def run_shared(kimkv, dev, args) -> int:
         "value": round(us_per_layer, 2), "unit": "us/layer", "higher_is_better": False,
         "logical_gb_per_s": round(logical_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "physical_gb_per_s": round(physical_bytes / (us_per_layer * 1e-6) / 1e9, 1),
-        "decode_kernel_avg_us": round(1000 * dec_ms, 2),
+        "decode_kernel_avg_us": round(1000 * dec_avg_ms, 2),
+        "decode_busy_us_per_launch": round(1000 * dec_ms, 2),
         "ms_per_step": round(ms_per_step, 3),
         "gpu_ms_per_step": round(gpu_ms / args.steps, 3), "host_ms_per_step": round(wall_ms / args.steps, 3),
         "roofline": {"bound": "hbm", "achieved": round(dec_bytes / (dec_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(dec_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": profiled_traffic("decode_kernel_shared_prefix.md", lanes=lanes, layers=L,
-                                                 logical_tokens=int(logical)),
+                     "traffic": profiled_traffic("decode_kernel_shared_prefix.md", lanes=lanes // n_groups,
+                                                 layers=L, logical_tokens=int(logical)),
                      "kernel": "decode_kernel", "launch_ms": round(dec_ms, 4), "timed_launches": dec_n,
                      "bytes_per_launch": int(dec_bytes),
                      "note": "bytes are the lanes' logical K/V; the fork groups share prefix pages, so the unique "
-                             "pages are about half of them; latency-bound (one round of 256-token chunks)"},
+                             "pages are about half of them; latency-bound (one round of 256-token chunks); with "
+                             "several lane groups two groups' launches overlap and launch_ms is the busy union "
+                             "per launch"},
         "config": {"workload": f"{lanes} lanes ({groups} groups of {per_group} forking a 2048+r-token prefix, "
                                f"partial-tail COW), contexts log-uniform in [128, 8192], {L} layers TinyLlama GQA "
-                               f"32q/4kv/64d fp16, through the engine",
-                   "logical_tokens": logical, "unique_physical_tokens": physical},
+                               f"32q/4kv/64d fp16, through the engine"
+                               + (f", as {n_groups} batches of {lanes // n_groups} lanes pipelined on "
+                                  f"{n_groups} streams" if n_groups > 1 else ""),
+                   "logical_tokens": logical, "unique_physical_tokens": physical,
+                   "lane_groups": n_groups, "lanes_per_batch": lanes // n_groups},
         "steps": args.steps, "warmup": args.warmup,
         "check": {"lanes": lanes, "layer": 0, "max_abs_err": worst, "within_tolerance": ok,
                   "tolerance": "2e-3 + 1e-3*|ref|"},
@@ -1430,6 +1470,9 @@ def main() -> int:
                          "commit); kernel: the C-ABI kernels driven directly with bench-built page tables")
     ap.add_argument("--group-streams", choices=["own", "shared"], default="own",
                     help="engine path: each lane group on its own stream (own) or all on one (shared)")
+    ap.add_argument("--shared-groups", type=int, default=1,
+                    help="shared config: lane groups (whole fork groups) pipelined on their own streams "
+                         "(1 = the 32 lanes as one batch per step)")
     ap.add_argument("--groups", type=int, default=2,
                     help="engine path: lane groups pipelined against each other (1 = one batch per step)")
     ap.add_argument("--slots", choices=["permuted", "sequential"], default="permuted",
