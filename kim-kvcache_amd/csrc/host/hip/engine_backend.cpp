@@ -691,9 +691,9 @@ public:
         kimkv_decode_layer_args args{};
         if (n <= KIMKV_DECODE_ARG_PREFIX_LANES && evenLayerArgs(batch, launched, writes, n, args)
             && (total == n || args.workspace != nullptr)) {
-            // Every lane's step-constant record from a device copy the step's
-            // first layer made: no workgroup reads host memory before its
-            // block table.
+            // Every chunk's step-constant record from a device copy (made by
+            // the reserve call, or here): no workgroup reads host memory
+            // before its block table.
             thread_local std::vector<unsigned char> records;
             laneRecordBytes(batch.host_items, writes, pre, chunk, n, records);
             // Layer 0 of a model with more layers copies the records at once
