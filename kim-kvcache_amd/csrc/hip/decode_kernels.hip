@@ -645,12 +645,17 @@ __device__ bool build_chunk_table(const PoolView& P, const kimkv_decode_item& it
 // same round trip as the lane record, where building it waits for that
 // record.  Per chunk: a 16-byte header, then `stride` 8-byte group entries.
 // A header whose tag is not the launch's (another step, or never written)
-// makes the workgroup build the table and store it with the launch's tag.
+// makes the workgroup build the table, and the chunk's first workgroup
+// stores it with the launch's tag and id.  A header stored by the same
+// launch is not trusted either: in the head-split mode a chunk has one
+// workgroup per kv head, and nothing orders one workgroup's entry stores
+// before another's reads within a launch (they may sit on different XCDs),
+// while the end of a launch makes its stores visible to the next one.
 struct TableCacheHeader {
     uint32_t tag;
+    uint32_t launch;    // id of the launch that stored it
     uint32_t ngroups;
-    uint32_t generic;
-    uint32_t new_ok;
+    uint32_t flags;     // bit 0: generic path, bit 1: new token readable
 };
 static_assert(sizeof(TableCacheHeader) == 16 && sizeof(GroupEntry) == 8, "cache layout");
 
@@ -658,6 +663,7 @@ struct TableCache {
     unsigned char* base;   // nullptr: no cache
     uint32_t stride;       // group entries per chunk (chunk_tokens / 8)
     uint32_t tag;          // nonzero
+    uint32_t launch;       // this launch's id: nonzero, unique among recent launches
 };
 // Entries one thread prefetches: chunks of up to 4096 tokens.
 constexpr uint32_t kTableCachePerThread = 2;
@@ -683,22 +689,25 @@ __device__ inline bool chunk_table_cached(const PoolView& P, const kimkv_decode_
     if (cache.base == nullptr || ngroups > cache.stride) return build_chunk_table(P, item, QH, c0, c1, lds, jv);
     __syncthreads();   // the header and entries copied into LDS
     uint32_t const G = QH / P.heads;
-    if (s_hdr.tag == cache.tag && s_hdr.ngroups == ngroups) {
+    if (s_hdr.tag == cache.tag && s_hdr.launch != cache.launch && s_hdr.ngroups == ngroups) {
         if (threadIdx.x == 0) {
-            lds.generic = s_hdr.generic;
-            lds.new_ok = s_hdr.new_ok;
+            lds.generic = s_hdr.flags & 1u;
+            lds.new_ok = (s_hdr.flags >> 1) & 1u;
         }
         __syncthreads();
         return P.dim == 64 && G <= 16 && lds.generic == 0;
     }
     __syncthreads();   // every thread has read the header before the table is rebuilt
     bool const fast = build_chunk_table(P, item, QH, c0, c1, lds, jv);
-    unsigned char* c = cache.base + table_cache_chunk_bytes(cache.stride) * chunk_id;
-    for (uint32_t g = threadIdx.x; g < ngroups; g += kBlock) {
-        reinterpret_cast<GroupEntry*>(c + sizeof(TableCacheHeader))[g] = lds.groups[g];
-    }
-    if (threadIdx.x == 0) {
-        *reinterpret_cast<TableCacheHeader*>(c) = TableCacheHeader{cache.tag, ngroups, lds.generic, lds.new_ok};
+    if (blockIdx.y == 0) {
+        unsigned char* c = cache.base + table_cache_chunk_bytes(cache.stride) * chunk_id;
+        for (uint32_t g = threadIdx.x; g < ngroups; g += kBlock) {
+            reinterpret_cast<GroupEntry*>(c + sizeof(TableCacheHeader))[g] = lds.groups[g];
+        }
+        if (threadIdx.x == 0) {
+            uint32_t const flags = (lds.generic != 0 ? 1u : 0u) | (lds.new_ok != 0 ? 2u : 0u);
+            *reinterpret_cast<TableCacheHeader*>(c) = TableCacheHeader{cache.tag, cache.launch, ngroups, flags};
+        }
     }
     return fast;
 }
@@ -1746,7 +1755,12 @@ kimkv_status kimkv_paged_decode_lanes(const kimkv_storage* storage, const kimkv_
             || table_cache_bytes / kimkv::table_cache_chunk_bytes(stride) < total_chunks) {
             return KIMKV_INVALID_ARGUMENT;
         }
-        cache = kimkv::TableCache{static_cast<unsigned char*>(device_table_cache), stride, table_tag};
+        // Launch ids: nonzero and unique among the launches a cache sees
+        // between two uses of one tag (they wrap after 2^32 launches).
+        static std::atomic<uint32_t> next_launch{1};
+        uint32_t launch = next_launch.fetch_add(1, std::memory_order_relaxed);
+        if (launch == 0) launch = next_launch.fetch_add(1, std::memory_order_relaxed);
+        cache = kimkv::TableCache{static_cast<unsigned char*>(device_table_cache), stride, table_tag, launch};
     }
     return kimkv::launch_decode(storage, nullptr, nullptr, lane_count, total_chunks, chunk_flags, query_heads,
                                 stream, nullptr, nullptr, true, static_cast<kimkv::DecodeLaneSlot*>(device_lane_slots),

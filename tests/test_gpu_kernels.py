@@ -363,6 +363,61 @@ def test_decode_write_batch_matches_append_then_decode(dev, mode):
     print(f"decode+write mode={mode} lanes={len(T)} chunks={total}", flush=True)
 
 
+def test_decode_lane_records_table_cache_head_split_many_rounds(dev):
+    """Head-split record launches (one workgroup per chunk and kv head) with a chunk table cache and far
+    more workgroups than the GPU holds at once, so the workgroups of a chunk's later heads start after
+    its first head's workgroup has stored the table in the same launch.  A launch trusts only tables an
+    earlier launch stored: the first launch of a tag and the two after it give the same outputs, bit for
+    bit, as the same launch without a cache, and so does a new tag."""
+    L, H, D, QH = 1, 4, 64, 32
+    n = 40
+    T = [4000 + 37 * i for i in range(n)]
+    micro_cap, ext_cap = sum(t // 8 + 2 for t in T), sum(t // 64 + 1 for t in T)
+    storage = dev.Storage(L, H, D, micro_cap, ext_cap)
+    alloc = helpers.SlotAllocator(micro_cap, ext_cap, seed=41)
+    chunk = 256 | dev.DECODE_HEAD_SPLIT
+    prefix = dev.chunk_prefix(T, chunk, D)
+    total = int(prefix[-1])
+    assert total * H > 2048                       # several rounds of resident workgroups
+    keep = []
+    lanes = np.zeros(n, dtype=dev.DECODE_LANE)
+    for i, t in enumerate(T):
+        table = helpers.hetero_table(t, alloc)
+        d = dev.upload(table)
+        keep.append(d)
+        storage.fill_table(d.ptr, len(table), 0, t, 45, i)
+        lanes[i] = (d.ptr, len(table), t, 0, 0, 0, 0, 0, 0, 0, 0, i, prefix[i], prefix[i + 1] - prefix[i], 0)
+    chunks = np.concatenate([np.repeat(lanes[i:i + 1], prefix[i + 1] - prefix[i]) for i in range(n)])
+    lbuf = dev.upload(chunks)
+    qs = dev.upload(np.stack([oracle.synth_rows(QH * D, 4600 + i, 0, D) for i in range(n)]))
+    out = dev.upload(np.zeros((n, QH * D), dtype=np.uint16))
+    ws_stride = max(max(dev.workspace_bytes(t, chunk, QH, D) for t in T), 256)
+    ws = dev.DeviceBuffer(n * ws_stride)
+    need = dev.table_cache_bytes(total, chunk)
+    cache = dev.upload(np.zeros(need // 2, dtype=np.uint16))
+    keep += [lbuf, qs, out, ws, cache]
+    a = dev.DecodeLayerArgs()
+    a.layer, a.attention_scale = 0, 0.125
+    a.query, a.query_stride = qs.ptr, QH * D * 2
+    a.output, a.output_stride = out.ptr, QH * D * 2
+    a.workspace, a.workspace_stride = ws.ptr, ws_stride
+    a.key, a.key_stride = qs.ptr, 0
+    a.value, a.value_stride = qs.ptr, 0
+    runs = [dict()] + [dict(cache_ptr=cache.ptr, cache_bytes=need, tag=t) for t in (9, 9, 9, 10)]
+    zeros = np.zeros((n, QH * D), dtype=np.uint16)
+    for kw in runs:
+        dev.copy_to_device(out.ptr, zeros)      # every launch writes every output afresh
+        assert storage.decode_lanes_launch(lbuf.ptr, n, total, chunk, QH, a, 0, host_prefix=prefix, **kw) == 0
+        dev.sync()
+        assert storage.faults() == (0, 0)
+        got = dev.download(out.ptr, (n, QH * D), np.uint16)
+        if not kw:
+            first = got
+            assert np.any(first != 0)
+        else:
+            assert np.array_equal(got, first), kw
+
+
 @pytest.mark.parametrize("mode,order", [("four_heads", 1), ("head_split", 1), ("four_heads", -1),
                                         ("head_split", -1)])
 def test_decode_lane_records_match_item_launch(dev, mode, order):
