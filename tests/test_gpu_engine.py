@@ -822,14 +822,14 @@ def test_engine_small_staging_ring(host, dev, monkeypatch):
     _engine_lane_batch_case(host, dev, steps=3, seed=78)
 
 
-def _lane_records_run(host, dev, shuffle, steps=3, seed=81, reverse_attend=False):
+def _lane_records_run(host, dev, shuffle, steps=3, seed=81, reverse_attend=False, heads=4):
     """24 lanes (two of them forks of one prefix with a partial tail, so their first token copies it on
     write; ragged contexts up to ~3000 tokens, so some lanes split into several chunks) through
     LaneBatch for `steps` tokens.  shuffle: lanes' query and output buffers in a random order (not
     evenly spaced).  reverse_attend: every layer's write and attention take the reserved transactions
     in reverse order (still evenly spaced, with negative strides).  Returns per-step outputs in lane
     order, the engine's lane_record_launches, and the inputs for an oracle check."""
-    L, H, D, QH, lanes = 3, 4, 64, 32, 24
+    L, H, D, QH, lanes = 3, heads, 64, 32, 24
     HD, QD = H * D, QH * D
     rng = np.random.default_rng(seed)
     T = [int(t) for t in rng.integers(20, 3000, lanes)]
@@ -955,6 +955,37 @@ def test_engine_lane_records_in_another_order(host, dev):
     assert n_fwd == steps * L and n_rev == steps * L, (n_fwd, n_rev)
     for s_ in range(steps):
         assert np.array_equal(fwd[s_], rev[s_]), s_
+
+
+def test_engine_lane_records_eight_kv_heads(host, dev):
+    """The lane-record path with 8 kv heads (group 4): two workgroups per chunk share its cached group
+    table and the reserve call's records; outputs equal the staged-item launches of shuffled buffers bit
+    for bit over three steps, and plain lanes match the oracle."""
+    even, n_even, T, qseed = _lane_records_run(host, dev, shuffle=False, heads=8)
+    mixed, n_mixed, _, _ = _lane_records_run(host, dev, shuffle=True, heads=8)
+    steps, L = len(even), even[0].shape[1]
+    assert n_even == steps * L and n_mixed == 0, (n_even, n_mixed)
+    for s_ in range(steps):
+        assert np.array_equal(even[s_], mixed[s_]), s_
+    H, D, QH, seed = 8, 64, 32, 81
+    HD = H * D
+    for i in range(2):
+        n = T[i] + steps
+        for l in range(L):
+            kv = np.empty((1, 2, n, H, D), dtype=np.uint16)
+            for c in range(2):
+                kv[0, c] = oracle.synth_rows(n * HD, seed, oracle.kv_row(i, l, c, 0), HD).reshape(n, H, D)
+            pages = (n + 7) // 8
+            pools = oracle.HostPools(1, H, D, pages, 1)
+            table = np.zeros(pages, dtype=oracle.DESC)
+            for k in range(pages):
+                table[k] = (k, 1, 8 * k, min(8, n - 8 * k), 8, 0)
+                pools.append_tokens(kv, n, 8 * k, 0, k, 0, min(8, n - 8 * k))
+            q = oracle.synth_rows(QH * D, qseed, oracle.kv_row(i, l, 0, n - 1), QH * D)
+            want = pools.paged_decode(table, n, 0, QH, q, 0.125, f32=True)
+            a = even[-1][i, l].view(np.float16).astype(np.float32)
+            err = np.abs(a - want)
+            assert np.all(err <= 2e-3 + 1e-3 * np.abs(want)), (i, l, float(err.max()))
 
 
 def test_inflight_transaction_pages_survive_sibling_release_and_promotion(host, dev):
