@@ -418,9 +418,11 @@ def test_decode_lane_records_table_cache_head_split_many_rounds(dev):
             assert np.array_equal(got, first), kw
 
 
-@pytest.mark.parametrize("mode,order,heads", [("four_heads", 1, 4), ("head_split", 1, 4), ("four_heads", -1, 4),
-                                              ("head_split", -1, 4), ("four_heads", 1, 8), ("head_split", 1, 8)])
-def test_decode_lane_records_match_item_launch(dev, mode, order, heads):
+@pytest.mark.parametrize("mode,order,heads,dim", [("four_heads", 1, 4, 64), ("head_split", 1, 4, 64),
+                                                  ("four_heads", -1, 4, 64), ("head_split", -1, 4, 64),
+                                                  ("four_heads", 1, 8, 64), ("head_split", 1, 8, 64),
+                                                  ("four_heads", 1, 4, 128)])
+def test_decode_lane_records_match_item_launch(dev, mode, order, heads, dim):
     """kimkv_paged_decode_lanes (each lane's item and job built in the kernel from a device lane record
     and the layer's evenly spaced addresses) equals kimkv_paged_decode_write_batch_slots_prefix with the
     same items and jobs, bit for bit in the outputs and the pages: tail writes, fresh pages, copy-on-write
@@ -428,8 +430,9 @@ def test_decode_lane_records_match_item_launch(dev, mode, order, heads):
     strides).  With a chunk table cache: the first launch of a tag builds and stores the tables, the next
     two read them, and a new tag over the same cache rebuilds them; every launch gives the same outputs.
     Malformed launches are refused without running.  With 8 kv heads a chunk has two workgroups of four
-    heads each (or eight in the head-split mode) sharing its cached table."""
-    shape = (3, heads, 64)
+    heads each (or eight in the head-split mode) sharing its cached table; head_dim 128 takes the generic
+    path (and the merge of two dims per lane)."""
+    shape = (3, heads, dim)
     L, H, D = shape
     QH, layer = 32, 1
     T = [5, 8, 63, 64, 100, 700, 1303, 2049, 17]
