@@ -676,11 +676,11 @@ __host__ __device__ inline uint64_t table_cache_chunk_bytes(uint32_t stride)
 
 // build_chunk_table for a kRecords launch with a table cache (see
 // TableCache): when the header this workgroup loaded with its lane record
-// carries the launch's tag and the chunk's group count, the entries it
-// copied into lds.groups are the table; otherwise the table is built from
-// the descriptors and stored with the launch's tag (every workgroup of a
-// chunk -- one per kv head in the head-split mode -- stores the same bytes).
-// Called by every thread of the block.
+// carries the launch's tag, another launch's id and the chunk's group count,
+// the entries it copied into lds.groups are the table; otherwise the table
+// is built from the descriptors, and the chunk's first workgroup (blockIdx.y
+// 0) stores it with the launch's tag and id.  Called by every thread of the
+// block.
 __device__ inline bool chunk_table_cached(const PoolView& P, const kimkv_decode_item& item, uint32_t QH, uint32_t c0,
                                           uint32_t c1, DecodeLds& lds, JobView const& jv, TableCache const& cache,
                                           uint32_t chunk_id, TableCacheHeader const& s_hdr)
