@@ -1270,10 +1270,28 @@ void attendPrefillBatch(PrefillChunk* const* chunks, std::size_t count, std::uin
                                    totals.data(), news.data(), static_cast<std::uint32_t>(items.size()), out,
                                    capacity, n);
     };
-    std::uint32_t order_count = 0;
-    static_cast<void>(plan(nullptr, 0, &order_count));
-    order.resize(order_count);
-    kimkv_status k = plan(order.data(), order_count, &order_count);
+    // The placement depends only on the shape and the items' token counts,
+    // which every layer of a step repeats: it is planned again only when
+    // they change (tens of microseconds of host time per plan).
+    thread_local std::vector<std::uint32_t> plan_key, planned_key;
+    plan_key.assign({kl.kv_head_count, kl.head_dimension, owner->config.query_head_count, units});
+    plan_key.insert(plan_key.end(), totals.begin(), totals.end());
+    plan_key.insert(plan_key.end(), news.begin(), news.end());
+    kimkv_status k = KIMKV_OK;
+    if (plan_key != planned_key) {
+        planned_key.clear();
+        std::uint32_t needed = 0;
+        k = plan(order.data(), static_cast<std::uint32_t>(order.size()), &needed);
+        if (k != KIMKV_OK && needed > order.size()) {
+            order.resize(needed);
+            k = plan(order.data(), needed, &needed);
+        }
+        if (k == KIMKV_OK) {
+            order.resize(needed);
+            planned_key = plan_key;
+        }
+    }
+    std::uint32_t const order_count = static_cast<std::uint32_t>(order.size());
     std::size_t const items_bytes = (items.size() * sizeof(kimkv_prefill_item) + 15) & ~std::size_t{15};
     thread_local std::vector<unsigned char> staging;
     staging.resize(items_bytes + order.size() * sizeof(kimkv_prefill_block));
