@@ -271,8 +271,10 @@ kimkv_status kimkv_patch_descriptors(const kimkv_descriptor_patch* patches, uint
 
 /* Set by kimkv_decode_plan in *chunk_tokens when each workgroup should take
  * one KV head and split its chunk over its four waves (merged in the
- * workgroup) instead of taking four KV heads; the other bits are the chunk
- * length.  Pass the planned value through to kimkv_paged_decode_batch and
+ * workgroup) instead of taking four KV heads (lanes of one chunk that four
+ * heads per workgroup would split, or a batch small enough that its chunks
+ * fit one round of resident workgroups either way); the other bits are the
+ * chunk length.  Pass the planned value through to kimkv_paged_decode_batch and
  * kimkv_decode_workspace_bytes unchanged. */
 #define KIMKV_DECODE_HEAD_SPLIT 0x80000000u
 

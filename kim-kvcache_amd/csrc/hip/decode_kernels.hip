@@ -1625,7 +1625,7 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
     // 128 lanes x 32k tokens it measured 0.638 ms per launch (six slices) and
     // 0.652 ms (three) against 0.628 ms for one head-split chunk per lane on
     // the same MI355X; callers may still request it explicitly.
-    bool const head_split = per_block < longest && per_head >= longest && fast_shape;
+    bool head_split = per_block < longest && per_head >= longest && fast_shape;
     uint64_t target = head_split ? longest : per_block;
     if (target < kMinChunk) target = kMinChunk;
     if (target > kMaxChunk) target = kMaxChunk;
@@ -1646,6 +1646,12 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
         if (acc > 0x7FFFFFFFu) return KIMKV_INVALID_ARGUMENT;
         chunk_prefix[i + 1] = static_cast<uint32_t>(acc);
     }
+    // A batch whose chunks stay within one round of resident workgroups even
+    // with one kv head per workgroup takes that form as well: each wave then
+    // streams a quarter of the chunk, a shorter chain of dependent loads
+    // (4 lanes of 18..1001 tokens: 33.3 us per engine step against 36.8 -
+    // 37.3 us; the 32-lane shared-prefix batch has too many chunks for it).
+    if (!head_split && fast_shape && acc * H <= slots) head_split = true;
     *chunk_tokens = static_cast<uint32_t>(target) | (head_split ? KIMKV_DECODE_HEAD_SPLIT : 0u);
     *total_chunks = static_cast<uint32_t>(acc);
     return KIMKV_OK;

@@ -845,7 +845,8 @@ def test_decode_combine_wide_heads_and_many_chunks(dev):
     chunk, total = _decode_case(dev, (1, 1, 256), [700, 2000], G=2, seed=14)
     assert total > 2
     chunk, total = _decode_case(dev, (1, 4, 64), [20000, 33], G=8, seed=15)
-    assert (20000 + chunk - 1) // chunk > 64
+    length = chunk & ~dev.DECODE_HEAD_SPLIT
+    assert (20000 + length - 1) // length > 64
 
 
 def test_decode_full_step_counts(dev):
