@@ -32,6 +32,7 @@ namespace {
 constexpr unsigned kBlock = 256;          // 4 waves
 constexpr unsigned kHeadsPerBlock = 4;
 constexpr unsigned kMinChunk = 256;
+constexpr unsigned kWholeLaneMax = 1024;   // tokens: longest lane a small batch keeps whole
 // Softmax weights of the fast path are 2^(s - m + kWeightShift): the largest
 // is 2^15 (fp16 max 65504), and weights down to 2^-29 of the largest stay
 // fp16 normal numbers.  o and l carry the same factor, so it cancels in the
@@ -1626,6 +1627,15 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
     // 0.652 ms (three) against 0.628 ms for one head-split chunk per lane on
     // the same MI355X; callers may still request it explicitly.
     bool head_split = per_block < longest && per_head >= longest && fast_shape;
+    // A small batch of lanes up to kWholeLaneMax tokens takes the same form
+    // when one workgroup per (lane, kv head) fits one round: each wave then
+    // streams at most a quarter of the lane and no merge launch follows (4
+    // lanes of 18..1001 tokens: 32.9 - 33.4 us per engine step against 34.0
+    // - 35.0 us with the lanes split into 256-token chunks, one kv head per
+    // workgroup).
+    bool const whole_lanes = !head_split && fast_shape && longest > kMinChunk && longest <= kWholeLaneMax
+        && lane_count * H <= slots;
+    head_split = head_split || whole_lanes;
     uint64_t target = head_split ? longest : per_block;
     if (target < kMinChunk) target = kMinChunk;
     if (target > kMaxChunk) target = kMaxChunk;
@@ -1649,8 +1659,9 @@ kimkv_status kimkv_decode_plan(const kimkv_storage* storage, const uint32_t* tok
     // A batch whose chunks stay within one round of resident workgroups even
     // with one kv head per workgroup takes that form as well: each wave then
     // streams a quarter of the chunk, a shorter chain of dependent loads
-    // (4 lanes of 18..1001 tokens: 33.3 us per engine step against 36.8 -
-    // 37.3 us; the 32-lane shared-prefix batch has too many chunks for it).
+    // (4 lanes of 18..1001 tokens in 256-token chunks: 33.3 us per engine
+    // step against 36.8 - 37.3 us with four kv heads per workgroup; the
+    // 32-lane shared-prefix batch has too many chunks for it).
     if (!head_split && fast_shape && acc * H <= slots) head_split = true;
     *chunk_tokens = static_cast<uint32_t>(target) | (head_split ? KIMKV_DECODE_HEAD_SPLIT : 0u);
     *total_chunks = static_cast<uint32_t>(acc);
